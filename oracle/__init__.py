@@ -1,0 +1,212 @@
+"""CPU oracle for the OSSM scan kernels — TEST INFRASTRUCTURE ONLY.
+
+Python face of ``oracle/scan_oracle.c`` (a C restatement of the reference's
+CPU kernels) and of ``oracle/_ref`` (the reference's own CPU kernels compiled
+from /root/reference by ``oracle/Makefile.ref``).  Only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import this
+package, and only as the checker or the timed CPU baseline.  The product path
+(``ossm_amd``) never imports it.
+
+All functions take and return numpy arrays in the reference's layouts:
+D-LinOSS ``bu [L,B,P]`` complex, states ``[L,B,P,2]`` complex; LinOSS
+``b_seq [L,B,P,2]`` complex with complex ``m_ij [P]``; selective scan
+``u, dt, gate [B,D,L]``, ``A [D,N]``, ``B, C [B,L,N]`` real.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "_build" / "libscan_oracle.so"
+_REF_DIR = _HERE / "_ref"
+
+VARIANTS = ("imex1", "imex2", "im", "ex")
+_VARIANT_CODE = {name: i for i, name in enumerate(VARIANTS)}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def build() -> None:
+    """Compile the C restatement (``make -C oracle``)."""
+    subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
+
+
+def _load() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(_LIB_PATH))
+    return _lib
+
+
+def num_threads() -> int:
+    return int(_load().oracle_num_threads())
+
+
+def _ptr(arr: Optional[np.ndarray]):
+    if arr is None:
+        return None
+    assert arr.flags["C_CONTIGUOUS"], "oracle inputs must be C-contiguous"
+    return arr.ctypes.data_as(ctypes.c_void_p)
+
+
+def _real_dtype(precision: str):
+    return np.float32 if precision == "f32" else np.float64
+
+
+def _complex_dtype(precision: str):
+    return np.complex64 if precision == "f32" else np.complex128
+
+
+def _prec_of(arr: np.ndarray) -> str:
+    return "f64" if arr.dtype in (np.float64, np.complex128) else "f32"
+
+
+def _fn(name: str, precision: str):
+    return getattr(_load(), f"{name}_{precision}")
+
+
+def _c(arr, dtype) -> np.ndarray:
+    return np.ascontiguousarray(arr, dtype=dtype)
+
+
+# ---------------------------------------------------------------- D-LinOSS
+def dlinoss_forward(variant: str, a_diag, g_diag, step, bu) -> np.ndarray:
+    """States ``[L,B,P,2]`` of the D-LinOSS recurrence (dlinoss_<v>.cpp forward)."""
+    prec = _prec_of(np.asarray(bu))
+    rt, ct = _real_dtype(prec), _complex_dtype(prec)
+    bu = _c(bu, ct)
+    L, B, P = bu.shape
+    a, g, s = _c(a_diag, rt), _c(g_diag, rt), _c(step, rt)
+    out = np.empty((L, B, P, 2), dtype=ct)
+    I = ctypes.c_int64
+    _fn("oracle_dlinoss_forward", prec)(
+        ctypes.c_int(_VARIANT_CODE[variant]), _ptr(a), _ptr(g), _ptr(s), _ptr(bu), _ptr(out),
+        I(L), I(B), I(P))
+    return out
+
+
+def dlinoss_backward(variant: str, a_diag, g_diag, step, bu, states, grad_output,
+                     grad_aux=None):
+    """``(grad_a, grad_g, grad_step, grad_bu)`` (dlinoss_<v>.cpp backward).
+
+    ``grad_aux`` is an oracle-only extra gradient w.r.t. state component 0;
+    ``None`` gives the reference's arithmetic exactly.
+    """
+    prec = _prec_of(np.asarray(bu))
+    rt, ct = _real_dtype(prec), _complex_dtype(prec)
+    bu = _c(bu, ct)
+    L, B, P = bu.shape
+    a, g, s = _c(a_diag, rt), _c(g_diag, rt), _c(step, rt)
+    states = _c(states, ct)
+    gout = _c(grad_output, ct)
+    gaux = None if grad_aux is None else _c(grad_aux, ct)
+    grad_bu = np.empty_like(bu)
+    ga, gg, gs = np.zeros(P, rt), np.zeros(P, rt), np.zeros(P, rt)
+    I = ctypes.c_int64
+    _fn("oracle_dlinoss_backward", prec)(
+        ctypes.c_int(_VARIANT_CODE[variant]), _ptr(a), _ptr(g), _ptr(s), _ptr(bu), _ptr(states),
+        _ptr(gout), _ptr(gaux), _ptr(grad_bu), _ptr(ga), _ptr(gg), _ptr(gs), I(L), I(B), I(P))
+    return ga, gg, gs, grad_bu
+
+
+# ------------------------------------------------------------------ LinOSS
+def linoss_forward(m11, m12, m21, m22, b_seq) -> np.ndarray:
+    """States ``[L,B,P,2]`` of ``s_t = M s_{t-1} + b_t`` (linoss_scan.cpp)."""
+    prec = _prec_of(np.asarray(b_seq))
+    ct = _complex_dtype(prec)
+    b_seq = _c(b_seq, ct)
+    L, B, P, _ = b_seq.shape
+    ms = [_c(m, ct) for m in (m11, m12, m21, m22)]
+    out = np.empty_like(b_seq)
+    I = ctypes.c_int64
+    _fn("oracle_linoss_forward", prec)(*[_ptr(m) for m in ms], _ptr(b_seq), _ptr(out),
+                                       I(L), I(B), I(P))
+    return out
+
+
+def linoss_backward(m11, m12, m21, m22, states, grad_output):
+    """``(grad_m [P,2,2], grad_b [L,B,P,2])`` restating linoss.py:83-151."""
+    prec = _prec_of(np.asarray(states))
+    ct = _complex_dtype(prec)
+    states = _c(states, ct)
+    gout = _c(grad_output, ct)
+    L, B, P, _ = states.shape
+    ms = [_c(m, ct) for m in (m11, m12, m21, m22)]
+    grad_m = np.zeros((P, 2, 2), dtype=ct)
+    grad_b = np.empty_like(states)
+    I = ctypes.c_int64
+    _fn("oracle_linoss_backward", prec)(*[_ptr(m) for m in ms], _ptr(states), _ptr(gout),
+                                        _ptr(grad_m), _ptr(grad_b), I(L), I(B), I(P))
+    return grad_m, grad_b
+
+
+# --------------------------------------------------------------- selective
+def selective_forward(u, dt, A, Bm, Cm, gate=None) -> np.ndarray:
+    """Selective scan output ``[B,D,L]`` (selective_scan_cpu.cpp:78-166)."""
+    prec = _prec_of(np.asarray(u))
+    rt = _real_dtype(prec)
+    u, dt, A, Bm, Cm = (_c(x, rt) for x in (u, dt, A, Bm, Cm))
+    gate = None if gate is None else _c(gate, rt)
+    Bsz, D, L = u.shape
+    N = A.shape[1]
+    out = np.empty_like(u)
+    I = ctypes.c_int64
+    _fn("oracle_selective_forward", prec)(_ptr(u), _ptr(dt), _ptr(A), _ptr(Bm), _ptr(Cm),
+                                          _ptr(gate), _ptr(out), I(Bsz), I(D), I(L), I(N))
+    return out
+
+
+def selective_backward(grad_output, u, dt, A, Bm, Cm, gate=None):
+    """``(du, ddt, dA, dB, dC, dgate)`` (selective_scan_cpu.cpp:168-360)."""
+    prec = _prec_of(np.asarray(u))
+    rt = _real_dtype(prec)
+    gout, u, dt, A, Bm, Cm = (_c(x, rt) for x in (grad_output, u, dt, A, Bm, Cm))
+    gate = None if gate is None else _c(gate, rt)
+    Bsz, D, L = u.shape
+    N = A.shape[1]
+    gu, gdt, ggate = np.empty_like(u), np.empty_like(u), np.empty_like(u)
+    gA = np.zeros_like(A)
+    gB, gC = np.zeros_like(Bm), np.zeros_like(Cm)
+    I = ctypes.c_int64
+    _fn("oracle_selective_backward", prec)(
+        _ptr(gout), _ptr(u), _ptr(dt), _ptr(A), _ptr(Bm), _ptr(Cm), _ptr(gate), _ptr(gu),
+        _ptr(gdt), _ptr(gA), _ptr(gB), _ptr(gC), _ptr(ggate), I(Bsz), I(D), I(L), I(N))
+    return gu, gdt, gA, gB, gC, ggate
+
+
+# ------------------------------------------------- reference CPU kernels
+def reference_module():
+    """The reference's own CPU kernels (``oracle/_ref/_ref_kernels.so``), or None.
+
+    Built in the survey container by ``make -f oracle/Makefile.ref`` from the
+    sources under /root/reference; torch must be imported first.
+    """
+    path = _REF_DIR / "_ref_kernels.so"
+    if not path.exists():
+        return None
+    import importlib.util
+
+    import torch  # noqa: F401  (loads libtorch for the extension)
+
+    spec = importlib.util.spec_from_file_location("_ref_kernels", str(path))
+    if spec is None or spec.loader is None:
+        return None
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def have_reference() -> bool:
+    return (_REF_DIR / "_ref_kernels.so").exists()
+
+
+os.environ.setdefault("OMP_PROC_BIND", "false")

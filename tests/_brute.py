@@ -1,0 +1,81 @@
+"""Brute-force fp64 PyTorch recurrences used to pin the oracle by autograd.
+
+These are sequential loops written from the mathematics of each scan, not
+from the oracle's code: their backward passes come from torch.autograd, so a
+wrong sign, index or transposition in the oracle's hand-written adjoint shows
+up as a mismatch.  CPU only, small sizes.
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+def dlinoss_matrices(variant: str, a, g, dt):
+    """``(M [P,2,2], f [P,2])`` of the D-LinOSS recurrence s_t = M s_{t-1} + f bu_t.
+
+    The variant table (reference _dlinoss_scan.py:54-101):
+      imex1: S=1+dt g, M=[[1/S, -dt^2 a/S], [1/S, 1-dt^2 a/S]], f=[dt^2/S, dt^2/S]
+      imex2: M=[[1-dt g, -dt a], [dt(1-dt g), 1-dt^2 a]], f=[dt, dt^2]
+      im:    D=1+dt g+dt^2 a, M=[[1/D, -dt a/D], [dt/D, (1+dt g)/D]], f=[dt/D, dt^2/D]
+      ex:    M=[[1-dt g, -dt a], [dt, 1]], f=[dt, 0]
+    """
+    one = torch.ones_like(a)
+    if variant == "imex1":
+        S = one + dt * g
+        m = [[one / S, -(dt * dt * a) / S], [one / S, one - (dt * dt * a) / S]]
+        f = [dt * dt / S, dt * dt / S]
+    elif variant == "imex2":
+        m = [[one - dt * g, -dt * a], [dt * (one - dt * g), one - dt * dt * a]]
+        f = [dt, dt * dt]
+    elif variant == "im":
+        D = one + dt * g + dt * dt * a
+        m = [[one / D, -(dt * a) / D], [dt / D, (one + dt * g) / D]]
+        f = [dt / D, dt * dt / D]
+    elif variant == "ex":
+        m = [[one - dt * g, -dt * a], [dt, one]]
+        f = [dt, torch.zeros_like(dt)]
+    else:
+        raise ValueError(variant)
+    M = torch.stack([torch.stack(r, -1) for r in m], -2)
+    return M, torch.stack(f, -1)
+
+
+def dlinoss_states(variant: str, a, g, dt, bu):
+    """States ``[L,B,P,2]`` by a plain loop; differentiable in every input."""
+    M, f = dlinoss_matrices(variant, a, g, dt)
+    L, B, P = bu.shape
+    s = torch.zeros(B, P, 2, dtype=bu.dtype)
+    out = []
+    Mc = M.to(bu.dtype)
+    fc = f.to(bu.dtype)
+    for t in range(L):
+        s = torch.einsum("pij,bpj->bpi", Mc, s) + fc.unsqueeze(0) * bu[t].unsqueeze(-1)
+        out.append(s)
+    return torch.stack(out, 0)
+
+
+def linoss_states(a_matrix, b_seq):
+    """``s_t = M s_{t-1} + b_t`` with complex ``M [P,2,2]``; ``b_seq [L,B,P,2]``."""
+    L, B, P, _ = b_seq.shape
+    s = torch.zeros(B, P, 2, dtype=b_seq.dtype)
+    out = []
+    for t in range(L):
+        s = torch.einsum("pij,bpj->bpi", a_matrix, s) + b_seq[t]
+        out.append(s)
+    return torch.stack(out, 0)
+
+
+def selective(u, dt, A, Bm, Cm, gate=None):
+    """Mamba recurrence h = exp(dt A) h + dt B u, y = C.h, y*silu(z)."""
+    Bsz, D, L = u.shape
+    h = torch.zeros(Bsz, D, A.shape[1], dtype=u.dtype)
+    ys = []
+    for t in range(L):
+        d = dt[:, :, t].unsqueeze(-1)
+        h = torch.exp(d * A.unsqueeze(0)) * h + (d * Bm[:, t].unsqueeze(1)) * u[:, :, t].unsqueeze(-1)
+        ys.append((h * Cm[:, t].unsqueeze(1)).sum(-1))
+    y = torch.stack(ys, -1)
+    if gate is not None:
+        y = y * torch.nn.functional.silu(gate)
+    return y

@@ -1,0 +1,253 @@
+"""Pins for the CPU oracle (oracle/): golden fixtures, the reference's own
+compiled CPU kernels, independent formulations and fp64 autograd.
+
+CPU only.  Each check is chosen so that a plausible slip in the oracle (a
+dropped term, a sign, a transposed operand, a wrong index) fails at least one.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests import _brute
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+VARIANTS = oracle.VARIANTS
+
+
+@pytest.fixture(scope="module")
+def vectors():
+    with np.load(GOLDEN / "ref_kernel_vectors.npz", allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def _close(actual, expected, rtol, atol, what=""):
+    np.testing.assert_allclose(actual, expected, rtol=rtol, atol=atol, err_msg=what)
+
+
+# --------------------------------------------------------------------- D-LinOSS
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_dlinoss_matches_reference_kernel_vectors(variant, vectors):
+    """Oracle vs the reference's own CPU kernels (oracle/_ref), fwd and bwd."""
+    v = vectors
+    st = oracle.dlinoss_forward(variant, v["dl_a"], v["dl_g"], v["dl_step"], v["dl_bu"])
+    _close(st, v[f"dl_{variant}_states"], 1e-5, 1e-5, "states")
+    ga, gg, gs, gb = oracle.dlinoss_backward(variant, v["dl_a"], v["dl_g"], v["dl_step"],
+                                             v["dl_bu"], v[f"dl_{variant}_states"], v["dl_grad"])
+    _close(gb, v[f"dl_{variant}_grad_bu"], 1e-5, 1e-5, "grad_bu")
+    for got, key in ((ga, "grad_a"), (gg, "grad_g"), (gs, "grad_step")):
+        ref = v[f"dl_{variant}_{key}"]
+        _close(got, ref, 1e-5, 1e-5 * np.abs(ref).max(), key)
+
+
+def _layer_case(variant: str, dtype: str):
+    cases = json.loads((GOLDEN / "dlinoss_reference_cases.json").read_text())["cases"]
+    return cases[variant][dtype]
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("dtype", ["float32", "float64"])
+def test_dlinoss_matches_reference_layer_fixture(variant, dtype):
+    """Golden layer fixture of the reference (tests/dlinoss_reference_cases.json).
+
+    The layer glue (bu = u B^T, y = Re(x C^T) + D u, loss of the reference test
+    test_dlinoss_parity.py:130-137) is written here in numpy; the scan and its
+    adjoint come from the oracle.
+    """
+    c = _layer_case(variant, dtype)
+    rt = np.float32 if dtype == "float32" else np.float64
+    ct = np.complex64 if dtype == "float32" else np.complex128
+    tol = 5e-6 if dtype == "float32" else 1e-9  # the reference test's tolerances
+    a, g, step = (np.asarray(c[k], rt) for k in ("A_diag", "G_diag", "step"))
+    Bw = np.asarray(c["B"], rt)          # [P, H, 2]
+    Cw = np.asarray(c["C"], rt)          # [H, P, 2]
+    Dw = np.asarray(c["D"], rt)          # [H]
+    u = np.asarray(c["inputs"], rt)      # [B, L, H]
+    Bc = (Bw[..., 0] + 1j * Bw[..., 1]).astype(ct)
+    bu = np.einsum("blh,ph->lbp", u.astype(ct), Bc).astype(ct)
+    states = oracle.dlinoss_forward(variant, a, g, step, bu)   # [L, B, P, 2]
+    main = states[..., 1].transpose(1, 0, 2)                   # [B, L, P]
+    aux = states[..., 0].transpose(1, 0, 2)
+    _close(np.stack([main.real, main.imag], -1), np.asarray(c["states"]["main"]), tol, tol, "main")
+    _close(np.stack([aux.real, aux.imag], -1), np.asarray(c["states"]["aux"]), tol, tol, "aux")
+    out = main.real @ Cw[..., 0].T - main.imag @ Cw[..., 1].T + u * Dw
+    _close(out, np.asarray(c["outputs"]), tol, tol, "outputs")
+
+    # loss = sum(out^2) + |main|^2 + |aux|^2  (complex grads as d/dre + i d/dim)
+    g_out = 2 * out
+    g_main = np.einsum("blh,hp->blp", g_out, Cw[..., 0] - 1j * Cw[..., 1]) + 2 * main
+    g_aux = 2 * aux
+    ga, gg, gs, gbu = oracle.dlinoss_backward(
+        variant, a, g, step, bu, states,
+        g_main.transpose(1, 0, 2).astype(ct), grad_aux=g_aux.transpose(1, 0, 2).astype(ct))
+    gB = np.stack([np.einsum("lbp,blh->ph", gbu.real, u), np.einsum("lbp,blh->ph", gbu.imag, u)], -1)
+    grads = c["grads"]
+    for got, key in ((ga, "A_diag"), (gg, "G_diag"), (gs, "step"), (gB, "B")):
+        _close(got, np.asarray(grads[key]), tol, tol, key)
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_dlinoss_backward_matches_fp64_autograd(variant):
+    """Hand-written adjoint vs torch.autograd of a plain fp64 loop."""
+    rng = np.random.default_rng(3)
+    L, B, P = 19, 2, 5
+    a = rng.uniform(0.1, 1.0, P)
+    g = rng.uniform(0.0, 1.0, P)
+    dt = 1.0 / (1.0 + np.exp(-rng.normal(size=P)))
+    bu = rng.normal(size=(L, B, P)) + 1j * rng.normal(size=(L, B, P))
+    G = rng.normal(size=(L, B, P)) + 1j * rng.normal(size=(L, B, P))
+    ta, tg, tdt = (torch.tensor(x, requires_grad=True) for x in (a, g, dt))
+    tbu = torch.tensor(bu, requires_grad=True)
+    s = _brute.dlinoss_states(variant, ta, tg, tdt, tbu)
+    # real loss whose gradient w.r.t. x = s[...,1] is G (re + i im convention)
+    loss = (s[..., 1] * torch.tensor(G).conj()).real.sum()
+    loss.backward()
+    states = oracle.dlinoss_forward(variant, a, g, dt, bu)
+    _close(states, s.detach().numpy(), 1e-12, 1e-12, "states")
+    ga, gg, gs, gbu = oracle.dlinoss_backward(variant, a, g, dt, bu, states, G)
+    _close(ga, ta.grad.numpy(), 1e-10, 1e-10, "grad_a")
+    _close(gg, tg.grad.numpy(), 1e-10, 1e-10, "grad_g")
+    _close(gs, tdt.grad.numpy(), 1e-10, 1e-10, "grad_step")
+    _close(gbu, tbu.grad.numpy(), 1e-10, 1e-10, "grad_bu")
+
+
+def test_dlinoss_imex1_matches_official_z_recurrence():
+    """imex1 evolves w = dt*z; the official D-LinOSS recurrence keeps z
+    (reference test_dlinoss.py:11-35, 174-188)."""
+    rng = np.random.default_rng(7)
+    L, B, P = 9, 2, 4
+    a, g = rng.uniform(size=P), rng.uniform(size=P)
+    dt = rng.uniform(size=P) * 0.5 + 0.1
+    bu = rng.normal(size=(L, B, P)) + 1j * rng.normal(size=(L, B, P))
+    states = oracle.dlinoss_forward("imex1", a, g, dt, bu)
+    z = np.zeros((B, P), complex)
+    x = np.zeros((B, P), complex)
+    for t in range(L):
+        z = (z + dt * (-a * x + bu[t])) / (1 + dt * g)
+        x = x + dt * z
+        _close(states[t, ..., 0] / dt, z, 1e-12, 1e-13, f"z[{t}]")
+        _close(states[t, ..., 1], x, 1e-12, 1e-13, f"x[{t}]")
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_dlinoss_special_cases(variant):
+    rng = np.random.default_rng(11)
+    P = 6
+    a, g = rng.uniform(0.1, 1, P), rng.uniform(0, 1, P)
+    dt = 1 / (1 + np.exp(-rng.normal(size=P)))
+    zero = np.zeros((5, 3, P), complex)
+    assert np.all(oracle.dlinoss_forward(variant, a, g, dt, zero) == 0)
+    # linearity: scan(x + 2y) = scan(x) + 2 scan(y)
+    x = rng.normal(size=(13, 2, P)) + 1j * rng.normal(size=(13, 2, P))
+    y = rng.normal(size=(13, 2, P)) + 1j * rng.normal(size=(13, 2, P))
+    sx, sy = (oracle.dlinoss_forward(variant, a, g, dt, v) for v in (x, y))
+    _close(oracle.dlinoss_forward(variant, a, g, dt, x + 2 * y), sx + 2 * sy, 1e-12, 1e-12)
+    # causality: changing bu at t=7 leaves states before 7 untouched
+    x2 = x.copy()
+    x2[7] += 1.0
+    s2 = oracle.dlinoss_forward(variant, a, g, dt, x2)
+    assert np.array_equal(s2[:7], sx[:7]) and not np.array_equal(s2[7:], sx[7:])
+    if variant == "ex":  # f2 = 0: x_0 = dt*w_{-1} + x_{-1} = 0
+        assert np.all(sx[0, ..., 1] == 0)
+
+
+# ----------------------------------------------------------------------- LinOSS
+def test_linoss_forward_matches_reference_kernel_vectors(vectors):
+    v = vectors
+    out = oracle.linoss_forward(v["lo_m11"], v["lo_m12"], v["lo_m21"], v["lo_m22"], v["lo_b"])
+    _close(out, v["lo_out"], 1e-5, 1e-5)
+
+
+def test_linoss_matches_reference_layer_snapshot():
+    """REFERENCE_LINOSS LinOSS-IM layer snapshot (test_linoss_parity.py:74-204);
+    layer glue from linoss.py:199-258, 293-314."""
+    ref = json.loads((GOLDEN / "linoss_reference_snapshot.json").read_text())
+    A = np.asarray(ref["A_diag"], np.float32)
+    Bw = np.asarray(ref["B"], np.float32)                  # [P, H, 2]
+    Cw = np.asarray(ref["C"], np.float32).reshape(6, 4, 2)  # [H, P, 2]
+    Dw = np.asarray(ref["D"], np.float32)
+    steps = np.asarray(ref["steps"], np.float32)
+    u = np.asarray(ref["inputs"], np.float32)              # [B, L, H]
+    a = np.maximum(A, 0)
+    dt = 1 / (1 + np.exp(-steps))
+    schur = 1 / (1 + dt * dt * a)
+    m11, m12, m21, m22 = 1 - dt * dt * a * schur, -dt * a * schur, dt * schur, schur
+    bu = np.einsum("blh,ph->lbp", u, Bw[..., 0] + 1j * Bw[..., 1]).astype(np.complex64)
+    b_seq = np.stack([bu * (m11 * dt), bu * (m21 * dt)], -1).astype(np.complex64)
+    ms = [m.astype(np.complex64) for m in (m11, m12, m21, m22)]
+    st = oracle.linoss_forward(*ms, b_seq)[..., 1].transpose(1, 0, 2)
+    out = st.real @ Cw[..., 0].T - st.imag @ Cw[..., 1].T + u * Dw
+    _close(out, np.asarray(ref["outputs"]), 5e-6, 5e-6)
+
+
+def test_linoss_backward_matches_fp64_autograd():
+    rng = np.random.default_rng(5)
+    L, B, P = 17, 3, 4
+    M = (rng.normal(size=(P, 2, 2)) + 1j * rng.normal(size=(P, 2, 2))) * 0.4
+    bs = rng.normal(size=(L, B, P, 2)) + 1j * rng.normal(size=(L, B, P, 2))
+    G = rng.normal(size=(L, B, P, 2)) + 1j * rng.normal(size=(L, B, P, 2))
+    tM = torch.tensor(M, requires_grad=True)
+    tb = torch.tensor(bs, requires_grad=True)
+    s = _brute.linoss_states(tM, tb)
+    (s * torch.tensor(G).conj()).real.sum().backward()
+    ms = [M[:, 0, 0], M[:, 0, 1], M[:, 1, 0], M[:, 1, 1]]
+    states = oracle.linoss_forward(*ms, bs)
+    _close(states, s.detach().numpy(), 1e-12, 1e-12)
+    gm, gb = oracle.linoss_backward(*ms, states, G)
+    _close(gm, tM.grad.numpy(), 1e-10, 1e-10, "grad_M")
+    _close(gb, tb.grad.numpy(), 1e-10, 1e-10, "grad_b")
+
+
+# -------------------------------------------------------------------- selective
+@pytest.mark.parametrize("tag", ["gate", "nogate"])
+def test_selective_matches_reference_kernel_vectors(tag, vectors):
+    v = vectors
+    gate = v["sel_z"] if tag == "gate" else None
+    args = (v["sel_u"], v["sel_dt"], v["sel_A"], v["sel_B"], v["sel_C"])
+    _close(oracle.selective_forward(*args, gate), v[f"sel_{tag}_out"], 1e-5, 1e-5, "out")
+    grads = oracle.selective_backward(v["sel_grad"], *args, gate)
+    for got, name in zip(grads, ("du", "ddt", "dA", "dB", "dC", "dz")):
+        ref = v[f"sel_{tag}_{name}"]
+        _close(got, ref, 1e-5, 1e-5 * max(1.0, np.abs(ref).max()), name)
+
+
+@pytest.mark.parametrize("gated", [True, False])
+def test_selective_backward_matches_fp64_autograd(gated):
+    rng = np.random.default_rng(9)
+    Bz, D, L, N = 2, 3, 23, 5
+    u = rng.normal(size=(Bz, D, L))
+    dt = np.log1p(np.exp(rng.normal(size=(Bz, D, L)) - 2))
+    A = -np.exp(rng.normal(size=(D, N)))
+    Bm, Cm = rng.normal(size=(Bz, L, N)), rng.normal(size=(Bz, L, N))
+    z = rng.normal(size=(Bz, D, L)) if gated else None
+    G = rng.normal(size=(Bz, D, L))
+    ts = [torch.tensor(x, requires_grad=True) for x in (u, dt, A, Bm, Cm)]
+    tz = torch.tensor(z, requires_grad=True) if gated else None
+    y = _brute.selective(*ts, tz)
+    (y * torch.tensor(G)).sum().backward()
+    _close(oracle.selective_forward(u, dt, A, Bm, Cm, z), y.detach().numpy(), 1e-12, 1e-12)
+    grads = oracle.selective_backward(G, u, dt, A, Bm, Cm, z)
+    names = ("du", "ddt", "dA", "dB", "dC")
+    for got, t, name in zip(grads, ts, names):
+        _close(got, t.grad.numpy(), 1e-10, 1e-10, name)
+    if gated:
+        _close(grads[5], tz.grad.numpy(), 1e-10, 1e-10, "dz")
+    else:
+        assert np.all(grads[5] == 0)
+
+
+def test_reference_module_when_present():
+    """oracle/_ref, when built, exports the reference's 21 CPU entry points."""
+    if not oracle.have_reference():
+        pytest.skip("oracle/_ref not built")
+    mod = oracle.reference_module()
+    for v in VARIANTS:
+        assert hasattr(mod, f"dlinoss_{v}_forward") and hasattr(mod, f"dlinoss_{v}_backward")
+    for name in ("linoss_scan", "selective_scan", "selective_scan_backward"):
+        assert hasattr(mod, name)
