@@ -1,0 +1,137 @@
+/*
+ * ossm_scan.h — C ABI of the MI355X (gfx950) scan library libossm_scan.so.
+ *
+ * Drop-in device side of the reference extension `ossm._kernels`
+ * (src/ossm/csrc/bindings.cpp:159-224).  Every entry point takes plain device
+ * pointers, sizes and a HIP stream (passed as void*), launches asynchronously
+ * on that stream, and returns 0 on success or a nonzero status with a message
+ * available from ossm_last_error().  Outputs are written, never allocated:
+ * the caller (e.g. the Python binding ossm_amd._kernels) allocates them.
+ *
+ * Layouts (all contiguous, complex = interleaved float re/im = complex64):
+ *   D-LinOSS:   a_diag, g_diag, step [P] f32;  bu [L,B,P] c64;
+ *               states [L,B,P,2] c64 (component 0 = auxiliary w, 1 = x)
+ *   LinOSS:     m11, m12, m21, m22 [P] c64;  b_seq, states [L,B,P,2] c64
+ *   selective:  u, dt, gate, out [B,D,L] f32;  A [D,N] f32;  Bm, Cm [B,L,N] f32
+ *
+ * Scratch: the library keeps one zero-initialised scratch buffer per
+ * (device, stream) for look-back records and partial sums; it grows on demand
+ * (hipMalloc outside the launch path) and never needs clearing between calls.
+ */
+#ifndef OSSM_SCAN_H
+#define OSSM_SCAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* ossm_stream_t; /* hipStream_t */
+
+enum {
+  OSSM_OK = 0,
+  OSSM_ERR_INVALID_ARGUMENT = 1, /* shape / pointer / variant problem (reference: TORCH_CHECK) */
+  OSSM_ERR_HIP = 2,              /* HIP runtime error (reference: AT_CUDA_CHECK) */
+  OSSM_ERR_UNSUPPORTED = 3       /* valid request this build does not implement */
+};
+
+enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
+
+/* Library ABI version (bumped on any signature change). */
+int ossm_abi_version(void);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* ossm_last_error(void);
+
+/*
+ * Synchronises `stream` and returns (then clears) the device-side error bits
+ * of its scratch buffer: bit 0 = a look-back wait gave up (bounded spin
+ * exceeded), bit 1 = a workgroup drew an out-of-range ticket.  0 means every
+ * launch on this stream since the last check completed its protocol.
+ */
+uint32_t ossm_device_error_bits(ossm_stream_t stream);
+
+/*
+ * D-LinOSS forward, replaces dlinoss_<v>_forward:
+ *   dlinoss_imex1.cpp:317-352, dlinoss_imex2.cpp:329-364,
+ *   dlinoss_im.cpp:347-382,    dlinoss_ex.cpp:264-299.
+ * s_t = M(a,g,dt) s_{t-1} + f(a,g,dt) bu_t per (b,p), s_{-1} = 0; writes all
+ * L states, both components.
+ */
+int ossm_dlinoss_forward(int variant, const float* a_diag, const float* g_diag,
+                         const float* step, const void* bu, void* states, int64_t length,
+                         int64_t batch, int64_t ssm, ossm_stream_t stream);
+
+/*
+ * D-LinOSS backward, replaces dlinoss_<v>_backward:
+ *   dlinoss_imex1.cpp:354-390, dlinoss_imex2.cpp:366-402,
+ *   dlinoss_im.cpp:384-420,    dlinoss_ex.cpp:301-365.
+ * grad_output is the gradient w.r.t. component 1 (x) of the states, [L,B,P] c64.
+ * Only the states at sub-chunk boundaries are read; the rest is recomputed
+ * from bu.  grad_a/grad_g/grad_step [P] f32 are overwritten (not accumulated).
+ */
+int ossm_dlinoss_backward(int variant, const float* a_diag, const float* g_diag,
+                          const float* step, const void* bu, const void* states,
+                          const void* grad_output, float* grad_a, float* grad_g,
+                          float* grad_step, void* grad_bu, int64_t length, int64_t batch,
+                          int64_t ssm, ossm_stream_t stream);
+
+/*
+ * LinOSS scan forward, replaces linoss_scan (linoss_scan.cpp:115-146):
+ * s_t = M s_{t-1} + b_t with complex M = [[m11, m12], [m21, m22]] per oscillator.
+ */
+int ossm_linoss_forward(const void* m11, const void* m12, const void* m21, const void* m22,
+                        const void* b_seq, void* states, int64_t length, int64_t batch,
+                        int64_t ssm, ossm_stream_t stream);
+
+/*
+ * LinOSS scan backward.  The reference has no native backward; this replaces
+ * the Python loop of _LinossScanFn.backward (models/linoss.py:83-151):
+ * g_t = grad_t + M^H g_{t+1};  grad_b_t = g_t;  grad_M_ij = sum g_i conj(s_j,t-1).
+ * grad_output, grad_b: [L,B,P,2] c64;  grad_m: [P,2,2] c64 (overwritten).
+ */
+int ossm_linoss_backward(const void* m11, const void* m12, const void* m21, const void* m22,
+                         const void* states, const void* grad_output, void* grad_m,
+                         void* grad_b, int64_t length, int64_t batch, int64_t ssm,
+                         ossm_stream_t stream);
+
+/* Number of time chunks the selective scan keeps checkpoints for (length > 0). */
+int64_t ossm_selective_num_chunks(int64_t length);
+
+/*
+ * Selective scan forward, replaces selective_scan_cuda_forward
+ * (selective_scan_cuda.cu:253-310) and, on the device, selective_scan_cpu
+ * (selective_scan_cpu.cpp:78-166):
+ *   h_t = exp(dt_t A_dn) h_{t-1} + dt_t Bm_tn u_t,  y_t = sum_n Cm_tn h_t,
+ *   out_t = y_t * silu(gate_t)  (out = y when gate == NULL).
+ * raw_out [B,D,L] receives y (may be NULL, or equal to out when gate == NULL).
+ * chunk_states [B,D,n_chunks,2N] f32 receives, per chunk, the state h at the
+ * chunk's end (first N) and exp(A * sum dt over the chunk) (last N); it may be
+ * NULL.  dstate <= 256.
+ */
+int ossm_selective_forward(const float* u, const float* dt, const float* A, const float* Bm,
+                           const float* Cm, const float* gate, float* out, float* raw_out,
+                           float* chunk_states, int64_t batch, int64_t dim, int64_t length,
+                           int64_t dstate, ossm_stream_t stream);
+
+/*
+ * Selective scan backward, replaces selective_scan_cuda_backward
+ * (selective_scan_cuda.cu:312-393) and selective_scan_cpu_backward
+ * (selective_scan_cpu.cpp:168-360).  chunk_states must come from
+ * ossm_selective_forward on the same inputs.  Writes du, ddt [B,D,L],
+ * dA [D,N], dB, dC [B,L,N] (all overwritten) and dgate [B,D,L] (zeros when
+ * gate == NULL; may be NULL then).
+ */
+int ossm_selective_backward(const float* grad_out, const float* u, const float* dt,
+                            const float* A, const float* Bm, const float* Cm, const float* gate,
+                            const float* chunk_states, float* du, float* ddt, float* dA,
+                            float* dB, float* dC, float* dgate, int64_t batch, int64_t dim,
+                            int64_t length, int64_t dstate, ossm_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OSSM_SCAN_H */

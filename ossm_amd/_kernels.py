@@ -1,0 +1,392 @@
+"""Drop-in replacement for the reference extension module ``ossm._kernels``.
+
+Same names, argument order, keyword names, return structure and RuntimeError
+messages as the pybind module of the reference (src/ossm/csrc/bindings.cpp:159-224),
+so the reference's kernel bridges (models/_dlinoss_scan.py, _linoss_scan.py,
+_selective_scan.py) run unchanged on top of it.  Device tensors (ROCm tensors
+report ``is_cuda``) run on the MI355X through libossm_scan.so; outputs are
+allocated here with torch's caching allocator on the input's device and
+stream, and the library only launches kernels.
+
+CPU tensors are not this module's job.  The reference's CPU kernels can be
+attached with :func:`set_cpu_delegate` (any object exposing the reference's
+CPU entry points, e.g. the reference's own ``ossm._kernels`` build); without a
+delegate a CPU call raises RuntimeError, which the reference bridges treat as
+"kernel unavailable".
+
+Export-only names with no HIP implementation in this build (sdlinoss_*,
+lru_scan, s5_scan, linear_rnn_scan) exist so attribute lookups behave like the
+reference's module; on device tensors they raise RuntimeError.
+"""
+
+from __future__ import annotations
+
+from typing import Any, List, Optional
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "linoss_scan",
+    "linoss_scan_backward",
+    "dlinoss_imex1_forward", "dlinoss_imex1_backward",
+    "dlinoss_imex2_forward", "dlinoss_imex2_backward",
+    "dlinoss_im_forward", "dlinoss_im_backward",
+    "dlinoss_ex_forward", "dlinoss_ex_backward",
+    "selective_scan", "selective_scan_backward",
+    "selective_scan_cuda", "selective_scan_cuda_backward",
+    "sdlinoss_imex1_forward", "sdlinoss_imex1_backward",
+    "sdlinoss_imex2_forward", "sdlinoss_imex2_backward",
+    "sdlinoss_im_forward", "sdlinoss_im_backward",
+    "sdlinoss_ex_forward", "sdlinoss_ex_backward",
+    "lru_scan", "s5_scan", "linear_rnn_scan",
+    "set_cpu_delegate",
+]
+
+_VARIANT_CODE = {"imex1": 0, "imex2": 1, "im": 2, "ex": 3}
+_MAX_DSTATE = 256  # reference MAX_DSTATE (selective_scan_common.h:41)
+
+_cpu_delegate: Optional[Any] = None
+
+
+def set_cpu_delegate(module: Optional[Any]) -> None:
+    """Route CPU-tensor calls to ``module`` (an object with the reference's CPU
+    entry points).  ``None`` removes the delegate."""
+    global _cpu_delegate
+    _cpu_delegate = module
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _delegate(name: str, *args):
+    if _cpu_delegate is None or not hasattr(_cpu_delegate, name):
+        raise RuntimeError(
+            f"{name}: CPU tensors are not handled by the MI355X scan library "
+            "(no CPU delegate attached)")
+    return getattr(_cpu_delegate, name)(*args)
+
+
+def _on_device(*tensors: Optional[torch.Tensor]) -> None:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        _check(t.is_cuda, "All tensors must be on the same device")
+        if dev is None:
+            dev = t.device
+        _check(t.device == dev, "All tensors must be on the same device")
+
+
+# ------------------------------------------------------------------- D-LinOSS
+def _dlinoss_forward(variant: str, a_diag, g_diag, step, bu):
+    # dlinoss_imex1.cpp:317-352 (same checks in the other variants)
+    _check(a_diag.dim() == 1 and g_diag.dim() == 1 and step.dim() == 1,
+           "Coefficient diagonals must be 1-D tensors")
+    _check(bu.dim() == 3, "bu must have shape (length, batch, ssm_size)")
+    length, batch, ssm = bu.shape
+    _check(a_diag.size(0) == ssm and g_diag.size(0) == ssm and step.size(0) == ssm,
+           "Coefficient diagonals must match state size")
+    output = torch.empty((length, batch, ssm, 2), dtype=bu.dtype, device=bu.device)
+    if length == 0:
+        return output
+    _check(a_diag.is_contiguous() and g_diag.is_contiguous() and step.is_contiguous(),
+           "Coefficient diagonals must be contiguous")
+    _check(bu.is_contiguous(), "bu must be contiguous")
+    if not bu.is_cuda:
+        return _delegate(f"dlinoss_{variant}_forward", a_diag, g_diag, step, bu)
+    _on_device(a_diag, g_diag, step, bu)
+    _check(bu.dtype == torch.complex64 and a_diag.dtype == torch.float32
+           and g_diag.dtype == torch.float32 and step.dtype == torch.float32,
+           f"dlinoss_{variant} HIP kernel supports complex64 bu with float32 coefficients")
+    with torch.cuda.device(bu.device):
+        _lib.check(_lib.load().ossm_dlinoss_forward(
+            _VARIANT_CODE[variant], a_diag.data_ptr(), g_diag.data_ptr(), step.data_ptr(),
+            bu.data_ptr(), output.data_ptr(), length, batch, ssm, _lib.stream_of(bu)))
+    return output
+
+
+def _dlinoss_backward(variant: str, a_diag, g_diag, step, bu, states, grad_output):
+    # dlinoss_imex1.cpp:354-390
+    _check(a_diag.dim() == 1 and g_diag.dim() == 1 and step.dim() == 1,
+           "Coefficient diagonals must be 1-D tensors")
+    _check(states.dim() == 4 and states.size(3) == 2,
+           "states must have shape (length, batch, ssm_size, 2)")
+    _check(bu.dim() == 3, "bu must have shape (length, batch, ssm_size)")
+    _check(grad_output.shape == bu.shape, "grad_output must match bu shape")
+    length, batch, ssm = bu.shape
+    _check(a_diag.size(0) == ssm and g_diag.size(0) == ssm and step.size(0) == ssm,
+           "Coefficient diagonals must match state size")
+    _check(tuple(states.shape[:3]) == (length, batch, ssm),
+           "states must have shape (length, batch, ssm_size, 2)")
+    grad_a = torch.zeros_like(a_diag)
+    grad_g = torch.zeros_like(g_diag)
+    grad_step = torch.zeros_like(step)
+    grad_bu = torch.empty_like(bu)
+    if length == 0:
+        return [grad_a, grad_g, grad_step, grad_bu]
+    _check(a_diag.is_contiguous() and g_diag.is_contiguous() and step.is_contiguous(),
+           "Coefficient diagonals must be contiguous")
+    _check(bu.is_contiguous(), "bu must be contiguous")
+    _check(states.is_contiguous() and grad_output.is_contiguous(),
+           "states and grad_output must be contiguous")
+    if not bu.is_cuda:
+        return _delegate(f"dlinoss_{variant}_backward", a_diag, g_diag, step, bu, states,
+                         grad_output)
+    _on_device(a_diag, g_diag, step, bu, states, grad_output)
+    _check(bu.dtype == torch.complex64 and states.dtype == torch.complex64
+           and grad_output.dtype == torch.complex64 and a_diag.dtype == torch.float32
+           and g_diag.dtype == torch.float32 and step.dtype == torch.float32,
+           f"dlinoss_{variant} HIP kernel supports complex64 tensors with float32 coefficients")
+    with torch.cuda.device(bu.device):
+        _lib.check(_lib.load().ossm_dlinoss_backward(
+            _VARIANT_CODE[variant], a_diag.data_ptr(), g_diag.data_ptr(), step.data_ptr(),
+            bu.data_ptr(), states.data_ptr(), grad_output.data_ptr(), grad_a.data_ptr(),
+            grad_g.data_ptr(), grad_step.data_ptr(), grad_bu.data_ptr(), length, batch, ssm,
+            _lib.stream_of(bu)))
+    return [grad_a, grad_g, grad_step, grad_bu]
+
+
+def dlinoss_imex1_forward(a_diag, g_diag, step, bu):
+    return _dlinoss_forward("imex1", a_diag, g_diag, step, bu)
+
+
+def dlinoss_imex1_backward(a_diag, g_diag, step, bu, states, grad_output):
+    return _dlinoss_backward("imex1", a_diag, g_diag, step, bu, states, grad_output)
+
+
+def dlinoss_imex2_forward(a_diag, g_diag, step, bu):
+    return _dlinoss_forward("imex2", a_diag, g_diag, step, bu)
+
+
+def dlinoss_imex2_backward(a_diag, g_diag, step, bu, states, grad_output):
+    return _dlinoss_backward("imex2", a_diag, g_diag, step, bu, states, grad_output)
+
+
+def dlinoss_im_forward(a_diag, g_diag, step, bu):
+    return _dlinoss_forward("im", a_diag, g_diag, step, bu)
+
+
+def dlinoss_im_backward(a_diag, g_diag, step, bu, states, grad_output):
+    return _dlinoss_backward("im", a_diag, g_diag, step, bu, states, grad_output)
+
+
+def dlinoss_ex_forward(a_diag, g_diag, step, bu):
+    return _dlinoss_forward("ex", a_diag, g_diag, step, bu)
+
+
+def dlinoss_ex_backward(a_diag, g_diag, step, bu, states, grad_output):
+    return _dlinoss_backward("ex", a_diag, g_diag, step, bu, states, grad_output)
+
+
+# --------------------------------------------------------------------- LinOSS
+def linoss_scan(m11, m12, m21, m22, b_seq):
+    """linoss_scan.cpp:115-146."""
+    output = torch.empty_like(b_seq)
+    if b_seq.size(0) == 0:
+        return output
+    _check(b_seq.dim() == 4,
+           f"b_seq must have shape (length, batch, ssm_size, 2), got {list(b_seq.shape)}")
+    _check(m11.is_contiguous() and m12.is_contiguous() and m21.is_contiguous()
+           and m22.is_contiguous(), "Coefficient tensors must be contiguous")
+    _check(b_seq.is_contiguous(), "b_seq must be contiguous")
+    if not b_seq.is_cuda:
+        return _delegate("linoss_scan", m11, m12, m21, m22, b_seq)
+    length, batch, ssm, two = b_seq.shape
+    _check(two == 2, "b_seq must have shape (length, batch, ssm_size, 2)")
+    _on_device(m11, m12, m21, m22, b_seq)
+    for m in (m11, m12, m21, m22):
+        _check(m.dim() == 1 and m.size(0) == ssm, "Coefficient tensors must have shape (ssm_size,)")
+        _check(m.dtype == torch.complex64, "linoss_scan HIP kernel supports complex64 only")
+    _check(b_seq.dtype == torch.complex64, "linoss_scan HIP kernel supports complex64 only")
+    with torch.cuda.device(b_seq.device):
+        _lib.check(_lib.load().ossm_linoss_forward(
+            m11.data_ptr(), m12.data_ptr(), m21.data_ptr(), m22.data_ptr(), b_seq.data_ptr(),
+            output.data_ptr(), length, batch, ssm, _lib.stream_of(b_seq)))
+    return output
+
+
+def linoss_scan_backward(m11, m12, m21, m22, states, grad_output):
+    """Native backward of :func:`linoss_scan` (the reference runs it as a Python
+    loop, models/linoss.py:83-151).  Returns ``[grad_m [P,2,2], grad_b [L,B,P,2]]``."""
+    _check(states.dim() == 4 and states.size(3) == 2,
+           "states must have shape (length, batch, ssm_size, 2)")
+    _check(grad_output.shape == states.shape, "grad_output must match states shape")
+    length, batch, ssm, _ = states.shape
+    grad_m = torch.zeros((ssm, 2, 2), dtype=states.dtype, device=states.device)
+    grad_b = torch.empty_like(grad_output)
+    if length == 0:
+        return [grad_m, grad_b]
+    _check(states.is_cuda, "linoss_scan_backward: HIP path needs device tensors")
+    _on_device(m11, m12, m21, m22, states, grad_output)
+    for m in (m11, m12, m21, m22):
+        _check(m.dim() == 1 and m.size(0) == ssm and m.is_contiguous()
+               and m.dtype == torch.complex64, "Coefficient tensors must be contiguous complex64 (ssm_size,)")
+    _check(states.is_contiguous() and grad_output.is_contiguous(),
+           "states and grad_output must be contiguous")
+    _check(states.dtype == torch.complex64 and grad_output.dtype == torch.complex64,
+           "linoss_scan_backward HIP kernel supports complex64 only")
+    with torch.cuda.device(states.device):
+        _lib.check(_lib.load().ossm_linoss_backward(
+            m11.data_ptr(), m12.data_ptr(), m21.data_ptr(), m22.data_ptr(), states.data_ptr(),
+            grad_output.data_ptr(), grad_m.data_ptr(), grad_b.data_ptr(), length, batch, ssm,
+            _lib.stream_of(states)))
+    return [grad_m, grad_b]
+
+
+# ------------------------------------------------------------- selective scan
+def _selective_checks(inputs, dt, A, B, C, gate, name: str) -> None:
+    # selective_scan_cuda.cu:60-102 (CPU twin: selective_scan_cpu.cpp:15-56)
+    _check(inputs.dtype == torch.float32, f"{name} requires float32 inputs")
+    _check(inputs.dim() == 3, "inputs must have shape (batch, channels, length)")
+    _check(dt.device == inputs.device, "dt must be on the same device as inputs")
+    _check(dt.dtype == torch.float32, "dt must be float32")
+    _check(dt.shape == inputs.shape, "dt shape mismatch")
+    _check(A.device == inputs.device, "A must be on the same device as inputs")
+    _check(A.dtype == torch.float32, "A must be float32")
+    _check(A.dim() == 2, "A must have shape (channels, state)")
+    _check(A.size(0) == inputs.size(1), "A channels mismatch")
+    _check(A.size(1) > 0, "state dimension must be positive")
+    _check(A.size(1) <= _MAX_DSTATE,
+           f"state dimension exceeds supported maximum ({_MAX_DSTATE})")
+    _check(B.device == inputs.device, "B must be on the same device as inputs")
+    _check(B.dtype == torch.float32, "B must be float32")
+    _check(B.dim() == 3, "B must have shape (batch, length, state)")
+    _check(B.size(0) == inputs.size(0) and B.size(1) == inputs.size(2) and B.size(2) == A.size(1),
+           "B shape mismatch")
+    _check(C.device == inputs.device, "C must be on the same device as inputs")
+    _check(C.dtype == torch.float32, "C must be float32")
+    _check(C.dim() == 3, "C must have shape (batch, length, state)")
+    _check(C.shape == B.shape, "C shape mismatch")
+    if gate is not None:
+        _check(gate.device == inputs.device, "gate must be on the same device as inputs")
+        _check(gate.dtype == torch.float32, "gate must be float32")
+        _check(gate.shape == inputs.shape, "gate shape mismatch")
+
+
+def _num_chunks(length: int) -> int:
+    return int(_lib.load().ossm_selective_num_chunks(length))
+
+
+def selective_scan_cuda(inputs, dt, A, B, C, gate=None, chunk_length=16):
+    """selective_scan_cuda.cu:253-310: returns ``[outputs, chunk_states, raw_outputs]``.
+
+    ``chunk_length`` is accepted and ignored, as in the reference (:259)."""
+    _check(inputs.is_cuda, "inputs must be CUDA tensor")
+    _selective_checks(inputs, dt, A, B, C, gate, "selective_scan_cuda")
+    batch, dim, length = inputs.shape
+    dstate = A.size(1)
+    if length == 0:
+        return [torch.zeros_like(inputs),
+                torch.zeros((batch, dim, 0, dstate * 2), dtype=inputs.dtype, device=inputs.device),
+                torch.zeros_like(inputs)]
+    u, d, a, b, c = (x.contiguous() for x in (inputs, dt, A, B, C))
+    z = gate.contiguous() if gate is not None else None
+    raw = torch.empty_like(u)
+    out = torch.empty_like(u) if z is not None else raw
+    chunks = torch.empty((batch, dim, _num_chunks(length), dstate * 2), dtype=u.dtype,
+                         device=u.device)
+    with torch.cuda.device(u.device):
+        _lib.check(_lib.load().ossm_selective_forward(
+            u.data_ptr(), d.data_ptr(), a.data_ptr(), b.data_ptr(), c.data_ptr(), _lib.ptr(z),
+            out.data_ptr(), raw.data_ptr(), chunks.data_ptr(), batch, dim, length, dstate,
+            _lib.stream_of(u)))
+    return [out, chunks, raw]
+
+
+def selective_scan_cuda_backward(grad_output, inputs, dt, A, B, C, gate=None, chunk_states=None,
+                                 raw_outputs=None, chunk_length=None):
+    """selective_scan_cuda.cu:312-393: returns ``[du, ddt, dA, dB, dC, dgate]``.
+
+    ``raw_outputs`` is checked like the reference does but not read: the
+    backward recomputes y from the chunk checkpoints."""
+    _check(inputs.is_cuda, "inputs must be CUDA tensor")
+    _selective_checks(inputs, dt, A, B, C, gate, "selective_scan_cuda")
+    _check(grad_output.device == inputs.device, "grad_output must be on the same device as inputs")
+    _check(grad_output.dtype == torch.float32, "grad_output must be float32")
+    _check(grad_output.shape == inputs.shape, "grad_output shape mismatch")
+    _check(chunk_states is not None, "chunk_states must have shape (batch, channels, num_chunks, state * 2)")
+    _check(chunk_states.device == inputs.device, "chunk_states must be on the same device as inputs")
+    _check(chunk_states.dtype == torch.float32, "chunk_states must be float32")
+    _check(chunk_states.dim() == 4,
+           "chunk_states must have shape (batch, channels, num_chunks, state * 2)")
+    if raw_outputs is not None:
+        _check(raw_outputs.device == inputs.device, "raw_outputs must be on the same device as inputs")
+        _check(raw_outputs.dtype == torch.float32, "raw_outputs must be float32")
+        _check(raw_outputs.shape == inputs.shape, "raw_outputs shape mismatch")
+    batch, dim, length = inputs.shape
+    dstate = A.size(1)
+    u, d, a, b, c = (x.contiguous() for x in (inputs, dt, A, B, C))
+    z = gate.contiguous() if gate is not None else None
+    gout = grad_output.contiguous()
+    du, ddt = torch.empty_like(u), torch.empty_like(d)
+    dA = torch.zeros_like(a)
+    dB, dC = torch.zeros_like(b), torch.zeros_like(c)
+    dz = torch.zeros_like(u)
+    if length == 0:
+        return [du, ddt, dA, dB, dC, dz]
+    cs = chunk_states.contiguous()
+    _check(tuple(cs.shape) == (batch, dim, _num_chunks(length), 2 * dstate),
+           "chunk_states do not match this library's forward for these inputs")
+    with torch.cuda.device(u.device):
+        _lib.check(_lib.load().ossm_selective_backward(
+            gout.data_ptr(), u.data_ptr(), d.data_ptr(), a.data_ptr(), b.data_ptr(), c.data_ptr(),
+            _lib.ptr(z), cs.data_ptr(), du.data_ptr(), ddt.data_ptr(), dA.data_ptr(),
+            dB.data_ptr(), dC.data_ptr(), dz.data_ptr(), batch, dim, length, dstate,
+            _lib.stream_of(u)))
+    return [du, ddt, dA, dB, dC, dz]
+
+
+def selective_scan(inputs, dt, A, B, C, gate=None):
+    """selective_scan_cpu.cpp:78-166 entry; device tensors run the HIP kernel."""
+    if not inputs.is_cuda:
+        return _delegate("selective_scan", inputs, dt, A, B, C, gate)
+    return selective_scan_cuda(inputs, dt, A, B, C, gate)[0]
+
+
+def selective_scan_backward(grad_output, inputs, dt, A, B, C, gate=None):
+    """selective_scan_cpu.cpp:168-360 entry; device tensors re-run the forward
+    for its checkpoints, then the HIP backward."""
+    if not inputs.is_cuda:
+        return _delegate("selective_scan_backward", grad_output, inputs, dt, A, B, C, gate)
+    _, chunks, raw = selective_scan_cuda(inputs, dt, A, B, C, gate)
+    return selective_scan_cuda_backward(grad_output, inputs, dt, A, B, C, gate, chunks, raw, 16)
+
+
+# ------------------------------------------------------ export-only names
+def _export_only(name: str):
+    def fn(*args, **kwargs):
+        tensors = [a for a in args if isinstance(a, torch.Tensor)]
+        if tensors and not tensors[0].is_cuda:
+            return _delegate(name, *args)
+        raise RuntimeError(f"{name} has no HIP implementation in this build")
+
+    fn.__name__ = name
+    fn.__doc__ = f"Export-only name of the reference module ({name}); see module docstring."
+    return fn
+
+
+sdlinoss_imex1_forward = _export_only("sdlinoss_imex1_forward")
+sdlinoss_imex1_backward = _export_only("sdlinoss_imex1_backward")
+sdlinoss_imex2_forward = _export_only("sdlinoss_imex2_forward")
+sdlinoss_imex2_backward = _export_only("sdlinoss_imex2_backward")
+sdlinoss_im_forward = _export_only("sdlinoss_im_forward")
+sdlinoss_im_backward = _export_only("sdlinoss_im_backward")
+sdlinoss_ex_forward = _export_only("sdlinoss_ex_forward")
+sdlinoss_ex_backward = _export_only("sdlinoss_ex_backward")
+lru_scan = _export_only("lru_scan")
+s5_scan = _export_only("s5_scan")
+linear_rnn_scan = _export_only("linear_rnn_scan")
+
+
+def _load_now() -> List[str]:
+    """Load the library (ImportError when missing) and return its exported ABI names."""
+    lib = _lib.load()
+    return [name for name in _lib.EXPORTED if hasattr(lib, name)]
+
+
+# Importing this module loads the library: a missing build fails loudly here.
+_load_now()

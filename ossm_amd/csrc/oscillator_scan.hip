@@ -1,0 +1,756 @@
+// Oscillatory 2x2 scans on gfx950: D-LinOSS (imex1, imex2, im, ex) and the
+// generic complex LinOSS scan, forward and backward.
+//
+// Layout and parallel decomposition
+//   The reference tensors are [L, B, P(, 2)] with the (b, p) channel index
+//   contiguous, so one wave = 64 consecutive channels and every per-step load
+//   or store is one coalesced row (512 B of bu, 1 KiB of states).  A
+//   workgroup of W waves owns one time chunk of W*T steps for its 64
+//   channels; wave w owns the sub-chunk of T steps starting at w*T.
+//
+// Forward (one pass over HBM: read bu once, write states once)
+//   1. each lane keeps its T inputs in registers and scans them from a zero
+//      state -> sub-chunk aggregate e_w;
+//   2. wave 0 combines the W aggregates through LDS with M^T (the sub-chunk
+//      transition) into the chunk aggregate, publishes it, and looks back over
+//      earlier chunks' records for the carry into the chunk (decoupled
+//      look-back, workgroups ordered by a launch ticket);
+//   3. every wave rebuilds its own carry from the LDS aggregates and re-runs
+//      its T steps from it, storing the states.
+//
+// Backward (reverse time; reads bu + grad once, states only at sub-chunk
+// starts, writes grad_bu once)
+//   The adjoint mu_t = M^T mu_{t+1} + (0, g_t) is the same chunked scan run
+//   backwards with the transposed transition.  States s_{t-1} needed by the
+//   parameter gradients are recomputed in registers from the checkpoint
+//   states[t0 - 1] instead of reading the whole trajectory.  Per-lane sums of
+//   <mu_i, s_j,t-1> and <mu_i, bu_t> go to a partials buffer; a second small
+//   kernel reduces them per oscillator in a fixed order (deterministic, fp64)
+//   and applies each variant's chain rule to (a, g, dt).
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+#include <cstdlib>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/ossm_scan.h"
+#include "runtime.hpp"
+#include "scan_device.hpp"
+
+namespace ossm {
+namespace {
+
+// ============================================================================
+// Models: what one step of each recurrence does.
+// ============================================================================
+
+// D-LinOSS per-oscillator coefficients, named as in the reference forward
+// kernels:  new0 = c0*s0 + c1*s1 + c2*bu ;  new1 = c3*s0 + c4*s1 + c5*bu,
+// except imex1 (new1 = new0 + s1, dlinoss_imex1.cpp:75-78) and ex
+// (new1 = c3*s0 + s1, dlinoss_ex.cpp:70-71).
+struct DlCoef {
+  float c0, c1, c2, c3, c4, c5;
+};
+
+template <int V>
+struct Dlinoss {
+  using In = float2;    // bu_t
+  using GIn = float2;   // grad of x_t
+  using GOut = float2;  // grad of bu_t
+  using Mat = RMat;
+  using Coef = DlCoef;
+  static constexpr int kSums = 6;
+  static constexpr bool kRecompute = true;  // s_{t-1} rebuilt from bu and a checkpoint
+
+  struct Params {
+    const float* a;
+    const float* g;
+    const float* dt;
+    int P;
+  };
+
+  // dlinoss_imex1.cpp:32-48, dlinoss_imex2.cpp:35-47, dlinoss_im.cpp:34-50, dlinoss_ex.cpp:33-42
+  static __device__ __forceinline__ Coef coef(const Params& prm, int ch) {
+    const int p = ch % prm.P;
+    const float alpha = prm.a[p], gamma = prm.g[p], sigma = prm.dt[p];
+    Coef k;
+    if constexpr (V == OSSM_DLINOSS_IMEX1) {
+      const float inv = 1.f / (1.f + sigma * gamma);
+      const float s2i = sigma * sigma * inv;
+      k = {inv, -alpha * s2i, s2i, 0.f, 0.f, 0.f};
+    } else if constexpr (V == OSSM_DLINOSS_IMEX2) {
+      const float s2 = sigma * sigma;
+      k = {1.f - sigma * gamma, -sigma * alpha, sigma, sigma - s2 * gamma, 1.f - s2 * alpha, s2};
+    } else if constexpr (V == OSSM_DLINOSS_IM) {
+      const float s2 = sigma * sigma;
+      const float inv = 1.f / (1.f + sigma * gamma + s2 * alpha);
+      const float si = sigma * inv;
+      k = {inv, -alpha * si, si, si, (1.f + sigma * gamma) * inv, s2 * inv};
+    } else {
+      k = {1.f - sigma * gamma, -sigma * alpha, sigma, sigma, 0.f, 0.f};
+    }
+    return k;
+  }
+
+  static __device__ __forceinline__ float4 step(const Coef& k, float4 s, float2 bu) {
+    const float n0r = s.x * k.c0 + s.z * k.c1 + bu.x * k.c2;
+    const float n0i = s.y * k.c0 + s.w * k.c1 + bu.y * k.c2;
+    if constexpr (V == OSSM_DLINOSS_IMEX1) {
+      return make_float4(n0r, n0i, n0r + s.z, n0i + s.w);
+    } else if constexpr (V == OSSM_DLINOSS_EX) {
+      return make_float4(n0r, n0i, s.x * k.c3 + s.z, s.y * k.c3 + s.w);
+    } else {
+      return make_float4(n0r, n0i, s.x * k.c3 + s.z * k.c4 + bu.x * k.c5,
+                         s.y * k.c3 + s.w * k.c4 + bu.y * k.c5);
+    }
+  }
+
+  // The homogeneous step as a matrix (columns = step of the unit vectors).
+  static __device__ __forceinline__ Mat matrix(const Coef& k) {
+    const float4 e0 = step(k, make_float4(1.f, 0.f, 0.f, 0.f), make_float2(0.f, 0.f));
+    const float4 e1 = step(k, make_float4(0.f, 0.f, 1.f, 0.f), make_float2(0.f, 0.f));
+    return {e0.x, e1.x, e0.z, e1.z};
+  }
+
+  // mu_t = carry + (0, g_t): the gradient w.r.t. the new state at t
+  // (grad_new0 = grad_state0, grad_new1 = grad_state1 + grad_out).
+  static __device__ __forceinline__ float4 mu(float4 carry, float2 go) {
+    return make_float4(carry.x, carry.y, carry.z + go.x, carry.w + go.y);
+  }
+
+  // carry to t-1 = M^T mu_t, in each variant's reference arithmetic
+  // (dlinoss_imex1.cpp:200-208, dlinoss_imex2.cpp:222-230, dlinoss_im.cpp:229-237,
+  //  dlinoss_ex.cpp:189-197).
+  static __device__ __forceinline__ float4 rev_carry(const Coef& k, float4 m) {
+    if constexpr (V == OSSM_DLINOSS_IMEX1) {
+      const float tr = m.x + m.z, ti = m.y + m.w;
+      return make_float4(tr * k.c0, ti * k.c0, m.z + tr * k.c1, m.w + ti * k.c1);
+    } else if constexpr (V == OSSM_DLINOSS_EX) {
+      return make_float4(m.x * k.c0 + m.z * k.c3, m.y * k.c0 + m.w * k.c3, m.x * k.c1 + m.z,
+                         m.y * k.c1 + m.w);
+    } else {
+      return make_float4(m.x * k.c0 + m.z * k.c3, m.y * k.c0 + m.w * k.c3,
+                         m.x * k.c1 + m.z * k.c4, m.y * k.c1 + m.w * k.c4);
+    }
+  }
+
+  // grad_bu_t = f^T mu_t
+  static __device__ __forceinline__ float2 grad_input(const Coef& k, float4 m) {
+    if constexpr (V == OSSM_DLINOSS_IMEX1) {
+      return make_float2((m.x + m.z) * k.c2, (m.y + m.w) * k.c2);
+    } else if constexpr (V == OSSM_DLINOSS_EX) {
+      return make_float2(m.x * k.c2, m.y * k.c2);
+    } else {
+      return make_float2(m.x * k.c2 + m.z * k.c5, m.y * k.c2 + m.w * k.c5);
+    }
+  }
+
+  // G_ij += <mu_i, s_j,t-1>,  F_i += <mu_i, bu_t>  (real inner products).
+  static __device__ __forceinline__ void accumulate(float* acc, float4 m, float4 sp, float2 bu) {
+    acc[0] += m.x * sp.x + m.y * sp.y;  // G00
+    acc[1] += m.x * sp.z + m.y * sp.w;  // G01
+    acc[2] += m.z * sp.x + m.w * sp.y;  // G10
+    acc[3] += m.z * sp.z + m.w * sp.w;  // G11
+    acc[4] += m.x * bu.x + m.y * bu.y;  // F0
+    acc[5] += m.z * bu.x + m.w * bu.y;  // F1
+  }
+};
+
+// Generic complex LinOSS: s_t = M s_{t-1} + b_t (linoss_scan.cpp:48-66).
+struct Linoss {
+  using In = float4;    // b_t (both components)
+  using GIn = float4;   // grad of s_t
+  using GOut = float4;  // grad of b_t
+  using Mat = CMat;
+  using Coef = CMat;
+  static constexpr int kSums = 8;
+  // The bridge keeps (M, states) but not b_seq (linoss.py:79), so the
+  // backward reads s_{t-1} from the saved trajectory.
+  static constexpr bool kRecompute = false;
+
+  struct Params {
+    const float2* m11;
+    const float2* m12;
+    const float2* m21;
+    const float2* m22;
+    int P;
+  };
+
+  static __device__ __forceinline__ Coef coef(const Params& prm, int ch) {
+    const int p = ch % prm.P;
+    return {prm.m11[p], prm.m12[p], prm.m21[p], prm.m22[p]};
+  }
+  static __device__ __forceinline__ float4 step(const Coef& m, float4 s, float4 b) {
+    return f4add(mat_apply(m, s), b);
+  }
+  static __device__ __forceinline__ Mat matrix(const Coef& m) { return m; }
+  static __device__ __forceinline__ float4 mu(float4 carry, float4 go) { return f4add(carry, go); }
+  // grad_next = M^H g (linoss.py:144-146)
+  static __device__ __forceinline__ float4 rev_carry(const Coef& m, float4 g) {
+    return mat_apply(mat_adjoint(m), g);
+  }
+  static __device__ __forceinline__ float4 grad_input(const Coef&, float4 g) { return g; }
+  // grad_M_ij += g_i * conj(s_j,t-1)  (linoss.py:129-133)
+  static __device__ __forceinline__ void accumulate(float* acc, float4 g, float4 sp, float4) {
+    acc[0] += g.x * sp.x + g.y * sp.y;  acc[1] += g.y * sp.x - g.x * sp.y;  // m11
+    acc[2] += g.x * sp.z + g.y * sp.w;  acc[3] += g.y * sp.z - g.x * sp.w;  // m12
+    acc[4] += g.z * sp.x + g.w * sp.y;  acc[5] += g.w * sp.x - g.z * sp.y;  // m21
+    acc[6] += g.z * sp.z + g.w * sp.w;  acc[7] += g.w * sp.z - g.z * sp.w;  // m22
+  }
+};
+
+template <class T>
+__device__ __forceinline__ T zero_of();
+template <>
+__device__ __forceinline__ float2 zero_of<float2>() { return make_float2(0.f, 0.f); }
+template <>
+__device__ __forceinline__ float4 zero_of<float4>() { return f4zero(); }
+
+// ============================================================================
+// Forward kernel
+// ============================================================================
+template <class Model, int T, int W>
+__global__ __launch_bounds__(W * kWave) void osc_forward_kernel(
+    typename Model::Params prm, const typename Model::In* __restrict__ in,
+    float4* __restrict__ out, int L, int nc, int n_groups, int n_chunks,
+    unsigned long long* __restrict__ rec, LaunchSync sync) {
+  __shared__ float4 s_agg[W][kWave];
+  __shared__ float4 s_carry[kWave];
+  __shared__ int s_ticket;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  const int ticket = draw_ticket(sync, n_groups * n_chunks, &s_ticket);
+  if (ticket < 0) return;
+  const int c = ticket / n_groups;
+  const int g = ticket - c * n_groups;
+  const int ch = g * kWave + lane;
+  const bool active = ch < nc;
+  const auto k = Model::coef(prm, active ? ch : 0);
+  const long long t0 = static_cast<long long>(c) * (T * W) + static_cast<long long>(w) * T;
+
+  typename Model::In x[T];
+#pragma unroll
+  for (int i = 0; i < T; ++i) {
+    const long long t = t0 + i;
+    x[i] = (active && t < L) ? in[static_cast<size_t>(t) * nc + ch] : zero_of<typename Model::In>();
+  }
+
+  // 1. sub-chunk aggregate from a zero state
+  float4 e = f4zero();
+#pragma unroll
+  for (int i = 0; i < T; ++i)
+    if (t0 + i < L) e = Model::step(k, e, x[i]);
+  s_agg[w][lane] = e;
+  const typename Model::Mat MT = mat_pow(Model::matrix(k), T);
+  __syncthreads();
+
+  // 2. chunk aggregate, look-back, inclusive prefix
+  if (w == 0) {
+    float4 E = f4zero();
+#pragma unroll
+    for (int v = 0; v < W; ++v) E = f4add(mat_apply(MT, E), s_agg[v][lane]);
+    float4 carry = f4zero();
+    if (active && n_chunks > 1) {
+      const typename Model::Mat MC = mat_pow(MT, W);
+      if (c == 0) {
+        rec_publish(rec, c, kRecInc, nc, ch, E, sync.tag);
+      } else {
+        rec_publish(rec, c, kRecAgg, nc, ch, E, sync.tag);
+        carry = lookback(rec, c, +1, n_chunks, nc, ch, MC, sync);
+        if (c + 1 < n_chunks) rec_publish(rec, c, kRecInc, nc, ch, f4add(mat_apply(MC, carry), E), sync.tag);
+      }
+    }
+    s_carry[lane] = carry;
+  }
+  __syncthreads();
+
+  // 3. own carry, then re-run the sub-chunk and store
+  float4 s = s_carry[lane];
+  for (int v = 0; v < w; ++v) s = f4add(mat_apply(MT, s), s_agg[v][lane]);
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      const long long t = t0 + i;
+      if (t < L) {
+        s = Model::step(k, s, x[i]);
+        out[static_cast<size_t>(t) * nc + ch] = s;
+      }
+    }
+  }
+}
+
+// ============================================================================
+// Backward kernel
+// ============================================================================
+template <class Model, int T, int W>
+__global__ __launch_bounds__(W * kWave) void osc_backward_kernel(
+    typename Model::Params prm, const typename Model::In* __restrict__ in,
+    const float4* __restrict__ states, const typename Model::GIn* __restrict__ gout,
+    typename Model::GOut* __restrict__ gin, float* __restrict__ partials, int L, int nc,
+    int n_groups, int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
+  constexpr int NS = Model::kSums;
+  __shared__ float4 s_agg[W][kWave];
+  __shared__ float4 s_carry[kWave];
+  __shared__ float s_sum[W][NS][kWave];
+  __shared__ int s_ticket;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  const int ticket = draw_ticket(sync, n_groups * n_chunks, &s_ticket);
+  if (ticket < 0) return;
+  const int cr = ticket / n_groups;          // chunks are handed out last-first
+  const int g = ticket - cr * n_groups;
+  const int c = n_chunks - 1 - cr;
+  const int ch = g * kWave + lane;
+  const bool active = ch < nc;
+  const auto k = Model::coef(prm, active ? ch : 0);
+  const long long t0 = static_cast<long long>(c) * (T * W) + static_cast<long long>(w) * T;
+
+  typename Model::In x[T];
+  typename Model::GIn go[T];
+  float4 sp[T];  // s_{t-1} for each step of the sub-chunk
+#pragma unroll
+  for (int i = 0; i < T; ++i) {
+    const long long t = t0 + i;
+    const bool ok = active && t < L;
+    if constexpr (Model::kRecompute) {
+      x[i] = ok ? in[static_cast<size_t>(t) * nc + ch] : zero_of<typename Model::In>();
+    } else {
+      x[i] = zero_of<typename Model::In>();
+      sp[i] = (ok && t >= 1) ? states[static_cast<size_t>(t - 1) * nc + ch] : f4zero();
+    }
+    go[i] = ok ? gout[static_cast<size_t>(t) * nc + ch] : zero_of<typename Model::GIn>();
+  }
+  if constexpr (Model::kRecompute) {
+    // rebuild s_{t-1} from the checkpoint states[t0 - 1] and the inputs
+    float4 s = (active && t0 >= 1 && t0 <= L) ? states[static_cast<size_t>(t0 - 1) * nc + ch] : f4zero();
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      sp[i] = s;
+      if (t0 + i < L) s = Model::step(k, s, x[i]);
+    }
+  }
+
+  // 1. reverse aggregate of the sub-chunk from a zero carry
+  float4 m = f4zero();
+#pragma unroll
+  for (int i = T - 1; i >= 0; --i)
+    if (t0 + i < L) m = Model::rev_carry(k, Model::mu(m, go[i]));
+  s_agg[w][lane] = m;
+  const typename Model::Mat KT = mat_pow(mat_adjoint(Model::matrix(k)), T);
+  __syncthreads();
+
+  // 2. chunk aggregate (waves W-1 .. 0), look-back over later chunks
+  if (w == 0) {
+    float4 E = f4zero();
+#pragma unroll
+    for (int v = W - 1; v >= 0; --v) E = f4add(mat_apply(KT, E), s_agg[v][lane]);
+    float4 carry = f4zero();
+    if (active && n_chunks > 1) {
+      const typename Model::Mat KC = mat_pow(KT, W);
+      if (c == n_chunks - 1) {
+        rec_publish(rec, c, kRecInc, nc, ch, E, sync.tag);
+      } else {
+        rec_publish(rec, c, kRecAgg, nc, ch, E, sync.tag);
+        carry = lookback(rec, c, -1, n_chunks, nc, ch, KC, sync);
+        if (c > 0) rec_publish(rec, c, kRecInc, nc, ch, f4add(mat_apply(KC, carry), E), sync.tag);
+      }
+    }
+    s_carry[lane] = carry;
+  }
+  __syncthreads();
+
+  // 3. own carry, final reverse pass: grad of the inputs and parameter sums
+  float4 y = s_carry[lane];
+  for (int v = W - 1; v > w; --v) y = f4add(mat_apply(KT, y), s_agg[v][lane]);
+  float acc[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) acc[j] = 0.f;
+  if (active) {
+#pragma unroll
+    for (int i = T - 1; i >= 0; --i) {
+      const long long t = t0 + i;
+      if (t < L) {
+        const float4 mu = Model::mu(y, go[i]);
+        gin[static_cast<size_t>(t) * nc + ch] = Model::grad_input(k, mu);
+        Model::accumulate(acc, mu, sp[i], x[i]);
+        y = Model::rev_carry(k, mu);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NS; ++j) s_sum[w][j][lane] = acc[j];
+  __syncthreads();
+  if (w == 0 && active) {
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      float v = 0.f;
+      for (int u = 0; u < W; ++u) v += s_sum[u][j][lane];
+      partials[(static_cast<size_t>(c) * NS + j) * nc + ch] = v;
+    }
+  }
+}
+
+// ============================================================================
+// Per-oscillator reduction of the partial sums + chain rule
+// ============================================================================
+constexpr int kReduceThreads = 256;
+
+// Zero-fill used where the reference returns zero gradients (empty scans);
+// a kernel rather than hipMemsetAsync so the call can sit in a captured graph.
+__global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
+int fill_zero(float* p, int64_t n, hipStream_t stream) {
+  if (n <= 0) return OSSM_OK;
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, p, n);
+  return launch_check("fill_zero_kernel");
+}
+
+template <int NS>
+__device__ void reduce_sums(const float* __restrict__ partials, int p, int P, int B, int n_chunks,
+                            int nc, double* out) {
+  __shared__ double s_red[NS][kReduceThreads];
+  double acc[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) acc[j] = 0.0;
+  const int items = n_chunks * B;
+  for (int it = threadIdx.x; it < items; it += kReduceThreads) {
+    const int c = it / B, b = it - c * B;
+    const size_t chi = static_cast<size_t>(b) * P + p;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) acc[j] += partials[(static_cast<size_t>(c) * NS + j) * nc + chi];
+  }
+#pragma unroll
+  for (int j = 0; j < NS; ++j) s_red[j][threadIdx.x] = acc[j];
+  __syncthreads();
+  for (int off = kReduceThreads / 2; off > 0; off >>= 1) {
+    if (threadIdx.x < off) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j) s_red[j][threadIdx.x] += s_red[j][threadIdx.x + off];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < NS; ++j) out[j] = s_red[j][0];
+}
+
+// Chain rule from the generic sums (G00, G01, G10, G11, F0, F1) to (a, g, dt):
+// imex1 dlinoss_imex1.cpp:219-232, im dlinoss_im.cpp:236-263, imex2/ex by
+// differentiating the coefficient tables of dlinoss_imex2.cpp:35-47 /
+// dlinoss_ex.cpp:33-42 (the same terms the reference accumulates per step).
+template <int V>
+__global__ __launch_bounds__(kReduceThreads) void dlinoss_param_grad_kernel(
+    const float* __restrict__ partials, const float* __restrict__ a_diag,
+    const float* __restrict__ g_diag, const float* __restrict__ step, float* __restrict__ grad_a,
+    float* __restrict__ grad_g, float* __restrict__ grad_step, int P, int B, int n_chunks, int nc) {
+  const int p = blockIdx.x;
+  double S[6];
+  reduce_sums<6>(partials, p, P, B, n_chunks, nc, S);
+  if (threadIdx.x != 0) return;
+  const double G00 = S[0], G01 = S[1], G10 = S[2], G11 = S[3], F0 = S[4], F1 = S[5];
+  const double a = a_diag[p], g = g_diag[p], dt = step[p];
+  double ga, gg, gs;
+  if constexpr (V == OSSM_DLINOSS_IMEX1) {
+    const double inv = 1.0 / (1.0 + dt * g);
+    const double s2i = dt * dt * inv;
+    const double ginv = G00 + G10;
+    const double gs2i = F0 + F1 - a * (G01 + G11);
+    ga = -s2i * (G01 + G11);
+    const double inv_total = ginv + gs2i * dt * dt;
+    gs = gs2i * (2.0 * dt * inv) - inv_total * g * inv * inv;
+    gg = -inv_total * dt * inv * inv;
+  } else if constexpr (V == OSSM_DLINOSS_IMEX2) {
+    ga = -dt * G01 - dt * dt * G11;
+    gg = -dt * G00 - dt * dt * G10;
+    gs = -g * G00 - a * G01 + (1.0 - 2.0 * dt * g) * G10 - 2.0 * dt * a * G11 + F0 + 2.0 * dt * F1;
+  } else if constexpr (V == OSSM_DLINOSS_IM) {
+    const double inv = 1.0 / (1.0 + dt * g + dt * dt * a);
+    const double si = dt * inv;
+    double gsi = F0 + G10, ginv = G00;
+    const double gs2i = F1;
+    gsi += G01 * (-a);
+    ga = G01 * (-si);
+    ginv += G11 * (1.0 + dt * g);
+    const double gt = G11 * inv;
+    gg = gt * dt;
+    gs = gt * g;
+    gs += gsi * inv;
+    ginv += gsi * dt;
+    gs += gs2i * (2.0 * dt * inv);
+    ginv += gs2i * dt * dt;
+    const double gden = -ginv * inv * inv;
+    ga += gden * dt * dt;
+    gg += gden * dt;
+    gs += gden * (g + 2.0 * dt * a);
+  } else {
+    ga = -dt * G01;
+    gg = -dt * G00;
+    gs = -g * G00 - a * G01 + F0 + G10;
+  }
+  grad_a[p] = static_cast<float>(ga);
+  grad_g[p] = static_cast<float>(gg);
+  grad_step[p] = static_cast<float>(gs);
+}
+
+__global__ __launch_bounds__(kReduceThreads) void linoss_param_grad_kernel(
+    const float* __restrict__ partials, float* __restrict__ grad_m, int P, int B, int n_chunks,
+    int nc) {
+  const int p = blockIdx.x;
+  double S[8];
+  reduce_sums<8>(partials, p, P, B, n_chunks, nc, S);
+  if (threadIdx.x != 0) return;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) grad_m[8 * p + j] = static_cast<float>(S[j]);
+}
+
+// ============================================================================
+// Host dispatch
+// ============================================================================
+struct Tile {
+  int T, W;
+};
+
+Tile parse_tile(const char* env, Tile dflt) {
+  const char* s = std::getenv(env);
+  if (!s) return dflt;
+  int t = 0, w = 0;
+  if (std::sscanf(s, "%dx%d", &t, &w) != 2) return dflt;
+  return {t, w};
+}
+
+// Instantiated tiles (T steps per lane, W waves per workgroup).
+#define OSSM_FWD_TILES(X) X(8, 8) X(16, 4) X(16, 8) X(16, 16) X(32, 8)
+#define OSSM_BWD_TILES(X) X(8, 4) X(8, 8) X(8, 16) X(16, 4) X(16, 8)
+
+template <class Model>
+int launch_forward(const typename Model::Params& prm, const void* in, void* out, int64_t L,
+                   int64_t nc, hipStream_t stream) {
+  static const Tile tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{16, 8});
+  const int64_t CL = int64_t(tile.T) * tile.W;
+  const int64_t n_chunks = (L + CL - 1) / CL;
+  const int64_t n_groups = (nc + kWave - 1) / kWave;
+  if (n_chunks * n_groups > INT_MAX)
+    return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
+  const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
+  void* payload = nullptr;
+  LaunchSync sync{};
+  if (int rc = acquire_scratch(stream, rec_bytes, n_chunks * n_groups, &payload, &sync)) return rc;
+  const dim3 grid(static_cast<unsigned>(n_chunks * n_groups));
+  bool launched = false;
+#define OSSM_LAUNCH_FWD(TT, WW)                                                               \
+  if (!launched && tile.T == TT && tile.W == WW) {                                            \
+    hipLaunchKernelGGL((osc_forward_kernel<Model, TT, WW>), grid, dim3(WW * kWave), 0, stream, \
+                       prm, static_cast<const typename Model::In*>(in),                       \
+                       static_cast<float4*>(out), static_cast<int>(L), static_cast<int>(nc),  \
+                       static_cast<int>(n_groups), static_cast<int>(n_chunks),                \
+                       static_cast<unsigned long long*>(payload), sync);                      \
+    launched = true;                                                                          \
+  }
+  OSSM_FWD_TILES(OSSM_LAUNCH_FWD)
+#undef OSSM_LAUNCH_FWD
+  if (!launched) {
+    release_unlaunched(stream, n_chunks * n_groups);
+    return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_FWD names no built tile");
+  }
+  if (int rc = launch_check("osc_forward_kernel")) {
+    release_unlaunched(stream, n_chunks * n_groups);
+    return rc;
+  }
+  return OSSM_OK;
+}
+
+template <class Model>
+int launch_backward(const typename Model::Params& prm, const void* in, const void* states,
+                    const void* gout, void* gin, int64_t L, int64_t nc, float** partials_out,
+                    int64_t* n_chunks_out, hipStream_t stream) {
+  static const Tile tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{8, 8});
+  const int64_t CL = int64_t(tile.T) * tile.W;
+  const int64_t n_chunks = (L + CL - 1) / CL;
+  const int64_t n_groups = (nc + kWave - 1) / kWave;
+  if (n_chunks * n_groups > INT_MAX)
+    return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
+  const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
+  const size_t part_bytes = static_cast<size_t>(n_chunks) * Model::kSums * nc * sizeof(float);
+  void* payload = nullptr;
+  LaunchSync sync{};
+  if (int rc = acquire_scratch(stream, rec_bytes + part_bytes, n_chunks * n_groups, &payload, &sync))
+    return rc;
+  float* partials = reinterpret_cast<float*>(static_cast<char*>(payload) + rec_bytes);
+  const dim3 grid(static_cast<unsigned>(n_chunks * n_groups));
+  bool launched = false;
+#define OSSM_LAUNCH_BWD(TT, WW)                                                                  \
+  if (!launched && tile.T == TT && tile.W == WW) {                                               \
+    hipLaunchKernelGGL((osc_backward_kernel<Model, TT, WW>), grid, dim3(WW * kWave), 0, stream,   \
+                       prm, static_cast<const typename Model::In*>(in),                          \
+                       static_cast<const float4*>(states),                                       \
+                       static_cast<const typename Model::GIn*>(gout),                            \
+                       static_cast<typename Model::GOut*>(gin), partials, static_cast<int>(L),    \
+                       static_cast<int>(nc), static_cast<int>(n_groups),                         \
+                       static_cast<int>(n_chunks), static_cast<unsigned long long*>(payload),    \
+                       sync);                                                                    \
+    launched = true;                                                                             \
+  }
+  OSSM_BWD_TILES(OSSM_LAUNCH_BWD)
+#undef OSSM_LAUNCH_BWD
+  if (!launched) {
+    release_unlaunched(stream, n_chunks * n_groups);
+    return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_BWD names no built tile");
+  }
+  if (int rc = launch_check("osc_backward_kernel")) {
+    release_unlaunched(stream, n_chunks * n_groups);
+    return rc;
+  }
+  *partials_out = partials;
+  *n_chunks_out = n_chunks;
+  return OSSM_OK;
+}
+
+int check_sizes(int64_t L, int64_t B, int64_t P, const char* what) {
+  if (L < 0 || B < 0 || P < 0)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": negative size");
+  if (L > INT_MAX || B * P > INT_MAX / 2 || P > INT_MAX)
+    return set_error(OSSM_ERR_UNSUPPORTED, std::string(what) + ": size exceeds 32-bit indexing");
+  return OSSM_OK;
+}
+
+template <int V>
+int dlinoss_forward_v(const float* a, const float* g, const float* dt, const void* bu, void* states,
+                      int64_t L, int64_t B, int64_t P, hipStream_t stream) {
+  typename Dlinoss<V>::Params prm{a, g, dt, static_cast<int>(P)};
+  return launch_forward<Dlinoss<V>>(prm, bu, states, L, B * P, stream);
+}
+
+template <int V>
+int dlinoss_backward_v(const float* a, const float* g, const float* dt, const void* bu,
+                       const void* states, const void* gout, float* ga, float* gg, float* gs,
+                       void* gbu, int64_t L, int64_t B, int64_t P, hipStream_t stream) {
+  typename Dlinoss<V>::Params prm{a, g, dt, static_cast<int>(P)};
+  float* partials = nullptr;
+  int64_t n_chunks = 0;
+  if (int rc = launch_backward<Dlinoss<V>>(prm, bu, states, gout, gbu, L, B * P, &partials,
+                                            &n_chunks, stream))
+    return rc;
+  hipLaunchKernelGGL(dlinoss_param_grad_kernel<V>, dim3(static_cast<unsigned>(P)),
+                     dim3(kReduceThreads), 0, stream, partials, a, g, dt, ga, gg, gs,
+                     static_cast<int>(P), static_cast<int>(B), static_cast<int>(n_chunks),
+                     static_cast<int>(B * P));
+  return launch_check("dlinoss_param_grad_kernel");
+}
+
+}  // namespace
+}  // namespace ossm
+
+using namespace ossm;
+
+extern "C" {
+
+int ossm_dlinoss_forward(int variant, const float* a_diag, const float* g_diag, const float* step,
+                         const void* bu, void* states, int64_t length, int64_t batch, int64_t ssm,
+                         ossm_stream_t stream_v) {
+  clear_error();
+  if (int rc = check_sizes(length, batch, ssm, "dlinoss_forward")) return rc;
+  if (length == 0 || batch == 0 || ssm == 0) return OSSM_OK;
+  if (!a_diag || !g_diag || !step || !bu || !states)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "dlinoss_forward: null pointer");
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  switch (variant) {
+    case OSSM_DLINOSS_IMEX1:
+      return dlinoss_forward_v<OSSM_DLINOSS_IMEX1>(a_diag, g_diag, step, bu, states, length, batch, ssm, stream);
+    case OSSM_DLINOSS_IMEX2:
+      return dlinoss_forward_v<OSSM_DLINOSS_IMEX2>(a_diag, g_diag, step, bu, states, length, batch, ssm, stream);
+    case OSSM_DLINOSS_IM:
+      return dlinoss_forward_v<OSSM_DLINOSS_IM>(a_diag, g_diag, step, bu, states, length, batch, ssm, stream);
+    case OSSM_DLINOSS_EX:
+      return dlinoss_forward_v<OSSM_DLINOSS_EX>(a_diag, g_diag, step, bu, states, length, batch, ssm, stream);
+    default:
+      return set_error(OSSM_ERR_INVALID_ARGUMENT, "Unknown D-LinOSS variant code");
+  }
+}
+
+int ossm_dlinoss_backward(int variant, const float* a_diag, const float* g_diag, const float* step,
+                          const void* bu, const void* states, const void* grad_output,
+                          float* grad_a, float* grad_g, float* grad_step, void* grad_bu,
+                          int64_t length, int64_t batch, int64_t ssm, ossm_stream_t stream_v) {
+  clear_error();
+  if (int rc = check_sizes(length, batch, ssm, "dlinoss_backward")) return rc;
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  if (ssm > 0 && (length == 0 || batch == 0)) {
+    // reference: zero gradients when there is nothing to scan (dlinoss_imex1.cpp:366-375)
+    if (!grad_a || !grad_g || !grad_step)
+      return set_error(OSSM_ERR_INVALID_ARGUMENT, "dlinoss_backward: null pointer");
+    for (float* p : {grad_a, grad_g, grad_step})
+      if (int rc = fill_zero(p, ssm, stream)) return rc;
+    return OSSM_OK;
+  }
+  if (length == 0 || batch == 0 || ssm == 0) return OSSM_OK;
+  if (!a_diag || !g_diag || !step || !bu || !states || !grad_output || !grad_a || !grad_g ||
+      !grad_step || !grad_bu)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "dlinoss_backward: null pointer");
+  switch (variant) {
+#define OSSM_BWD_CASE(V)                                                                       \
+  case V:                                                                                      \
+    return dlinoss_backward_v<V>(a_diag, g_diag, step, bu, states, grad_output, grad_a, grad_g, \
+                                 grad_step, grad_bu, length, batch, ssm, stream);
+    OSSM_BWD_CASE(OSSM_DLINOSS_IMEX1)
+    OSSM_BWD_CASE(OSSM_DLINOSS_IMEX2)
+    OSSM_BWD_CASE(OSSM_DLINOSS_IM)
+    OSSM_BWD_CASE(OSSM_DLINOSS_EX)
+#undef OSSM_BWD_CASE
+    default:
+      return set_error(OSSM_ERR_INVALID_ARGUMENT, "Unknown D-LinOSS variant code");
+  }
+}
+
+int ossm_linoss_forward(const void* m11, const void* m12, const void* m21, const void* m22,
+                        const void* b_seq, void* states, int64_t length, int64_t batch, int64_t ssm,
+                        ossm_stream_t stream_v) {
+  clear_error();
+  if (int rc = check_sizes(length, batch, ssm, "linoss_forward")) return rc;
+  if (length == 0 || batch == 0 || ssm == 0) return OSSM_OK;
+  if (!m11 || !m12 || !m21 || !m22 || !b_seq || !states)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "linoss_forward: null pointer");
+  Linoss::Params prm{static_cast<const float2*>(m11), static_cast<const float2*>(m12),
+                     static_cast<const float2*>(m21), static_cast<const float2*>(m22),
+                     static_cast<int>(ssm)};
+  return launch_forward<Linoss>(prm, b_seq, states, length, batch * ssm,
+                                static_cast<hipStream_t>(stream_v));
+}
+
+int ossm_linoss_backward(const void* m11, const void* m12, const void* m21, const void* m22,
+                         const void* states, const void* grad_output, void* grad_m, void* grad_b,
+                         int64_t length, int64_t batch, int64_t ssm, ossm_stream_t stream_v) {
+  clear_error();
+  if (int rc = check_sizes(length, batch, ssm, "linoss_backward")) return rc;
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  if (ssm > 0 && (length == 0 || batch == 0)) {
+    if (!grad_m) return set_error(OSSM_ERR_INVALID_ARGUMENT, "linoss_backward: null pointer");
+    return fill_zero(static_cast<float*>(grad_m), 8 * ssm, stream);
+  }
+  if (length == 0 || batch == 0 || ssm == 0) return OSSM_OK;
+  if (!m11 || !m12 || !m21 || !m22 || !states || !grad_output || !grad_m || !grad_b)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "linoss_backward: null pointer");
+  Linoss::Params prm{static_cast<const float2*>(m11), static_cast<const float2*>(m12),
+                     static_cast<const float2*>(m21), static_cast<const float2*>(m22),
+                     static_cast<int>(ssm)};
+  float* partials = nullptr;
+  int64_t n_chunks = 0;
+  if (int rc = launch_backward<Linoss>(prm, nullptr, states, grad_output, grad_b, length,
+                                       batch * ssm, &partials, &n_chunks, stream))
+    return rc;
+  hipLaunchKernelGGL(linoss_param_grad_kernel, dim3(static_cast<unsigned>(ssm)),
+                     dim3(kReduceThreads), 0, stream, partials, static_cast<float*>(grad_m),
+                     static_cast<int>(ssm), static_cast<int>(batch), static_cast<int>(n_chunks),
+                     static_cast<int>(batch * ssm));
+  return launch_check("linoss_param_grad_kernel");
+}
+
+}  // extern "C"

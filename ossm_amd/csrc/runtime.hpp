@@ -1,0 +1,51 @@
+// Host-side runtime shared by the scan entry points: error reporting and the
+// per-(device, stream) scratch buffer that carries look-back records, tickets
+// and partial sums between workgroups.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+namespace ossm {
+
+// Error bits a kernel may raise in the scratch header (see ossm_device_error_bits).
+constexpr uint32_t kErrSpinTimeout = 1u;
+constexpr uint32_t kErrBadTicket = 2u;
+
+// Layout of the scratch header (bytes from the buffer start).
+constexpr size_t kHdrTicket = 0;    // uint64_t monotonically increasing ticket counter
+constexpr size_t kHdrErr = 64;      // uint32_t error bits
+constexpr size_t kHdrBytes = 256;   // payload starts here, 256-byte aligned
+
+// Per-launch synchronisation arguments handed to a look-back kernel.
+struct LaunchSync {
+  unsigned long long* ticket;  // device counter, shared by all launches on this scratch
+  unsigned int* err;           // device error bits
+  unsigned long long base;     // value of *ticket when this launch starts
+  unsigned int tag;            // epoch tag of this launch's records (never 0)
+};
+
+// Records the message for ossm_last_error() and returns `status`.
+int set_error(int status, const std::string& msg);
+int clear_error();
+
+// Checks a HIP call, records "<what>: <hipGetErrorString>" on failure.
+int hip_check(hipError_t e, const char* what);
+
+// Returns a scratch payload of at least `payload_bytes` for `stream` and the
+// launch bookkeeping for a grid of `n_workgroups` look-back workgroups.  The
+// payload is zero-filled when first allocated and is never cleared again:
+// kernels tag what they write with sync.tag.
+int acquire_scratch(hipStream_t stream, size_t payload_bytes, uint64_t n_workgroups,
+                    void** payload, LaunchSync* sync);
+
+// Undo the ticket reservation of the last acquire_scratch on `stream` when
+// its kernel failed to launch (the device counter never advanced).
+void release_unlaunched(hipStream_t stream, uint64_t n_workgroups);
+
+// Launch-error check after a kernel launch (reference: C10_CUDA_KERNEL_LAUNCH_CHECK).
+int launch_check(const char* what);
+
+}  // namespace ossm

@@ -1,0 +1,177 @@
+// Device helpers for the chunked linear-recurrence scans on gfx950:
+// 2x2 transition algebra on complex 2-vectors, and the decoupled look-back
+// protocol that hands chunk carries from one workgroup to the next.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "runtime.hpp"
+
+namespace ossm {
+
+constexpr int kWave = 64;
+
+// A state is a complex 2-vector packed as float4 (s0.re, s0.im, s1.re, s1.im),
+// the [.., 2] complex64 layout of the reference's states tensors.
+__device__ __forceinline__ float4 f4add(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+__device__ __forceinline__ float4 f4zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+// ---- real 2x2 transition [[a, b], [c, d]] (D-LinOSS) -----------------------
+struct RMat {
+  float a, b, c, d;
+};
+__device__ __forceinline__ RMat mat_identity(RMat) { return {1.f, 0.f, 0.f, 1.f}; }
+__device__ __forceinline__ RMat mat_mul(RMat p, RMat q) {
+  return {p.a * q.a + p.b * q.c, p.a * q.b + p.b * q.d, p.c * q.a + p.d * q.c,
+          p.c * q.b + p.d * q.d};
+}
+__device__ __forceinline__ RMat mat_adjoint(RMat p) { return {p.a, p.c, p.b, p.d}; }
+__device__ __forceinline__ float4 mat_apply(RMat m, float4 s) {
+  return make_float4(m.a * s.x + m.b * s.z, m.a * s.y + m.b * s.w, m.c * s.x + m.d * s.z,
+                     m.c * s.y + m.d * s.w);
+}
+
+// ---- complex 2x2 transition (LinOSS) ----------------------------------------
+struct CMat {
+  float2 a, b, c, d;
+};
+__device__ __forceinline__ float2 cmul(float2 p, float2 q) {
+  return make_float2(p.x * q.x - p.y * q.y, p.x * q.y + p.y * q.x);
+}
+__device__ __forceinline__ float2 cadd(float2 p, float2 q) { return make_float2(p.x + q.x, p.y + q.y); }
+__device__ __forceinline__ float2 cconj(float2 p) { return make_float2(p.x, -p.y); }
+__device__ __forceinline__ CMat mat_identity(CMat) {
+  return {make_float2(1.f, 0.f), make_float2(0.f, 0.f), make_float2(0.f, 0.f), make_float2(1.f, 0.f)};
+}
+__device__ __forceinline__ CMat mat_mul(CMat p, CMat q) {
+  return {cadd(cmul(p.a, q.a), cmul(p.b, q.c)), cadd(cmul(p.a, q.b), cmul(p.b, q.d)),
+          cadd(cmul(p.c, q.a), cmul(p.d, q.c)), cadd(cmul(p.c, q.b), cmul(p.d, q.d))};
+}
+__device__ __forceinline__ CMat mat_adjoint(CMat p) {  // conjugate transpose
+  return {cconj(p.a), cconj(p.c), cconj(p.b), cconj(p.d)};
+}
+__device__ __forceinline__ float4 mat_apply(CMat m, float4 s) {
+  const float2 s0 = make_float2(s.x, s.y), s1 = make_float2(s.z, s.w);
+  const float2 n0 = cadd(cmul(m.a, s0), cmul(m.b, s1));
+  const float2 n1 = cadd(cmul(m.c, s0), cmul(m.d, s1));
+  return make_float4(n0.x, n0.y, n1.x, n1.y);
+}
+
+// m^n for n >= 1 by binary powering.
+template <class Mat>
+__device__ __forceinline__ Mat mat_pow(Mat m, int n) {
+  Mat r = mat_identity(m);
+  Mat b = m;
+  while (n > 0) {
+    if (n & 1) r = mat_mul(r, b);
+    n >>= 1;
+    if (n) b = mat_mul(b, b);
+  }
+  return r;
+}
+
+// ---- decoupled look-back ----------------------------------------------------
+//
+// Each (chunk, channel) owns two records, an aggregate (the chunk's effect on
+// a zero carry) and an inclusive prefix (the true state at the chunk's end),
+// each four 64-bit words: high half = launch tag, low half = float bits.  A
+// word is written once per launch with one 64-bit atomic store, so a reader
+// that sees this launch's tag in all four words has the complete value; no
+// fence, flag or clearing pass is needed, and records of earlier launches
+// (older tags) are simply not ready.
+//
+// Records layout: rec[((chunk * 2 + kind) * 4 + k) * nc + ch], kind 0 =
+// aggregate, 1 = inclusive.  Lanes of a wave touch consecutive channels, so
+// every record access is one coalesced 512-byte row per word.
+constexpr int kRecAgg = 0;
+constexpr int kRecInc = 1;
+constexpr uint32_t kSpinLimit = 1u << 22;  // ~ a few hundred ms of polling
+
+__device__ __forceinline__ size_t rec_index(int chunk, int kind, int k, int nc, int ch) {
+  return ((size_t(chunk) * 2 + kind) * 4 + k) * size_t(nc) + ch;
+}
+
+__device__ __forceinline__ void rec_publish(unsigned long long* rec, int chunk, int kind,
+                                            int nc, int ch, float4 v, unsigned int tag) {
+  const unsigned long long t = static_cast<unsigned long long>(tag) << 32;
+  const float vals[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const unsigned long long w = t | __float_as_uint(vals[k]);
+    __hip_atomic_store(rec + rec_index(chunk, kind, k, nc, ch), w, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__device__ __forceinline__ bool rec_read(unsigned long long* rec, int chunk, int kind, int nc,
+                                         int ch, unsigned int tag, float4* v) {
+  unsigned long long w[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    w[k] = __hip_atomic_load(rec + rec_index(chunk, kind, k, nc, ch), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  bool ok = true;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) ok = ok && (static_cast<unsigned int>(w[k] >> 32) == tag);
+  *v = make_float4(__uint_as_float(static_cast<unsigned int>(w[0])),
+                   __uint_as_float(static_cast<unsigned int>(w[1])),
+                   __uint_as_float(static_cast<unsigned int>(w[2])),
+                   __uint_as_float(static_cast<unsigned int>(w[3])));
+  return ok;
+}
+
+// Carry into chunk `c` for one channel: walks predecessors c - dir, c - 2 dir,
+// ... (dir = +1 forward in time, -1 for reverse scans), composing aggregates
+// with `step_mat` (the chunk transition) until an inclusive prefix is found.
+// Every predecessor drew an earlier ticket, so it is resident and publishes
+// its aggregate without waiting on anything: the walk always ends.  The spin
+// is still bounded; giving up raises kErrSpinTimeout instead of hanging.
+template <class Mat>
+__device__ float4 lookback(unsigned long long* rec, int c, int dir, int n_chunks, int nc, int ch,
+                           Mat step_mat, const LaunchSync& sync) {
+  float4 acc = f4zero();
+  Mat pw = mat_identity(step_mat);
+  for (int j = c - dir; j >= 0 && j < n_chunks; j -= dir) {
+    uint32_t spins = 0;
+    for (;;) {
+      float4 v;
+      if (rec_read(rec, j, kRecInc, nc, ch, sync.tag, &v)) {
+        return f4add(acc, mat_apply(pw, v));
+      }
+      if (rec_read(rec, j, kRecAgg, nc, ch, sync.tag, &v)) {
+        acc = f4add(acc, mat_apply(pw, v));
+        pw = mat_mul(pw, step_mat);
+        break;
+      }
+      if (++spins > kSpinLimit) {
+        __hip_atomic_fetch_or(sync.err, kErrSpinTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return acc;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  return acc;
+}
+
+// Draws this workgroup's ticket (launch order), broadcast through LDS.
+// Returns -1 (and raises kErrBadTicket) when the counter is out of step.
+__device__ __forceinline__ int draw_ticket(const LaunchSync& sync, int total, int* s_slot) {
+  if (threadIdx.x == 0) {
+    const unsigned long long t =
+        __hip_atomic_fetch_add(sync.ticket, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    long long rel = static_cast<long long>(t - sync.base);
+    if (rel < 0 || rel >= total) {
+      __hip_atomic_fetch_or(sync.err, kErrBadTicket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      rel = -1;
+    }
+    *s_slot = static_cast<int>(rel);
+  }
+  __syncthreads();
+  return *s_slot;
+}
+
+}  // namespace ossm

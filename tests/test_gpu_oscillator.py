@@ -1,0 +1,209 @@
+"""GPU parity of the D-LinOSS and LinOSS scans (through the drop-in module,
+i.e. the C ABI) against the CPU oracle and the reference's kernel vectors.
+
+Tolerance (north star): rtol 1e-4 / atol 1e-5 in fp32/complex64 against the
+reference CPU kernel.  Parameter gradients are sums over B*L terms; the
+reference accumulates them in one fp32 scalar, so they are compared with an
+atol scaled by the gradient's magnitude and checked against fp64 truth.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.gpu_util import (announce, assert_close, assert_parity, dlinoss_inputs, need_gpu,
+                            no_device_errors, rel_fro, to_dev, to_np)
+
+pytestmark = pytest.mark.gpu
+VARIANTS = oracle.VARIANTS
+GOLDEN = Path(__file__).resolve().parent / "golden"
+RTOL, ATOL = 1e-4, 1e-5
+
+
+@pytest.fixture(scope="module")
+def K():
+    need_gpu()
+    from ossm_amd import _kernels
+
+    return _kernels
+
+
+def _fwd(K, v, a, g, dt, bu):
+    return getattr(K, f"dlinoss_{v}_forward")(to_dev(a), to_dev(g), to_dev(dt), to_dev(bu))
+
+
+def _bwd(K, v, a, g, dt, bu, states, go):
+    return getattr(K, f"dlinoss_{v}_backward")(to_dev(a), to_dev(g), to_dev(dt), to_dev(bu),
+                                               states, to_dev(go))
+
+
+def _param_atol(ref: np.ndarray) -> float:
+    return 2e-5 * max(1.0, float(np.abs(ref).max()))
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_dlinoss_matches_reference_kernel_vectors(K, variant):
+    """GPU vs the outputs the reference's own CPU kernels produced (fixture)."""
+    with np.load(GOLDEN / "ref_kernel_vectors.npz") as z:
+        v = {k: z[k] for k in z.files}
+    announce(f"dlinoss golden {variant} L=53 B=3 P=7")
+    st = _fwd(K, variant, v["dl_a"], v["dl_g"], v["dl_step"], v["dl_bu"])
+    assert_close(to_np(st), v[f"dl_{variant}_states"], RTOL, ATOL, "states")
+    ga, gg, gs, gb = _bwd(K, variant, v["dl_a"], v["dl_g"], v["dl_step"], v["dl_bu"],
+                          to_dev(v[f"dl_{variant}_states"]), v["dl_grad"])
+    assert_close(to_np(gb), v[f"dl_{variant}_grad_bu"], RTOL, ATOL, "grad_bu")
+    for got, key in ((ga, "grad_a"), (gg, "grad_g"), (gs, "grad_step")):
+        ref = v[f"dl_{variant}_{key}"]
+        assert_close(to_np(got), ref, RTOL, _param_atol(ref), key)
+    no_device_errors()
+
+
+# shapes: tiny, ragged (P and B*P not multiples of 64), many chunks / groups
+SHAPES = [(1, 1, 1), (2, 3, 5), (129, 2, 33), (1000, 3, 70), (2100, 4, 64)]
+
+
+def _oracle64(variant, a, g, dt, bu, go):
+    a64, g64, d64 = (x.astype(np.float64) for x in (a, g, dt))
+    b64, go64 = bu.astype(np.complex128), go.astype(np.complex128)
+    st = oracle.dlinoss_forward(variant, a64, g64, d64, b64)
+    return st, oracle.dlinoss_backward(variant, a64, g64, d64, b64, st, go64)
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_dlinoss_forward_backward_vs_oracle(K, variant, shape):
+    L, B, P = shape
+    a, g, dt, bu, go = dlinoss_inputs(L, B, P, seed=L + 7 * B + 13 * P, variant=variant)
+    announce(f"dlinoss {variant} L={L} B={B} P={P}")
+    st = _fwd(K, variant, a, g, dt, bu)
+    ga, gg, gs, gb = _bwd(K, variant, a, g, dt, bu, st, go)
+    ref = oracle.dlinoss_forward(variant, a, g, dt, bu)
+    rga, rgg, rgs, rgb = oracle.dlinoss_backward(variant, a, g, dt, bu, ref, go)
+    st64, (tga, tgg, tgs, tgb) = _oracle64(variant, a, g, dt, bu, go)
+    assert_parity(to_np(st), ref, st64, RTOL, ATOL, "states")
+    assert_parity(to_np(gb), rgb, tgb, RTOL, ATOL, "grad_bu")
+    # parameter gradients are sums over B*L terms: atol scaled by their size
+    for got, r32, r64, key in ((ga, rga, tga, "grad_a"), (gg, rgg, tgg, "grad_g"),
+                               (gs, rgs, tgs, "grad_step")):
+        assert_parity(to_np(got), r32, r64, RTOL, _param_atol(r64), key)
+    no_device_errors()
+
+
+def test_dlinoss_zero_length_and_empty(K):
+    a, g, dt, bu, go = dlinoss_inputs(4, 2, 3, seed=1)
+    st = K.dlinoss_imex1_forward(to_dev(a), to_dev(g), to_dev(dt), to_dev(bu[:0]))
+    assert tuple(st.shape) == (0, 2, 3, 2)
+    grads = K.dlinoss_imex1_backward(to_dev(a), to_dev(g), to_dev(dt), to_dev(bu[:0]),
+                                     torch.empty((0, 2, 3, 2), dtype=torch.complex64, device="cuda"),
+                                     to_dev(go[:0]))
+    assert all(float(t.abs().sum()) == 0 for t in grads[:3])
+
+
+def test_dlinoss_rejects_bad_inputs(K):
+    a, g, dt, bu, _ = dlinoss_inputs(8, 2, 3, seed=2)
+    with pytest.raises(RuntimeError, match="bu must have shape"):
+        K.dlinoss_imex1_forward(to_dev(a), to_dev(g), to_dev(dt), to_dev(bu[0]))
+    with pytest.raises(RuntimeError, match="match state size"):
+        K.dlinoss_imex1_forward(to_dev(a[:2]), to_dev(g), to_dev(dt), to_dev(bu))
+    with pytest.raises(RuntimeError, match="bu must be contiguous"):
+        K.dlinoss_imex1_forward(to_dev(a), to_dev(g), to_dev(dt), to_dev(bu).transpose(0, 1))
+
+
+@pytest.mark.parametrize("variant", ["imex1", "im"])
+def test_dlinoss_config2_full_size(K, variant):
+    """BASELINE config 2 shape (B=32, L=4096, P=128): every channel of a slice
+    of oscillators checked against the oracle at full length, plus linearity
+    of the whole scan."""
+    L, B, P = 4096, 32, 128
+    a, g, dt, bu, go = dlinoss_inputs(L, B, P, seed=2024, variant=variant)
+    announce(f"dlinoss {variant} full config2")
+    st = _fwd(K, variant, a, g, dt, bu)
+    gp = _bwd(K, variant, a, g, dt, bu, st, go)
+    # channel slice: batches 0, 17, 31 and every oscillator
+    bs = [0, 17, 31]
+    bus, gos = np.ascontiguousarray(bu[:, bs]), np.ascontiguousarray(go[:, bs])
+    ref = oracle.dlinoss_forward(variant, a, g, dt, bus)
+    _, _, _, rgb = oracle.dlinoss_backward(variant, a, g, dt, bus, ref, gos)
+    st64, (_, _, _, tgb) = _oracle64(variant, a, g, dt, bus, gos)
+    assert_parity(to_np(st[:, bs]), ref, st64, RTOL, ATOL, "states slice")
+    assert_parity(to_np(gp[3][:, bs]), rgb, tgb, RTOL, ATOL, "grad_bu slice")
+    # whole-problem parameter gradients vs the oracle on all channels
+    full = oracle.dlinoss_forward(variant, a, g, dt, bu)
+    rg = oracle.dlinoss_backward(variant, a, g, dt, bu, full, go)
+    for got, r, key in zip(gp[:3], rg[:3], ("grad_a", "grad_g", "grad_step")):
+        assert rel_fro(to_np(got), r) < 1e-4, key
+    # linearity: scan(bu + 2 bu') = scan(bu) + 2 scan(bu')
+    bu2 = torch.roll(to_dev(bu), shifts=1, dims=1)
+    s2 = _fwd(K, variant, a, g, dt, to_np(bu2))
+    s12 = _fwd(K, variant, a, g, dt, to_np(to_dev(bu) + 2 * bu2))
+    assert rel_fro(to_np(s12), to_np(st + 2 * s2)) < 1e-5
+    no_device_errors()
+
+
+def test_dlinoss_config5_long_sequence(K):
+    """BASELINE config 5 (B=4, L=65536, P=256, forward only): cross-workgroup
+    carries over 512 chunks; checked per channel against the oracle and
+    against fp64 truth."""
+    L, B, P = 65536, 4, 256
+    a, g, dt, bu, _ = dlinoss_inputs(L, B, P, seed=5)
+    announce("dlinoss imex1 full config5")
+    st = to_np(_fwd(K, "imex1", a, g, dt, bu))
+    ref32 = oracle.dlinoss_forward("imex1", a, g, dt, bu)
+    ref64 = oracle.dlinoss_forward("imex1", a.astype(np.float64), g.astype(np.float64),
+                                   dt.astype(np.float64), bu.astype(np.complex128))
+    e_gpu = rel_fro(st, ref64)
+    e_cpu = rel_fro(ref32, ref64)
+    assert e_gpu <= 4 * e_cpu + 1e-6, (e_gpu, e_cpu)
+    assert rel_fro(st, ref32) < 1e-4
+    no_device_errors()
+
+
+# ------------------------------------------------------------------- LinOSS
+def _linoss_inputs(L, B, P, seed):
+    rng = np.random.default_rng(seed)
+    # LinOSS-IM transition of linoss.py:244-251 with a ~ U(0, 1), dt = sigmoid(N)
+    a = rng.uniform(0.0, 1.0, P)
+    dt = 1 / (1 + np.exp(-rng.normal(size=P)))
+    schur = 1 / (1 + dt * dt * a)
+    ms = [(1 - dt * dt * a * schur), (-dt * a * schur), (dt * schur), schur]
+    ms = [m + 1j * 0.05 * rng.normal(size=P) for m in ms]
+    # rescale so the perturbed transition stays non-expanding (rho <= 0.999)
+    M = np.stack([np.stack(ms[:2], -1), np.stack(ms[2:], -1)], -2)
+    rho = np.abs(np.linalg.eigvals(M)).max(-1)
+    scale = np.minimum(1.0, 0.999 / rho)
+    ms = [(m * scale).astype(np.complex64) for m in ms]
+    b = (rng.normal(size=(L, B, P, 2)) + 1j * rng.normal(size=(L, B, P, 2))).astype(np.complex64)
+    go = (rng.normal(size=(L, B, P, 2)) + 1j * rng.normal(size=(L, B, P, 2))).astype(np.complex64)
+    return ms, b, go
+
+
+def test_linoss_matches_reference_kernel_vectors(K):
+    with np.load(GOLDEN / "ref_kernel_vectors.npz") as z:
+        v = {k: z[k] for k in z.files}
+    announce("linoss golden")
+    out = K.linoss_scan(*[to_dev(v[k]) for k in ("lo_m11", "lo_m12", "lo_m21", "lo_m22", "lo_b")])
+    assert_close(to_np(out), v["lo_out"], RTOL, ATOL)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (37, 3, 5), (1500, 2, 96)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_linoss_forward_backward_vs_oracle(K, shape):
+    L, B, P = shape
+    ms, b, go = _linoss_inputs(L, B, P, seed=L + P)
+    announce(f"linoss L={L} B={B} P={P}")
+    st = K.linoss_scan(*[to_dev(m) for m in ms], to_dev(b))
+    ref = oracle.linoss_forward(*ms, b)
+    ms64 = [m.astype(np.complex128) for m in ms]
+    st64 = oracle.linoss_forward(*ms64, b.astype(np.complex128))
+    assert_parity(to_np(st), ref, st64, RTOL, ATOL, "states")
+    gm, gb = K.linoss_scan_backward(*[to_dev(m) for m in ms], st, to_dev(go))
+    rgm, rgb = oracle.linoss_backward(*ms, ref, go)
+    tgm, tgb = oracle.linoss_backward(*ms64, st64, go.astype(np.complex128))
+    assert_parity(to_np(gb), rgb, tgb, RTOL, ATOL, "grad_b")
+    assert_parity(to_np(gm), rgm, tgm, RTOL, _param_atol(tgm), "grad_m")
+    no_device_errors()
