@@ -256,7 +256,7 @@ __global__ __launch_bounds__(W * kWave) void osc_forward_kernel(
     for (int v = 0; v < W; ++v) E = f4add(mat_apply(MT, E), s_agg[v][lane]);
     float4 carry = f4zero();
     if (active && n_chunks > 1) {
-      const typename Model::Mat MC = mat_pow(MT, W);
+      const typename Model::Mat MC = mat_pow(Model::matrix(k), T * W);
       if (c == 0) {
         rec_publish(rec, c, kRecInc, nc, ch, E, sync.tag);
       } else {
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(W * kWave) void osc_backward_kernel(
     for (int v = W - 1; v >= 0; --v) E = f4add(mat_apply(KT, E), s_agg[v][lane]);
     float4 carry = f4zero();
     if (active && n_chunks > 1) {
-      const typename Model::Mat KC = mat_pow(KT, W);
+      const typename Model::Mat KC = mat_pow(mat_adjoint(Model::matrix(k)), T * W);
       if (c == n_chunks - 1) {
         rec_publish(rec, c, kRecInc, nc, ch, E, sync.tag);
       } else {

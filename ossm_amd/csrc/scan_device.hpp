@@ -61,17 +61,62 @@ __device__ __forceinline__ float4 mat_apply(CMat m, float4 s) {
   return make_float4(n0.x, n0.y, n1.x, n1.y);
 }
 
-// m^n for n >= 1 by binary powering.
+// ---- fp64 twins, used only to raise a transition to a power ------------------
+// A chunk transition M^n composed in fp32 by repeated squaring loses ~log2(n)
+// roundings per entry, and non-normal M (LinOSS) amplifies that through
+// cancellation.  The powers are computed once per lane, so they are formed in
+// fp64 and rounded to fp32 once.
+struct RMatD {
+  double a, b, c, d;
+};
+struct CMatD {
+  double ar, ai, br, bi, cr, ci, dr, di;
+};
+__device__ __forceinline__ RMatD widen(RMat m) { return {m.a, m.b, m.c, m.d}; }
+__device__ __forceinline__ RMat narrow(RMatD m) {
+  return {static_cast<float>(m.a), static_cast<float>(m.b), static_cast<float>(m.c),
+          static_cast<float>(m.d)};
+}
+__device__ __forceinline__ RMatD mat_identity(RMatD) { return {1.0, 0.0, 0.0, 1.0}; }
+__device__ __forceinline__ RMatD mat_mul(RMatD p, RMatD q) {
+  return {p.a * q.a + p.b * q.c, p.a * q.b + p.b * q.d, p.c * q.a + p.d * q.c,
+          p.c * q.b + p.d * q.d};
+}
+__device__ __forceinline__ CMatD widen(CMat m) {
+  return {m.a.x, m.a.y, m.b.x, m.b.y, m.c.x, m.c.y, m.d.x, m.d.y};
+}
+__device__ __forceinline__ CMat narrow(CMatD m) {
+  return {make_float2(static_cast<float>(m.ar), static_cast<float>(m.ai)),
+          make_float2(static_cast<float>(m.br), static_cast<float>(m.bi)),
+          make_float2(static_cast<float>(m.cr), static_cast<float>(m.ci)),
+          make_float2(static_cast<float>(m.dr), static_cast<float>(m.di))};
+}
+__device__ __forceinline__ CMatD mat_identity(CMatD) { return {1, 0, 0, 0, 0, 0, 1, 0}; }
+__device__ __forceinline__ CMatD mat_mul(CMatD p, CMatD q) {
+  // (p q)_ij = sum_k p_ik q_kj with complex entries a b / c d
+  CMatD r;
+  r.ar = p.ar * q.ar - p.ai * q.ai + p.br * q.cr - p.bi * q.ci;
+  r.ai = p.ar * q.ai + p.ai * q.ar + p.br * q.ci + p.bi * q.cr;
+  r.br = p.ar * q.br - p.ai * q.bi + p.br * q.dr - p.bi * q.di;
+  r.bi = p.ar * q.bi + p.ai * q.br + p.br * q.di + p.bi * q.dr;
+  r.cr = p.cr * q.ar - p.ci * q.ai + p.dr * q.cr - p.di * q.ci;
+  r.ci = p.cr * q.ai + p.ci * q.ar + p.dr * q.ci + p.di * q.cr;
+  r.dr = p.cr * q.br - p.ci * q.bi + p.dr * q.dr - p.di * q.di;
+  r.di = p.cr * q.bi + p.ci * q.br + p.dr * q.di + p.di * q.dr;
+  return r;
+}
+
+// m^n for n >= 1 by binary powering in fp64, rounded to fp32 once.
 template <class Mat>
 __device__ __forceinline__ Mat mat_pow(Mat m, int n) {
-  Mat r = mat_identity(m);
-  Mat b = m;
+  auto b = widen(m);
+  auto r = mat_identity(b);
   while (n > 0) {
     if (n & 1) r = mat_mul(r, b);
     n >>= 1;
     if (n) b = mat_mul(b, b);
   }
-  return r;
+  return narrow(r);
 }
 
 // ---- decoupled look-back ----------------------------------------------------
