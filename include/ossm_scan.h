@@ -14,9 +14,10 @@
  *   LinOSS:     m11, m12, m21, m22 [P] c64;  b_seq, states [L,B,P,2] c64
  *   selective:  u, dt, gate, out [B,D,L] f32;  A [D,N] f32;  Bm, Cm [B,L,N] f32
  *
- * Scratch: the library keeps one zero-initialised scratch buffer per
- * (device, stream) for look-back records and partial sums; it grows on demand
- * (hipMalloc outside the launch path) and never needs clearing between calls.
+ * Scratch: the library keeps, per (device, stream), one zero-initialised
+ * buffer of tagged look-back records (never cleared between calls) and one
+ * plain workspace for partial sums; both grow on demand (hipMalloc outside
+ * the kernels, after synchronising the stream) and live until process exit.
  */
 #ifndef OSSM_SCAN_H
 #define OSSM_SCAN_H
@@ -39,7 +40,7 @@ enum {
 
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
-/* Library ABI version (bumped on any signature change). */
+/* Library ABI version (bumped on any signature change; currently 2). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -97,7 +98,7 @@ int ossm_linoss_backward(const void* m11, const void* m12, const void* m21, cons
                          void* grad_b, int64_t length, int64_t batch, int64_t ssm,
                          ossm_stream_t stream);
 
-/* Number of time chunks the selective scan keeps checkpoints for (length > 0). */
+/* Number of rows of the selective scan's checkpoint tensor (ceil(length / 32); 0 for length 0). */
 int64_t ossm_selective_num_chunks(int64_t length);
 
 /*
@@ -107,9 +108,10 @@ int64_t ossm_selective_num_chunks(int64_t length);
  *   h_t = exp(dt_t A_dn) h_{t-1} + dt_t Bm_tn u_t,  y_t = sum_n Cm_tn h_t,
  *   out_t = y_t * silu(gate_t)  (out = y when gate == NULL).
  * raw_out [B,D,L] receives y (may be NULL, or equal to out when gate == NULL).
- * chunk_states [B,D,n_chunks,2N] f32 receives, per chunk, the state h at the
- * chunk's end (first N) and exp(A * sum dt over the chunk) (last N); it may be
- * NULL.  dstate <= 256.
+ * chunk_states [B,D,n_chunks,2N] f32 (may be NULL) receives checkpoints of the
+ * state: row c holds h after step 32c+15 (first N) and after step 32c+31
+ * (last N); a checkpoint past the end of the sequence holds the final state.
+ * 1 <= dstate <= 256.
  */
 int ossm_selective_forward(const float* u, const float* dt, const float* A, const float* Bm,
                            const float* Cm, const float* gate, float* out, float* raw_out,
@@ -119,16 +121,19 @@ int ossm_selective_forward(const float* u, const float* dt, const float* A, cons
 /*
  * Selective scan backward, replaces selective_scan_cuda_backward
  * (selective_scan_cuda.cu:312-393) and selective_scan_cpu_backward
- * (selective_scan_cpu.cpp:168-360).  chunk_states must come from
- * ossm_selective_forward on the same inputs.  Writes du, ddt [B,D,L],
- * dA [D,N], dB, dC [B,L,N] (all overwritten) and dgate [B,D,L] (zeros when
- * gate == NULL; may be NULL then).
+ * (selective_scan_cpu.cpp:168-360).  chunk_states and raw_out must come from
+ * ossm_selective_forward on the same inputs (raw_out is read only when a gate
+ * is given, for dgate).  Writes du, ddt [B,D,L], dA [D,N], dB, dC [B,L,N]
+ * (all overwritten) and dgate [B,D,L] (zeros when gate == NULL; may be NULL
+ * then).  The sums over channels (dB, dC) and over batch and time (dA) are
+ * formed in a fixed order: results are deterministic.
  */
 int ossm_selective_backward(const float* grad_out, const float* u, const float* dt,
                             const float* A, const float* Bm, const float* Cm, const float* gate,
-                            const float* chunk_states, float* du, float* ddt, float* dA,
-                            float* dB, float* dC, float* dgate, int64_t batch, int64_t dim,
-                            int64_t length, int64_t dstate, ossm_stream_t stream);
+                            const float* chunk_states, const float* raw_out, float* du,
+                            float* ddt, float* dA, float* dB, float* dC, float* dgate,
+                            int64_t batch, int64_t dim, int64_t length, int64_t dstate,
+                            ossm_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -301,8 +301,10 @@ def selective_scan_cuda_backward(grad_output, inputs, dt, A, B, C, gate=None, ch
                                  raw_outputs=None, chunk_length=None):
     """selective_scan_cuda.cu:312-393: returns ``[du, ddt, dA, dB, dC, dgate]``.
 
-    ``raw_outputs`` is checked like the reference does but not read: the
-    backward recomputes y from the chunk checkpoints."""
+    ``chunk_states`` must come from :func:`selective_scan_cuda` on the same
+    inputs (its rows are this library's state checkpoints).  ``raw_outputs``
+    (y before the gate) is read for ``dgate`` when a gate is given; if it is
+    missing the forward is re-run to produce it."""
     _check(inputs.is_cuda, "inputs must be CUDA tensor")
     _selective_checks(inputs, dt, A, B, C, gate, "selective_scan_cuda")
     _check(grad_output.device == inputs.device, "grad_output must be on the same device as inputs")
@@ -323,20 +325,24 @@ def selective_scan_cuda_backward(grad_output, inputs, dt, A, B, C, gate=None, ch
     z = gate.contiguous() if gate is not None else None
     gout = grad_output.contiguous()
     du, ddt = torch.empty_like(u), torch.empty_like(d)
-    dA = torch.zeros_like(a)
-    dB, dC = torch.zeros_like(b), torch.zeros_like(c)
-    dz = torch.zeros_like(u)
+    dA = torch.empty_like(a)
+    dB, dC = torch.empty_like(b), torch.empty_like(c)
+    dz = torch.empty_like(u)
     if length == 0:
-        return [du, ddt, dA, dB, dC, dz]
+        return [du, ddt, dA.zero_(), dB, dC, dz]
     cs = chunk_states.contiguous()
     _check(tuple(cs.shape) == (batch, dim, _num_chunks(length), 2 * dstate),
            "chunk_states do not match this library's forward for these inputs")
+    raw = None
+    if z is not None:
+        raw = raw_outputs.contiguous() if raw_outputs is not None else \
+            selective_scan_cuda(inputs, dt, A, B, C, gate)[2]
     with torch.cuda.device(u.device):
         _lib.check(_lib.load().ossm_selective_backward(
             gout.data_ptr(), u.data_ptr(), d.data_ptr(), a.data_ptr(), b.data_ptr(), c.data_ptr(),
-            _lib.ptr(z), cs.data_ptr(), du.data_ptr(), ddt.data_ptr(), dA.data_ptr(),
-            dB.data_ptr(), dC.data_ptr(), dz.data_ptr(), batch, dim, length, dstate,
-            _lib.stream_of(u)))
+            _lib.ptr(z), cs.data_ptr(), _lib.ptr(raw), du.data_ptr(), ddt.data_ptr(),
+            dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), dz.data_ptr(), batch, dim, length,
+            dstate, _lib.stream_of(u)))
     return [du, ddt, dA, dB, dC, dz]
 
 

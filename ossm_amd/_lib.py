@@ -40,8 +40,8 @@ _SIGNATURES = {
         [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _c_int64, _c_int64, _c_int64, _c_int64, _vp]),
     "ossm_selective_backward": (
         ctypes.c_int,
-        [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _c_int64, _c_int64,
-         _c_int64, _c_int64, _vp]),
+        [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _c_int64,
+         _c_int64, _c_int64, _c_int64, _vp]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

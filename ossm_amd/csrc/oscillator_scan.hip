@@ -580,11 +580,12 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
     return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
   const size_t part_bytes = static_cast<size_t>(n_chunks) * Model::kSums * nc * sizeof(float);
+  void* part_ws = nullptr;
+  if (int rc = acquire_workspace(stream, part_bytes, &part_ws)) return rc;
+  float* partials = static_cast<float*>(part_ws);
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(stream, rec_bytes + part_bytes, n_chunks * n_groups, &payload, &sync))
-    return rc;
-  float* partials = reinterpret_cast<float*>(static_cast<char*>(payload) + rec_bytes);
+  if (int rc = acquire_scratch(stream, rec_bytes, n_chunks * n_groups, &payload, &sync)) return rc;
   const dim3 grid(static_cast<unsigned>(n_chunks * n_groups));
   bool launched = false;
 #define OSSM_LAUNCH_BWD(TT, WW)                                                                  \

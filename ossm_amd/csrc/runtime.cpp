@@ -19,8 +19,14 @@ struct Scratch {
   unsigned long long next_ticket = 0;  // value of the device counter after all queued launches
 };
 
+struct Workspace {
+  void* base = nullptr;
+  size_t bytes = 0;
+};
+
 std::mutex g_mu;
 std::map<std::pair<int, hipStream_t>, Scratch> g_scratch;
+std::map<std::pair<int, hipStream_t>, Workspace> g_workspace;
 
 }  // namespace
 
@@ -81,6 +87,29 @@ int acquire_scratch(hipStream_t stream, size_t payload_bytes, uint64_t n_workgro
   return OSSM_OK;
 }
 
+int acquire_workspace(hipStream_t stream, size_t bytes, void** ptr) {
+  int dev = 0;
+  if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  std::lock_guard<std::mutex> lock(g_mu);
+  Workspace& w = g_workspace[{dev, stream}];
+  if (w.base == nullptr || w.bytes < bytes) {
+    if (w.base != nullptr) {
+      if (int rc = hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize")) return rc;
+      if (int rc = hip_check(hipFree(w.base), "hipFree(workspace)")) return rc;
+      w.base = nullptr;
+      w.bytes = 0;
+    }
+    size_t cap = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+    cap = (cap + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
+    void* p = nullptr;
+    if (int rc = hip_check(hipMalloc(&p, cap), "hipMalloc(workspace)")) return rc;
+    w.base = p;
+    w.bytes = cap;
+  }
+  *ptr = w.base;
+  return OSSM_OK;
+}
+
 void release_unlaunched(hipStream_t stream, uint64_t n_workgroups) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return;
@@ -94,7 +123,7 @@ void release_unlaunched(hipStream_t stream, uint64_t n_workgroups) {
 
 extern "C" {
 
-int ossm_abi_version(void) { return 1; }
+int ossm_abi_version(void) { return 2; }
 
 const char* ossm_last_error(void) { return ossm::g_last_error.c_str(); }
 

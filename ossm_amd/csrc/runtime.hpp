@@ -41,6 +41,12 @@ int hip_check(hipError_t e, const char* what);
 int acquire_scratch(hipStream_t stream, size_t payload_bytes, uint64_t n_workgroups,
                     void** payload, LaunchSync* sync);
 
+// Returns a plain device workspace of at least `bytes` for `stream`, separate
+// from the tagged look-back records: partial sums written here can never be
+// mistaken for a record.  Contents are unspecified; kernels write before they
+// read.  Grows on demand (synchronising `stream` before freeing the old one).
+int acquire_workspace(hipStream_t stream, size_t bytes, void** ptr);
+
 // Undo the ticket reservation of the last acquire_scratch on `stream` when
 // its kernel failed to launch (the device counter never advanced).
 void release_unlaunched(hipStream_t stream, uint64_t n_workgroups);
