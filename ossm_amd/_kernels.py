@@ -122,12 +122,13 @@ def _dlinoss_backward(variant: str, a_diag, g_diag, step, bu, states, grad_outpu
            "Coefficient diagonals must match state size")
     _check(tuple(states.shape[:3]) == (length, batch, ssm),
            "states must have shape (length, batch, ssm_size, 2)")
-    grad_a = torch.zeros_like(a_diag)
-    grad_g = torch.zeros_like(g_diag)
-    grad_step = torch.zeros_like(step)
     grad_bu = torch.empty_like(bu)
     if length == 0:
-        return [grad_a, grad_g, grad_step, grad_bu]
+        return [torch.zeros_like(a_diag), torch.zeros_like(g_diag), torch.zeros_like(step), grad_bu]
+    # overwritten by the library (it reduces the parameter sums in-kernel)
+    grad_a = torch.empty_like(a_diag)
+    grad_g = torch.empty_like(g_diag)
+    grad_step = torch.empty_like(step)
     _check(a_diag.is_contiguous() and g_diag.is_contiguous() and step.is_contiguous(),
            "Coefficient diagonals must be contiguous")
     _check(bu.is_contiguous(), "bu must be contiguous")
@@ -216,10 +217,10 @@ def linoss_scan_backward(m11, m12, m21, m22, states, grad_output):
            "states must have shape (length, batch, ssm_size, 2)")
     _check(grad_output.shape == states.shape, "grad_output must match states shape")
     length, batch, ssm, _ = states.shape
-    grad_m = torch.zeros((ssm, 2, 2), dtype=states.dtype, device=states.device)
     grad_b = torch.empty_like(grad_output)
     if length == 0:
-        return [grad_m, grad_b]
+        return [torch.zeros((ssm, 2, 2), dtype=states.dtype, device=states.device), grad_b]
+    grad_m = torch.empty((ssm, 2, 2), dtype=states.dtype, device=states.device)
     _check(states.is_cuda, "linoss_scan_backward: HIP path needs device tensors")
     _on_device(m11, m12, m21, m22, states, grad_output)
     for m in (m11, m12, m21, m22):

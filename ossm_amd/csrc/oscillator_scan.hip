@@ -24,9 +24,12 @@
 //   backwards with the transposed transition.  States s_{t-1} needed by the
 //   parameter gradients are recomputed in registers from the checkpoint
 //   states[t0 - 1] instead of reading the whole trajectory.  Per-lane sums of
-//   <mu_i, s_j,t-1> and <mu_i, bu_t> go to a partials buffer; a second small
-//   kernel reduces them per oscillator in a fixed order (deterministic, fp64)
-//   and applies each variant's chain rule to (a, g, dt).
+//   <mu_i, s_j,t-1> and <mu_i, bu_t> go to a partials buffer; two small
+//   kernels add them over time chunks (per channel), then over the batch (per
+//   oscillator) and apply each variant's chain rule to (a, g, dt).  Every sum
+//   runs in a fixed order in fp64, so the gradients are deterministic.  (A
+//   last-workgroup-done reduction inside the scan kernel was measured 3x
+//   slower: each agent-scope release fence writes back the XCD's L2.)
 
 #include <hip/hip_runtime.h>
 
@@ -158,6 +161,59 @@ struct Dlinoss {
     acc[4] += m.x * bu.x + m.y * bu.y;  // F0
     acc[5] += m.z * bu.x + m.w * bu.y;  // F1
   }
+
+  // Chain rule from the oscillator's summed (G00, G01, G10, G11, F0, F1) to
+  // (a, g, dt): imex1 dlinoss_imex1.cpp:219-232, im dlinoss_im.cpp:236-263,
+  // imex2 / ex by differentiating the coefficient tables of
+  // dlinoss_imex2.cpp:35-47 / dlinoss_ex.cpp:33-42 (the terms the reference
+  // accumulates per step).  out0/1/2 = grad_a, grad_g, grad_step.
+  static __device__ void epilogue(const Params& prm, int p, const double* S, float* grad_a,
+                                  float* grad_g, float* grad_step) {
+    const double G00 = S[0], G01 = S[1], G10 = S[2], G11 = S[3], F0 = S[4], F1 = S[5];
+    const double a = prm.a[p], g = prm.g[p], dt = prm.dt[p];
+    double ga, gg, gs;
+    if constexpr (V == OSSM_DLINOSS_IMEX1) {
+      const double inv = 1.0 / (1.0 + dt * g);
+      const double s2i = dt * dt * inv;
+      const double ginv = G00 + G10;
+      const double gs2i = F0 + F1 - a * (G01 + G11);
+      ga = -s2i * (G01 + G11);
+      const double inv_total = ginv + gs2i * dt * dt;
+      gs = gs2i * (2.0 * dt * inv) - inv_total * g * inv * inv;
+      gg = -inv_total * dt * inv * inv;
+    } else if constexpr (V == OSSM_DLINOSS_IMEX2) {
+      ga = -dt * G01 - dt * dt * G11;
+      gg = -dt * G00 - dt * dt * G10;
+      gs = -g * G00 - a * G01 + (1.0 - 2.0 * dt * g) * G10 - 2.0 * dt * a * G11 + F0 +
+           2.0 * dt * F1;
+    } else if constexpr (V == OSSM_DLINOSS_IM) {
+      const double inv = 1.0 / (1.0 + dt * g + dt * dt * a);
+      const double si = dt * inv;
+      double gsi = F0 + G10, ginv = G00;
+      const double gs2i = F1;
+      gsi += G01 * (-a);
+      ga = G01 * (-si);
+      ginv += G11 * (1.0 + dt * g);
+      const double gt = G11 * inv;
+      gg = gt * dt;
+      gs = gt * g;
+      gs += gsi * inv;
+      ginv += gsi * dt;
+      gs += gs2i * (2.0 * dt * inv);
+      ginv += gs2i * dt * dt;
+      const double gden = -ginv * inv * inv;
+      ga += gden * dt * dt;
+      gg += gden * dt;
+      gs += gden * (g + 2.0 * dt * a);
+    } else {
+      ga = -dt * G01;
+      gg = -dt * G00;
+      gs = -g * G00 - a * G01 + F0 + G10;
+    }
+    grad_a[p] = static_cast<float>(ga);
+    grad_g[p] = static_cast<float>(gg);
+    grad_step[p] = static_cast<float>(gs);
+  }
 };
 
 // Generic complex LinOSS: s_t = M s_{t-1} + b_t (linoss_scan.cpp:48-66).
@@ -200,6 +256,13 @@ struct Linoss {
     acc[2] += g.x * sp.z + g.y * sp.w;  acc[3] += g.y * sp.z - g.x * sp.w;  // m12
     acc[4] += g.z * sp.x + g.w * sp.y;  acc[5] += g.w * sp.x - g.z * sp.y;  // m21
     acc[6] += g.z * sp.z + g.w * sp.w;  acc[7] += g.w * sp.z - g.z * sp.w;  // m22
+  }
+
+  // grad_m [P, 2, 2] complex = the summed products themselves (out0).
+  static __device__ void epilogue(const Params&, int p, const double* S, float* grad_m, float*,
+                                  float*) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) grad_m[8 * p + j] = static_cast<float>(S[j]);
   }
 };
 
@@ -287,11 +350,16 @@ __global__ __launch_bounds__(W * kWave) void osc_forward_kernel(
 // ============================================================================
 // Backward kernel
 // ============================================================================
+// Destination of the backward's per-(chunk, channel) parameter partial sums.
+struct ParamReduce {
+  float* partials;  // [n_chunks][NS][nc]
+};
+
 template <class Model, int T, int W>
 __global__ __launch_bounds__(W * kWave) void osc_backward_kernel(
     typename Model::Params prm, const typename Model::In* __restrict__ in,
     const float4* __restrict__ states, const typename Model::GIn* __restrict__ gout,
-    typename Model::GOut* __restrict__ gin, float* __restrict__ partials, int L, int nc,
+    typename Model::GOut* __restrict__ gin, ParamReduce red, int L, int nc,
     int n_groups, int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
   constexpr int NS = Model::kSums;
   __shared__ float4 s_agg[W][kWave];
@@ -386,20 +454,77 @@ __global__ __launch_bounds__(W * kWave) void osc_backward_kernel(
 #pragma unroll
   for (int j = 0; j < NS; ++j) s_sum[w][j][lane] = acc[j];
   __syncthreads();
+
+  // 4. this chunk's parameter partial sums (one per channel and sum)
   if (w == 0 && active) {
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       float v = 0.f;
       for (int u = 0; u < W; ++u) v += s_sum[u][j][lane];
-      partials[(static_cast<size_t>(c) * NS + j) * nc + ch] = v;
+      red.partials[(static_cast<size_t>(c) * NS + j) * nc + ch] = v;
     }
   }
 }
 
 // ============================================================================
-// Per-oscillator reduction of the partial sums + chain rule
+// Per-oscillator parameter gradients from the chunk partials
 // ============================================================================
-constexpr int kReduceThreads = 256;
+// Stage 1: chan_tot[j][ch] = sum over time chunks of partials[c][j][ch] (fp64,
+// chunks in order).  One thread per (sum, channel): coalesced over channels.
+template <int NS>
+__global__ __launch_bounds__(256) void osc_reduce_chunks_kernel(const float* __restrict__ partials,
+                                                                double* __restrict__ chan_tot,
+                                                                int nc, int n_chunks) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<int64_t>(NS) * nc) return;
+  const int j = static_cast<int>(i / nc), ch = static_cast<int>(i - static_cast<int64_t>(j) * nc);
+  const float* p = partials + static_cast<size_t>(j) * nc + ch;
+  const size_t stride = static_cast<size_t>(NS) * nc;
+  double v = 0.0;
+  int c = 0;
+  for (; c + 8 <= n_chunks; c += 8) {
+    float x[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = p[(c + k) * stride];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v += static_cast<double>(x[k]);
+  }
+  for (; c < n_chunks; ++c) v += static_cast<double>(p[c * stride]);
+  chan_tot[i] = v;
+}
+
+// Stage 2: per oscillator p, S[j] = sum over the batch of chan_tot[j][b*P+p]
+// (fp64, batch in a fixed split and order), then Model::epilogue.  A block
+// covers 64 oscillators (lanes) with its 4 waves splitting the batch.
+template <class Model>
+__global__ __launch_bounds__(256) void osc_param_kernel(typename Model::Params prm,
+                                                        const double* __restrict__ chan_tot, int P,
+                                                        int B, float* out0, float* out1,
+                                                        float* out2) {
+  constexpr int NS = Model::kSums;
+  __shared__ double s_red[4][NS][kWave];
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  const int p = blockIdx.x * kWave + lane;
+  const size_t nc = static_cast<size_t>(B) * P;
+  double acc[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) acc[j] = 0.0;
+  if (p < P) {
+    for (int b = w; b < B; b += 4) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j) acc[j] += chan_tot[j * nc + static_cast<size_t>(b) * P + p];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NS; ++j) s_red[w][j][lane] = acc[j];
+  __syncthreads();
+  if (w == 0 && p < P) {
+    double S[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) S[j] = ((s_red[0][j][lane] + s_red[1][j][lane]) + s_red[2][j][lane]) + s_red[3][j][lane];
+    Model::epilogue(prm, p, S, out0, out1, out2);
+  }
+}
 
 // Zero-fill used where the reference returns zero gradients (empty scans);
 // a kernel rather than hipMemsetAsync so the call can sit in a captured graph.
@@ -415,106 +540,6 @@ int fill_zero(float* p, int64_t n, hipStream_t stream) {
   return launch_check("fill_zero_kernel");
 }
 
-template <int NS>
-__device__ void reduce_sums(const float* __restrict__ partials, int p, int P, int B, int n_chunks,
-                            int nc, double* out) {
-  __shared__ double s_red[NS][kReduceThreads];
-  double acc[NS];
-#pragma unroll
-  for (int j = 0; j < NS; ++j) acc[j] = 0.0;
-  const int items = n_chunks * B;
-  for (int it = threadIdx.x; it < items; it += kReduceThreads) {
-    const int c = it / B, b = it - c * B;
-    const size_t chi = static_cast<size_t>(b) * P + p;
-#pragma unroll
-    for (int j = 0; j < NS; ++j) acc[j] += partials[(static_cast<size_t>(c) * NS + j) * nc + chi];
-  }
-#pragma unroll
-  for (int j = 0; j < NS; ++j) s_red[j][threadIdx.x] = acc[j];
-  __syncthreads();
-  for (int off = kReduceThreads / 2; off > 0; off >>= 1) {
-    if (threadIdx.x < off) {
-#pragma unroll
-      for (int j = 0; j < NS; ++j) s_red[j][threadIdx.x] += s_red[j][threadIdx.x + off];
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int j = 0; j < NS; ++j) out[j] = s_red[j][0];
-}
-
-// Chain rule from the generic sums (G00, G01, G10, G11, F0, F1) to (a, g, dt):
-// imex1 dlinoss_imex1.cpp:219-232, im dlinoss_im.cpp:236-263, imex2/ex by
-// differentiating the coefficient tables of dlinoss_imex2.cpp:35-47 /
-// dlinoss_ex.cpp:33-42 (the same terms the reference accumulates per step).
-template <int V>
-__global__ __launch_bounds__(kReduceThreads) void dlinoss_param_grad_kernel(
-    const float* __restrict__ partials, const float* __restrict__ a_diag,
-    const float* __restrict__ g_diag, const float* __restrict__ step, float* __restrict__ grad_a,
-    float* __restrict__ grad_g, float* __restrict__ grad_step, int P, int B, int n_chunks, int nc) {
-  const int p = blockIdx.x;
-  double S[6];
-  reduce_sums<6>(partials, p, P, B, n_chunks, nc, S);
-  if (threadIdx.x != 0) return;
-  const double G00 = S[0], G01 = S[1], G10 = S[2], G11 = S[3], F0 = S[4], F1 = S[5];
-  const double a = a_diag[p], g = g_diag[p], dt = step[p];
-  double ga, gg, gs;
-  if constexpr (V == OSSM_DLINOSS_IMEX1) {
-    const double inv = 1.0 / (1.0 + dt * g);
-    const double s2i = dt * dt * inv;
-    const double ginv = G00 + G10;
-    const double gs2i = F0 + F1 - a * (G01 + G11);
-    ga = -s2i * (G01 + G11);
-    const double inv_total = ginv + gs2i * dt * dt;
-    gs = gs2i * (2.0 * dt * inv) - inv_total * g * inv * inv;
-    gg = -inv_total * dt * inv * inv;
-  } else if constexpr (V == OSSM_DLINOSS_IMEX2) {
-    ga = -dt * G01 - dt * dt * G11;
-    gg = -dt * G00 - dt * dt * G10;
-    gs = -g * G00 - a * G01 + (1.0 - 2.0 * dt * g) * G10 - 2.0 * dt * a * G11 + F0 + 2.0 * dt * F1;
-  } else if constexpr (V == OSSM_DLINOSS_IM) {
-    const double inv = 1.0 / (1.0 + dt * g + dt * dt * a);
-    const double si = dt * inv;
-    double gsi = F0 + G10, ginv = G00;
-    const double gs2i = F1;
-    gsi += G01 * (-a);
-    ga = G01 * (-si);
-    ginv += G11 * (1.0 + dt * g);
-    const double gt = G11 * inv;
-    gg = gt * dt;
-    gs = gt * g;
-    gs += gsi * inv;
-    ginv += gsi * dt;
-    gs += gs2i * (2.0 * dt * inv);
-    ginv += gs2i * dt * dt;
-    const double gden = -ginv * inv * inv;
-    ga += gden * dt * dt;
-    gg += gden * dt;
-    gs += gden * (g + 2.0 * dt * a);
-  } else {
-    ga = -dt * G01;
-    gg = -dt * G00;
-    gs = -g * G00 - a * G01 + F0 + G10;
-  }
-  grad_a[p] = static_cast<float>(ga);
-  grad_g[p] = static_cast<float>(gg);
-  grad_step[p] = static_cast<float>(gs);
-}
-
-__global__ __launch_bounds__(kReduceThreads) void linoss_param_grad_kernel(
-    const float* __restrict__ partials, float* __restrict__ grad_m, int P, int B, int n_chunks,
-    int nc) {
-  const int p = blockIdx.x;
-  double S[8];
-  reduce_sums<8>(partials, p, P, B, n_chunks, nc, S);
-  if (threadIdx.x != 0) return;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) grad_m[8 * p + j] = static_cast<float>(S[j]);
-}
-
-// ============================================================================
-// Host dispatch
-// ============================================================================
 struct Tile {
   int T, W;
 };
@@ -568,24 +593,32 @@ int launch_forward(const typename Model::Params& prm, const void* in, void* out,
   return OSSM_OK;
 }
 
+// Backward launch: one kernel computes grad_in and, through the in-kernel
+// reduction, the per-oscillator parameter gradients (out0..2, see
+// Model::epilogue).  nc = B * P channels.
 template <class Model>
 int launch_backward(const typename Model::Params& prm, const void* in, const void* states,
-                    const void* gout, void* gin, int64_t L, int64_t nc, float** partials_out,
-                    int64_t* n_chunks_out, hipStream_t stream) {
-  static const Tile tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{8, 8});
+                    const void* gout, void* gin, float* out0, float* out1, float* out2, int64_t L,
+                    int64_t B, int64_t P, hipStream_t stream) {
+  static const Tile tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{16, 8});
+  constexpr int NS = Model::kSums;
+  const int64_t nc = B * P;
   const int64_t CL = int64_t(tile.T) * tile.W;
   const int64_t n_chunks = (L + CL - 1) / CL;
   const int64_t n_groups = (nc + kWave - 1) / kWave;
   if (n_chunks * n_groups > INT_MAX)
     return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
-  const size_t part_bytes = static_cast<size_t>(n_chunks) * Model::kSums * nc * sizeof(float);
-  void* part_ws = nullptr;
-  if (int rc = acquire_workspace(stream, part_bytes, &part_ws)) return rc;
-  float* partials = static_cast<float*>(part_ws);
+  const size_t part_bytes =
+      (static_cast<size_t>(n_chunks) * NS * nc * sizeof(float) + 255) & ~static_cast<size_t>(255);
+  const size_t tot_bytes = static_cast<size_t>(NS) * nc * sizeof(double);
+  void* ws = nullptr;
+  if (int rc = acquire_workspace(stream, part_bytes + tot_bytes, &ws)) return rc;
   void* payload = nullptr;
   LaunchSync sync{};
   if (int rc = acquire_scratch(stream, rec_bytes, n_chunks * n_groups, &payload, &sync)) return rc;
+  ParamReduce red{static_cast<float*>(ws)};
+  double* chan_tot = reinterpret_cast<double*>(static_cast<char*>(ws) + part_bytes);
   const dim3 grid(static_cast<unsigned>(n_chunks * n_groups));
   bool launched = false;
 #define OSSM_LAUNCH_BWD(TT, WW)                                                                  \
@@ -594,7 +627,7 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
                        prm, static_cast<const typename Model::In*>(in),                          \
                        static_cast<const float4*>(states),                                       \
                        static_cast<const typename Model::GIn*>(gout),                            \
-                       static_cast<typename Model::GOut*>(gin), partials, static_cast<int>(L),    \
+                       static_cast<typename Model::GOut*>(gin), red, static_cast<int>(L),        \
                        static_cast<int>(nc), static_cast<int>(n_groups),                         \
                        static_cast<int>(n_chunks), static_cast<unsigned long long*>(payload),    \
                        sync);                                                                    \
@@ -610,9 +643,15 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
     release_unlaunched(stream, n_chunks * n_groups);
     return rc;
   }
-  *partials_out = partials;
-  *n_chunks_out = n_chunks;
-  return OSSM_OK;
+  const int64_t n_tot = static_cast<int64_t>(NS) * nc;
+  hipLaunchKernelGGL(osc_reduce_chunks_kernel<NS>, dim3(static_cast<unsigned>((n_tot + 255) / 256)),
+                     dim3(256), 0, stream, red.partials, chan_tot, static_cast<int>(nc),
+                     static_cast<int>(n_chunks));
+  if (int rc = launch_check("osc_reduce_chunks_kernel")) return rc;
+  hipLaunchKernelGGL(osc_param_kernel<Model>, dim3(static_cast<unsigned>((P + kWave - 1) / kWave)),
+                     dim3(256), 0, stream, prm, chan_tot, static_cast<int>(P), static_cast<int>(B),
+                     out0, out1, out2);
+  return launch_check("osc_param_kernel");
 }
 
 int check_sizes(int64_t L, int64_t B, int64_t P, const char* what) {
@@ -635,16 +674,7 @@ int dlinoss_backward_v(const float* a, const float* g, const float* dt, const vo
                        const void* states, const void* gout, float* ga, float* gg, float* gs,
                        void* gbu, int64_t L, int64_t B, int64_t P, hipStream_t stream) {
   typename Dlinoss<V>::Params prm{a, g, dt, static_cast<int>(P)};
-  float* partials = nullptr;
-  int64_t n_chunks = 0;
-  if (int rc = launch_backward<Dlinoss<V>>(prm, bu, states, gout, gbu, L, B * P, &partials,
-                                            &n_chunks, stream))
-    return rc;
-  hipLaunchKernelGGL(dlinoss_param_grad_kernel<V>, dim3(static_cast<unsigned>(P)),
-                     dim3(kReduceThreads), 0, stream, partials, a, g, dt, ga, gg, gs,
-                     static_cast<int>(P), static_cast<int>(B), static_cast<int>(n_chunks),
-                     static_cast<int>(B * P));
-  return launch_check("dlinoss_param_grad_kernel");
+  return launch_backward<Dlinoss<V>>(prm, bu, states, gout, gbu, ga, gg, gs, L, B, P, stream);
 }
 
 }  // namespace
@@ -742,16 +772,9 @@ int ossm_linoss_backward(const void* m11, const void* m12, const void* m21, cons
   Linoss::Params prm{static_cast<const float2*>(m11), static_cast<const float2*>(m12),
                      static_cast<const float2*>(m21), static_cast<const float2*>(m22),
                      static_cast<int>(ssm)};
-  float* partials = nullptr;
-  int64_t n_chunks = 0;
-  if (int rc = launch_backward<Linoss>(prm, nullptr, states, grad_output, grad_b, length,
-                                       batch * ssm, &partials, &n_chunks, stream))
-    return rc;
-  hipLaunchKernelGGL(linoss_param_grad_kernel, dim3(static_cast<unsigned>(ssm)),
-                     dim3(kReduceThreads), 0, stream, partials, static_cast<float*>(grad_m),
-                     static_cast<int>(ssm), static_cast<int>(batch), static_cast<int>(n_chunks),
-                     static_cast<int>(batch * ssm));
-  return launch_check("linoss_param_grad_kernel");
+  return launch_backward<Linoss>(prm, nullptr, states, grad_output, grad_b,
+                                 static_cast<float*>(grad_m), nullptr, nullptr, length, batch, ssm,
+                                 stream);
 }
 
 }  // extern "C"

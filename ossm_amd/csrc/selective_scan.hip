@@ -44,8 +44,10 @@
 
 #include <algorithm>
 #include <climits>
+#include <initializer_list>
 #include <cstdint>
 #include <string>
+#include <type_traits>
 
 #include "../../include/ossm_scan.h"
 #include "runtime.hpp"
@@ -112,45 +114,128 @@ __device__ __forceinline__ void reduce8(const float (&v)[8], float& o0, float& o
 }
 
 // ---- tile staging -----------------------------------------------------------
-// Stages rows d0..d0+63 of a [.., L] tensor, columns t0..t0+TT-1, into LDS
-// s[r * RS + c] (zero outside the tensor).  `vec` = rows are 16-byte aligned
-// (L % 4 == 0), then the loads are float4.
-template <int TT, int RS>
-__device__ __forceinline__ void stage_rows(float* __restrict__ s, const float* __restrict__ g,
-                                           size_t row0, int d0, int D, int t0, int L, bool vec) {
-  if (vec) {
-    constexpr int C4 = TT / 4;
-    for (int i = threadIdx.x; i < kWave * C4; i += blockDim.x) {
-      const int r = i / C4, c = (i - r * C4) * 4;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (d0 + r < D && t0 + c < L)
-        v = *reinterpret_cast<const float4*>(g + row0 + static_cast<size_t>(d0 + r) * L + t0 + c);
-      float* p = s + r * RS + c;
-      p[0] = v.x;
-      p[1] = v.y;
-      p[2] = v.z;
-      p[3] = v.w;
-    }
-  } else {
-    for (int i = threadIdx.x; i < kWave * TT; i += blockDim.x) {
-      const int r = i / TT, c = i - r * TT;
-      float v = 0.f;
-      if (d0 + r < D && t0 + c < L) v = g[row0 + static_cast<size_t>(d0 + r) * L + t0 + c];
-      s[r * RS + c] = v;
+// Every launch runs kThreads threads.  A tile of a [.., L] tensor is 64 rows
+// (channels d0..d0+63) x TT steps; thread i owns the float4 column groups
+// q = i + k * kThreads of it, so its global loads are 16-byte row segments,
+// consecutive threads covering a row.  Loads go to registers first and are
+// written to LDS one tile later: the next tile's HBM reads overlap this
+// tile's recurrence.
+constexpr int kThreads = kMaxWaves * kWave;
+
+template <int TT>
+struct RowRegs {
+  static constexpr int kQ = kWave * TT / 4 / kThreads;
+  float4 v[kQ];
+};
+
+template <int TT>
+__device__ __forceinline__ void tile_pos(int k, int& row, int& c) {
+  constexpr int C4 = TT / 4;
+  const int q = threadIdx.x + k * kThreads;
+  row = q / C4;
+  c = (q - row * C4) * 4;
+}
+
+// Loads the thread's share of rows d0.. columns t0..  VEC: rows are 16-byte
+// aligned (float4 loads).  Out-of-range elements read a clamped in-range
+// address, so the loads carry no branches and all stay in flight together;
+// they are zeroed when the tile is written to LDS (store_rows), not here, so
+// that nothing waits on the loads before then.
+template <int TT, bool VEC>
+__device__ __forceinline__ void load_rows(RowRegs<TT>& r, const float* __restrict__ g,
+                                          size_t row0, int d0, int D, int t0, int L) {
+#pragma unroll
+  for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+    int row, c;
+    tile_pos<TT>(k, row, c);
+    const int t = t0 + c;
+    const size_t base = row0 + static_cast<size_t>(min(d0 + row, D - 1)) * L;
+    if constexpr (VEC) {
+      r.v[k] = *reinterpret_cast<const float4*>(g + base + min(t, L - 4));
+    } else {
+      r.v[k].x = g[base + min(t, L - 1)];
+      r.v[k].y = g[base + min(t + 1, L - 1)];
+      r.v[k].z = g[base + min(t + 2, L - 1)];
+      r.v[k].w = g[base + min(t + 3, L - 1)];
     }
   }
 }
 
-// Stages B or C rows t0..t0+TT-1, states n_base..n_base+15, into s[t * 16 + j]
-// (zero outside the tensor, so padded states contribute nothing).
+// The loaded element (k, e) of a row tile is inside the tensor.
 template <int TT>
-__device__ __forceinline__ void stage_states(float* __restrict__ s, const float* __restrict__ g,
-                                             size_t base, int t0, int L, int N, int n_base) {
-  for (int i = threadIdx.x; i < TT * kPassStates; i += blockDim.x) {
-    const int t = i / kPassStates, j = i - t * kPassStates;
-    float v = 0.f;
-    if (t0 + t < L && n_base + j < N) v = g[base + static_cast<size_t>(t0 + t) * N + n_base + j];
-    s[i] = v;
+__device__ __forceinline__ bool row_ok(int k, int e, int d0, int D, int t0, int L) {
+  int row, c;
+  tile_pos<TT>(k, row, c);
+  return d0 + row < D && t0 + c + e < L;
+}
+
+template <int TT>
+__device__ __forceinline__ float4 masked(const RowRegs<TT>& r, int k, int d0, int D, int t0,
+                                         int L) {
+  const float4 v = r.v[k];
+  return make_float4(row_ok<TT>(k, 0, d0, D, t0, L) ? v.x : 0.f,
+                     row_ok<TT>(k, 1, d0, D, t0, L) ? v.y : 0.f,
+                     row_ok<TT>(k, 2, d0, D, t0, L) ? v.z : 0.f,
+                     row_ok<TT>(k, 3, d0, D, t0, L) ? v.w : 0.f);
+}
+
+template <int TT, int RS>
+__device__ __forceinline__ void store_rows(float* __restrict__ s, const RowRegs<TT>& r, int d0,
+                                           int D, int t0, int L) {
+#pragma unroll
+  for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+    int row, c;
+    tile_pos<TT>(k, row, c);
+    const float4 v = masked<TT>(r, k, d0, D, t0, L);
+    float* p = s + row * RS + c;
+    p[0] = v.x;
+    p[1] = v.y;
+    p[2] = v.z;
+    p[3] = v.w;
+  }
+}
+
+// Stores 4 consecutive steps of one row of a [.., L] tensor.
+template <bool VEC>
+__device__ __forceinline__ void store_row4(float* __restrict__ g, size_t off, int t, int L,
+                                           float4 v) {
+  if constexpr (VEC) {
+    *reinterpret_cast<float4*>(g + off) = v;
+  } else {
+    g[off] = v.x;
+    if (t + 1 < L) g[off + 1] = v.y;
+    if (t + 2 < L) g[off + 2] = v.z;
+    if (t + 3 < L) g[off + 3] = v.w;
+  }
+}
+
+// B or C rows t0..t0+TT-1, states n_base..n_base+15 (zero outside the
+// tensor, so padded states contribute nothing); LDS layout s[t * 16 + j].
+template <int TT>
+struct StateRegs {
+  static constexpr int kQ = TT * kPassStates / kThreads;
+  float v[kQ];
+};
+
+template <int TT>
+__device__ __forceinline__ void load_states(StateRegs<TT>& r, const float* __restrict__ g,
+                                            size_t base, int t0, int L, int N, int n_base) {
+#pragma unroll
+  for (int k = 0; k < StateRegs<TT>::kQ; ++k) {
+    const int e = threadIdx.x + k * kThreads;
+    const int t = e / kPassStates, j = e - t * kPassStates;
+    r.v[k] = g[base + static_cast<size_t>(min(t0 + t, L - 1)) * N + min(n_base + j, N - 1)];
+  }
+}
+
+template <int TT>
+__device__ __forceinline__ void store_states(float* __restrict__ s, const StateRegs<TT>& r, int t0,
+                                             int L, int N, int n_base) {
+#pragma unroll
+  for (int k = 0; k < StateRegs<TT>::kQ; ++k) {
+    const int e = threadIdx.x + k * kThreads;
+    const int t = e / kPassStates, j = e - t * kPassStates;
+    s[e] = (t0 + t < L && n_base + j < N) ? r.v[k] : 0.f;
   }
 }
 
@@ -178,7 +263,25 @@ __device__ __forceinline__ void write_ckpt(float* ckpt, size_t lane_row, int slo
     if (n0 + j < N) p[n0 + j] = h[j];
 }
 
-__global__ __launch_bounds__(kMaxWaves * kWave) void selective_fwd_kernel(FwdArgs a) {
+struct FwdTile {
+  RowRegs<kFwdTile> u, dt, z;
+  StateRegs<kFwdTile> B, C;
+};
+
+template <bool VEC, bool GATED>
+__device__ __forceinline__ void fwd_prefetch(FwdTile& f, const FwdArgs& a, size_t row0, size_t bc0,
+                                             int d0, int t0) {
+  load_rows<kFwdTile, VEC>(f.u, a.u, row0, d0, a.D, t0, a.L);
+  load_rows<kFwdTile, VEC>(f.dt, a.dt, row0, d0, a.D, t0, a.L);
+  if constexpr (GATED) load_rows<kFwdTile, VEC>(f.z, a.z, row0, d0, a.D, t0, a.L);
+  load_states<kFwdTile>(f.B, a.Bm, bc0, t0, a.L, a.N, a.n_base);
+  load_states<kFwdTile>(f.C, a.Cm, bc0, t0, a.L, a.N, a.n_base);
+}
+
+// GATED kernels multiply by silu(z) in the last pass; VEC: L % 4 == 0 and
+// u/dt/z/out rows 16-byte aligned.
+template <bool VEC, bool GATED>
+__global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs a) {
   constexpr int TT = kFwdTile;
   constexpr int RS = TT + 1;  // odd row stride: lane-per-row accesses hit distinct banks
   __shared__ float s_u[kWave * RS];
@@ -187,7 +290,6 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void selective_fwd_kernel(FwdArg
   __shared__ __align__(16) float s_C[TT * kPassStates];
   __shared__ float s_y[kMaxWaves * kWave * RS];
 
-  const int nw = blockDim.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
   const int b = blockIdx.y;
@@ -195,6 +297,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void selective_fwd_kernel(FwdArg
   const int d = d0 + lane;
   const bool dvalid = d < a.D;
   const int n0 = a.n_base + w * kNpw;  // first state of this wave
+  const int nw = min(kMaxWaves, (a.N - a.n_base + kNpw - 1) / kNpw);  // waves with states
+  const bool wave_active = w < nw;
 
   float A2[kNpw], h[kNpw];
 #pragma unroll
@@ -207,65 +311,97 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void selective_fwd_kernel(FwdArg
   const size_t ck_row = (static_cast<size_t>(b) * a.D + (dvalid ? d : 0)) * a.n_chunks * 2 * a.N;
   const int n_slots = (a.L + kCkpt - 1) / kCkpt;
 
+  FwdTile nxt;
+  fwd_prefetch<VEC, GATED>(nxt, a, row0, bc0, d0, 0);
   for (int t0 = 0; t0 < a.L; t0 += TT) {
+    __syncthreads();  // the previous tile's LDS readers are done
+    store_rows<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
+    store_rows<TT, RS>(s_dt, nxt.dt, d0, a.D, t0, a.L);
+    store_states<TT>(s_B, nxt.B, t0, a.L, a.N, a.n_base);
+    store_states<TT>(s_C, nxt.C, t0, a.L, a.N, a.n_base);
+    const RowRegs<TT> zt = nxt.z;
     __syncthreads();
-    stage_rows<TT, RS>(s_u, a.u, row0, d0, a.D, t0, a.L, a.vec);
-    stage_rows<TT, RS>(s_dt, a.dt, row0, d0, a.D, t0, a.L, a.vec);
-    stage_states<TT>(s_B, a.Bm, bc0, t0, a.L, a.N, a.n_base);
-    stage_states<TT>(s_C, a.Cm, bc0, t0, a.L, a.N, a.n_base);
-    __syncthreads();
+    if (t0 + TT < a.L) fwd_prefetch<VEC, GATED>(nxt, a, row0, bc0, d0, t0 + TT);
 
     const int nsteps = min(TT, a.L - t0);
-    float* yrow = s_y + (w * kWave + lane) * RS;
+    if (wave_active) {
+      float* yrow = s_y + (w * kWave + lane) * RS;
+      const bool ck = a.ckpt != nullptr && dvalid;
+      // FULL: all TT steps exist, so the step loop needs no bounds checks and
+      // the checkpoints fall on fixed steps (15 and 31).
+      auto steps = [&](auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
-    for (int i = 0; i < TT; ++i) {
-      if (i < nsteps) {
-        const float dtv = s_dt[lane * RS + i];
-        const float dtu = dtv * s_u[lane * RS + i];
-        const float4 Bt = *reinterpret_cast<const float4*>(s_B + i * kPassStates + w * kNpw);
-        const float4 Ct = *reinterpret_cast<const float4*>(s_C + i * kPassStates + w * kNpw);
-        const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
-        const float Cv[4] = {Ct.x, Ct.y, Ct.z, Ct.w};
-        float y = 0.f;
+        for (int i = 0; i < TT; ++i) {
+          if (FULL || i < nsteps) {
+            const float dtv = s_dt[lane * RS + i];
+            const float dtu = dtv * s_u[lane * RS + i];
+            const float4 Bt = *reinterpret_cast<const float4*>(s_B + i * kPassStates + w * kNpw);
+            const float4 Ct = *reinterpret_cast<const float4*>(s_C + i * kPassStates + w * kNpw);
+            const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
+            const float Cv[4] = {Ct.x, Ct.y, Ct.z, Ct.w};
+            float y = 0.f;
 #pragma unroll
-        for (int j = 0; j < kNpw; ++j) {
-          const float dA = fast_exp2(dtv * A2[j]);
-          h[j] = fmaf(dA, h[j], dtu * Bv[j]);
-          y = fmaf(Cv[j], h[j], y);
-        }
-        yrow[i] = y;
-        if (a.ckpt != nullptr && dvalid) {
-          const int t = t0 + i;
-          if ((t + 1) % kCkpt == 0 || t + 1 == a.L) {
-            const int slot = t / kCkpt;
-            write_ckpt(a.ckpt, ck_row, slot, a.N, n0, h);
-            // an odd number of slots leaves the last row's second half: final h
-            if (t + 1 == a.L && (n_slots & 1)) write_ckpt(a.ckpt, ck_row, slot + 1, a.N, n0, h);
+            for (int j = 0; j < kNpw; ++j) {
+              const float dA = fast_exp2(dtv * A2[j]);
+              h[j] = fmaf(dA, h[j], dtu * Bv[j]);
+              y = fmaf(Cv[j], h[j], y);
+            }
+            yrow[i] = y;
+            if ((i + 1) % kCkpt == 0 && ck) write_ckpt(a.ckpt, ck_row, (t0 + i) / kCkpt, a.N, n0, h);
           }
+        }
+      };
+      if (nsteps == TT) {
+        steps(std::true_type{});
+      } else {
+        steps(std::false_type{});
+        // last tile: its final state fills the last slot (and, for an odd
+        // number of slots, the unused second half of the last row)
+        if (ck) {
+          const int slot = (a.L - 1) / kCkpt;
+          write_ckpt(a.ckpt, ck_row, slot, a.N, n0, h);
+          if (n_slots & 1) write_ckpt(a.ckpt, ck_row, slot + 1, a.N, n0, h);
         }
       }
     }
     __syncthreads();
 
     // finish y over the waves (states), gate, store
-    for (int i = threadIdx.x; i < kWave * TT; i += blockDim.x) {
-      const int r = i / TT, c = i - r * TT;
+#pragma unroll
+    for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+      int r, c;
+      tile_pos<TT>(k, r, c);
       const int dd = d0 + r, t = t0 + c;
       if (dd >= a.D || t >= a.L) continue;
-      float y = 0.f;
-      for (int v = 0; v < nw; ++v) y += s_y[(v * kWave + r) * RS + c];
+      float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int v = 0; v < nw; ++v) {
+        const float* p = s_y + (v * kWave + r) * RS + c;
+        y.x += p[0];
+        y.y += p[1];
+        y.z += p[2];
+        y.w += p[3];
+      }
       const size_t gi = row0 + static_cast<size_t>(dd) * a.L + t;
-      if (!a.first) y += a.acc[gi];
+      if (!a.first) {
+        y.x += a.acc[gi];
+        if (t + 1 < a.L) y.y += a.acc[gi + 1];
+        if (t + 2 < a.L) y.z += a.acc[gi + 2];
+        if (t + 3 < a.L) y.w += a.acc[gi + 3];
+      }
       if (a.last) {
-        if (a.acc != a.out) a.acc[gi] = y;
-        float o = y;
-        if (a.z != nullptr) {
-          const float zz = a.z[gi];
-          o = y * (zz * sigmoid(zz));
+        if (a.acc != a.out) store_row4<VEC>(a.acc, gi, t, a.L, y);
+        float4 o = y;
+        if constexpr (GATED) {
+          const float4 zz = zt.v[k];
+          o.x *= zz.x * sigmoid(zz.x);
+          o.y *= zz.y * sigmoid(zz.y);
+          o.z *= zz.z * sigmoid(zz.z);
+          o.w *= zz.w * sigmoid(zz.w);
         }
-        a.out[gi] = o;
+        store_row4<VEC>(a.out, gi, t, a.L, o);
       } else {
-        a.acc[gi] = y;
+        store_row4<VEC>(a.acc, gi, t, a.L, y);
       }
     }
   }
@@ -292,7 +428,36 @@ struct BwdArgs {
   int first, vec;
 };
 
-__global__ __launch_bounds__(kMaxWaves * kWave) void selective_bwd_kernel(BwdArgs a) {
+struct BwdTile {
+  RowRegs<kBwdTile> u, dt, go, z, raw;
+  StateRegs<kBwdTile> B, C;
+  float h0[kNpw];  // state after the step before the tile (this lane, this wave's states), unmasked
+};
+
+template <bool VEC, bool GATED>
+__device__ __forceinline__ void bwd_prefetch(BwdTile& f, const BwdArgs& a, size_t row0, size_t bc0,
+                                             size_t ck_row, int d0, bool dvalid, int n0, int tile) {
+  const int t0 = tile * kBwdTile;
+  load_rows<kBwdTile, VEC>(f.u, a.u, row0, d0, a.D, t0, a.L);
+  load_rows<kBwdTile, VEC>(f.dt, a.dt, row0, d0, a.D, t0, a.L);
+  load_rows<kBwdTile, VEC>(f.go, a.gout, row0, d0, a.D, t0, a.L);
+  if constexpr (GATED) {
+    load_rows<kBwdTile, VEC>(f.z, a.z, row0, d0, a.D, t0, a.L);
+    load_rows<kBwdTile, VEC>(f.raw, a.raw, row0, d0, a.D, t0, a.L);
+  }
+  load_states<kBwdTile>(f.B, a.Bm, bc0, t0, a.L, a.N, a.n_base);
+  load_states<kBwdTile>(f.C, a.Cm, bc0, t0, a.L, a.N, a.n_base);
+  // state after step t0 - 1 = checkpoint slot tile - 1 (zero before the start)
+  const int slot = max(tile - 1, 0);
+  const float* p = a.ckpt + ck_row + static_cast<size_t>(slot >> 1) * 2 * a.N + (slot & 1) * a.N;
+#pragma unroll
+  for (int j = 0; j < kNpw; ++j) {
+    f.h0[j] = p[min(n0 + j, a.N - 1)];  // masked where it is consumed
+  }
+}
+
+template <bool VEC, bool GATED>
+__global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs a) {
   constexpr int TT = kBwdTile;
   constexpr int RS = TT + 1;
   __shared__ float s_u[kWave * RS];
@@ -303,7 +468,6 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void selective_bwd_kernel(BwdArg
   __shared__ float s_du[kMaxWaves * kWave * RS];
   __shared__ float s_ddt[kMaxWaves * kWave * RS];
 
-  const int nw = blockDim.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
   const int b = blockIdx.y;
@@ -311,6 +475,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void selective_bwd_kernel(BwdArg
   const int d = d0 + lane;
   const bool dvalid = d < a.D;
   const int n0 = a.n_base + w * kNpw;
+  const int nw = min(kMaxWaves, (a.N - a.n_base + kNpw - 1) / kNpw);
+  const bool wave_active = w < nw;
 
   float A2[kNpw], Af[kNpw], gs[kNpw], gA[kNpw];
 #pragma unroll
@@ -326,150 +492,174 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void selective_bwd_kernel(BwdArg
   const size_t part0 = (static_cast<size_t>(blockIdx.x) * a.Bsz + b) * a.L * a.N;
   const int n_tiles = (a.L + TT - 1) / TT;
 
+  BwdTile nxt;
+  bwd_prefetch<VEC, GATED>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, n_tiles - 1);
   for (int tile = n_tiles - 1; tile >= 0; --tile) {
     const int t0 = tile * TT;
     const int nsteps = min(TT, a.L - t0);
-    __syncthreads();
-    stage_rows<TT, RS>(s_u, a.u, row0, d0, a.D, t0, a.L, a.vec);
-    stage_rows<TT, RS>(s_dt, a.dt, row0, d0, a.D, t0, a.L, a.vec);
-    stage_states<TT>(s_B, a.Bm, bc0, t0, a.L, a.N, a.n_base);
-    stage_states<TT>(s_C, a.Cm, bc0, t0, a.L, a.N, a.n_base);
-    // gated upstream gradient; the first pass also writes dz
-    for (int i = threadIdx.x; i < kWave * TT; i += blockDim.x) {
-      const int r = i / TT, c = i - r * TT;
-      const int dd = d0 + r, t = t0 + c;
-      float gy = 0.f;
-      if (dd < a.D && t < a.L) {
-        const size_t gi = row0 + static_cast<size_t>(dd) * a.L + t;
-        const float go = a.gout[gi];
-        gy = go;
-        if (a.z != nullptr) {
-          const float zz = a.z[gi];
-          const float sg = sigmoid(zz);
-          gy = go * (zz * sg);
-          if (a.first) a.dz[gi] = go * a.raw[gi] * (sg * (1.f + zz * (1.f - sg)));
+    __syncthreads();  // the previous tile's LDS readers are done
+    store_rows<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
+    store_rows<TT, RS>(s_dt, nxt.dt, d0, a.D, t0, a.L);
+    store_states<TT>(s_B, nxt.B, t0, a.L, a.N, a.n_base);
+    store_states<TT>(s_C, nxt.C, t0, a.L, a.N, a.n_base);
+    // gated upstream gradient into LDS; the first pass also writes dz
+#pragma unroll
+    for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+      int r, c;
+      tile_pos<TT>(k, r, c);
+      float4 gy = masked<TT>(nxt.go, k, d0, a.D, t0, a.L);
+      if constexpr (GATED) {
+        const float4 zz = nxt.z.v[k], go = gy;
+        const float4 sg = make_float4(sigmoid(zz.x), sigmoid(zz.y), sigmoid(zz.z), sigmoid(zz.w));
+        gy = make_float4(go.x * zz.x * sg.x, go.y * zz.y * sg.y, go.z * zz.z * sg.z,
+                         go.w * zz.w * sg.w);
+        const int dd = d0 + r, t = t0 + c;
+        if (a.first && dd < a.D && t < a.L) {
+          const float4 y = nxt.raw.v[k];
+          const float4 dzv = make_float4(go.x * y.x * (sg.x * (1.f + zz.x * (1.f - sg.x))),
+                                         go.y * y.y * (sg.y * (1.f + zz.y * (1.f - sg.y))),
+                                         go.z * y.z * (sg.z * (1.f + zz.z * (1.f - sg.z))),
+                                         go.w * y.w * (sg.w * (1.f + zz.w * (1.f - sg.w))));
+          store_row4<VEC>(a.dz, row0 + static_cast<size_t>(dd) * a.L + t, t, a.L, dzv);
         }
       }
-      s_gy[r * RS + c] = gy;
+      float* p = s_gy + r * RS + c;
+      p[0] = gy.x;
+      p[1] = gy.y;
+      p[2] = gy.z;
+      p[3] = gy.w;
     }
-    __syncthreads();
-
-    // state after step t0 - 1 (checkpoint slot tile - 1)
     float h0[kNpw];
 #pragma unroll
-    for (int j = 0; j < kNpw; ++j) h0[j] = 0.f;
-    if (tile > 0 && dvalid) {
-      const int slot = tile - 1;
-      const float* p = a.ckpt + ck_row + static_cast<size_t>(slot >> 1) * 2 * a.N + (slot & 1) * a.N;
-#pragma unroll
-      for (int j = 0; j < kNpw; ++j)
-        if (n0 + j < a.N) h0[j] = p[n0 + j];
-    }
+    for (int j = 0; j < kNpw; ++j) h0[j] = (tile > 0 && dvalid && n0 + j < a.N) ? nxt.h0[j] : 0.f;
+    __syncthreads();
+    if (tile > 0) bwd_prefetch<VEC, GATED>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile - 1);
 
-    // re-run the tile forward in registers
-    float hs[TT][kNpw], dAs[TT][kNpw];
-    {
-      float h[kNpw];
+    if (wave_active) {
+      // FULL: all TT steps exist (every tile but possibly the last in time)
+      auto tile_body = [&](auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
+        // re-run the tile forward in registers
+        float hs[TT][kNpw], dAs[TT][kNpw];
+        {
+          float h[kNpw];
 #pragma unroll
-      for (int j = 0; j < kNpw; ++j) h[j] = h0[j];
+          for (int j = 0; j < kNpw; ++j) h[j] = h0[j];
 #pragma unroll
-      for (int i = 0; i < TT; ++i) {
-        if (i < nsteps) {
-          const float dtv = s_dt[lane * RS + i];
-          const float dtu = dtv * s_u[lane * RS + i];
-          const float4 Bt = *reinterpret_cast<const float4*>(s_B + i * kPassStates + w * kNpw);
-          const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
+          for (int i = 0; i < TT; ++i) {
+            if (FULL || i < nsteps) {
+              const float dtv = s_dt[lane * RS + i];
+              const float dtu = dtv * s_u[lane * RS + i];
+              const float4 Bt = *reinterpret_cast<const float4*>(s_B + i * kPassStates + w * kNpw);
+              const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
 #pragma unroll
-          for (int j = 0; j < kNpw; ++j) {
-            const float dA = fast_exp2(dtv * A2[j]);
-            h[j] = fmaf(dA, h[j], dtu * Bv[j]);
-            hs[i][j] = h[j];
-            dAs[i][j] = dA;
-          }
-        } else {
+              for (int j = 0; j < kNpw; ++j) {
+                const float dA = fast_exp2(dtv * A2[j]);
+                h[j] = fmaf(dA, h[j], dtu * Bv[j]);
+                hs[i][j] = h[j];
+                dAs[i][j] = dA;
+              }
+            } else {
 #pragma unroll
-          for (int j = 0; j < kNpw; ++j) {
-            hs[i][j] = 0.f;
-            dAs[i][j] = 0.f;
+              for (int j = 0; j < kNpw; ++j) {
+                hs[i][j] = 0.f;
+                dAs[i][j] = 0.f;
+              }
+            }
           }
         }
-      }
-    }
 
-    // reverse sweep
-    float keep0 = 0.f, keep1 = 0.f;
-    float* durow = s_du + (w * kWave + lane) * RS;
-    float* ddtrow = s_ddt + (w * kWave + lane) * RS;
+        // reverse sweep
+        float keep0 = 0.f, keep1 = 0.f;
+        float* durow = s_du + (w * kWave + lane) * RS;
+        float* ddtrow = s_ddt + (w * kWave + lane) * RS;
 #pragma unroll
-    for (int i = TT - 1; i >= 0; --i) {
-      if (i < nsteps) {
-        const float gy = s_gy[lane * RS + i];
-        const float dtv = s_dt[lane * RS + i];
-        const float uv = s_u[lane * RS + i];
-        const float dtu = dtv * uv;
-        const float4 Bt = *reinterpret_cast<const float4*>(s_B + i * kPassStates + w * kNpw);
-        const float4 Ct = *reinterpret_cast<const float4*>(s_C + i * kPassStates + w * kNpw);
-        const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
-        const float Cv[4] = {Ct.x, Ct.y, Ct.z, Ct.w};
-        float S1 = 0.f, S2 = 0.f;
-        float v[8];
+        for (int i = TT - 1; i >= 0; --i) {
+          if (FULL || i < nsteps) {
+            const float gy = s_gy[lane * RS + i];
+            const float dtv = s_dt[lane * RS + i];
+            const float uv = s_u[lane * RS + i];
+            const float dtu = dtv * uv;
+            const float4 Bt = *reinterpret_cast<const float4*>(s_B + i * kPassStates + w * kNpw);
+            const float4 Ct = *reinterpret_cast<const float4*>(s_C + i * kPassStates + w * kNpw);
+            const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
+            const float Cv[4] = {Ct.x, Ct.y, Ct.z, Ct.w};
+            float S1 = 0.f, S2 = 0.f;
+            float v[8];
 #pragma unroll
-        for (int j = 0; j < kNpw; ++j) {
-          const float hprev = i > 0 ? hs[i > 0 ? i - 1 : 0][j] : h0[j];
-          const float gacc = fmaf(gy, Cv[j], gs[j]);
-          const float gsn = gacc * dAs[i][j];
-          const float q = gsn * hprev;
-          gA[j] = fmaf(dtv, q, gA[j]);
-          S2 = fmaf(Af[j], q, S2);
-          S1 = fmaf(gacc, Bv[j], S1);
-          v[j] = gacc * dtu;          // dB contribution
-          v[4 + j] = gy * hs[i][j];   // dC contribution
-          gs[j] = gsn;
+            for (int j = 0; j < kNpw; ++j) {
+              const float hprev = i > 0 ? hs[i > 0 ? i - 1 : 0][j] : h0[j];
+              const float gacc = fmaf(gy, Cv[j], gs[j]);
+              const float gsn = gacc * dAs[i][j];
+              const float q = gsn * hprev;
+              gA[j] = fmaf(dtv, q, gA[j]);
+              S2 = fmaf(Af[j], q, S2);
+              S1 = fmaf(gacc, Bv[j], S1);
+              v[j] = gacc * dtu;          // dB contribution
+              v[4 + j] = gy * hs[i][j];   // dC contribution
+              gs[j] = gsn;
+            }
+            durow[i] = dtv * S1;
+            ddtrow[i] = fmaf(uv, S1, S2);
+            float o0, o1;
+            reduce8(v, o0, o1);
+            if ((lane & 15) == i) {
+              keep0 = o0;
+              keep1 = o1;
+            }
+          }
         }
-        durow[i] = dtv * S1;
-        ddtrow[i] = fmaf(uv, S1, S2);
-        float o0, o1;
-        reduce8(v, o0, o1);
-        if ((lane & 15) == i) {
-          keep0 = o0;
-          keep1 = o1;
+        // lane (row r, column c) holds the tile-partials of step t0 + c:
+        // r = 0: dB[n0], dB[n0+1]; r = 1: dB[n0+2], dB[n0+3]; r = 2, 3: same for dC
+        const int r = lane >> 4, c = lane & 15;
+        if (FULL || c < nsteps) {
+          float* dst = (r < 2 ? a.part_dB : a.part_dC) + part0 + static_cast<size_t>(t0 + c) * a.N;
+          const int nn = n0 + 2 * (r & 1);
+          if (nn < a.N) dst[nn] = keep0;
+          if (nn + 1 < a.N) dst[nn + 1] = keep1;
         }
-      }
-    }
-    // lane (row r, column c) holds the tile-partials of step t0 + c:
-    // r = 0: dB[n0], dB[n0+1]; r = 1: dB[n0+2], dB[n0+3]; r = 2, 3: same for dC
-    {
-      const int r = lane >> 4, c = lane & 15;
-      if (c < nsteps) {
-        float* dst = (r < 2 ? a.part_dB : a.part_dC) + part0 + static_cast<size_t>(t0 + c) * a.N;
-        const int nn = n0 + 2 * (r & 1);
-        if (nn < a.N) dst[nn] = keep0;
-        if (nn + 1 < a.N) dst[nn + 1] = keep1;
-      }
+      };
+      if (nsteps == TT)
+        tile_body(std::true_type{});
+      else
+        tile_body(std::false_type{});
     }
     __syncthreads();
 
     // finish du / ddt over the waves (states), accumulate over passes
-    for (int i = threadIdx.x; i < kWave * TT; i += blockDim.x) {
-      const int r = i / TT, c = i - r * TT;
+#pragma unroll
+    for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+      int r, c;
+      tile_pos<TT>(k, r, c);
       const int dd = d0 + r, t = t0 + c;
       if (dd >= a.D || t >= a.L) continue;
-      float su = 0.f, sd = 0.f;
+      float4 su = make_float4(0.f, 0.f, 0.f, 0.f), sd = su;
       for (int v = 0; v < nw; ++v) {
-        su += s_du[(v * kWave + r) * RS + c];
-        sd += s_ddt[(v * kWave + r) * RS + c];
+        const float* pu = s_du + (v * kWave + r) * RS + c;
+        const float* pd = s_ddt + (v * kWave + r) * RS + c;
+        su.x += pu[0];
+        su.y += pu[1];
+        su.z += pu[2];
+        su.w += pu[3];
+        sd.x += pd[0];
+        sd.y += pd[1];
+        sd.z += pd[2];
+        sd.w += pd[3];
       }
       const size_t gi = row0 + static_cast<size_t>(dd) * a.L + t;
       if (!a.first) {
-        su += a.du[gi];
-        sd += a.ddt[gi];
+        su.x += a.du[gi];
+        sd.x += a.ddt[gi];
+        if (t + 1 < a.L) { su.y += a.du[gi + 1]; sd.y += a.ddt[gi + 1]; }
+        if (t + 2 < a.L) { su.z += a.du[gi + 2]; sd.z += a.ddt[gi + 2]; }
+        if (t + 3 < a.L) { su.w += a.du[gi + 3]; sd.w += a.ddt[gi + 3]; }
       }
-      a.du[gi] = su;
-      a.ddt[gi] = sd;
+      store_row4<VEC>(a.du, gi, t, a.L, su);
+      store_row4<VEC>(a.ddt, gi, t, a.L, sd);
     }
   }
 
-  if (dvalid) {
+  if (dvalid && wave_active) {
 #pragma unroll
     for (int j = 0; j < kNpw; ++j)
       if (n0 + j < a.N) a.part_dA[(static_cast<size_t>(b) * a.D + d) * a.N + n0 + j] = gA[j];
@@ -518,11 +708,13 @@ int check_selective(int64_t Bsz, int64_t D, int64_t L, int64_t N, const char* wh
 
 int64_t num_chunks(int64_t L) { return L <= 0 ? 0 : (L + kChunk - 1) / kChunk; }
 
-// Rows of [.., L] can be staged with float4 loads when every row start is
-// 16-byte aligned.
-bool rows_vectorizable(int64_t L, const float* p, const float* q) {
-  return L % 4 == 0 && reinterpret_cast<uintptr_t>(p) % 16 == 0 &&
-         reinterpret_cast<uintptr_t>(q) % 16 == 0;
+// Rows of [.., L] tensors can move as float4 when L % 4 == 0 and every row
+// tensor starts 16-byte aligned (null pointers are not used and pass).
+bool rows_vectorizable(int64_t L, std::initializer_list<const float*> ptrs) {
+  if (L % 4 != 0) return false;
+  for (const float* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
+  return true;
 }
 
 }  // namespace
@@ -558,16 +750,16 @@ int ossm_selective_forward(const float* u, const float* dt, const float* A, cons
   a.L = static_cast<int>(length);
   a.N = static_cast<int>(dstate);
   a.n_chunks = static_cast<int>(num_chunks(length));
-  a.vec = rows_vectorizable(length, u, dt) ? 1 : 0;
+  a.vec = rows_vectorizable(length, {u, dt, gate, out, raw_out}) ? 1 : 0;
   const dim3 grid(static_cast<unsigned>((dim + kWave - 1) / kWave), static_cast<unsigned>(batch));
   const int n_pass = static_cast<int>((dstate + kPassStates - 1) / kPassStates);
   for (int p = 0; p < n_pass; ++p) {
     a.n_base = p * kPassStates;
     a.first = p == 0;
     a.last = p == n_pass - 1;
-    const int states = static_cast<int>(std::min<int64_t>(kPassStates, dstate - a.n_base));
-    const int waves = (states + kNpw - 1) / kNpw;
-    hipLaunchKernelGGL(selective_fwd_kernel, grid, dim3(waves * kWave), 0, stream, a);
+    auto kern = a.vec ? (gate ? selective_fwd_kernel<true, true> : selective_fwd_kernel<true, false>)
+                      : (gate ? selective_fwd_kernel<false, true> : selective_fwd_kernel<false, false>);
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, a);
     if (int rc = launch_check("selective_fwd_kernel")) return rc;
   }
   return OSSM_OK;
@@ -631,15 +823,15 @@ int ossm_selective_backward(const float* grad_out, const float* u, const float* 
   a.L = static_cast<int>(length);
   a.N = static_cast<int>(dstate);
   a.n_chunks = static_cast<int>(num_chunks(length));
-  a.vec = rows_vectorizable(length, u, dt) ? 1 : 0;
+  a.vec = rows_vectorizable(length, {grad_out, u, dt, gate, raw_out, du, ddt, dgate}) ? 1 : 0;
   const dim3 grid(static_cast<unsigned>(n_dtiles), static_cast<unsigned>(batch));
   const int n_pass = static_cast<int>((dstate + kPassStates - 1) / kPassStates);
   for (int p = 0; p < n_pass; ++p) {
     a.n_base = p * kPassStates;
     a.first = p == 0;
-    const int states = static_cast<int>(std::min<int64_t>(kPassStates, dstate - a.n_base));
-    const int waves = (states + kNpw - 1) / kNpw;
-    hipLaunchKernelGGL(selective_bwd_kernel, grid, dim3(waves * kWave), 0, stream, a);
+    auto kern = a.vec ? (gate ? selective_bwd_kernel<true, true> : selective_bwd_kernel<true, false>)
+                      : (gate ? selective_bwd_kernel<false, true> : selective_bwd_kernel<false, false>);
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, a);
     if (int rc = launch_check("selective_bwd_kernel")) return rc;
   }
   const int64_t n_fin = n_bln > n_dn ? n_bln : n_dn;
