@@ -1,19 +1,25 @@
 #!/usr/bin/env python3
-"""Scan state-steps/s on one MI355X: D-LinOSS imex1 forward + backward at
-BASELINE config 2 (B=32, L=4096, P=128, H=128), through the drop-in
-``ossm._kernels`` entry points (ossm_amd._kernels -> libossm_scan.so).
+"""Scan state-steps/s on one MI355X, through the drop-in ``ossm._kernels``
+entry points (ossm_amd._kernels -> libossm_scan.so).
 
-A "step" is one forward (dlinoss_imex1_forward: states [L,B,P,2]) plus one
-backward (dlinoss_imex1_backward: grads of a, g, dt and bu) over one batch of
-synthetic, seeded inputs already resident in HBM.  Timing uses HIP events on
+Headline (``value``): D-LinOSS imex1 forward + backward at BASELINE config 2
+(B=32, L=4096, P=128, H=128).  A "step" is one forward
+(dlinoss_imex1_forward: states [L,B,P,2]) plus one backward
+(dlinoss_imex1_backward: grads of a, g, dt and bu) over one batch of seeded
+synthetic inputs already resident in HBM.  Timing uses HIP events recorded on
 the stream the kernels run on (torch's current stream).
 
-Prints ONE JSON line (rank 0).  Extra fields:
+One JSON line is printed.  Besides the contract fields:
   roofline      HBM roofline of the dominant launch (algorithmic bytes / its
-                mean event-timed duration vs 8 TB/s)
+                mean event-timed duration, vs 8 TB/s); ``traffic`` is the
+                measured HBM bytes per launch from rocprofv3 FETCH_SIZE /
+                WRITE_SIZE (profiles/dlinoss_imex1_config2_pmc.json) or null
   cpu_baseline  the reference's own CPU kernels (oracle/_ref, compiled from the
                 reference sources) on the same workload on this host's cores
-  detail        per-direction figures (forward, backward)
+  detail        per-direction figures and the other BASELINE configs
+
+``--calibrate-copy`` runs only a device-to-device copy of known size, for
+scaling the FETCH_SIZE / WRITE_SIZE counters.
 """
 
 from __future__ import annotations
@@ -25,20 +31,43 @@ import platform
 import statistics
 import sys
 import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
 
 PEAK_HBM = 8.0e12  # MI355X HBM3E, bytes/s
 METRIC = "scan state-steps/s (B·L·state) + % of HBM peak, fwd and fwd+bwd, 1 GPU"
-BYTES_FWD = 24  # per state-step: read bu (8) + write states (16)
-BYTES_BWD = 24  # per state-step: read bu (8) + read grad (8) + write grad_bu (8)
+# algorithmic bytes per state-step (each required input read once, each output written once)
+DL_BYTES_FWD = 24  # read bu (8) + write states (16)
+DL_BYTES_BWD = 24  # read bu (8) + read grad (8) + write grad_bu (8)
+PMC_FILE = ROOT / "profiles" / "dlinoss_imex1_config2_pmc.json"
 
 
-def _inputs(torch, L, B, P, device, seed=0):
-    """Config-2 distributions: A ~ U(0.1,1), G ~ U(0,1), dt = sigmoid(N(0,1)),
+# ----------------------------------------------------------------- timing
+def _ev_time(torch, fn, reps: int, warm: int) -> float:
+    """Median milliseconds of fn() between two events on the current stream."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    for e0, e1 in evs:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+
+
+# ----------------------------------------------------------------- inputs
+def dlinoss_inputs(torch, L, B, P, device, H=128, seed=0):
+    """Config-2/5 distributions: A ~ U(0.1,1), G ~ U(0,1), dt = sigmoid(N(0,1)),
     A projected into DampedLinOSSLayer's stable band (dlinoss.py:252-267),
     bu = u B^T with B complex N(0, 1/H), u ~ N(0,1) (formed once, untimed),
     upstream grad complex N(0,1)."""
     g = torch.Generator(device=device).manual_seed(seed)
-    H = 128
     a = torch.rand(P, device=device, generator=g) * 0.9 + 0.1
     gam = torch.rand(P, device=device, generator=g)
     dt = torch.sigmoid(torch.randn(P, device=device, generator=g))
@@ -50,14 +79,61 @@ def _inputs(torch, L, B, P, device, seed=0):
                        torch.randn(P, H, device=device, generator=g)) / (H ** 0.5)
     u = torch.randn(L, B, H, device=device, generator=g)
     bu = torch.matmul(u.to(torch.complex64), Bw.t().contiguous()).contiguous()
+    del u
     go = torch.complex(torch.randn(L, B, P, device=device, generator=g),
                        torch.randn(L, B, P, device=device, generator=g))
     return a.contiguous(), gam.contiguous(), dt.contiguous(), bu, go
 
 
-def _cpu_baseline(L, B, P, budget_s=12.0):
-    """Reference CPU kernels (oracle/_ref) on the full config-2 workload."""
-    import numpy as np
+def selective_inputs(torch, Bz, D, L, N, device, seed=0, gated=True):
+    """Config-3/4 distributions: A = -exp(log(1..N)), dt = softplus(N(0,1) - 4),
+    u, B, C, z, upstream grad ~ N(0,1); B/C in the API layout [B, L, N]."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    u = torch.randn(Bz, D, L, device=device, generator=g)
+    dt = torch.nn.functional.softplus(torch.randn(Bz, D, L, device=device, generator=g) - 4.0)
+    A = -torch.exp(torch.log(torch.arange(1, N + 1, device=device, dtype=torch.float32))).repeat(D, 1)
+    Bm = torch.randn(Bz, L, N, device=device, generator=g)
+    Cm = torch.randn(Bz, L, N, device=device, generator=g)
+    z = torch.randn(Bz, D, L, device=device, generator=g) if gated else None
+    go = torch.randn(Bz, D, L, device=device, generator=g)
+    return u, dt, A.contiguous(), Bm, Cm, z, go
+
+
+def linoss_im_inputs(torch, L, B, P, device, H=64, seed=0):
+    """Config-1: A = relu(N(0,1)) + 0.1, dt = sigmoid(N(0,1)), B complex N(0,1/H),
+    u ~ N(0,1); LinOSS-IM transition and b_seq = (bu m11 dt, bu m21 dt)
+    (linoss.py:244-251), formed once, untimed."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    A = torch.relu(torch.randn(P, device=device, generator=g)) + 0.1
+    dt = torch.sigmoid(torch.randn(P, device=device, generator=g))
+    Bw = torch.complex(torch.randn(P, H, device=device, generator=g),
+                       torch.randn(P, H, device=device, generator=g)) / (H ** 0.5)
+    u = torch.randn(B, L, H, device=device, generator=g)
+    bu = torch.matmul(u.to(torch.complex64), Bw.t().contiguous()).permute(1, 0, 2)  # [L,B,P]
+    schur = 1.0 / (1.0 + dt * dt * A)
+    m11 = (1.0 - dt * dt * A * schur).to(torch.complex64)
+    m12 = (-dt * A * schur).to(torch.complex64)
+    m21 = (dt * schur).to(torch.complex64)
+    m22 = schur.to(torch.complex64)
+    b_seq = torch.stack([bu * m11 * dt, bu * m21 * dt], dim=-1).contiguous()
+    return m11, m12, m21, m22, b_seq
+
+
+# ------------------------------------------------------------ CPU baseline
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def cpu_baseline(L, B, P, budget_s=12.0):
+    """The reference's own CPU kernels (oracle/_ref) on the full config-2
+    workload, else the C restatement (oracle/)."""
     import torch
 
     try:
@@ -65,10 +141,9 @@ def _cpu_baseline(L, B, P, budget_s=12.0):
     except Exception as exc:  # pragma: no cover
         return {"error": f"oracle unavailable: {exc}"}
     ref = oracle.reference_module()
-    kind = "reference"
-    threads = os.cpu_count() or 1
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     torch.set_num_threads(threads)
-    a, gam, dt, bu, go = (x.cpu() for x in _inputs(torch, L, B, P, torch.device("cpu"), seed=0))
+    a, gam, dt, bu, go = (x.cpu() for x in dlinoss_inputs(torch, L, B, P, torch.device("cpu")))
     if ref is None:
         kind = "port"
 
@@ -78,6 +153,8 @@ def _cpu_baseline(L, B, P, budget_s=12.0):
                                     go.numpy())
         threads = oracle.num_threads()
     else:
+        kind = "reference"
+
         def run():
             st = ref.dlinoss_imex1_forward(a, gam, dt, bu)
             ref.dlinoss_imex1_backward(a, gam, dt, bu, st, go)
@@ -90,27 +167,76 @@ def _cpu_baseline(L, B, P, budget_s=12.0):
         run()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as fh:
-            for line in fh:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    src = ("reference CPU kernels compiled from src/ossm/csrc (oracle/_ref)" if kind == "reference"
+           else "C restatement of the reference CPU kernels (oracle/)")
     return {
         "value": L * B * P / med,
         "unit": "state-steps/s",
         "cores": threads,
         "kind": kind,
-        "sample": (f"full config-2 workload (D-LinOSS imex1 fwd+bwd, B={B} L={L} P={P}), "
-                   f"median of {len(times)} runs after 2 warmups, "
-                   f"{'reference CPU kernels compiled from src/ossm/csrc (oracle/_ref)' if kind == 'reference' else 'C restatement (oracle/)'}; "
-                   f"the reference parallelises over P only (at most {P} threads)"),
+        "sample": (f"the full config-2 workload (D-LinOSS imex1 fwd+bwd, B={B} L={L} P={P}), "
+                   f"median of {len(times)} runs after 2 warmups ({sum(times):.1f} s of CPU work), "
+                   f"{src}; the reference parallelises over P only (at most {P} threads)"),
         "seconds_per_step": med,
-        "cpu_model": cpu_model or platform.processor(),
+        "cpu_model": _cpu_model(),
     }
+
+
+# ------------------------------------------------------------ other configs
+def _detail_configs(torch, K, dev, reps=10):
+    """The other BASELINE configs, each timed with events (median of `reps`)."""
+    out = {}
+    # C1: LinOSS-IM forward, B=8 L=1024 P=64
+    L, B, P = 1024, 8, 64
+    m11, m12, m21, m22, b_seq = linoss_im_inputs(torch, L, B, P, dev)
+    ms = _ev_time(torch, lambda: K.linoss_scan(m11, m12, m21, m22, b_seq), reps, 3)
+    n = L * B * P
+    out["c1_linoss_im_fwd"] = {"ms": ms, "state_steps_per_s": n / (ms / 1e3),
+                               "hbm_frac": n * 32 / (ms / 1e3) / PEAK_HBM}
+    del b_seq
+    # C5: D-LinOSS imex1 forward, B=4 L=65536 P=256
+    L, B, P = 65536, 4, 256
+    a, gam, dt, bu, _ = dlinoss_inputs(torch, L, B, P, dev, H=64, seed=5)
+    ms = _ev_time(torch, lambda: K.dlinoss_imex1_forward(a, gam, dt, bu), reps, 3)
+    n = L * B * P
+    out["c5_dlinoss_fwd_long"] = {"ms": ms, "state_steps_per_s": n / (ms / 1e3),
+                                  "GBps": n * DL_BYTES_FWD / (ms / 1e3) / 1e9,
+                                  "hbm_frac": n * DL_BYTES_FWD / (ms / 1e3) / PEAK_HBM}
+    del bu
+    # C3 / C4-shape: selective scan fwd+bwd, fp32, gated
+    for key, (Bz, D, L, N) in (("c3_selective_fp32", (256, 128, 200, 16)),
+                               ("c4_shape_selective_fp32", (16, 1536, 2048, 16))):
+        u, dts, A, Bm, Cm, z, go = selective_inputs(torch, Bz, D, L, N, dev)
+        res = K.selective_scan_cuda(u, dts, A, Bm, Cm, z)
+        tf = _ev_time(torch, lambda: K.selective_scan_cuda(u, dts, A, Bm, Cm, z), reps, 3)
+        tb = _ev_time(torch, lambda: K.selective_scan_cuda_backward(
+            go, u, dts, A, Bm, Cm, z, res[1], res[2], 16), reps, 3)
+        T = Bz * D * L
+        fb = T * 16 + Bz * L * N * 8          # u, dt, z in; out out; B, C in
+        bb = T * 28 + Bz * L * N * 16         # u, dt, z, dout in; du, ddt, dz out; B, C in; dB, dC out
+        out[key] = {"fwd_ms": tf, "bwd_ms": tb,
+                    "state_steps_per_s_fwd_bwd": T * N / ((tf + tb) / 1e3),
+                    "hbm_frac_fwd": fb / (tf / 1e3) / PEAK_HBM,
+                    "hbm_frac_bwd": bb / (tb / 1e3) / PEAK_HBM,
+                    "hbm_frac_fwd_bwd": (fb + bb) / ((tf + tb) / 1e3) / PEAK_HBM,
+                    "note": "bound by VALU (one exp and ~20 FMA-class ops per state-step fwd+bwd), not HBM"}
+        del u, dts, Bm, Cm, z, go, res
+    torch.cuda.empty_cache()
+    return out
+
+
+def calibrate_copy(nbytes=1 << 30, reps=5):
+    """A plain device copy of `nbytes`, for scaling FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).uniform_()
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": nbytes, "launches": reps}), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -120,22 +246,27 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--variant", default="imex1", choices=["imex1", "imex2", "im", "ex"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-detail", action="store_true", help="skip the other BASELINE configs")
+    ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
 
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: every box in this run has "
-                          "a single MI355X and the scan needs no collectives; see DESIGN.md "
-                          "for how the path would shard", "n_gpus": args.gpus}))
+                          "a single MI355X and the scans need no collectives; DESIGN.md "
+                          "describes how the path would shard", "n_gpus": args.gpus}))
         return 2
+    if args.calibrate_copy:
+        return calibrate_copy()
 
     import torch
 
     from ossm_amd import _kernels as K
+    from ossm_amd import _lib
 
     L, B, P = 4096, 32, 128
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    a, gam, dt, bu, go = _inputs(torch, L, B, P, dev, seed=0)
+    a, gam, dt, bu, go = dlinoss_inputs(torch, L, B, P, dev, seed=0)
     fwd = getattr(K, f"dlinoss_{args.variant}_forward")
     bwd = getattr(K, f"dlinoss_{args.variant}_backward")
 
@@ -158,29 +289,43 @@ def main() -> int:
     end.record()
     torch.cuda.synchronize()
 
-    from ossm_amd import _lib
-
     err_bits = _lib.device_error_bits(dev)
     total_ms = start.elapsed_time(end)
     fwd_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1, _ in ev)
     bwd_ms = statistics.mean(e1.elapsed_time(e2) for _, e1, e2 in ev)
     ms_per_step = total_ms / args.steps
-    steps_units = L * B * P
-    value = steps_units * args.steps / (total_ms / 1e3)
+    units = L * B * P
+    value = units * args.steps / (total_ms / 1e3)
 
-    fwd_bw = steps_units * BYTES_FWD / (fwd_ms / 1e3)
-    bwd_bw = steps_units * BYTES_BWD / (bwd_ms / 1e3)
-    dom = ("backward", bwd_bw, bwd_ms, BYTES_BWD) if bwd_ms >= fwd_ms else ("forward", fwd_bw, fwd_ms, BYTES_FWD)
+    fwd_bw = units * DL_BYTES_FWD / (fwd_ms / 1e3)
+    bwd_bw = units * DL_BYTES_BWD / (bwd_ms / 1e3)
+    if bwd_ms >= fwd_ms:
+        dom = {"name": f"dlinoss_{args.variant}_backward",
+               "launches": ["osc_backward_kernel<Dlinoss>", "osc_reduce_chunks_kernel",
+                            "osc_param_kernel"],
+               "bw": bwd_bw, "ms": bwd_ms, "bytes": units * DL_BYTES_BWD, "key": "backward"}
+    else:
+        dom = {"name": f"dlinoss_{args.variant}_forward", "launches": ["osc_forward_kernel<Dlinoss>"],
+               "bw": fwd_bw, "ms": fwd_ms, "bytes": units * DL_BYTES_FWD, "key": "forward"}
+    traffic = None
+    if PMC_FILE.exists():
+        try:
+            pmc = json.loads(PMC_FILE.read_text())
+            traffic = pmc.get(dom["key"], {}).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
     roofline = {
         "bound": "hbm",
-        "achieved": dom[1] / 1e9,
+        "achieved": dom["bw"] / 1e9,
         "peak": PEAK_HBM / 1e9,
         "unit": "GB/s",
-        "frac": dom[1] / PEAK_HBM,
-        "traffic": None,
-        "kernel": f"dlinoss_{args.variant} {dom[0]} (scan kernel + per-oscillator reduction)"
-        if dom[0] == "backward" else f"dlinoss_{args.variant} forward scan kernel",
-        "algorithmic_bytes_per_launch": steps_units * dom[3],
+        "frac": dom["bw"] / PEAK_HBM,
+        "traffic": traffic,
+        "kernel": dom["name"],
+        "launches": dom["launches"],
+        "algorithmic_bytes_per_launch": dom["bytes"],
+        "bytes_per_state_step": DL_BYTES_BWD if dom["key"] == "backward" else DL_BYTES_FWD,
+        "mean_launch_ms": dom["ms"],
     }
     out = {
         "metric": METRIC,
@@ -198,19 +343,26 @@ def main() -> int:
         "config": {"workload": f"D-LinOSS {args.variant} fwd+bwd (BASELINE config 2)",
                    "batch": B, "seq_len": L, "ssm_size": P, "hidden_dim": 128},
         "roofline": roofline,
-        "detail": {
-            "forward": {"ms": fwd_ms, "state_steps_per_s": steps_units / (fwd_ms / 1e3),
-                        "GBps": fwd_bw / 1e9, "hbm_frac": fwd_bw / PEAK_HBM},
-            "backward": {"ms": bwd_ms, "state_steps_per_s": steps_units / (bwd_ms / 1e3),
-                         "GBps": bwd_bw / 1e9, "hbm_frac": bwd_bw / PEAK_HBM},
-            "fwd_bwd_hbm_frac": steps_units * (BYTES_FWD + BYTES_BWD) / (ms_per_step / 1e3) / PEAK_HBM,
-            "device_error_bits": err_bits,
-        },
     }
+    detail = {
+        "forward": {"ms": fwd_ms, "state_steps_per_s": units / (fwd_ms / 1e3),
+                    "GBps": fwd_bw / 1e9, "hbm_frac": fwd_bw / PEAK_HBM},
+        "backward": {"ms": bwd_ms, "state_steps_per_s": units / (bwd_ms / 1e3),
+                     "GBps": bwd_bw / 1e9, "hbm_frac": bwd_bw / PEAK_HBM},
+        "fwd_bwd_hbm_frac": units * (DL_BYTES_FWD + DL_BYTES_BWD) / (ms_per_step / 1e3) / PEAK_HBM,
+        "device_error_bits": err_bits,
+    }
+    del st
+    if not args.no_detail:
+        del a, gam, dt, bu, go
+        torch.cuda.empty_cache()
+        detail["configs"] = _detail_configs(torch, K, dev)
+        detail["device_error_bits"] |= _lib.device_error_bits(dev)
+    out["detail"] = detail
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = _cpu_baseline(L, B, P)
+        out["cpu_baseline"] = cpu_baseline(L, B, P)
     print(json.dumps(out), flush=True)
-    return 0 if err_bits == 0 else 1
+    return 0 if detail["device_error_bits"] == 0 else 1
 
 
 if __name__ == "__main__":

@@ -1,0 +1,172 @@
+"""Autograd bridges over the MI355X scan library, mirroring the reference's
+kernel bridges (the L2 layer above ``ossm._kernels``):
+
+* D-LinOSS: ``run_dlinoss``, ``has_kernels``, ``extension_error`` and one
+  autograd Function per variant — reference src/ossm/models/_dlinoss_scan.py:416-680.
+  Forward saves ``(a, g, step, bu, states)`` and returns ``states[..., 1]``;
+  backward passes ``grad_output.contiguous()`` (:461-498).
+* LinOSS: ``try_run_scan`` (_linoss_scan.py:44-63) plus ``LinossScanFn`` whose
+  backward is the native ``linoss_scan_backward`` instead of the reference's
+  Python loop (models/linoss.py:83-151).
+* Selective scan: ``try_selective_scan`` and ``SelectiveScanFn``
+  (_selective_scan.py:127-297): fp32 only, the no-grad shortcut, the
+  ``(out, chunk_states, raw_out)`` forward saved for the backward.
+
+Differences from the reference bridges, on purpose: there is no pure-PyTorch
+fallback and no swallowed RuntimeError.  A missing library is an ImportError
+at import time; an unsupported dtype or device raises RuntimeError.  (When this
+library is installed as ``ossm._kernels`` under the reference's own bridges,
+those bridges keep their fp64 and error fallbacks; this module is for callers
+that use the MI355X path directly.)
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _kernels
+
+__all__ = [
+    "has_kernels", "extension_error", "run_dlinoss", "run_dlinoss_imex1", "DlinossFn",
+    "try_run_scan", "LinossScanFn", "try_selective_scan", "SelectiveScanFn",
+]
+
+SUPPORTED_VARIANTS = ("imex1", "imex2", "im", "ex")
+
+
+def has_kernels(variant: Optional[str] = None) -> bool:
+    """True when the device kernels for ``variant`` (or all variants) exist
+    (reference _dlinoss_scan.py:416-435)."""
+    if variant is None:
+        return all(has_kernels(v) for v in SUPPORTED_VARIANTS)
+    variant = variant.lower()
+    if variant not in SUPPORTED_VARIANTS:
+        raise ValueError(f"Unknown D-LinOSS variant '{variant}'.")
+    return hasattr(_kernels, f"dlinoss_{variant}_forward")
+
+
+def extension_error() -> Optional[Exception]:
+    """Always None: the library loads at import or the import fails."""
+    return None
+
+
+# ------------------------------------------------------------------ D-LinOSS
+class DlinossFn(torch.autograd.Function):
+    """Autograd bridge of one D-LinOSS variant (reference _DlinossImex1Fn and
+    siblings, _dlinoss_scan.py:458-600)."""
+
+    @staticmethod
+    def forward(ctx, variant: str, a_diag: Tensor, g_diag: Tensor, step: Tensor,
+                bu: Tensor) -> Tensor:  # type: ignore[override]
+        states = getattr(_kernels, f"dlinoss_{variant}_forward")(a_diag, g_diag, step, bu)
+        ctx.variant = variant
+        ctx.save_for_backward(a_diag, g_diag, step, bu, states)
+        return states[..., 1]
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):  # type: ignore[override]
+        a_diag, g_diag, step, bu, states = ctx.saved_tensors
+        grad_a, grad_g, grad_step, grad_bu = getattr(_kernels, f"dlinoss_{ctx.variant}_backward")(
+            a_diag, g_diag, step, bu, states, grad_output.contiguous())
+        return None, grad_a, grad_g, grad_step, grad_bu
+
+
+def run_dlinoss(variant: str, a_diag: Tensor, g_diag: Tensor, step: Tensor, bu: Tensor) -> Tensor:
+    """x = states[..., 1] of the D-LinOSS recurrence for ``variant``
+    (reference run_dlinoss, _dlinoss_scan.py:630-680).  bu is [L, B, P]
+    complex64 on the device; a, g, step are [P] float32."""
+    variant = variant.lower()
+    if variant not in SUPPORTED_VARIANTS:
+        raise ValueError(f"Unknown D-LinOSS variant '{variant}'.")
+    if bu.numel() == 0:
+        return bu
+    if bu.dtype != torch.complex64 or any(t.dtype != torch.float32 for t in (a_diag, g_diag, step)):
+        raise RuntimeError("the MI355X D-LinOSS kernels compute in float32/complex64; "
+                           f"got bu {bu.dtype}, coefficients {a_diag.dtype}")
+    return DlinossFn.apply(variant, a_diag, g_diag, step, bu)
+
+
+def run_dlinoss_imex1(a_diag: Tensor, g_diag: Tensor, step: Tensor, bu: Tensor) -> Tensor:
+    """reference run_dlinoss_imex1 (_dlinoss_scan.py:683-686)."""
+    return run_dlinoss("imex1", a_diag, g_diag, step, bu)
+
+
+# -------------------------------------------------------------------- LinOSS
+class LinossScanFn(torch.autograd.Function):
+    """``s_t = M s_{t-1} + b_t`` with complex M per oscillator (reference
+    _LinossScanFn, models/linoss.py:57-157); the backward runs on the device."""
+
+    @staticmethod
+    def forward(ctx, m11: Tensor, m12: Tensor, m21: Tensor, m22: Tensor,
+                b_seq: Tensor) -> Tensor:  # type: ignore[override]
+        states = _kernels.linoss_scan(m11, m12, m21, m22, b_seq)
+        ctx.save_for_backward(m11, m12, m21, m22, states)
+        return states
+
+    @staticmethod
+    def backward(ctx, grad_states: Tensor):  # type: ignore[override]
+        m11, m12, m21, m22, states = ctx.saved_tensors
+        grad_m, grad_b = _kernels.linoss_scan_backward(m11, m12, m21, m22, states,
+                                                       grad_states.contiguous())
+        return grad_m[:, 0, 0], grad_m[:, 0, 1], grad_m[:, 1, 0], grad_m[:, 1, 1], grad_b
+
+
+def try_run_scan(m11: Tensor, m12: Tensor, m21: Tensor, m22: Tensor, b_seq: Tensor) -> Tensor:
+    """States [L, B, P, 2] of the LinOSS scan (reference try_run_scan,
+    _linoss_scan.py:44-63), differentiable through the native backward."""
+    if b_seq.numel() == 0:
+        return b_seq
+    return LinossScanFn.apply(m11, m12, m21, m22, b_seq)
+
+
+# ----------------------------------------------------------- selective scan
+class SelectiveScanFn(torch.autograd.Function):
+    """Reference _SelectiveScanFn (_selective_scan.py:199-297), device path."""
+
+    @staticmethod
+    def forward(ctx, inputs: Tensor, dt: Tensor, A: Tensor, B: Tensor, C: Tensor,
+                gate: Optional[Tensor], chunk_length: int) -> Tensor:  # type: ignore[override]
+        if inputs.dtype != torch.float32:
+            raise RuntimeError("Selective scan kernels require float32 inputs")
+        if dt.dtype != torch.float32 or A.dtype != torch.float32:
+            raise RuntimeError("Selective scan kernels require float32 parameters")
+        if gate is not None and gate.dtype != torch.float32:
+            raise RuntimeError("Selective scan kernels require float32 gate")
+        if int(chunk_length) <= 0:
+            raise RuntimeError("chunk_length must be positive")
+        gate_c = gate.contiguous() if gate is not None else None
+        tensors = [x.contiguous() for x in (inputs, dt, A, B, C)]
+        out, chunk_states, raw = _kernels.selective_scan_cuda(*tensors, gate_c, int(chunk_length))
+        ctx.has_gate = gate_c is not None
+        ctx.chunk = int(chunk_length)
+        ctx.save_for_backward(*tensors, gate_c if gate_c is not None else inputs.new_empty(0),
+                              chunk_states, raw)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):  # type: ignore[override]
+        inputs, dt, A, B, C, gate_saved, chunk_states, raw = ctx.saved_tensors
+        gate = gate_saved if ctx.has_gate else None
+        grads = _kernels.selective_scan_cuda_backward(grad_output.contiguous(), inputs, dt, A, B, C,
+                                                      gate, chunk_states, raw, ctx.chunk)
+        du, ddt, dA, dB, dC, dz = grads
+        return du, ddt, dA, dB, dC, (dz if ctx.has_gate else None), None
+
+
+def try_selective_scan(inputs: Tensor, dt: Tensor, A: Tensor, B: Tensor, C: Tensor,
+                       gate: Optional[Tensor], chunk_length: int = 64) -> Tensor:
+    """Fused selective scan on the device (reference try_selective_scan,
+    _selective_scan.py:127-196): the no-grad case skips the autograd wrapper."""
+    if inputs.numel() == 0:
+        return inputs
+    if not inputs.is_cuda:
+        raise RuntimeError("try_selective_scan: the MI355X path needs device tensors")
+    requires_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (inputs, dt, A, B, C, gate))
+    if not requires_grad:
+        return _kernels.selective_scan_cuda(inputs, dt, A, B, C, gate, chunk_length)[0]
+    return SelectiveScanFn.apply(inputs, dt, A, B, C, gate, chunk_length)
+

@@ -1,0 +1,174 @@
+"""Layer-level parity through the autograd bridges (ossm_amd.bridge), in the
+shape of the reference's kernel-vs-fallback tests: the reference compares its
+kernel path with its pure-PyTorch path on a layer's outputs and every
+parameter gradient (tests/test_dlinoss_kernels.py:14-70, fp32 atol 1e-4 /
+rtol 5e-4; tests/test_scan_parity.py:138-183 for the selective scan).  Here the
+other side is a plain fp64 loop on the CPU (tests/_brute.py) differentiated by
+torch.autograd.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from tests import _brute
+from tests.gpu_util import announce, need_gpu
+
+pytestmark = pytest.mark.gpu
+VARIANTS = ("imex1", "imex2", "im", "ex")
+
+
+@pytest.fixture(scope="module")
+def bridge():
+    need_gpu()
+    from ossm_amd import bridge
+
+    return bridge
+
+
+def _layer_params(P, H, seed):
+    g = torch.Generator().manual_seed(seed)
+    A = torch.rand(P, generator=g) * 0.9 + 0.1
+    G = torch.rand(P, generator=g)
+    steps = torch.randn(P, generator=g)
+    Bw = torch.randn(P, H, 2, generator=g) / H ** 0.5
+    Cw = torch.randn(H, P, 2, generator=g) / P ** 0.5
+    Dw = torch.randn(H, generator=g)
+    return A, G, steps, Bw, Cw, Dw
+
+
+def _dlinoss_layer(run, variant, A, G, steps, Bw, Cw, Dw, u):
+    """DampedLinOSSLayer.forward glue (dlinoss.py:184-278): projected
+    parameters, bu = u B^T, x = scan, y = Re(x C^T) + D u."""
+    dt = torch.sigmoid(steps)
+    g = torch.relu(G)
+    s = dt * g
+    base = torch.sqrt(torch.clamp(1.0 + s, min=1e-6))
+    denom = torch.clamp(dt * dt, min=1e-6)
+    a = torch.minimum(torch.maximum(A, (2.0 + s - 2.0 * base) / denom), (2.0 + s + 2.0 * base) / denom)
+    Bc = torch.complex(Bw[..., 0], Bw[..., 1])
+    Cc = torch.complex(Cw[..., 0], Cw[..., 1])
+    bu = torch.matmul(u.to(Bc.dtype), Bc.transpose(0, 1)).permute(1, 0, 2).contiguous()  # [L,B,P]
+    x = run(variant, a, g, dt, bu).permute(1, 0, 2)                                        # [B,L,P]
+    return torch.matmul(x, Cc.transpose(0, 1)).real + u * Dw
+
+
+# (B, L, P, H): the reference test's layer (ssm_size=8, hidden_dim=16, inputs
+# [3, 12, 16]) and a longer sequence
+LAYER_SHAPES = [(3, 12, 8, 16), (3, 300, 24, 16)]
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("shape", LAYER_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_dlinoss_layer_outputs_and_grads(bridge, variant, shape):
+    Bsz, L, P, H = shape
+    announce(f"bridge dlinoss layer {variant} {shape}")
+    params = _layer_params(P, H, seed=7)
+    if variant == "ex" and L > 50:
+        # the explicit variant grows by sqrt(1 + dt^2 a - dt g) per step where
+        # dt a > g; keep dt small so 300 steps stay representable in fp32
+        params = (params[0], params[1], params[2] - 3.0) + params[3:]
+    u = torch.randn(Bsz, L, H, generator=torch.Generator().manual_seed(8))
+    w = torch.randn(Bsz, L, H, generator=torch.Generator().manual_seed(9))
+
+    dev = [p.cuda().requires_grad_() for p in params]
+    y = _dlinoss_layer(bridge.run_dlinoss, variant, *dev, u.cuda())
+    (y * w.cuda()).sum().backward()
+
+    ref = [p.double().requires_grad_() for p in params]
+
+    def brute(variant, a, g, dt, bu):
+        return _brute.dlinoss_states(variant, a, g, dt, bu)[..., 1]
+
+    y64 = _dlinoss_layer(brute, variant, *ref, u.double())
+    (y64 * w.double()).sum().backward()
+    np.testing.assert_allclose(y.detach().cpu().numpy(), y64.detach().numpy(), rtol=5e-4, atol=1e-4)
+    for got, r, name in zip(dev, ref, ("A", "G", "steps", "B", "C", "D")):
+        np.testing.assert_allclose(got.grad.cpu().numpy(), r.grad.numpy(), rtol=5e-4,
+                                   atol=1e-4 * max(1.0, float(r.grad.abs().max())), err_msg=name)
+
+
+def test_dlinoss_bridge_rejects_fp64_and_bad_variant(bridge):
+    x = torch.zeros(4, 1, 2, dtype=torch.complex128, device="cuda")
+    p = torch.ones(2, dtype=torch.float64, device="cuda")
+    with pytest.raises(RuntimeError, match="float32"):
+        bridge.run_dlinoss("imex1", p, p, p, x)
+    with pytest.raises(ValueError, match="Unknown D-LinOSS variant"):
+        bridge.run_dlinoss("nope", p, p, p, x)
+    assert bridge.has_kernels() and bridge.has_kernels("im")
+
+
+def test_linoss_im_layer_grads(bridge):
+    """LinOSS-IM recurrence (linoss.py:244-251, 260-315) through try_run_scan
+    with the native backward, vs autograd of a fp64 loop."""
+    Bsz, L, P, H = 2, 400, 20, 12
+    announce("bridge linoss IM")
+    g = torch.Generator().manual_seed(3)
+    A0 = torch.rand(P, generator=g)
+    st0 = torch.randn(P, generator=g)
+    Bw0 = torch.randn(P, H, 2, generator=g) / H ** 0.5
+    u = torch.randn(Bsz, L, H, generator=g)
+    w = torch.randn(L, Bsz, P, generator=g)
+
+    def layer(scan, A, steps, Bw, uu):
+        dt = torch.sigmoid(steps)
+        a = torch.relu(A)
+        schur = 1.0 / (1.0 + dt * dt * a)
+        m11, m12, m21, m22 = (1.0 - dt * dt * a * schur), (-dt * a * schur), dt * schur, schur
+        Bc = torch.complex(Bw[..., 0], Bw[..., 1])
+        bu = torch.matmul(uu.to(Bc.dtype), Bc.transpose(0, 1)).permute(1, 0, 2)
+        cd = Bc.dtype
+        b_seq = torch.stack([bu * (m11 * dt).to(cd), bu * (m21 * dt).to(cd)], -1).contiguous()
+        states = scan(m11.to(cd).contiguous(), m12.to(cd).contiguous(), m21.to(cd).contiguous(),
+                      m22.to(cd).contiguous(), b_seq)
+        return states[..., 1].real
+
+    dev = [x.cuda().requires_grad_() for x in (A0, st0, Bw0)]
+    out = layer(bridge.try_run_scan, *dev, u.cuda())
+    (out * w.cuda()).sum().backward()
+
+    def brute_scan(m11, m12, m21, m22, b_seq):
+        M = torch.stack([torch.stack([m11, m12], -1), torch.stack([m21, m22], -1)], -2)
+        return _brute.linoss_states(M, b_seq)
+
+    ref = [x.double().requires_grad_() for x in (A0, st0, Bw0)]
+    out64 = layer(brute_scan, *ref, u.double())
+    (out64 * w.double()).sum().backward()
+    np.testing.assert_allclose(out.detach().cpu().numpy(), out64.detach().numpy(), rtol=5e-4, atol=1e-4)
+    for got, r, name in zip(dev, ref, ("A", "steps", "B")):
+        np.testing.assert_allclose(got.grad.cpu().numpy(), r.grad.numpy(), rtol=5e-4,
+                                   atol=1e-4 * max(1.0, float(r.grad.abs().max())), err_msg=name)
+
+
+@pytest.mark.parametrize("gated", [True, False], ids=["gate", "nogate"])
+def test_selective_bridge_grads(bridge, gated):
+    """try_selective_scan with autograd vs the fp64 Mamba loop (the reference's
+    CUDA parity test shape: B=2, D=32, L=256, N=32, rtol 2e-4 / atol 1e-4)."""
+    Bsz, D, L, N = 2, 32, 256, 32
+    announce(f"bridge selective gated={gated}")
+    g = torch.Generator().manual_seed(21)
+    u = torch.randn(Bsz, D, L, generator=g)
+    dt = torch.nn.functional.softplus(torch.randn(Bsz, D, L, generator=g) - 4.0)
+    A = -torch.exp(torch.log(torch.arange(1, N + 1, dtype=torch.float32))).repeat(D, 1)
+    Bm = torch.randn(Bsz, L, N, generator=g)
+    Cm = torch.randn(Bsz, L, N, generator=g)
+    z = torch.randn(Bsz, D, L, generator=g) if gated else None
+    w = torch.randn(Bsz, D, L, generator=g)
+    base = [u, dt, A, Bm, Cm] + ([z] if gated else [])
+    dev = [x.cuda().requires_grad_() for x in base]
+    y = bridge.try_selective_scan(*dev[:5], dev[5] if gated else None)
+    (y * w.cuda()).sum().backward()
+    ref = [x.double().requires_grad_() for x in base]
+    y64 = _brute.selective(*ref[:5], ref[5] if gated else None)
+    (y64 * w.double()).sum().backward()
+    np.testing.assert_allclose(y.detach().cpu().numpy(), y64.detach().numpy(), rtol=2e-4, atol=1e-4)
+    names = ("u", "dt", "A", "B", "C", "z")
+    for got, r, name in zip(dev, ref, names):
+        np.testing.assert_allclose(got.grad.cpu().numpy(), r.grad.numpy(), rtol=2e-4,
+                                   atol=1e-4 * max(1.0, float(r.grad.abs().max())), err_msg=name)
+    with torch.no_grad():
+        y_ng = bridge.try_selective_scan(*[x.detach() for x in dev[:5]],
+                                         dev[5].detach() if gated else None)
+    assert torch.equal(y_ng, y.detach())
