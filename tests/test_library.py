@@ -1,0 +1,101 @@
+"""CPU-side checks of the boundary: the C-ABI library loads and exports every
+symbol include/ossm_scan.h declares, and the drop-in module exposes every
+name of the reference's ``ossm._kernels`` (bindings.cpp:159-224).  No
+compute call is made (there is no GPU here)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "ossm_scan.h"
+
+# every Python-visible name of the reference extension module
+REFERENCE_NAMES = (
+    [f"dlinoss_{v}_{d}" for v in ("imex1", "imex2", "im", "ex") for d in ("forward", "backward")]
+    + [f"sdlinoss_{v}_{d}" for v in ("imex1", "imex2", "im", "ex") for d in ("forward", "backward")]
+    + ["linoss_scan", "lru_scan", "s5_scan", "linear_rnn_scan", "selective_scan",
+       "selective_scan_backward", "selective_scan_cuda", "selective_scan_cuda_backward"]
+)
+
+
+def _declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(ossm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared_functions()
+    for n in ("ossm_dlinoss_forward", "ossm_dlinoss_backward", "ossm_linoss_forward",
+              "ossm_linoss_backward", "ossm_selective_forward", "ossm_selective_backward",
+              "ossm_selective_num_chunks", "ossm_abi_version", "ossm_last_error",
+              "ossm_device_error_bits"):
+        assert n in names, n
+
+
+def test_library_exports_every_declared_symbol():
+    import torch  # noqa: F401  (binds the HIP runtime first, as the product does)
+
+    from ossm_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libossm_scan.so not built (python -m ossm_amd.build)")
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in _declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    # every declared symbol has a ctypes signature in the binding
+    assert set(_declared_functions()) == set(_lib.EXPORTED)
+    assert _lib.load().ossm_abi_version() == 2
+
+
+def test_dropin_module_has_every_reference_name():
+    from ossm_amd import _kernels
+
+    for name in REFERENCE_NAMES:
+        assert callable(getattr(_kernels, name)), name
+
+
+def test_cpu_tensors_without_delegate_raise_runtime_error():
+    import torch
+
+    from ossm_amd import _kernels
+
+    _kernels.set_cpu_delegate(None)
+    a = torch.ones(3)
+    bu = torch.zeros(4, 2, 3, dtype=torch.complex64)
+    with pytest.raises(RuntimeError, match="CPU tensors"):
+        _kernels.dlinoss_imex1_forward(a, a, a, bu)
+    with pytest.raises(RuntimeError, match="bu must have shape"):
+        _kernels.dlinoss_imex1_forward(a, a, a, bu[0])
+    with pytest.raises(RuntimeError):
+        _kernels.lru_scan(torch.ones(3), torch.ones(3), torch.zeros(4, 2, 3, 2))
+
+
+def test_cpu_delegate_routes_to_the_reference_module():
+    """With the reference's CPU build attached (oracle/_ref, when built), CPU
+    calls return the reference's own results."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from ossm_amd import _kernels
+
+    ref = oracle.reference_module()
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+    _kernels.set_cpu_delegate(ref)
+    try:
+        rng = np.random.default_rng(0)
+        a = torch.tensor(rng.uniform(0.1, 1, 5), dtype=torch.float32)
+        g = torch.tensor(rng.uniform(0, 1, 5), dtype=torch.float32)
+        dt = torch.tensor(rng.uniform(0.1, 0.9, 5), dtype=torch.float32)
+        bu = torch.tensor(rng.normal(size=(7, 2, 5)) + 1j * rng.normal(size=(7, 2, 5)),
+                          dtype=torch.complex64)
+        got = _kernels.dlinoss_im_forward(a, g, dt, bu)
+        assert torch.equal(got, ref.dlinoss_im_forward(a, g, dt, bu))
+    finally:
+        _kernels.set_cpu_delegate(None)
