@@ -25,8 +25,8 @@
 //   parameter gradients are recomputed in registers from the checkpoint
 //   states[t0 - 1] instead of reading the whole trajectory.  Per-lane sums of
 //   <mu_i, s_j,t-1> and <mu_i, bu_t> go to a partials buffer; two small
-//   kernels add them over time chunks (per channel), then over the batch (per
-//   oscillator) and apply each variant's chain rule to (a, g, dt).  Every sum
+//   kernels add them over time chunks and batch rows per oscillator (a
+//   column reduction) and apply each variant's chain rule to (a, g, dt).  Every sum
 //   runs in a fixed order in fp64, so the gradients are deterministic.  (A
 //   last-workgroup-done reduction inside the scan kernel was measured 3x
 //   slower: each agent-scope release fence writes back the XCD's L2.)
@@ -76,10 +76,20 @@ struct Dlinoss {
     int P;
   };
 
-  // dlinoss_imex1.cpp:32-48, dlinoss_imex2.cpp:35-47, dlinoss_im.cpp:34-50, dlinoss_ex.cpp:33-42
-  static __device__ __forceinline__ Coef coef(const Params& prm, int ch) {
+  // The raw per-oscillator parameters (a, g, dt), loaded once per chunk.
+  struct Raw {
+    float a, g, dt;
+  };
+  static __device__ __forceinline__ Raw load_raw(const Params& prm, int ch) {
     const int p = ch % prm.P;
-    const float alpha = prm.a[p], gamma = prm.g[p], sigma = prm.dt[p];
+    return {prm.a[p], prm.g[p], prm.dt[p]};
+  }
+  static __device__ __forceinline__ Coef coef(const Params& prm, int ch) {
+    return coef_of(load_raw(prm, ch));
+  }
+  // dlinoss_imex1.cpp:32-48, dlinoss_imex2.cpp:35-47, dlinoss_im.cpp:34-50, dlinoss_ex.cpp:33-42
+  static __device__ __forceinline__ Coef coef_of(const Raw& r) {
+    const float alpha = r.a, gamma = r.g, sigma = r.dt;
     Coef k;
     if constexpr (V == OSSM_DLINOSS_IMEX1) {
       const float inv = 1.f / (1.f + sigma * gamma);
@@ -236,10 +246,13 @@ struct Linoss {
     int P;
   };
 
-  static __device__ __forceinline__ Coef coef(const Params& prm, int ch) {
+  using Raw = CMat;
+  static __device__ __forceinline__ Raw load_raw(const Params& prm, int ch) {
     const int p = ch % prm.P;
     return {prm.m11[p], prm.m12[p], prm.m21[p], prm.m22[p]};
   }
+  static __device__ __forceinline__ Coef coef_of(const Raw& r) { return r; }
+  static __device__ __forceinline__ Coef coef(const Params& prm, int ch) { return load_raw(prm, ch); }
   static __device__ __forceinline__ float4 step(const Coef& m, float4 s, float4 b) {
     return f4add(mat_apply(m, s), b);
   }
@@ -276,8 +289,8 @@ __device__ __forceinline__ float4 zero_of<float4>() { return f4zero(); }
 // ============================================================================
 // Forward kernel
 // ============================================================================
-template <class Model, int T, int W>
-__global__ __launch_bounds__(W * kWave) void osc_forward_kernel(
+template <class Model, int T, int W, int OCC>
+__global__ __launch_bounds__(W * kWave, OCC) void osc_forward_kernel(
     typename Model::Params prm, const typename Model::In* __restrict__ in,
     float4* __restrict__ out, int L, int nc, int n_groups, int n_chunks,
     unsigned long long* __restrict__ rec, LaunchSync sync) {
@@ -287,7 +300,7 @@ __global__ __launch_bounds__(W * kWave) void osc_forward_kernel(
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
-  const int ticket = draw_ticket(sync, n_groups * n_chunks, &s_ticket);
+  const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
   if (ticket < 0) return;
   const int c = ticket / n_groups;
   const int g = ticket - c * n_groups;
@@ -355,52 +368,106 @@ struct ParamReduce {
   float* partials;  // [n_chunks][NS][nc]
 };
 
-template <class Model, int T, int W>
-__global__ __launch_bounds__(W * kWave) void osc_backward_kernel(
-    typename Model::Params prm, const typename Model::In* __restrict__ in,
-    const float4* __restrict__ states, const typename Model::GIn* __restrict__ gout,
-    typename Model::GOut* __restrict__ gin, ParamReduce red, int L, int nc,
-    int n_groups, int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
-  constexpr int NS = Model::kSums;
-  __shared__ float4 s_agg[W][kWave];
-  __shared__ float4 s_carry[kWave];
-  __shared__ float s_sum[W][NS][kWave];
-  __shared__ int s_ticket;
-
-  const int lane = threadIdx.x & (kWave - 1);
-  const int w = threadIdx.x / kWave;
-  const int ticket = draw_ticket(sync, n_groups * n_chunks, &s_ticket);
-  if (ticket < 0) return;
-  const int cr = ticket / n_groups;          // chunks are handed out last-first
-  const int g = ticket - cr * n_groups;
-  const int c = n_chunks - 1 - cr;
-  const int ch = g * kWave + lane;
-  const bool active = ch < nc;
-  const auto k = Model::coef(prm, active ? ch : 0);
-  const long long t0 = static_cast<long long>(c) * (T * W) + static_cast<long long>(w) * T;
-
-  typename Model::In x[T];
+// One workgroup's inputs for one chunk, loaded ahead of its use.  Loads use
+// clamped in-range addresses and no branches; out-of-range steps are masked
+// where the values are consumed.
+template <class Model, int T>
+struct BwdBuf {
+  typename Model::In x[Model::kRecompute ? T : 1];  // bu_t (recomputing models)
+  float4 sp[Model::kRecompute ? 1 : T];             // s_{t-1} read from states (LinOSS)
   typename Model::GIn go[T];
-  float4 sp[T];  // s_{t-1} for each step of the sub-chunk
+  float4 ck;                                        // states[t0 - 1] (recomputing models)
+  typename Model::Raw raw;                          // the channel's oscillator parameters
+};
+
+struct BwdTicket {
+  int c, g, ch;
+  bool active;
+  long long t0;  // first step of this wave's sub-chunk
+};
+
+template <int T, int W>
+__device__ __forceinline__ BwdTicket bwd_ticket(int ticket, int n_groups, int n_chunks, int nc) {
+  BwdTicket k;
+  const int cr = ticket / n_groups;  // chunks are handed out last-first
+  k.g = ticket - cr * n_groups;
+  k.c = n_chunks - 1 - cr;
+  k.ch = k.g * kWave + (threadIdx.x & (kWave - 1));
+  k.active = k.ch < nc;
+  k.t0 = static_cast<long long>(k.c) * (T * W) + static_cast<long long>(threadIdx.x / kWave) * T;
+  return k;
+}
+
+template <class Model, int T, int W>
+__device__ __forceinline__ void bwd_load(BwdBuf<Model, T>& b, const BwdTicket& k,
+                                         const typename Model::Params& prm,
+                                         const typename Model::In* __restrict__ in,
+                                         const float4* __restrict__ states,
+                                         const typename Model::GIn* __restrict__ gout, int L,
+                                         int nc) {
+  const size_t ch = static_cast<size_t>(k.active ? k.ch : nc - 1);
+  b.raw = Model::load_raw(prm, static_cast<int>(ch));
 #pragma unroll
   for (int i = 0; i < T; ++i) {
-    const long long t = t0 + i;
-    const bool ok = active && t < L;
+    const size_t t = static_cast<size_t>(min(k.t0 + i, static_cast<long long>(L - 1)));
     if constexpr (Model::kRecompute) {
-      x[i] = ok ? in[static_cast<size_t>(t) * nc + ch] : zero_of<typename Model::In>();
+      b.x[i] = in[t * nc + ch];
     } else {
-      x[i] = zero_of<typename Model::In>();
-      sp[i] = (ok && t >= 1) ? states[static_cast<size_t>(t - 1) * nc + ch] : f4zero();
+      const size_t tp = static_cast<size_t>(max(min(k.t0 + i - 1, static_cast<long long>(L - 1)), 0ll));
+      b.sp[i] = states[tp * nc + ch];
     }
-    go[i] = ok ? gout[static_cast<size_t>(t) * nc + ch] : zero_of<typename Model::GIn>();
+    b.go[i] = gout[t * nc + ch];
   }
   if constexpr (Model::kRecompute) {
-    // rebuild s_{t-1} from the checkpoint states[t0 - 1] and the inputs
-    float4 s = (active && t0 >= 1 && t0 <= L) ? states[static_cast<size_t>(t0 - 1) * nc + ch] : f4zero();
+    const size_t tc = static_cast<size_t>(max(min(k.t0 - 1, static_cast<long long>(L - 1)), 0ll));
+    b.ck = states[tc * nc + ch];
+  }
+}
+
+// Processes one chunk: recompute s_{t-1}, reverse aggregate, look-back for
+// the carry from later chunks, final reverse pass (grad_in and the parameter
+// sums), per-chunk partials.  All waves call it together.
+template <class Model, int T, int W, int S>
+__device__ __forceinline__ void bwd_process(
+    BwdBuf<Model, T>& b, const BwdTicket& k,
+    typename Model::GOut* __restrict__ gin, const ParamReduce& red, int L, int nc, int n_chunks,
+    unsigned long long* __restrict__ rec, const LaunchSync& sync, float4 (*s_agg)[kWave],
+    float4* s_carry, float4 (*s_sp)[S][kWave]) {
+  constexpr int NS = Model::kSums;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  const auto cf = Model::coef_of(b.raw);
+  auto valid = [&](int i) { return k.active && k.t0 + i < L; };
+
+  // zero the out-of-range steps in place (the buffer's registers are reused,
+  // not copied); s_{t-1} rebuilt from the checkpoint
+  typename Model::GIn* go = b.go;
+#pragma unroll
+  for (int i = 0; i < T; ++i)
+    if (!valid(i)) go[i] = typename Model::GIn{};
+  // s_{t-1}: recomputed from the checkpoint into LDS (registers are the
+  // occupancy limit of this kernel), or read from the saved trajectory
+  typename Model::In xz[Model::kRecompute ? 1 : T];
+  typename Model::In* x = Model::kRecompute ? b.x : xz;
+  auto sp_at = [&](int i) -> float4 {
+    if constexpr (Model::kRecompute) return s_sp[w][i][lane];
+    else return b.sp[i];
+  };
+  if constexpr (Model::kRecompute) {
+#pragma unroll
+    for (int i = 0; i < T; ++i)
+      if (!valid(i)) x[i] = typename Model::In{};
+    float4 s = (k.active && k.t0 >= 1 && k.t0 <= L) ? b.ck : f4zero();
 #pragma unroll
     for (int i = 0; i < T; ++i) {
-      sp[i] = s;
-      if (t0 + i < L) s = Model::step(k, s, x[i]);
+      s_sp[w][i][lane] = s;
+      if (k.t0 + i < L) s = Model::step(cf, s, x[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      x[i] = typename Model::In{};
+      if (!(valid(i) && k.t0 + i >= 1)) b.sp[i] = f4zero();
     }
   }
 
@@ -408,9 +475,9 @@ __global__ __launch_bounds__(W * kWave) void osc_backward_kernel(
   float4 m = f4zero();
 #pragma unroll
   for (int i = T - 1; i >= 0; --i)
-    if (t0 + i < L) m = Model::rev_carry(k, Model::mu(m, go[i]));
+    if (k.t0 + i < L) m = Model::rev_carry(cf, Model::mu(m, go[i]));
   s_agg[w][lane] = m;
-  const typename Model::Mat KT = mat_pow(mat_adjoint(Model::matrix(k)), T);
+  const typename Model::Mat KT = mat_pow(mat_adjoint(Model::matrix(cf)), T);
   __syncthreads();
 
   // 2. chunk aggregate (waves W-1 .. 0), look-back over later chunks
@@ -419,14 +486,14 @@ __global__ __launch_bounds__(W * kWave) void osc_backward_kernel(
 #pragma unroll
     for (int v = W - 1; v >= 0; --v) E = f4add(mat_apply(KT, E), s_agg[v][lane]);
     float4 carry = f4zero();
-    if (active && n_chunks > 1) {
-      const typename Model::Mat KC = mat_pow(mat_adjoint(Model::matrix(k)), T * W);
-      if (c == n_chunks - 1) {
-        rec_publish(rec, c, kRecInc, nc, ch, E, sync.tag);
+    if (k.active && n_chunks > 1) {
+      const typename Model::Mat KC = mat_pow(mat_adjoint(Model::matrix(cf)), T * W);
+      if (k.c == n_chunks - 1) {
+        rec_publish(rec, k.c, kRecInc, nc, k.ch, E, sync.tag);
       } else {
-        rec_publish(rec, c, kRecAgg, nc, ch, E, sync.tag);
-        carry = lookback(rec, c, -1, n_chunks, nc, ch, KC, sync);
-        if (c > 0) rec_publish(rec, c, kRecInc, nc, ch, f4add(mat_apply(KC, carry), E), sync.tag);
+        rec_publish(rec, k.c, kRecAgg, nc, k.ch, E, sync.tag);
+        carry = lookback(rec, k.c, -1, n_chunks, nc, k.ch, KC, sync);
+        if (k.c > 0) rec_publish(rec, k.c, kRecInc, nc, k.ch, f4add(mat_apply(KC, carry), E), sync.tag);
       }
     }
     s_carry[lane] = carry;
@@ -439,91 +506,119 @@ __global__ __launch_bounds__(W * kWave) void osc_backward_kernel(
   float acc[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) acc[j] = 0.f;
-  if (active) {
+  if (k.active) {
 #pragma unroll
     for (int i = T - 1; i >= 0; --i) {
-      const long long t = t0 + i;
+      const long long t = k.t0 + i;
       if (t < L) {
         const float4 mu = Model::mu(y, go[i]);
-        gin[static_cast<size_t>(t) * nc + ch] = Model::grad_input(k, mu);
-        Model::accumulate(acc, mu, sp[i], x[i]);
-        y = Model::rev_carry(k, mu);
+        gin[static_cast<size_t>(t) * nc + k.ch] = Model::grad_input(cf, mu);
+        Model::accumulate(acc, mu, sp_at(i), x[i]);
+        y = Model::rev_carry(cf, mu);
       }
     }
   }
+  // the per-wave sums go into this wave's own LDS region (its s_{t-1} slots
+  // are no longer read), so no barrier is needed before the writes
+  float* sums = reinterpret_cast<float*>(&s_sp[w][0][0]);
 #pragma unroll
-  for (int j = 0; j < NS; ++j) s_sum[w][j][lane] = acc[j];
+  for (int j = 0; j < NS; ++j) sums[j * kWave + lane] = acc[j];
   __syncthreads();
 
   // 4. this chunk's parameter partial sums (one per channel and sum)
-  if (w == 0 && active) {
+  if (w == 0 && k.active) {
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       float v = 0.f;
-      for (int u = 0; u < W; ++u) v += s_sum[u][j][lane];
-      red.partials[(static_cast<size_t>(c) * NS + j) * nc + ch] = v;
+      for (int u = 0; u < W; ++u) v += reinterpret_cast<const float*>(&s_sp[u][0][0])[j * kWave + lane];
+      red.partials[(static_cast<size_t>(k.c) * NS + j) * nc + k.ch] = v;
     }
   }
+}
+
+// One workgroup per (chunk, channel group), chunks handed out last-first in
+// launch-ticket order (so every chunk a look-back waits on is resident).
+template <class Model, int T, int W, int OCC>
+__global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
+    typename Model::Params prm, const typename Model::In* __restrict__ in,
+    const float4* __restrict__ states, const typename Model::GIn* __restrict__ gout,
+    typename Model::GOut* __restrict__ gin, ParamReduce red, int L, int nc,
+    int n_groups, int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
+  constexpr int NS = Model::kSums;
+  __shared__ float4 s_agg[W][kWave];
+  __shared__ float4 s_carry[kWave];
+  // per wave: its T recomputed states s_{t-1}, later its NS partial sums
+  constexpr int kSlots = (Model::kRecompute ? T : 0) > (NS + 3) / 4 ? T : (NS + 3) / 4;
+  __shared__ float4 s_sp[W][kSlots][kWave];
+  __shared__ int s_ticket;
+  const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
+  if (ticket < 0) return;
+  const BwdTicket k = bwd_ticket<T, W>(ticket, n_groups, n_chunks, nc);
+  BwdBuf<Model, T> b;
+  bwd_load<Model, T, W>(b, k, prm, in, states, gout, L, nc);
+  bwd_process<Model, T, W, kSlots>(b, k, gin, red, L, nc, n_chunks, rec, sync, s_agg, s_carry, s_sp);
 }
 
 // ============================================================================
 // Per-oscillator parameter gradients from the chunk partials
 // ============================================================================
-// Stage 1: chan_tot[j][ch] = sum over time chunks of partials[c][j][ch] (fp64,
-// chunks in order).  One thread per (sum, channel): coalesced over channels.
-template <int NS>
-__global__ __launch_bounds__(256) void osc_reduce_chunks_kernel(const float* __restrict__ partials,
-                                                                double* __restrict__ chan_tot,
-                                                                int nc, int n_chunks) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= static_cast<int64_t>(NS) * nc) return;
-  const int j = static_cast<int>(i / nc), ch = static_cast<int>(i - static_cast<int64_t>(j) * nc);
-  const float* p = partials + static_cast<size_t>(j) * nc + ch;
-  const size_t stride = static_cast<size_t>(NS) * nc;
-  double v = 0.0;
-  int c = 0;
-  for (; c + 8 <= n_chunks; c += 8) {
-    float x[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) x[k] = p[(c + k) * stride];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) v += static_cast<double>(x[k]);
-  }
-  for (; c < n_chunks; ++c) v += static_cast<double>(p[c * stride]);
-  chan_tot[i] = v;
-}
+// The partials form, for each sum j, a matrix of R = n_chunks * B rows
+// (chunk c, batch row b) by P columns (oscillator p): address
+// (c * NS + j) * nc + b * P + p.  Column sums in two passes:
+//   pass 1: block (column tile of 64, row group g) sums rows r = g*4 + w + k*G*4
+//           (w = wave) in fp64, waves combined through LDS -> colsum[g][j][p];
+//   pass 2: per oscillator, adds the G row groups in order, then the chain rule.
+// Fixed order everywhere: deterministic.
+constexpr int kRowGroups = 16;
 
-// Stage 2: per oscillator p, S[j] = sum over the batch of chan_tot[j][b*P+p]
-// (fp64, batch in a fixed split and order), then Model::epilogue.  A block
-// covers 64 oscillators (lanes) with its 4 waves splitting the batch.
-template <class Model>
-__global__ __launch_bounds__(256) void osc_param_kernel(typename Model::Params prm,
-                                                        const double* __restrict__ chan_tot, int P,
-                                                        int B, float* out0, float* out1,
-                                                        float* out2) {
-  constexpr int NS = Model::kSums;
+template <int NS>
+__global__ __launch_bounds__(256) void osc_colsum_kernel(const float* __restrict__ partials,
+                                                         double* __restrict__ colsum, int P,
+                                                         int B, int n_chunks) {
   __shared__ double s_red[4][NS][kWave];
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const int p = blockIdx.x * kWave + lane;
+  const int g = blockIdx.y;
   const size_t nc = static_cast<size_t>(B) * P;
+  const int R = n_chunks * B;
   double acc[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) acc[j] = 0.0;
   if (p < P) {
-    for (int b = w; b < B; b += 4) {
+    for (int r = g * 4 + w; r < R; r += kRowGroups * 4) {
+      const int c = r / B, b = r - c * B;
+      const float* src = partials + static_cast<size_t>(c) * NS * nc + static_cast<size_t>(b) * P + p;
 #pragma unroll
-      for (int j = 0; j < NS; ++j) acc[j] += chan_tot[j * nc + static_cast<size_t>(b) * P + p];
+      for (int j = 0; j < NS; ++j) acc[j] += static_cast<double>(src[j * nc]);
     }
   }
 #pragma unroll
   for (int j = 0; j < NS; ++j) s_red[w][j][lane] = acc[j];
   __syncthreads();
   if (w == 0 && p < P) {
-    double S[NS];
 #pragma unroll
-    for (int j = 0; j < NS; ++j) S[j] = ((s_red[0][j][lane] + s_red[1][j][lane]) + s_red[2][j][lane]) + s_red[3][j][lane];
-    Model::epilogue(prm, p, S, out0, out1, out2);
+    for (int j = 0; j < NS; ++j)
+      colsum[(static_cast<size_t>(g) * NS + j) * P + p] =
+          ((s_red[0][j][lane] + s_red[1][j][lane]) + s_red[2][j][lane]) + s_red[3][j][lane];
   }
+}
+
+template <class Model>
+__global__ __launch_bounds__(256) void osc_param_kernel(typename Model::Params prm,
+                                                        const double* __restrict__ colsum, int P,
+                                                        float* out0, float* out1, float* out2) {
+  constexpr int NS = Model::kSums;
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= P) return;
+  double S[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    double v = 0.0;
+#pragma unroll
+    for (int g = 0; g < kRowGroups; ++g) v += colsum[(static_cast<size_t>(g) * NS + j) * P + p];
+    S[j] = v;
+  }
+  Model::epilogue(prm, p, S, out0, out1, out2);
 }
 
 // Zero-fill used where the reference returns zero gradients (empty scans);
@@ -540,26 +635,28 @@ int fill_zero(float* p, int64_t n, hipStream_t stream) {
   return launch_check("fill_zero_kernel");
 }
 
+// T steps per lane, W waves per workgroup, OCC = minimum waves per SIMD the
+// register allocation must allow (__launch_bounds__' second argument).
 struct Tile {
-  int T, W;
+  int T, W, O;
 };
 
 Tile parse_tile(const char* env, Tile dflt) {
   const char* s = std::getenv(env);
   if (!s) return dflt;
-  int t = 0, w = 0;
-  if (std::sscanf(s, "%dx%d", &t, &w) != 2) return dflt;
-  return {t, w};
+  int t = 0, w = 0, o = 0;
+  if (std::sscanf(s, "%dx%dx%d", &t, &w, &o) != 3) return dflt;
+  return {t, w, o};
 }
 
-// Instantiated tiles (T steps per lane, W waves per workgroup).
-#define OSSM_FWD_TILES(X) X(8, 8) X(16, 4) X(16, 8) X(16, 16) X(32, 8)
-#define OSSM_BWD_TILES(X) X(8, 4) X(8, 8) X(8, 16) X(16, 4) X(16, 8)
+// Instantiated tiles (T, W, OCC).
+#define OSSM_FWD_TILES(X) X(16, 8, 1) X(16, 8, 4) X(8, 8, 4) X(16, 4, 4) X(8, 16, 4) X(32, 4, 2)
+#define OSSM_BWD_TILES(X) X(16, 8, 1) X(16, 4, 1) X(8, 8, 1) X(32, 4, 1) X(8, 16, 1) X(4, 16, 2)
 
 template <class Model>
 int launch_forward(const typename Model::Params& prm, const void* in, void* out, int64_t L,
                    int64_t nc, hipStream_t stream) {
-  static const Tile tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{16, 8});
+  static const Tile tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{16, 8, 1});
   const int64_t CL = int64_t(tile.T) * tile.W;
   const int64_t n_chunks = (L + CL - 1) / CL;
   const int64_t n_groups = (nc + kWave - 1) / kWave;
@@ -571,9 +668,9 @@ int launch_forward(const typename Model::Params& prm, const void* in, void* out,
   if (int rc = acquire_scratch(stream, rec_bytes, n_chunks * n_groups, &payload, &sync)) return rc;
   const dim3 grid(static_cast<unsigned>(n_chunks * n_groups));
   bool launched = false;
-#define OSSM_LAUNCH_FWD(TT, WW)                                                               \
-  if (!launched && tile.T == TT && tile.W == WW) {                                            \
-    hipLaunchKernelGGL((osc_forward_kernel<Model, TT, WW>), grid, dim3(WW * kWave), 0, stream, \
+#define OSSM_LAUNCH_FWD(TT, WW, OO)                                                           \
+  if (!launched && tile.T == TT && tile.W == WW && tile.O == OO) {                            \
+    hipLaunchKernelGGL((osc_forward_kernel<Model, TT, WW, OO>), grid, dim3(WW * kWave), 0, stream, \
                        prm, static_cast<const typename Model::In*>(in),                       \
                        static_cast<float4*>(out), static_cast<int>(L), static_cast<int>(nc),  \
                        static_cast<int>(n_groups), static_cast<int>(n_chunks),                \
@@ -600,7 +697,7 @@ template <class Model>
 int launch_backward(const typename Model::Params& prm, const void* in, const void* states,
                     const void* gout, void* gin, float* out0, float* out1, float* out2, int64_t L,
                     int64_t B, int64_t P, hipStream_t stream) {
-  static const Tile tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{16, 8});
+  static const Tile tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{16, 8, 1});
   constexpr int NS = Model::kSums;
   const int64_t nc = B * P;
   const int64_t CL = int64_t(tile.T) * tile.W;
@@ -611,19 +708,20 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
   const size_t part_bytes =
       (static_cast<size_t>(n_chunks) * NS * nc * sizeof(float) + 255) & ~static_cast<size_t>(255);
-  const size_t tot_bytes = static_cast<size_t>(NS) * nc * sizeof(double);
+  const size_t tot_bytes = static_cast<size_t>(kRowGroups) * NS * P * sizeof(double);
   void* ws = nullptr;
   if (int rc = acquire_workspace(stream, part_bytes + tot_bytes, &ws)) return rc;
+  ParamReduce red{static_cast<float*>(ws)};
+  double* colsum = reinterpret_cast<double*>(static_cast<char*>(ws) + part_bytes);
+  const int64_t total = n_chunks * n_groups;
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(stream, rec_bytes, n_chunks * n_groups, &payload, &sync)) return rc;
-  ParamReduce red{static_cast<float*>(ws)};
-  double* chan_tot = reinterpret_cast<double*>(static_cast<char*>(ws) + part_bytes);
-  const dim3 grid(static_cast<unsigned>(n_chunks * n_groups));
+  if (int rc = acquire_scratch(stream, rec_bytes, total, &payload, &sync)) return rc;
   bool launched = false;
-#define OSSM_LAUNCH_BWD(TT, WW)                                                                  \
-  if (!launched && tile.T == TT && tile.W == WW) {                                               \
-    hipLaunchKernelGGL((osc_backward_kernel<Model, TT, WW>), grid, dim3(WW * kWave), 0, stream,   \
+#define OSSM_LAUNCH_BWD(TT, WW, OO)                                                              \
+  if (!launched && tile.T == TT && tile.W == WW && tile.O == OO) {                               \
+    hipLaunchKernelGGL((osc_backward_kernel<Model, TT, WW, OO>), dim3(static_cast<unsigned>(total)), \
+                       dim3(WW * kWave), 0, stream,                                              \
                        prm, static_cast<const typename Model::In*>(in),                          \
                        static_cast<const float4*>(states),                                       \
                        static_cast<const typename Model::GIn*>(gout),                            \
@@ -631,26 +729,25 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
                        static_cast<int>(nc), static_cast<int>(n_groups),                         \
                        static_cast<int>(n_chunks), static_cast<unsigned long long*>(payload),    \
                        sync);                                                                    \
+    if (int rc = launch_check("osc_backward_kernel")) {                                          \
+      release_unlaunched(stream, total);                                                         \
+      return rc;                                                                                 \
+    }                                                                                            \
     launched = true;                                                                             \
   }
   OSSM_BWD_TILES(OSSM_LAUNCH_BWD)
 #undef OSSM_LAUNCH_BWD
   if (!launched) {
-    release_unlaunched(stream, n_chunks * n_groups);
+    release_unlaunched(stream, total);
     return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_BWD names no built tile");
   }
-  if (int rc = launch_check("osc_backward_kernel")) {
-    release_unlaunched(stream, n_chunks * n_groups);
-    return rc;
-  }
-  const int64_t n_tot = static_cast<int64_t>(NS) * nc;
-  hipLaunchKernelGGL(osc_reduce_chunks_kernel<NS>, dim3(static_cast<unsigned>((n_tot + 255) / 256)),
-                     dim3(256), 0, stream, red.partials, chan_tot, static_cast<int>(nc),
+  hipLaunchKernelGGL(osc_colsum_kernel<NS>,
+                     dim3(static_cast<unsigned>((P + kWave - 1) / kWave), kRowGroups), dim3(256), 0,
+                     stream, red.partials, colsum, static_cast<int>(P), static_cast<int>(B),
                      static_cast<int>(n_chunks));
-  if (int rc = launch_check("osc_reduce_chunks_kernel")) return rc;
-  hipLaunchKernelGGL(osc_param_kernel<Model>, dim3(static_cast<unsigned>((P + kWave - 1) / kWave)),
-                     dim3(256), 0, stream, prm, chan_tot, static_cast<int>(P), static_cast<int>(B),
-                     out0, out1, out2);
+  if (int rc = launch_check("osc_colsum_kernel")) return rc;
+  hipLaunchKernelGGL(osc_param_kernel<Model>, dim3(static_cast<unsigned>((P + 255) / 256)),
+                     dim3(256), 0, stream, prm, colsum, static_cast<int>(P), out0, out1, out2);
   return launch_check("osc_param_kernel");
 }
 

@@ -1,6 +1,7 @@
 // Host runtime of libossm_scan: error strings and scratch management.
 #include "runtime.hpp"
 
+#include <cstdlib>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -49,8 +50,18 @@ int launch_check(const char* what) {
   return hip_check(hipGetLastError(), what);
 }
 
+bool scan_order_by_ticket() {
+  static const bool by_ticket = [] {
+    const char* v = std::getenv("OSSM_SCAN_ORDER");
+    return v == nullptr || std::string(v) != "dispatch";
+  }();
+  return by_ticket;
+}
+
 int acquire_scratch(hipStream_t stream, size_t payload_bytes, uint64_t n_workgroups,
                     void** payload, LaunchSync* sync) {
+  const bool by_ticket = scan_order_by_ticket();
+  if (!by_ticket) n_workgroups = 0;  // no ticket is drawn
   int dev = 0;
   if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
   std::lock_guard<std::mutex> lock(g_mu);
@@ -82,6 +93,7 @@ int acquire_scratch(hipStream_t stream, size_t payload_bytes, uint64_t n_workgro
   sync->err = reinterpret_cast<unsigned int*>(b + kHdrErr);
   sync->base = s.next_ticket;
   sync->tag = s.epoch;
+  sync->use_ticket = by_ticket ? 1 : 0;
   s.next_ticket += n_workgroups;
   *payload = b + kHdrBytes;
   return OSSM_OK;
@@ -111,6 +123,7 @@ int acquire_workspace(hipStream_t stream, size_t bytes, void** ptr) {
 }
 
 void release_unlaunched(hipStream_t stream, uint64_t n_workgroups) {
+  if (!scan_order_by_ticket()) return;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return;
   std::lock_guard<std::mutex> lock(g_mu);

@@ -25,7 +25,12 @@ struct LaunchSync {
   unsigned int* err;           // device error bits
   unsigned long long base;     // value of *ticket when this launch starts
   unsigned int tag;            // epoch tag of this launch's records (never 0)
+  int use_ticket;              // 1: chunks follow the ticket counter, 0: dispatch order
 };
+
+// Whether look-back kernels order their chunks by the ticket counter (the
+// default) or by workgroup index (environment OSSM_SCAN_ORDER=dispatch).
+bool scan_order_by_ticket();
 
 // Records the message for ossm_last_error() and returns `status`.
 int set_error(int status, const std::string& msg);

@@ -202,6 +202,21 @@ __device__ float4 lookback(unsigned long long* rec, int c, int dir, int n_chunks
   return acc;
 }
 
+// The order in which this workgroup's chunk is scheduled.  A chunk only waits
+// on chunks of smaller order, so if the workgroup of the smallest unfinished
+// order is always resident, every look-back ends.
+//
+// Ticket order (default, sync.use_ticket): a global atomic counter drawn at
+// workgroup start guarantees that under any dispatch order, at the price of
+// one serialised atomic per workgroup (~10 us per 2048 workgroups measured
+// on a streaming kernel of the same shape).
+//
+// Dispatch order (OSSM_SCAN_ORDER=dispatch): the workgroup index.  This
+// relies on each XCD dispatching its share of the grid in increasing index
+// order; measured faster for long sequences (config 5 forward 324 vs 346 us)
+// and slower for config 2's forward (86 vs 79 us).
+__device__ __forceinline__ int launch_order(const LaunchSync& sync, int total, int* s_slot);
+
 // Draws this workgroup's ticket (launch order), broadcast through LDS.
 // Returns -1 (and raises kErrBadTicket) when the counter is out of step.
 __device__ __forceinline__ int draw_ticket(const LaunchSync& sync, int total, int* s_slot) {
@@ -217,6 +232,11 @@ __device__ __forceinline__ int draw_ticket(const LaunchSync& sync, int total, in
   }
   __syncthreads();
   return *s_slot;
+}
+
+__device__ __forceinline__ int launch_order(const LaunchSync& sync, int total, int* s_slot) {
+  if (!sync.use_ticket) return static_cast<int>(blockIdx.x);
+  return draw_ticket(sync, total, s_slot);
 }
 
 }  // namespace ossm
