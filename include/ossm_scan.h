@@ -13,6 +13,7 @@
  *               states [L,B,P,2] c64 (component 0 = auxiliary w, 1 = x)
  *   LinOSS:     m11, m12, m21, m22 [P] c64;  b_seq, states [L,B,P,2] c64
  *   selective:  u, dt, gate, out [B,D,L] f32;  A [D,N] f32;  Bm, Cm [B,L,N] f32
+ *               (the _bf16 entries: the same layouts with bf16 except A, dA, chunk_states)
  *
  * Scratch: the library keeps, per (device, stream), one zero-initialised
  * buffer of tagged look-back records (never cleared between calls) and one
@@ -40,7 +41,7 @@ enum {
 
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
-/* Library ABI version (bumped on any signature change; currently 2). */
+/* Library ABI version (bumped on any change of the entry points; currently 3). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -134,6 +135,29 @@ int ossm_selective_backward(const float* grad_out, const float* u, const float* 
                             float* ddt, float* dA, float* dB, float* dC, float* dgate,
                             int64_t batch, int64_t dim, int64_t length, int64_t dstate,
                             ossm_stream_t stream);
+
+/*
+ * bf16 storage variants of the two entries above.  No counterpart in the
+ * reference, whose selective-scan extension is fp32 only
+ * (selective_scan_cuda.cu:253-393); they serve callers that keep activations
+ * in bf16 (the reference's bridge upcasts them to fp32 first,
+ * _selective_scan.py:141-160).  u, dt, gate, out, raw_out, Bm, Cm, grad_out,
+ * du, ddt, dgate, dB, dC are bf16 (pointers as void*); A, dA and chunk_states
+ * stay fp32.  Loads widen exactly to fp32, the recurrence and every sum run in
+ * fp32 (also across the 16-state passes), and each stored value is rounded to
+ * nearest-even once.
+ */
+int ossm_selective_forward_bf16(const void* u, const void* dt, const float* A, const void* Bm,
+                                const void* Cm, const void* gate, void* out, void* raw_out,
+                                float* chunk_states, int64_t batch, int64_t dim, int64_t length,
+                                int64_t dstate, ossm_stream_t stream);
+
+int ossm_selective_backward_bf16(const void* grad_out, const void* u, const void* dt,
+                                 const float* A, const void* Bm, const void* Cm, const void* gate,
+                                 const float* chunk_states, const void* raw_out, void* du,
+                                 void* ddt, float* dA, void* dB, void* dC, void* dgate,
+                                 int64_t batch, int64_t dim, int64_t length, int64_t dstate,
+                                 ossm_stream_t stream);
 
 #ifdef __cplusplus
 }

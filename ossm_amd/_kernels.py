@@ -36,6 +36,7 @@ __all__ = [
     "dlinoss_ex_forward", "dlinoss_ex_backward",
     "selective_scan", "selective_scan_backward",
     "selective_scan_cuda", "selective_scan_cuda_backward",
+    "selective_scan_cuda_bf16", "selective_scan_cuda_bf16_backward",
     "sdlinoss_imex1_forward", "sdlinoss_imex1_backward",
     "sdlinoss_imex2_forward", "sdlinoss_imex2_backward",
     "sdlinoss_im_forward", "sdlinoss_im_backward",
@@ -239,12 +240,16 @@ def linoss_scan_backward(m11, m12, m21, m22, states, grad_output):
 
 
 # ------------------------------------------------------------- selective scan
-def _selective_checks(inputs, dt, A, B, C, gate, name: str) -> None:
-    # selective_scan_cuda.cu:60-102 (CPU twin: selective_scan_cpu.cpp:15-56)
-    _check(inputs.dtype == torch.float32, f"{name} requires float32 inputs")
+def _selective_checks(inputs, dt, A, B, C, gate, name: str,
+                      dtype: torch.dtype = torch.float32) -> None:
+    # selective_scan_cuda.cu:60-102 (CPU twin: selective_scan_cpu.cpp:15-56);
+    # ``dtype`` is the storage type of every tensor but A (float32 for the
+    # reference's names, bfloat16 for the *_bf16 extension)
+    dn = "float32" if dtype == torch.float32 else "bfloat16"
+    _check(inputs.dtype == dtype, f"{name} requires {dn} inputs")
     _check(inputs.dim() == 3, "inputs must have shape (batch, channels, length)")
     _check(dt.device == inputs.device, "dt must be on the same device as inputs")
-    _check(dt.dtype == torch.float32, "dt must be float32")
+    _check(dt.dtype == dtype, f"dt must be {dn}")
     _check(dt.shape == inputs.shape, "dt shape mismatch")
     _check(A.device == inputs.device, "A must be on the same device as inputs")
     _check(A.dtype == torch.float32, "A must be float32")
@@ -254,17 +259,17 @@ def _selective_checks(inputs, dt, A, B, C, gate, name: str) -> None:
     _check(A.size(1) <= _MAX_DSTATE,
            f"state dimension exceeds supported maximum ({_MAX_DSTATE})")
     _check(B.device == inputs.device, "B must be on the same device as inputs")
-    _check(B.dtype == torch.float32, "B must be float32")
+    _check(B.dtype == dtype, f"B must be {dn}")
     _check(B.dim() == 3, "B must have shape (batch, length, state)")
     _check(B.size(0) == inputs.size(0) and B.size(1) == inputs.size(2) and B.size(2) == A.size(1),
            "B shape mismatch")
     _check(C.device == inputs.device, "C must be on the same device as inputs")
-    _check(C.dtype == torch.float32, "C must be float32")
+    _check(C.dtype == dtype, f"C must be {dn}")
     _check(C.dim() == 3, "C must have shape (batch, length, state)")
     _check(C.shape == B.shape, "C shape mismatch")
     if gate is not None:
         _check(gate.device == inputs.device, "gate must be on the same device as inputs")
-        _check(gate.dtype == torch.float32, "gate must be float32")
+        _check(gate.dtype == dtype, f"gate must be {dn}")
         _check(gate.shape == inputs.shape, "gate shape mismatch")
 
 
@@ -276,22 +281,36 @@ def selective_scan_cuda(inputs, dt, A, B, C, gate=None, chunk_length=16):
     """selective_scan_cuda.cu:253-310: returns ``[outputs, chunk_states, raw_outputs]``.
 
     ``chunk_length`` is accepted and ignored, as in the reference (:259)."""
+    return _selective_forward(inputs, dt, A, B, C, gate, torch.float32, "selective_scan_cuda")
+
+
+def selective_scan_cuda_bf16(inputs, dt, A, B, C, gate=None, chunk_length=16):
+    """bfloat16 storage variant of :func:`selective_scan_cuda` (no counterpart in
+    the reference, whose extension is float32 only): inputs, dt, B, C, gate and
+    the outputs are bfloat16, A and chunk_states float32; the scan runs in
+    float32 and each output is rounded once."""
+    return _selective_forward(inputs, dt, A, B, C, gate, torch.bfloat16, "selective_scan_cuda_bf16")
+
+
+def _selective_forward(inputs, dt, A, B, C, gate, dtype, name):
     _check(inputs.is_cuda, "inputs must be CUDA tensor")
-    _selective_checks(inputs, dt, A, B, C, gate, "selective_scan_cuda")
+    _selective_checks(inputs, dt, A, B, C, gate, name, dtype)
     batch, dim, length = inputs.shape
     dstate = A.size(1)
     if length == 0:
         return [torch.zeros_like(inputs),
-                torch.zeros((batch, dim, 0, dstate * 2), dtype=inputs.dtype, device=inputs.device),
+                torch.zeros((batch, dim, 0, dstate * 2), dtype=torch.float32, device=inputs.device),
                 torch.zeros_like(inputs)]
     u, d, a, b, c = (x.contiguous() for x in (inputs, dt, A, B, C))
     z = gate.contiguous() if gate is not None else None
     raw = torch.empty_like(u)
     out = torch.empty_like(u) if z is not None else raw
-    chunks = torch.empty((batch, dim, _num_chunks(length), dstate * 2), dtype=u.dtype,
+    chunks = torch.empty((batch, dim, _num_chunks(length), dstate * 2), dtype=torch.float32,
                          device=u.device)
+    fn = _lib.load().ossm_selective_forward if dtype == torch.float32 else \
+        _lib.load().ossm_selective_forward_bf16
     with torch.cuda.device(u.device):
-        _lib.check(_lib.load().ossm_selective_forward(
+        _lib.check(fn(
             u.data_ptr(), d.data_ptr(), a.data_ptr(), b.data_ptr(), c.data_ptr(), _lib.ptr(z),
             out.data_ptr(), raw.data_ptr(), chunks.data_ptr(), batch, dim, length, dstate,
             _lib.stream_of(u)))
@@ -306,10 +325,27 @@ def selective_scan_cuda_backward(grad_output, inputs, dt, A, B, C, gate=None, ch
     inputs (its rows are this library's state checkpoints).  ``raw_outputs``
     (y before the gate) is read for ``dgate`` when a gate is given; if it is
     missing the forward is re-run to produce it."""
+    return _selective_backward(grad_output, inputs, dt, A, B, C, gate, chunk_states, raw_outputs,
+                               torch.float32, "selective_scan_cuda")
+
+
+def selective_scan_cuda_bf16_backward(grad_output, inputs, dt, A, B, C, gate=None,
+                                      chunk_states=None, raw_outputs=None, chunk_length=None):
+    """bfloat16 storage variant of :func:`selective_scan_cuda_backward`:
+    ``[du, ddt, dA, dB, dC, dgate]`` with dA float32 and the rest bfloat16;
+    ``chunk_states`` (float32) and ``raw_outputs`` come from
+    :func:`selective_scan_cuda_bf16`."""
+    return _selective_backward(grad_output, inputs, dt, A, B, C, gate, chunk_states, raw_outputs,
+                               torch.bfloat16, "selective_scan_cuda_bf16")
+
+
+def _selective_backward(grad_output, inputs, dt, A, B, C, gate, chunk_states, raw_outputs, dtype,
+                        name):
+    dn = "float32" if dtype == torch.float32 else "bfloat16"
     _check(inputs.is_cuda, "inputs must be CUDA tensor")
-    _selective_checks(inputs, dt, A, B, C, gate, "selective_scan_cuda")
+    _selective_checks(inputs, dt, A, B, C, gate, name, dtype)
     _check(grad_output.device == inputs.device, "grad_output must be on the same device as inputs")
-    _check(grad_output.dtype == torch.float32, "grad_output must be float32")
+    _check(grad_output.dtype == dtype, f"grad_output must be {dn}")
     _check(grad_output.shape == inputs.shape, "grad_output shape mismatch")
     _check(chunk_states is not None, "chunk_states must have shape (batch, channels, num_chunks, state * 2)")
     _check(chunk_states.device == inputs.device, "chunk_states must be on the same device as inputs")
@@ -318,7 +354,7 @@ def selective_scan_cuda_backward(grad_output, inputs, dt, A, B, C, gate=None, ch
            "chunk_states must have shape (batch, channels, num_chunks, state * 2)")
     if raw_outputs is not None:
         _check(raw_outputs.device == inputs.device, "raw_outputs must be on the same device as inputs")
-        _check(raw_outputs.dtype == torch.float32, "raw_outputs must be float32")
+        _check(raw_outputs.dtype == dtype, f"raw_outputs must be {dn}")
         _check(raw_outputs.shape == inputs.shape, "raw_outputs shape mismatch")
     batch, dim, length = inputs.shape
     dstate = A.size(1)
@@ -326,7 +362,7 @@ def selective_scan_cuda_backward(grad_output, inputs, dt, A, B, C, gate=None, ch
     z = gate.contiguous() if gate is not None else None
     gout = grad_output.contiguous()
     du, ddt = torch.empty_like(u), torch.empty_like(d)
-    dA = torch.empty_like(a)
+    dA = torch.empty_like(a)  # float32 in both storage types
     dB, dC = torch.empty_like(b), torch.empty_like(c)
     dz = torch.empty_like(u)
     if length == 0:
@@ -337,9 +373,11 @@ def selective_scan_cuda_backward(grad_output, inputs, dt, A, B, C, gate=None, ch
     raw = None
     if z is not None:
         raw = raw_outputs.contiguous() if raw_outputs is not None else \
-            selective_scan_cuda(inputs, dt, A, B, C, gate)[2]
+            _selective_forward(inputs, dt, A, B, C, gate, dtype, name)[2]
+    fn = _lib.load().ossm_selective_backward if dtype == torch.float32 else \
+        _lib.load().ossm_selective_backward_bf16
     with torch.cuda.device(u.device):
-        _lib.check(_lib.load().ossm_selective_backward(
+        _lib.check(fn(
             gout.data_ptr(), u.data_ptr(), d.data_ptr(), a.data_ptr(), b.data_ptr(), c.data_ptr(),
             _lib.ptr(z), cs.data_ptr(), _lib.ptr(raw), du.data_ptr(), ddt.data_ptr(),
             dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), dz.data_ptr(), batch, dim, length,

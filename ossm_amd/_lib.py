@@ -42,6 +42,13 @@ _SIGNATURES = {
         ctypes.c_int,
         [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _c_int64,
          _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_selective_forward_bf16": (
+        ctypes.c_int,
+        [_vp, _vp, _fp, _vp, _vp, _vp, _vp, _vp, _fp, _c_int64, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_selective_backward_bf16": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _fp, _vp, _vp, _vp, _fp, _vp, _vp, _vp, _fp, _vp, _vp, _vp, _c_int64,
+         _c_int64, _c_int64, _c_int64, _vp]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

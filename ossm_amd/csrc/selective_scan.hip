@@ -113,6 +113,53 @@ __device__ __forceinline__ void reduce8(const float (&v)[8], float& o0, float& o
   o1 = row_allreduce(s1 + s3);
 }
 
+// ---- element types -----------------------------------------------------------
+// The row tensors (u, dt, z, out, grads) and B/C are fp32 or bf16 in HBM; the
+// recurrence, its state and every sum run in fp32.  bf16 is stored as its
+// 16 bits; conversions are exact widening and round-to-nearest-even narrowing.
+using bf16_t = uint16_t;
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x40u);  // NaN
+  return static_cast<bf16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+template <class E>
+struct Elem;
+
+template <>
+struct Elem<float> {
+  static __device__ __forceinline__ float4 load4(const float* p) {
+    return *reinterpret_cast<const float4*>(p);
+  }
+  static __device__ __forceinline__ float load1(const float* p) { return *p; }
+  static __device__ __forceinline__ void store4(float* p, float4 v) {
+    *reinterpret_cast<float4*>(p) = v;
+  }
+  static __device__ __forceinline__ void store1(float* p, float v) { *p = v; }
+};
+
+template <>
+struct Elem<bf16_t> {
+  static __device__ __forceinline__ float4 load4(const bf16_t* p) {
+    const uint2 w = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                       __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+  }
+  static __device__ __forceinline__ float load1(const bf16_t* p) { return bf16_to_f32(*p); }
+  static __device__ __forceinline__ void store4(bf16_t* p, float4 v) {
+    uint2 w;
+    w.x = static_cast<uint32_t>(f32_to_bf16(v.x)) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16);
+    w.y = static_cast<uint32_t>(f32_to_bf16(v.z)) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16);
+    *reinterpret_cast<uint2*>(p) = w;
+  }
+  static __device__ __forceinline__ void store1(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+};
+
 // ---- tile staging -----------------------------------------------------------
 // Every launch runs kThreads threads.  A tile of a [.., L] tensor is 64 rows
 // (channels d0..d0+63) x TT steps; thread i owns the float4 column groups
@@ -141,8 +188,8 @@ __device__ __forceinline__ void tile_pos(int k, int& row, int& c) {
 // address, so the loads carry no branches and all stay in flight together;
 // they are zeroed when the tile is written to LDS (store_rows), not here, so
 // that nothing waits on the loads before then.
-template <int TT, bool VEC>
-__device__ __forceinline__ void load_rows(RowRegs<TT>& r, const float* __restrict__ g,
+template <int TT, bool VEC, class E>
+__device__ __forceinline__ void load_rows(RowRegs<TT>& r, const E* __restrict__ g,
                                           size_t row0, int d0, int D, int t0, int L) {
 #pragma unroll
   for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
@@ -151,12 +198,12 @@ __device__ __forceinline__ void load_rows(RowRegs<TT>& r, const float* __restric
     const int t = t0 + c;
     const size_t base = row0 + static_cast<size_t>(min(d0 + row, D - 1)) * L;
     if constexpr (VEC) {
-      r.v[k] = *reinterpret_cast<const float4*>(g + base + min(t, L - 4));
+      r.v[k] = Elem<E>::load4(g + base + min(t, L - 4));
     } else {
-      r.v[k].x = g[base + min(t, L - 1)];
-      r.v[k].y = g[base + min(t + 1, L - 1)];
-      r.v[k].z = g[base + min(t + 2, L - 1)];
-      r.v[k].w = g[base + min(t + 3, L - 1)];
+      r.v[k].x = Elem<E>::load1(g + base + min(t, L - 1));
+      r.v[k].y = Elem<E>::load1(g + base + min(t + 1, L - 1));
+      r.v[k].z = Elem<E>::load1(g + base + min(t + 2, L - 1));
+      r.v[k].w = Elem<E>::load1(g + base + min(t + 3, L - 1));
     }
   }
 }
@@ -196,16 +243,16 @@ __device__ __forceinline__ void store_rows(float* __restrict__ s, const RowRegs<
 }
 
 // Stores 4 consecutive steps of one row of a [.., L] tensor.
-template <bool VEC>
-__device__ __forceinline__ void store_row4(float* __restrict__ g, size_t off, int t, int L,
+template <bool VEC, class E>
+__device__ __forceinline__ void store_row4(E* __restrict__ g, size_t off, int t, int L,
                                            float4 v) {
   if constexpr (VEC) {
-    *reinterpret_cast<float4*>(g + off) = v;
+    Elem<E>::store4(g + off, v);
   } else {
-    g[off] = v.x;
-    if (t + 1 < L) g[off + 1] = v.y;
-    if (t + 2 < L) g[off + 2] = v.z;
-    if (t + 3 < L) g[off + 3] = v.w;
+    Elem<E>::store1(g + off, v.x);
+    if (t + 1 < L) Elem<E>::store1(g + off + 1, v.y);
+    if (t + 2 < L) Elem<E>::store1(g + off + 2, v.z);
+    if (t + 3 < L) Elem<E>::store1(g + off + 3, v.w);
   }
 }
 
@@ -217,14 +264,15 @@ struct StateRegs {
   float v[kQ];
 };
 
-template <int TT>
-__device__ __forceinline__ void load_states(StateRegs<TT>& r, const float* __restrict__ g,
+template <int TT, class E>
+__device__ __forceinline__ void load_states(StateRegs<TT>& r, const E* __restrict__ g,
                                             size_t base, int t0, int L, int N, int n_base) {
 #pragma unroll
   for (int k = 0; k < StateRegs<TT>::kQ; ++k) {
     const int e = threadIdx.x + k * kThreads;
     const int t = e / kPassStates, j = e - t * kPassStates;
-    r.v[k] = g[base + static_cast<size_t>(min(t0 + t, L - 1)) * N + min(n_base + j, N - 1)];
+    r.v[k] = Elem<E>::load1(g + base + static_cast<size_t>(min(t0 + t, L - 1)) * N +
+                            min(n_base + j, N - 1));
   }
 }
 
@@ -240,15 +288,17 @@ __device__ __forceinline__ void store_states(float* __restrict__ s, const StateR
 }
 
 // ---- forward ------------------------------------------------------------------
+template <class E>
 struct FwdArgs {
-  const float* u;
-  const float* dt;
+  const E* u;
+  const E* dt;
   const float* A;
-  const float* Bm;
-  const float* Cm;
-  const float* z;    // may be null
-  float* out;
-  float* acc;        // y accumulator across passes (raw_out, or out when raw_out is null)
+  const E* Bm;
+  const E* Cm;
+  const E* z;        // may be null
+  E* out;
+  E* raw;            // y before the gate, written by the last pass; may be null
+  float* acc;        // fp32 y summed over the passes before the last; null for one pass
   float* ckpt;       // chunk_states, may be null
   int D, L, N, n_base, n_chunks;
   int first, last, vec;
@@ -268,9 +318,9 @@ struct FwdTile {
   StateRegs<kFwdTile> B, C;
 };
 
-template <bool VEC, bool GATED>
-__device__ __forceinline__ void fwd_prefetch(FwdTile& f, const FwdArgs& a, size_t row0, size_t bc0,
-                                             int d0, int t0) {
+template <class E, bool VEC, bool GATED>
+__device__ __forceinline__ void fwd_prefetch(FwdTile& f, const FwdArgs<E>& a, size_t row0,
+                                             size_t bc0, int d0, int t0) {
   load_rows<kFwdTile, VEC>(f.u, a.u, row0, d0, a.D, t0, a.L);
   load_rows<kFwdTile, VEC>(f.dt, a.dt, row0, d0, a.D, t0, a.L);
   if constexpr (GATED) load_rows<kFwdTile, VEC>(f.z, a.z, row0, d0, a.D, t0, a.L);
@@ -280,8 +330,8 @@ __device__ __forceinline__ void fwd_prefetch(FwdTile& f, const FwdArgs& a, size_
 
 // GATED kernels multiply by silu(z) in the last pass; VEC: L % 4 == 0 and
 // u/dt/z/out rows 16-byte aligned.
-template <bool VEC, bool GATED>
-__global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs a) {
+template <class E, bool VEC, bool GATED>
+__global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   constexpr int TT = kFwdTile;
   constexpr int RS = TT + 1;  // odd row stride: lane-per-row accesses hit distinct banks
   __shared__ float s_u[kWave * RS];
@@ -312,7 +362,7 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs a) {
   const int n_slots = (a.L + kCkpt - 1) / kCkpt;
 
   FwdTile nxt;
-  fwd_prefetch<VEC, GATED>(nxt, a, row0, bc0, d0, 0);
+  fwd_prefetch<E, VEC, GATED>(nxt, a, row0, bc0, d0, 0);
   for (int t0 = 0; t0 < a.L; t0 += TT) {
     __syncthreads();  // the previous tile's LDS readers are done
     store_rows<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
@@ -321,7 +371,7 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs a) {
     store_states<TT>(s_C, nxt.C, t0, a.L, a.N, a.n_base);
     const RowRegs<TT> zt = nxt.z;
     __syncthreads();
-    if (t0 + TT < a.L) fwd_prefetch<VEC, GATED>(nxt, a, row0, bc0, d0, t0 + TT);
+    if (t0 + TT < a.L) fwd_prefetch<E, VEC, GATED>(nxt, a, row0, bc0, d0, t0 + TT);
 
     const int nsteps = min(TT, a.L - t0);
     if (wave_active) {
@@ -390,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs a) {
         if (t + 3 < a.L) y.w += a.acc[gi + 3];
       }
       if (a.last) {
-        if (a.acc != a.out) store_row4<VEC>(a.acc, gi, t, a.L, y);
+        if (a.raw != nullptr) store_row4<VEC>(a.raw, gi, t, a.L, y);
         float4 o = y;
         if constexpr (GATED) {
           const float4 zz = zt.v[k];
@@ -408,24 +458,27 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs a) {
 }
 
 // ---- backward -----------------------------------------------------------------
+template <class E>
 struct BwdArgs {
-  const float* gout;
-  const float* u;
-  const float* dt;
+  const E* gout;
+  const E* u;
+  const E* dt;
   const float* A;
-  const float* Bm;
-  const float* Cm;
-  const float* z;      // may be null
-  const float* raw;    // y from the forward; needed when z is given
+  const E* Bm;
+  const E* Cm;
+  const E* z;          // may be null
+  const E* raw;        // y from the forward; needed when z is given
   const float* ckpt;
-  float* du;
-  float* ddt;
-  float* dz;           // written by the first pass when z is given
+  E* du;               // written by the last pass
+  E* ddt;
+  E* dz;               // written by the first pass when z is given
+  float* du_acc;       // fp32 du / ddt summed over the passes before the last
+  float* ddt_acc;
   float* part_dB;      // [n_dtiles, B, L, N]
   float* part_dC;
   float* part_dA;      // [B, D, N]
   int Bsz, D, L, N, n_base, n_chunks;
-  int first, vec;
+  int first, last, vec;
 };
 
 struct BwdTile {
@@ -434,8 +487,8 @@ struct BwdTile {
   float h0[kNpw];  // state after the step before the tile (this lane, this wave's states), unmasked
 };
 
-template <bool VEC, bool GATED>
-__device__ __forceinline__ void bwd_prefetch(BwdTile& f, const BwdArgs& a, size_t row0, size_t bc0,
+template <class E, bool VEC, bool GATED>
+__device__ __forceinline__ void bwd_prefetch(BwdTile& f, const BwdArgs<E>& a, size_t row0, size_t bc0,
                                              size_t ck_row, int d0, bool dvalid, int n0, int tile) {
   const int t0 = tile * kBwdTile;
   load_rows<kBwdTile, VEC>(f.u, a.u, row0, d0, a.D, t0, a.L);
@@ -456,8 +509,8 @@ __device__ __forceinline__ void bwd_prefetch(BwdTile& f, const BwdArgs& a, size_
   }
 }
 
-template <bool VEC, bool GATED>
-__global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs a) {
+template <class E, bool VEC, bool GATED>
+__global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   constexpr int TT = kBwdTile;
   constexpr int RS = TT + 1;
   __shared__ float s_u[kWave * RS];
@@ -493,7 +546,7 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs a) {
   const int n_tiles = (a.L + TT - 1) / TT;
 
   BwdTile nxt;
-  bwd_prefetch<VEC, GATED>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, n_tiles - 1);
+  bwd_prefetch<E, VEC, GATED>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, n_tiles - 1);
   for (int tile = n_tiles - 1; tile >= 0; --tile) {
     const int t0 = tile * TT;
     const int nsteps = min(TT, a.L - t0);
@@ -533,7 +586,7 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs a) {
 #pragma unroll
     for (int j = 0; j < kNpw; ++j) h0[j] = (tile > 0 && dvalid && n0 + j < a.N) ? nxt.h0[j] : 0.f;
     __syncthreads();
-    if (tile > 0) bwd_prefetch<VEC, GATED>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile - 1);
+    if (tile > 0) bwd_prefetch<E, VEC, GATED>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile - 1);
 
     if (wave_active) {
       // FULL: all TT steps exist (every tile but possibly the last in time)
@@ -648,14 +701,19 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs a) {
       }
       const size_t gi = row0 + static_cast<size_t>(dd) * a.L + t;
       if (!a.first) {
-        su.x += a.du[gi];
-        sd.x += a.ddt[gi];
-        if (t + 1 < a.L) { su.y += a.du[gi + 1]; sd.y += a.ddt[gi + 1]; }
-        if (t + 2 < a.L) { su.z += a.du[gi + 2]; sd.z += a.ddt[gi + 2]; }
-        if (t + 3 < a.L) { su.w += a.du[gi + 3]; sd.w += a.ddt[gi + 3]; }
+        su.x += a.du_acc[gi];
+        sd.x += a.ddt_acc[gi];
+        if (t + 1 < a.L) { su.y += a.du_acc[gi + 1]; sd.y += a.ddt_acc[gi + 1]; }
+        if (t + 2 < a.L) { su.z += a.du_acc[gi + 2]; sd.z += a.ddt_acc[gi + 2]; }
+        if (t + 3 < a.L) { su.w += a.du_acc[gi + 3]; sd.w += a.ddt_acc[gi + 3]; }
       }
-      store_row4<VEC>(a.du, gi, t, a.L, su);
-      store_row4<VEC>(a.ddt, gi, t, a.L, sd);
+      if (a.last) {
+        store_row4<VEC>(a.du, gi, t, a.L, su);
+        store_row4<VEC>(a.ddt, gi, t, a.L, sd);
+      } else {
+        store_row4<VEC>(a.du_acc, gi, t, a.L, su);
+        store_row4<VEC>(a.ddt_acc, gi, t, a.L, sd);
+      }
     }
   }
 
@@ -668,10 +726,11 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs a) {
 
 // Adds the per-tile partials in a fixed order: dB, dC over channel tiles,
 // dA over batch rows.
+template <class E>
 __global__ void selective_finish_kernel(const float* __restrict__ part_dB,
                                         const float* __restrict__ part_dC,
-                                        const float* __restrict__ part_dA, float* __restrict__ dB,
-                                        float* __restrict__ dC, float* __restrict__ dA,
+                                        const float* __restrict__ part_dA, E* __restrict__ dB,
+                                        E* __restrict__ dC, float* __restrict__ dA,
                                         int64_t n_bln, int n_dtiles, int64_t n_dn, int Bsz) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n_bln) {
@@ -680,8 +739,8 @@ __global__ void selective_finish_kernel(const float* __restrict__ part_dB,
       sb += part_dB[static_cast<size_t>(k) * n_bln + i];
       sc += part_dC[static_cast<size_t>(k) * n_bln + i];
     }
-    dB[i] = sb;
-    dC[i] = sc;
+    Elem<E>::store1(dB + i, sb);
+    Elem<E>::store1(dC + i, sc);
   }
   if (i < n_dn) {
     float s = 0.f;
@@ -690,9 +749,10 @@ __global__ void selective_finish_kernel(const float* __restrict__ part_dB,
   }
 }
 
-__global__ void selective_zero_kernel(float* __restrict__ p, int64_t n) {
+template <class E>
+__global__ void selective_zero_kernel(E* __restrict__ p, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0.f;
+  if (i < n) Elem<E>::store1(p + i, 0.f);
 }
 
 int check_selective(int64_t Bsz, int64_t D, int64_t L, int64_t N, const char* what) {
@@ -708,13 +768,162 @@ int check_selective(int64_t Bsz, int64_t D, int64_t L, int64_t N, const char* wh
 
 int64_t num_chunks(int64_t L) { return L <= 0 ? 0 : (L + kChunk - 1) / kChunk; }
 
-// Rows of [.., L] tensors can move as float4 when L % 4 == 0 and every row
-// tensor starts 16-byte aligned (null pointers are not used and pass).
-bool rows_vectorizable(int64_t L, std::initializer_list<const float*> ptrs) {
+// Rows of [.., L] tensors move four elements at a time when L % 4 == 0 and
+// every row tensor starts aligned to four elements (null pointers pass).
+bool rows_vectorizable(int64_t L, size_t elem_bytes, std::initializer_list<const void*> ptrs) {
   if (L % 4 != 0) return false;
-  for (const float* p : ptrs)
-    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) % (4 * elem_bytes) != 0) return false;
   return true;
+}
+
+template <class E>
+int zero_fill(E* p, int64_t n, hipStream_t stream) {
+  if (p == nullptr || n <= 0) return OSSM_OK;
+  hipLaunchKernelGGL(selective_zero_kernel<E>, dim3(static_cast<unsigned>((n + 255) / 256)),
+                     dim3(256), 0, stream, p, n);
+  return launch_check("selective_zero_kernel");
+}
+
+// E = float: the fp32 API of the reference.  E = bf16_t: the same scan with
+// bf16 rows, B and C in HBM (A, chunk_states and dA stay fp32).
+template <class E>
+int selective_forward_impl(const E* u, const E* dt, const float* A, const E* Bm, const E* Cm,
+                           const E* gate, E* out, E* raw_out, float* chunk_states, int64_t batch,
+                           int64_t dim, int64_t length, int64_t dstate, hipStream_t stream,
+                           const char* what) {
+  clear_error();
+  if (int rc = check_selective(batch, dim, length, dstate, what)) return rc;
+  if (batch == 0 || dim == 0 || length == 0) return OSSM_OK;
+  if (!u || !dt || !A || !Bm || !Cm || !out)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": null pointer");
+  const int n_pass = static_cast<int>((dstate + kPassStates - 1) / kPassStates);
+  FwdArgs<E> a{};
+  a.u = u;
+  a.dt = dt;
+  a.A = A;
+  a.Bm = Bm;
+  a.Cm = Cm;
+  a.z = gate;
+  a.out = out;
+  a.raw = raw_out;
+  a.acc = nullptr;
+  if (n_pass > 1) {
+    if constexpr (std::is_same_v<E, float>) {
+      a.acc = raw_out != nullptr ? raw_out : out;  // summed in place, then overwritten
+    } else {
+      void* ws = nullptr;
+      if (int rc = acquire_workspace(stream, static_cast<size_t>(batch * dim * length) * sizeof(float), &ws))
+        return rc;
+      a.acc = static_cast<float*>(ws);
+    }
+  }
+  a.ckpt = chunk_states;
+  a.D = static_cast<int>(dim);
+  a.L = static_cast<int>(length);
+  a.N = static_cast<int>(dstate);
+  a.n_chunks = static_cast<int>(num_chunks(length));
+  a.vec = rows_vectorizable(length, sizeof(E), {u, dt, gate, out, raw_out}) ? 1 : 0;
+  const dim3 grid(static_cast<unsigned>((dim + kWave - 1) / kWave), static_cast<unsigned>(batch));
+  for (int p = 0; p < n_pass; ++p) {
+    a.n_base = p * kPassStates;
+    a.first = p == 0;
+    a.last = p == n_pass - 1;
+    auto kern = a.vec ? (gate ? selective_fwd_kernel<E, true, true> : selective_fwd_kernel<E, true, false>)
+                      : (gate ? selective_fwd_kernel<E, false, true> : selective_fwd_kernel<E, false, false>);
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, a);
+    if (int rc = launch_check("selective_fwd_kernel")) return rc;
+  }
+  return OSSM_OK;
+}
+
+template <class E>
+int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const float* A,
+                            const E* Bm, const E* Cm, const E* gate, const float* chunk_states,
+                            const E* raw_out, E* du, E* ddt, float* dA, E* dB, E* dC, E* dgate,
+                            int64_t batch, int64_t dim, int64_t length, int64_t dstate,
+                            hipStream_t stream, const char* what) {
+  clear_error();
+  if (int rc = check_selective(batch, dim, length, dstate, what)) return rc;
+  if (batch == 0 || dim == 0 || length == 0) {
+    // nothing to scan: every gradient is zero (dA still has D*N entries)
+    if (int rc = zero_fill(dA, dim * dstate, stream)) return rc;
+    if (int rc = zero_fill(dB, batch * length * dstate, stream)) return rc;
+    if (int rc = zero_fill(dC, batch * length * dstate, stream)) return rc;
+    return OSSM_OK;
+  }
+  if (!grad_out || !u || !dt || !A || !Bm || !Cm || !chunk_states || !du || !ddt || !dA || !dB ||
+      !dC)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": null pointer");
+  if (gate != nullptr && (raw_out == nullptr || dgate == nullptr))
+    return set_error(OSSM_ERR_INVALID_ARGUMENT,
+                     std::string(what) + ": a gated scan needs raw_outputs and dgate");
+  const int n_pass = static_cast<int>((dstate + kPassStates - 1) / kPassStates);
+  const int64_t n_dtiles = (dim + kWave - 1) / kWave;
+  const int64_t n_bln = batch * length * dstate;
+  const int64_t n_dn = dim * dstate;
+  const int64_t n_rows = batch * dim * length;
+  const bool staged = !std::is_same_v<E, float> && n_pass > 1;  // fp32 du/ddt between passes
+  const size_t part_floats =
+      static_cast<size_t>(2 * n_dtiles * n_bln + batch * n_dn) + (staged ? 2 * n_rows : 0);
+  void* ws = nullptr;
+  if (int rc = acquire_workspace(stream, part_floats * sizeof(float), &ws)) return rc;
+  float* part_dB = static_cast<float*>(ws);
+  float* part_dC = part_dB + n_dtiles * n_bln;
+  float* part_dA = part_dC + n_dtiles * n_bln;
+
+  BwdArgs<E> a{};
+  a.gout = grad_out;
+  a.u = u;
+  a.dt = dt;
+  a.A = A;
+  a.Bm = Bm;
+  a.Cm = Cm;
+  a.z = gate;
+  a.raw = raw_out;
+  a.ckpt = chunk_states;
+  a.du = du;
+  a.ddt = ddt;
+  a.dz = dgate;
+  if constexpr (std::is_same_v<E, float>) {
+    a.du_acc = du;  // summed in place
+    a.ddt_acc = ddt;
+  } else {
+    a.du_acc = staged ? part_dA + batch * n_dn : nullptr;
+    a.ddt_acc = staged ? a.du_acc + n_rows : nullptr;
+  }
+  a.part_dB = part_dB;
+  a.part_dC = part_dC;
+  a.part_dA = part_dA;
+  a.Bsz = static_cast<int>(batch);
+  a.D = static_cast<int>(dim);
+  a.L = static_cast<int>(length);
+  a.N = static_cast<int>(dstate);
+  a.n_chunks = static_cast<int>(num_chunks(length));
+  // the staged fp32 sums sit at a 16-byte multiple only when n_bln and B*D*N are
+  // multiples of 4; otherwise the rows go element by element
+  const bool staged_aligned = !staged || (n_bln % 4 == 0 && (batch * n_dn) % 4 == 0);
+  a.vec = staged_aligned &&
+                  rows_vectorizable(length, sizeof(E), {grad_out, u, dt, gate, raw_out, du, ddt, dgate})
+              ? 1
+              : 0;
+  const dim3 grid(static_cast<unsigned>(n_dtiles), static_cast<unsigned>(batch));
+  for (int p = 0; p < n_pass; ++p) {
+    a.n_base = p * kPassStates;
+    a.first = p == 0;
+    a.last = p == n_pass - 1;
+    auto kern = a.vec ? (gate ? selective_bwd_kernel<E, true, true> : selective_bwd_kernel<E, true, false>)
+                      : (gate ? selective_bwd_kernel<E, false, true> : selective_bwd_kernel<E, false, false>);
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, a);
+    if (int rc = launch_check("selective_bwd_kernel")) return rc;
+  }
+  const int64_t n_fin = n_bln > n_dn ? n_bln : n_dn;
+  hipLaunchKernelGGL(selective_finish_kernel<E>, dim3(static_cast<unsigned>((n_fin + 255) / 256)),
+                     dim3(256), 0, stream, part_dB, part_dC, part_dA, dB, dC, dA, n_bln,
+                     static_cast<int>(n_dtiles), n_dn, static_cast<int>(batch));
+  if (int rc = launch_check("selective_finish_kernel")) return rc;
+  if (gate == nullptr && dgate != nullptr) return zero_fill(dgate, n_rows, stream);
+  return OSSM_OK;
 }
 
 }  // namespace
@@ -729,118 +938,47 @@ int64_t ossm_selective_num_chunks(int64_t length) { return ossm::num_chunks(leng
 int ossm_selective_forward(const float* u, const float* dt, const float* A, const float* Bm,
                            const float* Cm, const float* gate, float* out, float* raw_out,
                            float* chunk_states, int64_t batch, int64_t dim, int64_t length,
-                           int64_t dstate, ossm_stream_t stream_v) {
-  clear_error();
-  if (int rc = check_selective(batch, dim, length, dstate, "selective_forward")) return rc;
-  if (batch == 0 || dim == 0 || length == 0) return OSSM_OK;
-  if (!u || !dt || !A || !Bm || !Cm || !out)
-    return set_error(OSSM_ERR_INVALID_ARGUMENT, "selective_forward: null pointer");
-  hipStream_t stream = static_cast<hipStream_t>(stream_v);
-  FwdArgs a{};
-  a.u = u;
-  a.dt = dt;
-  a.A = A;
-  a.Bm = Bm;
-  a.Cm = Cm;
-  a.z = gate;
-  a.out = out;
-  a.acc = raw_out != nullptr ? raw_out : out;
-  a.ckpt = chunk_states;
-  a.D = static_cast<int>(dim);
-  a.L = static_cast<int>(length);
-  a.N = static_cast<int>(dstate);
-  a.n_chunks = static_cast<int>(num_chunks(length));
-  a.vec = rows_vectorizable(length, {u, dt, gate, out, raw_out}) ? 1 : 0;
-  const dim3 grid(static_cast<unsigned>((dim + kWave - 1) / kWave), static_cast<unsigned>(batch));
-  const int n_pass = static_cast<int>((dstate + kPassStates - 1) / kPassStates);
-  for (int p = 0; p < n_pass; ++p) {
-    a.n_base = p * kPassStates;
-    a.first = p == 0;
-    a.last = p == n_pass - 1;
-    auto kern = a.vec ? (gate ? selective_fwd_kernel<true, true> : selective_fwd_kernel<true, false>)
-                      : (gate ? selective_fwd_kernel<false, true> : selective_fwd_kernel<false, false>);
-    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, a);
-    if (int rc = launch_check("selective_fwd_kernel")) return rc;
-  }
-  return OSSM_OK;
+                           int64_t dstate, ossm_stream_t stream) {
+  return selective_forward_impl<float>(u, dt, A, Bm, Cm, gate, out, raw_out, chunk_states, batch,
+                                       dim, length, dstate, static_cast<hipStream_t>(stream),
+                                       "selective_forward");
 }
 
 int ossm_selective_backward(const float* grad_out, const float* u, const float* dt, const float* A,
                             const float* Bm, const float* Cm, const float* gate,
                             const float* chunk_states, const float* raw_out, float* du, float* ddt,
                             float* dA, float* dB, float* dC, float* dgate, int64_t batch,
-                            int64_t dim, int64_t length, int64_t dstate, ossm_stream_t stream_v) {
-  clear_error();
-  if (int rc = check_selective(batch, dim, length, dstate, "selective_backward")) return rc;
-  hipStream_t stream = static_cast<hipStream_t>(stream_v);
-  auto zero = [&](float* p, int64_t n) -> int {
-    if (p == nullptr || n <= 0) return OSSM_OK;
-    hipLaunchKernelGGL(selective_zero_kernel, dim3(static_cast<unsigned>((n + 255) / 256)),
-                       dim3(256), 0, stream, p, n);
-    return launch_check("selective_zero_kernel");
-  };
-  if (batch == 0 || dim == 0 || length == 0) {
-    // nothing to scan: every gradient is zero (dA still has D*N entries)
-    if (int rc = zero(dA, dim * dstate)) return rc;
-    if (int rc = zero(dB, batch * length * dstate)) return rc;
-    if (int rc = zero(dC, batch * length * dstate)) return rc;
-    return OSSM_OK;
-  }
-  if (!grad_out || !u || !dt || !A || !Bm || !Cm || !chunk_states || !du || !ddt || !dA || !dB ||
-      !dC)
-    return set_error(OSSM_ERR_INVALID_ARGUMENT, "selective_backward: null pointer");
-  if (gate != nullptr && (raw_out == nullptr || dgate == nullptr))
-    return set_error(OSSM_ERR_INVALID_ARGUMENT,
-                     "selective_backward: a gated scan needs raw_outputs and dgate");
-  const int64_t n_dtiles = (dim + kWave - 1) / kWave;
-  const int64_t n_bln = batch * length * dstate;
-  const int64_t n_dn = dim * dstate;
-  const size_t part_bytes = (static_cast<size_t>(2 * n_dtiles * n_bln) + batch * n_dn) * sizeof(float);
-  void* ws = nullptr;
-  if (int rc = acquire_workspace(stream, part_bytes, &ws)) return rc;
-  float* part_dB = static_cast<float*>(ws);
-  float* part_dC = part_dB + n_dtiles * n_bln;
-  float* part_dA = part_dC + n_dtiles * n_bln;
+                            int64_t dim, int64_t length, int64_t dstate, ossm_stream_t stream) {
+  return selective_backward_impl<float>(grad_out, u, dt, A, Bm, Cm, gate, chunk_states, raw_out, du,
+                                        ddt, dA, dB, dC, dgate, batch, dim, length, dstate,
+                                        static_cast<hipStream_t>(stream), "selective_backward");
+}
 
-  BwdArgs a{};
-  a.gout = grad_out;
-  a.u = u;
-  a.dt = dt;
-  a.A = A;
-  a.Bm = Bm;
-  a.Cm = Cm;
-  a.z = gate;
-  a.raw = raw_out;
-  a.ckpt = chunk_states;
-  a.du = du;
-  a.ddt = ddt;
-  a.dz = dgate;
-  a.part_dB = part_dB;
-  a.part_dC = part_dC;
-  a.part_dA = part_dA;
-  a.Bsz = static_cast<int>(batch);
-  a.D = static_cast<int>(dim);
-  a.L = static_cast<int>(length);
-  a.N = static_cast<int>(dstate);
-  a.n_chunks = static_cast<int>(num_chunks(length));
-  a.vec = rows_vectorizable(length, {grad_out, u, dt, gate, raw_out, du, ddt, dgate}) ? 1 : 0;
-  const dim3 grid(static_cast<unsigned>(n_dtiles), static_cast<unsigned>(batch));
-  const int n_pass = static_cast<int>((dstate + kPassStates - 1) / kPassStates);
-  for (int p = 0; p < n_pass; ++p) {
-    a.n_base = p * kPassStates;
-    a.first = p == 0;
-    auto kern = a.vec ? (gate ? selective_bwd_kernel<true, true> : selective_bwd_kernel<true, false>)
-                      : (gate ? selective_bwd_kernel<false, true> : selective_bwd_kernel<false, false>);
-    hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, a);
-    if (int rc = launch_check("selective_bwd_kernel")) return rc;
-  }
-  const int64_t n_fin = n_bln > n_dn ? n_bln : n_dn;
-  hipLaunchKernelGGL(selective_finish_kernel, dim3(static_cast<unsigned>((n_fin + 255) / 256)),
-                     dim3(256), 0, stream, part_dB, part_dC, part_dA, dB, dC, dA, n_bln,
-                     static_cast<int>(n_dtiles), n_dn, static_cast<int>(batch));
-  if (int rc = launch_check("selective_finish_kernel")) return rc;
-  if (gate == nullptr && dgate != nullptr) return zero(dgate, batch * dim * length);
-  return OSSM_OK;
+int ossm_selective_forward_bf16(const void* u, const void* dt, const float* A, const void* Bm,
+                                const void* Cm, const void* gate, void* out, void* raw_out,
+                                float* chunk_states, int64_t batch, int64_t dim, int64_t length,
+                                int64_t dstate, ossm_stream_t stream) {
+  using E = bf16_t;
+  return selective_forward_impl<E>(
+      static_cast<const E*>(u), static_cast<const E*>(dt), A, static_cast<const E*>(Bm),
+      static_cast<const E*>(Cm), static_cast<const E*>(gate), static_cast<E*>(out),
+      static_cast<E*>(raw_out), chunk_states, batch, dim, length, dstate,
+      static_cast<hipStream_t>(stream), "selective_forward_bf16");
+}
+
+int ossm_selective_backward_bf16(const void* grad_out, const void* u, const void* dt,
+                                 const float* A, const void* Bm, const void* Cm, const void* gate,
+                                 const float* chunk_states, const void* raw_out, void* du,
+                                 void* ddt, float* dA, void* dB, void* dC, void* dgate,
+                                 int64_t batch, int64_t dim, int64_t length, int64_t dstate,
+                                 ossm_stream_t stream) {
+  using E = bf16_t;
+  return selective_backward_impl<E>(
+      static_cast<const E*>(grad_out), static_cast<const E*>(u), static_cast<const E*>(dt), A,
+      static_cast<const E*>(Bm), static_cast<const E*>(Cm), static_cast<const E*>(gate),
+      chunk_states, static_cast<const E*>(raw_out), static_cast<E*>(du), static_cast<E*>(ddt), dA,
+      static_cast<E*>(dB), static_cast<E*>(dC), static_cast<E*>(dgate), batch, dim, length, dstate,
+      static_cast<hipStream_t>(stream), "selective_backward_bf16");
 }
 
 }  // extern "C"

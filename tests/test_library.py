@@ -33,7 +33,8 @@ def test_header_declares_the_entry_points():
     for n in ("ossm_dlinoss_forward", "ossm_dlinoss_backward", "ossm_linoss_forward",
               "ossm_linoss_backward", "ossm_selective_forward", "ossm_selective_backward",
               "ossm_selective_num_chunks", "ossm_abi_version", "ossm_last_error",
-              "ossm_device_error_bits"):
+              "ossm_device_error_bits", "ossm_selective_forward_bf16",
+              "ossm_selective_backward_bf16"):
         assert n in names, n
 
 
@@ -49,7 +50,7 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     # every declared symbol has a ctypes signature in the binding
     assert set(_declared_functions()) == set(_lib.EXPORTED)
-    assert _lib.load().ossm_abi_version() == 2
+    assert _lib.load().ossm_abi_version() == 3
 
 
 def test_dropin_module_has_every_reference_name():
