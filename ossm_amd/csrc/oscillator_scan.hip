@@ -33,12 +33,14 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdint>
 #include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <type_traits>
 
 #include "../../include/ossm_scan.h"
 #include "runtime.hpp"
@@ -66,7 +68,9 @@ struct Dlinoss {
   using GOut = float2;  // grad of bu_t
   using Mat = RMat;
   using Coef = DlCoef;
-  static constexpr int kSums = 6;
+  // Number of per-oscillator sums the variant's chain rule reads (see accumulate).
+  static constexpr int kSums =
+      (V == OSSM_DLINOSS_IMEX1 || V == OSSM_DLINOSS_EX) ? 3 : (V == OSSM_DLINOSS_IM ? 5 : 6);
   static constexpr bool kRecompute = true;  // s_{t-1} rebuilt from bu and a checkpoint
 
   struct Params {
@@ -162,44 +166,73 @@ struct Dlinoss {
     }
   }
 
-  // G_ij += <mu_i, s_j,t-1>,  F_i += <mu_i, bu_t>  (real inner products).
+  // The chain rule to (a, g, dt) reads the sums G_ij = sum <mu_i, s_j,t-1>
+  // and F_i = sum <mu_i, bu_t> (real inner products) only in the
+  // combinations below, so each lane accumulates just those:
+  //   imex1: G00 + G10, G01 + G11, F0 + F1  (both rows enter through mu0 + mu1)
+  //   ex:    G00, G01, F0 + G10
+  //   im:    G00, G01, G11, F0 + G10, F1
+  //   imex2: G00, G01, G10, G11, F0, F1
   static __device__ __forceinline__ void accumulate(float* acc, float4 m, float4 sp, float2 bu) {
-    acc[0] += m.x * sp.x + m.y * sp.y;  // G00
-    acc[1] += m.x * sp.z + m.y * sp.w;  // G01
-    acc[2] += m.z * sp.x + m.w * sp.y;  // G10
-    acc[3] += m.z * sp.z + m.w * sp.w;  // G11
-    acc[4] += m.x * bu.x + m.y * bu.y;  // F0
-    acc[5] += m.z * bu.x + m.w * bu.y;  // F1
+    // acc += p.x * q.x + p.y * q.y as two fused steps
+    auto dot = [](float a, float px, float py, float qx, float qy) {
+      return fmaf(py, qy, fmaf(px, qx, a));
+    };
+    if constexpr (V == OSSM_DLINOSS_IMEX1) {
+      const float tr = m.x + m.z, ti = m.y + m.w;
+      acc[0] = dot(acc[0], tr, ti, sp.x, sp.y);
+      acc[1] = dot(acc[1], tr, ti, sp.z, sp.w);
+      acc[2] = dot(acc[2], tr, ti, bu.x, bu.y);
+    } else if constexpr (V == OSSM_DLINOSS_EX) {
+      acc[0] = dot(acc[0], m.x, m.y, sp.x, sp.y);
+      acc[1] = dot(acc[1], m.x, m.y, sp.z, sp.w);
+      acc[2] = dot(dot(acc[2], m.x, m.y, bu.x, bu.y), m.z, m.w, sp.x, sp.y);
+    } else if constexpr (V == OSSM_DLINOSS_IM) {
+      acc[0] = dot(acc[0], m.x, m.y, sp.x, sp.y);
+      acc[1] = dot(acc[1], m.x, m.y, sp.z, sp.w);
+      acc[2] = dot(acc[2], m.z, m.w, sp.z, sp.w);
+      acc[3] = dot(dot(acc[3], m.x, m.y, bu.x, bu.y), m.z, m.w, sp.x, sp.y);
+      acc[4] = dot(acc[4], m.z, m.w, bu.x, bu.y);
+    } else {
+      acc[0] = dot(acc[0], m.x, m.y, sp.x, sp.y);  // G00
+      acc[1] = dot(acc[1], m.x, m.y, sp.z, sp.w);  // G01
+      acc[2] = dot(acc[2], m.z, m.w, sp.x, sp.y);  // G10
+      acc[3] = dot(acc[3], m.z, m.w, sp.z, sp.w);  // G11
+      acc[4] = dot(acc[4], m.x, m.y, bu.x, bu.y);  // F0
+      acc[5] = dot(acc[5], m.z, m.w, bu.x, bu.y);  // F1
+    }
   }
 
-  // Chain rule from the oscillator's summed (G00, G01, G10, G11, F0, F1) to
-  // (a, g, dt): imex1 dlinoss_imex1.cpp:219-232, im dlinoss_im.cpp:236-263,
-  // imex2 / ex by differentiating the coefficient tables of
-  // dlinoss_imex2.cpp:35-47 / dlinoss_ex.cpp:33-42 (the terms the reference
-  // accumulates per step).  out0/1/2 = grad_a, grad_g, grad_step.
+  // Chain rule from the oscillator's sums (see accumulate) to (a, g, dt):
+  // imex1 dlinoss_imex1.cpp:219-232, im dlinoss_im.cpp:236-263, imex2 / ex by
+  // differentiating the coefficient tables of dlinoss_imex2.cpp:35-47 /
+  // dlinoss_ex.cpp:33-42 (the terms the reference accumulates per step).
+  // out0/1/2 = grad_a, grad_g, grad_step.
   static __device__ void epilogue(const Params& prm, int p, const double* S, float* grad_a,
                                   float* grad_g, float* grad_step) {
-    const double G00 = S[0], G01 = S[1], G10 = S[2], G11 = S[3], F0 = S[4], F1 = S[5];
     const double a = prm.a[p], g = prm.g[p], dt = prm.dt[p];
     double ga, gg, gs;
     if constexpr (V == OSSM_DLINOSS_IMEX1) {
+      const double G0 = S[0], G1 = S[1], F = S[2];  // G00+G10, G01+G11, F0+F1
       const double inv = 1.0 / (1.0 + dt * g);
       const double s2i = dt * dt * inv;
-      const double ginv = G00 + G10;
-      const double gs2i = F0 + F1 - a * (G01 + G11);
-      ga = -s2i * (G01 + G11);
+      const double ginv = G0;
+      const double gs2i = F - a * G1;
+      ga = -s2i * G1;
       const double inv_total = ginv + gs2i * dt * dt;
       gs = gs2i * (2.0 * dt * inv) - inv_total * g * inv * inv;
       gg = -inv_total * dt * inv * inv;
     } else if constexpr (V == OSSM_DLINOSS_IMEX2) {
+      const double G00 = S[0], G01 = S[1], G10 = S[2], G11 = S[3], F0 = S[4], F1 = S[5];
       ga = -dt * G01 - dt * dt * G11;
       gg = -dt * G00 - dt * dt * G10;
       gs = -g * G00 - a * G01 + (1.0 - 2.0 * dt * g) * G10 - 2.0 * dt * a * G11 + F0 +
            2.0 * dt * F1;
     } else if constexpr (V == OSSM_DLINOSS_IM) {
+      const double G00 = S[0], G01 = S[1], G11 = S[2], F0G10 = S[3], F1 = S[4];
       const double inv = 1.0 / (1.0 + dt * g + dt * dt * a);
       const double si = dt * inv;
-      double gsi = F0 + G10, ginv = G00;
+      double gsi = F0G10, ginv = G00;
       const double gs2i = F1;
       gsi += G01 * (-a);
       ga = G01 * (-si);
@@ -216,9 +249,10 @@ struct Dlinoss {
       gg += gden * dt;
       gs += gden * (g + 2.0 * dt * a);
     } else {
+      const double G00 = S[0], G01 = S[1], F0G10 = S[2];
       ga = -dt * G01;
       gg = -dt * G00;
-      gs = -g * G00 - a * G01 + F0 + G10;
+      gs = -g * G00 - a * G01 + F0G10;
     }
     grad_a[p] = static_cast<float>(ga);
     grad_g[p] = static_cast<float>(gg);
@@ -279,12 +313,20 @@ struct Linoss {
   }
 };
 
-template <class T>
-__device__ __forceinline__ T zero_of();
-template <>
-__device__ __forceinline__ float2 zero_of<float2>() { return make_float2(0.f, 0.f); }
-template <>
-__device__ __forceinline__ float4 zero_of<float4>() { return f4zero(); }
+
+// Row t of a [L, nc] tensor, from the first channel of channel group g.  t,
+// nc and g are uniform across the wave, so the pointer is a scalar and each
+// lane adds only its 32-bit lane offset.
+template <class E>
+__device__ __forceinline__ E* group_row(E* base, long long t, int nc, int g) {
+  return base + static_cast<size_t>(t) * nc + static_cast<size_t>(g) * kWave;
+}
+
+// The lane's offset within its group, clamped onto the group's last channel
+// for lanes past the end (their loads stay in bounds; results are unused).
+__device__ __forceinline__ unsigned clamped_lane(int g, int nc) {
+  return static_cast<unsigned>(min(static_cast<int>(threadIdx.x & (kWave - 1)), nc - 1 - g * kWave));
+}
 
 // ============================================================================
 // Forward kernel
@@ -299,7 +341,7 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_forward_kernel(
   __shared__ int s_ticket;
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int w = threadIdx.x / kWave;
+  const int w = wave_id();
   const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
   if (ticket < 0) return;
   const int c = ticket / n_groups;
@@ -309,39 +351,53 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_forward_kernel(
   const auto k = Model::coef(prm, active ? ch : 0);
   const long long t0 = static_cast<long long>(c) * (T * W) + static_cast<long long>(w) * T;
 
+  // Clamped in-range addresses and no selects on the loaded values: the
+  // aggregate below consumes the steps as they arrive instead of waiting for
+  // all T loads (steps past L and inactive lanes are never used).
   typename Model::In x[T];
+  const unsigned lc = clamped_lane(g, nc);
 #pragma unroll
-  for (int i = 0; i < T; ++i) {
-    const long long t = t0 + i;
-    x[i] = (active && t < L) ? in[static_cast<size_t>(t) * nc + ch] : zero_of<typename Model::In>();
-  }
+  for (int i = 0; i < T; ++i) x[i] = group_row(in, min(t0 + i, static_cast<long long>(L - 1)), nc, g)[lc];
 
-  // 1. sub-chunk aggregate from a zero state
+  // 1. sub-chunk aggregate from a zero state (FULL: all T steps in range)
+  const bool full = t0 + T <= L;
   float4 e = f4zero();
+  if (full) {
 #pragma unroll
-  for (int i = 0; i < T; ++i)
-    if (t0 + i < L) e = Model::step(k, e, x[i]);
+    for (int i = 0; i < T; ++i) e = Model::step(k, e, x[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < T; ++i)
+      if (t0 + i < L) e = Model::step(k, e, x[i]);
+  }
   s_agg[w][lane] = e;
   const typename Model::Mat MT = mat_pow(Model::matrix(k), T);
   __syncthreads();
 
-  // 2. chunk aggregate, look-back, inclusive prefix
-  if (w == 0) {
+  // 2. chunk aggregate, look-back, inclusive prefix.  The aggregate is
+  // published by wave 1 while wave 0 walks back: a wave's loads complete in
+  // issue order behind its own stores, so a look-back issued after the
+  // publishing store would first wait for that store to reach memory.
+  constexpr int kPub = W > 1 ? 1 : 0;
+  if (w == 0 || w == kPub) {
     float4 E = f4zero();
 #pragma unroll
     for (int v = 0; v < W; ++v) E = f4add(mat_apply(MT, E), s_agg[v][lane]);
-    float4 carry = f4zero();
-    if (active && n_chunks > 1) {
-      const typename Model::Mat MC = mat_pow(Model::matrix(k), T * W);
-      if (c == 0) {
-        rec_publish(rec, c, kRecInc, nc, ch, E, sync.tag);
-      } else {
-        rec_publish(rec, c, kRecAgg, nc, ch, E, sync.tag);
-        carry = lookback(rec, c, +1, n_chunks, nc, ch, MC, sync);
-        if (c + 1 < n_chunks) rec_publish(rec, c, kRecInc, nc, ch, f4add(mat_apply(MC, carry), E), sync.tag);
+    const bool scan = active && n_chunks > 1;
+    if (w == kPub && scan && c > 0) rec_publish(rec, c, kRecAgg, nc, ch, E, sync.tag);
+    if (w == 0) {
+      float4 carry = f4zero();
+      if (scan) {
+        const typename Model::Mat MC = mat_pow(Model::matrix(k), T * W);
+        if (c == 0) {
+          rec_publish(rec, c, kRecInc, nc, ch, E, sync.tag);
+        } else {
+          carry = lookback(rec, c, +1, n_chunks, nc, ch, MC, sync);
+          if (c + 1 < n_chunks) rec_publish(rec, c, kRecInc, nc, ch, f4add(mat_apply(MC, carry), E), sync.tag);
+        }
       }
+      s_carry[lane] = carry;
     }
-    s_carry[lane] = carry;
   }
   __syncthreads();
 
@@ -349,12 +405,20 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_forward_kernel(
   float4 s = s_carry[lane];
   for (int v = 0; v < w; ++v) s = f4add(mat_apply(MT, s), s_agg[v][lane]);
   if (active) {
+    if (full) {
 #pragma unroll
-    for (int i = 0; i < T; ++i) {
-      const long long t = t0 + i;
-      if (t < L) {
+      for (int i = 0; i < T; ++i) {
         s = Model::step(k, s, x[i]);
-        out[static_cast<size_t>(t) * nc + ch] = s;
+        group_row(out, t0 + i, nc, g)[lane] = s;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < T; ++i) {
+        const long long t = t0 + i;
+        if (t < L) {
+          s = Model::step(k, s, x[i]);
+          group_row(out, t, nc, g)[lane] = s;
+        }
       }
     }
   }
@@ -394,7 +458,7 @@ __device__ __forceinline__ BwdTicket bwd_ticket(int ticket, int n_groups, int n_
   k.c = n_chunks - 1 - cr;
   k.ch = k.g * kWave + (threadIdx.x & (kWave - 1));
   k.active = k.ch < nc;
-  k.t0 = static_cast<long long>(k.c) * (T * W) + static_cast<long long>(threadIdx.x / kWave) * T;
+  k.t0 = static_cast<long long>(k.c) * (T * W) + static_cast<long long>(wave_id()) * T;
   return k;
 }
 
@@ -402,153 +466,202 @@ template <class Model, int T, int W>
 __device__ __forceinline__ void bwd_load(BwdBuf<Model, T>& b, const BwdTicket& k,
                                          const typename Model::Params& prm,
                                          const typename Model::In* __restrict__ in,
-                                         const float4* __restrict__ states,
+                                         const float4* states,
                                          const typename Model::GIn* __restrict__ gout, int L,
                                          int nc) {
-  const size_t ch = static_cast<size_t>(k.active ? k.ch : nc - 1);
-  b.raw = Model::load_raw(prm, static_cast<int>(ch));
+  // Issue order = order of use (loads complete in order): parameters and the
+  // checkpoint, then the forward recompute's inputs, then the upstream
+  // gradient last step first, as the reverse sweep consumes it.
+  const unsigned lc = clamped_lane(k.g, nc);
+  b.raw = Model::load_raw(prm, k.g * kWave + static_cast<int>(lc));
+  if constexpr (Model::kRecompute)
+    b.ck = group_row(states, max(min(k.t0 - 1, static_cast<long long>(L - 1)), 0ll), nc, k.g)[lc];
+  asm volatile("" ::: "memory");  // keep the issue order: the compiler would sink these
 #pragma unroll
   for (int i = 0; i < T; ++i) {
-    const size_t t = static_cast<size_t>(min(k.t0 + i, static_cast<long long>(L - 1)));
-    if constexpr (Model::kRecompute) {
-      b.x[i] = in[t * nc + ch];
-    } else {
-      const size_t tp = static_cast<size_t>(max(min(k.t0 + i - 1, static_cast<long long>(L - 1)), 0ll));
-      b.sp[i] = states[tp * nc + ch];
-    }
-    b.go[i] = gout[t * nc + ch];
+    if constexpr (Model::kRecompute)
+      b.x[i] = group_row(in, min(k.t0 + i, static_cast<long long>(L - 1)), nc, k.g)[lc];
+    else
+      b.sp[i] = group_row(states, max(min(k.t0 + i - 1, static_cast<long long>(L - 1)), 0ll), nc, k.g)[lc];
   }
-  if constexpr (Model::kRecompute) {
-    const size_t tc = static_cast<size_t>(max(min(k.t0 - 1, static_cast<long long>(L - 1)), 0ll));
-    b.ck = states[tc * nc + ch];
-  }
-}
-
-// Processes one chunk: recompute s_{t-1}, reverse aggregate, look-back for
-// the carry from later chunks, final reverse pass (grad_in and the parameter
-// sums), per-chunk partials.  All waves call it together.
-template <class Model, int T, int W, int S>
-__device__ __forceinline__ void bwd_process(
-    BwdBuf<Model, T>& b, const BwdTicket& k,
-    typename Model::GOut* __restrict__ gin, const ParamReduce& red, int L, int nc, int n_chunks,
-    unsigned long long* __restrict__ rec, const LaunchSync& sync, float4 (*s_agg)[kWave],
-    float4* s_carry, float4 (*s_sp)[S][kWave]) {
-  constexpr int NS = Model::kSums;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int w = threadIdx.x / kWave;
-  const auto cf = Model::coef_of(b.raw);
-  auto valid = [&](int i) { return k.active && k.t0 + i < L; };
-
-  // zero the out-of-range steps in place (the buffer's registers are reused,
-  // not copied); s_{t-1} rebuilt from the checkpoint
-  typename Model::GIn* go = b.go;
-#pragma unroll
-  for (int i = 0; i < T; ++i)
-    if (!valid(i)) go[i] = typename Model::GIn{};
-  // s_{t-1}: recomputed from the checkpoint into LDS (registers are the
-  // occupancy limit of this kernel), or read from the saved trajectory
-  typename Model::In xz[Model::kRecompute ? 1 : T];
-  typename Model::In* x = Model::kRecompute ? b.x : xz;
-  auto sp_at = [&](int i) -> float4 {
-    if constexpr (Model::kRecompute) return s_sp[w][i][lane];
-    else return b.sp[i];
-  };
-  if constexpr (Model::kRecompute) {
-#pragma unroll
-    for (int i = 0; i < T; ++i)
-      if (!valid(i)) x[i] = typename Model::In{};
-    float4 s = (k.active && k.t0 >= 1 && k.t0 <= L) ? b.ck : f4zero();
-#pragma unroll
-    for (int i = 0; i < T; ++i) {
-      s_sp[w][i][lane] = s;
-      if (k.t0 + i < L) s = Model::step(cf, s, x[i]);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < T; ++i) {
-      x[i] = typename Model::In{};
-      if (!(valid(i) && k.t0 + i >= 1)) b.sp[i] = f4zero();
-    }
-  }
-
-  // 1. reverse aggregate of the sub-chunk from a zero carry
-  float4 m = f4zero();
+  asm volatile("" ::: "memory");
 #pragma unroll
   for (int i = T - 1; i >= 0; --i)
-    if (k.t0 + i < L) m = Model::rev_carry(cf, Model::mu(m, go[i]));
+    b.go[i] = group_row(gout, min(k.t0 + i, static_cast<long long>(L - 1)), nc, k.g)[lc];
+}
+
+// First part of one chunk: reverse aggregate, look-back for the carry from
+// later chunks.  Returns the carry into the wave's sub-chunk (the adjoint
+// after its last step) and sets KT = (M^T)^T.  For recomputing models the
+// states s_{t-1} are rebuilt from the checkpoint states[t0 - 1] in H segments
+// of T/H steps, each staged in LDS (S = T/H slots per wave) just before the
+// final pass reads it (bwd_back): with H = 1 the front stages all of them;
+// with H = 2 it only runs to the middle of the sub-chunk (s_mid) and the
+// back recomputes each half in turn, halving the LDS footprint for one extra
+// half sweep.  All waves call it together.
+template <class Model, int T, int W, int S, int H>
+__device__ __forceinline__ float4 bwd_front(
+    BwdBuf<Model, T>& b, const BwdTicket& k, int L, int nc, int n_chunks,
+    unsigned long long* __restrict__ rec, const LaunchSync& sync, float4 (*s_agg)[kWave],
+    float4* s_carry, float4 (*s_sp)[S][kWave], typename Model::Mat& KT, float4& s_mid) {
+  static_assert(H == 1 || H == 2, "one or two staging segments");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = wave_id();
+  const auto cf = Model::coef_of(b.raw);
+
+  // Steps at or past L are never used (every use below is guarded), and lanes
+  // past the last channel only feed values that are never stored, so the
+  // loaded buffers need no masking.  FULL: the whole sub-chunk is in range
+  // (uniform), so the step loops run without guards.
+  auto sweep = [&](auto full_tag) -> float4 {
+    constexpr bool FULL = decltype(full_tag)::value;
+    auto live = [&](int i) { return FULL || k.t0 + i < L; };
+    if constexpr (Model::kRecompute) {
+      float4 s = k.t0 >= 1 ? b.ck : f4zero();
+      if constexpr (H == 1) {
+#pragma unroll
+        for (int i = 0; i < T; ++i) {
+          s_sp[w][i][lane] = s;
+          if (live(i)) s = Model::step(cf, s, b.x[i]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < T / 2; ++i)
+          if (live(i)) s = Model::step(cf, s, b.x[i]);
+        s_mid = s;
+      }
+    } else {
+      if (k.t0 == 0) b.sp[0] = f4zero();  // s_{-1} = 0
+    }
+    // 1. reverse aggregate of the sub-chunk from a zero carry
+    float4 m = f4zero();
+#pragma unroll
+    for (int i = T - 1; i >= 0; --i)
+      if (live(i)) m = Model::rev_carry(cf, Model::mu(m, b.go[i]));
+    return m;
+  };
+  const float4 m = k.t0 + T <= L ? sweep(std::true_type{}) : sweep(std::false_type{});
   s_agg[w][lane] = m;
-  const typename Model::Mat KT = mat_pow(mat_adjoint(Model::matrix(cf)), T);
+  KT = mat_pow(mat_adjoint(Model::matrix(cf)), T);
+  typename Model::Mat KC{};
+  if (w == 0 && n_chunks > 1) KC = mat_pow(mat_adjoint(Model::matrix(cf)), T * W);
   __syncthreads();
 
-  // 2. chunk aggregate (waves W-1 .. 0), look-back over later chunks
-  if (w == 0) {
+  // 2. chunk aggregate (waves W-1 .. 0), look-back over later chunks; the
+  // aggregate is published by wave 1 so that wave 0's look-back loads do not
+  // queue behind the publishing stores (a wave's memory operations complete
+  // in issue order)
+  constexpr int kPub = W > 1 ? 1 : 0;
+  if (w == 0 || w == kPub) {
     float4 E = f4zero();
 #pragma unroll
     for (int v = W - 1; v >= 0; --v) E = f4add(mat_apply(KT, E), s_agg[v][lane]);
-    float4 carry = f4zero();
-    if (k.active && n_chunks > 1) {
-      const typename Model::Mat KC = mat_pow(mat_adjoint(Model::matrix(cf)), T * W);
-      if (k.c == n_chunks - 1) {
-        rec_publish(rec, k.c, kRecInc, nc, k.ch, E, sync.tag);
-      } else {
-        rec_publish(rec, k.c, kRecAgg, nc, k.ch, E, sync.tag);
-        carry = lookback(rec, k.c, -1, n_chunks, nc, k.ch, KC, sync);
-        if (k.c > 0) rec_publish(rec, k.c, kRecInc, nc, k.ch, f4add(mat_apply(KC, carry), E), sync.tag);
+    const bool scan = k.active && n_chunks > 1;
+    if (w == kPub && scan && k.c < n_chunks - 1) rec_publish(rec, k.c, kRecAgg, nc, k.ch, E, sync.tag);
+    if (w == 0) {
+      float4 carry = f4zero();
+      if (scan) {
+        if (k.c == n_chunks - 1) {
+          rec_publish(rec, k.c, kRecInc, nc, k.ch, E, sync.tag);
+        } else {
+          carry = lookback(rec, k.c, -1, n_chunks, nc, k.ch, KC, sync);
+          if (k.c > 0) rec_publish(rec, k.c, kRecInc, nc, k.ch, f4add(mat_apply(KC, carry), E), sync.tag);
+        }
       }
+      s_carry[lane] = carry;
     }
-    s_carry[lane] = carry;
   }
   __syncthreads();
 
-  // 3. own carry, final reverse pass: grad of the inputs and parameter sums
+  // the wave's own carry: the chunk carry through the later waves' sub-chunks
   float4 y = s_carry[lane];
   for (int v = W - 1; v > w; --v) y = f4add(mat_apply(KT, y), s_agg[v][lane]);
+  return y;
+}
+
+// Second part: the final reverse pass (grad of the inputs and the parameter
+// sums) from carry y, then the chunk's per-channel partial sums.  `sp_lds` is
+// the wave's own S = T/H staging slots (see bwd_front); `s_sums` holds each
+// wave's NS sums, which wave 0 adds after a barrier.
+template <class Model, int T, int W, int H>
+__device__ __forceinline__ void bwd_back(BwdBuf<Model, T>& b, const BwdTicket& k, float4 y,
+                                         float4 s_mid, float4* sp_lds,
+                                         typename Model::GOut* __restrict__ gin,
+                                         const ParamReduce& red, int L, int nc, float* s_sums,
+                                         int sums_stride) {
+  constexpr int NS = Model::kSums;
+  constexpr int Q = T / H;  // steps per staged segment
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = wave_id();
+  const auto cf = Model::coef_of(b.raw);
   float acc[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) acc[j] = 0.f;
-  if (k.active) {
+  auto sweep = [&](auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    auto live = [&](int i) { return FULL || k.t0 + i < L; };
 #pragma unroll
-    for (int i = T - 1; i >= 0; --i) {
-      const long long t = k.t0 + i;
-      if (t < L) {
-        const float4 mu = Model::mu(y, go[i]);
-        gin[static_cast<size_t>(t) * nc + k.ch] = Model::grad_input(cf, mu);
-        Model::accumulate(acc, mu, sp_at(i), x[i]);
-        y = Model::rev_carry(cf, mu);
+    for (int h = H - 1; h >= 0; --h) {
+      if constexpr (Model::kRecompute && H > 1) {
+        // stage segment h: s_{t-1} for its Q steps, from its first state
+        float4 s = h == 0 ? (k.t0 >= 1 ? b.ck : f4zero()) : s_mid;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+          sp_lds[q * kWave + lane] = s;
+          if (live(h * Q + q)) s = Model::step(cf, s, b.x[h * Q + q]);
+        }
+      }
+#pragma unroll
+      for (int q = Q - 1; q >= 0; --q) {
+        const int i = h * Q + q;
+        if (live(i)) {
+          const float4 mu = Model::mu(y, b.go[i]);
+          group_row(gin, k.t0 + i, nc, k.g)[lane] = Model::grad_input(cf, mu);
+          if constexpr (Model::kRecompute)
+            Model::accumulate(acc, mu, sp_lds[(H > 1 ? q : i) * kWave + lane], b.x[i]);
+          else
+            Model::accumulate(acc, mu, b.sp[i], b.x[0]);
+          y = Model::rev_carry(cf, mu);
+        }
       }
     }
+  };
+  if (k.active) {
+    if (k.t0 + T <= L)
+      sweep(std::true_type{});
+    else
+      sweep(std::false_type{});
   }
-  // the per-wave sums go into this wave's own LDS region (its s_{t-1} slots
-  // are no longer read), so no barrier is needed before the writes
-  float* sums = reinterpret_cast<float*>(&s_sp[w][0][0]);
+  float* mine = s_sums + w * sums_stride;
 #pragma unroll
-  for (int j = 0; j < NS; ++j) sums[j * kWave + lane] = acc[j];
+  for (int j = 0; j < NS; ++j) mine[j * kWave + lane] = acc[j];
   __syncthreads();
 
-  // 4. this chunk's parameter partial sums (one per channel and sum)
+  // this chunk's parameter partial sums (one per channel and sum)
   if (w == 0 && k.active) {
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       float v = 0.f;
-      for (int u = 0; u < W; ++u) v += reinterpret_cast<const float*>(&s_sp[u][0][0])[j * kWave + lane];
-      red.partials[(static_cast<size_t>(k.c) * NS + j) * nc + k.ch] = v;
+      for (int u = 0; u < W; ++u) v += s_sums[u * sums_stride + j * kWave + lane];
+      group_row(red.partials, static_cast<long long>(k.c) * NS + j, nc, k.g)[lane] = v;
     }
   }
 }
 
 // One workgroup per (chunk, channel group), chunks handed out last-first in
 // launch-ticket order (so every chunk a look-back waits on is resident).
-template <class Model, int T, int W, int OCC>
+template <class Model, int T, int W, int OCC, int H>
 __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
     typename Model::Params prm, const typename Model::In* __restrict__ in,
-    const float4* __restrict__ states, const typename Model::GIn* __restrict__ gout,
+    const float4* states, const typename Model::GIn* __restrict__ gout,
     typename Model::GOut* __restrict__ gin, ParamReduce red, int L, int nc,
     int n_groups, int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
   constexpr int NS = Model::kSums;
   __shared__ float4 s_agg[W][kWave];
   __shared__ float4 s_carry[kWave];
-  // per wave: its T recomputed states s_{t-1}, later its NS partial sums
-  constexpr int kSlots = (Model::kRecompute ? T : 0) > (NS + 3) / 4 ? T : (NS + 3) / 4;
+  // per wave: its T / H staged states s_{t-1}, later its NS partial sums
+  constexpr int kStage = Model::kRecompute ? T / H : 0;
+  constexpr int kSlots = kStage > (NS + 3) / 4 ? kStage : (NS + 3) / 4;
   __shared__ float4 s_sp[W][kSlots][kWave];
   __shared__ int s_ticket;
   const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
@@ -556,7 +669,14 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
   const BwdTicket k = bwd_ticket<T, W>(ticket, n_groups, n_chunks, nc);
   BwdBuf<Model, T> b;
   bwd_load<Model, T, W>(b, k, prm, in, states, gout, L, nc);
-  bwd_process<Model, T, W, kSlots>(b, k, gin, red, L, nc, n_chunks, rec, sync, s_agg, s_carry, s_sp);
+  typename Model::Mat KT;
+  float4 s_mid = f4zero();
+  const float4 y = bwd_front<Model, T, W, kSlots, H>(b, k, L, nc, n_chunks, rec, sync, s_agg,
+                                                     s_carry, s_sp, KT, s_mid);
+  // the per-wave sums go into the wave's own s_{t-1} region, which only the
+  // wave itself reads before this point
+  bwd_back<Model, T, W, H>(b, k, y, s_mid, &s_sp[wave_id()][0][0], gin, red, L, nc,
+                           reinterpret_cast<float*>(&s_sp[0][0][0]), kSlots * kWave * 4);
 }
 
 // ============================================================================
@@ -565,32 +685,46 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
 // The partials form, for each sum j, a matrix of R = n_chunks * B rows
 // (chunk c, batch row b) by P columns (oscillator p): address
 // (c * NS + j) * nc + b * P + p.  Column sums in two passes:
-//   pass 1: block (column tile of 64, row group g) sums rows r = g*4 + w + k*G*4
-//           (w = wave) in fp64, waves combined through LDS -> colsum[g][j][p];
-//   pass 2: per oscillator, adds the G row groups in order, then the chain rule.
+//   pass 1: block (column tile of 64, row group g) sums rows r = g*4 + w + k*4G
+//           (w = wave) in fp64, four rows in flight per lane, waves combined
+//           through LDS -> colsum[g][j][p];
+//   pass 2: one wave per oscillator, lane g holding row group g, adds them
+//           by a butterfly over the wave, then the chain rule.
 // Fixed order everywhere: deterministic.
-constexpr int kRowGroups = 16;
+constexpr int kRowGroups = kWave;
+constexpr int kColsumRows = 4;  // rows per lane per round (independent loads)
 
 template <int NS>
 __global__ __launch_bounds__(256) void osc_colsum_kernel(const float* __restrict__ partials,
                                                          double* __restrict__ colsum, int P,
                                                          int B, int n_chunks) {
   __shared__ double s_red[4][NS][kWave];
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1), w = wave_id();
   const int p = blockIdx.x * kWave + lane;
+  const int pc = min(p, P - 1);
   const int g = blockIdx.y;
   const size_t nc = static_cast<size_t>(B) * P;
   const int R = n_chunks * B;
+  constexpr int kStride = kRowGroups * 4;
   double acc[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) acc[j] = 0.0;
-  if (p < P) {
-    for (int r = g * 4 + w; r < R; r += kRowGroups * 4) {
-      const int c = r / B, b = r - c * B;
-      const float* src = partials + static_cast<size_t>(c) * NS * nc + static_cast<size_t>(b) * P + p;
+  for (int r0 = g * 4 + w; r0 < R; r0 += kStride * kColsumRows) {
+    float v[kColsumRows][NS];
 #pragma unroll
-      for (int j = 0; j < NS; ++j) acc[j] += static_cast<double>(src[j * nc]);
+    for (int u = 0; u < kColsumRows; ++u) {
+      const int r = min(r0 + u * kStride, R - 1);
+      const int c = r / B, b = r - c * B;
+      const float* src = partials + static_cast<size_t>(c) * NS * nc + static_cast<size_t>(b) * P + pc;
+#pragma unroll
+      for (int j = 0; j < NS; ++j) v[u][j] = src[j * nc];
     }
+#pragma unroll
+    for (int u = 0; u < kColsumRows; ++u)
+      if (r0 + u * kStride < R) {
+#pragma unroll
+        for (int j = 0; j < NS; ++j) acc[j] += static_cast<double>(v[u][j]);
+      }
   }
 #pragma unroll
   for (int j = 0; j < NS; ++j) s_red[w][j][lane] = acc[j];
@@ -603,21 +737,24 @@ __global__ __launch_bounds__(256) void osc_colsum_kernel(const float* __restrict
   }
 }
 
+// 256 threads = four oscillators per block.
 template <class Model>
 __global__ __launch_bounds__(256) void osc_param_kernel(typename Model::Params prm,
                                                         const double* __restrict__ colsum, int P,
                                                         float* out0, float* out1, float* out2) {
   constexpr int NS = Model::kSums;
-  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int p = blockIdx.x * 4 + wave_id();
   if (p >= P) return;
   double S[NS];
 #pragma unroll
-  for (int j = 0; j < NS; ++j) {
-    double v = 0.0;
+  for (int j = 0; j < NS; ++j) S[j] = colsum[(static_cast<size_t>(lane) * NS + j) * P + p];
 #pragma unroll
-    for (int g = 0; g < kRowGroups; ++g) v += colsum[(static_cast<size_t>(g) * NS + j) * P + p];
-    S[j] = v;
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+#pragma unroll
+    for (int j = 0; j < NS; ++j) S[j] += __shfl_xor(S[j], off, kWave);
   }
+  if (lane != 0) return;
   Model::epilogue(prm, p, S, out0, out1, out2);
 }
 
@@ -637,26 +774,32 @@ int fill_zero(float* p, int64_t n, hipStream_t stream) {
 
 // T steps per lane, W waves per workgroup, OCC = minimum waves per SIMD the
 // register allocation must allow (__launch_bounds__' second argument).
+// H (backward only) = staging segments of the recomputed states.
 struct Tile {
-  int T, W, O;
+  int T, W, O, H;
 };
 
+// "TxWxO" or "TxWxOxH" (H defaults to 1).
 Tile parse_tile(const char* env, Tile dflt) {
   const char* s = std::getenv(env);
   if (!s) return dflt;
-  int t = 0, w = 0, o = 0;
-  if (std::sscanf(s, "%dx%dx%d", &t, &w, &o) != 3) return dflt;
-  return {t, w, o};
+  int t = 0, w = 0, o = 0, h = 1;
+  const int n = std::sscanf(s, "%dx%dx%dx%d", &t, &w, &o, &h);
+  if (n < 3) return dflt;
+  return {t, w, o, h};
 }
 
 // Instantiated tiles (T, W, OCC).
 #define OSSM_FWD_TILES(X) X(16, 8, 1) X(16, 8, 4) X(8, 8, 4) X(16, 4, 4) X(8, 16, 4) X(32, 4, 2)
-#define OSSM_BWD_TILES(X) X(16, 8, 1) X(16, 4, 1) X(8, 8, 1) X(32, 4, 1) X(8, 16, 1) X(4, 16, 2)
+// Backward tiles (T, W, OCC, H): H = staging segments of the recomputed states.
+#define OSSM_BWD_TILES(X)                                                                     \
+  X(16, 8, 1, 1) X(16, 8, 4, 2) X(16, 8, 2, 2) X(16, 4, 1, 1) X(8, 8, 1, 1) X(8, 8, 4, 2)      \
+  X(32, 4, 1, 1) X(32, 4, 2, 2) X(8, 16, 1, 1)
 
 template <class Model>
 int launch_forward(const typename Model::Params& prm, const void* in, void* out, int64_t L,
                    int64_t nc, hipStream_t stream) {
-  static const Tile tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{16, 8, 1});
+  static const Tile tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{16, 8, 1, 1});
   const int64_t CL = int64_t(tile.T) * tile.W;
   const int64_t n_chunks = (L + CL - 1) / CL;
   const int64_t n_groups = (nc + kWave - 1) / kWave;
@@ -697,7 +840,7 @@ template <class Model>
 int launch_backward(const typename Model::Params& prm, const void* in, const void* states,
                     const void* gout, void* gin, float* out0, float* out1, float* out2, int64_t L,
                     int64_t B, int64_t P, hipStream_t stream) {
-  static const Tile tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{16, 8, 1});
+  static const Tile tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{16, 8, 1, 1});
   constexpr int NS = Model::kSums;
   const int64_t nc = B * P;
   const int64_t CL = int64_t(tile.T) * tile.W;
@@ -718,9 +861,10 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   LaunchSync sync{};
   if (int rc = acquire_scratch(stream, rec_bytes, total, &payload, &sync)) return rc;
   bool launched = false;
-#define OSSM_LAUNCH_BWD(TT, WW, OO)                                                              \
-  if (!launched && tile.T == TT && tile.W == WW && tile.O == OO) {                               \
-    hipLaunchKernelGGL((osc_backward_kernel<Model, TT, WW, OO>), dim3(static_cast<unsigned>(total)), \
+#define OSSM_LAUNCH_BWD(TT, WW, OO, HH)                                                          \
+  if (!launched && tile.T == TT && tile.W == WW && tile.O == OO && tile.H == HH) {               \
+    hipLaunchKernelGGL((osc_backward_kernel<Model, TT, WW, OO, HH>),                             \
+                       dim3(static_cast<unsigned>(total)),                                       \
                        dim3(WW * kWave), 0, stream,                                              \
                        prm, static_cast<const typename Model::In*>(in),                          \
                        static_cast<const float4*>(states),                                       \
@@ -730,7 +874,7 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
                        static_cast<int>(n_chunks), static_cast<unsigned long long*>(payload),    \
                        sync);                                                                    \
     if (int rc = launch_check("osc_backward_kernel")) {                                          \
-      release_unlaunched(stream, total);                                                         \
+      release_unlaunched(stream, total);                                                       \
       return rc;                                                                                 \
     }                                                                                            \
     launched = true;                                                                             \
@@ -746,7 +890,7 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
                      stream, red.partials, colsum, static_cast<int>(P), static_cast<int>(B),
                      static_cast<int>(n_chunks));
   if (int rc = launch_check("osc_colsum_kernel")) return rc;
-  hipLaunchKernelGGL(osc_param_kernel<Model>, dim3(static_cast<unsigned>((P + 255) / 256)),
+  hipLaunchKernelGGL(osc_param_kernel<Model>, dim3(static_cast<unsigned>((P + 3) / 4)),
                      dim3(256), 0, stream, prm, colsum, static_cast<int>(P), out0, out1, out2);
   return launch_check("osc_param_kernel");
 }

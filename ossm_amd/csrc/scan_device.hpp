@@ -152,13 +152,18 @@ __device__ __forceinline__ void rec_publish(unsigned long long* rec, int chunk, 
   }
 }
 
-__device__ __forceinline__ bool rec_read(unsigned long long* rec, int chunk, int kind, int nc,
-                                         int ch, unsigned int tag, float4* v) {
-  unsigned long long w[4];
+// Loads the four words of one record without waiting for them.
+__device__ __forceinline__ void rec_fetch(const unsigned long long* rec, int chunk, int kind, int nc,
+                                          int ch, unsigned long long (&w)[4]) {
 #pragma unroll
   for (int k = 0; k < 4; ++k)
     w[k] = __hip_atomic_load(rec + rec_index(chunk, kind, k, nc, ch), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Whether all four words carry this launch's tag; the value in *v.
+__device__ __forceinline__ bool rec_decode(const unsigned long long (&w)[4], unsigned int tag,
+                                           float4* v) {
   bool ok = true;
 #pragma unroll
   for (int k = 0; k < 4; ++k) ok = ok && (static_cast<unsigned int>(w[k] >> 32) == tag);
@@ -169,6 +174,15 @@ __device__ __forceinline__ bool rec_read(unsigned long long* rec, int chunk, int
   return ok;
 }
 
+// Predecessor records fetched per round trip of the look-back.  Records live
+// in memory shared by all XCDs, so each read is a full memory round trip;
+// fetching both records of kLookbackWindow predecessors at once turns a walk
+// over k chunks from 2k round trips into about k / kLookbackWindow.
+#ifndef OSSM_LOOKBACK_WINDOW
+#define OSSM_LOOKBACK_WINDOW 1
+#endif
+constexpr int kLookbackWindow = OSSM_LOOKBACK_WINDOW;
+
 // Carry into chunk `c` for one channel: walks predecessors c - dir, c - 2 dir,
 // ... (dir = +1 forward in time, -1 for reverse scans), composing aggregates
 // with `step_mat` (the chunk transition) until an inclusive prefix is found.
@@ -178,20 +192,38 @@ __device__ __forceinline__ bool rec_read(unsigned long long* rec, int chunk, int
 template <class Mat>
 __device__ float4 lookback(unsigned long long* rec, int c, int dir, int n_chunks, int nc, int ch,
                            Mat step_mat, const LaunchSync& sync) {
+  constexpr int K = kLookbackWindow;
   float4 acc = f4zero();
   Mat pw = mat_identity(step_mat);
-  for (int j = c - dir; j >= 0 && j < n_chunks; j -= dir) {
-    uint32_t spins = 0;
-    for (;;) {
+  int j = c - dir;  // next predecessor to fold in
+  uint32_t spins = 0;
+  while (j >= 0 && j < n_chunks) {
+    unsigned long long wi[K][4], wa[K][4];
+#pragma unroll
+    for (int q = 0; q < K; ++q) {
+      const int jj = min(max(j - q * dir, 0), n_chunks - 1);  // in range; unused past the end
+      rec_fetch(rec, jj, kRecInc, nc, ch, wi[q]);
+      rec_fetch(rec, jj, kRecAgg, nc, ch, wa[q]);
+    }
+    bool moved = false, done = false;
+#pragma unroll
+    for (int q = 0; q < K; ++q) {
+      if (done || !(j >= 0 && j < n_chunks)) break;
       float4 v;
-      if (rec_read(rec, j, kRecInc, nc, ch, sync.tag, &v)) {
-        return f4add(acc, mat_apply(pw, v));
-      }
-      if (rec_read(rec, j, kRecAgg, nc, ch, sync.tag, &v)) {
+      if (rec_decode(wi[q], sync.tag, &v)) {
+        acc = f4add(acc, mat_apply(pw, v));
+        done = true;
+      } else if (rec_decode(wa[q], sync.tag, &v)) {
         acc = f4add(acc, mat_apply(pw, v));
         pw = mat_mul(pw, step_mat);
-        break;
+        j -= dir;
+        moved = true;
+      } else {
+        break;  // not published yet: fetch again from j
       }
+    }
+    if (done) return acc;
+    if (!moved) {
       if (++spins > kSpinLimit) {
         __hip_atomic_fetch_or(sync.err, kErrSpinTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return acc;
@@ -236,7 +268,13 @@ __device__ __forceinline__ int draw_ticket(const LaunchSync& sync, int total, in
 
 __device__ __forceinline__ int launch_order(const LaunchSync& sync, int total, int* s_slot) {
   if (!sync.use_ticket) return static_cast<int>(blockIdx.x);
-  return draw_ticket(sync, total, s_slot);
+  // uniform across the workgroup: keep it (and what derives from it) scalar
+  return __builtin_amdgcn_readfirstlane(draw_ticket(sync, total, s_slot));
+}
+
+// Index of the calling wave in its workgroup, as a scalar value.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
 }
 
 }  // namespace ossm
