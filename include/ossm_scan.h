@@ -12,6 +12,7 @@
  *   D-LinOSS:   a_diag, g_diag, step [P] f32;  bu [L,B,P] c64;
  *               states [L,B,P,2] c64 (component 0 = auxiliary w, 1 = x)
  *   LinOSS:     m11, m12, m21, m22 [P] c64;  b_seq, states [L,B,P,2] c64
+ *   sel. D-LinOSS: A, G, step [L|1, B|1, M] f32;  bu [L,B,M] c64;  states [L,B,M,2] c64
  *   selective:  u, dt, gate, out [B,D,L] f32;  A [D,N] f32;  Bm, Cm [B,L,N] f32
  *               (the _bf16 entries: the same layouts with bf16 except A, dA, chunk_states)
  *
@@ -41,7 +42,7 @@ enum {
 
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
-/* Library ABI version (bumped on any change of the entry points; currently 3). */
+/* Library ABI version (bumped on any change of the entry points; currently 4). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -135,6 +136,37 @@ int ossm_selective_backward(const float* grad_out, const float* u, const float* 
                             float* ddt, float* dA, float* dB, float* dC, float* dgate,
                             int64_t batch, int64_t dim, int64_t length, int64_t dstate,
                             ossm_stream_t stream);
+
+/*
+ * Selective D-LinOSS forward, replaces sdlinoss_<v>_forward (bindings.cpp:60-106,
+ * 169-176; dispatcher sdlinoss_imex1.cpp:317-355, CPU kernel :33-97, and siblings).
+ * Per step, dt = clamp(step, 1e-6, 1): comb = -a x + bu, tmpw = alpha w + dt^2 comb,
+ * w' = tmpw / S, x' = x + w', with (alpha, S) per variant:
+ *   imex1 (1, max(1 + dt g, 1e-6)), imex2 (1 - dt g, max(1 + dt^2 a, 1e-6)),
+ *   im (1, max(1 + dt g + dt^2 a, 1e-6)), ex (1 - dt g, 1).
+ * A, G, step are fp32 [X_len, X_batch, M] contiguous with X_len in {1, length} and
+ * X_batch in {1, batch} (broadcast over time / batch); bu [L,B,M] c64; states
+ * [L,B,M,2] c64 (component 0 = w, 1 = x).
+ */
+int ossm_sdlinoss_forward(int variant, const float* A, int64_t a_len, int64_t a_batch,
+                          const float* G, int64_t g_len, int64_t g_batch, const float* step,
+                          int64_t s_len, int64_t s_batch, const void* bu, void* states,
+                          int64_t length, int64_t batch, int64_t ssm, ossm_stream_t stream);
+
+/*
+ * Selective D-LinOSS backward, replaces sdlinoss_<v>_backward (dispatcher
+ * sdlinoss_imex1.cpp:357-425, CPU kernel :99-231, and siblings).  states must be the forward's output on the same inputs (the
+ * backward reads it at sub-chunk starts only and recomputes the steps in between).
+ * Writes grad_bu [L,B,M] c64 and grad_A, grad_G, grad_step with the shapes of A, G,
+ * step: per-step gradients summed over the broadcast axes (sdlinoss_cpu_utils.h:84-97)
+ * in a fixed order.  grad_step is zero where step was clamped.
+ */
+int ossm_sdlinoss_backward(int variant, const float* A, int64_t a_len, int64_t a_batch,
+                           const float* G, int64_t g_len, int64_t g_batch, const float* step,
+                           int64_t s_len, int64_t s_batch, const void* bu, const void* states,
+                           const void* grad_output, float* grad_A, float* grad_G,
+                           float* grad_step, void* grad_bu, int64_t length, int64_t batch,
+                           int64_t ssm, ossm_stream_t stream);
 
 /*
  * bf16 storage variants of the two entries above.  No counterpart in the

@@ -8,7 +8,8 @@ package, and only as the checker or the timed CPU baseline.  The product path
 (``ossm_amd``) never imports it.
 
 All functions take and return numpy arrays in the reference's layouts:
-D-LinOSS ``bu [L,B,P]`` complex, states ``[L,B,P,2]`` complex; LinOSS
+D-LinOSS ``bu [L,B,P]`` complex, states ``[L,B,P,2]`` complex (the selective
+D-LinOSS alike, with parameters (M,), (L,M), (B,M) or (L|1,B|1,M)); LinOSS
 ``b_seq [L,B,P,2]`` complex with complex ``m_ij [P]``; selective scan
 ``u, dt, gate [B,D,L]``, ``A [D,N]``, ``B, C [B,L,N]`` real.
 """
@@ -181,6 +182,73 @@ def selective_backward(grad_output, u, dt, A, Bm, Cm, gate=None):
         _ptr(gout), _ptr(u), _ptr(dt), _ptr(A), _ptr(Bm), _ptr(Cm), _ptr(gate), _ptr(gu),
         _ptr(gdt), _ptr(gA), _ptr(gB), _ptr(gC), _ptr(ggate), I(Bsz), I(D), I(L), I(N))
     return gu, gdt, gA, gB, gC, ggate
+
+
+# ------------------------------------------------------ selective D-LinOSS
+def _sdl_view(param, length: int, batch: int, ssm: int) -> np.ndarray:
+    """normalize_param_view_cpu (sdlinoss_cpu_utils.h:11-72) as a [La, Ba, M] view."""
+    p = np.asarray(param)
+    if p.ndim == 1 and p.shape[0] == ssm:
+        return p.reshape(1, 1, ssm)
+    if p.ndim == 2 and p.shape[1] == ssm:
+        if p.shape[0] == length:
+            return p.reshape(length, 1, ssm)
+        if p.shape[0] == batch:
+            return p.reshape(1, batch, ssm)
+    if p.ndim == 3 and p.shape[2] == ssm and p.shape[0] in (1, length) and p.shape[1] in (1, batch):
+        return p
+    raise ValueError(f"parameter must be shaped as (M,), (L,M), (B,M), or (L,B,M); got {p.shape}")
+
+
+def _sdl_full(param, length, batch, ssm, rt) -> np.ndarray:
+    """materialize_param_cpu (sdlinoss_cpu_utils.h:74-82)."""
+    return _c(np.broadcast_to(_sdl_view(param, length, batch, ssm), (length, batch, ssm)), rt)
+
+
+def sdlinoss_forward(variant: str, A, G, step, bu) -> np.ndarray:
+    """States ``[L,B,M,2]`` of the selective D-LinOSS recurrence (sdlinoss_<v>.cpp forward);
+    A, G, step may be (M,), (L,M), (B,M) or (L|1, B|1, M)."""
+    prec = _prec_of(np.asarray(bu))
+    rt, ct = _real_dtype(prec), _complex_dtype(prec)
+    bu = _c(bu, ct)
+    L, B, M = bu.shape
+    full = [_sdl_full(x, L, B, M, rt) for x in (A, G, step)]
+    out = np.empty((L, B, M, 2), dtype=ct)
+    I = ctypes.c_int64
+    _fn("oracle_sdlinoss_forward", prec)(
+        ctypes.c_int(_VARIANT_CODE[variant]), *[_ptr(x) for x in full], _ptr(bu), _ptr(out),
+        I(L), I(B), I(M))
+    return out
+
+
+def sdlinoss_backward(variant: str, A, G, step, bu, states, grad_output):
+    """``(grad_A, grad_G, grad_step, grad_bu)`` (sdlinoss_<v>.cpp backward); parameter
+    gradients summed over broadcast axes and shaped like the parameters
+    (reduce_broadcast_grad, sdlinoss_cpu_utils.h:84-97)."""
+    prec = _prec_of(np.asarray(bu))
+    rt, ct = _real_dtype(prec), _complex_dtype(prec)
+    bu = _c(bu, ct)
+    L, B, M = bu.shape
+    params = (A, G, step)
+    full = [_sdl_full(x, L, B, M, rt) for x in params]
+    states = _c(states, ct)
+    gout = _c(grad_output, ct)
+    grad_bu = np.empty_like(bu)
+    g_full = [np.zeros((L, B, M), rt) for _ in range(3)]
+    I = ctypes.c_int64
+    _fn("oracle_sdlinoss_backward", prec)(
+        ctypes.c_int(_VARIANT_CODE[variant]), *[_ptr(x) for x in full], _ptr(bu), _ptr(states),
+        _ptr(gout), _ptr(grad_bu), *[_ptr(x) for x in g_full], I(L), I(B), I(M))
+    out = []
+    for p, gf in zip(params, g_full):
+        view = _sdl_view(p, L, B, M)
+        g = gf
+        if view.shape[0] == 1 and L > 1:
+            g = g.sum(0, keepdims=True)
+        if view.shape[1] == 1 and B > 1:
+            g = g.sum(1, keepdims=True)
+        out.append(np.ascontiguousarray(g.reshape(np.asarray(p).shape), dtype=rt))
+    return out[0], out[1], out[2], grad_bu
 
 
 # ------------------------------------------------- reference CPU kernels

@@ -483,3 +483,134 @@ void SFX(oracle_selective_backward)(const REAL* gout, const REAL* u, const REAL*
   }
   free(gA_part);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Selective D-LinOSS (time- and batch-varying parameters)                   */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Restates the reference's CPU kernels: forward sdlinoss_imex1.cpp:33-97,
+ * sdlinoss_imex2.cpp:33-97, sdlinoss_im.cpp:33-97, sdlinoss_ex.cpp:25-84;
+ * backward sdlinoss_imex1.cpp:99-231, sdlinoss_imex2.cpp:100-230,
+ * sdlinoss_im.cpp:100-230, sdlinoss_ex.cpp:86-200.  Parallel over the
+ * B*M series, time inner, as there.  A, G, step are materialised [L,B,M]
+ * (materialize_param_cpu, sdlinoss_cpu_utils.h:74-82); the per-element
+ * parameter gradients are returned [L,B,M] and summed over broadcast axes
+ * by the Python wrapper (reduce_broadcast_grad, sdlinoss_cpu_utils.h:84-97).
+ */
+static REAL SFX(sdl_clamp_step)(REAL raw) {
+  const REAL lo = (REAL)1e-6, hi = (REAL)1.0;
+  return raw < lo ? lo : (raw > hi ? hi : raw);
+}
+
+static REAL SFX(sdl_s_raw)(int variant, REAL dt, REAL g, REAL a) {
+  switch (variant) {
+    case 0: return (REAL)1 + dt * g;              /* imex1 */
+    case 1: return (REAL)1 + dt * dt * a;         /* imex2 */
+    case 2: return (REAL)1 + dt * g + dt * dt * a; /* im */
+    default: return (REAL)1;                      /* ex: no implicit part */
+  }
+}
+
+void SFX(oracle_sdlinoss_forward)(int variant, const REAL* A, const REAL* G, const REAL* step,
+                                  const REAL* bu, REAL* out, int64_t length, int64_t batch,
+                                  int64_t ssm) {
+  const int64_t series = batch * ssm;
+#pragma omp parallel for schedule(static)
+  for (int64_t idx = 0; idx < series; ++idx) {
+    REAL wr = 0, wi = 0, xr = 0, xi = 0;
+    for (int64_t t = 0; t < length; ++t) {
+      const int64_t off = t * series + idx;
+      const REAL a = A[off], g = G[off];
+      const REAL dt = SFX(sdl_clamp_step)(step[off]);
+      const REAL dt2 = dt * dt;
+      const REAL bur = bu[2 * off], bui = bu[2 * off + 1];
+      const REAL combr = -a * xr + bur, combi = -a * xi + bui;
+      REAL nwr, nwi;
+      if (variant == 3) { /* ex */
+        const REAL alpha = (REAL)1 - dt * g;
+        nwr = FMA(dt2, combr, alpha * wr);
+        nwi = FMA(dt2, combi, alpha * wi);
+      } else {
+        REAL S = SFX(sdl_s_raw)(variant, dt, g, a);
+        if (S < (REAL)1e-6) S = (REAL)1e-6;
+        const REAL inv = (REAL)1 / S;
+        REAL tr, ti;
+        if (variant == 1) { /* imex2 */
+          const REAL alpha = (REAL)1 - dt * g;
+          tr = alpha * wr + dt2 * combr;
+          ti = alpha * wi + dt2 * combi;
+        } else {
+          tr = FMA(dt2, combr, wr);
+          ti = FMA(dt2, combi, wi);
+        }
+        nwr = tr * inv;
+        nwi = ti * inv;
+      }
+      const REAL nxr = xr + nwr, nxi = xi + nwi;
+      REAL* o = out + 4 * off;
+      o[0] = nwr; o[1] = nwi; o[2] = nxr; o[3] = nxi;
+      wr = nwr; wi = nwi; xr = nxr; xi = nxi;
+    }
+  }
+}
+
+void SFX(oracle_sdlinoss_backward)(int variant, const REAL* A, const REAL* G, const REAL* step,
+                                   const REAL* bu, const REAL* states, const REAL* grad_out,
+                                   REAL* grad_bu, REAL* grad_A, REAL* grad_G, REAL* grad_step,
+                                   int64_t length, int64_t batch, int64_t ssm) {
+  const int64_t series = batch * ssm;
+#pragma omp parallel for schedule(static)
+  for (int64_t idx = 0; idx < series; ++idx) {
+    REAL gwnr = 0, gwni = 0, gxnr = 0, gxni = 0; /* gradients carried from t + 1 */
+    for (int64_t t = length - 1; t >= 0; --t) {
+      const int64_t off = t * series + idx;
+      REAL wpr = 0, wpi = 0, xpr = 0, xpi = 0;
+      if (t > 0) {
+        const REAL* p = states + 4 * (off - series);
+        wpr = p[0]; wpi = p[1]; xpr = p[2]; xpi = p[3];
+      }
+      const REAL gor = grad_out[2 * off], goi = grad_out[2 * off + 1];
+      const REAL gxr = gor + gxnr, gxi = goi + gxni; /* d/dx_t */
+      /* d/dw_t through both outputs (x_t = x_{t-1} + w_t) */
+      const REAL gwr = gwnr + gxr, gwi = gwni + gxi;
+      const REAL a = A[off], g = G[off], raw = step[off];
+      const REAL dt = SFX(sdl_clamp_step)(raw);
+      const REAL mask = (raw > (REAL)1e-6 && raw < (REAL)1.0) ? (REAL)1 : (REAL)0;
+      const REAL dt2 = dt * dt;
+      const REAL bur = bu[2 * off], bui = bu[2 * off + 1];
+      const REAL combr = -a * xpr + bur, combi = -a * xpi + bui;
+      const REAL alpha = (variant == 1 || variant == 3) ? (REAL)1 - dt * g : (REAL)1;
+      REAL gs = 0, ga = 0, gg = 0;
+      REAL gtr = gwr, gti = gwi; /* d/dtmpw */
+      if (variant != 3) {
+        const REAL s_raw = SFX(sdl_s_raw)(variant, dt, g, a);
+        const REAL S = s_raw < (REAL)1e-6 ? (REAL)1e-6 : s_raw;
+        const REAL cm = s_raw > (REAL)1e-6 ? (REAL)1 : (REAL)0;
+        const REAL inv = (REAL)1 / S;
+        const REAL tmr = alpha * wpr + dt2 * combr, tmi = alpha * wpi + dt2 * combi;
+        gtr = gwr * inv;
+        gti = gwi * inv;
+        const REAL gS = -(gwr * tmr + gwi * tmi) * (inv * inv) * cm;
+        if (variant == 0) { gs += gS * g; gg += gS * dt; }
+        else if (variant == 1) { gs += gS * ((REAL)2 * dt * a); ga += gS * dt2; }
+        else { gs += gS * (g + (REAL)2 * dt * a); ga += gS * dt2; gg += gS * dt; }
+      }
+      if (variant == 1 || variant == 3) {
+        gs += gtr * (-g * wpr + (REAL)2 * dt * combr) + gti * (-g * wpi + (REAL)2 * dt * combi);
+        gg += gtr * (-dt * wpr) + gti * (-dt * wpi);
+      } else {
+        gs += gtr * ((REAL)2 * dt * combr) + gti * ((REAL)2 * dt * combi);
+      }
+      ga += gtr * (-dt2 * xpr) + gti * (-dt2 * xpi);
+      grad_A[off] = ga;
+      grad_G[off] = gg;
+      grad_step[off] = gs * mask;
+      grad_bu[2 * off] = gtr * dt2;
+      grad_bu[2 * off + 1] = gti * dt2;
+      /* carry to t - 1 */
+      gwnr = gtr * alpha; gwni = gti * alpha;
+      gxnr = gxr + gtr * (-dt2 * a); gxni = gxi + gti * (-dt2 * a);
+    }
+  }
+}

@@ -14,9 +14,9 @@ CPU entry points, e.g. the reference's own ``ossm._kernels`` build); without a
 delegate a CPU call raises RuntimeError, which the reference bridges treat as
 "kernel unavailable".
 
-Export-only names with no HIP implementation in this build (sdlinoss_*,
-lru_scan, s5_scan, linear_rnn_scan) exist so attribute lookups behave like the
-reference's module; on device tensors they raise RuntimeError.
+Export-only names with no HIP implementation in this build (lru_scan, s5_scan,
+linear_rnn_scan) exist so attribute lookups behave like the reference's
+module; on device tensors they raise RuntimeError.
 """
 
 from __future__ import annotations
@@ -401,6 +401,124 @@ def selective_scan_backward(grad_output, inputs, dt, A, B, C, gate=None):
     return selective_scan_cuda_backward(grad_output, inputs, dt, A, B, C, gate, chunks, raw, 16)
 
 
+# ---------------------------------------------------- selective D-LinOSS
+def _sdl_param(param: torch.Tensor, name: str, length: int, batch: int, ssm: int):
+    """normalize_param_view_cpu (sdlinoss_cpu_utils.h:11-72): the (La, Ba, M)
+    view of a parameter given as (M,), (L,M), (B,M) or (L|1, B|1, M);
+    returns the contiguous float32 view and (La, Ba)."""
+    shape = list(param.shape)
+    _check(1 <= param.dim() <= 3,
+           f"{name} must be shaped as (M,), (L,M), (B,M), or (L,B,M); got {shape}")
+    _check(param.size(-1) == ssm,
+           f"{name} must have size {ssm} along the last dimension; got {shape}")
+    if param.dim() == 1:
+        la, ba = 1, 1
+    elif param.dim() == 2:
+        if param.size(0) == length:
+            la, ba = length, 1
+        elif param.size(0) == batch:
+            la, ba = 1, batch
+        else:
+            raise RuntimeError(f"{name} must be shaped as (M,), (L,M), (B,M), or (L,B,M); got {shape}")
+    else:
+        _check(param.size(0) in (length, 1) and param.size(1) in (batch, 1),
+               f"{name} must have shape (L,B,M) with optional singleton L/B axes; got {shape}")
+        la, ba = param.size(0), param.size(1)
+    _check(param.dtype == torch.float32,
+           f"{name} must be float32 on the device (the MI355X kernels compute complex64 only)")
+    return param.contiguous(), la, ba
+
+
+def _sdl_forward(variant: str, A, G, step, bu):
+    # sdlinoss_imex1.cpp:317-355 (and siblings)
+    _check(bu.dim() == 3, "bu must have shape (length, batch, ssm_size)")
+    _check(A.device == bu.device and G.device == bu.device and step.device == bu.device,
+           "All tensors must live on the same device")
+    if not bu.is_cuda:
+        return _delegate(f"sdlinoss_{variant}_forward", A, G, step, bu)
+    length, batch, ssm = bu.shape
+    out = torch.empty((length, batch, ssm, 2), dtype=bu.dtype, device=bu.device)
+    if length == 0:
+        return out
+    _check(bu.dtype == torch.complex64,
+           f"sdlinoss_{variant}_forward: the MI355X kernels compute complex64 only")
+    views = [_sdl_param(p, n, length, batch, ssm) for p, n in ((A, "A"), (G, "G"), (step, "step"))]
+    b = bu.contiguous()
+    args = []
+    for v, la, ba in views:
+        args += [v.data_ptr(), la, ba]
+    with torch.cuda.device(bu.device):
+        _lib.check(_lib.load().ossm_sdlinoss_forward(
+            _VARIANT_CODE[variant], *args, b.data_ptr(), out.data_ptr(), length, batch, ssm,
+            _lib.stream_of(b)))
+    return out
+
+
+def _sdl_backward(variant: str, A, G, step, bu, states, grad_output):
+    # sdlinoss_imex1.cpp:357-425 (and siblings); returns [grad_A, grad_G, grad_step, grad_bu]
+    _check(states.dim() == 4 and states.size(3) == 2,
+           "states must have shape (length, batch, ssm_size, 2)")
+    _check(bu.dim() == 3, "bu must have shape (length, batch, ssm_size)")
+    _check(grad_output.shape == bu.shape, "grad_output must match bu shape")
+    if not bu.is_cuda:
+        return _delegate(f"sdlinoss_{variant}_backward", A, G, step, bu, states, grad_output)
+    _on_device(A, G, step, bu, states, grad_output)
+    _check(states.is_contiguous() and grad_output.is_contiguous(),
+           "states and grad_output must be contiguous on CUDA")
+    length, batch, ssm = bu.shape
+    grads = [torch.empty(p.shape, dtype=p.dtype, device=p.device) for p in (A, G, step)]
+    grad_bu = torch.empty_like(bu)
+    if length == 0 or batch == 0 or ssm == 0:
+        return [g.zero_() for g in grads] + [grad_bu]
+    _check(bu.dtype == torch.complex64,
+           f"sdlinoss_{variant}_backward: the MI355X kernels compute complex64 only")
+    _check(tuple(states.shape) == (length, batch, ssm, 2),
+           "states must have shape (length, batch, ssm_size, 2)")
+    views = [_sdl_param(p, n, length, batch, ssm) for p, n in ((A, "A"), (G, "G"), (step, "step"))]
+    b = bu.contiguous()
+    args = []
+    for v, la, ba in views:
+        args += [v.data_ptr(), la, ba]
+    with torch.cuda.device(bu.device):
+        _lib.check(_lib.load().ossm_sdlinoss_backward(
+            _VARIANT_CODE[variant], *args, b.data_ptr(), states.data_ptr(), grad_output.data_ptr(),
+            grads[0].data_ptr(), grads[1].data_ptr(), grads[2].data_ptr(), grad_bu.data_ptr(),
+            length, batch, ssm, _lib.stream_of(b)))
+    return grads + [grad_bu]
+
+
+def sdlinoss_imex1_forward(A, G, step, bu):
+    return _sdl_forward("imex1", A, G, step, bu)
+
+
+def sdlinoss_imex1_backward(A, G, step, bu, states, grad_output):
+    return _sdl_backward("imex1", A, G, step, bu, states, grad_output)
+
+
+def sdlinoss_imex2_forward(A, G, step, bu):
+    return _sdl_forward("imex2", A, G, step, bu)
+
+
+def sdlinoss_imex2_backward(A, G, step, bu, states, grad_output):
+    return _sdl_backward("imex2", A, G, step, bu, states, grad_output)
+
+
+def sdlinoss_im_forward(A, G, step, bu):
+    return _sdl_forward("im", A, G, step, bu)
+
+
+def sdlinoss_im_backward(A, G, step, bu, states, grad_output):
+    return _sdl_backward("im", A, G, step, bu, states, grad_output)
+
+
+def sdlinoss_ex_forward(A, G, step, bu):
+    return _sdl_forward("ex", A, G, step, bu)
+
+
+def sdlinoss_ex_backward(A, G, step, bu, states, grad_output):
+    return _sdl_backward("ex", A, G, step, bu, states, grad_output)
+
+
 # ------------------------------------------------------ export-only names
 def _export_only(name: str):
     def fn(*args, **kwargs):
@@ -414,14 +532,6 @@ def _export_only(name: str):
     return fn
 
 
-sdlinoss_imex1_forward = _export_only("sdlinoss_imex1_forward")
-sdlinoss_imex1_backward = _export_only("sdlinoss_imex1_backward")
-sdlinoss_imex2_forward = _export_only("sdlinoss_imex2_forward")
-sdlinoss_imex2_backward = _export_only("sdlinoss_imex2_backward")
-sdlinoss_im_forward = _export_only("sdlinoss_im_forward")
-sdlinoss_im_backward = _export_only("sdlinoss_im_backward")
-sdlinoss_ex_forward = _export_only("sdlinoss_ex_forward")
-sdlinoss_ex_backward = _export_only("sdlinoss_ex_backward")
 lru_scan = _export_only("lru_scan")
 s5_scan = _export_only("s5_scan")
 linear_rnn_scan = _export_only("linear_rnn_scan")

@@ -5,6 +5,8 @@ kernel bridges (the L2 layer above ``ossm._kernels``):
   autograd Function per variant — reference src/ossm/models/_dlinoss_scan.py:416-680.
   Forward saves ``(a, g, step, bu, states)`` and returns ``states[..., 1]``;
   backward passes ``grad_output.contiguous()`` (:461-498).
+* Selective D-LinOSS: ``run_sdlinoss`` and ``SdlinossFn``
+  (_sdlinoss_scan.py:286-452), same save/return semantics.
 * LinOSS: ``try_run_scan`` (_linoss_scan.py:44-63) plus ``LinossScanFn`` whose
   backward is the native ``linoss_scan_backward`` instead of the reference's
   Python loop (models/linoss.py:83-151).
@@ -31,6 +33,7 @@ from . import _kernels
 
 __all__ = [
     "has_kernels", "extension_error", "run_dlinoss", "run_dlinoss_imex1", "DlinossFn",
+    "run_sdlinoss", "SdlinossFn",
     "try_run_scan", "LinossScanFn", "try_selective_scan", "SelectiveScanFn",
 ]
 
@@ -92,6 +95,45 @@ def run_dlinoss(variant: str, a_diag: Tensor, g_diag: Tensor, step: Tensor, bu: 
 def run_dlinoss_imex1(a_diag: Tensor, g_diag: Tensor, step: Tensor, bu: Tensor) -> Tensor:
     """reference run_dlinoss_imex1 (_dlinoss_scan.py:683-686)."""
     return run_dlinoss("imex1", a_diag, g_diag, step, bu)
+
+
+# -------------------------------------------------------- selective D-LinOSS
+class SdlinossFn(torch.autograd.Function):
+    """Autograd bridge of one selective D-LinOSS variant (reference
+    _SdlinossImex1Fn and siblings, _sdlinoss_scan.py:286-379): the forward saves
+    ``(A, G, step, bu, states)`` and returns ``states[..., 1]``; the backward
+    passes ``grad_output.contiguous()``."""
+
+    @staticmethod
+    def forward(ctx, variant: str, A: Tensor, G: Tensor, step: Tensor,
+                bu: Tensor) -> Tensor:  # type: ignore[override]
+        states = getattr(_kernels, f"sdlinoss_{variant}_forward")(A, G, step, bu)
+        ctx.variant = variant
+        ctx.save_for_backward(A, G, step, bu, states)
+        return states[..., 1]
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):  # type: ignore[override]
+        A, G, step, bu, states = ctx.saved_tensors
+        grad_A, grad_G, grad_step, grad_bu = getattr(_kernels, f"sdlinoss_{ctx.variant}_backward")(
+            A, G, step, bu, states, grad_output.contiguous())
+        return None, grad_A, grad_G, grad_step, grad_bu
+
+
+def run_sdlinoss(variant: str, a_diag: Tensor, g_diag: Tensor, step: Tensor, bu: Tensor) -> Tensor:
+    """x = states[..., 1] of the selective D-LinOSS recurrence (reference
+    run_sdlinoss, _sdlinoss_scan.py:382-452).  bu is [L, B, M] complex64 on the
+    device; A, G, step are float32 shaped (M,), (L, M), (B, M) or (L|1, B|1, M);
+    their gradients come back in the same shapes (summed over broadcast axes)."""
+    variant = variant.lower()
+    if variant not in SUPPORTED_VARIANTS:
+        raise ValueError(
+            f"Unsupported variant '{variant}'. Expected one of {', '.join(SUPPORTED_VARIANTS)}.")
+    if bu.dim() != 3:
+        raise ValueError("bu must be (length, batch, ssm_size) complex.")
+    if bu.size(0) == 0:
+        return bu.new_empty((0, bu.size(1), bu.size(2)))
+    return SdlinossFn.apply(variant, a_diag, g_diag, step, bu)
 
 
 # -------------------------------------------------------------------- LinOSS

@@ -23,7 +23,7 @@ LIBDIR = PKG / "_lib"
 OBJDIR = PKG / "_build"
 LIB = LIBDIR / "libossm_scan.so"
 
-SOURCES = ["runtime.cpp", "oscillator_scan.hip", "selective_scan.hip"]
+SOURCES = ["runtime.cpp", "oscillator_scan.hip", "selective_scan.hip", "sdlinoss_scan.hip"]
 ARCH = "gfx950"
 
 

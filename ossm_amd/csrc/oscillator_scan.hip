@@ -27,7 +27,7 @@
 //   <mu_i, s_j,t-1> and <mu_i, bu_t> go to a partials buffer; two small
 //   kernels add them over time chunks and batch rows per oscillator (a
 //   column reduction) and apply each variant's chain rule to (a, g, dt).  Every sum
-//   runs in a fixed order in fp64, so the gradients are deterministic.  (A
+//   runs in a fixed order in fp64, with no atomics.  (A
 //   last-workgroup-done reduction inside the scan kernel was measured 3x
 //   slower: each agent-scope release fence writes back the XCD's L2.)
 
@@ -690,7 +690,7 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
 //           through LDS -> colsum[g][j][p];
 //   pass 2: one wave per oscillator, lane g holding row group g, adds them
 //           by a butterfly over the wave, then the chain rule.
-// Fixed order everywhere: deterministic.
+// Fixed order everywhere (no atomics).
 constexpr int kRowGroups = kWave;
 constexpr int kColsumRows = 4;  // rows per lane per round (independent loads)
 

@@ -1,0 +1,799 @@
+// Selective D-LinOSS scans on gfx950: the D-LinOSS recurrence with
+// per-step (time- and batch-varying) parameters, forward and backward, for
+// the four discretisations imex1, imex2, im and ex.
+//
+// Recurrence (sdlinoss_<v>.cpp forward kernels; the bridge's fallback
+// restates it in _sdlinoss_scan.py:150-197).  Per step, with
+// dt = clamp(step, 1e-6, 1):
+//   comb = -a x + bu,  tmpw = alpha w + dt^2 comb,  w' = tmpw / S,  x' = x + w'
+//   imex1: alpha = 1,         S = max(1 + dt g, 1e-6)
+//   imex2: alpha = 1 - dt g,  S = max(1 + dt^2 a, 1e-6)
+//   im:    alpha = 1,         S = max(1 + dt g + dt^2 a, 1e-6)
+//   ex:    alpha = 1 - dt g,  S = 1
+// i.e. (w, x) -> M_t (w, x) + f_t bu with the real 2x2
+//   M_t = [[c0, c1], [c0, 1 + c1]],  f_t = (c2, c2),
+//   c0 = alpha / S,  c1 = -dt^2 a / S,  c2 = dt^2 / S.
+//
+// Parameters a, g, step are [La, Ba, M] with La in {1, L} and Ba in {1, B}
+// (broadcast over time and/or batch, as normalize_param_view_cpu allows,
+// sdlinoss_cpu_utils.h:11-72).  bu is [L, B, M] complex64 and the states
+// [L, B, M, 2] complex64 (component 0 = w, 1 = x), channel ch = b M + m
+// contiguous: one wave = 64 consecutive channels.
+//
+// Both directions are the chunked scan of the oscillator kernels with the
+// chunk transition no longer a matrix power: each lane composes its
+// sub-chunk's matrices while it scans, workgroups combine (matrix, vector)
+// aggregates through LDS, and the look-back records carry both.
+//
+// Backward: the adjoint lambda_t = (0, g_t) + M_{t+1}^T lambda_{t+1} in
+// reverse time; the states s_{t-1} are rebuilt from states[t0 - 1] at each
+// sub-chunk start into LDS; the per-step gradients of a, g and step follow
+// the reference's chain rule (sdlinoss_<v>.cpp backward kernels) and are
+// written per element; parameters broadcast over time or batch are then
+// summed over those axes by a two-pass column reduction in a fixed order.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cstdint>
+#include <cstdlib>
+#include <cstdio>
+#include <string>
+#include <type_traits>
+
+#include "../../include/ossm_scan.h"
+#include "runtime.hpp"
+#include "scan_device.hpp"
+
+namespace ossm {
+namespace {
+
+constexpr float kDtMin = 1e-6f;
+constexpr float kDtMax = 1.0f;
+constexpr float kClampMin = 1e-6f;
+
+// One parameter tensor [La, Ba, M]: element (t, ch) lives at
+// p[t * t_stride + (by_channel ? ch : ch % M)].
+struct ParamView {
+  const float* p;
+  long long t_stride;  // Ba * M, or 0 when broadcast over time
+  int by_channel;      // 1: Ba == B (index by channel); 0: broadcast over batch (index by m)
+};
+
+struct SdlParams {
+  ParamView a, g, s;
+  int M;
+};
+
+// ---- per-step coefficients -------------------------------------------------
+template <int V>
+struct SdlCoef {
+  float c0, c1, c2;
+};
+
+template <int V>
+__device__ __forceinline__ float sdl_alpha(float dt, float g) {
+  if constexpr (V == OSSM_DLINOSS_IMEX2 || V == OSSM_DLINOSS_EX) return 1.f - dt * g;
+  else return 1.f;
+}
+
+template <int V>
+__device__ __forceinline__ float sdl_s_raw(float dt, float g, float a) {
+  if constexpr (V == OSSM_DLINOSS_IMEX1) return 1.f + dt * g;
+  else if constexpr (V == OSSM_DLINOSS_IMEX2) return 1.f + dt * dt * a;
+  else if constexpr (V == OSSM_DLINOSS_IM) return 1.f + dt * g + dt * dt * a;
+  else return 1.f;
+}
+
+__device__ __forceinline__ float sdl_dt(float step_raw) {
+  return fminf(fmaxf(step_raw, kDtMin), kDtMax);
+}
+
+// 1 / S (exactly 1 for ex, which has no implicit part)
+template <int V>
+__device__ __forceinline__ float sdl_inv(float dt, float g, float a) {
+  if constexpr (V == OSSM_DLINOSS_EX) return 1.f;
+  else return 1.f / fmaxf(sdl_s_raw<V>(dt, g, a), kClampMin);
+}
+
+template <int V>
+__device__ __forceinline__ SdlCoef<V> sdl_coef(float a, float g, float step_raw) {
+  const float dt = sdl_dt(step_raw);
+  const float dt2 = dt * dt;
+  const float inv = sdl_inv<V>(dt, g, a);
+  return {sdl_alpha<V>(dt, g) * inv, -dt2 * a * inv, dt2 * inv};
+}
+
+// (w, x) -> (c0 w + c1 x + c2 bu, x + w')
+template <int V>
+__device__ __forceinline__ float4 sdl_step(const SdlCoef<V>& k, float4 s, float2 bu) {
+  const float wr = fmaf(k.c0, s.x, fmaf(k.c1, s.z, k.c2 * bu.x));
+  const float wi = fmaf(k.c0, s.y, fmaf(k.c1, s.w, k.c2 * bu.y));
+  return make_float4(wr, wi, s.z + wr, s.w + wi);
+}
+
+// M_t * P for a 2x2 P (rows of M_t: (c0, c1), (c0, 1 + c1))
+template <int V>
+__device__ __forceinline__ RMat sdl_mat_left(const SdlCoef<V>& k, RMat p) {
+  const float a = fmaf(k.c0, p.a, k.c1 * p.c);
+  const float b = fmaf(k.c0, p.b, k.c1 * p.d);
+  return {a, b, a + p.c, b + p.d};
+}
+
+// M_t^T * P (rows of M_t^T: (c0, c0), (c1, 1 + c1))
+template <int V>
+__device__ __forceinline__ RMat sdl_matT_left(const SdlCoef<V>& k, RMat p) {
+  const float sa = p.a + p.c, sb = p.b + p.d;
+  return {k.c0 * sa, k.c0 * sb, fmaf(k.c1, sa, p.c), fmaf(k.c1, sb, p.d)};
+}
+
+// M_t^T applied to an adjoint (lw, lx): (c0 (lw + lx), lx + c1 (lw + lx))
+template <int V>
+__device__ __forceinline__ float4 sdl_matT_apply(const SdlCoef<V>& k, float4 l) {
+  const float sr = l.x + l.z, si = l.y + l.w;
+  return make_float4(k.c0 * sr, k.c0 * si, fmaf(k.c1, sr, l.z), fmaf(k.c1, si, l.w));
+}
+
+__device__ __forceinline__ float4 rmat_pack(RMat m) { return make_float4(m.a, m.b, m.c, m.d); }
+__device__ __forceinline__ RMat rmat_unpack(float4 v) { return {v.x, v.y, v.z, v.w}; }
+
+// ---- look-back with per-chunk matrices ---------------------------------------
+// Records per (chunk, channel): kind 0 = aggregate vector, 1 = inclusive
+// prefix, 2 = aggregate matrix; four tagged 64-bit words each (the protocol
+// of scan_device.hpp: a word written once per launch, valid when it carries
+// this launch's tag).
+constexpr int kTvKinds = 3;
+constexpr int kTvAgg = 0, kTvInc = 1, kTvMat = 2;
+
+__device__ __forceinline__ size_t tv_index(int chunk, int kind, int k, int nc, int ch) {
+  return ((size_t(chunk) * kTvKinds + kind) * 4 + k) * size_t(nc) + ch;
+}
+
+__device__ __forceinline__ void tv_publish(unsigned long long* rec, int chunk, int kind, int nc,
+                                           int ch, float4 v, unsigned int tag) {
+  const unsigned long long t = static_cast<unsigned long long>(tag) << 32;
+  const float vals[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    __hip_atomic_store(rec + tv_index(chunk, kind, k, nc, ch), t | __float_as_uint(vals[k]),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void tv_fetch(const unsigned long long* rec, int chunk, int kind, int nc,
+                                         int ch, unsigned long long (&w)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    w[k] = __hip_atomic_load(rec + tv_index(chunk, kind, k, nc, ch), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Carry into chunk c for one channel, walking predecessors c - dir, ...:
+// acc + P * (inclusive of j), where each aggregate (E_j, K_j) passed over
+// adds P E_j to acc and turns P into P K_j.  Bounded spin as in lookback().
+__device__ float4 lookback_tv(unsigned long long* rec, int c, int dir, int n_chunks, int nc,
+                              int ch, const LaunchSync& sync) {
+  float4 acc = f4zero();
+  RMat P = {1.f, 0.f, 0.f, 1.f};
+  int j = c - dir;
+  uint32_t spins = 0;
+  while (j >= 0 && j < n_chunks) {
+    unsigned long long wi[4], wa[4], wm[4];
+    tv_fetch(rec, j, kTvInc, nc, ch, wi);
+    tv_fetch(rec, j, kTvAgg, nc, ch, wa);
+    tv_fetch(rec, j, kTvMat, nc, ch, wm);
+    float4 v, e, km;
+    if (rec_decode(wi, sync.tag, &v)) return f4add(acc, mat_apply(P, v));
+    const bool ea = rec_decode(wa, sync.tag, &e);
+    const bool em = rec_decode(wm, sync.tag, &km);
+    if (ea && em) {
+      acc = f4add(acc, mat_apply(P, e));
+      P = mat_mul(P, rmat_unpack(km));
+      j -= dir;
+      continue;
+    }
+    if (++spins > kSpinLimit) {
+      __hip_atomic_fetch_or(sync.err, kErrSpinTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return acc;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return acc;
+}
+
+// ---- addressing ---------------------------------------------------------------
+template <class E>
+__device__ __forceinline__ E* row_of(E* base, long long t, int nc, int g) {
+  return base + static_cast<size_t>(t) * nc + static_cast<size_t>(g) * kWave;
+}
+
+// Per-lane indices of one workgroup's channel group: lanes past the last
+// channel are clamped onto it (their loads stay in bounds; nothing of theirs
+// is stored).
+struct LaneIdx {
+  unsigned lc;  // lane offset within the group, clamped
+  int pch;      // index of the lane's channel within a parameter row of B*M
+  int pm;       // index of the lane's oscillator m within a parameter row of M
+};
+
+__device__ __forceinline__ LaneIdx lane_idx(int g, int nc, int M) {
+  LaneIdx r;
+  r.lc = static_cast<unsigned>(min(static_cast<int>(threadIdx.x & (kWave - 1)), nc - 1 - g * kWave));
+  r.pch = g * kWave + static_cast<int>(r.lc);
+  r.pm = r.pch % M;
+  return r;
+}
+
+__device__ __forceinline__ float param_at(const ParamView& v, long long t, const LaneIdx& li) {
+  return v.p[static_cast<size_t>(t * v.t_stride) + (v.by_channel ? li.pch : li.pm)];
+}
+
+// ============================================================================
+// Forward
+// ============================================================================
+// One workgroup = one time chunk of W*T steps for 64 channels; wave w owns
+// steps [t0, t0 + T).  Workgroups take chunks first-first in ticket order.
+template <int V, int T, int W>
+__global__ __launch_bounds__(W * kWave) void sdl_forward_kernel(
+    SdlParams prm, const float2* __restrict__ bu, float4* __restrict__ out, int L, int nc,
+    int n_groups, int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
+  __shared__ float4 s_e[W][kWave];
+  __shared__ float4 s_m[W][kWave];
+  __shared__ float4 s_carry[kWave];
+  __shared__ int s_ticket;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = wave_id();
+  const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
+  if (ticket < 0) return;
+  const int c = ticket / n_groups;
+  const int g = ticket - c * n_groups;
+  const int ch = g * kWave + lane;
+  const bool active = ch < nc;
+  const long long t0 = static_cast<long long>(c) * (T * W) + static_cast<long long>(w) * T;
+  const LaneIdx li = lane_idx(g, nc, prm.M);
+
+  // loads (clamped rows): parameters, then bu
+  float pa[T], pg[T], ps[T];
+  float2 x[T];
+#pragma unroll
+  for (int i = 0; i < T; ++i) {
+    const long long t = min(t0 + i, static_cast<long long>(L - 1));
+    pa[i] = param_at(prm.a, t, li);
+    pg[i] = param_at(prm.g, t, li);
+    ps[i] = param_at(prm.s, t, li);
+  }
+#pragma unroll
+  for (int i = 0; i < T; ++i) x[i] = row_of(bu, min(t0 + i, static_cast<long long>(L - 1)), nc, g)[li.lc];
+
+  // 1. sub-chunk aggregate from a zero state, composing the matrices
+  const bool full = t0 + T <= L;
+  SdlCoef<V> k[T];
+  float4 e = f4zero();
+  RMat Mc = {1.f, 0.f, 0.f, 1.f};
+#pragma unroll
+  for (int i = 0; i < T; ++i) {
+    k[i] = sdl_coef<V>(pa[i], pg[i], ps[i]);
+    if (full || t0 + i < L) {
+      e = sdl_step<V>(k[i], e, x[i]);
+      Mc = sdl_mat_left<V>(k[i], Mc);
+    }
+  }
+  s_e[w][lane] = e;
+  s_m[w][lane] = rmat_pack(Mc);
+  __syncthreads();
+
+  // 2. chunk aggregate, look-back (wave 0), aggregate published by wave 1
+  constexpr int kPub = W > 1 ? 1 : 0;
+  if (w == 0 || w == kPub) {
+    float4 E = f4zero();
+    RMat Mch = {1.f, 0.f, 0.f, 1.f};
+#pragma unroll
+    for (int v = 0; v < W; ++v) {
+      const RMat Mv = rmat_unpack(s_m[v][lane]);
+      E = f4add(mat_apply(Mv, E), s_e[v][lane]);
+      Mch = mat_mul(Mv, Mch);
+    }
+    const bool scan = active && n_chunks > 1;
+    if (w == kPub && scan && c > 0) {
+      tv_publish(rec, c, kTvAgg, nc, ch, E, sync.tag);
+      tv_publish(rec, c, kTvMat, nc, ch, rmat_pack(Mch), sync.tag);
+    }
+    if (w == 0) {
+      float4 carry = f4zero();
+      if (scan) {
+        if (c == 0) {
+          tv_publish(rec, c, kTvInc, nc, ch, E, sync.tag);
+        } else {
+          carry = lookback_tv(rec, c, +1, n_chunks, nc, ch, sync);
+          if (c + 1 < n_chunks)
+            tv_publish(rec, c, kTvInc, nc, ch, f4add(mat_apply(Mch, carry), E), sync.tag);
+        }
+      }
+      s_carry[lane] = carry;
+    }
+  }
+  __syncthreads();
+
+  // 3. own carry through the earlier waves, then re-run and store
+  float4 s = s_carry[lane];
+  for (int v = 0; v < w; ++v) s = f4add(mat_apply(rmat_unpack(s_m[v][lane]), s), s_e[v][lane]);
+  if (active) {
+    if (full) {
+#pragma unroll
+      for (int i = 0; i < T; ++i) {
+        s = sdl_step<V>(k[i], s, x[i]);
+        row_of(out, t0 + i, nc, g)[lane] = s;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < T; ++i) {
+        if (t0 + i < L) {
+          s = sdl_step<V>(k[i], s, x[i]);
+          row_of(out, t0 + i, nc, g)[lane] = s;
+        }
+      }
+    }
+  }
+}
+
+// ============================================================================
+// Backward
+// ============================================================================
+// Per-step gradients, given the adjoint lam = (lw, lx) of the new state, the
+// previous state sp = (w_prev, x_prev), bu and the raw parameters; returns
+// the adjoint carried to the previous step (M_t^T lam).  The arithmetic
+// follows the reference backward kernels: sdlinoss_imex1.cpp:186-220,
+// sdlinoss_imex2.cpp:178-221, sdlinoss_im.cpp:176-225, sdlinoss_ex.cpp:163-189.
+template <int V>
+__device__ __forceinline__ float4 sdl_grad_step(float a, float g, float step_raw, float4 sp,
+                                                float2 bu, float4 lam, float2& gbu, float& ga,
+                                                float& gg, float& gs) {
+  const float dt = sdl_dt(step_raw);
+  const float dt2 = dt * dt;
+  const float alpha = sdl_alpha<V>(dt, g);
+  // gradient w.r.t. the new w, through both components (x' = x + w')
+  const float gwr = lam.x + lam.z, gwi = lam.y + lam.w;
+  const float combr = fmaf(-a, sp.z, bu.x), combi = fmaf(-a, sp.w, bu.y);
+  float gdt = 0.f, gA = 0.f, gG = 0.f;
+  float gtr = gwr, gti = gwi;  // gradient w.r.t. tmpw
+  if constexpr (V != OSSM_DLINOSS_EX) {
+    const float s_raw = sdl_s_raw<V>(dt, g, a);
+    const float inv = 1.f / fmaxf(s_raw, kClampMin);
+    const float tmpr = fmaf(alpha, sp.x, dt2 * combr), tmpi = fmaf(alpha, sp.y, dt2 * combi);
+    gtr = gwr * inv;
+    gti = gwi * inv;
+    const float gS = -(gwr * tmpr + gwi * tmpi) * (inv * inv) * (s_raw > kClampMin ? 1.f : 0.f);
+    if constexpr (V == OSSM_DLINOSS_IMEX1) {
+      gdt = gS * g;
+      gG = gS * dt;
+    } else if constexpr (V == OSSM_DLINOSS_IMEX2) {
+      gdt = gS * (2.f * dt * a);
+      gA = gS * dt2;
+    } else {
+      gdt = gS * (g + 2.f * dt * a);
+      gA = gS * dt2;
+      gG = gS * dt;
+    }
+  }
+  // tmpw = alpha w_prev + dt^2 (-a x_prev + bu)
+  if constexpr (V == OSSM_DLINOSS_IMEX2 || V == OSSM_DLINOSS_EX) {
+    gdt += gtr * (-g * sp.x + 2.f * dt * combr) + gti * (-g * sp.y + 2.f * dt * combi);
+    gG += gtr * (-dt * sp.x) + gti * (-dt * sp.y);
+  } else {
+    gdt += gtr * (2.f * dt * combr) + gti * (2.f * dt * combi);
+  }
+  gA += gtr * (-dt2 * sp.z) + gti * (-dt2 * sp.w);
+  gbu = make_float2(gtr * dt2, gti * dt2);
+  ga = gA;
+  gg = gG;
+  gs = (step_raw > kDtMin && step_raw < kDtMax) ? gdt : 0.f;
+  // carry to the previous step: d/dw_prev = alpha gt, d/dx_prev = lx - dt^2 a gt
+  return make_float4(alpha * gtr, alpha * gti, fmaf(-dt2 * a, gtr, lam.z), fmaf(-dt2 * a, gti, lam.w));
+}
+
+// Destinations of the per-element parameter gradients ([L, B*M] each).
+struct SdlGradOut {
+  float* a;
+  float* g;
+  float* s;
+};
+
+template <int V, int T, int W>
+__global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
+    SdlParams prm, const float2* __restrict__ bu, const float4* states,
+    const float2* __restrict__ gout, float2* __restrict__ gin, SdlGradOut go_prm, int L, int nc,
+    int n_groups, int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
+  __shared__ float4 s_e[W][kWave];
+  __shared__ float4 s_k[W][kWave];
+  __shared__ float4 s_carry[kWave];
+  __shared__ float4 s_sp[W][T][kWave];  // recomputed s_{t-1}
+  __shared__ int s_ticket;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = wave_id();
+  const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
+  if (ticket < 0) return;
+  // chunks are handed out last-first
+  const int cr = ticket / n_groups;
+  const int g = ticket - cr * n_groups;
+  const int c = n_chunks - 1 - cr;
+  const int ch = g * kWave + lane;
+  const bool active = ch < nc;
+  const long long t0 = static_cast<long long>(c) * (T * W) + static_cast<long long>(w) * T;
+  const LaneIdx li = lane_idx(g, nc, prm.M);
+
+  // loads in order of use: checkpoint, parameters and bu (forward
+  // recompute), upstream gradient last step first (reverse sweep)
+  const float4 ck = row_of(states, max(min(t0 - 1, static_cast<long long>(L - 1)), 0ll), nc, g)[li.lc];
+  asm volatile("" ::: "memory");
+  float pa[T], pg[T], ps[T];
+  float2 x[T], go[T];
+#pragma unroll
+  for (int i = 0; i < T; ++i) {
+    const long long t = min(t0 + i, static_cast<long long>(L - 1));
+    pa[i] = param_at(prm.a, t, li);
+    pg[i] = param_at(prm.g, t, li);
+    ps[i] = param_at(prm.s, t, li);
+    x[i] = row_of(bu, t, nc, g)[li.lc];
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = T - 1; i >= 0; --i) go[i] = row_of(gout, min(t0 + i, static_cast<long long>(L - 1)), nc, g)[li.lc];
+
+  const bool full = t0 + T <= L;
+  auto live = [&](int i) { return full || t0 + i < L; };
+
+  // recompute s_{t-1} into LDS; reverse aggregate (e, K) of the sub-chunk
+  {
+    float4 s = t0 >= 1 ? ck : f4zero();
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      s_sp[w][i][lane] = s;
+      if (live(i)) s = sdl_step<V>(sdl_coef<V>(pa[i], pg[i], ps[i]), s, x[i]);
+    }
+  }
+  float4 e = f4zero();
+  RMat K = {1.f, 0.f, 0.f, 1.f};
+#pragma unroll
+  for (int i = T - 1; i >= 0; --i) {
+    if (live(i)) {
+      const SdlCoef<V> k = sdl_coef<V>(pa[i], pg[i], ps[i]);
+      e = sdl_matT_apply<V>(k, make_float4(e.x, e.y, e.z + go[i].x, e.w + go[i].y));
+      K = sdl_matT_left<V>(k, K);
+    }
+  }
+  s_e[w][lane] = e;
+  s_k[w][lane] = rmat_pack(K);
+  __syncthreads();
+
+  // chunk aggregate over waves W-1 .. 0; look-back over later chunks
+  constexpr int kPub = W > 1 ? 1 : 0;
+  if (w == 0 || w == kPub) {
+    float4 E = f4zero();
+    RMat Kch = {1.f, 0.f, 0.f, 1.f};
+#pragma unroll
+    for (int v = W - 1; v >= 0; --v) {
+      const RMat Kv = rmat_unpack(s_k[v][lane]);
+      E = f4add(mat_apply(Kv, E), s_e[v][lane]);
+      Kch = mat_mul(Kv, Kch);
+    }
+    const bool scan = active && n_chunks > 1;
+    if (w == kPub && scan && c < n_chunks - 1) {
+      tv_publish(rec, c, kTvAgg, nc, ch, E, sync.tag);
+      tv_publish(rec, c, kTvMat, nc, ch, rmat_pack(Kch), sync.tag);
+    }
+    if (w == 0) {
+      float4 carry = f4zero();
+      if (scan) {
+        if (c == n_chunks - 1) {
+          tv_publish(rec, c, kTvInc, nc, ch, E, sync.tag);
+        } else {
+          carry = lookback_tv(rec, c, -1, n_chunks, nc, ch, sync);
+          if (c > 0) tv_publish(rec, c, kTvInc, nc, ch, f4add(mat_apply(Kch, carry), E), sync.tag);
+        }
+      }
+      s_carry[lane] = carry;
+    }
+  }
+  __syncthreads();
+
+  // the wave's carry: the chunk carry through the later waves' sub-chunks
+  float4 rho = s_carry[lane];
+  for (int v = W - 1; v > w; --v) rho = f4add(mat_apply(rmat_unpack(s_k[v][lane]), rho), s_e[v][lane]);
+
+  // final reverse pass: per-step gradients
+  if (active) {
+#pragma unroll
+    for (int i = T - 1; i >= 0; --i) {
+      if (live(i)) {
+        const long long t = t0 + i;
+        const float4 lam = make_float4(rho.x, rho.y, rho.z + go[i].x, rho.w + go[i].y);
+        float2 gbu;
+        float ga, gg, gs;
+        rho = sdl_grad_step<V>(pa[i], pg[i], ps[i], s_sp[w][i][lane], x[i], lam, gbu, ga, gg, gs);
+        row_of(gin, t, nc, g)[lane] = gbu;
+        row_of(go_prm.a, t, nc, g)[lane] = ga;
+        row_of(go_prm.g, t, nc, g)[lane] = gg;
+        row_of(go_prm.s, t, nc, g)[lane] = gs;
+      }
+    }
+  }
+}
+
+// ============================================================================
+// Sums over broadcast axes: out[n][c] = sum_r in[n][r][c], in fp64, fixed
+// order.  Pass 1: block (64-column tile, row group q) sums rows
+// r = q*4 + wave + k*4G; pass 2 adds the G row groups.
+// ============================================================================
+constexpr int kSumGroups = 32;
+
+// grid: x = n * col_tiles + column tile, y = row group q
+__global__ __launch_bounds__(256) void sdl_colsum_pass1(const float* __restrict__ in,
+                                                        double* __restrict__ part, int R, int C,
+                                                        int col_tiles) {
+  __shared__ double s_red[4][kWave];
+  const int lane = threadIdx.x & (kWave - 1), w = wave_id();
+  const int n = blockIdx.x / col_tiles;
+  const int col = (blockIdx.x - n * col_tiles) * kWave + lane;
+  const int q = blockIdx.y;
+  const int cc = min(col, C - 1);
+  const float* src = in + static_cast<size_t>(n) * R * C + cc;
+  double acc = 0.0;
+  constexpr int kStride = kSumGroups * 4;
+  for (int r0 = q * 4 + w; r0 < R; r0 += kStride * 4) {
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = src[static_cast<size_t>(min(r0 + u * kStride, R - 1)) * C];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (r0 + u * kStride < R) acc += static_cast<double>(v[u]);
+  }
+  s_red[w][lane] = acc;
+  __syncthreads();
+  if (w == 0 && col < C)
+    part[(static_cast<size_t>(n) * kSumGroups + q) * C + col] =
+        ((s_red[0][lane] + s_red[1][lane]) + s_red[2][lane]) + s_red[3][lane];
+}
+
+__global__ __launch_bounds__(256) void sdl_colsum_pass2(const double* __restrict__ part,
+                                                        float* __restrict__ out, int C, int nb) {
+  const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<long long>(nb) * C) return;
+  const int n = static_cast<int>(i / C), col = static_cast<int>(i - static_cast<long long>(n) * C);
+  double s = 0.0;
+#pragma unroll 8
+  for (int q = 0; q < kSumGroups; ++q) s += part[(static_cast<size_t>(n) * kSumGroups + q) * C + col];
+  out[i] = static_cast<float>(s);
+}
+
+__global__ void sdl_zero_kernel(float* __restrict__ p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
+// ============================================================================
+// Host side
+// ============================================================================
+struct ParamShape {
+  const float* p;
+  int64_t la, ba;  // leading dims of [La, Ba, M]
+};
+
+int check_param(const ParamShape& s, int64_t L, int64_t B, const char* what, const char* name) {
+  if (s.p == nullptr) return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": null " + name);
+  if (!(s.la == 1 || s.la == L) || !(s.ba == 1 || s.ba == B))
+    return set_error(OSSM_ERR_INVALID_ARGUMENT,
+                     std::string(name) + " must have shape (L,B,M) with optional singleton L/B axes");
+  return OSSM_OK;
+}
+
+ParamView view_of(const ParamShape& s, int64_t L, int64_t B, int64_t M) {
+  ParamView v;
+  v.p = s.p;
+  v.t_stride = (s.la == 1 && L > 1) ? 0 : s.ba * M;
+  v.by_channel = (s.ba == B) ? 1 : 0;
+  return v;
+}
+
+// Whether a parameter's gradient needs a sum over broadcast axes.
+bool needs_sum(const ParamShape& s, int64_t L, int64_t B) {
+  return (s.la == 1 && L > 1) || (s.ba == 1 && B > 1);
+}
+
+int launch_colsum(const float* in, float* out, double* part, int64_t nb, int64_t R, int64_t C,
+                  hipStream_t stream) {
+  const int64_t col_tiles = (C + kWave - 1) / kWave;
+  if (nb * col_tiles > INT_MAX) return set_error(OSSM_ERR_UNSUPPORTED, "gradient reduction too large");
+  const dim3 g1(static_cast<unsigned>(nb * col_tiles), kSumGroups);
+  hipLaunchKernelGGL(sdl_colsum_pass1, g1, dim3(256), 0, stream, in, part, static_cast<int>(R),
+                     static_cast<int>(C), static_cast<int>(col_tiles));
+  if (int rc = launch_check("sdl_colsum_pass1")) return rc;
+  const int64_t n_out = nb * C;
+  hipLaunchKernelGGL(sdl_colsum_pass2, dim3(static_cast<unsigned>((n_out + 255) / 256)), dim3(256),
+                     0, stream, part, out, static_cast<int>(C), static_cast<int>(nb));
+  return launch_check("sdl_colsum_pass2");
+}
+
+// Sums a per-element gradient [L, B, M] over the broadcast axes of `s` into
+// `out` (shape [La, Ba, M]).
+int reduce_grad(const float* full, float* out, const ParamShape& s, int64_t L, int64_t B, int64_t M,
+                double* part, hipStream_t stream) {
+  const bool rt = s.la == 1 && L > 1, rb = s.ba == 1 && B > 1;
+  if (rt && rb) return launch_colsum(full, out, part, 1, L * B, M, stream);
+  if (rt) return launch_colsum(full, out, part, 1, L, B * M, stream);
+  return launch_colsum(full, out, part, L, B, M, stream);  // rb only
+}
+
+int fill_zero_f(float* p, int64_t n, hipStream_t stream) {
+  if (n <= 0) return OSSM_OK;
+  hipLaunchKernelGGL(sdl_zero_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     stream, p, n);
+  return launch_check("sdl_zero_kernel");
+}
+
+constexpr int kFwdT = 8, kFwdW = 16;
+constexpr int kBwdT = 8, kBwdW = 8;
+
+template <int V>
+int sdl_forward_v(const SdlParams& prm, const void* bu, void* states, int64_t L, int64_t nc,
+                  hipStream_t stream) {
+  constexpr int T = kFwdT, W = kFwdW;
+  const int64_t n_chunks = (L + T * W - 1) / (T * W);
+  const int64_t n_groups = (nc + kWave - 1) / kWave;
+  if (n_chunks * n_groups > INT_MAX)
+    return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
+  const size_t rec_bytes = static_cast<size_t>(n_chunks) * kTvKinds * 4 * nc * sizeof(unsigned long long);
+  void* payload = nullptr;
+  LaunchSync sync{};
+  const int64_t total = n_chunks * n_groups;
+  if (int rc = acquire_scratch(stream, rec_bytes, total, &payload, &sync)) return rc;
+  hipLaunchKernelGGL((sdl_forward_kernel<V, T, W>), dim3(static_cast<unsigned>(total)),
+                     dim3(W * kWave), 0, stream, prm, static_cast<const float2*>(bu),
+                     static_cast<float4*>(states), static_cast<int>(L), static_cast<int>(nc),
+                     static_cast<int>(n_groups), static_cast<int>(n_chunks),
+                     static_cast<unsigned long long*>(payload), sync);
+  if (int rc = launch_check("sdl_forward_kernel")) {
+    release_unlaunched(stream, total);
+    return rc;
+  }
+  return OSSM_OK;
+}
+
+template <int V>
+int sdl_backward_v(const SdlParams& prm, const ParamShape (&shapes)[3], const void* bu,
+                   const void* states, const void* gout, float* const (&grads)[3], void* gbu,
+                   int64_t L, int64_t B, int64_t M, hipStream_t stream) {
+  constexpr int T = kBwdT, W = kBwdW;
+  const int64_t nc = B * M;
+  const int64_t n_chunks = (L + T * W - 1) / (T * W);
+  const int64_t n_groups = (nc + kWave - 1) / kWave;
+  if (n_chunks * n_groups > INT_MAX)
+    return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
+  // per-element gradient buffers for the broadcast parameters, then the
+  // column-sum partials
+  const size_t elems = static_cast<size_t>(L) * nc;
+  int n_full = 0;
+  for (const auto& s : shapes) n_full += needs_sum(s, L, B) ? 1 : 0;
+  const size_t full_bytes = (n_full * elems * sizeof(float) + 255) & ~static_cast<size_t>(255);
+  const int64_t max_c = nc;  // the widest reduction output (L x M <= L x B x M as well)
+  const size_t part_bytes = static_cast<size_t>(kSumGroups) * std::max<int64_t>(max_c, L * M) * sizeof(double);
+  float* buf[3] = {nullptr, nullptr, nullptr};
+  double* part = nullptr;
+  if (n_full > 0) {
+    void* ws = nullptr;
+    if (int rc = acquire_workspace(stream, full_bytes + part_bytes, &ws)) return rc;
+    float* next = static_cast<float*>(ws);
+    for (int p = 0; p < 3; ++p)
+      if (needs_sum(shapes[p], L, B)) {
+        buf[p] = next;
+        next += elems;
+      }
+    part = reinterpret_cast<double*>(static_cast<char*>(ws) + full_bytes);
+  }
+  SdlGradOut dst{buf[0] ? buf[0] : grads[0], buf[1] ? buf[1] : grads[1], buf[2] ? buf[2] : grads[2]};
+
+  const size_t rec_bytes = static_cast<size_t>(n_chunks) * kTvKinds * 4 * nc * sizeof(unsigned long long);
+  void* payload = nullptr;
+  LaunchSync sync{};
+  const int64_t total = n_chunks * n_groups;
+  if (int rc = acquire_scratch(stream, rec_bytes, total, &payload, &sync)) return rc;
+  hipLaunchKernelGGL((sdl_backward_kernel<V, T, W>), dim3(static_cast<unsigned>(total)),
+                     dim3(W * kWave), 0, stream, prm, static_cast<const float2*>(bu),
+                     static_cast<const float4*>(states), static_cast<const float2*>(gout),
+                     static_cast<float2*>(gbu), dst, static_cast<int>(L), static_cast<int>(nc),
+                     static_cast<int>(n_groups), static_cast<int>(n_chunks),
+                     static_cast<unsigned long long*>(payload), sync);
+  if (int rc = launch_check("sdl_backward_kernel")) {
+    release_unlaunched(stream, total);
+    return rc;
+  }
+  for (int p = 0; p < 3; ++p)
+    if (buf[p] != nullptr)
+      if (int rc = reduce_grad(buf[p], grads[p], shapes[p], L, B, M, part, stream)) return rc;
+  return OSSM_OK;
+}
+
+int check_sdl(int variant, int64_t L, int64_t B, int64_t M, const char* what) {
+  if (variant < 0 || variant > 3)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "Unknown selective D-LinOSS variant code");
+  if (L < 0 || B < 0 || M < 0)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": negative size");
+  if (L > INT_MAX / 2 || B * M > INT_MAX / 2 || L * B * M > (int64_t(1) << 40))
+    return set_error(OSSM_ERR_UNSUPPORTED, std::string(what) + ": size exceeds 32-bit indexing");
+  return OSSM_OK;
+}
+
+}  // namespace
+}  // namespace ossm
+
+using namespace ossm;
+
+extern "C" {
+
+int ossm_sdlinoss_forward(int variant, const float* A, int64_t a_len, int64_t a_batch,
+                          const float* G, int64_t g_len, int64_t g_batch, const float* step,
+                          int64_t s_len, int64_t s_batch, const void* bu, void* states,
+                          int64_t length, int64_t batch, int64_t ssm, ossm_stream_t stream_v) {
+  clear_error();
+  if (int rc = check_sdl(variant, length, batch, ssm, "sdlinoss_forward")) return rc;
+  if (length == 0 || batch == 0 || ssm == 0) return OSSM_OK;
+  const ParamShape shapes[3] = {{A, a_len, a_batch}, {G, g_len, g_batch}, {step, s_len, s_batch}};
+  const char* names[3] = {"A", "G", "step"};
+  for (int p = 0; p < 3; ++p)
+    if (int rc = check_param(shapes[p], length, batch, "sdlinoss_forward", names[p])) return rc;
+  if (!bu || !states) return set_error(OSSM_ERR_INVALID_ARGUMENT, "sdlinoss_forward: null pointer");
+  const SdlParams prm{view_of(shapes[0], length, batch, ssm), view_of(shapes[1], length, batch, ssm),
+                      view_of(shapes[2], length, batch, ssm), static_cast<int>(ssm)};
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  const int64_t nc = batch * ssm;
+  switch (variant) {
+    case OSSM_DLINOSS_IMEX1: return sdl_forward_v<OSSM_DLINOSS_IMEX1>(prm, bu, states, length, nc, stream);
+    case OSSM_DLINOSS_IMEX2: return sdl_forward_v<OSSM_DLINOSS_IMEX2>(prm, bu, states, length, nc, stream);
+    case OSSM_DLINOSS_IM: return sdl_forward_v<OSSM_DLINOSS_IM>(prm, bu, states, length, nc, stream);
+    default: return sdl_forward_v<OSSM_DLINOSS_EX>(prm, bu, states, length, nc, stream);
+  }
+}
+
+int ossm_sdlinoss_backward(int variant, const float* A, int64_t a_len, int64_t a_batch,
+                           const float* G, int64_t g_len, int64_t g_batch, const float* step,
+                           int64_t s_len, int64_t s_batch, const void* bu, const void* states,
+                           const void* grad_output, float* grad_A, float* grad_G,
+                           float* grad_step, void* grad_bu, int64_t length, int64_t batch,
+                           int64_t ssm, ossm_stream_t stream_v) {
+  clear_error();
+  if (int rc = check_sdl(variant, length, batch, ssm, "sdlinoss_backward")) return rc;
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  const ParamShape shapes[3] = {{A, a_len, a_batch}, {G, g_len, g_batch}, {step, s_len, s_batch}};
+  float* const grads[3] = {grad_A, grad_G, grad_step};
+  if (length == 0 || batch == 0 || ssm == 0) {
+    // nothing to scan: zero parameter gradients (the reference's zeros_like)
+    for (int p = 0; p < 3; ++p) {
+      if (grads[p] == nullptr) return set_error(OSSM_ERR_INVALID_ARGUMENT, "sdlinoss_backward: null pointer");
+      if (int rc = fill_zero_f(grads[p], shapes[p].la * shapes[p].ba * ssm, stream)) return rc;
+    }
+    return OSSM_OK;
+  }
+  const char* names[3] = {"A", "G", "step"};
+  for (int p = 0; p < 3; ++p)
+    if (int rc = check_param(shapes[p], length, batch, "sdlinoss_backward", names[p])) return rc;
+  if (!bu || !states || !grad_output || !grad_A || !grad_G || !grad_step || !grad_bu)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "sdlinoss_backward: null pointer");
+  const SdlParams prm{view_of(shapes[0], length, batch, ssm), view_of(shapes[1], length, batch, ssm),
+                      view_of(shapes[2], length, batch, ssm), static_cast<int>(ssm)};
+  switch (variant) {
+#define OSSM_SDL_BWD(V)                                                                          \
+  case V:                                                                                        \
+    return sdl_backward_v<V>(prm, shapes, bu, states, grad_output, grads, grad_bu, length, batch, \
+                             ssm, stream);
+    OSSM_SDL_BWD(OSSM_DLINOSS_IMEX1)
+    OSSM_SDL_BWD(OSSM_DLINOSS_IMEX2)
+    OSSM_SDL_BWD(OSSM_DLINOSS_IM)
+    default:
+      return sdl_backward_v<OSSM_DLINOSS_EX>(prm, shapes, bu, states, grad_output, grads, grad_bu,
+                                             length, batch, ssm, stream);
+#undef OSSM_SDL_BWD
+  }
+}
+
+}  // extern "C"

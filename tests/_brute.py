@@ -79,3 +79,42 @@ def selective(u, dt, A, Bm, Cm, gate=None):
     if gate is not None:
         y = y * torch.nn.functional.silu(gate)
     return y
+
+
+def sdlinoss_states(variant: str, A, G, step, bu):
+    """States ``[L,B,M,2]`` of the selective D-LinOSS recurrence by a plain loop.
+
+    Parameters broadcast against ``bu [L,B,M]`` the torch way (shapes (M,),
+    (L,1,M), (1,B,M), (L,B,M)), so autograd sums their gradients over the
+    broadcast axes.  Per step, dt = clamp(step, 1e-6, 1):
+      imex1: w = (w + dt^2 (bu - a x)) / max(1 + dt g, 1e-6)
+      imex2: w = ((1 - dt g) w + dt^2 (bu - a x)) / max(1 + dt^2 a, 1e-6)
+      im:    w = (w + dt^2 (bu - a x)) / max(1 + dt g + dt^2 a, 1e-6)
+      ex:    w = (1 - dt g) w + dt^2 (bu - a x)
+    then x = x + w (the bridge's fallback, _sdlinoss_scan.py:150-197).
+    """
+    L, B, M = bu.shape
+    shape = (L, B, M)
+    a = A.expand(shape) if A.dim() == 3 else A.reshape(1, 1, M).expand(shape)
+    g = G.expand(shape) if G.dim() == 3 else G.reshape(1, 1, M).expand(shape)
+    st = step.expand(shape) if step.dim() == 3 else step.reshape(1, 1, M).expand(shape)
+    dt = torch.clamp(st, min=1e-6, max=1.0)
+    w = torch.zeros(B, M, dtype=bu.dtype)
+    x = torch.zeros(B, M, dtype=bu.dtype)
+    out = []
+    for t in range(L):
+        d, at, gt = dt[t], a[t], g[t]
+        comb = bu[t] - at * x
+        if variant == "imex1":
+            w = (w + d * d * comb) / torch.clamp(1.0 + d * gt, min=1e-6)
+        elif variant == "imex2":
+            w = ((1.0 - d * gt) * w + d * d * comb) / torch.clamp(1.0 + d * d * at, min=1e-6)
+        elif variant == "im":
+            w = (w + d * d * comb) / torch.clamp(1.0 + d * gt + d * d * at, min=1e-6)
+        elif variant == "ex":
+            w = (1.0 - d * gt) * w + d * d * comb
+        else:
+            raise ValueError(variant)
+        x = x + w
+        out.append(torch.stack([w, x], -1))
+    return torch.stack(out, 0)

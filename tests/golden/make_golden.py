@@ -12,11 +12,16 @@ Three kinds of data, none of it reference source:
    kernels (``oracle/_ref``, compiled from src/ossm/csrc by oracle/Makefile.ref)
    on small seeded cases: D-LinOSS forward/backward for every variant, LinOSS
    scan forward, selective scan forward/backward with and without the gate.
+4. ``sdl_kernel_vectors.npz`` — the same for the selective D-LinOSS kernels
+   (every variant, every accepted parameter layout, both clamps exercised).
 
 Usage (from the repository root, with /root/reference present and
 ``make -f oracle/Makefile.ref`` done):
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [dlinoss] [linoss] [kernels] [sdlinoss]
+
+(no argument: all).  The reference's OpenMP kernels add some sums in a
+thread-dependent order, so regenerating a fixture changes its last bits.
 """
 
 from __future__ import annotations
@@ -125,10 +130,56 @@ def _ref_kernel_vectors() -> None:
     np.savez_compressed(OUT / "ref_kernel_vectors.npz", **vec)
 
 
+def _sdl_kernel_vectors() -> None:
+    """Selective D-LinOSS: the reference's CPU kernels (sdlinoss_<v>.cpp) on a
+    ragged shape with every parameter layout the kernels accept, with steps and
+    stiffnesses that hit both clamps (dt outside (1e-6, 1), S below 1e-6)."""
+    import torch
+
+    import oracle
+
+    ref = oracle.reference_module()
+    assert ref is not None, "build oracle/_ref first: make -f oracle/Makefile.ref"
+    rng = np.random.default_rng(20241130)
+    T = torch.from_numpy
+    L, B, M = 29, 2, 5
+    vec: dict[str, np.ndarray] = {}
+    bu = (rng.normal(size=(L, B, M)) + 1j * rng.normal(size=(L, B, M))).astype(np.complex64)
+    go = (rng.normal(size=(L, B, M)) + 1j * rng.normal(size=(L, B, M))).astype(np.complex64)
+    vec.update(bu=bu, grad=go)
+    shapes = {"full": (L, B, M), "bcast_t": (1, B, M), "bcast_b": (L, 1, M), "m": (M,)}
+    for v in oracle.VARIANTS:
+        for tag, shp in shapes.items():
+            if tag != "full" and v in ("imex2", "ex"):
+                continue
+            A = rng.uniform(0.1, 1.5, shp).astype(np.float32)
+            G = rng.uniform(0.0, 1.0, shp).astype(np.float32)
+            S = rng.uniform(-0.2, 1.3, shp).astype(np.float32)  # clamps dt on both sides
+            if v in ("imex1", "im") and len(shp) == 3 and shp[0] == L:
+                # S = 1 + dt g (+ dt^2 a) below the 1e-6 clamp, at the last step only
+                # (earlier, the 1e6 gain would overflow the rest of the sequence)
+                G[-1, :, ::2] = -3.0
+                S[-1, :, ::2] = 0.9
+            st = getattr(ref, f"sdlinoss_{v}_forward")(T(A), T(G), T(S), T(bu)).numpy()
+            ga, gg, gs, gb = (x.numpy() for x in getattr(ref, f"sdlinoss_{v}_backward")(
+                T(A), T(G), T(S), T(bu), T(st), T(go)))
+            key = f"{v}_{tag}"
+            vec.update({f"{key}_A": A, f"{key}_G": G, f"{key}_step": S, f"{key}_states": st,
+                        f"{key}_grad_A": ga, f"{key}_grad_G": gg, f"{key}_grad_step": gs,
+                        f"{key}_grad_bu": gb})
+    np.savez_compressed(OUT / "sdl_kernel_vectors.npz", **vec)
+
+
 def main() -> None:
-    _copy_dlinoss_fixture()
-    _extract_linoss_snapshot()
-    _ref_kernel_vectors()
+    only = sys.argv[1:]
+    if not only or "dlinoss" in only:
+        _copy_dlinoss_fixture()
+    if not only or "linoss" in only:
+        _extract_linoss_snapshot()
+    if not only or "kernels" in only:
+        _ref_kernel_vectors()
+    if not only or "sdlinoss" in only:
+        _sdl_kernel_vectors()
     for p in sorted(OUT.iterdir()):
         print(f"{p.name:40s} {p.stat().st_size:>10d} B")
 

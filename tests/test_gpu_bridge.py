@@ -172,3 +172,70 @@ def test_selective_bridge_grads(bridge, gated):
         y_ng = bridge.try_selective_scan(*[x.detach() for x in dev[:5]],
                                          dev[5].detach() if gated else None)
     assert torch.equal(y_ng, y.detach())
+
+
+def _sdlinoss_layer(run, variant, W, u):
+    """SelectiveDLinOSSLayer.forward glue (sdlinoss.py:153-238, without the
+    causal conv): per-step (r, theta, dt) heads, the variant's (A, G) from them,
+    bu = u B^T, x = scan, y = Re(x C^T) + D u."""
+    Wf, Wr, Wth, Wdt, rb, thb, dtb, Bw, Cw, Dw = W
+    feats = torch.tanh(u @ Wf)
+    r = torch.sigmoid(rb + feats @ Wr)
+    theta = np.pi * torch.tanh(thb + feats @ Wth)
+    dt = 0.02 + 0.98 * torch.sigmoid(dtb + feats @ Wdt)
+    r2 = torch.clamp(r * r, min=1e-8)
+    c = torch.cos(theta)
+    if variant == "imex1":
+        A, G = (r2 - 2 * r * c + 1) / (dt * dt * r2), (1 - r2) / (dt * r2)
+    elif variant == "imex2":
+        A, G = (r2 - 2 * r * c + 1) / (dt * dt), (1 - r2) / dt
+    elif variant == "im":
+        A, G = (r2 - 2 * r * c + 1) / (dt * dt * r2), (-2 * r2 + 2 * r * c) / (dt * r2)
+    else:
+        A, G = (r2 - 2 * r * c + 1) / (dt * dt), (2 - 2 * r * c) / dt
+    Bc = torch.complex(Bw[..., 0], Bw[..., 1])
+    Cc = torch.complex(Cw[..., 0], Cw[..., 1])
+    bu = torch.matmul(u.to(Bc.dtype), Bc.transpose(0, 1))
+    perm = lambda t: t.permute(1, 0, 2).contiguous()  # noqa: E731  [B,L,M] -> [L,B,M]
+    x = run(variant, perm(A), perm(G), perm(dt), perm(bu)).permute(1, 0, 2)
+    return torch.matmul(x, Cc.transpose(0, 1)).real + u * Dw
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("shape", [(2, 12, 8, 16), (3, 257, 24, 16)], ids=lambda s: "x".join(map(str, s)))
+def test_sdlinoss_layer_outputs_and_grads(bridge, variant, shape):
+    """Selective D-LinOSS layer through ``run_sdlinoss``: outputs and every weight's
+    gradient vs torch.autograd of the fp64 loop (tolerances of the D-LinOSS test).
+    Pole radii r = sigmoid(.) around 0.4: a radius near 1 integrates the input into
+    states of 1e5 and more, whose fp32 rounding alone exceeds these tolerances."""
+    Bsz, L, M, H = shape
+    announce(f"bridge sdlinoss layer {variant} {shape}")
+    g = torch.Generator().manual_seed(21)
+    W = [torch.randn(H, H, generator=g) / H ** 0.5, torch.randn(H, M, generator=g) * 0.3,
+         torch.randn(H, M, generator=g) * 0.3, torch.randn(H, M, generator=g) * 0.3,
+         torch.randn(M, generator=g) * 0.5 - 0.5, torch.randn(M, generator=g) * 0.5,
+         torch.randn(M, generator=g) - 1.0, torch.randn(M, H, 2, generator=g) / H ** 0.5,
+         torch.randn(H, M, 2, generator=g) / M ** 0.5, torch.randn(H, generator=g)]
+    if variant == "ex":
+        # the explicit scheme's poles leave the unit disc as theta -> pi
+        # (det M = 2 r cos(theta) - 1): keep theta small
+        W[2], W[5] = W[2] * 0.2, W[5] * 0.2
+    u = torch.randn(Bsz, L, H, generator=torch.Generator().manual_seed(22))
+    w = torch.randn(Bsz, L, H, generator=torch.Generator().manual_seed(23))
+
+    dev = [p.cuda().requires_grad_() for p in W]
+    y = _sdlinoss_layer(bridge.run_sdlinoss, variant, dev, u.cuda())
+    (y * w.cuda()).sum().backward()
+
+    ref = [p.double().requires_grad_() for p in W]
+
+    def brute(variant, A, G, dt, bu):
+        return _brute.sdlinoss_states(variant, A, G, dt, bu)[..., 1]
+
+    y64 = _sdlinoss_layer(brute, variant, ref, u.double())
+    (y64 * w.double()).sum().backward()
+    np.testing.assert_allclose(y.detach().cpu().numpy(), y64.detach().numpy(), rtol=5e-4, atol=1e-4)
+    names = ("Wf", "Wr", "Wth", "Wdt", "r_base", "th_base", "dt_base", "B", "C", "D")
+    for got, r, name in zip(dev, ref, names):
+        np.testing.assert_allclose(got.grad.cpu().numpy(), r.grad.numpy(), rtol=5e-4,
+                                   atol=1e-4 * max(1.0, float(r.grad.abs().max())), err_msg=name)

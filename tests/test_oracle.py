@@ -251,3 +251,89 @@ def test_reference_module_when_present():
         assert hasattr(mod, f"dlinoss_{v}_forward") and hasattr(mod, f"dlinoss_{v}_backward")
     for name in ("linoss_scan", "selective_scan", "selective_scan_backward"):
         assert hasattr(mod, name)
+
+
+# ----------------------------------------------------------- selective D-LinOSS
+@pytest.fixture(scope="module")
+def sdl_vectors():
+    with np.load(GOLDEN / "sdl_kernel_vectors.npz", allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+SDL_CASES = [(v, tag) for v in VARIANTS for tag in ("full", "bcast_t", "bcast_b", "m")
+             if tag == "full" or v in ("imex1", "im")]
+
+
+@pytest.mark.parametrize("variant,tag", SDL_CASES)
+def test_sdlinoss_matches_reference_kernel_vectors(variant, tag, sdl_vectors):
+    """Oracle vs the reference's own CPU kernels (fixture written from oracle/_ref),
+    every accepted parameter layout, both clamps hit."""
+    v = sdl_vectors
+    k = f"{variant}_{tag}"
+    A, G, S = v[f"{k}_A"], v[f"{k}_G"], v[f"{k}_step"]
+    st = oracle.sdlinoss_forward(variant, A, G, S, v["bu"])
+    scale = np.abs(v[f"{k}_states"]).max()
+    _close(st, v[f"{k}_states"], 1e-5, 1e-6 * scale, "states")
+    grads = oracle.sdlinoss_backward(variant, A, G, S, v["bu"], v[f"{k}_states"], v["grad"])
+    for got, name in zip(grads, ("grad_A", "grad_G", "grad_step", "grad_bu")):
+        ref = v[f"{k}_{name}"]
+        assert got.shape == ref.shape, name
+        _close(got, ref, 1e-4, 1e-5 * max(1.0, np.abs(ref).max()), name)
+
+
+SDL_SHAPES = {"full": lambda L, B, M: (L, B, M), "bcast_t": lambda L, B, M: (1, B, M),
+              "bcast_b": lambda L, B, M: (L, 1, M), "m": lambda L, B, M: (M,)}
+
+
+@pytest.mark.parametrize("tag", list(SDL_SHAPES))
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_sdlinoss_backward_matches_fp64_autograd(variant, tag):
+    """Hand-written per-step adjoint (and the sum over broadcast axes) vs
+    torch.autograd of a plain fp64 loop; steps on both sides of the dt clamp."""
+    rng = np.random.default_rng(11)
+    L, B, M = 17, 3, 4
+    shp = SDL_SHAPES[tag](L, B, M)
+    A = rng.uniform(0.1, 1.2, shp)
+    G = rng.uniform(0.0, 1.0, shp)
+    S = rng.uniform(-0.3, 1.4, shp)
+    S[np.abs(S - 1e-6) < 1e-3] = 0.5  # keep away from the clamp's kinks
+    S[np.abs(S - 1.0) < 1e-3] = 0.5
+    bu = rng.normal(size=(L, B, M)) + 1j * rng.normal(size=(L, B, M))
+    Gout = rng.normal(size=(L, B, M)) + 1j * rng.normal(size=(L, B, M))
+    tA, tG, tS = (torch.tensor(x, requires_grad=True) for x in (A, G, S))
+    tbu = torch.tensor(bu, requires_grad=True)
+    s = _brute.sdlinoss_states(variant, tA, tG, tS, tbu)
+    loss = (s[..., 1] * torch.tensor(Gout).conj()).real.sum()
+    loss.backward()
+    states = oracle.sdlinoss_forward(variant, A, G, S, bu)
+    _close(states, s.detach().numpy(), 1e-12, 1e-12, "states")
+    gA, gG, gS, gbu = oracle.sdlinoss_backward(variant, A, G, S, bu, states, Gout)
+    _close(gA, tA.grad.numpy(), 1e-10, 1e-10, "grad_A")
+    _close(gG, tG.grad.numpy(), 1e-10, 1e-10, "grad_G")
+    _close(gS, tS.grad.numpy(), 1e-10, 1e-10, "grad_step")
+    _close(gbu, tbu.grad.numpy(), 1e-10, 1e-10, "grad_bu")
+
+
+def test_sdlinoss_stiff_clamp_matches_fp64_autograd():
+    """S = 1 + dt g below 1e-6 (imex1, im) at the last step: the clamp's zero
+    gradient w.r.t. S is honoured."""
+    rng = np.random.default_rng(12)
+    L, B, M = 9, 2, 3
+    for variant in ("imex1", "im"):
+        A = rng.uniform(0.1, 1.0, (L, B, M))
+        G = rng.uniform(0.0, 1.0, (L, B, M))
+        S = rng.uniform(0.1, 0.9, (L, B, M))
+        G[-1] = -4.0
+        S[-1] = 0.8
+        bu = rng.normal(size=(L, B, M)) + 1j * rng.normal(size=(L, B, M))
+        Gout = rng.normal(size=(L, B, M)) + 1j * rng.normal(size=(L, B, M))
+        tA, tG, tS = (torch.tensor(x, requires_grad=True) for x in (A, G, S))
+        tbu = torch.tensor(bu, requires_grad=True)
+        s = _brute.sdlinoss_states(variant, tA, tG, tS, tbu)
+        (s[..., 1] * torch.tensor(Gout).conj()).real.sum().backward()
+        states = oracle.sdlinoss_forward(variant, A, G, S, bu)
+        gA, gG, gS, gbu = oracle.sdlinoss_backward(variant, A, G, S, bu, states, Gout)
+        for got, ref, name in ((gA, tA.grad, "A"), (gG, tG.grad, "G"), (gS, tS.grad, "step"),
+                               (gbu, tbu.grad, "bu")):
+            ref = ref.numpy()
+            _close(got, ref, 1e-9, 1e-9 * np.abs(ref).max(), f"{variant} grad_{name}")
