@@ -213,6 +213,32 @@ def _detail_configs(torch, K, dev, reps=10):
                                   "GBps": n * DL_BYTES_FWD / (ms / 1e3) / 1e9,
                                   "hbm_frac": n * DL_BYTES_FWD / (ms / 1e3) / PEAK_HBM}
     del bu
+    # Selective D-LinOSS imex1 at config 2's shape (no BASELINE config of its own):
+    # per-step parameters [L,B,M] (12 B/state-step more each way), and
+    # time-invariant per-channel parameters [1,B,M]
+    L, B, P = 4096, 32, 128
+    g = torch.Generator(device=dev).manual_seed(6)
+    bu = torch.complex(torch.randn(L, B, P, device=dev, generator=g),
+                       torch.randn(L, B, P, device=dev, generator=g))
+    go = torch.complex(torch.randn(L, B, P, device=dev, generator=g),
+                       torch.randn(L, B, P, device=dev, generator=g))
+    n = L * B * P
+    for key, shp, pbytes in (("sdlinoss_imex1_c2_full", (L, B, P), 12),
+                             ("sdlinoss_imex1_c2_per_channel", (1, B, P), 0)):
+        A = torch.rand(shp, device=dev, generator=g) * 0.9 + 0.1
+        G = torch.rand(shp, device=dev, generator=g)
+        S = torch.sigmoid(torch.randn(shp, device=dev, generator=g))
+        st = K.sdlinoss_imex1_forward(A, G, S, bu)
+        tf = _ev_time(torch, lambda: K.sdlinoss_imex1_forward(A, G, S, bu), reps, 3)
+        tb = _ev_time(torch, lambda: K.sdlinoss_imex1_backward(A, G, S, bu, st, go), reps, 3)
+        fb, bb = n * (24 + pbytes), n * (24 + 2 * pbytes)
+        out[key] = {"fwd_ms": tf, "bwd_ms": tb,
+                    "state_steps_per_s_fwd_bwd": n / ((tf + tb) / 1e3),
+                    "hbm_frac_fwd": fb / (tf / 1e3) / PEAK_HBM,
+                    "hbm_frac_bwd": bb / (tb / 1e3) / PEAK_HBM,
+                    "bytes_per_state_step": [24 + pbytes, 24 + 2 * pbytes]}
+        del A, G, S, st
+    del bu, go
     # C3 / C4-shape: selective scan fwd+bwd, fp32, gated
     for key, (Bz, D, L, N) in (("c3_selective_fp32", (256, 128, 200, 16)),
                                ("c4_shape_selective_fp32", (16, 1536, 2048, 16))):

@@ -97,12 +97,22 @@ __device__ __forceinline__ float sdl_inv(float dt, float g, float a) {
   else return 1.f / fmaxf(sdl_s_raw<V>(dt, g, a), kClampMin);
 }
 
+// The coefficients given 1/S (computed once per step and reused).
 template <int V>
-__device__ __forceinline__ SdlCoef<V> sdl_coef(float a, float g, float step_raw) {
+__device__ __forceinline__ SdlCoef<V> sdl_coef_inv(float a, float g, float step_raw, float inv) {
   const float dt = sdl_dt(step_raw);
   const float dt2 = dt * dt;
-  const float inv = sdl_inv<V>(dt, g, a);
   return {sdl_alpha<V>(dt, g) * inv, -dt2 * a * inv, dt2 * inv};
+}
+
+template <int V>
+__device__ __forceinline__ float sdl_inv_of(float a, float g, float step_raw) {
+  return sdl_inv<V>(sdl_dt(step_raw), g, a);
+}
+
+template <int V>
+__device__ __forceinline__ SdlCoef<V> sdl_coef(float a, float g, float step_raw) {
+  return sdl_coef_inv<V>(a, g, step_raw, sdl_inv_of<V>(a, g, step_raw));
 }
 
 // (w, x) -> (c0 w + c1 x + c2 bu, x + w')
@@ -346,9 +356,9 @@ __global__ __launch_bounds__(W * kWave) void sdl_forward_kernel(
 // follows the reference backward kernels: sdlinoss_imex1.cpp:186-220,
 // sdlinoss_imex2.cpp:178-221, sdlinoss_im.cpp:176-225, sdlinoss_ex.cpp:163-189.
 template <int V>
-__device__ __forceinline__ float4 sdl_grad_step(float a, float g, float step_raw, float4 sp,
-                                                float2 bu, float4 lam, float2& gbu, float& ga,
-                                                float& gg, float& gs) {
+__device__ __forceinline__ float4 sdl_grad_step(float a, float g, float step_raw, float inv,
+                                                float4 sp, float2 bu, float4 lam, float2& gbu,
+                                                float& ga, float& gg, float& gs) {
   const float dt = sdl_dt(step_raw);
   const float dt2 = dt * dt;
   const float alpha = sdl_alpha<V>(dt, g);
@@ -359,7 +369,6 @@ __device__ __forceinline__ float4 sdl_grad_step(float a, float g, float step_raw
   float gtr = gwr, gti = gwi;  // gradient w.r.t. tmpw
   if constexpr (V != OSSM_DLINOSS_EX) {
     const float s_raw = sdl_s_raw<V>(dt, g, a);
-    const float inv = 1.f / fmaxf(s_raw, kClampMin);
     const float tmpr = fmaf(alpha, sp.x, dt2 * combr), tmpi = fmaf(alpha, sp.y, dt2 * combi);
     gtr = gwr * inv;
     gti = gwi * inv;
@@ -392,11 +401,13 @@ __device__ __forceinline__ float4 sdl_grad_step(float a, float g, float step_raw
   return make_float4(alpha * gtr, alpha * gti, fmaf(-dt2 * a, gtr, lam.z), fmaf(-dt2 * a, gti, lam.w));
 }
 
-// Destinations of the per-element parameter gradients ([L, B*M] each).
+// Destinations of the parameter gradients.  Bit p of `tsum` (p = 0 a, 1 g,
+// 2 step) set: the parameter is broadcast over time, so each workgroup writes
+// its chunk's sum over time (row c of a [n_chunks, B*M] partials array);
+// clear: per-element gradients ([L, B*M]).
 struct SdlGradOut {
-  float* a;
-  float* g;
-  float* s;
+  float* p[3];
+  int tsum;
 };
 
 template <int V, int T, int W>
@@ -408,6 +419,7 @@ __global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
   __shared__ float4 s_k[W][kWave];
   __shared__ float4 s_carry[kWave];
   __shared__ float4 s_sp[W][T][kWave];  // recomputed s_{t-1}
+  __shared__ float s_psum[3][W][kWave];  // per-wave sums over time (broadcast parameters)
   __shared__ int s_ticket;
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -444,13 +456,16 @@ __global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
   const bool full = t0 + T <= L;
   auto live = [&](int i) { return full || t0 + i < L; };
 
-  // recompute s_{t-1} into LDS; reverse aggregate (e, K) of the sub-chunk
+  // recompute s_{t-1} into LDS (1/S of every step kept for the later
+  // passes); reverse aggregate (e, K) of the sub-chunk
+  float inv[T];
   {
     float4 s = t0 >= 1 ? ck : f4zero();
 #pragma unroll
     for (int i = 0; i < T; ++i) {
+      inv[i] = sdl_inv_of<V>(pa[i], pg[i], ps[i]);
       s_sp[w][i][lane] = s;
-      if (live(i)) s = sdl_step<V>(sdl_coef<V>(pa[i], pg[i], ps[i]), s, x[i]);
+      if (live(i)) s = sdl_step<V>(sdl_coef_inv<V>(pa[i], pg[i], ps[i], inv[i]), s, x[i]);
     }
   }
   float4 e = f4zero();
@@ -458,7 +473,7 @@ __global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
 #pragma unroll
   for (int i = T - 1; i >= 0; --i) {
     if (live(i)) {
-      const SdlCoef<V> k = sdl_coef<V>(pa[i], pg[i], ps[i]);
+      const SdlCoef<V> k = sdl_coef_inv<V>(pa[i], pg[i], ps[i], inv[i]);
       e = sdl_matT_apply<V>(k, make_float4(e.x, e.y, e.z + go[i].x, e.w + go[i].y));
       K = sdl_matT_left<V>(k, K);
     }
@@ -502,7 +517,9 @@ __global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
   float4 rho = s_carry[lane];
   for (int v = W - 1; v > w; --v) rho = f4add(mat_apply(rmat_unpack(s_k[v][lane]), rho), s_e[v][lane]);
 
-  // final reverse pass: per-step gradients
+  // final reverse pass: per-step gradients (per element, or summed over the
+  // sub-chunk for parameters broadcast over time)
+  float psum[3] = {0.f, 0.f, 0.f};
   if (active) {
 #pragma unroll
     for (int i = T - 1; i >= 0; --i) {
@@ -510,12 +527,29 @@ __global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
         const long long t = t0 + i;
         const float4 lam = make_float4(rho.x, rho.y, rho.z + go[i].x, rho.w + go[i].y);
         float2 gbu;
-        float ga, gg, gs;
-        rho = sdl_grad_step<V>(pa[i], pg[i], ps[i], s_sp[w][i][lane], x[i], lam, gbu, ga, gg, gs);
+        float gp[3];
+        rho = sdl_grad_step<V>(pa[i], pg[i], ps[i], inv[i], s_sp[w][i][lane], x[i], lam, gbu,
+                               gp[0], gp[1], gp[2]);
         row_of(gin, t, nc, g)[lane] = gbu;
-        row_of(go_prm.a, t, nc, g)[lane] = ga;
-        row_of(go_prm.g, t, nc, g)[lane] = gg;
-        row_of(go_prm.s, t, nc, g)[lane] = gs;
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+          if (go_prm.tsum & (1 << p)) psum[p] += gp[p];
+          else row_of(go_prm.p[p], t, nc, g)[lane] = gp[p];
+        }
+      }
+    }
+  }
+  if (go_prm.tsum != 0) {
+#pragma unroll
+    for (int p = 0; p < 3; ++p) s_psum[p][w][lane] = psum[p];
+    __syncthreads();
+    if (w == 0 && active) {
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        if (!(go_prm.tsum & (1 << p))) continue;
+        float v = 0.f;
+        for (int u = 0; u < W; ++u) v += s_psum[p][u][lane];
+        row_of(go_prm.p[p], c, nc, g)[lane] = v;
       }
     }
   }
@@ -528,10 +562,26 @@ __global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
 // ============================================================================
 constexpr int kSumGroups = 32;
 
-// grid: x = n * col_tiles + column tile, y = row group q
-__global__ __launch_bounds__(256) void sdl_colsum_pass1(const float* __restrict__ in,
-                                                        double* __restrict__ part, int R, int C,
-                                                        int col_tiles) {
+// One reduction: out[n][c] = sum_r in[n][r][c] for n < nb, r < R, c < C.
+struct ColSum {
+  const float* in;
+  float* out;
+  double* part;  // [nb][kSumGroups][C]
+  int nb, R, C, col_tiles;
+};
+
+// Up to three reductions per launch (one per parameter), selected by blockIdx.z.
+struct ColSums {
+  ColSum s[3];
+};
+
+// grid: x = n * col_tiles + column tile (up to the largest reduction), y = row group q
+__global__ __launch_bounds__(256) void sdl_colsum_pass1(ColSums all) {
+  const ColSum& cs = all.s[blockIdx.z];
+  const float* in = cs.in;
+  double* part = cs.part;
+  const int R = cs.R, C = cs.C, col_tiles = cs.col_tiles;
+  if (blockIdx.x >= static_cast<unsigned>(cs.nb * col_tiles)) return;  // uniform per block
   __shared__ double s_red[4][kWave];
   const int lane = threadIdx.x & (kWave - 1), w = wave_id();
   const int n = blockIdx.x / col_tiles;
@@ -556,8 +606,11 @@ __global__ __launch_bounds__(256) void sdl_colsum_pass1(const float* __restrict_
         ((s_red[0][lane] + s_red[1][lane]) + s_red[2][lane]) + s_red[3][lane];
 }
 
-__global__ __launch_bounds__(256) void sdl_colsum_pass2(const double* __restrict__ part,
-                                                        float* __restrict__ out, int C, int nb) {
+__global__ __launch_bounds__(256) void sdl_colsum_pass2(ColSums all) {
+  const ColSum& cs = all.s[blockIdx.z];
+  const double* part = cs.part;
+  float* out = cs.out;
+  const int C = cs.C, nb = cs.nb;
   const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= static_cast<long long>(nb) * C) return;
   const int n = static_cast<int>(i / C), col = static_cast<int>(i - static_cast<long long>(n) * C);
@@ -596,33 +649,21 @@ ParamView view_of(const ParamShape& s, int64_t L, int64_t B, int64_t M) {
   return v;
 }
 
-// Whether a parameter's gradient needs a sum over broadcast axes.
-bool needs_sum(const ParamShape& s, int64_t L, int64_t B) {
-  return (s.la == 1 && L > 1) || (s.ba == 1 && B > 1);
-}
-
-int launch_colsum(const float* in, float* out, double* part, int64_t nb, int64_t R, int64_t C,
-                  hipStream_t stream) {
-  const int64_t col_tiles = (C + kWave - 1) / kWave;
-  if (nb * col_tiles > INT_MAX) return set_error(OSSM_ERR_UNSUPPORTED, "gradient reduction too large");
-  const dim3 g1(static_cast<unsigned>(nb * col_tiles), kSumGroups);
-  hipLaunchKernelGGL(sdl_colsum_pass1, g1, dim3(256), 0, stream, in, part, static_cast<int>(R),
-                     static_cast<int>(C), static_cast<int>(col_tiles));
+// Runs the `n` reductions of `all` in two launches.
+int launch_colsums(const ColSums& all, int n, hipStream_t stream) {
+  if (n == 0) return OSSM_OK;
+  int64_t max_blocks = 0, max_out = 0;
+  for (int k = 0; k < n; ++k) {
+    max_blocks = std::max<int64_t>(max_blocks, static_cast<int64_t>(all.s[k].nb) * all.s[k].col_tiles);
+    max_out = std::max<int64_t>(max_out, static_cast<int64_t>(all.s[k].nb) * all.s[k].C);
+  }
+  if (max_blocks > INT_MAX) return set_error(OSSM_ERR_UNSUPPORTED, "gradient reduction too large");
+  hipLaunchKernelGGL(sdl_colsum_pass1, dim3(static_cast<unsigned>(max_blocks), kSumGroups, n),
+                     dim3(256), 0, stream, all);
   if (int rc = launch_check("sdl_colsum_pass1")) return rc;
-  const int64_t n_out = nb * C;
-  hipLaunchKernelGGL(sdl_colsum_pass2, dim3(static_cast<unsigned>((n_out + 255) / 256)), dim3(256),
-                     0, stream, part, out, static_cast<int>(C), static_cast<int>(nb));
+  hipLaunchKernelGGL(sdl_colsum_pass2, dim3(static_cast<unsigned>((max_out + 255) / 256), 1, n),
+                     dim3(256), 0, stream, all);
   return launch_check("sdl_colsum_pass2");
-}
-
-// Sums a per-element gradient [L, B, M] over the broadcast axes of `s` into
-// `out` (shape [La, Ba, M]).
-int reduce_grad(const float* full, float* out, const ParamShape& s, int64_t L, int64_t B, int64_t M,
-                double* part, hipStream_t stream) {
-  const bool rt = s.la == 1 && L > 1, rb = s.ba == 1 && B > 1;
-  if (rt && rb) return launch_colsum(full, out, part, 1, L * B, M, stream);
-  if (rt) return launch_colsum(full, out, part, 1, L, B * M, stream);
-  return launch_colsum(full, out, part, L, B, M, stream);  // rb only
 }
 
 int fill_zero_f(float* p, int64_t n, hipStream_t stream) {
@@ -632,13 +673,24 @@ int fill_zero_f(float* p, int64_t n, hipStream_t stream) {
   return launch_check("sdl_zero_kernel");
 }
 
-constexpr int kFwdT = 8, kFwdW = 16;
-constexpr int kBwdT = 8, kBwdW = 8;
+// Tiles (T steps per lane, W waves): defaults, and the instantiated choices
+// for OSSM_SDL_TILE_FWD / OSSM_SDL_TILE_BWD ("TxW").
+struct TileTW {
+  int T, W;
+};
+#define OSSM_SDL_FWD_TILES(X) X(8, 16) X(16, 8) X(8, 8) X(16, 4) X(4, 16)
+#define OSSM_SDL_BWD_TILES(X) X(8, 8) X(8, 4) X(4, 8) X(4, 16) X(16, 4)
 
-template <int V>
-int sdl_forward_v(const SdlParams& prm, const void* bu, void* states, int64_t L, int64_t nc,
-                  hipStream_t stream) {
-  constexpr int T = kFwdT, W = kFwdW;
+TileTW sdl_tile(const char* env, TileTW dflt) {
+  const char* e = std::getenv(env);
+  TileTW t{0, 0};
+  if (e == nullptr || std::sscanf(e, "%dx%d", &t.T, &t.W) != 2) return dflt;
+  return t;
+}
+
+template <int V, int T, int W>
+int sdl_forward_tw(const SdlParams& prm, const void* bu, void* states, int64_t L, int64_t nc,
+                   hipStream_t stream) {
   const int64_t n_chunks = (L + T * W - 1) / (T * W);
   const int64_t n_groups = (nc + kWave - 1) / kWave;
   if (n_chunks * n_groups > INT_MAX)
@@ -661,37 +713,58 @@ int sdl_forward_v(const SdlParams& prm, const void* bu, void* states, int64_t L,
 }
 
 template <int V>
-int sdl_backward_v(const SdlParams& prm, const ParamShape (&shapes)[3], const void* bu,
-                   const void* states, const void* gout, float* const (&grads)[3], void* gbu,
-                   int64_t L, int64_t B, int64_t M, hipStream_t stream) {
-  constexpr int T = kBwdT, W = kBwdW;
+int sdl_forward_v(const SdlParams& prm, const void* bu, void* states, int64_t L, int64_t nc,
+                  hipStream_t stream) {
+  static const TileTW tile = sdl_tile("OSSM_SDL_TILE_FWD", TileTW{8, 16});
+#define OSSM_SDL_FWD_CASE(TT, WW) \
+  if (tile.T == TT && tile.W == WW) return sdl_forward_tw<V, TT, WW>(prm, bu, states, L, nc, stream);
+  OSSM_SDL_FWD_TILES(OSSM_SDL_FWD_CASE)
+#undef OSSM_SDL_FWD_CASE
+  return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_SDL_TILE_FWD names no built tile");
+}
+
+template <int V, int T, int W>
+int sdl_backward_tw(const SdlParams& prm, const ParamShape (&shapes)[3], const void* bu,
+                    const void* states, const void* gout, float* const (&grads)[3], void* gbu,
+                    int64_t L, int64_t B, int64_t M, hipStream_t stream) {
   const int64_t nc = B * M;
   const int64_t n_chunks = (L + T * W - 1) / (T * W);
   const int64_t n_groups = (nc + kWave - 1) / kWave;
   if (n_chunks * n_groups > INT_MAX)
     return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
-  // per-element gradient buffers for the broadcast parameters, then the
-  // column-sum partials
-  const size_t elems = static_cast<size_t>(L) * nc;
-  int n_full = 0;
-  for (const auto& s : shapes) n_full += needs_sum(s, L, B) ? 1 : 0;
-  const size_t full_bytes = (n_full * elems * sizeof(float) + 255) & ~static_cast<size_t>(255);
-  const int64_t max_c = nc;  // the widest reduction output (L x M <= L x B x M as well)
-  const size_t part_bytes = static_cast<size_t>(kSumGroups) * std::max<int64_t>(max_c, L * M) * sizeof(double);
-  float* buf[3] = {nullptr, nullptr, nullptr};
-  double* part = nullptr;
-  if (n_full > 0) {
-    void* ws = nullptr;
-    if (int rc = acquire_workspace(stream, full_bytes + part_bytes, &ws)) return rc;
-    float* next = static_cast<float*>(ws);
-    for (int p = 0; p < 3; ++p)
-      if (needs_sum(shapes[p], L, B)) {
-        buf[p] = next;
-        next += elems;
-      }
-    part = reinterpret_cast<double*>(static_cast<char*>(ws) + full_bytes);
+  // Where each parameter's gradient goes: straight to the output (full
+  // shape), per-chunk sums over time [n_chunks, B*M] (broadcast over time,
+  // summed over the chunks and, if also broadcast over batch, the batch rows
+  // afterwards), or per element [L, B*M] (broadcast over batch only, summed
+  // over the batch rows afterwards).
+  SdlGradOut dst{};
+  size_t ws_floats = 0;
+  size_t offs[3] = {0, 0, 0};
+  int64_t max_out = 0;  // the largest reduction output (batches x columns)
+  for (int p = 0; p < 3; ++p) {
+    const bool rt = shapes[p].la == 1 && L > 1, rb = shapes[p].ba == 1 && B > 1;
+    if (rt) dst.tsum |= 1 << p;
+    if (rt || rb) {
+      offs[p] = ws_floats;
+      ws_floats += static_cast<size_t>(rt ? n_chunks : L) * nc;
+      max_out = std::max<int64_t>(max_out, rt ? (rb ? M : nc) : L * M);
+    }
   }
-  SdlGradOut dst{buf[0] ? buf[0] : grads[0], buf[1] ? buf[1] : grads[1], buf[2] ? buf[2] : grads[2]};
+  double* part = nullptr;
+  float* bufs = nullptr;
+  if (ws_floats > 0) {
+    const size_t buf_bytes = (ws_floats * sizeof(float) + 255) & ~static_cast<size_t>(255);
+    const size_t part_bytes = 3 * static_cast<size_t>(kSumGroups) * max_out * sizeof(double);
+    void* ws = nullptr;
+    if (int rc = acquire_workspace(stream, buf_bytes + part_bytes, &ws)) return rc;
+    bufs = static_cast<float*>(ws);
+    part = reinterpret_cast<double*>(static_cast<char*>(ws) + buf_bytes);
+  }
+  bool staged[3];
+  for (int p = 0; p < 3; ++p) {
+    staged[p] = (shapes[p].la == 1 && L > 1) || (shapes[p].ba == 1 && B > 1);
+    dst.p[p] = staged[p] ? bufs + offs[p] : grads[p];
+  }
 
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * kTvKinds * 4 * nc * sizeof(unsigned long long);
   void* payload = nullptr;
@@ -708,10 +781,39 @@ int sdl_backward_v(const SdlParams& prm, const ParamShape (&shapes)[3], const vo
     release_unlaunched(stream, total);
     return rc;
   }
-  for (int p = 0; p < 3; ++p)
-    if (buf[p] != nullptr)
-      if (int rc = reduce_grad(buf[p], grads[p], shapes[p], L, B, M, part, stream)) return rc;
-  return OSSM_OK;
+  ColSums sums{};
+  int n_sums = 0;
+  for (int p = 0; p < 3; ++p) {
+    if (!staged[p]) continue;
+    const bool rt = shapes[p].la == 1 && L > 1, rb = shapes[p].ba == 1 && B > 1;
+    ColSum& cs = sums.s[n_sums];
+    cs.in = dst.p[p];
+    cs.out = grads[p];
+    cs.part = part + static_cast<size_t>(n_sums) * kSumGroups * max_out;
+    if (rt && rb) {  // [n_chunks, B, M] -> [M]
+      cs.nb = 1; cs.R = static_cast<int>(n_chunks * B); cs.C = static_cast<int>(M);
+    } else if (rt) {  // [n_chunks, B*M] -> [B*M]
+      cs.nb = 1; cs.R = static_cast<int>(n_chunks); cs.C = static_cast<int>(nc);
+    } else {  // [L, B, M] -> [L, M]
+      cs.nb = static_cast<int>(L); cs.R = static_cast<int>(B); cs.C = static_cast<int>(M);
+    }
+    cs.col_tiles = (cs.C + kWave - 1) / kWave;
+    ++n_sums;
+  }
+  return launch_colsums(sums, n_sums, stream);
+}
+
+template <int V>
+int sdl_backward_v(const SdlParams& prm, const ParamShape (&shapes)[3], const void* bu,
+                   const void* states, const void* gout, float* const (&grads)[3], void* gbu,
+                   int64_t L, int64_t B, int64_t M, hipStream_t stream) {
+  static const TileTW tile = sdl_tile("OSSM_SDL_TILE_BWD", TileTW{16, 4});
+#define OSSM_SDL_BWD_CASE(TT, WW)                                                            \
+  if (tile.T == TT && tile.W == WW)                                                          \
+    return sdl_backward_tw<V, TT, WW>(prm, shapes, bu, states, gout, grads, gbu, L, B, M, stream);
+  OSSM_SDL_BWD_TILES(OSSM_SDL_BWD_CASE)
+#undef OSSM_SDL_BWD_CASE
+  return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_SDL_TILE_BWD names no built tile");
 }
 
 int check_sdl(int variant, int64_t L, int64_t B, int64_t M, const char* what) {
