@@ -239,6 +239,26 @@ def _detail_configs(torch, K, dev, reps=10):
                     "bytes_per_state_step": [24 + pbytes, 24 + 2 * pbytes]}
         del A, G, S, st
     del bu, go
+    # Diagonal complex scan (LRU / S5) at config 2's shape (no BASELINE config of
+    # its own): forward reads b, writes x (16 B/state-step); the native backward
+    # reads grad and the saved states and writes grad_b (24 B/state-step)
+    L, B, P = 4096, 32, 128
+    g = torch.Generator(device=dev).manual_seed(7)
+    r = torch.rand(P, device=dev, generator=g) * 0.499 + 0.5
+    th = torch.rand(P, device=dev, generator=g) * 6.28
+    lre, lim = r * torch.cos(th), r * torch.sin(th)
+    b_seq = torch.randn(L, B, P, 2, device=dev, generator=g)
+    go = torch.randn(L, B, P, 2, device=dev, generator=g)
+    st = K.lru_scan(lre, lim, b_seq)
+    tf = _ev_time(torch, lambda: K.lru_scan(lre, lim, b_seq), reps, 3)
+    tb = _ev_time(torch, lambda: K.lru_scan_backward(lre, lim, st, go), reps, 3)
+    n = L * B * P
+    out["lru_s5_diag_c2_shape"] = {"fwd_ms": tf, "bwd_ms": tb,
+                                   "state_steps_per_s_fwd_bwd": n / ((tf + tb) / 1e3),
+                                   "hbm_frac_fwd": n * 16 / (tf / 1e3) / PEAK_HBM,
+                                   "hbm_frac_bwd": n * 24 / (tb / 1e3) / PEAK_HBM,
+                                   "bytes_per_state_step": [16, 24]}
+    del b_seq, go, st
     # C3 / C4-shape: selective scan fwd+bwd, fp32, gated
     for key, (Bz, D, L, N) in (("c3_selective_fp32", (256, 128, 200, 16)),
                                ("c4_shape_selective_fp32", (16, 1536, 2048, 16))):

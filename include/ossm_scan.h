@@ -42,7 +42,7 @@ enum {
 
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
-/* Library ABI version (bumped on any change of the entry points; currently 4). */
+/* Library ABI version (bumped on any change of the entry points; currently 5). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -190,6 +190,39 @@ int ossm_selective_backward_bf16(const void* grad_out, const void* u, const void
                                  void* ddt, float* dA, void* dB, void* dC, void* dgate,
                                  int64_t batch, int64_t dim, int64_t length, int64_t dstate,
                                  ossm_stream_t stream);
+
+/*
+ * Diagonal complex scan x_t = lambda_p * x_{t-1} + b_t, x_{-1} = 0, per channel
+ * (b, p): replaces lru_scan and s5_scan (dispatchers lru_scan.cpp:126-146 and
+ * s5_scan.cpp:126-146, CPU kernels lru_scan.cpp:10-58 / s5_scan.cpp:10-66, CUDA
+ * lru_scan_cuda.cu:77-115).  lambda_real, lambda_imag [state]; b_seq and out
+ * [L, B, state] complex64 (the reference's [L, B, state, 2] real view).
+ */
+int ossm_diag_scan_forward(const float* lambda_real, const float* lambda_imag, const void* b_seq,
+                           void* out, int64_t length, int64_t batch, int64_t state,
+                           ossm_stream_t stream);
+
+/*
+ * Native backward of the diagonal scan; the reference runs it as a Python loop
+ * (_LRUScanFn.backward lru.py:52-80, _S5ScanFn.backward s5.py:137-165).  From the
+ * forward's states and grad_output [L, B, state] complex64: grad_b_t = g_t with
+ * g_t = grad_output_t + conj(lambda) g_{t+1}, and grad_lambda [state] complex64 =
+ * sum over t, b of g_t conj(x_{t-1}) (summed in fp64 in a fixed order).
+ */
+int ossm_diag_scan_backward(const float* lambda_real, const float* lambda_imag, const void* states,
+                            const void* grad_output, void* grad_lambda, void* grad_b,
+                            int64_t length, int64_t batch, int64_t state, ossm_stream_t stream);
+
+/* fp64 (complex128) twins of the two entries above (the reference dispatches
+ * lru_scan / s5_scan over float and double, lru_scan_cuda.cu:102). */
+int ossm_diag_scan_forward_f64(const double* lambda_real, const double* lambda_imag,
+                               const void* b_seq, void* out, int64_t length, int64_t batch,
+                               int64_t state, ossm_stream_t stream);
+
+int ossm_diag_scan_backward_f64(const double* lambda_real, const double* lambda_imag,
+                                const void* states, const void* grad_output, void* grad_lambda,
+                                void* grad_b, int64_t length, int64_t batch, int64_t state,
+                                ossm_stream_t stream);
 
 #ifdef __cplusplus
 }

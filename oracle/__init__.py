@@ -10,7 +10,8 @@ package, and only as the checker or the timed CPU baseline.  The product path
 All functions take and return numpy arrays in the reference's layouts:
 D-LinOSS ``bu [L,B,P]`` complex, states ``[L,B,P,2]`` complex (the selective
 D-LinOSS alike, with parameters (M,), (L,M), (B,M) or (L|1,B|1,M)); LinOSS
-``b_seq [L,B,P,2]`` complex with complex ``m_ij [P]``; selective scan
+``b_seq [L,B,P,2]`` complex with complex ``m_ij [P]``; diagonal (LRU / S5)
+scans ``b_seq [L,B,P]`` complex with complex ``lambda_bar [P]``; selective scan
 ``u, dt, gate [B,D,L]``, ``A [D,N]``, ``B, C [B,L,N]`` real.
 """
 
@@ -148,6 +149,39 @@ def linoss_backward(m11, m12, m21, m22, states, grad_output):
     _fn("oracle_linoss_backward", prec)(*[_ptr(m) for m in ms], _ptr(states), _ptr(gout),
                                         _ptr(grad_m), _ptr(grad_b), I(L), I(B), I(P))
     return grad_m, grad_b
+
+
+# ------------------------------------------------------ diagonal (LRU, S5)
+def diag_forward(lambda_bar, b_seq) -> np.ndarray:
+    """Complex states ``[L,B,P]`` of ``x_t = lambda * x_{t-1} + b_t``
+    (lru_scan.cpp:10-58 / s5_scan.cpp:10-66); ``lambda_bar [P]`` complex."""
+    prec = _prec_of(np.asarray(b_seq))
+    rt, ct = _real_dtype(prec), _complex_dtype(prec)
+    b_seq = _c(b_seq, ct)
+    L, B, P = b_seq.shape
+    lam = np.asarray(lambda_bar)
+    lre, lim = _c(lam.real, rt), _c(lam.imag, rt)
+    out = np.empty_like(b_seq)
+    I = ctypes.c_int64
+    _fn("oracle_diag_forward", prec)(_ptr(lre), _ptr(lim), _ptr(b_seq), _ptr(out), I(L), I(B), I(P))
+    return out
+
+
+def diag_backward(lambda_bar, states, grad_output):
+    """``(grad_lambda [P], grad_b [L,B,P])`` restating lru.py:52-80 (s5.py:137-165)."""
+    prec = _prec_of(np.asarray(states))
+    rt, ct = _real_dtype(prec), _complex_dtype(prec)
+    states = _c(states, ct)
+    gout = _c(grad_output, ct)
+    L, B, P = states.shape
+    lam = np.asarray(lambda_bar)
+    lre, lim = _c(lam.real, rt), _c(lam.imag, rt)
+    grad_lambda = np.zeros(P, dtype=ct)
+    grad_b = np.empty_like(states)
+    I = ctypes.c_int64
+    _fn("oracle_diag_backward", prec)(_ptr(lre), _ptr(lim), _ptr(states), _ptr(gout),
+                                      _ptr(grad_lambda), _ptr(grad_b), I(L), I(B), I(P))
+    return grad_lambda, grad_b
 
 
 # --------------------------------------------------------------- selective

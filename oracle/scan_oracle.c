@@ -3,8 +3,9 @@
  *
  * A plain-C restatement of the reference's CPU kernels (loop order, parallel
  * decomposition and arithmetic of src/ossm/csrc/dlinoss_{imex1,imex2,im,ex}.cpp,
- * linoss_scan.cpp, selective_scan_cpu.cpp, and the Python LinOSS backward of
- * models/linoss.py:83-151).  Only tests/, __graft_entry__.smoke() and
+ * linoss_scan.cpp, selective_scan_cpu.cpp, sdlinoss_{imex1,imex2,im,ex}.cpp,
+ * lru_scan.cpp / s5_scan.cpp, and the Python backwards of models/linoss.py:83-151
+ * and models/lru.py:52-80 / s5.py:137-165).  Only tests/, __graft_entry__.smoke() and
  * bench.py's cpu_baseline leg load it, as the checker; the HIP library never
  * links or calls it.
  *

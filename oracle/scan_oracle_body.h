@@ -352,6 +352,83 @@ void SFX(oracle_linoss_backward)(const REAL* m11, const REAL* m12, const REAL* m
 }
 
 /* ------------------------------------------------------------------------ */
+/* Diagonal complex scans (LRU, S5)                                          */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * x_t = lambda_p * x_{t-1} + b_t per (b, p), x_{-1} = 0.  Follows
+ * lru_scan.cpp:10-58 (s5_scan.cpp:10-66 is the same loop): batch rows in
+ * parallel, time outer, state inner; the c10::complex product
+ * (re = lr*xr - li*xi, im = lr*xi + li*xr) and then the add.
+ * lam_re, lam_im: [P]; b_seq, out: [L, B, P] complex.
+ */
+void SFX(oracle_diag_forward)(const REAL* lam_re, const REAL* lam_im, const REAL* b_seq,
+                              REAL* out, int64_t length, int64_t batch, int64_t ssm) {
+  const int64_t series = batch * ssm;
+#pragma omp parallel for schedule(static)
+  for (int64_t b = 0; b < batch; ++b) {
+    REAL* st = (REAL*)calloc((size_t)(ssm > 0 ? 2 * ssm : 1), sizeof(REAL));
+    for (int64_t t = 0; t < length; ++t) {
+      for (int64_t p = 0; p < ssm; ++p) {
+        const int64_t off = 2 * (t * series + b * ssm + p);
+        const REAL lr = lam_re[p], li = lam_im[p];
+        const REAL xr = st[2 * p], xi = st[2 * p + 1];
+        const REAL nr = (lr * xr - li * xi) + b_seq[off];
+        const REAL ni = (lr * xi + li * xr) + b_seq[off + 1];
+        st[2 * p] = nr;
+        st[2 * p + 1] = ni;
+        out[off] = nr;
+        out[off + 1] = ni;
+      }
+    }
+    free(st);
+  }
+}
+
+/*
+ * Backward, restating _LRUScanFn.backward (lru.py:52-80; _S5ScanFn.backward,
+ * s5.py:137-165, is the same loop): for t = L-1..0,  g_t = grad_out_t +
+ * grad_next,  grad_b_t = g_t,  grad_lambda += sum_b g_t * conj(x_{t-1})
+ * (x_{-1} = 0),  grad_next = g_t * conj(lambda).  The per-step batch sum is
+ * formed first and then added, as in the loop.  grad_lambda: [P] complex.
+ */
+void SFX(oracle_diag_backward)(const REAL* lam_re, const REAL* lam_im, const REAL* states,
+                               const REAL* grad_out, REAL* grad_lambda, REAL* grad_b,
+                               int64_t length, int64_t batch, int64_t ssm) {
+  const int64_t series = batch * ssm;
+#pragma omp parallel for schedule(static)
+  for (int64_t p = 0; p < ssm; ++p) {
+    const REAL lr = lam_re[p], li = lam_im[p];
+    REAL accr = 0, acci = 0;
+    REAL* nxt = (REAL*)calloc((size_t)(batch > 0 ? 2 * batch : 1), sizeof(REAL));
+    for (int64_t t = length - 1; t >= 0; --t) {
+      REAL sr = 0, si = 0;
+      for (int64_t b = 0; b < batch; ++b) {
+        const int64_t off = 2 * (t * series + b * ssm + p);
+        const REAL gr = grad_out[off] + nxt[2 * b], gi = grad_out[off + 1] + nxt[2 * b + 1];
+        grad_b[off] = gr;
+        grad_b[off + 1] = gi;
+        REAL xr = 0, xi = 0;
+        if (t > 0) {
+          xr = states[off - 2 * series];
+          xi = states[off - 2 * series + 1];
+        }
+        sr += gr * xr + gi * xi;
+        si += gi * xr - gr * xi;
+        /* g * conj(lambda) */
+        nxt[2 * b] = gr * lr + gi * li;
+        nxt[2 * b + 1] = gi * lr - gr * li;
+      }
+      accr += sr;
+      acci += si;
+    }
+    free(nxt);
+    grad_lambda[2 * p] = accr;
+    grad_lambda[2 * p + 1] = acci;
+  }
+}
+
+/* ------------------------------------------------------------------------ */
 /* Selective scan                                                            */
 /* ------------------------------------------------------------------------ */
 

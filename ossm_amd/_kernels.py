@@ -14,9 +14,9 @@ CPU entry points, e.g. the reference's own ``ossm._kernels`` build); without a
 delegate a CPU call raises RuntimeError, which the reference bridges treat as
 "kernel unavailable".
 
-Export-only names with no HIP implementation in this build (lru_scan, s5_scan,
-linear_rnn_scan) exist so attribute lookups behave like the reference's
-module; on device tensors they raise RuntimeError.
+``linear_rnn_scan`` has no HIP implementation in this build: it exists so
+attribute lookups behave like the reference's module, and on device tensors it
+raises RuntimeError (the reference's bridge then runs its Python loop).
 """
 
 from __future__ import annotations
@@ -41,7 +41,8 @@ __all__ = [
     "sdlinoss_imex2_forward", "sdlinoss_imex2_backward",
     "sdlinoss_im_forward", "sdlinoss_im_backward",
     "sdlinoss_ex_forward", "sdlinoss_ex_backward",
-    "lru_scan", "s5_scan", "linear_rnn_scan",
+    "lru_scan", "s5_scan", "lru_scan_backward", "s5_scan_backward",
+    "linear_rnn_scan",
     "set_cpu_delegate",
 ]
 
@@ -532,9 +533,91 @@ def _export_only(name: str):
     return fn
 
 
-lru_scan = _export_only("lru_scan")
-s5_scan = _export_only("s5_scan")
 linear_rnn_scan = _export_only("linear_rnn_scan")
+
+
+# ------------------------------------------------------ diagonal scans (LRU, S5)
+def _diag_lambda(lambda_real, lambda_imag, state: int, dtype):
+    _check(lambda_real.dim() == 1, "lambda_real must be 1-D")
+    _check(lambda_imag.dim() == 1, "lambda_imag must be 1-D")
+    _check(lambda_real.size(0) == state, "lambda_real must match state dimension")
+    _check(lambda_imag.size(0) == state, "lambda_imag must match state dimension")
+    _check(lambda_real.dtype == dtype and lambda_imag.dtype == dtype,
+           "lambda_real, lambda_imag and b_seq must share one floating dtype")
+    return lambda_real.contiguous(), lambda_imag.contiguous()
+
+
+def _diag_entry(dtype, direction: str):
+    _check(dtype in (torch.float32, torch.float64),
+           f"diagonal scan HIP kernel supports float32 and float64, got {dtype}")
+    suffix = "" if dtype == torch.float32 else "_f64"
+    return getattr(_lib.load(), f"ossm_diag_scan_{direction}{suffix}")
+
+
+def _diag_forward(name: str, lambda_real, lambda_imag, b_seq):
+    """lru_scan.cpp:126-146 / s5_scan.cpp:126-146 (dispatch) with the checks of the
+    CPU path (:68-92); the GPU result is the same recurrence on the device."""
+    if b_seq.size(0) == 0:
+        return torch.empty_like(b_seq)
+    _check(b_seq.dim() == 4,
+           f"b_seq must have shape (length, batch, state, 2), got {list(b_seq.shape)}")
+    if not b_seq.is_cuda:
+        return _delegate(name, lambda_real, lambda_imag, b_seq)
+    _check(b_seq.size(-1) == 2, "b_seq must have shape (length, batch, state, 2)")
+    _on_device(lambda_real, lambda_imag, b_seq)
+    length, batch, state, _ = b_seq.shape
+    lre, lim = _diag_lambda(lambda_real, lambda_imag, state, b_seq.dtype)
+    fn = _diag_entry(b_seq.dtype, "forward")
+    b_seq = b_seq.contiguous()
+    result = torch.empty_like(b_seq)
+    with torch.cuda.device(b_seq.device):
+        _lib.check(fn(lre.data_ptr(), lim.data_ptr(), b_seq.data_ptr(), result.data_ptr(),
+                      length, batch, state, _lib.stream_of(b_seq)))
+    return result
+
+
+def _diag_backward(lambda_real, lambda_imag, states, grad_output):
+    """Native backward of the diagonal scan, in the layout of the forward:
+    ``[grad_lambda [P,2], grad_b [L,B,P,2]]`` (real views of complex tensors).
+    The reference runs it as a Python loop (lru.py:52-80, s5.py:137-165)."""
+    _check(states.dim() == 4 and states.size(-1) == 2,
+           "states must have shape (length, batch, state, 2)")
+    _check(grad_output.shape == states.shape, "grad_output must match states shape")
+    _check(states.is_cuda, "diagonal scan backward: HIP path needs device tensors")
+    _on_device(lambda_real, lambda_imag, states, grad_output)
+    length, batch, state, _ = states.shape
+    _check(grad_output.dtype == states.dtype, "grad_output must match the dtype of states")
+    lre, lim = _diag_lambda(lambda_real, lambda_imag, state, states.dtype)
+    fn = _diag_entry(states.dtype, "backward")
+    states = states.contiguous()
+    grad_output = grad_output.contiguous()
+    grad_lambda = torch.empty((state, 2), dtype=states.dtype, device=states.device)
+    grad_b = torch.empty_like(grad_output)
+    with torch.cuda.device(states.device):
+        _lib.check(fn(lre.data_ptr(), lim.data_ptr(), states.data_ptr(), grad_output.data_ptr(),
+                      grad_lambda.data_ptr(), grad_b.data_ptr(), length, batch, state,
+                      _lib.stream_of(states)))
+    return [grad_lambda, grad_b]
+
+
+def lru_scan(lambda_real, lambda_imag, b_seq):
+    """``x_t = lambda * x_{t-1} + b_t`` over ``b_seq [L,B,P,2]`` (lru_scan.cpp:126-146)."""
+    return _diag_forward("lru_scan", lambda_real, lambda_imag, b_seq)
+
+
+def s5_scan(lambda_real, lambda_imag, b_seq):
+    """Same recurrence under the S5 name (s5_scan.cpp:126-146)."""
+    return _diag_forward("s5_scan", lambda_real, lambda_imag, b_seq)
+
+
+def lru_scan_backward(lambda_real, lambda_imag, states, grad_output):
+    """Native backward of :func:`lru_scan` (no counterpart in the reference module)."""
+    return _diag_backward(lambda_real, lambda_imag, states, grad_output)
+
+
+def s5_scan_backward(lambda_real, lambda_imag, states, grad_output):
+    """Native backward of :func:`s5_scan` (no counterpart in the reference module)."""
+    return _diag_backward(lambda_real, lambda_imag, states, grad_output)
 
 
 def _load_now() -> List[str]:

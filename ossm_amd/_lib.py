@@ -57,6 +57,14 @@ _SIGNATURES = {
         ctypes.c_int,
         [_vp, _vp, _vp, _fp, _vp, _vp, _vp, _fp, _vp, _vp, _vp, _fp, _vp, _vp, _vp, _c_int64,
          _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_diag_scan_forward": (
+        ctypes.c_int, [_fp, _fp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_diag_scan_backward": (
+        ctypes.c_int, [_fp, _fp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_diag_scan_forward_f64": (
+        ctypes.c_int, [_fp, _fp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_diag_scan_backward_f64": (
+        ctypes.c_int, [_fp, _fp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -13,6 +13,11 @@ kernel bridges (the L2 layer above ``ossm._kernels``):
 * Selective scan: ``try_selective_scan`` and ``SelectiveScanFn``
   (_selective_scan.py:127-297): fp32 only, the no-grad shortcut, the
   ``(out, chunk_states, raw_out)`` forward saved for the backward.
+* Diagonal scans (LRU, S5): ``try_run_lru_scan`` / ``try_run_s5_scan``
+  (_lru_scan.py:21-40, _s5_scan.py:21-40) over ``DiagScanFn``, which saves
+  ``(lambda_bar, states)`` like _LRUScanFn / _S5ScanFn (lru.py:33-80,
+  s5.py:118-165) and runs the backward on the device instead of their Python
+  loop over time.
 
 Differences from the reference bridges, on purpose: there is no pure-PyTorch
 fallback and no swallowed RuntimeError.  A missing library is an ImportError
@@ -35,6 +40,7 @@ __all__ = [
     "has_kernels", "extension_error", "run_dlinoss", "run_dlinoss_imex1", "DlinossFn",
     "run_sdlinoss", "SdlinossFn",
     "try_run_scan", "LinossScanFn", "try_selective_scan", "SelectiveScanFn",
+    "DiagScanFn", "try_run_lru_scan", "try_run_s5_scan",
 ]
 
 SUPPORTED_VARIANTS = ("imex1", "imex2", "im", "ex")
@@ -212,3 +218,51 @@ def try_selective_scan(inputs: Tensor, dt: Tensor, A: Tensor, B: Tensor, C: Tens
         return _kernels.selective_scan_cuda(inputs, dt, A, B, C, gate, chunk_length)[0]
     return SelectiveScanFn.apply(inputs, dt, A, B, C, gate, chunk_length)
 
+
+# ------------------------------------------------------ diagonal scans (LRU, S5)
+class DiagScanFn(torch.autograd.Function):
+    """``x_t = lambda_bar * x_{t-1} + b_t`` over complex ``b_seq [L, B, P]``
+    (reference _LRUScanFn / _S5ScanFn, lru.py:33-80, s5.py:118-165): the forward
+    saves ``(lambda_bar, states)``; the backward returns ``(grad_lambda,
+    grad_b)`` from the device kernel (grad_b_t = g_t with g_t = grad_t +
+    conj(lambda_bar) g_{t+1}; grad_lambda = sum over t, b of g_t conj(x_{t-1}))."""
+
+    @staticmethod
+    def forward(ctx, name: str, lambda_bar: Tensor, b_seq: Tensor) -> Tensor:  # type: ignore[override]
+        if b_seq.size(0) == 0:
+            ctx.save_for_backward(lambda_bar, b_seq)
+            return b_seq
+        fwd = _kernels.lru_scan if name == "lru" else _kernels.s5_scan
+        lam = lambda_bar.resolve_conj()
+        result = fwd(lam.real.contiguous(), lam.imag.contiguous(),
+                     torch.view_as_real(b_seq.contiguous()))
+        states = torch.view_as_complex(result)
+        ctx.save_for_backward(lambda_bar, states)
+        return states
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):  # type: ignore[override]
+        lambda_bar, states = ctx.saved_tensors
+        if grad_output.size(0) == 0:
+            return None, torch.zeros_like(lambda_bar), grad_output
+        lam = lambda_bar.resolve_conj()
+        grad_lambda, grad_b = _kernels.lru_scan_backward(
+            lam.real.contiguous(), lam.imag.contiguous(), torch.view_as_real(states),
+            torch.view_as_real(grad_output.resolve_conj().contiguous()))
+        return None, torch.view_as_complex(grad_lambda), torch.view_as_complex(grad_b)
+
+
+def try_run_lru_scan(lambda_bar: Tensor, b_seq: Tensor) -> Tensor:
+    """Complex states ``[L, B, P]`` of the LRU scan (reference try_run_lru_scan,
+    _lru_scan.py:21-40), differentiable through the native backward."""
+    if b_seq.numel() == 0:
+        return b_seq
+    return DiagScanFn.apply("lru", lambda_bar, b_seq)
+
+
+def try_run_s5_scan(lambda_bar: Tensor, b_seq: Tensor) -> Tensor:
+    """Complex states ``[L, B, P]`` of the S5 scan (reference try_run_s5_scan,
+    _s5_scan.py:21-40), differentiable through the native backward."""
+    if b_seq.numel() == 0:
+        return b_seq
+    return DiagScanFn.apply("s5", lambda_bar, b_seq)

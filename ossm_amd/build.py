@@ -23,7 +23,8 @@ LIBDIR = PKG / "_lib"
 OBJDIR = PKG / "_build"
 LIB = LIBDIR / "libossm_scan.so"
 
-SOURCES = ["runtime.cpp", "oscillator_scan.hip", "selective_scan.hip", "sdlinoss_scan.hip"]
+SOURCES = ["runtime.cpp", "oscillator_scan.hip", "selective_scan.hip", "sdlinoss_scan.hip",
+           "diag_scan.hip"]
 ARCH = "gfx950"
 
 
@@ -51,8 +52,6 @@ def _compile(src: str) -> Path:
     OBJDIR.mkdir(parents=True, exist_ok=True)
     obj = OBJDIR / (Path(src).stem + ".o")
     cmd = [hipcc(), *_flags(), "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
-    if src.endswith(".cpp"):
-        cmd = [hipcc(), *_flags(), "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")

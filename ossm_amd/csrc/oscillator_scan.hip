@@ -45,6 +45,7 @@
 #include "../../include/ossm_scan.h"
 #include "runtime.hpp"
 #include "scan_device.hpp"
+#include "scan_reduce.hpp"
 
 namespace ossm {
 namespace {
@@ -312,21 +313,6 @@ struct Linoss {
     for (int j = 0; j < 8; ++j) grad_m[8 * p + j] = static_cast<float>(S[j]);
   }
 };
-
-
-// Row t of a [L, nc] tensor, from the first channel of channel group g.  t,
-// nc and g are uniform across the wave, so the pointer is a scalar and each
-// lane adds only its 32-bit lane offset.
-template <class E>
-__device__ __forceinline__ E* group_row(E* base, long long t, int nc, int g) {
-  return base + static_cast<size_t>(t) * nc + static_cast<size_t>(g) * kWave;
-}
-
-// The lane's offset within its group, clamped onto the group's last channel
-// for lanes past the end (their loads stay in bounds; results are unused).
-__device__ __forceinline__ unsigned clamped_lane(int g, int nc) {
-  return static_cast<unsigned>(min(static_cast<int>(threadIdx.x & (kWave - 1)), nc - 1 - g * kWave));
-}
 
 // ============================================================================
 // Forward kernel
@@ -682,62 +668,8 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
 // ============================================================================
 // Per-oscillator parameter gradients from the chunk partials
 // ============================================================================
-// The partials form, for each sum j, a matrix of R = n_chunks * B rows
-// (chunk c, batch row b) by P columns (oscillator p): address
-// (c * NS + j) * nc + b * P + p.  Column sums in two passes:
-//   pass 1: block (column tile of 64, row group g) sums rows r = g*4 + w + k*4G
-//           (w = wave) in fp64, four rows in flight per lane, waves combined
-//           through LDS -> colsum[g][j][p];
-//   pass 2: one wave per oscillator, lane g holding row group g, adds them
-//           by a butterfly over the wave, then the chain rule.
-// Fixed order everywhere (no atomics).
-constexpr int kRowGroups = kWave;
-constexpr int kColsumRows = 4;  // rows per lane per round (independent loads)
-
-template <int NS>
-__global__ __launch_bounds__(256) void osc_colsum_kernel(const float* __restrict__ partials,
-                                                         double* __restrict__ colsum, int P,
-                                                         int B, int n_chunks) {
-  __shared__ double s_red[4][NS][kWave];
-  const int lane = threadIdx.x & (kWave - 1), w = wave_id();
-  const int p = blockIdx.x * kWave + lane;
-  const int pc = min(p, P - 1);
-  const int g = blockIdx.y;
-  const size_t nc = static_cast<size_t>(B) * P;
-  const int R = n_chunks * B;
-  constexpr int kStride = kRowGroups * 4;
-  double acc[NS];
-#pragma unroll
-  for (int j = 0; j < NS; ++j) acc[j] = 0.0;
-  for (int r0 = g * 4 + w; r0 < R; r0 += kStride * kColsumRows) {
-    float v[kColsumRows][NS];
-#pragma unroll
-    for (int u = 0; u < kColsumRows; ++u) {
-      const int r = min(r0 + u * kStride, R - 1);
-      const int c = r / B, b = r - c * B;
-      const float* src = partials + static_cast<size_t>(c) * NS * nc + static_cast<size_t>(b) * P + pc;
-#pragma unroll
-      for (int j = 0; j < NS; ++j) v[u][j] = src[j * nc];
-    }
-#pragma unroll
-    for (int u = 0; u < kColsumRows; ++u)
-      if (r0 + u * kStride < R) {
-#pragma unroll
-        for (int j = 0; j < NS; ++j) acc[j] += static_cast<double>(v[u][j]);
-      }
-  }
-#pragma unroll
-  for (int j = 0; j < NS; ++j) s_red[w][j][lane] = acc[j];
-  __syncthreads();
-  if (w == 0 && p < P) {
-#pragma unroll
-    for (int j = 0; j < NS; ++j)
-      colsum[(static_cast<size_t>(g) * NS + j) * P + p] =
-          ((s_red[0][j][lane] + s_red[1][j][lane]) + s_red[2][j][lane]) + s_red[3][j][lane];
-  }
-}
-
-// 256 threads = four oscillators per block.
+// Pass 2 of the column reduction (osc_colsum_kernel gives pass 1): one wave
+// per oscillator, 256 threads = four oscillators per block.
 template <class Model>
 __global__ __launch_bounds__(256) void osc_param_kernel(typename Model::Params prm,
                                                         const double* __restrict__ colsum, int P,
@@ -756,20 +688,6 @@ __global__ __launch_bounds__(256) void osc_param_kernel(typename Model::Params p
   }
   if (lane != 0) return;
   Model::epilogue(prm, p, S, out0, out1, out2);
-}
-
-// Zero-fill used where the reference returns zero gradients (empty scans);
-// a kernel rather than hipMemsetAsync so the call can sit in a captured graph.
-__global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0.f;
-}
-
-int fill_zero(float* p, int64_t n, hipStream_t stream) {
-  if (n <= 0) return OSSM_OK;
-  const int64_t blocks = (n + 255) / 256;
-  hipLaunchKernelGGL(fill_zero_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, p, n);
-  return launch_check("fill_zero_kernel");
 }
 
 // T steps per lane, W waves per workgroup, OCC = minimum waves per SIMD the
@@ -885,11 +803,7 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
     release_unlaunched(stream, total);
     return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_BWD names no built tile");
   }
-  hipLaunchKernelGGL(osc_colsum_kernel<NS>,
-                     dim3(static_cast<unsigned>((P + kWave - 1) / kWave), kRowGroups), dim3(256), 0,
-                     stream, red.partials, colsum, static_cast<int>(P), static_cast<int>(B),
-                     static_cast<int>(n_chunks));
-  if (int rc = launch_check("osc_colsum_kernel")) return rc;
+  if (int rc = launch_colsum<NS>(red.partials, colsum, P, B, n_chunks, stream)) return rc;
   hipLaunchKernelGGL(osc_param_kernel<Model>, dim3(static_cast<unsigned>((P + 3) / 4)),
                      dim3(256), 0, stream, prm, colsum, static_cast<int>(P), out0, out1, out2);
   return launch_check("osc_param_kernel");

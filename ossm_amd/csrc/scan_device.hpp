@@ -277,4 +277,18 @@ __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
 }
 
+// Row t of a [L, nc] tensor, from the first channel of channel group g.  t,
+// nc and g are uniform across the wave, so the pointer is a scalar and each
+// lane adds only its 32-bit lane offset.
+template <class E>
+__device__ __forceinline__ E* group_row(E* base, long long t, int nc, int g) {
+  return base + static_cast<size_t>(t) * nc + static_cast<size_t>(g) * kWave;
+}
+
+// The lane's offset within its group, clamped onto the group's last channel
+// for lanes past the end (their loads stay in bounds; results are unused).
+__device__ __forceinline__ unsigned clamped_lane(int g, int nc) {
+  return static_cast<unsigned>(min(static_cast<int>(threadIdx.x & (kWave - 1)), nc - 1 - g * kWave));
+}
+
 }  // namespace ossm

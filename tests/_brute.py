@@ -118,3 +118,13 @@ def sdlinoss_states(variant: str, A, G, step, bu):
         x = x + w
         out.append(torch.stack([w, x], -1))
     return torch.stack(out, 0)
+
+
+def diag_states(lam, b_seq):
+    """x_t = lam * x_{t-1} + b_t over complex b_seq [L, B, P] with complex lam [P]."""
+    x = torch.zeros_like(b_seq[0])
+    out = []
+    for t in range(b_seq.shape[0]):
+        x = lam * x + b_seq[t]
+        out.append(x)
+    return torch.stack(out, 0)

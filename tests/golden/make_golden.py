@@ -14,11 +14,16 @@ Three kinds of data, none of it reference source:
    scan forward, selective scan forward/backward with and without the gate.
 4. ``sdl_kernel_vectors.npz`` — the same for the selective D-LinOSS kernels
    (every variant, every accepted parameter layout, both clamps exercised).
+5. ``diag_kernel_vectors.npz`` — the reference's ``lru_scan`` and ``s5_scan`` CPU
+   kernels (lru_scan.cpp, s5_scan.cpp) in fp32 and fp64 on a ragged shape.
+6. ``complex_scan_reference.json`` — the numbers of the reference's
+   ``REFERENCE_COMPLEX_{LAMBDA,B,STATES}`` (tests/test_scan_parity.py:186-349),
+   read as text with ``ast`` and stored as [re, im] pairs.
 
 Usage (from the repository root, with /root/reference present and
 ``make -f oracle/Makefile.ref`` done):
 
-    python tests/golden/make_golden.py [dlinoss] [linoss] [kernels] [sdlinoss]
+    python tests/golden/make_golden.py [dlinoss] [linoss] [kernels] [sdlinoss] [diag] [complex]
 
 (no argument: all).  The reference's OpenMP kernels add some sums in a
 thread-dependent order, so regenerating a fixture changes its last bits.
@@ -170,6 +175,54 @@ def _sdl_kernel_vectors() -> None:
     np.savez_compressed(OUT / "sdl_kernel_vectors.npz", **vec)
 
 
+def _diag_kernel_vectors() -> None:
+    """Diagonal scans: lru_scan / s5_scan of the reference's CPU build on a ragged
+    shape, eigenvalues inside the unit disc (some close to it, some negative or
+    purely imaginary), in fp32 and fp64."""
+    import torch
+
+    import oracle
+
+    ref = oracle.reference_module()
+    assert ref is not None, "build oracle/_ref first: make -f oracle/Makefile.ref"
+    rng = np.random.default_rng(20240611)
+    L, B, P = 37, 3, 7
+    radius = np.array([0.0, 0.3, 0.9, 0.99, 0.999, 0.6, 0.5])
+    angle = np.array([0.0, 2.5, -0.4, 0.05, np.pi, np.pi / 2, -3.0])
+    lam = radius * np.exp(1j * angle)
+    b = rng.normal(size=(L, B, P)) + 1j * rng.normal(size=(L, B, P))
+    vec: dict[str, np.ndarray] = {}
+    for prec, ct in (("f32", np.complex64), ("f64", np.complex128)):
+        lc = lam.astype(ct)
+        bc = b.astype(ct)
+        T = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+        args = (T(lc.real), T(lc.imag), torch.view_as_real(T(bc)).contiguous())
+        vec[f"{prec}_lambda"], vec[f"{prec}_b"] = lc, bc
+        vec[f"{prec}_lru"] = torch.view_as_complex(ref.lru_scan(*args).contiguous()).numpy()
+        vec[f"{prec}_s5"] = torch.view_as_complex(ref.s5_scan(*args).contiguous()).numpy()
+    np.savez_compressed(OUT / "diag_kernel_vectors.npz", **vec)
+
+
+def _extract_complex_reference() -> None:
+    text = (REF / "tests" / "test_scan_parity.py").read_text()
+    tree = ast.parse(text)
+    want = ("REFERENCE_COMPLEX_LAMBDA", "REFERENCE_COMPLEX_B", "REFERENCE_COMPLEX_STATES")
+    data = {}
+    for node in tree.body:
+        if isinstance(node, ast.Assign):
+            for t in node.targets:
+                if isinstance(t, ast.Name) and t.id in want:
+                    arr = np.asarray(_tensor_literal(node.value), dtype=np.complex128)
+                    data[t.id] = np.stack([arr.real, arr.imag], axis=-1).tolist()
+    assert set(data) == set(want), f"literals not found: {set(want) - set(data)}"
+    data["_provenance"] = (
+        "numbers of REFERENCE_COMPLEX_LAMBDA / _B / _STATES, reference "
+        "tests/test_scan_parity.py:186-349 (complex64 literals, stored as [re, im]); "
+        "states = lru_scan / s5_scan of lambda over b (test at :465-474, atol=rtol=5e-6)"
+    )
+    (OUT / "complex_scan_reference.json").write_text(json.dumps(data))
+
+
 def main() -> None:
     only = sys.argv[1:]
     if not only or "dlinoss" in only:
@@ -180,6 +233,10 @@ def main() -> None:
         _ref_kernel_vectors()
     if not only or "sdlinoss" in only:
         _sdl_kernel_vectors()
+    if not only or "diag" in only:
+        _diag_kernel_vectors()
+    if not only or "complex" in only:
+        _extract_complex_reference()
     for p in sorted(OUT.iterdir()):
         print(f"{p.name:40s} {p.stat().st_size:>10d} B")
 

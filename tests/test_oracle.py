@@ -337,3 +337,71 @@ def test_sdlinoss_stiff_clamp_matches_fp64_autograd():
                                (gbu, tbu.grad, "bu")):
             ref = ref.numpy()
             _close(got, ref, 1e-9, 1e-9 * np.abs(ref).max(), f"{variant} grad_{name}")
+
+
+# ------------------------------------------------------ diagonal scans (LRU, S5)
+@pytest.fixture(scope="module")
+def diag_vectors():
+    with np.load(GOLDEN / "diag_kernel_vectors.npz", allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.mark.parametrize("prec", ["f32", "f64"])
+def test_diag_forward_matches_reference_kernel_vectors(prec, diag_vectors):
+    """lru_scan and s5_scan of the reference's CPU build (fixture) agree with the
+    restatement; eigenvalues from 0 to 0.999 in modulus, real, negative, imaginary."""
+    v = diag_vectors
+    got = oracle.diag_forward(v[f"{prec}_lambda"], v[f"{prec}_b"])
+    tol = 1e-6 if prec == "f32" else 1e-13
+    for name in ("lru", "s5"):
+        _close(got, v[f"{prec}_{name}"], tol, tol, name)
+
+
+def test_diag_forward_matches_reference_complex_literal():
+    """The reference test's own literals (test_scan_parity.py:186-349, checked there at
+    atol = rtol = 5e-6, :465-474)."""
+    d = json.loads((GOLDEN / "complex_scan_reference.json").read_text())
+    c = lambda k: np.asarray(d[k])[..., 0] + 1j * np.asarray(d[k])[..., 1]  # noqa: E731
+    lam = c("REFERENCE_COMPLEX_LAMBDA").astype(np.complex64)
+    b = c("REFERENCE_COMPLEX_B").astype(np.complex64)
+    _close(oracle.diag_forward(lam, b), c("REFERENCE_COMPLEX_STATES"), 5e-6, 5e-6)
+
+
+def test_diag_backward_matches_fp64_autograd():
+    """The restated Python backward (lru.py:52-80) against autograd of the plain
+    loop, which the reference's own test uses as its oracle (test_scan_parity.py:352-370):
+    a dropped conj on lambda or x, or a shifted x_{t-1}, fails here."""
+    rng = np.random.default_rng(11)
+    L, B, P = 23, 3, 5
+    lam = (rng.uniform(0.2, 0.95, P) * np.exp(1j * rng.uniform(-np.pi, np.pi, P)))
+    b = rng.normal(size=(L, B, P)) + 1j * rng.normal(size=(L, B, P))
+    G = rng.normal(size=(L, B, P)) + 1j * rng.normal(size=(L, B, P))
+    tl = torch.tensor(lam, requires_grad=True)
+    tb = torch.tensor(b, requires_grad=True)
+    x = _brute.diag_states(tl, tb)
+    gl, gb = torch.autograd.grad(x, (tl, tb), grad_outputs=torch.tensor(G))
+    states = oracle.diag_forward(lam, b)
+    _close(states, x.detach().numpy(), 1e-12, 1e-12, "states")
+    ol, ob = oracle.diag_backward(lam, states, G)
+    _close(ol, gl.numpy(), 1e-10, 1e-10, "grad_lambda")
+    _close(ob, gb.numpy(), 1e-10, 1e-10, "grad_b")
+
+
+def test_diag_special_cases():
+    """lambda = 0: x = b and grad_lambda = sum_t g_t conj(b_{t-1}); one step: grad_b =
+    grad, grad_lambda = 0; lambda = 1: x is the running sum of b."""
+    rng = np.random.default_rng(3)
+    L, B, P = 9, 2, 4
+    b = rng.normal(size=(L, B, P)) + 1j * rng.normal(size=(L, B, P))
+    G = rng.normal(size=(L, B, P)) + 1j * rng.normal(size=(L, B, P))
+    zero = np.zeros(P, complex)
+    x = oracle.diag_forward(zero, b)
+    _close(x, b, 0, 0, "lambda=0 states")
+    gl, gb = oracle.diag_backward(zero, x, G)
+    _close(gb, G, 0, 0, "lambda=0 grad_b")
+    _close(gl, (G[1:] * np.conj(b[:-1])).sum(axis=(0, 1)), 1e-12, 1e-12, "lambda=0 grad_lambda")
+    gl1, gb1 = oracle.diag_backward(zero + 0.5, b[:1], G[:1])
+    _close(gl1, np.zeros(P), 0, 0, "one step grad_lambda")
+    _close(gb1, G[:1], 0, 0, "one step grad_b")
+    _close(oracle.diag_forward(np.ones(P, complex), b), np.cumsum(b, axis=0), 1e-12, 1e-12,
+           "lambda=1 running sum")
