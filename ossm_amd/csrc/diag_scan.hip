@@ -22,8 +22,8 @@
 //             stores grad_b and accumulates g_t conj(x_{t-1}) per lane from the
 //             saved states.  HBM: read grad + states, write grad_b (24 B per
 //             state-step).  Per-(chunk, channel) sums are reduced to
-//             grad_lambda[P] by a two-pass column reduction in fp64 in a fixed
-//             order (no atomics).
+//             grad_lambda[P] by one column-sum launch (64 row groups in fp64 in
+//             a fixed order, added into grad_lambda with float atomics).
 //
 // Records carry a complex value as 32-bit payload words, each in a 64-bit word
 // with the launch tag in its high half (2 words in fp32, 4 in fp64: a double
@@ -349,8 +349,9 @@ __global__ __launch_bounds__(W * kWave) void diag_forward_kernel(
 template <class R, int T, int W>
 __global__ __launch_bounds__(W * kWave) void diag_backward_kernel(
     const R* __restrict__ lam_re, const R* __restrict__ lam_im, int P, const Cx<R>* states,
-    const Cx<R>* __restrict__ gout, Cx<R>* __restrict__ gin, R* __restrict__ partials, int L,
-    int nc, int n_groups, int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
+    const Cx<R>* __restrict__ gout, Cx<R>* __restrict__ gin, R* __restrict__ partials,
+    ZeroFill zero, int L, int nc, int n_groups, int n_chunks, unsigned long long* __restrict__ rec,
+    LaunchSync sync) {
   using V = Cx<R>;
   __shared__ V s_agg[W][kWave];
   __shared__ V s_carry[kWave];
@@ -361,6 +362,7 @@ __global__ __launch_bounds__(W * kWave) void diag_backward_kernel(
   const int w = wave_id();
   const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
   if (ticket < 0) return;
+  if (ticket == 0) zero_fill_block(zero);  // grad_lambda, for column_sum_kernel
   const int cr = ticket / n_groups;
   const int g = ticket - cr * n_groups;
   const int c = n_chunks - 1 - cr;
@@ -457,26 +459,15 @@ __global__ __launch_bounds__(W * kWave) void diag_backward_kernel(
   }
 }
 
-// Pass 2 of the grad_lambda reduction: one wave per state column (256 threads
-// = four columns per block), lane g holding row group g's fp64 sums.
+// grad_lambda[p] += one row group's two column sums (column_sum_kernel).
 template <class R>
-__global__ __launch_bounds__(256) void diag_lambda_kernel(const double* __restrict__ colsum, int P,
-                                                          R* __restrict__ grad_lambda) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int p = blockIdx.x * 4 + wave_id();
-  if (p >= P) return;
-  double re = colsum[(static_cast<size_t>(lane) * 2 + 0) * P + p];
-  double im = colsum[(static_cast<size_t>(lane) * 2 + 1) * P + p];
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    re += __shfl_xor(re, off, kWave);
-    im += __shfl_xor(im, off, kWave);
+struct DiagEpilogue {
+  R* grad_lambda;  // [P] complex as (re, im), zeroed by the scan kernel
+  __device__ void add(int p, const double* S) const {
+    atomic_put(grad_lambda + 2 * p, S[0]);
+    atomic_put(grad_lambda + 2 * p + 1, S[1]);
   }
-  if (lane == 0) {
-    grad_lambda[2 * p] = static_cast<R>(re);
-    grad_lambda[2 * p + 1] = static_cast<R>(im);
-  }
-}
+};
 
 // ============================================================================
 // Host side
@@ -576,21 +567,21 @@ int diag_backward_impl(const R* lam_re, const R* lam_im, const void* states, con
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * CxOf<R>::kWords * nc * sizeof(unsigned long long);
   const size_t part_bytes =
       (static_cast<size_t>(n_chunks) * 2 * nc * sizeof(R) + 255) & ~static_cast<size_t>(255);
-  const size_t tot_bytes = static_cast<size_t>(kRowGroups) * 2 * P * sizeof(double);
   void* ws = nullptr;
-  if (int rc = acquire_workspace(stream, part_bytes + tot_bytes, &ws)) return rc;
+  if (int rc = acquire_workspace(stream, part_bytes, &ws)) return rc;
   R* partials = static_cast<R*>(ws);
-  double* colsum = reinterpret_cast<double*>(static_cast<char*>(ws) + part_bytes);
   void* payload = nullptr;
   LaunchSync sync{};
   if (int rc = acquire_scratch(stream, rec_bytes, total, &payload, &sync)) return rc;
+  const ZeroFill zero{{reinterpret_cast<float*>(grad_lambda), nullptr, nullptr},
+                      static_cast<int>(2 * P * (sizeof(R) / sizeof(float)))};
   bool launched = false;
 #define OSSM_LAUNCH_DIAG_BWD(TT, WW)                                                              \
   if (!launched && tile.T == TT && tile.W == WW) {                                                \
     hipLaunchKernelGGL((diag_backward_kernel<R, TT, WW>), dim3(static_cast<unsigned>(total)),     \
                        dim3(WW * kWave), 0, stream, lam_re, lam_im, static_cast<int>(P),          \
                        static_cast<const Cx<R>*>(states), static_cast<const Cx<R>*>(gout),        \
-                       static_cast<Cx<R>*>(grad_b), partials, static_cast<int>(L),                \
+                       static_cast<Cx<R>*>(grad_b), partials, zero, static_cast<int>(L),          \
                        static_cast<int>(nc), static_cast<int>(n_groups),                          \
                        static_cast<int>(n_chunks), static_cast<unsigned long long*>(payload), sync); \
     launched = true;                                                                              \
@@ -609,10 +600,7 @@ int diag_backward_impl(const R* lam_re, const R* lam_im, const void* states, con
     release_unlaunched(stream, total);
     return rc;
   }
-  if (int rc = launch_colsum<2>(partials, colsum, P, B, n_chunks, stream)) return rc;
-  hipLaunchKernelGGL(diag_lambda_kernel<R>, dim3(static_cast<unsigned>((P + 3) / 4)), dim3(256), 0,
-                     stream, colsum, static_cast<int>(P), grad_lambda);
-  return launch_check("diag_lambda_kernel");
+  return launch_column_sums<2>(partials, P, B, n_chunks, DiagEpilogue<R>{grad_lambda}, stream);
 }
 
 template <class R>

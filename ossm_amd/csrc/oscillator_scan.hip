@@ -24,12 +24,16 @@
 //   backwards with the transposed transition.  States s_{t-1} needed by the
 //   parameter gradients are recomputed in registers from the checkpoint
 //   states[t0 - 1] instead of reading the whole trajectory.  Per-lane sums of
-//   <mu_i, s_j,t-1> and <mu_i, bu_t> go to a partials buffer; two small
-//   kernels add them over time chunks and batch rows per oscillator (a
-//   column reduction) and apply each variant's chain rule to (a, g, dt).  Every sum
-//   runs in a fixed order in fp64, with no atomics.  (A
-//   last-workgroup-done reduction inside the scan kernel was measured 3x
-//   slower: each agent-scope release fence writes back the XCD's L2.)
+//   <mu_i, s_j,t-1> and <mu_i, bu_t> go to a partials buffer; one small
+//   kernel adds them over time chunks and batch rows per oscillator in 64 row
+//   groups (fixed order, fp64), applies each variant's chain rule (linear in
+//   the sums) to every group's share and adds the shares into grad a, g, dt
+//   with float atomics (scan_reduce.hpp).  (A last-workgroup-done reduction
+//   inside the scan kernel was measured 3x slower: each agent-scope release
+//   fence writes back the XCD's L2, dirty with the workgroup's grad_bu rows;
+//   a fixed tree of tagged records over chunks inside the scan, which needs no
+//   fence, cost the scan kernel as much as it saved, the reducing workgroups
+//   holding their CU while they gather.)
 
 #include <hip/hip_runtime.h>
 
@@ -208,7 +212,9 @@ struct Dlinoss {
   // imex1 dlinoss_imex1.cpp:219-232, im dlinoss_im.cpp:236-263, imex2 / ex by
   // differentiating the coefficient tables of dlinoss_imex2.cpp:35-47 /
   // dlinoss_ex.cpp:33-42 (the terms the reference accumulates per step).
-  // out0/1/2 = grad_a, grad_g, grad_step.
+  // out0/1/2 = grad_a, grad_g, grad_step.  Linear in S: applied to a share of
+  // the sums, it adds that share's contribution to the outputs.
+  static constexpr int kOutsPerColumn = 1;
   static __device__ void epilogue(const Params& prm, int p, const double* S, float* grad_a,
                                   float* grad_g, float* grad_step) {
     const double a = prm.a[p], g = prm.g[p], dt = prm.dt[p];
@@ -255,9 +261,9 @@ struct Dlinoss {
       gg = -dt * G00;
       gs = -g * G00 - a * G01 + F0G10;
     }
-    grad_a[p] = static_cast<float>(ga);
-    grad_g[p] = static_cast<float>(gg);
-    grad_step[p] = static_cast<float>(gs);
+    atomic_put(grad_a + p, ga);
+    atomic_put(grad_g + p, gg);
+    atomic_put(grad_step + p, gs);
   }
 };
 
@@ -306,11 +312,12 @@ struct Linoss {
     acc[6] += g.z * sp.z + g.w * sp.w;  acc[7] += g.w * sp.z - g.z * sp.w;  // m22
   }
 
-  // grad_m [P, 2, 2] complex = the summed products themselves (out0).
+  // grad_m [P, 2, 2] complex = the summed products themselves (out0), added.
+  static constexpr int kOutsPerColumn = 8;
   static __device__ void epilogue(const Params&, int p, const double* S, float* grad_m, float*,
                                   float*) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) grad_m[8 * p + j] = static_cast<float>(S[j]);
+    for (int j = 0; j < 8; ++j) atomic_put(grad_m + 8 * p + j, S[j]);
   }
 };
 
@@ -640,7 +647,7 @@ template <class Model, int T, int W, int OCC, int H>
 __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
     typename Model::Params prm, const typename Model::In* __restrict__ in,
     const float4* states, const typename Model::GIn* __restrict__ gout,
-    typename Model::GOut* __restrict__ gin, ParamReduce red, int L, int nc,
+    typename Model::GOut* __restrict__ gin, ParamReduce red, ZeroFill zero, int L, int nc,
     int n_groups, int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
   constexpr int NS = Model::kSums;
   __shared__ float4 s_agg[W][kWave];
@@ -652,6 +659,7 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
   __shared__ int s_ticket;
   const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
   if (ticket < 0) return;
+  if (ticket == 0) zero_fill_block(zero);  // the parameter-gradient outputs, for column_sum_kernel
   const BwdTicket k = bwd_ticket<T, W>(ticket, n_groups, n_chunks, nc);
   BwdBuf<Model, T> b;
   bwd_load<Model, T, W>(b, k, prm, in, states, gout, L, nc);
@@ -666,29 +674,19 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
 }
 
 // ============================================================================
-// Per-oscillator parameter gradients from the chunk partials
+// Per-oscillator parameter gradients from the column sums
 // ============================================================================
-// Pass 2 of the column reduction (osc_colsum_kernel gives pass 1): one wave
-// per oscillator, 256 threads = four oscillators per block.
+// column_sum_kernel calls this with each oscillator's NS sums over one row
+// group of (time chunk, batch row): the variant's chain rule, added into the
+// outputs.
 template <class Model>
-__global__ __launch_bounds__(256) void osc_param_kernel(typename Model::Params prm,
-                                                        const double* __restrict__ colsum, int P,
-                                                        float* out0, float* out1, float* out2) {
-  constexpr int NS = Model::kSums;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int p = blockIdx.x * 4 + wave_id();
-  if (p >= P) return;
-  double S[NS];
-#pragma unroll
-  for (int j = 0; j < NS; ++j) S[j] = colsum[(static_cast<size_t>(lane) * NS + j) * P + p];
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-#pragma unroll
-    for (int j = 0; j < NS; ++j) S[j] += __shfl_xor(S[j], off, kWave);
-  }
-  if (lane != 0) return;
-  Model::epilogue(prm, p, S, out0, out1, out2);
-}
+struct OscEpilogue {
+  typename Model::Params prm;
+  float* out0;
+  float* out1;
+  float* out2;
+  __device__ void add(int p, const double* S) const { Model::epilogue(prm, p, S, out0, out1, out2); }
+};
 
 // T steps per lane, W waves per workgroup, OCC = minimum waves per SIMD the
 // register allocation must allow (__launch_bounds__' second argument).
@@ -751,8 +749,9 @@ int launch_forward(const typename Model::Params& prm, const void* in, void* out,
   return OSSM_OK;
 }
 
-// Backward launch: one kernel computes grad_in and, through the in-kernel
-// reduction, the per-oscillator parameter gradients (out0..2, see
+// Backward launch: the scan kernel computes grad_in and per-(chunk, channel)
+// parameter sums and clears out0..2; column_sum_kernel reduces the sums per
+// oscillator and adds the chain rule's result into out0..2 (see
 // Model::epilogue).  nc = B * P channels.
 template <class Model>
 int launch_backward(const typename Model::Params& prm, const void* in, const void* states,
@@ -769,15 +768,14 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
   const size_t part_bytes =
       (static_cast<size_t>(n_chunks) * NS * nc * sizeof(float) + 255) & ~static_cast<size_t>(255);
-  const size_t tot_bytes = static_cast<size_t>(kRowGroups) * NS * P * sizeof(double);
   void* ws = nullptr;
-  if (int rc = acquire_workspace(stream, part_bytes + tot_bytes, &ws)) return rc;
+  if (int rc = acquire_workspace(stream, part_bytes, &ws)) return rc;
   ParamReduce red{static_cast<float*>(ws)};
-  double* colsum = reinterpret_cast<double*>(static_cast<char*>(ws) + part_bytes);
   const int64_t total = n_chunks * n_groups;
   void* payload = nullptr;
   LaunchSync sync{};
   if (int rc = acquire_scratch(stream, rec_bytes, total, &payload, &sync)) return rc;
+  const ZeroFill zero{{out0, out1, out2}, static_cast<int>(Model::kOutsPerColumn * P)};
   bool launched = false;
 #define OSSM_LAUNCH_BWD(TT, WW, OO, HH)                                                          \
   if (!launched && tile.T == TT && tile.W == WW && tile.O == OO && tile.H == HH) {               \
@@ -787,7 +785,7 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
                        prm, static_cast<const typename Model::In*>(in),                          \
                        static_cast<const float4*>(states),                                       \
                        static_cast<const typename Model::GIn*>(gout),                            \
-                       static_cast<typename Model::GOut*>(gin), red, static_cast<int>(L),        \
+                       static_cast<typename Model::GOut*>(gin), red, zero, static_cast<int>(L),  \
                        static_cast<int>(nc), static_cast<int>(n_groups),                         \
                        static_cast<int>(n_chunks), static_cast<unsigned long long*>(payload),    \
                        sync);                                                                    \
@@ -803,10 +801,8 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
     release_unlaunched(stream, total);
     return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_BWD names no built tile");
   }
-  if (int rc = launch_colsum<NS>(red.partials, colsum, P, B, n_chunks, stream)) return rc;
-  hipLaunchKernelGGL(osc_param_kernel<Model>, dim3(static_cast<unsigned>((P + 3) / 4)),
-                     dim3(256), 0, stream, prm, colsum, static_cast<int>(P), out0, out1, out2);
-  return launch_check("osc_param_kernel");
+  return launch_column_sums<NS>(red.partials, P, B, n_chunks,
+                                OscEpilogue<Model>{prm, out0, out1, out2}, stream);
 }
 
 int check_sizes(int64_t L, int64_t B, int64_t P, const char* what) {

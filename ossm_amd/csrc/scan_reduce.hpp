@@ -16,20 +16,24 @@ namespace {
 
 // The partials form, for each sum j, a matrix of R = n_chunks * B rows
 // (chunk c, batch row b) by P columns (state column p): address
-// (c * NS + j) * nc + b * P + p.  Column sums in two passes:
-//   pass 1: block (column tile of 64, row group g) sums rows r = g*4 + w + k*4G
-//           (w = wave) in fp64, four rows in flight per lane, waves combined
-//           through LDS -> colsum[g][j][p];
-//   pass 2 (per model): one wave per column, lane g holding row group g,
-//           adds them by a butterfly over the wave, then the model's chain rule.
-// Fixed order everywhere (no atomics).
+// (c * NS + j) * nc + b * P + p.  Column sums in one launch: block (column
+// tile of 64, row group g) sums rows r = g*4 + w + k*4G (w = wave) in fp64,
+// four rows in flight per lane, waves combined through LDS in a fixed order,
+// then calls Epi::add(p, S) with its row group's NS sums.  Every epilogue here
+// is linear in the sums (parameter gradients = a per-column Jacobian times
+// them), so each row group applies it to its own share and adds the result to
+// the zero-initialised outputs with one hardware float atomic per output: the
+// 64-way combine is the only unordered step.  (Finishing a column inside one
+// launch without atomics costs a cross-block handoff, measured no cheaper than
+// a second launch: 20 us with a fetch-add counter and tagged fp64 row-group
+// sums, 68 us with a compare-and-swap counter, 77 us with an acq_rel counter
+// whose release writes back an L2 still dirty with the scan's output rows.)
 constexpr int kRowGroups = kWave;
 constexpr int kColsumRows = 4;  // rows per lane per round (independent loads)
 
-template <int NS, class PT = float>
-__global__ __launch_bounds__(256) void osc_colsum_kernel(const PT* __restrict__ partials,
-                                                         double* __restrict__ colsum, int P,
-                                                         int B, int n_chunks) {
+template <int NS, class PT, class Epi>
+__global__ __launch_bounds__(256) void column_sum_kernel(const PT* __restrict__ partials, int P,
+                                                         int B, int n_chunks, Epi epi) {
   __shared__ double s_red[4][NS][kWave];
   const int lane = threadIdx.x & (kWave - 1), w = wave_id();
   const int p = blockIdx.x * kWave + lane;
@@ -38,6 +42,7 @@ __global__ __launch_bounds__(256) void osc_colsum_kernel(const PT* __restrict__ 
   const size_t nc = static_cast<size_t>(B) * P;
   const int R = n_chunks * B;
   constexpr int kStride = kRowGroups * 4;
+  if (g * 4 >= R) return;  // an empty row group adds nothing
   double acc[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) acc[j] = 0.0;
@@ -62,23 +67,45 @@ __global__ __launch_bounds__(256) void osc_colsum_kernel(const PT* __restrict__ 
   for (int j = 0; j < NS; ++j) s_red[w][j][lane] = acc[j];
   __syncthreads();
   if (w == 0 && p < P) {
+    double S[NS];
 #pragma unroll
     for (int j = 0; j < NS; ++j)
-      colsum[(static_cast<size_t>(g) * NS + j) * P + p] =
-          ((s_red[0][j][lane] + s_red[1][j][lane]) + s_red[2][j][lane]) + s_red[3][j][lane];
+      S[j] = ((s_red[0][j][lane] + s_red[1][j][lane]) + s_red[2][j][lane]) + s_red[3][j][lane];
+    epi.add(p, S);
   }
 }
 
-// Launches pass 1 over `partials` ([n_chunks][NS][B * P]) into `colsum`
-// ([kRowGroups][NS][P]).
-template <int NS, class PT>
-int launch_colsum(const PT* partials, double* colsum, int64_t P, int64_t B, int64_t n_chunks,
-                  hipStream_t stream) {
-  hipLaunchKernelGGL((osc_colsum_kernel<NS, PT>),
+// Column sums of `partials` ([n_chunks][NS][B * P]) added into Epi's outputs,
+// which must hold zeros when the kernel starts.
+template <int NS, class PT, class Epi>
+int launch_column_sums(const PT* partials, int64_t P, int64_t B, int64_t n_chunks, const Epi& epi,
+                       hipStream_t stream) {
+  hipLaunchKernelGGL((column_sum_kernel<NS, PT, Epi>),
                      dim3(static_cast<unsigned>((P + kWave - 1) / kWave), kRowGroups), dim3(256), 0,
-                     stream, partials, colsum, static_cast<int>(P), static_cast<int>(B),
-                     static_cast<int>(n_chunks));
-  return launch_check("osc_colsum_kernel");
+                     stream, partials, static_cast<int>(P), static_cast<int>(B),
+                     static_cast<int>(n_chunks), epi);
+  return launch_check("column_sum_kernel");
+}
+
+// Output accumulation for the epilogues: one hardware float atomic add.
+__device__ __forceinline__ void atomic_put(float* dst, double v) {
+  unsafeAtomicAdd(dst, static_cast<float>(v));
+}
+__device__ __forceinline__ void atomic_put(double* dst, double v) { unsafeAtomicAdd(dst, v); }
+
+// Up to three output arrays a backward scan kernel clears before the column
+// sums add into them (the workgroup with the first ticket does it; the
+// column-sum launch runs after the scan kernel has finished).
+struct ZeroFill {
+  float* p[3];
+  int n;  // floats per array
+};
+
+__device__ __forceinline__ void zero_fill_block(const ZeroFill& z) {
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+    if (z.p[k] != nullptr)
+      for (int i = threadIdx.x; i < z.n; i += blockDim.x) z.p[k][i] = 0.f;
 }
 
 // Zero-fill used where the reference returns zero gradients (empty scans);

@@ -214,7 +214,7 @@ def test_diag_bridge_autograd(K):
 
 def test_diag_repeatable(K):
     """Two runs agree to rounding (look-back association depends on publish
-    timing; the grad_lambda sums are fixed-order)."""
+    timing, and the 64 row-group shares of grad_lambda are added atomically)."""
     lam, b, go = diag_inputs(3000, 4, 96, seed=9)
     announce("diag repeatability")
     s1, l1, b1 = _run(K, lam, b, go)
