@@ -67,7 +67,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ float sigmoid(float z) { return 1.f / (1.f + __expf(-z)); }
+// 1 / (1 + e^-z) with the hardware reciprocal (1 ulp) instead of an IEEE
+// division sequence: the gate is evaluated for every output element.
+__device__ __forceinline__ float sigmoid(float z) {
+  return __builtin_amdgcn_rcpf(1.f + fast_exp2(-z * kLog2e));
+}
 
 // ---- cross-lane helpers -------------------------------------------------------
 // permlane32 swap: lanes 32..63 of a trade places with lanes 0..31 of b.
@@ -314,18 +318,77 @@ __device__ __forceinline__ void write_ckpt(float* ckpt, size_t lane_row, int slo
 }
 
 struct FwdTile {
-  RowRegs<kFwdTile> u, dt, z;
+  RowRegs<kFwdTile> u, dt;
   StateRegs<kFwdTile> B, C;
 };
 
-template <class E, bool VEC, bool GATED>
+template <class E, bool VEC>
 __device__ __forceinline__ void fwd_prefetch(FwdTile& f, const FwdArgs<E>& a, size_t row0,
                                              size_t bc0, int d0, int t0) {
   load_rows<kFwdTile, VEC>(f.u, a.u, row0, d0, a.D, t0, a.L);
   load_rows<kFwdTile, VEC>(f.dt, a.dt, row0, d0, a.D, t0, a.L);
-  if constexpr (GATED) load_rows<kFwdTile, VEC>(f.z, a.z, row0, d0, a.D, t0, a.L);
   load_states<kFwdTile>(f.B, a.Bm, bc0, t0, a.L, a.N, a.n_base);
   load_states<kFwdTile>(f.C, a.Cm, bc0, t0, a.L, a.N, a.n_base);
+}
+
+// The forward's lane layout: lane = (channel c = lane % 16, state group
+// g = lane / 16), so a wave holds all 16 states of 16 channels and a lane's
+// finished outputs are 8 consecutive steps of its channel.
+constexpr int kGroups = kPassStates / kNpw;  // state groups per channel (4)
+constexpr int kWaveCh = kWave / kGroups;     // channels per wave (16)
+constexpr int kSeg = kFwdTile / kGroups;     // output steps per lane per tile (8)
+
+// 8 consecutive steps of one row of a [.., L] tensor, from step t (a multiple
+// of 4); reads past the end use clamped in-range addresses (values unused).
+template <bool VEC, class E>
+__device__ __forceinline__ void load_seg(float (&v)[kSeg], const E* __restrict__ g, size_t row,
+                                         int t, int L) {
+  if constexpr (VEC) {
+#pragma unroll
+    for (int q = 0; q < kSeg / 4; ++q) {
+      const float4 x = Elem<E>::load4(g + row + min(t + 4 * q, L - 4));
+      v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kSeg; ++k) v[k] = Elem<E>::load1(g + row + min(t + k, L - 1));
+  }
+}
+
+// Stores the steps of an 8-step segment that lie before L.
+template <bool VEC, class E>
+__device__ __forceinline__ void store_seg(E* __restrict__ g, size_t row, int t, int L,
+                                          const float (&v)[kSeg]) {
+  if constexpr (VEC) {  // L % 4 == 0, so a group of 4 is all in or all out
+#pragma unroll
+    for (int q = 0; q < kSeg / 4; ++q)
+      if (t + 4 * q < L)
+        Elem<E>::store4(g + row + t + 4 * q, make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]));
+  } else {
+#pragma unroll
+    for (int k = 0; k < kSeg; ++k)
+      if (t + k < L) Elem<E>::store1(g + row + t + k, v[k]);
+  }
+}
+
+// Sums y over the kGroups state groups of each channel: lane (c, g) enters
+// with its group's partial y for steps 0..31 of the tile and leaves with the
+// full y of steps 8g .. 8g+7.  permlane32 swaps pair groups g and g ^ 2 (the
+// two halves keep steps 0..15 and 16..31), permlane16 swaps pair g and g ^ 1.
+__device__ __forceinline__ void reduce_groups(float (&yv)[kFwdTile], float (&out)[kSeg]) {
+  float s1[kFwdTile / 2];
+#pragma unroll
+  for (int i = 0; i < kFwdTile / 2; ++i) {
+    float lo = yv[i], hi = yv[i + kFwdTile / 2];
+    swap32(lo, hi);
+    s1[i] = lo + hi;  // lanes 0..31: step i, lanes 32..63: step i + 16 (groups g, g ^ 2)
+  }
+#pragma unroll
+  for (int i = 0; i < kSeg; ++i) {
+    float lo = s1[i], hi = s1[i + kSeg];
+    swap16(lo, hi);
+    out[i] = lo + hi;  // row r: step 8r + i, all four groups
+  }
 }
 
 // GATED kernels multiply by silu(z) in the last pass; VEC: L % 4 == 0 and
@@ -334,21 +397,21 @@ template <class E, bool VEC, bool GATED>
 __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   constexpr int TT = kFwdTile;
   constexpr int RS = TT + 1;  // odd row stride: lane-per-row accesses hit distinct banks
+  static_assert(kGroups == 4 && TT == 32 && kSeg == 8, "reduce_groups assumes 4 x 32 steps");
   __shared__ float s_u[kWave * RS];
   __shared__ float s_dt[kWave * RS];
   __shared__ __align__(16) float s_B[TT * kPassStates];
   __shared__ __align__(16) float s_C[TT * kPassStates];
-  __shared__ float s_y[kMaxWaves * kWave * RS];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int w = threadIdx.x / kWave;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const int c = lane & (kWaveCh - 1), g = lane / kWaveCh;
   const int b = blockIdx.y;
   const int d0 = blockIdx.x * kWave;
-  const int d = d0 + lane;
+  const int r = w * kWaveCh + c;  // the lane's channel row in the workgroup's tile
+  const int d = d0 + r;
   const bool dvalid = d < a.D;
-  const int n0 = a.n_base + w * kNpw;  // first state of this wave
-  const int nw = min(kMaxWaves, (a.N - a.n_base + kNpw - 1) / kNpw);  // waves with states
-  const bool wave_active = w < nw;
+  const int n0 = a.n_base + g * kNpw;  // first state of this lane
 
   float A2[kNpw], h[kNpw];
 #pragma unroll
@@ -359,99 +422,111 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   const size_t row0 = static_cast<size_t>(b) * a.D * a.L;     // (b, 0, 0) in [B,D,L]
   const size_t bc0 = static_cast<size_t>(b) * a.L * a.N;      // (b, 0, 0) in [B,L,N]
   const size_t ck_row = (static_cast<size_t>(b) * a.D + (dvalid ? d : 0)) * a.n_chunks * 2 * a.N;
-  const int n_slots = (a.L + kCkpt - 1) / kCkpt;
+  const size_t my_row = row0 + static_cast<size_t>(dvalid ? d : a.D - 1) * a.L;  // [.., L] row of d
+  const bool ck = a.ckpt != nullptr && dvalid;
 
   FwdTile nxt;
-  fwd_prefetch<E, VEC, GATED>(nxt, a, row0, bc0, d0, 0);
+  float zn[kSeg];  // the gate of the lane's output segment, one tile ahead
+  fwd_prefetch<E, VEC>(nxt, a, row0, bc0, d0, 0);
+  if constexpr (GATED) load_seg<VEC>(zn, a.z, my_row, kSeg * g, a.L);
   for (int t0 = 0; t0 < a.L; t0 += TT) {
     __syncthreads();  // the previous tile's LDS readers are done
     store_rows<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
     store_rows<TT, RS>(s_dt, nxt.dt, d0, a.D, t0, a.L);
     store_states<TT>(s_B, nxt.B, t0, a.L, a.N, a.n_base);
     store_states<TT>(s_C, nxt.C, t0, a.L, a.N, a.n_base);
-    const RowRegs<TT> zt = nxt.z;
+    float zt[kSeg];
+#pragma unroll
+    for (int k = 0; k < kSeg; ++k) zt[k] = zn[k];
     __syncthreads();
-    if (t0 + TT < a.L) fwd_prefetch<E, VEC, GATED>(nxt, a, row0, bc0, d0, t0 + TT);
+    if (t0 + TT < a.L) {
+      fwd_prefetch<E, VEC>(nxt, a, row0, bc0, d0, t0 + TT);
+      if constexpr (GATED) load_seg<VEC>(zn, a.z, my_row, t0 + TT + kSeg * g, a.L);
+    }
 
-    const int nsteps = min(TT, a.L - t0);
-    if (wave_active) {
-      float* yrow = s_y + (w * kWave + lane) * RS;
-      const bool ck = a.ckpt != nullptr && dvalid;
-      // FULL: all TT steps exist, so the step loop needs no bounds checks and
-      // the checkpoints fall on fixed steps (15 and 31).
-      auto steps = [&](auto full_tag) {
-        constexpr bool FULL = decltype(full_tag)::value;
+    // Every tile runs all TT steps: past L the staged dt, u, B and C are zero,
+    // so h stays at the last step's state and y is zero there; the checkpoint
+    // slots of the last tile then hold that final state, as their layout says.
+    float yv[TT];  // this lane's y partial (its 4 states) per step
+    float hck[TT / kCkpt][kNpw];  // h after steps 15 and 31, checkpointed after the loop
+    auto step = [&](int i, float dtv, float uv, float4 Bt, float4 Ct) {
+      const float dtu = dtv * uv;
+      const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
+      const float Cv[4] = {Ct.x, Ct.y, Ct.z, Ct.w};
+      float y = 0.f;
 #pragma unroll
-        for (int i = 0; i < TT; ++i) {
-          if (FULL || i < nsteps) {
-            const float dtv = s_dt[lane * RS + i];
-            const float dtu = dtv * s_u[lane * RS + i];
-            const float4 Bt = *reinterpret_cast<const float4*>(s_B + i * kPassStates + w * kNpw);
-            const float4 Ct = *reinterpret_cast<const float4*>(s_C + i * kPassStates + w * kNpw);
-            const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
-            const float Cv[4] = {Ct.x, Ct.y, Ct.z, Ct.w};
-            float y = 0.f;
+      for (int j = 0; j < kNpw; ++j) {
+        const float dA = fast_exp2(dtv * A2[j]);
+        h[j] = fmaf(dA, h[j], dtu * Bv[j]);
+        y = fmaf(Cv[j], h[j], y);
+      }
+      // pin y here: left alone, the compiler sinks these FMAs to the reduction
+      // after the loop and keeps every step's h and C alive (256 VGPRs)
+      asm volatile("" : "+v"(y));
+      yv[i] = y;
+      if ((i + 1) % kCkpt == 0) {
 #pragma unroll
-            for (int j = 0; j < kNpw; ++j) {
-              const float dA = fast_exp2(dtv * A2[j]);
-              h[j] = fmaf(dA, h[j], dtu * Bv[j]);
-              y = fmaf(Cv[j], h[j], y);
-            }
-            yrow[i] = y;
-            if ((i + 1) % kCkpt == 0 && ck) write_ckpt(a.ckpt, ck_row, (t0 + i) / kCkpt, a.N, n0, h);
-          }
+        for (int j = 0; j < kNpw; ++j) hck[i / kCkpt][j] = h[j];
+      }
+    };
+    const float* urow = s_u + r * RS;
+    const float* dtrow = s_dt + r * RS;
+    const float* Bcol = s_B + g * kNpw;
+    const float* Ccol = s_C + g * kNpw;
+    {
+      // Software-pipelined: the LDS operands of the next kGroup steps are read
+      // before this group is computed, so a read's latency is covered by a
+      // group of steps; a compiler fence per group keeps the compiler from
+      // hoisting every step's reads to the top (256 VGPRs without it).
+      constexpr int kGroup = 4;
+      float pdt[2][kGroup], pu[2][kGroup];
+      float4 pB[2][kGroup], pC[2][kGroup];
+      auto fetch = [&](int buf, int gr) {
+#pragma unroll
+        for (int q = 0; q < kGroup; ++q) {
+          const int i = gr * kGroup + q;
+          pdt[buf][q] = dtrow[i];
+          pu[buf][q] = urow[i];
+          pB[buf][q] = *reinterpret_cast<const float4*>(Bcol + i * kPassStates);
+          pC[buf][q] = *reinterpret_cast<const float4*>(Ccol + i * kPassStates);
         }
       };
-      if (nsteps == TT) {
-        steps(std::true_type{});
-      } else {
-        steps(std::false_type{});
-        // last tile: its final state fills the last slot (and, for an odd
-        // number of slots, the unused second half of the last row)
-        if (ck) {
-          const int slot = (a.L - 1) / kCkpt;
-          write_ckpt(a.ckpt, ck_row, slot, a.N, n0, h);
-          if (n_slots & 1) write_ckpt(a.ckpt, ck_row, slot + 1, a.N, n0, h);
-        }
+      fetch(0, 0);
+#pragma unroll
+      for (int gr = 0; gr < TT / kGroup; ++gr) {
+        const int cur = gr & 1;
+        if (gr + 1 < TT / kGroup) fetch(cur ^ 1, gr + 1);
+#pragma unroll
+        for (int q = 0; q < kGroup; ++q)
+          step(gr * kGroup + q, pdt[cur][q], pu[cur][q], pB[cur][q], pC[cur][q]);
+        asm volatile("" ::: "memory");
       }
     }
-    __syncthreads();
-
-    // finish y over the waves (states), gate, store
+    if (ck) {
 #pragma unroll
-    for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
-      int r, c;
-      tile_pos<TT>(k, r, c);
-      const int dd = d0 + r, t = t0 + c;
-      if (dd >= a.D || t >= a.L) continue;
-      float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int v = 0; v < nw; ++v) {
-        const float* p = s_y + (v * kWave + r) * RS + c;
-        y.x += p[0];
-        y.y += p[1];
-        y.z += p[2];
-        y.w += p[3];
-      }
-      const size_t gi = row0 + static_cast<size_t>(dd) * a.L + t;
+      for (int q = 0; q < TT / kCkpt; ++q) write_ckpt(a.ckpt, ck_row, t0 / kCkpt + q, a.N, n0, hck[q]);
+    }
+
+    // y over the state groups (within the wave), then this lane's 8 outputs
+    float y[kSeg];
+    reduce_groups(yv, y);
+    if (dvalid) {
+      const int t = t0 + kSeg * g;
       if (!a.first) {
-        y.x += a.acc[gi];
-        if (t + 1 < a.L) y.y += a.acc[gi + 1];
-        if (t + 2 < a.L) y.z += a.acc[gi + 2];
-        if (t + 3 < a.L) y.w += a.acc[gi + 3];
+        float prev[kSeg];
+        load_seg<false>(prev, a.acc, my_row, t, a.L);
+#pragma unroll
+        for (int k = 0; k < kSeg; ++k) y[k] += prev[k];
       }
       if (a.last) {
-        if (a.raw != nullptr) store_row4<VEC>(a.raw, gi, t, a.L, y);
-        float4 o = y;
+        if (a.raw != nullptr) store_seg<VEC>(a.raw, my_row, t, a.L, y);
         if constexpr (GATED) {
-          const float4 zz = zt.v[k];
-          o.x *= zz.x * sigmoid(zz.x);
-          o.y *= zz.y * sigmoid(zz.y);
-          o.z *= zz.z * sigmoid(zz.z);
-          o.w *= zz.w * sigmoid(zz.w);
+#pragma unroll
+          for (int k = 0; k < kSeg; ++k) y[k] *= zt[k] * sigmoid(zt[k]);
         }
-        store_row4<VEC>(a.out, gi, t, a.L, o);
+        store_seg<VEC>(a.out, my_row, t, a.L, y);
       } else {
-        store_row4<VEC>(a.acc, gi, t, a.L, y);
+        store_seg<VEC>(a.acc, my_row, t, a.L, y);
       }
     }
   }
