@@ -809,8 +809,25 @@ __global__ void selective_finish_kernel(const float* __restrict__ part_dB,
                                         int64_t n_bln, int n_dtiles, int64_t n_dn, int Bsz) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n_bln) {
+    // tiles added in ascending order; the loads of 8 tiles are issued before
+    // any of them is added (the sum stays the same, bit for bit)
+    constexpr int kBatch = 8;
     float sb = 0.f, sc = 0.f;
-    for (int k = 0; k < n_dtiles; ++k) {
+    int k = 0;
+    for (; k + kBatch <= n_dtiles; k += kBatch) {
+      float vb[kBatch], vc[kBatch];
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        vb[q] = part_dB[static_cast<size_t>(k + q) * n_bln + i];
+        vc[q] = part_dC[static_cast<size_t>(k + q) * n_bln + i];
+      }
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        sb += vb[q];
+        sc += vc[q];
+      }
+    }
+    for (; k < n_dtiles; ++k) {
       sb += part_dB[static_cast<size_t>(k) * n_bln + i];
       sc += part_dC[static_cast<size_t>(k) * n_bln + i];
     }
