@@ -1,6 +1,7 @@
 // Reductions shared by the scan backwards: per-channel partial sums of every
-// (time chunk, batch row) reduced to one value per state column, in a fixed
-// order in fp64 (no atomics), and a graph-safe zero fill.
+// (time chunk, batch row) reduced to one value per state column (fixed-order
+// fp64 sums per row group, row groups combined with float atomics), and a
+// graph-safe zero fill.
 #pragma once
 
 #include <hip/hip_runtime.h>

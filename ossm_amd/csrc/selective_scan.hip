@@ -5,16 +5,18 @@
 // per (batch b, channel d), tensors u, dt, z, out [B,D,L]; A [D,N]; B, C [B,L,N].
 //
 // Parallel decomposition
-//   A workgroup owns one batch row b and 64 consecutive channels d (one lane
-//   per channel) and walks the whole sequence; its waves split the states:
-//   wave w carries states n_base + 4w .. n_base + 4w + 3 in registers, so the
-//   B/C values a wave needs at a step are the same for all its lanes (LDS
-//   broadcast reads).  Up to 16 states run per launch ("pass"); larger N runs
-//   ceil(N/16) passes that accumulate y (forward) and du/ddt (backward) in the
-//   output tensors.  Time is processed in tiles staged through LDS: u, dt (and
-//   the gated upstream gradient) are loaded with coalesced row reads and read
-//   back by lane = channel.  The sum over states (y, du, ddt) is finished
-//   across the waves through LDS.
+//   A workgroup owns one batch row b and 64 consecutive channels d and walks
+//   the whole sequence; up to 16 states run per launch ("pass"), 4 per lane in
+//   registers; larger N runs ceil(N/16) passes that accumulate y (forward) and
+//   du/ddt (backward) in the output tensors.  Time is processed in tiles
+//   staged through LDS: u, dt (and the gated upstream gradient) are loaded with
+//   coalesced row reads and read back per channel.
+//   Forward: lane = (channel c = lane % 16, state group g = lane / 16), so a
+//   wave holds all 16 states of 16 channels and y is summed over the states
+//   inside the wave (cross-row swaps), with no LDS round trip.
+//   Backward: lane = channel and wave w carries states 4w .. 4w + 3, so the
+//   sums over channels (dB, dC) finish inside a wave and the sums over states
+//   (du, ddt) across the waves through LDS.
 //
 // Transcendentals: exp(dt A) = exp2(dt * (A log2 e)) with A log2 e formed once
 //   per lane, so each state-step costs one v_exp_f32.
@@ -31,6 +33,11 @@
 //   du_t  = dt_t sum_n gacc B_t,   ddt_t = sum_n gacc (A e^{dt A} h_{t-1} + B_t u_t)
 //   dA    = sum_{b,t} gacc dt e^{dt A} h_{t-1},   dz = gout * y * silu'(z) (y = raw_out)
 //   dB_t  = sum_d gacc dt u,   dC_t = sum_d gy h_t
+// A tile is done in two 8-step halves, the later one first: the forward is
+// re-run from the checkpoint (once more over the first half, to reach the
+// second), each half's h and exp(dt A) are held in registers while the adjoint
+// runs over it in reverse.  Holding all 16 steps costs 64 more VGPRs: one wave
+// per SIMD instead of two.
 // dB/dC are sums over channels: each wave reduces its 64 lanes with the
 // gfx950 cross-row swaps (v_permlane32_swap / v_permlane16_swap) and row DPP,
 // and writes one partial per 64-channel tile; dA partials are per batch row.
@@ -587,6 +594,7 @@ __device__ __forceinline__ void bwd_prefetch(BwdTile& f, const BwdArgs<E>& a, si
 template <class E, bool VEC, bool GATED>
 __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   constexpr int TT = kBwdTile;
+  constexpr int HT = TT / 2;  // steps whose trajectory is held in registers at once
   constexpr int RS = TT + 1;
   __shared__ float s_u[kWave * RS];
   __shared__ float s_dt[kWave * RS];
@@ -597,7 +605,7 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   __shared__ float s_ddt[kMaxWaves * kWave * RS];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int w = threadIdx.x / kWave;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int b = blockIdx.y;
   const int d0 = blockIdx.x * kWave;
   const int d = d0 + lane;
@@ -664,93 +672,123 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
     if (tile > 0) bwd_prefetch<E, VEC, GATED>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile - 1);
 
     if (wave_active) {
-      // FULL: all TT steps exist (every tile but possibly the last in time)
-      auto tile_body = [&](auto full_tag) {
-        constexpr bool FULL = decltype(full_tag)::value;
-        // re-run the tile forward in registers
-        float hs[TT][kNpw], dAs[TT][kNpw];
+      const float* dtrow = s_dt + lane * RS;
+      const float* urow = s_u + lane * RS;
+      const float* gyrow = s_gy + lane * RS;
+      const float* Bcol = s_B + w * kNpw;
+      const float* Ccol = s_C + w * kNpw;
+      float* durow = s_du + (w * kWave + lane) * RS;
+      float* ddtrow = s_ddt + (w * kWave + lane) * RS;
+      float keep0 = 0.f, keep1 = 0.f;
+
+      // Steps s0 .. s0 + HT - 1 of the tile, entered with the state before
+      // step s0: the forward is re-run into registers, then the adjoint runs in
+      // reverse.  Steps past L were staged as zeros, so they leave h unchanged
+      // and contribute exact zeros.  Each step's LDS operands are read one step
+      // ahead; the empty asm with a memory clobber after every step keeps the
+      // compiler from hoisting all of them to the top (registers).
+      auto sub_tile = [&](auto s0_tag, const float (&hst)[kNpw]) {
+        constexpr int s0 = decltype(s0_tag)::value;
+        float hs[HT][kNpw], dAs[HT][kNpw];
         {
           float h[kNpw];
 #pragma unroll
-          for (int j = 0; j < kNpw; ++j) h[j] = h0[j];
+          for (int j = 0; j < kNpw; ++j) h[j] = hst[j];
+          float ndt = dtrow[s0], nu = urow[s0];
+          float4 nB = *reinterpret_cast<const float4*>(Bcol + s0 * kPassStates);
 #pragma unroll
-          for (int i = 0; i < TT; ++i) {
-            if (FULL || i < nsteps) {
-              const float dtv = s_dt[lane * RS + i];
-              const float dtu = dtv * s_u[lane * RS + i];
-              const float4 Bt = *reinterpret_cast<const float4*>(s_B + i * kPassStates + w * kNpw);
-              const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
-#pragma unroll
-              for (int j = 0; j < kNpw; ++j) {
-                const float dA = fast_exp2(dtv * A2[j]);
-                h[j] = fmaf(dA, h[j], dtu * Bv[j]);
-                hs[i][j] = h[j];
-                dAs[i][j] = dA;
-              }
-            } else {
-#pragma unroll
-              for (int j = 0; j < kNpw; ++j) {
-                hs[i][j] = 0.f;
-                dAs[i][j] = 0.f;
-              }
+          for (int i = 0; i < HT; ++i) {
+            const float dtv = ndt, uv = nu;
+            const float Bv[4] = {nB.x, nB.y, nB.z, nB.w};
+            if (i + 1 < HT) {
+              ndt = dtrow[s0 + i + 1];
+              nu = urow[s0 + i + 1];
+              nB = *reinterpret_cast<const float4*>(Bcol + (s0 + i + 1) * kPassStates);
             }
-          }
-        }
-
-        // reverse sweep
-        float keep0 = 0.f, keep1 = 0.f;
-        float* durow = s_du + (w * kWave + lane) * RS;
-        float* ddtrow = s_ddt + (w * kWave + lane) * RS;
-#pragma unroll
-        for (int i = TT - 1; i >= 0; --i) {
-          if (FULL || i < nsteps) {
-            const float gy = s_gy[lane * RS + i];
-            const float dtv = s_dt[lane * RS + i];
-            const float uv = s_u[lane * RS + i];
             const float dtu = dtv * uv;
-            const float4 Bt = *reinterpret_cast<const float4*>(s_B + i * kPassStates + w * kNpw);
-            const float4 Ct = *reinterpret_cast<const float4*>(s_C + i * kPassStates + w * kNpw);
-            const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
-            const float Cv[4] = {Ct.x, Ct.y, Ct.z, Ct.w};
-            float S1 = 0.f, S2 = 0.f;
-            float v[8];
 #pragma unroll
             for (int j = 0; j < kNpw; ++j) {
-              const float hprev = i > 0 ? hs[i > 0 ? i - 1 : 0][j] : h0[j];
-              const float gacc = fmaf(gy, Cv[j], gs[j]);
-              const float gsn = gacc * dAs[i][j];
-              const float q = gsn * hprev;
-              gA[j] = fmaf(dtv, q, gA[j]);
-              S2 = fmaf(Af[j], q, S2);
-              S1 = fmaf(gacc, Bv[j], S1);
-              v[j] = gacc * dtu;          // dB contribution
-              v[4 + j] = gy * hs[i][j];   // dC contribution
-              gs[j] = gsn;
+              const float dA = fast_exp2(dtv * A2[j]);
+              h[j] = fmaf(dA, h[j], dtu * Bv[j]);
+              hs[i][j] = h[j];
+              dAs[i][j] = dA;
             }
-            durow[i] = dtv * S1;
-            ddtrow[i] = fmaf(uv, S1, S2);
-            float o0, o1;
-            reduce8(v, o0, o1);
-            if ((lane & 15) == i) {
-              keep0 = o0;
-              keep1 = o1;
-            }
+            asm volatile("" ::: "memory");
           }
         }
-        // lane (row r, column c) holds the tile-partials of step t0 + c:
-        // r = 0: dB[n0], dB[n0+1]; r = 1: dB[n0+2], dB[n0+3]; r = 2, 3: same for dC
-        const int r = lane >> 4, c = lane & 15;
-        if (FULL || c < nsteps) {
-          float* dst = (r < 2 ? a.part_dB : a.part_dC) + part0 + static_cast<size_t>(t0 + c) * a.N;
-          const int nn = n0 + 2 * (r & 1);
-          if (nn < a.N) dst[nn] = keep0;
-          if (nn + 1 < a.N) dst[nn + 1] = keep1;
+        constexpr int il = HT - 1;
+        float ngy = gyrow[s0 + il], ndt = dtrow[s0 + il], nu = urow[s0 + il];
+        float4 nB = *reinterpret_cast<const float4*>(Bcol + (s0 + il) * kPassStates);
+        float4 nC = *reinterpret_cast<const float4*>(Ccol + (s0 + il) * kPassStates);
+#pragma unroll
+        for (int i = il; i >= 0; --i) {
+          const float gy = ngy, dtv = ndt, uv = nu;
+          const float Bv[4] = {nB.x, nB.y, nB.z, nB.w};
+          const float Cv[4] = {nC.x, nC.y, nC.z, nC.w};
+          if (i > 0) {
+            ngy = gyrow[s0 + i - 1];
+            ndt = dtrow[s0 + i - 1];
+            nu = urow[s0 + i - 1];
+            nB = *reinterpret_cast<const float4*>(Bcol + (s0 + i - 1) * kPassStates);
+            nC = *reinterpret_cast<const float4*>(Ccol + (s0 + i - 1) * kPassStates);
+          }
+          const float dtu = dtv * uv;
+          float S1 = 0.f, S2 = 0.f;
+          float v[8];
+#pragma unroll
+          for (int j = 0; j < kNpw; ++j) {
+            const float hprev = i > 0 ? hs[i > 0 ? i - 1 : 0][j] : hst[j];
+            const float gacc = fmaf(gy, Cv[j], gs[j]);
+            const float gsn = gacc * dAs[i][j];
+            const float q = gsn * hprev;
+            gA[j] = fmaf(dtv, q, gA[j]);
+            S2 = fmaf(Af[j], q, S2);
+            S1 = fmaf(gacc, Bv[j], S1);
+            v[j] = gacc * dtu;         // dB contribution
+            v[4 + j] = gy * hs[i][j];  // dC contribution
+            gs[j] = gsn;
+          }
+          durow[s0 + i] = dtv * S1;
+          ddtrow[s0 + i] = fmaf(uv, S1, S2);
+          float o0, o1;
+          reduce8(v, o0, o1);
+          if ((lane & 15) == s0 + i) {
+            keep0 = o0;
+            keep1 = o1;
+          }
+          asm volatile("" ::: "memory");
         }
       };
-      if (nsteps == TT)
-        tile_body(std::true_type{});
-      else
-        tile_body(std::false_type{});
+
+      // The second half first (from the state after step HT - 1, found by one
+      // more forward pass over the first half), then the first half.  A tile
+      // that ends within its first half skips the second: all padding.
+      if (nsteps > HT) {
+        float hmid[kNpw];
+#pragma unroll
+        for (int j = 0; j < kNpw; ++j) hmid[j] = h0[j];
+#pragma unroll
+        for (int i = 0; i < HT; ++i) {
+          const float dtv = dtrow[i];
+          const float dtu = dtv * urow[i];
+          const float4 Bt = *reinterpret_cast<const float4*>(Bcol + i * kPassStates);
+          const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
+#pragma unroll
+          for (int j = 0; j < kNpw; ++j) hmid[j] = fmaf(fast_exp2(dtv * A2[j]), hmid[j], dtu * Bv[j]);
+        }
+        sub_tile(std::integral_constant<int, HT>{}, hmid);
+      }
+      sub_tile(std::integral_constant<int, 0>{}, h0);
+
+      // lane (row r, column c) holds the tile-partials of step t0 + c:
+      // r = 0: dB[n0], dB[n0+1]; r = 1: dB[n0+2], dB[n0+3]; r = 2, 3: same for dC
+      const int r = lane >> 4, c = lane & 15;
+      if (c < nsteps) {
+        float* dst = (r < 2 ? a.part_dB : a.part_dC) + part0 + static_cast<size_t>(t0 + c) * a.N;
+        const int nn = n0 + 2 * (r & 1);
+        if (nn < a.N) dst[nn] = keep0;
+        if (nn + 1 < a.N) dst[nn + 1] = keep1;
+      }
     }
     __syncthreads();
 
