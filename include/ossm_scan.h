@@ -42,7 +42,7 @@ enum {
 
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
-/* Library ABI version (bumped on any change of the entry points; currently 5). */
+/* Library ABI version (bumped on any change of the entry points; currently 6). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -223,6 +223,21 @@ int ossm_diag_scan_backward_f64(const double* lambda_real, const double* lambda_
                                 const void* states, const void* grad_output, void* grad_lambda,
                                 void* grad_b, int64_t length, int64_t batch, int64_t state,
                                 ossm_stream_t stream);
+
+/*
+ * Fused D-LinOSS layer forward, replaces the body of DampedLinOSSLayer.forward
+ * after the parameter projection (dlinoss.py:210-247: bu = u B^T as two real
+ * GEMMs, permutes, run_dlinoss, y = Re(x C^T) + D u).  inputs / outputs
+ * [batch, length, hidden] fp32 row-major; B [ssm, hidden, 2] and C
+ * [hidden, ssm, 2] (real, imaginary parts last, the layer's parameter layout);
+ * D [hidden]; a_diag, g_diag, step [ssm] as returned by _project_parameters
+ * (dlinoss.py:249-264).  bu and the states stay on chip.  hidden and ssm up to
+ * 256 (OSSM_ERR_UNSUPPORTED beyond).
+ */
+int ossm_dlinoss_layer_forward(int variant, const float* inputs, const float* B, const float* C,
+                               const float* D, const float* a_diag, const float* g_diag,
+                               const float* step, float* outputs, int64_t batch, int64_t length,
+                               int64_t hidden, int64_t ssm, ossm_stream_t stream);
 
 #ifdef __cplusplus
 }

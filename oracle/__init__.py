@@ -12,7 +12,8 @@ D-LinOSS ``bu [L,B,P]`` complex, states ``[L,B,P,2]`` complex (the selective
 D-LinOSS alike, with parameters (M,), (L,M), (B,M) or (L|1,B|1,M)); LinOSS
 ``b_seq [L,B,P,2]`` complex with complex ``m_ij [P]``; diagonal (LRU / S5)
 scans ``b_seq [L,B,P]`` complex with complex ``lambda_bar [P]``; selective scan
-``u, dt, gate [B,D,L]``, ``A [D,N]``, ``B, C [B,L,N]`` real.
+``u, dt, gate [B,D,L]``, ``A [D,N]``, ``B, C [B,L,N]`` real; the D-LinOSS
+layer ``inputs, outputs [B,L,H]`` real with ``B [P,H,2]``, ``C [H,P,2]``.
 """
 
 from __future__ import annotations
@@ -118,6 +119,32 @@ def dlinoss_backward(variant: str, a_diag, g_diag, step, bu, states, grad_output
         ctypes.c_int(_VARIANT_CODE[variant]), _ptr(a), _ptr(g), _ptr(s), _ptr(bu), _ptr(states),
         _ptr(gout), _ptr(gaux), _ptr(grad_bu), _ptr(ga), _ptr(gg), _ptr(gs), I(L), I(B), I(P))
     return ga, gg, gs, grad_bu
+
+
+# ------------------------------------------------------------ D-LinOSS layer
+def dlinoss_layer_forward(variant: str, inputs, B, C, D, a_diag, g_diag, step):
+    """``(y, states)`` of DampedLinOSSLayer.forward after the parameter
+    projection (dlinoss.py:210-247), in the inputs' precision: ``bu = u B^T``
+    with ``B[..., 0] + i B[..., 1]`` (two real GEMMs, dlinoss.py:219-224), the
+    scan above on ``bu`` permuted to ``[L,B,P]``, then
+    ``y = Re(x) C[..., 0]^T - Im(x) C[..., 1]^T + D u`` (dlinoss.py:237-245) with
+    ``x = states[..., 1]``.  ``u, y [B,L,H]``; ``B [P,H,2]``; ``C [H,P,2]``;
+    ``D [H]``; states ``[L,B,P,2]``."""
+    u = np.asarray(inputs)
+    prec = _prec_of(u)
+    rt, ct = _real_dtype(prec), _complex_dtype(prec)
+    u = _c(u, rt)
+    Bw, Cw, Dw = _c(B, rt), _c(C, rt), _c(D, rt)
+    nb, L, H = u.shape
+    P = Bw.shape[0]
+    flat = u.reshape(nb * L, H)
+    bu = (flat @ Bw[..., 0].T).astype(rt) + 1j * (flat @ Bw[..., 1].T).astype(rt)
+    bu = np.ascontiguousarray(bu.astype(ct).reshape(nb, L, P).transpose(1, 0, 2))
+    states = dlinoss_forward(variant, a_diag, g_diag, step, bu)
+    x = states[..., 1].transpose(1, 0, 2).reshape(nb * L, P)
+    proj = (x.real.astype(rt) @ Cw[..., 0].T).astype(rt) - (x.imag.astype(rt) @ Cw[..., 1].T).astype(rt)
+    y = proj.reshape(nb, L, H) + u * Dw
+    return y.astype(rt), states
 
 
 # ------------------------------------------------------------------ LinOSS

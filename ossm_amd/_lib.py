@@ -65,6 +65,10 @@ _SIGNATURES = {
         ctypes.c_int, [_fp, _fp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
     "ossm_diag_scan_backward_f64": (
         ctypes.c_int, [_fp, _fp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_dlinoss_layer_forward": (
+        ctypes.c_int,
+        [ctypes.c_int, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _c_int64, _c_int64, _c_int64,
+         _c_int64, _vp]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

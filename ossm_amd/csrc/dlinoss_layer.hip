@@ -1,0 +1,379 @@
+// Fused D-LinOSS layer forward on gfx950: the in-projection, the D-LinOSS scan
+// and the out-projection with the D skip in one kernel (DampedLinOSSLayer.forward,
+// dlinoss.py:184-247, after the parameter projection of dlinoss.py:249-264):
+//
+//   bu[b,t,p] = sum_h u[b,t,h] (B[p,h,0] + i B[p,h,1])
+//   s_t       = M s_{t-1} + f bu_t       (per variant, s_{-1} = 0; x = s1)
+//   y[b,t,h]  = sum_p (Re x[b,t,p] C[h,p,0] - Im x[b,t,p] C[h,p,1]) + D[h] u[b,t,h]
+//
+// u, y [B,L,H] fp32 row-major; B [P,H,2]; C [H,P,2]; D [H]; a, g, dt [P]
+// (already projected).  The unfused layer moves bu and the states through HBM
+// several times (GEMM outputs, complex assembly, two permutes, the scan's
+// [L,B,P,2] states); here only u is read and y written: 8 bytes per (t, h).
+//
+// Decomposition: one workgroup (4 waves) per (batch row b, 32-step chunk).
+//   1. The chunk's u rows (contiguous in HBM) are staged in LDS.
+//   2. In-projection on the matrix cores, v_mfma_f32_32x32x2f32 (fp32 products
+//      and sums, no reduced precision): the 32 x 2P result (re and im planes)
+//      stays in LDS.  Wave w owns oscillator groups w, w+4, ... of 32; its
+//      lanes read the weights straight from HBM/L2 (every workgroup reads
+//      the same B, so it stays in L2).
+//   3. One lane per oscillator scans the 32 steps from a zero state; the
+//      chunk aggregate goes through the decoupled look-back of the oscillatory
+//      scans (tagged records, launch tickets, chunk transition M^32 formed in
+//      fp64) for the carry; the lane re-runs the chunk from the carry and
+//      overwrites the projection with x (imaginary part negated).
+//   4. Out-projection on the matrix cores (K = the oscillators, the two
+//      components as the MFMA's two k slots), plus D u, stored as y rows.
+//
+// MFMA operand layout (v_mfma_f32_32x32x2f32, 64 lanes): lane l supplies
+// A[m = l % 32][k = l / 32] and B[k = l / 32][n = l % 32]; accumulator register
+// r of lane l holds D[m = 8 (r / 4) + 4 (l / 32) + r % 4][n = l % 32].  The two
+// k slots of one instruction take h (or the component) from the two lane
+// halves; the sum over k is order-free in the math, so the in-projection gives
+// lane half j the h range [j H'/2, (j+1) H'/2) and reads both operands as
+// 16-byte runs along h.
+//
+// Limits: hidden and ssm sizes up to 256 (LDS of one workgroup: 32 rows of u
+// and 2 x 32 rows of the projection, padded to multiples of 32).
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+#include <string>
+
+#include "../../include/ossm_scan.h"
+#include "runtime.hpp"
+#include "scan_device.hpp"
+#include "dlinoss_model.hpp"
+
+namespace ossm {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kLc = 32;            // time steps per chunk = MFMA tile rows
+constexpr int kLayerWaves = 4;
+constexpr int kLayerThreads = kLayerWaves * kWave;
+constexpr int kLayerMax = 256;     // largest hidden / ssm size
+constexpr int kAhead = 8;          // weight groups (of 4 k-steps) loaded ahead
+
+__device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int round32(int n) { return (n + 31) & ~31; }
+
+struct LayerArgs {
+  const float* u;   // [B, L, H]
+  const float* Bw;  // [P, H, 2]
+  const float* Cw;  // [H, P, 2]
+  const float* Dw;  // [H]
+  const float* a;
+  const float* g;
+  const float* dt;
+  float* y;         // [B, L, H]
+  int Bsz, L, H, P, n_chunks;
+};
+
+// Row m of the accumulator register r (see the layout above).
+__device__ __forceinline__ int acc_row(int r, int lane) {
+  return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+}
+
+// In-projection weights of oscillator p for h = h0 .. h0 + 3, as
+// (re h0, im h0, re h0+1, im h0+1) and (re h0+2, ..): B[p, h, 0..1].  Zero
+// outside the tensor.  VEC: H % 4 == 0 and B 16-byte aligned.
+template <bool VEC>
+__device__ __forceinline__ void load_bw(const LayerArgs& A, int p, int h0, float4 (&w)[2]) {
+  if (VEC) {
+    if (p < A.P && h0 < A.H) {
+      const float4* src = reinterpret_cast<const float4*>(A.Bw + (static_cast<size_t>(p) * A.H + h0) * 2);
+      w[0] = src[0];
+      w[1] = src[1];
+    } else {
+      w[0] = w[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  } else {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int h = h0 + (j >> 1);
+      v[j] = (p < A.P && h < A.H) ? A.Bw[(static_cast<size_t>(p) * A.H + h) * 2 + (j & 1)] : 0.f;
+    }
+    w[0] = make_float4(v[0], v[1], v[2], v[3]);
+    w[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+// Out-projection weights of output column h for oscillators p0, p0 + 1:
+// (re p0, im p0, re p0+1, im p0+1) = C[h, p0 .. p0+1, 0..1], zero outside.
+// VEC: P % 4 == 0 (p0 even) and C 16-byte aligned.
+template <bool VEC>
+__device__ __forceinline__ float4 load_cw(const LayerArgs& A, int h, int p0) {
+  if (VEC) {
+    if (h < A.H && p0 < A.P)
+      return *reinterpret_cast<const float4*>(A.Cw + (static_cast<size_t>(h) * A.P + p0) * 2);
+    return make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int pj = p0 + (j >> 1);
+    v[j] = (h < A.H && pj < A.P) ? A.Cw[(static_cast<size_t>(h) * A.P + pj) * 2 + (j & 1)] : 0.f;
+  }
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+template <int V, bool VEC>
+__global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_fwd_kernel(
+    LayerArgs A, unsigned long long* __restrict__ rec, LaunchSync sync) {
+  using Model = Dlinoss<V>;
+  extern __shared__ __align__(16) float smem[];
+  __shared__ int s_ticket;
+
+  const int Hp = round32(A.H), Pp = round32(A.P);
+  const int HS = Hp + 4, XS = 2 * Pp + 4;  // row strides (floats): 16-byte rows, banks staggered
+  float* sU = smem;                        // [kLc][HS]     u rows of the chunk
+  float* sX = smem + kLc * HS;             // [kLc][Pp][2]  bu (re, im), then (x.re, -x.im)
+  float4* s_agg = reinterpret_cast<float4*>(sX + kLc * XS);  // [P] chunk aggregates
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = wave_id();
+  const int ticket = launch_order(sync, A.Bsz * A.n_chunks, &s_ticket);
+  if (ticket < 0) return;
+  const int c = ticket / A.Bsz;  // every chunk-(c-1) workgroup holds an earlier ticket
+  const int b = ticket - c * A.Bsz;
+  const int t0 = c * kLc;
+  const int nt = min(kLc, A.L - t0);
+  const size_t row0 = (static_cast<size_t>(b) * A.L + t0) * A.H;  // u / y row t0 of batch b
+
+  // 1. u rows t0 .. t0 + nt - 1 (contiguous) -> LDS, zero-padded to 32 x Hp
+  {
+    const int q4 = Hp / 4;
+    for (int e = threadIdx.x; e < kLc * q4; e += kLayerThreads) {
+      const int t = e / q4, h = (e - t * q4) * 4;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (t < nt) {
+        const float* src = A.u + row0 + static_cast<size_t>(t) * A.H + h;
+        if (VEC) {
+          if (h < A.H) v = *reinterpret_cast<const float4*>(src);
+        } else {
+          v.x = h < A.H ? src[0] : 0.f;
+          v.y = h + 1 < A.H ? src[1] : 0.f;
+          v.z = h + 2 < A.H ? src[2] : 0.f;
+          v.w = h + 3 < A.H ? src[3] : 0.f;
+        }
+      }
+      *reinterpret_cast<float4*>(sU + t * HS + h) = v;
+    }
+  }
+  __syncthreads();
+
+  // 2. in-projection: for oscillator group pg (32 oscillators) the wave forms
+  //    the re and im 32 x 32 tiles, K = Hp split over the two lane halves.
+  {
+    const int half = lane >> 5, m = lane & 31;
+    const int hh = Hp / 2;        // h per lane half (a multiple of 16)
+    const int ng = hh / 4;        // groups of 4 k-steps (a multiple of 4)
+    const float* arow = sU + m * HS + half * hh;
+    for (int pg = w; pg < Pp / 32; pg += kLayerWaves) {
+      const int p = pg * 32 + m;
+      floatx16 acc_re, acc_im;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc_re[r] = acc_im[r] = 0.f;
+      float4 wb[kAhead][2];
+#pragma unroll
+      for (int j = 0; j < kAhead; ++j) load_bw<VEC>(A, p, half * hh + 4 * j, wb[j]);
+      for (int q0 = 0; q0 < ng; q0 += kAhead) {
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) {
+          const int q = q0 + j;
+          if (q >= ng) break;  // uniform; ng need not be a multiple of kAhead
+          const float4 av = *reinterpret_cast<const float4*>(arow + 4 * q);
+          const float4 w0 = wb[j][0], w1 = wb[j][1];
+          if (q + kAhead < ng) load_bw<VEC>(A, p, half * hh + 4 * (q + kAhead), wb[j]);
+          acc_re = mfma32(av.x, w0.x, acc_re);
+          acc_im = mfma32(av.x, w0.y, acc_im);
+          acc_re = mfma32(av.y, w0.z, acc_re);
+          acc_im = mfma32(av.y, w0.w, acc_im);
+          acc_re = mfma32(av.z, w1.x, acc_re);
+          acc_im = mfma32(av.z, w1.y, acc_im);
+          acc_re = mfma32(av.w, w1.z, acc_re);
+          acc_im = mfma32(av.w, w1.w, acc_im);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = acc_row(r, lane);
+        *reinterpret_cast<float2*>(sX + t * XS + 2 * (pg * 32 + m)) = make_float2(acc_re[r], acc_im[r]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // 3. the scan, one thread per oscillator
+  const int p = threadIdx.x;
+  const bool osc = p < A.P;
+  const int nc = A.Bsz * A.P;
+  const int ch = b * A.P + p;
+  const bool scan = A.n_chunks > 1;
+  typename Model::Coef k{};
+  if (osc) k = Model::coef_of({A.a[p], A.g[p], A.dt[p]});
+  // All 32 steps run: rows past L hold zeros (zero u rows), which only the
+  // last chunk has; its aggregate is never read and its rows past L never stored.
+  const float2* bu_col = reinterpret_cast<const float2*>(sX) + p;
+  const int xs2 = XS / 2;
+  float4 e = f4zero();
+  if (osc) {
+#pragma unroll
+    for (int t = 0; t < kLc; ++t) e = Model::step(k, e, bu_col[t * xs2]);
+    s_agg[p] = e;
+  }
+  // The aggregate is published by a wave that does not then walk back when
+  // there is one (P <= 128: waves 2 and 3): a wave's loads complete in issue
+  // order behind its own stores.
+  const bool split_pub = A.P <= 2 * kWave;
+  if (scan && c > 0) {
+    if (split_pub) {
+      __syncthreads();
+      const int q = threadIdx.x - 2 * kWave;
+      if (q >= 0 && q < A.P) rec_publish(rec, c, kRecAgg, nc, b * A.P + q, s_agg[q], sync.tag);
+    } else if (osc) {
+      rec_publish(rec, c, kRecAgg, nc, ch, e, sync.tag);
+    }
+  }
+  if (osc) {
+    float4 s = f4zero();
+    if (scan) {
+      const RMat MC = mat_pow(Model::matrix(k), kLc);
+      if (c == 0) {
+        rec_publish(rec, c, kRecInc, nc, ch, e, sync.tag);
+      } else {
+        s = lookback(rec, c, +1, A.n_chunks, nc, ch, MC, sync);
+        if (c + 1 < A.n_chunks) rec_publish(rec, c, kRecInc, nc, ch, f4add(mat_apply(MC, s), e), sync.tag);
+      }
+    }
+    float2* x_col = reinterpret_cast<float2*>(sX) + p;
+#pragma unroll
+    for (int t = 0; t < kLc; ++t) {
+      s = Model::step(k, s, x_col[t * xs2]);
+      x_col[t * xs2] = make_float2(s.z, -s.w);
+    }
+  }
+  __syncthreads();
+
+  // 4. out-projection + D skip: wave w owns output column groups w, w+4, ...
+  //    Group q covers oscillators 4q .. 4q+3; lane half kk takes 4q + 2kk and
+  //    4q + 2kk + 1, so A (x.re, -x.im of two oscillators, from LDS) and B
+  //    (C[h, p, re], C[h, p, im] of the same two) are matching 16-byte runs.
+  {
+    const int kk = lane >> 5, m = lane & 31;
+    const int ng = Pp / 4;  // groups of 4 oscillators (a multiple of 8)
+    const float* arow = sX + m * XS + 4 * kk;
+    for (int hg = w; hg < Hp / 32; hg += kLayerWaves) {
+      const int h = hg * 32 + m;
+      floatx16 acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+      float4 cb[kAhead];
+#pragma unroll
+      for (int j = 0; j < kAhead; ++j) cb[j] = load_cw<VEC>(A, h, 4 * j + 2 * kk);
+      for (int q0 = 0; q0 < ng; q0 += kAhead) {
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) {
+          const int q = q0 + j;
+          if (q >= ng) break;  // uniform
+          const float4 av = *reinterpret_cast<const float4*>(arow + 8 * q);
+          const float4 cv = cb[j];
+          if (q + kAhead < ng) cb[j] = load_cw<VEC>(A, h, 4 * (q + kAhead) + 2 * kk);
+          acc = mfma32(av.x, cv.x, acc);
+          acc = mfma32(av.y, cv.y, acc);
+          acc = mfma32(av.z, cv.z, acc);
+          acc = mfma32(av.w, cv.w, acc);
+        }
+      }
+      if (h < A.H) {
+        const float dh = A.Dw[h];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int t = acc_row(r, lane);
+          if (t < nt) A.y[row0 + static_cast<size_t>(t) * A.H + h] = acc[r] + sU[t * HS + h] * dh;
+        }
+      }
+    }
+  }
+}
+
+size_t layer_lds_bytes(int64_t H, int64_t P) {
+  const int64_t Hp = (H + 31) / 32 * 32, Pp = (P + 31) / 32 * 32;
+  return static_cast<size_t>(kLc * (Hp + 4) + kLc * (2 * Pp + 4) + 4 * P) * sizeof(float);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int V>
+int launch_layer(const LayerArgs& args, hipStream_t stream) {
+  const int64_t n_wg = static_cast<int64_t>(args.Bsz) * args.n_chunks;
+  const int64_t nc = static_cast<int64_t>(args.Bsz) * args.P;
+  const size_t rec_bytes = static_cast<size_t>(args.n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
+  void* payload = nullptr;
+  LaunchSync sync{};
+  if (int rc = acquire_scratch(stream, rec_bytes, n_wg, &payload, &sync)) return rc;
+  const bool vec = args.H % 4 == 0 && args.P % 4 == 0 && aligned16(args.u) && aligned16(args.Bw) &&
+                   aligned16(args.Cw);
+  auto kern = vec ? dlinoss_layer_fwd_kernel<V, true> : dlinoss_layer_fwd_kernel<V, false>;
+  const size_t lds = layer_lds_bytes(args.H, args.P);
+  if (int rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(lds)),
+                         "hipFuncSetAttribute"))
+    return rc;
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(n_wg)), dim3(kLayerThreads), lds, stream, args,
+                     static_cast<unsigned long long*>(payload), sync);
+  if (hipPeekAtLastError() != hipSuccess) release_unlaunched(stream, n_wg);
+  return launch_check("dlinoss_layer_fwd_kernel");
+}
+
+}  // namespace
+}  // namespace ossm
+
+using namespace ossm;
+
+extern "C" {
+
+int ossm_dlinoss_layer_forward(int variant, const float* inputs, const float* B, const float* C,
+                               const float* D, const float* a_diag, const float* g_diag,
+                               const float* step, float* outputs, int64_t batch, int64_t length,
+                               int64_t hidden, int64_t ssm, ossm_stream_t stream_v) {
+  clear_error();
+  const char* what = "dlinoss_layer_forward";
+  if (batch < 0 || length < 0 || hidden < 0 || ssm < 0)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": negative size");
+  if (variant < OSSM_DLINOSS_IMEX1 || variant > OSSM_DLINOSS_EX)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": unknown variant");
+  if (hidden > kLayerMax || ssm > kLayerMax)
+    return set_error(OSSM_ERR_UNSUPPORTED, std::string(what) + ": hidden_dim and ssm_size up to " +
+                                               std::to_string(kLayerMax) + " are supported, got " +
+                                               std::to_string(hidden) + " and " + std::to_string(ssm));
+  if (batch == 0 || length == 0 || hidden == 0) return OSSM_OK;
+  const int64_t n_chunks = (length + kLc - 1) / kLc;
+  if (length > INT_MAX || batch * n_chunks > INT_MAX || batch * length * hidden > (int64_t(1) << 62) ||
+      batch * ssm > INT_MAX / 8)
+    return set_error(OSSM_ERR_UNSUPPORTED, std::string(what) + ": size exceeds 32-bit indexing");
+  if (!inputs || !D || !outputs || (ssm > 0 && (!B || !C || !a_diag || !g_diag || !step)))
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": null pointer");
+  LayerArgs args{inputs, B, C, D, a_diag, g_diag, step, outputs,
+                 static_cast<int>(batch), static_cast<int>(length), static_cast<int>(hidden),
+                 static_cast<int>(ssm), static_cast<int>(n_chunks)};
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  switch (variant) {
+    case OSSM_DLINOSS_IMEX1: return launch_layer<OSSM_DLINOSS_IMEX1>(args, stream);
+    case OSSM_DLINOSS_IMEX2: return launch_layer<OSSM_DLINOSS_IMEX2>(args, stream);
+    case OSSM_DLINOSS_IM: return launch_layer<OSSM_DLINOSS_IM>(args, stream);
+    default: return launch_layer<OSSM_DLINOSS_EX>(args, stream);
+  }
+}
+
+}  // extern "C"
