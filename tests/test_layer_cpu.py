@@ -137,4 +137,5 @@ def test_layer_module_interface():
     with pytest.raises(RuntimeError, match="float32"):
         layer.double()(torch.zeros(1, 2, 4, dtype=torch.float64))
     bound = 1.0 / math.sqrt(4)
-    assert float(layer.B.abs().max()) <= bound and float(layer.C.abs().max()) <= 1.0 / math.sqrt(6)
+    assert float(layer.B.detach().abs().max()) <= bound
+    assert float(layer.C.detach().abs().max()) <= 1.0 / math.sqrt(6)
