@@ -42,7 +42,7 @@ enum {
 
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
-/* Library ABI version (bumped on any change of the entry points; currently 6). */
+/* Library ABI version (bumped on any change of the entry points; currently 7). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -238,6 +238,55 @@ int ossm_dlinoss_layer_forward(int variant, const float* inputs, const float* B,
                                const float* D, const float* a_diag, const float* g_diag,
                                const float* step, float* outputs, int64_t batch, int64_t length,
                                int64_t hidden, int64_t ssm, ossm_stream_t stream);
+
+/*
+ * Selective scan in the Mamba mixer's layout (mambarec.py:136-184 feeds the
+ * scan transposed copies; this reads the mixer's tensors in place).  u, dt,
+ * gate [batch, length, dim] with row strides ld_u, ld_dt, ld_z (>= dim); dt is
+ * given before its softplus: the scan uses softplus(dt + dt_bias[d])
+ * (mambarec.py:155, torch's threshold 20; dt_bias may be null); B, C
+ * [batch, length, dstate] views with row stride ld_bc (the x_proj output
+ * split, mambarec.py:153); A [dim, dstate].  out, raw_out dense
+ * [batch, length, dim]; chunk_states as ossm_selective_forward.  Same
+ * recurrence and gate as ossm_selective_forward (selective_scan_cuda.cu:253-310).
+ */
+int ossm_selective_mamba_forward(const float* u, int64_t ld_u, const float* dt, int64_t ld_dt,
+                                 const float* dt_bias, const float* A, const float* B,
+                                 const float* C, int64_t ld_bc, const float* gate, int64_t ld_z,
+                                 float* out, float* raw_out, float* chunk_states, int64_t batch,
+                                 int64_t dim, int64_t length, int64_t dstate, ossm_stream_t stream);
+
+/*
+ * Backward of ossm_selective_mamba_forward (selective_scan_cuda.cu:312-393 in
+ * this layout).  du, ddt, dgate dense [batch, length, dim]; ddt is the gradient
+ * w.r.t. dt before the softplus (the dt_bias gradient is its sum over batch and
+ * length); dA [dim, dstate]; dB, dC dense [batch, length, dstate].
+ */
+int ossm_selective_mamba_backward(const float* grad_out, const float* u, int64_t ld_u,
+                                  const float* dt, int64_t ld_dt, const float* dt_bias,
+                                  const float* A, const float* B, const float* C, int64_t ld_bc,
+                                  const float* gate, int64_t ld_z, const float* chunk_states,
+                                  const float* raw_out, float* du, float* ddt, float* dA,
+                                  float* dB, float* dC, float* dgate, int64_t batch, int64_t dim,
+                                  int64_t length, int64_t dstate, ossm_stream_t stream);
+
+/*
+ * The Mamba mixer's causal depthwise convolution + SiLU (mambarec.py:143-150:
+ * pad K-1 on the left, Conv1d(groups=D), SiLU), in the [batch, length, dim]
+ * layout: out[b,t,d] = silu(bias[d] + sum_k weight[d,k] x[b,t-K+1+k,d]).  x has
+ * row stride ld_x (the x half of in_proj's output); weight [dim, width]
+ * (Conv1d's [dim, 1, width]); bias [dim] or null; out dense.  width 1..8.
+ */
+int ossm_mamba_conv_forward(const float* x, int64_t ld_x, const float* weight, const float* bias,
+                            float* out, int64_t batch, int64_t length, int64_t dim, int64_t width,
+                            ossm_stream_t stream);
+
+/* Backward of the above: grad_x dense [batch, length, dim]; grad_weight
+ * [dim, width] and grad_bias [dim] (may be null) summed in a fixed order. */
+int ossm_mamba_conv_backward(const float* x, int64_t ld_x, const float* weight, const float* bias,
+                             const float* grad_out, float* grad_x, float* grad_weight,
+                             float* grad_bias, int64_t batch, int64_t length, int64_t dim,
+                             int64_t width, ossm_stream_t stream);
 
 #ifdef __cplusplus
 }

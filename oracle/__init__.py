@@ -13,7 +13,8 @@ D-LinOSS alike, with parameters (M,), (L,M), (B,M) or (L|1,B|1,M)); LinOSS
 ``b_seq [L,B,P,2]`` complex with complex ``m_ij [P]``; diagonal (LRU / S5)
 scans ``b_seq [L,B,P]`` complex with complex ``lambda_bar [P]``; selective scan
 ``u, dt, gate [B,D,L]``, ``A [D,N]``, ``B, C [B,L,N]`` real; the D-LinOSS
-layer ``inputs, outputs [B,L,H]`` real with ``B [P,H,2]``, ``C [H,P,2]``.
+layer ``inputs, outputs [B,L,H]`` real with ``B [P,H,2]``, ``C [H,P,2]``; the
+Mamba mixer's steps in its ``[B,L,D]`` layout.
 """
 
 from __future__ import annotations
@@ -225,6 +226,42 @@ def selective_forward(u, dt, A, Bm, Cm, gate=None) -> np.ndarray:
     _fn("oracle_selective_forward", prec)(_ptr(u), _ptr(dt), _ptr(A), _ptr(Bm), _ptr(Cm),
                                           _ptr(gate), _ptr(out), I(Bsz), I(D), I(L), I(N))
     return out
+
+
+# ------------------------------------------------ Mamba mixer pre/post steps
+def softplus(x) -> np.ndarray:
+    """F.softplus with torch's defaults (beta 1, threshold 20: x itself above),
+    as mambarec.py:155 applies it to dt."""
+    x = np.asarray(x)
+    return np.where(x > 20, x, np.log1p(np.exp(np.minimum(x, 20)))).astype(x.dtype)
+
+
+def mamba_conv_silu(x, weight, bias=None) -> np.ndarray:
+    """``silu(Conv1d(pad_left(x^T, K-1)))^T`` of mambarec.py:143-150 for x
+    ``[B,L,D]``, depthwise weight ``[D,1,K]`` or ``[D,K]``, bias ``[D]``:
+    ``pre[b,t,d] = bias[d] + sum_k w[d,k] x[b,t-K+1+k,d]`` (zero before t = 0)."""
+    x = np.asarray(x)
+    rt = x.dtype
+    nb, L, D = x.shape
+    w = np.asarray(weight, rt).reshape(D, -1)
+    K = w.shape[1]
+    pad = np.concatenate([np.zeros((nb, K - 1, D), rt), x], axis=1)
+    pre = np.zeros((nb, L, D), rt) + (np.asarray(bias, rt) if bias is not None else 0)
+    for k in range(K):
+        pre = pre + w[:, k] * pad[:, k:k + L, :]
+    return (pre / (1 + np.exp(-pre))).astype(rt)
+
+
+def selective_forward_bld(u, dt_pre, A, Bm, Cm, gate=None, dt_bias=None) -> np.ndarray:
+    """The selective scan in the mixer's ``[B,L,D]`` layout with dt given before
+    its softplus (mambarec.py:155-170): transposes to ``[B,D,L]``, the scan
+    above, and back."""
+    u = np.asarray(u)
+    dt = np.asarray(dt_pre) + (0 if dt_bias is None else np.asarray(dt_bias))
+    t = lambda a: np.ascontiguousarray(np.asarray(a).transpose(0, 2, 1))
+    y = selective_forward(t(u), t(softplus(dt.astype(u.dtype))), A, Bm, Cm,
+                          None if gate is None else t(gate))
+    return np.ascontiguousarray(y.transpose(0, 2, 1))
 
 
 def selective_backward(grad_output, u, dt, A, Bm, Cm, gate=None):

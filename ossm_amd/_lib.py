@@ -69,6 +69,19 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_int, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _c_int64, _c_int64, _c_int64,
          _c_int64, _vp]),
+    "ossm_selective_mamba_forward": (
+        ctypes.c_int,
+        [_fp, _c_int64, _fp, _c_int64, _fp, _fp, _fp, _fp, _c_int64, _fp, _c_int64, _fp, _fp, _fp,
+         _c_int64, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_selective_mamba_backward": (
+        ctypes.c_int,
+        [_fp, _fp, _c_int64, _fp, _c_int64, _fp, _fp, _fp, _fp, _c_int64, _fp, _c_int64, _fp, _fp,
+         _fp, _fp, _fp, _fp, _fp, _fp, _c_int64, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_mamba_conv_forward": (
+        ctypes.c_int, [_fp, _c_int64, _fp, _fp, _fp, _c_int64, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_mamba_conv_backward": (
+        ctypes.c_int,
+        [_fp, _c_int64, _fp, _fp, _fp, _fp, _fp, _fp, _c_int64, _c_int64, _c_int64, _c_int64, _vp]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -267,6 +267,115 @@ __device__ __forceinline__ void store_row4(E* __restrict__ g, size_t off, int t,
   }
 }
 
+// ---- [B, L, D] tensors (the Mamba mixer's layout: channels contiguous) -----
+// The same 64-channel x TT-step tile, loaded as 16-byte runs along the
+// channels: thread i owns groups q = i + k * kThreads, step q / 16, channels
+// 4 (q % 16) .. +3; written to LDS transposed (s[channel * RS + step]), the
+// layout the kernels read.  `base` is the tensor's (b, 0, 0), `ld` its row
+// stride (elements per step).  VEC: D % 4 == 0, ld % 4 == 0, 16-byte base.
+template <int TT>
+__device__ __forceinline__ void tile_pos_bld(int k, int& step, int& c4) {
+  const int q = threadIdx.x + k * kThreads;
+  step = q >> 4;
+  c4 = (q & 15) * 4;
+}
+
+template <int TT, bool VEC, class E>
+__device__ __forceinline__ void load_cols(RowRegs<TT>& r, const E* __restrict__ g, size_t base,
+                                          int ld, int d0, int D, int t0, int L) {
+#pragma unroll
+  for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+    int step, c4;
+    tile_pos_bld<TT>(k, step, c4);
+    const E* row = g + base + static_cast<size_t>(min(t0 + step, L - 1)) * ld;
+    if constexpr (VEC) {
+      r.v[k] = Elem<E>::load4(row + min(d0 + c4, D - 4));
+    } else {
+      r.v[k].x = Elem<E>::load1(row + min(d0 + c4, D - 1));
+      r.v[k].y = Elem<E>::load1(row + min(d0 + c4 + 1, D - 1));
+      r.v[k].z = Elem<E>::load1(row + min(d0 + c4 + 2, D - 1));
+      r.v[k].w = Elem<E>::load1(row + min(d0 + c4 + 3, D - 1));
+    }
+  }
+}
+
+template <int TT>
+__device__ __forceinline__ bool col_ok(int k, int e, int d0, int D, int t0, int L) {
+  int step, c4;
+  tile_pos_bld<TT>(k, step, c4);
+  return d0 + c4 + e < D && t0 + step < L;
+}
+
+template <int TT>
+__device__ __forceinline__ float4 masked_cols(const RowRegs<TT>& r, int k, int d0, int D, int t0,
+                                              int L) {
+  const float4 v = r.v[k];
+  return make_float4(col_ok<TT>(k, 0, d0, D, t0, L) ? v.x : 0.f,
+                     col_ok<TT>(k, 1, d0, D, t0, L) ? v.y : 0.f,
+                     col_ok<TT>(k, 2, d0, D, t0, L) ? v.z : 0.f,
+                     col_ok<TT>(k, 3, d0, D, t0, L) ? v.w : 0.f);
+}
+
+__device__ __forceinline__ void put_col4(float* __restrict__ s, int RS, int c4, int step, float4 v) {
+  s[c4 * RS + step] = v.x;
+  s[(c4 + 1) * RS + step] = v.y;
+  s[(c4 + 2) * RS + step] = v.z;
+  s[(c4 + 3) * RS + step] = v.w;
+}
+
+template <int TT, int RS>
+__device__ __forceinline__ void store_cols(float* __restrict__ s, const RowRegs<TT>& r, int d0,
+                                           int D, int t0, int L) {
+#pragma unroll
+  for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+    int step, c4;
+    tile_pos_bld<TT>(k, step, c4);
+    put_col4(s, RS, c4, step, masked_cols<TT>(r, k, d0, D, t0, L));
+  }
+}
+
+// softplus(x) = log(1 + e^x), and x itself above 20 (torch's default threshold,
+// F.softplus as mambarec.py:155 applies it).
+__device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
+// dt = softplus(dt_pre + bias[d]) staged like store_cols (bias may be null).
+template <int TT, int RS>
+__device__ __forceinline__ void store_cols_softplus(float* __restrict__ s, const RowRegs<TT>& r,
+                                                    const float* __restrict__ bias, int d0, int D,
+                                                    int t0, int L) {
+#pragma unroll
+  for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+    int step, c4;
+    tile_pos_bld<TT>(k, step, c4);
+    const float4 v = r.v[k];
+    const float x[4] = {v.x, v.y, v.z, v.w};
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = min(d0 + c4 + e, D - 1);
+      o[e] = col_ok<TT>(k, e, d0, D, t0, L) ? softplus(x[e] + (bias != nullptr ? bias[d] : 0.f)) : 0.f;
+    }
+    put_col4(s, RS, c4, step, make_float4(o[0], o[1], o[2], o[3]));
+  }
+}
+
+// kSeg consecutive steps t .. of channel d of a [B, L, D] tensor (row stride
+// ld): strided scalar accesses; reads past L use a clamped in-range step.
+template <class E>
+__device__ __forceinline__ void load_seg_bld(float (&v)[8], const E* __restrict__ g, size_t base,
+                                             int ld, int d, int t, int L) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = Elem<E>::load1(g + base + static_cast<size_t>(min(t + k, L - 1)) * ld + d);
+}
+
+template <class E>
+__device__ __forceinline__ void store_seg_bld(E* __restrict__ g, size_t base, int ld, int d, int t,
+                                              int L, const float (&v)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (t + k < L) Elem<E>::store1(g + base + static_cast<size_t>(t + k) * ld + d, v[k]);
+}
+
 // B or C rows t0..t0+TT-1, states n_base..n_base+15 (zero outside the
 // tensor, so padded states contribute nothing); LDS layout s[t * 16 + j].
 template <int TT>
@@ -275,14 +384,16 @@ struct StateRegs {
   float v[kQ];
 };
 
+// `ld` is the row stride (N for a dense [B, L, N] tensor; wider for a view
+// into a projection's output).
 template <int TT, class E>
 __device__ __forceinline__ void load_states(StateRegs<TT>& r, const E* __restrict__ g,
-                                            size_t base, int t0, int L, int N, int n_base) {
+                                            size_t base, int ld, int t0, int L, int N, int n_base) {
 #pragma unroll
   for (int k = 0; k < StateRegs<TT>::kQ; ++k) {
     const int e = threadIdx.x + k * kThreads;
     const int t = e / kPassStates, j = e - t * kPassStates;
-    r.v[k] = Elem<E>::load1(g + base + static_cast<size_t>(min(t0 + t, L - 1)) * N +
+    r.v[k] = Elem<E>::load1(g + base + static_cast<size_t>(min(t0 + t, L - 1)) * ld +
                             min(n_base + j, N - 1));
   }
 }
@@ -313,6 +424,11 @@ struct FwdArgs {
   float* ckpt;       // chunk_states, may be null
   int D, L, N, n_base, n_chunks;
   int first, last, vec;
+  int ld_bc;         // row stride of B and C
+  // [B, L, D] layout only: row strides of u, dt and z (out, raw, acc: D), and
+  // dt given before its softplus, with an optional per-channel bias
+  int ld_u, ld_dt, ld_z;
+  const float* dt_bias;
 };
 
 __device__ __forceinline__ void write_ckpt(float* ckpt, size_t lane_row, int slot, int N,
@@ -329,13 +445,20 @@ struct FwdTile {
   StateRegs<kFwdTile> B, C;
 };
 
-template <class E, bool VEC>
+// row0: (b, 0, 0) of the [B, D, L] tensors; with BLD, bl0 = b * L is the
+// first row of batch b and each tensor adds its own row stride.
+template <class E, bool VEC, bool BLD>
 __device__ __forceinline__ void fwd_prefetch(FwdTile& f, const FwdArgs<E>& a, size_t row0,
                                              size_t bc0, int d0, int t0) {
-  load_rows<kFwdTile, VEC>(f.u, a.u, row0, d0, a.D, t0, a.L);
-  load_rows<kFwdTile, VEC>(f.dt, a.dt, row0, d0, a.D, t0, a.L);
-  load_states<kFwdTile>(f.B, a.Bm, bc0, t0, a.L, a.N, a.n_base);
-  load_states<kFwdTile>(f.C, a.Cm, bc0, t0, a.L, a.N, a.n_base);
+  if constexpr (BLD) {
+    load_cols<kFwdTile, VEC>(f.u, a.u, row0 * a.ld_u, a.ld_u, d0, a.D, t0, a.L);
+    load_cols<kFwdTile, VEC>(f.dt, a.dt, row0 * a.ld_dt, a.ld_dt, d0, a.D, t0, a.L);
+  } else {
+    load_rows<kFwdTile, VEC>(f.u, a.u, row0, d0, a.D, t0, a.L);
+    load_rows<kFwdTile, VEC>(f.dt, a.dt, row0, d0, a.D, t0, a.L);
+  }
+  load_states<kFwdTile>(f.B, a.Bm, bc0, a.ld_bc, t0, a.L, a.N, a.n_base);
+  load_states<kFwdTile>(f.C, a.Cm, bc0, a.ld_bc, t0, a.L, a.N, a.n_base);
 }
 
 // The forward's lane layout: lane = (channel c = lane % 16, state group
@@ -400,7 +523,7 @@ __device__ __forceinline__ void reduce_groups(float (&yv)[kFwdTile], float (&out
 
 // GATED kernels multiply by silu(z) in the last pass; VEC: L % 4 == 0 and
 // u/dt/z/out rows 16-byte aligned.
-template <class E, bool VEC, bool GATED>
+template <class E, bool VEC, bool GATED, bool BLD>
 __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   constexpr int TT = kFwdTile;
   constexpr int RS = TT + 1;  // odd row stride: lane-per-row accesses hit distinct banks
@@ -426,20 +549,36 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     A2[j] = (dvalid && n0 + j < a.N) ? a.A[static_cast<size_t>(d) * a.N + n0 + j] * kLog2e : 0.f;
     h[j] = 0.f;
   }
-  const size_t row0 = static_cast<size_t>(b) * a.D * a.L;     // (b, 0, 0) in [B,D,L]
-  const size_t bc0 = static_cast<size_t>(b) * a.L * a.N;      // (b, 0, 0) in [B,L,N]
+  // BDL: row0 = (b, 0, 0) of [B,D,L]; BLD: row0 = b * L, the first row of batch b
+  const size_t row0 = BLD ? static_cast<size_t>(b) * a.L : static_cast<size_t>(b) * a.D * a.L;
+  const size_t bc0 = static_cast<size_t>(b) * a.L * a.ld_bc;  // (b, 0, 0) of B and C
   const size_t ck_row = (static_cast<size_t>(b) * a.D + (dvalid ? d : 0)) * a.n_chunks * 2 * a.N;
-  const size_t my_row = row0 + static_cast<size_t>(dvalid ? d : a.D - 1) * a.L;  // [.., L] row of d
+  const int dc = dvalid ? d : a.D - 1;
+  const size_t my_row = row0 + static_cast<size_t>(dc) * a.L;  // [.., L] row of d (BDL)
+  const size_t out0 = row0 * a.D;                              // (b, 0, 0) of out/raw/acc (BLD)
   const bool ck = a.ckpt != nullptr && dvalid;
+  auto load_gate = [&](float (&zv)[kSeg], int t) {
+    if constexpr (BLD) load_seg_bld(zv, a.z, row0 * a.ld_z, a.ld_z, dc, t, a.L);
+    else load_seg<VEC>(zv, a.z, my_row, t, a.L);
+  };
+  auto put_seg = [&](auto* dst, int t, const float (&v)[kSeg]) {
+    if constexpr (BLD) store_seg_bld(dst, out0, a.D, d, t, a.L, v);
+    else store_seg<VEC>(dst, my_row, t, a.L, v);
+  };
 
   FwdTile nxt;
   float zn[kSeg];  // the gate of the lane's output segment, one tile ahead
-  fwd_prefetch<E, VEC>(nxt, a, row0, bc0, d0, 0);
-  if constexpr (GATED) load_seg<VEC>(zn, a.z, my_row, kSeg * g, a.L);
+  fwd_prefetch<E, VEC, BLD>(nxt, a, row0, bc0, d0, 0);
+  if constexpr (GATED) load_gate(zn, kSeg * g);
   for (int t0 = 0; t0 < a.L; t0 += TT) {
     __syncthreads();  // the previous tile's LDS readers are done
-    store_rows<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
-    store_rows<TT, RS>(s_dt, nxt.dt, d0, a.D, t0, a.L);
+    if constexpr (BLD) {
+      store_cols<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
+      store_cols_softplus<TT, RS>(s_dt, nxt.dt, a.dt_bias, d0, a.D, t0, a.L);
+    } else {
+      store_rows<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
+      store_rows<TT, RS>(s_dt, nxt.dt, d0, a.D, t0, a.L);
+    }
     store_states<TT>(s_B, nxt.B, t0, a.L, a.N, a.n_base);
     store_states<TT>(s_C, nxt.C, t0, a.L, a.N, a.n_base);
     float zt[kSeg];
@@ -447,8 +586,8 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     for (int k = 0; k < kSeg; ++k) zt[k] = zn[k];
     __syncthreads();
     if (t0 + TT < a.L) {
-      fwd_prefetch<E, VEC>(nxt, a, row0, bc0, d0, t0 + TT);
-      if constexpr (GATED) load_seg<VEC>(zn, a.z, my_row, t0 + TT + kSeg * g, a.L);
+      fwd_prefetch<E, VEC, BLD>(nxt, a, row0, bc0, d0, t0 + TT);
+      if constexpr (GATED) load_gate(zn, t0 + TT + kSeg * g);
     }
 
     // Every tile runs all TT steps: past L the staged dt, u, B and C are zero,
@@ -521,19 +660,20 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
       const int t = t0 + kSeg * g;
       if (!a.first) {
         float prev[kSeg];
-        load_seg<false>(prev, a.acc, my_row, t, a.L);
+        if constexpr (BLD) load_seg_bld(prev, a.acc, out0, a.D, d, t, a.L);
+        else load_seg<false>(prev, a.acc, my_row, t, a.L);
 #pragma unroll
         for (int k = 0; k < kSeg; ++k) y[k] += prev[k];
       }
       if (a.last) {
-        if (a.raw != nullptr) store_seg<VEC>(a.raw, my_row, t, a.L, y);
+        if (a.raw != nullptr) put_seg(a.raw, t, y);
         if constexpr (GATED) {
 #pragma unroll
           for (int k = 0; k < kSeg; ++k) y[k] *= zt[k] * sigmoid(zt[k]);
         }
-        store_seg<VEC>(a.out, my_row, t, a.L, y);
+        put_seg(a.out, t, y);
       } else {
-        store_seg<VEC>(a.acc, my_row, t, a.L, y);
+        put_seg(a.acc, t, y);
       }
     }
   }
@@ -561,6 +701,11 @@ struct BwdArgs {
   float* part_dA;      // [B, D, N]
   int Bsz, D, L, N, n_base, n_chunks;
   int first, last, vec;
+  int ld_bc;           // row stride of B and C
+  // [B, L, D] layout only: row strides of u, dt and z (gout, raw, du, ddt, dz:
+  // D); dt is given before its softplus and ddt is returned w.r.t. it
+  int ld_u, ld_dt, ld_z;
+  const float* dt_bias;
 };
 
 struct BwdTile {
@@ -569,19 +714,29 @@ struct BwdTile {
   float h0[kNpw];  // state after the step before the tile (this lane, this wave's states), unmasked
 };
 
-template <class E, bool VEC, bool GATED>
+template <class E, bool VEC, bool GATED, bool BLD>
 __device__ __forceinline__ void bwd_prefetch(BwdTile& f, const BwdArgs<E>& a, size_t row0, size_t bc0,
                                              size_t ck_row, int d0, bool dvalid, int n0, int tile) {
   const int t0 = tile * kBwdTile;
-  load_rows<kBwdTile, VEC>(f.u, a.u, row0, d0, a.D, t0, a.L);
-  load_rows<kBwdTile, VEC>(f.dt, a.dt, row0, d0, a.D, t0, a.L);
-  load_rows<kBwdTile, VEC>(f.go, a.gout, row0, d0, a.D, t0, a.L);
-  if constexpr (GATED) {
-    load_rows<kBwdTile, VEC>(f.z, a.z, row0, d0, a.D, t0, a.L);
-    load_rows<kBwdTile, VEC>(f.raw, a.raw, row0, d0, a.D, t0, a.L);
+  if constexpr (BLD) {
+    load_cols<kBwdTile, VEC>(f.u, a.u, row0 * a.ld_u, a.ld_u, d0, a.D, t0, a.L);
+    load_cols<kBwdTile, VEC>(f.dt, a.dt, row0 * a.ld_dt, a.ld_dt, d0, a.D, t0, a.L);
+    load_cols<kBwdTile, VEC>(f.go, a.gout, row0 * a.D, a.D, d0, a.D, t0, a.L);
+    if constexpr (GATED) {
+      load_cols<kBwdTile, VEC>(f.z, a.z, row0 * a.ld_z, a.ld_z, d0, a.D, t0, a.L);
+      load_cols<kBwdTile, VEC>(f.raw, a.raw, row0 * a.D, a.D, d0, a.D, t0, a.L);
+    }
+  } else {
+    load_rows<kBwdTile, VEC>(f.u, a.u, row0, d0, a.D, t0, a.L);
+    load_rows<kBwdTile, VEC>(f.dt, a.dt, row0, d0, a.D, t0, a.L);
+    load_rows<kBwdTile, VEC>(f.go, a.gout, row0, d0, a.D, t0, a.L);
+    if constexpr (GATED) {
+      load_rows<kBwdTile, VEC>(f.z, a.z, row0, d0, a.D, t0, a.L);
+      load_rows<kBwdTile, VEC>(f.raw, a.raw, row0, d0, a.D, t0, a.L);
+    }
   }
-  load_states<kBwdTile>(f.B, a.Bm, bc0, t0, a.L, a.N, a.n_base);
-  load_states<kBwdTile>(f.C, a.Cm, bc0, t0, a.L, a.N, a.n_base);
+  load_states<kBwdTile>(f.B, a.Bm, bc0, a.ld_bc, t0, a.L, a.N, a.n_base);
+  load_states<kBwdTile>(f.C, a.Cm, bc0, a.ld_bc, t0, a.L, a.N, a.n_base);
   // state after step t0 - 1 = checkpoint slot tile - 1 (zero before the start)
   const int slot = max(tile - 1, 0);
   const float* p = a.ckpt + ck_row + static_cast<size_t>(slot >> 1) * 2 * a.N + (slot & 1) * a.N;
@@ -591,8 +746,9 @@ __device__ __forceinline__ void bwd_prefetch(BwdTile& f, const BwdArgs<E>& a, si
   }
 }
 
-template <class E, bool VEC, bool GATED>
+template <class E, bool VEC, bool GATED, bool BLD>
 __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
+  static_assert(!BLD || std::is_same_v<E, float>, "the [B, L, D] layout is fp32");
   constexpr int TT = kBwdTile;
   constexpr int HT = TT / 2;  // steps whose trajectory is held in registers at once
   constexpr int RS = TT + 1;
@@ -622,23 +778,60 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
     gs[j] = 0.f;
     gA[j] = 0.f;
   }
-  const size_t row0 = static_cast<size_t>(b) * a.D * a.L;
-  const size_t bc0 = static_cast<size_t>(b) * a.L * a.N;
+  // BDL: row0 = (b, 0, 0) of [B,D,L]; BLD: row0 = b * L, the first row of batch b
+  const size_t row0 = BLD ? static_cast<size_t>(b) * a.L : static_cast<size_t>(b) * a.D * a.L;
+  const size_t bc0 = static_cast<size_t>(b) * a.L * a.ld_bc;
   const size_t ck_row = (static_cast<size_t>(b) * a.D + (dvalid ? d : 0)) * a.n_chunks * 2 * a.N;
   const size_t part0 = (static_cast<size_t>(blockIdx.x) * a.Bsz + b) * a.L * a.N;
   const int n_tiles = (a.L + TT - 1) / TT;
 
   BwdTile nxt;
-  bwd_prefetch<E, VEC, GATED>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, n_tiles - 1);
+  bwd_prefetch<E, VEC, GATED, BLD>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, n_tiles - 1);
   for (int tile = n_tiles - 1; tile >= 0; --tile) {
     const int t0 = tile * TT;
     const int nsteps = min(TT, a.L - t0);
     __syncthreads();  // the previous tile's LDS readers are done
-    store_rows<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
-    store_rows<TT, RS>(s_dt, nxt.dt, d0, a.D, t0, a.L);
+    if constexpr (BLD) {
+      store_cols<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
+      store_cols_softplus<TT, RS>(s_dt, nxt.dt, a.dt_bias, d0, a.D, t0, a.L);
+    } else {
+      store_rows<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
+      store_rows<TT, RS>(s_dt, nxt.dt, d0, a.D, t0, a.L);
+    }
     store_states<TT>(s_B, nxt.B, t0, a.L, a.N, a.n_base);
     store_states<TT>(s_C, nxt.C, t0, a.L, a.N, a.n_base);
     // gated upstream gradient into LDS; the first pass also writes dz
+    if constexpr (BLD) {
+#pragma unroll
+      for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+        int step, c4;
+        tile_pos_bld<TT>(k, step, c4);
+        float4 gy = masked_cols<TT>(nxt.go, k, d0, a.D, t0, a.L);
+        if constexpr (GATED) {
+          const float4 zz = nxt.z.v[k], go = gy;
+          const float4 sg = make_float4(sigmoid(zz.x), sigmoid(zz.y), sigmoid(zz.z), sigmoid(zz.w));
+          gy = make_float4(go.x * zz.x * sg.x, go.y * zz.y * sg.y, go.z * zz.z * sg.z,
+                           go.w * zz.w * sg.w);
+          const int dd = d0 + c4, t = t0 + step;
+          if (a.first && t < a.L && dd < a.D) {
+            const float4 y = nxt.raw.v[k];
+            const float dzv[4] = {go.x * y.x * (sg.x * (1.f + zz.x * (1.f - sg.x))),
+                                  go.y * y.y * (sg.y * (1.f + zz.y * (1.f - sg.y))),
+                                  go.z * y.z * (sg.z * (1.f + zz.z * (1.f - sg.z))),
+                                  go.w * y.w * (sg.w * (1.f + zz.w * (1.f - sg.w)))};
+            E* dst = a.dz + (row0 + t) * a.D + dd;
+            if constexpr (VEC) {
+              Elem<E>::store4(dst, make_float4(dzv[0], dzv[1], dzv[2], dzv[3]));
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (dd + e < a.D) Elem<E>::store1(dst + e, dzv[e]);
+            }
+          }
+        }
+        put_col4(s_gy, RS, c4, step, gy);
+      }
+    } else {
 #pragma unroll
     for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
       int r, c;
@@ -665,11 +858,12 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
       p[2] = gy.z;
       p[3] = gy.w;
     }
+    }
     float h0[kNpw];
 #pragma unroll
     for (int j = 0; j < kNpw; ++j) h0[j] = (tile > 0 && dvalid && n0 + j < a.N) ? nxt.h0[j] : 0.f;
     __syncthreads();
-    if (tile > 0) bwd_prefetch<E, VEC, GATED>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile - 1);
+    if (tile > 0) bwd_prefetch<E, VEC, GATED, BLD>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile - 1);
 
     if (wave_active) {
       const float* dtrow = s_dt + lane * RS;
@@ -793,6 +987,50 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
     __syncthreads();
 
     // finish du / ddt over the waves (states), accumulate over passes
+    if constexpr (BLD) {
+      // 4 channels at one step per thread; ddt is taken through the softplus:
+      // d softplus(x) / dx = sigmoid(x) = 1 - e^{-softplus(x)} (staged in s_dt)
+#pragma unroll
+      for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+        int step, c4;
+        tile_pos_bld<TT>(k, step, c4);
+        const int dd = d0 + c4, t = t0 + step;
+        if (dd >= a.D || t >= a.L) continue;
+        float su[4] = {0.f, 0.f, 0.f, 0.f}, sd[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int v = 0; v < nw; ++v) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            su[e] += s_du[(v * kWave + c4 + e) * RS + step];
+            sd[e] += s_ddt[(v * kWave + c4 + e) * RS + step];
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sd[e] *= -expm1f(-s_dt[(c4 + e) * RS + step]);
+        const size_t gi = (row0 + t) * a.D + dd;
+        const int ne = min(4, a.D - dd);
+        if (!a.first) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (e < ne) {
+              su[e] += a.du_acc[gi + e];
+              sd[e] += a.ddt_acc[gi + e];
+            }
+        }
+        E* du = a.last ? a.du : reinterpret_cast<E*>(a.du_acc);
+        E* ddt = a.last ? a.ddt : reinterpret_cast<E*>(a.ddt_acc);
+        if (VEC) {
+          Elem<E>::store4(du + gi, make_float4(su[0], su[1], su[2], su[3]));
+          Elem<E>::store4(ddt + gi, make_float4(sd[0], sd[1], sd[2], sd[3]));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (e < ne) {
+              Elem<E>::store1(du + gi + e, su[e]);
+              Elem<E>::store1(ddt + gi + e, sd[e]);
+            }
+        }
+      }
+    } else {
 #pragma unroll
     for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
       int r, c;
@@ -827,6 +1065,7 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
         store_row4<VEC>(a.du_acc, gi, t, a.L, su);
         store_row4<VEC>(a.ddt_acc, gi, t, a.L, sd);
       }
+    }
     }
   }
 
@@ -915,13 +1154,33 @@ int zero_fill(E* p, int64_t n, hipStream_t stream) {
   return launch_check("selective_zero_kernel");
 }
 
+// The Mamba mixer's layout: u, dt, z and the outputs as [B, L, D] (row
+// strides below; outputs dense), dt before its softplus (plus an optional
+// per-channel bias), B and C as [B, L, N] views with row stride ld_bc.
+struct MambaLayout {
+  int64_t ld_u, ld_dt, ld_z, ld_bc;
+  const float* dt_bias;
+};
+
+bool aligned_to(const void* p, size_t bytes) { return reinterpret_cast<uintptr_t>(p) % bytes == 0; }
+
+// 16-byte moves along the channels: D and every row stride a multiple of 4
+// and every tensor 16-byte aligned (null pointers pass).
+bool cols_vectorizable(int64_t D, const MambaLayout& ml, std::initializer_list<const void*> ptrs) {
+  if (D % 4 != 0 || ml.ld_u % 4 != 0 || ml.ld_dt % 4 != 0 || ml.ld_z % 4 != 0) return false;
+  for (const void* p : ptrs)
+    if (!aligned_to(p, 16)) return false;
+  return true;
+}
+
 // E = float: the fp32 API of the reference.  E = bf16_t: the same scan with
-// bf16 rows, B and C in HBM (A, chunk_states and dA stay fp32).
+// bf16 rows, B and C in HBM (A, chunk_states and dA stay fp32).  ml: the
+// [B, L, D] layout (fp32 only); null for the reference's [B, D, L].
 template <class E>
 int selective_forward_impl(const E* u, const E* dt, const float* A, const E* Bm, const E* Cm,
                            const E* gate, E* out, E* raw_out, float* chunk_states, int64_t batch,
                            int64_t dim, int64_t length, int64_t dstate, hipStream_t stream,
-                           const char* what) {
+                           const char* what, const MambaLayout* ml = nullptr) {
   clear_error();
   if (int rc = check_selective(batch, dim, length, dstate, what)) return rc;
   if (batch == 0 || dim == 0 || length == 0) return OSSM_OK;
@@ -953,14 +1212,36 @@ int selective_forward_impl(const E* u, const E* dt, const float* A, const E* Bm,
   a.L = static_cast<int>(length);
   a.N = static_cast<int>(dstate);
   a.n_chunks = static_cast<int>(num_chunks(length));
-  a.vec = rows_vectorizable(length, sizeof(E), {u, dt, gate, out, raw_out}) ? 1 : 0;
+  a.ld_bc = static_cast<int>(dstate);
+  if (ml != nullptr) {
+    a.ld_bc = static_cast<int>(ml->ld_bc);
+    a.ld_u = static_cast<int>(ml->ld_u);
+    a.ld_dt = static_cast<int>(ml->ld_dt);
+    a.ld_z = static_cast<int>(ml->ld_z);
+    a.dt_bias = ml->dt_bias;
+    a.vec = cols_vectorizable(dim, *ml, {u, dt, gate, out, raw_out}) ? 1 : 0;
+  } else {
+    a.vec = rows_vectorizable(length, sizeof(E), {u, dt, gate, out, raw_out}) ? 1 : 0;
+  }
   const dim3 grid(static_cast<unsigned>((dim + kWave - 1) / kWave), static_cast<unsigned>(batch));
   for (int p = 0; p < n_pass; ++p) {
     a.n_base = p * kPassStates;
     a.first = p == 0;
     a.last = p == n_pass - 1;
-    auto kern = a.vec ? (gate ? selective_fwd_kernel<E, true, true> : selective_fwd_kernel<E, true, false>)
-                      : (gate ? selective_fwd_kernel<E, false, true> : selective_fwd_kernel<E, false, false>);
+    using K = void (*)(FwdArgs<E>);
+    K kern;
+    if constexpr (std::is_same_v<E, float>) {
+      if (ml != nullptr) {
+        kern = a.vec ? (gate ? selective_fwd_kernel<E, true, true, true> : selective_fwd_kernel<E, true, false, true>)
+                     : (gate ? selective_fwd_kernel<E, false, true, true> : selective_fwd_kernel<E, false, false, true>);
+      } else {
+        kern = a.vec ? (gate ? selective_fwd_kernel<E, true, true, false> : selective_fwd_kernel<E, true, false, false>)
+                     : (gate ? selective_fwd_kernel<E, false, true, false> : selective_fwd_kernel<E, false, false, false>);
+      }
+    } else {
+      kern = a.vec ? (gate ? selective_fwd_kernel<E, true, true, false> : selective_fwd_kernel<E, true, false, false>)
+                   : (gate ? selective_fwd_kernel<E, false, true, false> : selective_fwd_kernel<E, false, false, false>);
+    }
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, a);
     if (int rc = launch_check("selective_fwd_kernel")) return rc;
   }
@@ -972,7 +1253,8 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
                             const E* Bm, const E* Cm, const E* gate, const float* chunk_states,
                             const E* raw_out, E* du, E* ddt, float* dA, E* dB, E* dC, E* dgate,
                             int64_t batch, int64_t dim, int64_t length, int64_t dstate,
-                            hipStream_t stream, const char* what) {
+                            hipStream_t stream, const char* what,
+                            const MambaLayout* ml = nullptr) {
   clear_error();
   if (int rc = check_selective(batch, dim, length, dstate, what)) return rc;
   if (batch == 0 || dim == 0 || length == 0) {
@@ -1033,17 +1315,39 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
   // the staged fp32 sums sit at a 16-byte multiple only when n_bln and B*D*N are
   // multiples of 4; otherwise the rows go element by element
   const bool staged_aligned = !staged || (n_bln % 4 == 0 && (batch * n_dn) % 4 == 0);
-  a.vec = staged_aligned &&
-                  rows_vectorizable(length, sizeof(E), {grad_out, u, dt, gate, raw_out, du, ddt, dgate})
-              ? 1
-              : 0;
+  a.ld_bc = static_cast<int>(dstate);
+  if (ml != nullptr) {
+    a.ld_bc = static_cast<int>(ml->ld_bc);
+    a.ld_u = static_cast<int>(ml->ld_u);
+    a.ld_dt = static_cast<int>(ml->ld_dt);
+    a.ld_z = static_cast<int>(ml->ld_z);
+    a.dt_bias = ml->dt_bias;
+    a.vec = cols_vectorizable(dim, *ml, {grad_out, u, dt, gate, raw_out, du, ddt, dgate}) ? 1 : 0;
+  } else {
+    a.vec = staged_aligned &&
+                    rows_vectorizable(length, sizeof(E), {grad_out, u, dt, gate, raw_out, du, ddt, dgate})
+                ? 1
+                : 0;
+  }
   const dim3 grid(static_cast<unsigned>(n_dtiles), static_cast<unsigned>(batch));
   for (int p = 0; p < n_pass; ++p) {
     a.n_base = p * kPassStates;
     a.first = p == 0;
     a.last = p == n_pass - 1;
-    auto kern = a.vec ? (gate ? selective_bwd_kernel<E, true, true> : selective_bwd_kernel<E, true, false>)
-                      : (gate ? selective_bwd_kernel<E, false, true> : selective_bwd_kernel<E, false, false>);
+    using K = void (*)(BwdArgs<E>);
+    K kern;
+    if constexpr (std::is_same_v<E, float>) {
+      if (ml != nullptr) {
+        kern = a.vec ? (gate ? selective_bwd_kernel<E, true, true, true> : selective_bwd_kernel<E, true, false, true>)
+                     : (gate ? selective_bwd_kernel<E, false, true, true> : selective_bwd_kernel<E, false, false, true>);
+      } else {
+        kern = a.vec ? (gate ? selective_bwd_kernel<E, true, true, false> : selective_bwd_kernel<E, true, false, false>)
+                     : (gate ? selective_bwd_kernel<E, false, true, false> : selective_bwd_kernel<E, false, false, false>);
+      }
+    } else {
+      kern = a.vec ? (gate ? selective_bwd_kernel<E, true, true, false> : selective_bwd_kernel<E, true, false, false>)
+                   : (gate ? selective_bwd_kernel<E, false, true, false> : selective_bwd_kernel<E, false, false, false>);
+    }
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, a);
     if (int rc = launch_check("selective_bwd_kernel")) return rc;
   }
@@ -1082,6 +1386,50 @@ int ossm_selective_backward(const float* grad_out, const float* u, const float* 
   return selective_backward_impl<float>(grad_out, u, dt, A, Bm, Cm, gate, chunk_states, raw_out, du,
                                         ddt, dA, dB, dC, dgate, batch, dim, length, dstate,
                                         static_cast<hipStream_t>(stream), "selective_backward");
+}
+
+// Row strides of the [B, L, D] layout: at least D (and N for B and C).
+static int check_mamba_strides(int64_t D, int64_t N, int64_t ld_u, int64_t ld_dt, int64_t ld_z,
+                               bool gated, int64_t ld_bc, const char* what) {
+  if (ld_u < D || ld_dt < D || (gated && ld_z < D) || ld_bc < N || ld_u > INT_MAX ||
+      ld_dt > INT_MAX || ld_z > INT_MAX || ld_bc > INT_MAX)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT,
+                     std::string(what) + ": row strides must be at least the row length");
+  return OSSM_OK;
+}
+
+int ossm_selective_mamba_forward(const float* u, int64_t ld_u, const float* dt, int64_t ld_dt,
+                                 const float* dt_bias, const float* A, const float* Bm,
+                                 const float* Cm, int64_t ld_bc, const float* gate, int64_t ld_z,
+                                 float* out, float* raw_out, float* chunk_states, int64_t batch,
+                                 int64_t dim, int64_t length, int64_t dstate, ossm_stream_t stream) {
+  const char* what = "selective_mamba_forward";
+  clear_error();
+  if (dstate > 0)
+    if (int rc = check_mamba_strides(dim, dstate, ld_u, ld_dt, ld_z, gate != nullptr, ld_bc, what))
+      return rc;
+  const MambaLayout ml{ld_u, ld_dt, gate != nullptr ? ld_z : dim, ld_bc, dt_bias};
+  return selective_forward_impl<float>(u, dt, A, Bm, Cm, gate, out, raw_out, chunk_states, batch,
+                                       dim, length, dstate, static_cast<hipStream_t>(stream), what,
+                                       &ml);
+}
+
+int ossm_selective_mamba_backward(const float* grad_out, const float* u, int64_t ld_u,
+                                  const float* dt, int64_t ld_dt, const float* dt_bias,
+                                  const float* A, const float* Bm, const float* Cm, int64_t ld_bc,
+                                  const float* gate, int64_t ld_z, const float* chunk_states,
+                                  const float* raw_out, float* du, float* ddt, float* dA,
+                                  float* dB, float* dC, float* dgate, int64_t batch, int64_t dim,
+                                  int64_t length, int64_t dstate, ossm_stream_t stream) {
+  const char* what = "selective_mamba_backward";
+  clear_error();
+  if (dstate > 0)
+    if (int rc = check_mamba_strides(dim, dstate, ld_u, ld_dt, ld_z, gate != nullptr, ld_bc, what))
+      return rc;
+  const MambaLayout ml{ld_u, ld_dt, gate != nullptr ? ld_z : dim, ld_bc, dt_bias};
+  return selective_backward_impl<float>(grad_out, u, dt, A, Bm, Cm, gate, chunk_states, raw_out,
+                                        du, ddt, dA, dB, dC, dgate, batch, dim, length, dstate,
+                                        static_cast<hipStream_t>(stream), what, &ml);
 }
 
 int ossm_selective_forward_bf16(const void* u, const void* dt, const float* A, const void* Bm,

@@ -128,3 +128,32 @@ def diag_states(lam, b_seq):
         x = lam * x + b_seq[t]
         out.append(x)
     return torch.stack(out, 0)
+
+
+def mamba_mixer(inputs, params, d_conv: int, dt_rank: int, d_state: int):
+    """The Mamba mixer forward of mambarec.py:136-184 as plain torch ops in the
+    inputs' dtype: in_proj, causal depthwise conv + SiLU (torch's conv1d), x_proj,
+    softplus(dt_proj(.)), the selective scan as a per-step loop in the
+    reference's [B, C, L] layout (mambarec.py:23-61), the SiLU gate, out_proj.
+    ``params`` maps the reference module's parameter names to tensors."""
+    F = torch.nn.functional
+    xz = inputs @ params["in_proj.weight"].T
+    Di = xz.shape[-1] // 2
+    x, z = xz[..., :Di], xz[..., Di:]
+    xc = F.conv1d(F.pad(x.transpose(1, 2), (d_conv - 1, 0)), params["conv1d.weight"],
+                  params.get("conv1d.bias"), groups=Di)
+    xc = F.silu(xc)                                   # [B, D, L]
+    proj = xc.transpose(1, 2) @ params["x_proj.weight"].T
+    dt_raw = proj[..., :dt_rank]
+    Bg = proj[..., dt_rank:dt_rank + d_state]
+    Cg = proj[..., dt_rank + d_state:]
+    dt = F.softplus(dt_raw @ params["dt_proj.weight"].T + params["dt_proj.bias"]).transpose(1, 2)
+    A = -torch.exp(params["A_log"])
+    h = torch.zeros(xc.shape[0], Di, d_state, dtype=xc.dtype)
+    ys = []
+    for t in range(xc.shape[2]):
+        d = dt[:, :, t, None]
+        h = torch.exp(d * A) * h + (d * Bg[:, t, None, :]) * xc[:, :, t, None]
+        ys.append((h * Cg[:, t, None, :]).sum(-1))
+    y = torch.stack(ys, -1) * F.silu(z.transpose(1, 2))
+    return y.transpose(1, 2) @ params["out_proj.weight"].T
