@@ -18,7 +18,8 @@ One JSON line is printed.  Besides the contract fields:
                 WRITE_SIZE (profiles/dlinoss_imex1_config2_pmc.json) or null
   cpu_baseline  the reference's own CPU kernels (oracle/_ref, compiled from the
                 reference sources) on the same workload on this host's cores
-  detail        per-direction figures and the other BASELINE configs
+  detail        per-direction figures, the other BASELINE configs and the fused
+                layers (D-LinOSS layer, Mamba mixer)
 
 ``--calibrate-copy`` runs only a device-to-device copy of known size, for
 scaling the FETCH_SIZE / WRITE_SIZE counters.
@@ -40,6 +41,7 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 PEAK_HBM = 8.0e12  # MI355X HBM3E, bytes/s
+PEAK_MFMA_FP32 = 157.3e12  # MI355X dense fp32 matrix, flop/s
 METRIC = "scan state-steps/s (B·L·state) + % of HBM peak, fwd and fwd+bwd, 1 GPU"
 # algorithmic bytes per state-step (each required input read once, each output written once)
 DL_BYTES_FWD = 24  # read bu (8) + write states (16)
@@ -296,6 +298,44 @@ def _detail_configs(torch, K, dev, reps=10):
                                 "hbm_frac_fwd_bwd": (fb + bb) / ((tf + tb) / 1e3) / PEAK_HBM,
                                 "note": "bound by VALU as the fp32 case; bf16 halves the bytes only"}
     del u, dts, Bm, Cm, z, go, res
+    # Fused D-LinOSS layer forward at config 2's shape (H = P = 128): one kernel,
+    # MFMA-bound (8 H P flops per (b, t)); against the unfused layer's steps
+    from ossm_amd import layers as LY
+    L, B, H, P = 4096, 32, 128, 128
+    g = torch.Generator(device=dev).manual_seed(8)
+    args = (torch.randn(B, L, H, device=dev, generator=g),
+            (torch.rand(P, H, 2, device=dev, generator=g) * 2 - 1) / H ** 0.5,
+            (torch.rand(H, P, 2, device=dev, generator=g) * 2 - 1) / P ** 0.5,
+            torch.randn(H, device=dev, generator=g),
+            torch.rand(P, device=dev, generator=g) * 0.9 + 0.1,
+            torch.rand(P, device=dev, generator=g),
+            torch.sigmoid(torch.randn(P, device=dev, generator=g)))
+    tf = _ev_time(torch, lambda: LY.dlinoss_layer_forward("imex1", *args), reps, 3)
+    with torch.no_grad():
+        tu = _ev_time(torch, lambda: LY.unfused_layer_forward("imex1", *args), reps, 3)
+    flops = 8 * B * L * H * P
+    out["dlinoss_layer_fwd_c2_shape"] = {"fused_ms": tf, "unfused_ms": tu,
+                                         "TFLOPs": flops / (tf / 1e3) / 1e12,
+                                         "mfma_frac_fp32": flops / (tf / 1e3) / PEAK_MFMA_FP32}
+    del args
+    # Fused Mamba mixer (projections included) at C3's and C4's shapes, forward
+    # and forward + backward
+    from ossm_amd.mamba import MambaMixer
+    for key, (Bz, L, dm) in (("mamba_mixer_c3_shape", (256, 200, 64)),
+                             ("mamba_mixer_c4_shape", (16, 2048, 768))):
+        torch.manual_seed(9)
+        mixer = MambaMixer(dm, d_state=16, d_conv=4, expand=2).to(dev)
+        u = torch.randn(Bz, L, dm, device=dev, requires_grad=True)
+        gy = torch.randn(Bz, L, dm, device=dev)
+        with torch.no_grad():
+            tf = _ev_time(torch, lambda: mixer(u), reps, 3)
+
+        def step():
+            mixer(u).backward(gy)
+
+        tfb = _ev_time(torch, step, reps, 3)
+        out[key] = {"fwd_ms": tf, "fwd_bwd_ms": tfb, "d_inner": 2 * dm, "d_state": 16}
+        del mixer, u, gy
     torch.cuda.empty_cache()
     return out
 

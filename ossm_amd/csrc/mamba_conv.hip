@@ -12,10 +12,13 @@
 //   dbias[d] = sum_{b,t} dpre[b,t,d].
 //
 // Memory-bound elementwise work: a thread owns 4 channels (16-byte runs along
-// d, so a wave moves 1 KiB per step) and a span of steps, keeping the K-1
-// previous inputs in registers.  The weight and bias gradients are per-thread
-// partial sums over its span, written per (batch row, span) and added by a
-// second kernel in a fixed order in fp64 (deterministic).
+// d, so a wave moves 1 KiB per step) and a span of steps, loading all of the
+// span's inputs (and the K-1 before it) before the first is used.  Threads are
+// numbered channel group fastest, then span, then batch row, so narrow D still
+// fills whole waves.  The weight and bias gradients are per-thread partial
+// sums over its span, written per (batch row, span) and reduced over those
+// rows by the column-sum kernel shared with the scans (fp64 per row group,
+// row groups combined with float atomics).
 
 #include <hip/hip_runtime.h>
 
@@ -25,6 +28,7 @@
 
 #include "../../include/ossm_scan.h"
 #include "runtime.hpp"
+#include "scan_reduce.hpp"
 
 namespace ossm {
 namespace {
@@ -32,7 +36,7 @@ namespace {
 constexpr int kConvThreads = 256;
 constexpr int kFwdSpan = 16;   // steps per thread, forward
 constexpr int kBwdTile = 8;    // steps per register tile, backward
-constexpr int kBwdSpan = 128;  // steps per thread, backward (kBwdSpan / kBwdTile tiles)
+constexpr int kBwdSpan = 32;   // steps per thread, backward (kBwdSpan / kBwdTile tiles)
 constexpr int kMaxK = 8;
 
 struct ConvArgs {
@@ -42,8 +46,25 @@ struct ConvArgs {
   const float* dout;  // backward: [B, L, D] dense
   float* out;         // forward: [B, L, D] dense; backward: dx [B, L, D] dense
   float* partials;    // backward: [B * n_spans][K + 1][D]
+  float* grad_w;      // backward: zeroed by the first workgroup (the column sums add into it)
+  float* grad_bias;
   int B, L, D, ld_x;
+  int n_spans;
 };
+
+// The thread's (batch row, span, first channel) in the flat numbering; false
+// past the end.
+template <int C>
+__device__ __forceinline__ bool conv_pos(const ConvArgs& a, int& b, int& span, int& d) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kConvThreads + threadIdx.x;
+  const int Q = a.D / C;
+  const int64_t rest = gid / Q;
+  if (rest >= static_cast<int64_t>(a.B) * a.n_spans) return false;
+  d = static_cast<int>(gid - rest * Q) * C;
+  span = static_cast<int>(rest % a.n_spans);
+  b = static_cast<int>(rest / a.n_spans);
+  return true;
+}
 
 __device__ __forceinline__ float sigm(float p) { return 1.f / (1.f + __expf(-p)); }
 
@@ -100,12 +121,12 @@ __device__ __forceinline__ void load_weights(const ConvArgs& a, int d, float (&w
   }
 }
 
-// grid (channel groups, spans of kFwdSpan steps, batch)
+// one thread per (batch row, span of kFwdSpan steps, C channels)
 template <int K, int C>
 __global__ __launch_bounds__(kConvThreads) void conv_silu_fwd_kernel(ConvArgs a) {
-  const int d = (blockIdx.x * kConvThreads + threadIdx.x) * C;
-  if (d >= a.D) return;  // no barriers below
-  const int b = blockIdx.z, t0 = blockIdx.y * kFwdSpan;
+  int b, span, d;
+  if (!conv_pos<C>(a, b, span, d)) return;  // no barriers below
+  const int t0 = span * kFwdSpan;
   const size_t xb = static_cast<size_t>(b) * a.L * a.ld_x;
   const size_t ob = static_cast<size_t>(b) * a.L * a.D;
   float w[K][C], bias[C];
@@ -130,12 +151,16 @@ __global__ __launch_bounds__(kConvThreads) void conv_silu_fwd_kernel(ConvArgs a)
   }
 }
 
-// grid (channel groups, spans of kBwdSpan steps, batch)
+// one thread per (batch row, span of kBwdSpan steps, C channels)
 template <int K, int C>
 __global__ __launch_bounds__(kConvThreads) void conv_silu_bwd_kernel(ConvArgs a) {
-  const int d = (blockIdx.x * kConvThreads + threadIdx.x) * C;
-  if (d >= a.D) return;  // no barriers below
-  const int b = blockIdx.z, span = blockIdx.y;
+  if (blockIdx.x == 0) {  // the column sums that follow add into zeroed outputs
+    for (int i = threadIdx.x; i < a.D * K; i += kConvThreads) a.grad_w[i] = 0.f;
+    if (a.grad_bias != nullptr)
+      for (int i = threadIdx.x; i < a.D; i += kConvThreads) a.grad_bias[i] = 0.f;
+  }
+  int b, span, d;
+  if (!conv_pos<C>(a, b, span, d)) return;  // no barriers below
   const size_t xb = static_cast<size_t>(b) * a.L * a.ld_x;
   const size_t ob = static_cast<size_t>(b) * a.L * a.D;
   float w[K][C], bias[C];
@@ -185,8 +210,7 @@ __global__ __launch_bounds__(kConvThreads) void conv_silu_bwd_kernel(ConvArgs a)
     }
   }
   // partials row (b, span): [K + 1][D]
-  const int n_spans = gridDim.y;
-  float* prow = a.partials + (static_cast<size_t>(b) * n_spans + span) * (K + 1) * a.D;
+  float* prow = a.partials + (static_cast<size_t>(b) * a.n_spans + span) * (K + 1) * a.D;
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     Vec<C> v;
@@ -200,22 +224,17 @@ __global__ __launch_bounds__(kConvThreads) void conv_silu_bwd_kernel(ConvArgs a)
   store_vec<C>(prow + static_cast<size_t>(K) * a.D + d, v);
 }
 
-// grad_w[d, k] (j < K) and grad_bias[d] (j = K): the R partial rows added in
-// row order in fp64.  One thread per (j, d).
-__global__ void conv_param_sum_kernel(const float* __restrict__ partials, int R, int KP1, int D,
-                                      float* __restrict__ grad_w, float* __restrict__ grad_bias) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= static_cast<int64_t>(KP1) * D) return;
-  const int j = static_cast<int>(i / D), d = static_cast<int>(i - static_cast<int64_t>(j) * D);
-  const size_t stride = static_cast<size_t>(KP1) * D;
-  double s = 0.0;
-  for (int r = 0; r < R; ++r) s += static_cast<double>(partials[r * stride + i]);
-  if (j < KP1 - 1) {
-    grad_w[static_cast<size_t>(d) * (KP1 - 1) + j] = static_cast<float>(s);
-  } else if (grad_bias != nullptr) {
-    grad_bias[d] = static_cast<float>(s);
+// Column-sum epilogue: S[k] for k < K is grad_w[d, k], S[K] grad_bias[d].
+template <int K>
+struct ConvEpilogue {
+  float* grad_w;
+  float* grad_bias;
+  __device__ void add(int d, const double* S) const {
+#pragma unroll
+    for (int k = 0; k < K; ++k) atomic_put(grad_w + static_cast<size_t>(d) * K + k, S[k]);
+    if (grad_bias != nullptr) atomic_put(grad_bias + d, S[K]);
   }
-}
+};
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -227,17 +246,19 @@ int check_conv(int64_t B, int64_t L, int64_t D, int64_t K, int64_t ld_x, const c
                                                std::to_string(kMaxK) + " supported, got " +
                                                std::to_string(K));
   if (ld_x < D) return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": ld_x < D");
-  if (B > 65535 || L > int64_t(65535) * kFwdSpan || D > INT_MAX / 8 || ld_x > INT_MAX)
+  if (B > 65535 || L > INT_MAX / 2 || D > INT_MAX / 8 || ld_x > INT_MAX || B * L * D > (int64_t(1) << 40))
     return set_error(OSSM_ERR_UNSUPPORTED, std::string(what) + ": size exceeds launch limits");
   return OSSM_OK;
 }
 
+dim3 flat_grid(const ConvArgs& a, int C) {
+  const int64_t threads = static_cast<int64_t>(a.B) * a.n_spans * (a.D / C);
+  return dim3(static_cast<unsigned>((threads + kConvThreads - 1) / kConvThreads));
+}
+
 template <int K>
 int launch_fwd(const ConvArgs& a, bool vec, hipStream_t stream) {
-  const int C = vec ? 4 : 1;
-  const int64_t groups = (a.D / C + kConvThreads - 1) / kConvThreads;
-  const dim3 grid(static_cast<unsigned>(groups), static_cast<unsigned>((a.L + kFwdSpan - 1) / kFwdSpan),
-                  static_cast<unsigned>(a.B));
+  const dim3 grid = flat_grid(a, vec ? 4 : 1);
   if (vec)
     hipLaunchKernelGGL((conv_silu_fwd_kernel<K, 4>), grid, dim3(kConvThreads), 0, stream, a);
   else
@@ -246,16 +267,16 @@ int launch_fwd(const ConvArgs& a, bool vec, hipStream_t stream) {
 }
 
 template <int K>
-int launch_bwd(const ConvArgs& a, bool vec, int n_spans, hipStream_t stream) {
-  const int C = vec ? 4 : 1;
-  const int64_t groups = (a.D / C + kConvThreads - 1) / kConvThreads;
-  const dim3 grid(static_cast<unsigned>(groups), static_cast<unsigned>(n_spans),
-                  static_cast<unsigned>(a.B));
+int launch_bwd(const ConvArgs& a, bool vec, hipStream_t stream) {
+  const dim3 grid = flat_grid(a, vec ? 4 : 1);
   if (vec)
     hipLaunchKernelGGL((conv_silu_bwd_kernel<K, 4>), grid, dim3(kConvThreads), 0, stream, a);
   else
     hipLaunchKernelGGL((conv_silu_bwd_kernel<K, 1>), grid, dim3(kConvThreads), 0, stream, a);
-  return launch_check("conv_silu_bwd_kernel");
+  if (int rc = launch_check("conv_silu_bwd_kernel")) return rc;
+  return launch_column_sums<K + 1>(static_cast<const float*>(a.partials), a.D, 1,
+                                   static_cast<int64_t>(a.B) * a.n_spans,
+                                   ConvEpilogue<K>{a.grad_w, a.grad_bias}, stream);
 }
 
 template <template <int> class F, class... Args>
@@ -278,7 +299,7 @@ struct FwdLaunch {
 };
 template <int K>
 struct BwdLaunch {
-  static int run(const ConvArgs& a, bool vec, int n, hipStream_t s) { return launch_bwd<K>(a, vec, n, s); }
+  static int run(const ConvArgs& a, bool vec, hipStream_t s) { return launch_bwd<K>(a, vec, s); }
 };
 
 __global__ void conv_zero_kernel(float* __restrict__ p, int64_t n) {
@@ -308,8 +329,9 @@ int ossm_mamba_conv_forward(const float* x, int64_t ld_x, const float* weight, c
   if (batch == 0 || length == 0 || dim == 0) return OSSM_OK;
   if (!x || !weight || !out)
     return set_error(OSSM_ERR_INVALID_ARGUMENT, "mamba_conv_forward: null pointer");
-  ConvArgs a{x, weight, bias, nullptr, out, nullptr, static_cast<int>(batch),
-             static_cast<int>(length), static_cast<int>(dim), static_cast<int>(ld_x)};
+  ConvArgs a{x, weight, bias, nullptr, out, nullptr, nullptr, nullptr, static_cast<int>(batch),
+             static_cast<int>(length), static_cast<int>(dim), static_cast<int>(ld_x),
+             static_cast<int>((length + kFwdSpan - 1) / kFwdSpan)};
   const bool vec = dim % 4 == 0 && ld_x % 4 == 0 && aligned16(x) && aligned16(out);
   return by_width<FwdLaunch>(static_cast<int>(width), a, vec, static_cast<hipStream_t>(stream_v));
 }
@@ -334,16 +356,12 @@ int ossm_mamba_conv_backward(const float* x, int64_t ld_x, const float* weight, 
   void* ws = nullptr;
   if (int rc = acquire_workspace(stream, static_cast<size_t>(R * (width + 1) * dim) * sizeof(float), &ws))
     return rc;
-  ConvArgs a{x, weight, bias, grad_out, grad_x, static_cast<float*>(ws), static_cast<int>(batch),
-             static_cast<int>(length), static_cast<int>(dim), static_cast<int>(ld_x)};
+  ConvArgs a{x, weight, bias, grad_out, grad_x, static_cast<float*>(ws), grad_weight, grad_bias,
+             static_cast<int>(batch), static_cast<int>(length), static_cast<int>(dim),
+             static_cast<int>(ld_x), n_spans};
   const bool vec = dim % 4 == 0 && ld_x % 4 == 0 && aligned16(x) && aligned16(grad_out) &&
                    aligned16(grad_x) && aligned16(ws);
-  if (int rc = by_width<BwdLaunch>(static_cast<int>(width), a, vec, n_spans, stream)) return rc;
-  const int64_t n = (width + 1) * dim;
-  hipLaunchKernelGGL(conv_param_sum_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
-                     stream, static_cast<const float*>(ws), static_cast<int>(R),
-                     static_cast<int>(width + 1), static_cast<int>(dim), grad_weight, grad_bias);
-  return launch_check("conv_param_sum_kernel");
+  return by_width<BwdLaunch>(static_cast<int>(width), a, vec, stream);
 }
 
 }  // extern "C"

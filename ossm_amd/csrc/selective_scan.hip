@@ -335,8 +335,25 @@ __device__ __forceinline__ void store_cols(float* __restrict__ s, const RowRegs<
 }
 
 // softplus(x) = log(1 + e^x), and x itself above 20 (torch's default threshold,
-// F.softplus as mambarec.py:155 applies it).
-__device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+// F.softplus as mambarec.py:155 applies it), as max(x, 0) + log1p(e) with
+// e = e^-|x| <= 1: below e = 1/64 by the series e - e^2/2 + e^3/3 - e^4/4
+// (truncation < e^5/5, 2e-10 relative), above it by the hardware log of 1 + e
+// (rounding of 1 + e costs < 2^-24 / e relative, < 4e-6).
+__device__ __forceinline__ float softplus(float x) {
+  if (x > 20.f) return x;
+  const float e = fast_exp2(-fabsf(x) * kLog2e);
+  const float l = e < 0.015625f ? e * (1.f - e * (0.5f - e * (1.f / 3.f - 0.25f * e)))
+                                : __builtin_amdgcn_logf(1.f + e) * 0.69314718055994531f;
+  return fmaxf(x, 0.f) + l;
+}
+
+// d softplus(x) / dx = sigmoid(x) = 1 - e^-s with s = softplus(x) >= 0: below
+// s = 1/64 by the series s - s^2/2 + s^3/6 - s^4/24 (no cancellation), above
+// it as 1 - e^-s.
+__device__ __forceinline__ float sigmoid_of_softplus(float s) {
+  return s < 0.015625f ? s * (1.f - s * (0.5f - s * (1.f / 6.f - s * (1.f / 24.f))))
+                       : 1.f - fast_exp2(-s * kLog2e);
+}
 
 // dt = softplus(dt_pre + bias[d]) staged like store_cols (bias may be null).
 template <int TT, int RS>
@@ -532,6 +549,9 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   __shared__ float s_dt[kWave * RS];
   __shared__ __align__(16) float s_B[TT * kPassStates];
   __shared__ __align__(16) float s_C[TT * kPassStates];
+  // BLD: the tile's y, [step][channel], stored to HBM as rows of channels
+  constexpr int YS = kWave + 4;  // row stride (floats): 16-byte rows, banks staggered
+  __shared__ __align__(16) float s_y[BLD ? TT * YS : 1];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
@@ -569,7 +589,7 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   FwdTile nxt;
   float zn[kSeg];  // the gate of the lane's output segment, one tile ahead
   fwd_prefetch<E, VEC, BLD>(nxt, a, row0, bc0, d0, 0);
-  if constexpr (GATED) load_gate(zn, kSeg * g);
+  if constexpr (GATED && !BLD) load_gate(zn, kSeg * g);
   for (int t0 = 0; t0 < a.L; t0 += TT) {
     __syncthreads();  // the previous tile's LDS readers are done
     if constexpr (BLD) {
@@ -587,8 +607,11 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     __syncthreads();
     if (t0 + TT < a.L) {
       fwd_prefetch<E, VEC, BLD>(nxt, a, row0, bc0, d0, t0 + TT);
-      if constexpr (GATED) load_gate(zn, t0 + TT + kSeg * g);
+      if constexpr (GATED && !BLD) load_gate(zn, t0 + TT + kSeg * g);
     }
+    // BLD: this tile's gate, for the row stores after the step loop
+    RowRegs<TT> zq;
+    if constexpr (GATED && BLD) load_cols<TT, VEC>(zq, a.z, row0 * a.ld_z, a.ld_z, d0, a.D, t0, a.L);
 
     // Every tile runs all TT steps: past L the staged dt, u, B and C are zero,
     // so h stays at the last step's state and y is zero there; the checkpoint
@@ -656,7 +679,49 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     // y over the state groups (within the wave), then this lane's 8 outputs
     float y[kSeg];
     reduce_groups(yv, y);
-    if (dvalid) {
+    if constexpr (BLD) {
+      // through LDS, so that rows of 64 channels leave as 16-byte runs
+#pragma unroll
+      for (int k = 0; k < kSeg; ++k) s_y[(kSeg * g + k) * YS + r] = y[k];
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+        int step, c4;
+        tile_pos_bld<TT>(k, step, c4);
+        const int t = t0 + step, dd = d0 + c4;
+        if (t >= a.L || dd >= a.D) continue;
+        const int ne = min(4, a.D - dd);
+        const float4 v4 = *reinterpret_cast<const float4*>(s_y + step * YS + c4);
+        float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        const size_t gi = (row0 + t) * a.D + dd;
+        if (!a.first) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (e < ne) v[e] += a.acc[gi + e];
+        }
+        auto put = [&](auto* dst) {
+          if constexpr (VEC) {
+            Elem<std::remove_pointer_t<decltype(dst)>>::store4(dst + gi, make_float4(v[0], v[1], v[2], v[3]));
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (e < ne) Elem<std::remove_pointer_t<decltype(dst)>>::store1(dst + gi + e, v[e]);
+          }
+        };
+        if (a.last) {
+          if (a.raw != nullptr) put(a.raw);
+          if constexpr (GATED) {
+            const float4 zz = zq.v[k];
+            const float zv[4] = {zz.x, zz.y, zz.z, zz.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] *= zv[e] * sigmoid(zv[e]);
+          }
+          put(a.out);
+        } else {
+          put(a.acc);
+        }
+      }
+    } else if (dvalid) {
       const int t = t0 + kSeg * g;
       if (!a.first) {
         float prev[kSeg];
@@ -989,7 +1054,7 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
     // finish du / ddt over the waves (states), accumulate over passes
     if constexpr (BLD) {
       // 4 channels at one step per thread; ddt is taken through the softplus:
-      // d softplus(x) / dx = sigmoid(x) = 1 - e^{-softplus(x)} (staged in s_dt)
+      // d softplus(x) / dx = sigmoid(x), from softplus(x) staged in s_dt
 #pragma unroll
       for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
         int step, c4;
@@ -1005,7 +1070,7 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
           }
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sd[e] *= -expm1f(-s_dt[(c4 + e) * RS + step]);
+        for (int e = 0; e < 4; ++e) sd[e] *= sigmoid_of_softplus(s_dt[(c4 + e) * RS + step]);
         const size_t gi = (row0 + t) * a.D + dd;
         const int ne = min(4, a.D - dd);
         if (!a.first) {
