@@ -42,7 +42,7 @@ enum {
 
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
-/* Library ABI version (bumped on any change of the entry points; currently 7). */
+/* Library ABI version (bumped on any change of the entry points; currently 8). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -231,13 +231,35 @@ int ossm_diag_scan_backward_f64(const double* lambda_real, const double* lambda_
  * [batch, length, hidden] fp32 row-major; B [ssm, hidden, 2] and C
  * [hidden, ssm, 2] (real, imaginary parts last, the layer's parameter layout);
  * D [hidden]; a_diag, g_diag, step [ssm] as returned by _project_parameters
- * (dlinoss.py:249-264).  bu and the states stay on chip.  hidden and ssm up to
- * 256 (OSSM_ERR_UNSUPPORTED beyond).
+ * (dlinoss.py:249-264).  bu and the states stay on chip.  carries (may be
+ * null): [batch, ceil(length / 32), ssm] complex 2-vectors (4 floats), the
+ * state entering each 32-step chunk, for ossm_dlinoss_layer_backward.  hidden
+ * and ssm up to 256 (OSSM_ERR_UNSUPPORTED beyond).
  */
 int ossm_dlinoss_layer_forward(int variant, const float* inputs, const float* B, const float* C,
                                const float* D, const float* a_diag, const float* g_diag,
-                               const float* step, float* outputs, int64_t batch, int64_t length,
-                               int64_t hidden, int64_t ssm, ossm_stream_t stream);
+                               const float* step, float* outputs, void* carries, int64_t batch,
+                               int64_t length, int64_t hidden, int64_t ssm, ossm_stream_t stream);
+
+/*
+ * Backward of ossm_dlinoss_layer_forward (the reference differentiates
+ * dlinoss.py:210-247 with autograd around dlinoss_<v>_backward): from the
+ * inputs, grad_output [batch, length, hidden] and the forward's carries,
+ * writes grad_inputs [batch, length, hidden], grad_a / grad_g / grad_step
+ * [ssm], and the two factors of the weight gradients, grad_bu and x_conj
+ * [batch, length, ssm] complex (grad of bu; x with its imaginary part
+ * negated): grad_B[p, h, c] = sum_{b,t} grad_bu[b,t,p].c u[b,t,h] and
+ * grad_C[h, p, c] = sum_{b,t} grad_output[b,t,h] x_conj[b,t,p].c, plain GEMMs
+ * the caller runs; grad_D = sum grad_output * inputs.  OSSM_ERR_UNSUPPORTED
+ * when hidden and ssm need more LDS than one workgroup has (e.g. both 256).
+ */
+int ossm_dlinoss_layer_backward(int variant, const float* inputs, const float* grad_output,
+                                const float* B, const float* C, const float* D,
+                                const float* a_diag, const float* g_diag, const float* step,
+                                const void* carries, float* grad_inputs, void* grad_bu,
+                                void* x_conj, float* grad_a, float* grad_g, float* grad_step,
+                                int64_t batch, int64_t length, int64_t hidden, int64_t ssm,
+                                ossm_stream_t stream);
 
 /*
  * Selective scan in the Mamba mixer's layout (mambarec.py:136-184 feeds the

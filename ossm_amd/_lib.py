@@ -67,8 +67,12 @@ _SIGNATURES = {
         ctypes.c_int, [_fp, _fp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
     "ossm_dlinoss_layer_forward": (
         ctypes.c_int,
-        [ctypes.c_int, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _c_int64, _c_int64, _c_int64,
+        [ctypes.c_int, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _vp, _c_int64, _c_int64, _c_int64,
          _c_int64, _vp]),
+    "ossm_dlinoss_layer_backward": (
+        ctypes.c_int,
+        [ctypes.c_int, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _vp, _fp, _vp, _vp, _fp, _fp, _fp,
+         _c_int64, _c_int64, _c_int64, _c_int64, _vp]),
     "ossm_selective_mamba_forward": (
         ctypes.c_int,
         [_fp, _c_int64, _fp, _c_int64, _fp, _fp, _fp, _fp, _c_int64, _fp, _c_int64, _fp, _fp, _fp,

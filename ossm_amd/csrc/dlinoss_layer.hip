@@ -65,6 +65,8 @@ __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
 
 __device__ __forceinline__ int round32(int n) { return (n + 31) & ~31; }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 struct LayerArgs {
   const float* u;   // [B, L, H]
   const float* Bw;  // [P, H, 2]
@@ -74,6 +76,7 @@ struct LayerArgs {
   const float* g;
   const float* dt;
   float* y;         // [B, L, H]
+  float4* carries;  // [B, n_chunks, P]: state entering each chunk (for the backward); may be null
   int Bsz, L, H, P, n_chunks;
 };
 
@@ -255,6 +258,7 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_fwd_kernel(
         if (c + 1 < A.n_chunks) rec_publish(rec, c, kRecInc, nc, ch, f4add(mat_apply(MC, s), e), sync.tag);
       }
     }
+    if (A.carries != nullptr) A.carries[(static_cast<size_t>(b) * A.n_chunks + c) * A.P + p] = s;
     float2* x_col = reinterpret_cast<float2*>(sX) + p;
 #pragma unroll
     for (int t = 0; t < kLc; ++t) {
@@ -306,12 +310,393 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_fwd_kernel(
   }
 }
 
+// ============================================================================
+// Backward.  For y = Re(x C^T) + D u with x the states driven by bu = u B^T:
+//   g_x   = gy (C_re - i C_im)                          (complex gradient of x)
+//   mu_t  = M^T mu_{t+1} + (0, g_x,t),  grad_bu_t = f^T mu_t   (the scan adjoint)
+//   grad_u = Re(grad_bu) B_re + Im(grad_bu) B_im + D gy
+//   sums of <mu, s_{t-1}>, <mu, bu> -> grad a, g, dt  (the scan's chain rule)
+// One workgroup per (batch row, 32-step chunk), chunks in reverse time order:
+//   1. gy rows -> LDS; g_x on the matrix cores (K = H) -> LDS (re, im pairs);
+//   2. u rows -> LDS (over gy); bu on the matrix cores -> LDS;
+//   3. one lane per oscillator re-runs the forward over the chunk from the
+//      carry the forward saved, keeping the 32 states s_{t-1} in registers and
+//      writing x (re, -im) for the weight gradient of C; the adjoint runs from
+//      zero over the chunk, its aggregate goes through the look-back (reverse,
+//      transition (M^T)^32), then it re-runs from the carry: grad_bu over g_x
+//      in LDS, the parameter sums per lane (partials for the column sums);
+//   4. grad_u on the matrix cores (K = the oscillators, the components as k
+//      slots, as the forward's out-projection) plus D gy; grad_bu rows stored.
+// grad_B = grad_bu^T u and grad_C = gy^T x' are sums over all (b, t): plain
+// GEMMs over the stored grad_bu and x' (the caller runs them).
+// ============================================================================
+struct LayerBwdArgs {
+  const float* u;        // [B, L, H]
+  const float* gy;       // [B, L, H]
+  const float* Bw;       // [P, H, 2]
+  const float* Cw;       // [H, P, 2]
+  const float* Dw;       // [H]
+  const float* a;
+  const float* g;
+  const float* dt;
+  const float4* carries; // [B, n_chunks, P] from the forward
+  float* grad_u;         // [B, L, H]
+  float2* grad_bu;       // [B, L, P] (re, im)
+  float2* xq;            // [B, L, P] (x.re, -x.im)
+  float* partials;       // [n_chunks][NS][B * P]
+  ZeroFill zero;         // grad a, g, dt, cleared by the first workgroup
+  int Bsz, L, H, P, n_chunks;
+};
+
+// Weights of the g_x projection for output h and oscillator p: (C_re, C_im)[h, p].
+template <bool VEC>
+__device__ __forceinline__ void load_cw_pair(const LayerBwdArgs& A, int h0, int p, float4 (&w)[2]) {
+  // h = h0 .. h0 + 3 for one oscillator: (re h0, im h0, re h0+1, im h0+1), (.. h0+2, h0+3)
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int h = h0 + j;
+    const bool ok = p < A.P && h < A.H;
+    if (VEC && ok) {
+      const float2 c = *reinterpret_cast<const float2*>(A.Cw + (static_cast<size_t>(h) * A.P + p) * 2);
+      v[2 * j] = c.x;
+      v[2 * j + 1] = c.y;
+    } else {
+      v[2 * j] = ok ? A.Cw[(static_cast<size_t>(h) * A.P + p) * 2] : 0.f;
+      v[2 * j + 1] = ok ? A.Cw[(static_cast<size_t>(h) * A.P + p) * 2 + 1] : 0.f;
+    }
+  }
+  w[0] = make_float4(v[0], v[1], v[2], v[3]);
+  w[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+template <bool VEC>
+__device__ __forceinline__ void load_bw_b(const LayerBwdArgs& A, int p, int h0, float4 (&w)[2]) {
+  LayerArgs la{};
+  la.Bw = A.Bw;
+  la.H = A.H;
+  la.P = A.P;
+  load_bw<VEC>(la, p, h0, w);
+}
+
+// (B_re, B_im)[p0, h], (B_re, B_im)[p0 + 1, h], zero outside.
+__device__ __forceinline__ float4 load_bw_pair(const LayerBwdArgs& A, int h, int p0) {
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int pj = p0 + j;
+    const bool ok = pj < A.P && h < A.H;
+    if (ok) {
+      const float2 b = *reinterpret_cast<const float2*>(A.Bw + (static_cast<size_t>(pj) * A.H + h) * 2);
+      v[2 * j] = b.x;
+      v[2 * j + 1] = b.y;
+    } else {
+      v[2 * j] = v[2 * j + 1] = 0.f;
+    }
+  }
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Rows t0 .. t0 + nt - 1 of a [B, L, H] tensor -> LDS [kLc][HS], zero-padded.
+template <bool VEC>
+__device__ __forceinline__ void stage_rows(float* __restrict__ dst, const float* __restrict__ src,
+                                           size_t row0, int nt, int H, int Hp, int HS) {
+  const int q4 = Hp / 4;
+  for (int e = threadIdx.x; e < kLc * q4; e += kLayerThreads) {
+    const int t = e / q4, h = (e - t * q4) * 4;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < nt) {
+      const float* p = src + row0 + static_cast<size_t>(t) * H + h;
+      if (VEC) {
+        if (h < H) v = *reinterpret_cast<const float4*>(p);
+      } else {
+        v.x = h < H ? p[0] : 0.f;
+        v.y = h + 1 < H ? p[1] : 0.f;
+        v.z = h + 2 < H ? p[2] : 0.f;
+        v.w = h + 3 < H ? p[3] : 0.f;
+      }
+    }
+    *reinterpret_cast<float4*>(dst + t * HS + h) = v;
+  }
+}
+
+template <int V, bool VEC>
+__global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
+    LayerBwdArgs A, unsigned long long* __restrict__ rec, LaunchSync sync) {
+  using Model = Dlinoss<V>;
+  constexpr int NS = Model::kSums;
+  extern __shared__ __align__(16) float smem[];
+  __shared__ int s_ticket;
+
+  const int Hp = round32(A.H), Pp = round32(A.P);
+  const int HS = Hp + 4, XS = 2 * Pp + 4;
+  float* sA = smem;                   // [kLc][HS]   gy rows, then u rows
+  float* sX = sA + kLc * HS;          // [kLc][Pp][2] bu
+  float* sG = sX + kLc * XS;          // [kLc][Pp][2] g_x, then grad_bu
+  float4* s_agg = reinterpret_cast<float4*>(sG + kLc * XS);  // [P]
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = wave_id();
+  const int ticket = launch_order(sync, A.Bsz * A.n_chunks, &s_ticket);
+  if (ticket < 0) return;
+  if (ticket == 0) zero_fill_block(A.zero);
+  const int cr = ticket / A.Bsz;     // chunks in reverse time order
+  const int c = A.n_chunks - 1 - cr;
+  const int b = ticket - cr * A.Bsz;
+  const int t0 = c * kLc;
+  const int nt = min(kLc, A.L - t0);
+  const size_t row0 = (static_cast<size_t>(b) * A.L + t0) * A.H;
+  const size_t prow0 = (static_cast<size_t>(b) * A.L + t0) * A.P;  // grad_bu / xq rows
+  const int half = lane >> 5, m = lane & 31;
+  const int hh = Hp / 2, ng1 = hh / 4;
+
+  // 1. gy -> LDS; g_x = gy (C_re - i C_im) on the matrix cores -> sG
+  stage_rows<VEC>(sA, A.gy, row0, nt, A.H, Hp, HS);
+  __syncthreads();
+  {
+    const float* arow = sA + m * HS + half * hh;
+    for (int pg = w; pg < Pp / 32; pg += kLayerWaves) {
+      const int p = pg * 32 + m;
+      floatx16 acc_re, acc_im;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc_re[r] = acc_im[r] = 0.f;
+      float4 wb[kAhead][2];
+#pragma unroll
+      for (int j = 0; j < kAhead; ++j) load_cw_pair<VEC>(A, half * hh + 4 * j, p, wb[j]);
+      for (int q0 = 0; q0 < ng1; q0 += kAhead) {
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) {
+          const int q = q0 + j;
+          if (q >= ng1) break;
+          const float4 av = *reinterpret_cast<const float4*>(arow + 4 * q);
+          const float4 w0 = wb[j][0], w1 = wb[j][1];
+          if (q + kAhead < ng1) load_cw_pair<VEC>(A, half * hh + 4 * (q + kAhead), p, wb[j]);
+          acc_re = mfma32(av.x, w0.x, acc_re);
+          acc_im = mfma32(av.x, w0.y, acc_im);
+          acc_re = mfma32(av.y, w0.z, acc_re);
+          acc_im = mfma32(av.y, w0.w, acc_im);
+          acc_re = mfma32(av.z, w1.x, acc_re);
+          acc_im = mfma32(av.z, w1.y, acc_im);
+          acc_re = mfma32(av.w, w1.z, acc_re);
+          acc_im = mfma32(av.w, w1.w, acc_im);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = acc_row(r, lane);
+        *reinterpret_cast<float2*>(sG + t * XS + 2 * p) = make_float2(acc_re[r], -acc_im[r]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // 2. u -> LDS (over gy); bu on the matrix cores -> sX
+  stage_rows<VEC>(sA, A.u, row0, nt, A.H, Hp, HS);
+  __syncthreads();
+  {
+    const float* arow = sA + m * HS + half * hh;
+    for (int pg = w; pg < Pp / 32; pg += kLayerWaves) {
+      const int p = pg * 32 + m;
+      floatx16 acc_re, acc_im;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc_re[r] = acc_im[r] = 0.f;
+      float4 wb[kAhead][2];
+#pragma unroll
+      for (int j = 0; j < kAhead; ++j) load_bw_b<VEC>(A, p, half * hh + 4 * j, wb[j]);
+      for (int q0 = 0; q0 < ng1; q0 += kAhead) {
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) {
+          const int q = q0 + j;
+          if (q >= ng1) break;
+          const float4 av = *reinterpret_cast<const float4*>(arow + 4 * q);
+          const float4 w0 = wb[j][0], w1 = wb[j][1];
+          if (q + kAhead < ng1) load_bw_b<VEC>(A, p, half * hh + 4 * (q + kAhead), wb[j]);
+          acc_re = mfma32(av.x, w0.x, acc_re);
+          acc_im = mfma32(av.x, w0.y, acc_im);
+          acc_re = mfma32(av.y, w0.z, acc_re);
+          acc_im = mfma32(av.y, w0.w, acc_im);
+          acc_re = mfma32(av.z, w1.x, acc_re);
+          acc_im = mfma32(av.z, w1.y, acc_im);
+          acc_re = mfma32(av.w, w1.z, acc_re);
+          acc_im = mfma32(av.w, w1.w, acc_im);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = acc_row(r, lane);
+        *reinterpret_cast<float2*>(sX + t * XS + 2 * p) = make_float2(acc_re[r], acc_im[r]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // 3. states, adjoint, grad_bu, parameter sums: one thread per oscillator
+  const int p = threadIdx.x;
+  const bool osc = p < A.P;
+  const int nc = A.Bsz * A.P;
+  const int ch = b * A.P + p;
+  const bool scan = A.n_chunks > 1;
+  const float2* bu_col = reinterpret_cast<const float2*>(sX) + p;
+  float2* g_col = reinterpret_cast<float2*>(sG) + p;
+  const int xs2 = XS / 2;
+  typename Model::Coef k{};
+  float4 sp[kLc];  // state before step t of the chunk
+  float4 e = f4zero();
+  if (osc) {
+    k = Model::coef_of({A.a[p], A.g[p], A.dt[p]});
+    float4 s = A.carries[(static_cast<size_t>(b) * A.n_chunks + c) * A.P + p];
+#pragma unroll
+    for (int t = 0; t < kLc; ++t) {
+      sp[t] = s;
+      s = Model::step(k, s, bu_col[t * xs2]);
+      if (t < nt) A.xq[prow0 + static_cast<size_t>(t) * A.P + p] = make_float2(s.z, -s.w);
+    }
+    // adjoint from zero over the chunk (rows past L carry zero gradients)
+#pragma unroll
+    for (int t = kLc - 1; t >= 0; --t) e = Model::rev_carry(k, Model::mu(e, g_col[t * xs2]));
+    s_agg[p] = e;
+  }
+  const bool split_pub = A.P <= 2 * kWave;
+  if (scan && c < A.n_chunks - 1) {
+    if (split_pub) {
+      __syncthreads();
+      const int q = threadIdx.x - 2 * kWave;
+      if (q >= 0 && q < A.P) rec_publish(rec, c, kRecAgg, nc, b * A.P + q, s_agg[q], sync.tag);
+    } else if (osc) {
+      rec_publish(rec, c, kRecAgg, nc, ch, e, sync.tag);
+    }
+  }
+  if (osc) {
+    float4 carry = f4zero();
+    if (scan) {
+      const RMat KC = mat_pow(mat_adjoint(Model::matrix(k)), kLc);
+      if (c == A.n_chunks - 1) {
+        rec_publish(rec, c, kRecInc, nc, ch, e, sync.tag);
+      } else {
+        carry = lookback(rec, c, -1, A.n_chunks, nc, ch, KC, sync);
+        if (c > 0) rec_publish(rec, c, kRecInc, nc, ch, f4add(mat_apply(KC, carry), e), sync.tag);
+      }
+    }
+    float acc[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) acc[j] = 0.f;
+    float4 mcar = carry;
+#pragma unroll
+    for (int t = kLc - 1; t >= 0; --t) {
+      const float4 mu = Model::mu(mcar, g_col[t * xs2]);
+      const float2 gb = Model::grad_input(k, mu);
+      Model::accumulate(acc, mu, sp[t], bu_col[t * xs2]);
+      g_col[t * xs2] = gb;
+      mcar = Model::rev_carry(k, mu);
+    }
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
+      A.partials[(static_cast<size_t>(c) * NS + j) * nc + ch] = acc[j];
+  }
+  __syncthreads();
+
+  // 4. grad_bu rows out; grad_u = grad_bu (B_re, B_im) + D gy on the matrix cores
+  {
+    const int q2 = A.P;  // float2 per row
+    for (int e2 = threadIdx.x; e2 < kLc * q2; e2 += kLayerThreads) {
+      const int t = e2 / q2, pp = e2 - t * q2;
+      if (t < nt) A.grad_bu[prow0 + static_cast<size_t>(t) * A.P + pp] = reinterpret_cast<const float2*>(sG)[t * xs2 + pp];
+    }
+  }
+  {
+    const int kk = lane >> 5;
+    const int ng = Pp / 4;
+    const float* arow = sG + m * XS + 4 * kk;
+    for (int hg = w; hg < Hp / 32; hg += kLayerWaves) {
+      const int h = hg * 32 + m;
+      floatx16 acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+      float4 cb[kAhead];
+#pragma unroll
+      for (int j = 0; j < kAhead; ++j) cb[j] = load_bw_pair(A, h, 4 * j + 2 * kk);
+      for (int q0 = 0; q0 < ng; q0 += kAhead) {
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) {
+          const int q = q0 + j;
+          if (q >= ng) break;
+          const float4 av = *reinterpret_cast<const float4*>(arow + 8 * q);
+          const float4 cv = cb[j];
+          if (q + kAhead < ng) cb[j] = load_bw_pair(A, h, 4 * (q + kAhead) + 2 * kk);
+          acc = mfma32(av.x, cv.x, acc);
+          acc = mfma32(av.y, cv.y, acc);
+          acc = mfma32(av.z, cv.z, acc);
+          acc = mfma32(av.w, cv.w, acc);
+        }
+      }
+      if (h < A.H) {
+        const float dh = A.Dw[h];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int t = acc_row(r, lane);
+          if (t < nt) {
+            const size_t gi = row0 + static_cast<size_t>(t) * A.H + h;
+            A.grad_u[gi] = acc[r] + A.gy[gi] * dh;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <class Model>
+struct LayerParamEpilogue {
+  typename Model::Params prm;
+  float *ga, *gg, *gs;
+  __device__ void add(int p, const double* S) const { Model::epilogue(prm, p, S, ga, gg, gs); }
+};
+
+size_t layer_bwd_lds_bytes(int64_t H, int64_t P) {
+  const int64_t Hp = (H + 31) / 32 * 32, Pp = (P + 31) / 32 * 32;
+  return static_cast<size_t>(kLc * (Hp + 4) + 2 * kLc * (2 * Pp + 4) + 4 * P) * sizeof(float);
+}
+
+constexpr size_t kMaxLds = 160 * 1024;
+
+template <int V>
+int launch_layer_bwd(LayerBwdArgs args, float* ga, float* gg, float* gs, hipStream_t stream) {
+  using Model = Dlinoss<V>;
+  constexpr int NS = Model::kSums;
+  const int64_t n_wg = static_cast<int64_t>(args.Bsz) * args.n_chunks;
+  const int64_t nc = static_cast<int64_t>(args.Bsz) * args.P;
+  const size_t rec_bytes = static_cast<size_t>(args.n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
+  void* payload = nullptr;
+  LaunchSync sync{};
+  void* ws = nullptr;
+  if (int rc = acquire_workspace(stream, static_cast<size_t>(args.n_chunks) * NS * nc * sizeof(float), &ws))
+    return rc;
+  args.partials = static_cast<float*>(ws);
+  args.zero = ZeroFill{{ga, gg, gs}, args.P};
+  if (int rc = acquire_scratch(stream, rec_bytes, n_wg, &payload, &sync)) return rc;
+  const bool vec = args.H % 4 == 0 && args.P % 4 == 0 && aligned16(args.u) && aligned16(args.gy) &&
+                   aligned16(args.Bw) && aligned16(args.Cw);
+  auto kern = vec ? dlinoss_layer_bwd_kernel<V, true> : dlinoss_layer_bwd_kernel<V, false>;
+  const size_t lds = layer_bwd_lds_bytes(args.H, args.P);
+  if (int rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(lds)),
+                         "hipFuncSetAttribute"))
+    return rc;
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(n_wg)), dim3(kLayerThreads), lds, stream, args,
+                     static_cast<unsigned long long*>(payload), sync);
+  if (hipPeekAtLastError() != hipSuccess) release_unlaunched(stream, n_wg);
+  if (int rc = launch_check("dlinoss_layer_bwd_kernel")) return rc;
+  if (args.P == 0) return OSSM_OK;
+  const typename Model::Params prm{args.a, args.g, args.dt, args.P};
+  return launch_column_sums<NS>(static_cast<const float*>(ws), args.P, args.Bsz, args.n_chunks,
+                                LayerParamEpilogue<Model>{prm, ga, gg, gs}, stream);
+}
+
 size_t layer_lds_bytes(int64_t H, int64_t P) {
   const int64_t Hp = (H + 31) / 32 * 32, Pp = (P + 31) / 32 * 32;
   return static_cast<size_t>(kLc * (Hp + 4) + kLc * (2 * Pp + 4) + 4 * P) * sizeof(float);
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <int V>
 int launch_layer(const LayerArgs& args, hipStream_t stream) {
@@ -345,8 +730,9 @@ extern "C" {
 
 int ossm_dlinoss_layer_forward(int variant, const float* inputs, const float* B, const float* C,
                                const float* D, const float* a_diag, const float* g_diag,
-                               const float* step, float* outputs, int64_t batch, int64_t length,
-                               int64_t hidden, int64_t ssm, ossm_stream_t stream_v) {
+                               const float* step, float* outputs, void* carries, int64_t batch,
+                               int64_t length, int64_t hidden, int64_t ssm,
+                               ossm_stream_t stream_v) {
   clear_error();
   const char* what = "dlinoss_layer_forward";
   if (batch < 0 || length < 0 || hidden < 0 || ssm < 0)
@@ -364,7 +750,7 @@ int ossm_dlinoss_layer_forward(int variant, const float* inputs, const float* B,
     return set_error(OSSM_ERR_UNSUPPORTED, std::string(what) + ": size exceeds 32-bit indexing");
   if (!inputs || !D || !outputs || (ssm > 0 && (!B || !C || !a_diag || !g_diag || !step)))
     return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": null pointer");
-  LayerArgs args{inputs, B, C, D, a_diag, g_diag, step, outputs,
+  LayerArgs args{inputs, B, C, D, a_diag, g_diag, step, outputs, static_cast<float4*>(carries),
                  static_cast<int>(batch), static_cast<int>(length), static_cast<int>(hidden),
                  static_cast<int>(ssm), static_cast<int>(n_chunks)};
   hipStream_t stream = static_cast<hipStream_t>(stream_v);
@@ -373,6 +759,56 @@ int ossm_dlinoss_layer_forward(int variant, const float* inputs, const float* B,
     case OSSM_DLINOSS_IMEX2: return launch_layer<OSSM_DLINOSS_IMEX2>(args, stream);
     case OSSM_DLINOSS_IM: return launch_layer<OSSM_DLINOSS_IM>(args, stream);
     default: return launch_layer<OSSM_DLINOSS_EX>(args, stream);
+  }
+}
+
+int ossm_dlinoss_layer_backward(int variant, const float* inputs, const float* grad_output,
+                                const float* B, const float* C, const float* D,
+                                const float* a_diag, const float* g_diag, const float* step,
+                                const void* carries, float* grad_inputs, void* grad_bu,
+                                void* x_conj, float* grad_a, float* grad_g, float* grad_step,
+                                int64_t batch, int64_t length, int64_t hidden, int64_t ssm,
+                                ossm_stream_t stream_v) {
+  clear_error();
+  const char* what = "dlinoss_layer_backward";
+  if (batch < 0 || length < 0 || hidden < 0 || ssm < 0)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": negative size");
+  if (variant < OSSM_DLINOSS_IMEX1 || variant > OSSM_DLINOSS_EX)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": unknown variant");
+  if (hidden > kLayerMax || ssm > kLayerMax || layer_bwd_lds_bytes(hidden, ssm) > kMaxLds)
+    return set_error(OSSM_ERR_UNSUPPORTED,
+                     std::string(what) + ": hidden_dim " + std::to_string(hidden) + " and ssm_size " +
+                         std::to_string(ssm) + " exceed one workgroup's LDS");
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  if (ssm > 0 && (!grad_a || !grad_g || !grad_step))
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": null pointer");
+  if (batch == 0 || length == 0 || hidden == 0) {
+    // no terms: zero parameter gradients (grad_inputs, grad_bu, x_conj are empty
+    // or, with hidden == 0, hold no dependence on the scan)
+    for (float* p : {grad_a, grad_g, grad_step})
+      if (int rc = fill_zero(p, ssm, stream)) return rc;
+    if (hidden == 0 && batch > 0 && length > 0 && ssm > 0) {
+      if (int rc = fill_zero(static_cast<float*>(grad_bu), 2 * batch * length * ssm, stream)) return rc;
+      if (int rc = fill_zero(static_cast<float*>(x_conj), 2 * batch * length * ssm, stream)) return rc;
+    }
+    return OSSM_OK;
+  }
+  const int64_t n_chunks = (length + kLc - 1) / kLc;
+  if (length > INT_MAX || batch * n_chunks > INT_MAX || batch * ssm > INT_MAX / 8)
+    return set_error(OSSM_ERR_UNSUPPORTED, std::string(what) + ": size exceeds 32-bit indexing");
+  if (!inputs || !grad_output || !D || !grad_inputs ||
+      (ssm > 0 && (!B || !C || !a_diag || !g_diag || !step || !carries || !grad_bu || !x_conj)))
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": null pointer");
+  LayerBwdArgs args{inputs, grad_output, B, C, D, a_diag, g_diag, step,
+                    static_cast<const float4*>(carries), grad_inputs,
+                    static_cast<float2*>(grad_bu), static_cast<float2*>(x_conj), nullptr,
+                    ZeroFill{}, static_cast<int>(batch), static_cast<int>(length),
+                    static_cast<int>(hidden), static_cast<int>(ssm), static_cast<int>(n_chunks)};
+  switch (variant) {
+    case OSSM_DLINOSS_IMEX1: return launch_layer_bwd<OSSM_DLINOSS_IMEX1>(args, grad_a, grad_g, grad_step, stream);
+    case OSSM_DLINOSS_IMEX2: return launch_layer_bwd<OSSM_DLINOSS_IMEX2>(args, grad_a, grad_g, grad_step, stream);
+    case OSSM_DLINOSS_IM: return launch_layer_bwd<OSSM_DLINOSS_IM>(args, grad_a, grad_g, grad_step, stream);
+    default: return launch_layer_bwd<OSSM_DLINOSS_EX>(args, grad_a, grad_g, grad_step, stream);
   }
 }
 

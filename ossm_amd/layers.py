@@ -9,10 +9,13 @@ same stable-region projection and the same forward contract, so a reference
 Forward on a GPU float32 (or bf16 / fp16, computed in float32 as the
 reference does) input is ``ossm_dlinoss_layer_forward``: the in-projection
 ``bu = u B^T``, the D-LinOSS scan and ``y = Re(x C^T) + D u`` in one launch,
-with bu and the states kept on chip.  The backward recomputes bu and the
-states through the unfused composition of this library's kernels
-(``bridge.run_dlinoss`` and plain GEMMs) and differentiates that, so training
-keeps only the layer input between forward and backward.
+with bu and the states kept on chip; for training it also saves the state
+entering each 32-step chunk.  The backward is ``ossm_dlinoss_layer_backward``
+(the projections of the upstream gradient and of u on the matrix cores, the
+states re-run from those carries, the scan adjoint, grad_u), followed by the
+two weight-gradient GEMMs over the grad_bu and x it returns.  Shapes whose
+backward does not fit one workgroup's LDS recompute through the unfused
+composition (``unfused_layer_forward``) and differentiate that.
 
 No CPU path computes here: CPU tensors go through the same composition, whose
 scan delegates to the reference's CPU module when it is installed (as the
@@ -23,7 +26,7 @@ kernels compute in float32 / complex64.
 from __future__ import annotations
 
 import math
-from typing import Tuple
+from typing import Optional, Tuple
 
 import torch
 from torch import Tensor, nn
@@ -31,11 +34,20 @@ from torch import Tensor, nn
 from . import _lib
 from .bridge import run_dlinoss
 
-__all__ = ["DampedLinOSSLayer", "dlinoss_layer_forward", "DlinossLayerFn", "project_parameters",
-           "unfused_layer_forward"]
+__all__ = ["DampedLinOSSLayer", "dlinoss_layer_forward", "dlinoss_layer_backward", "DlinossLayerFn",
+           "project_parameters", "unfused_layer_forward"]
 
 _VARIANTS = {"imex1": 0, "imex2": 1, "im": 2, "ex": 3}
 _LAYER_MAX = 256  # largest hidden_dim / ssm_size of the fused kernel
+_CHUNK = 32       # steps per workgroup chunk (the carries' second dimension)
+_LDS = 160 * 1024
+
+
+def _bwd_fits(hidden: int, ssm: int) -> bool:
+    """The fused backward's LDS (u or gy rows, bu and grad_bu tiles) fits one
+    workgroup (mirrors layer_bwd_lds_bytes in dlinoss_layer.hip)."""
+    hp, pp = -(-hidden // 32) * 32, -(-ssm // 32) * 32
+    return (_CHUNK * (hp + 4) + 2 * _CHUNK * (2 * pp + 4) + 4 * ssm) * 4 <= _LDS
 
 
 def project_parameters(A_diag: Tensor, G_diag: Tensor, steps: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
@@ -73,9 +85,12 @@ def _check_layer_args(inputs: Tensor, B: Tensor, C: Tensor, D: Tensor, a: Tensor
 
 
 def dlinoss_layer_forward(variant: str, inputs: Tensor, B: Tensor, C: Tensor, D: Tensor,
-                          a_diag: Tensor, g_diag: Tensor, step: Tensor) -> Tensor:
+                          a_diag: Tensor, g_diag: Tensor, step: Tensor,
+                          carries: Optional[Tensor] = None) -> Tensor:
     """y = Re(x C^T) + D u with x the D-LinOSS states driven by bu = u B^T, in
-    one kernel launch.  Every tensor float32 on one GPU; a, g, step projected."""
+    one kernel launch.  Every tensor float32 on one GPU; a, g, step projected.
+    ``carries`` (float32 [batch, ceil(length / 32), ssm, 4]) receives the state
+    entering each chunk, for ``dlinoss_layer_backward``."""
     variant = variant.lower()
     if variant not in _VARIANTS:
         raise ValueError(f"Unknown D-LinOSS variant '{variant}'.")
@@ -93,13 +108,61 @@ def dlinoss_layer_forward(variant: str, inputs: Tensor, B: Tensor, C: Tensor, D:
     out = torch.empty_like(u)
     if out.numel() == 0:
         return out
+    if carries is not None:
+        want = (batch, -(-length // _CHUNK), ssm, 4)
+        if tuple(carries.shape) != want or carries.dtype != torch.float32 or \
+                not carries.is_contiguous() or carries.device != u.device:
+            raise RuntimeError(f"carries must be a contiguous float32 {want} tensor on {u.device}")
     lib = _lib.load()
     with torch.cuda.device(u.device):
         _lib.check(lib.ossm_dlinoss_layer_forward(
             _VARIANTS[variant], u.data_ptr(), Bc.data_ptr(), Cc.data_ptr(), Dc.data_ptr(),
-            a.data_ptr(), g.data_ptr(), s.data_ptr(), out.data_ptr(), batch, length, hidden, ssm,
-            _lib.stream_of(u)))
+            a.data_ptr(), g.data_ptr(), s.data_ptr(), out.data_ptr(), _lib.ptr(carries), batch,
+            length, hidden, ssm, _lib.stream_of(u)))
     return out
+
+
+def dlinoss_layer_backward(variant: str, inputs: Tensor, grad_output: Tensor, B: Tensor,
+                           C: Tensor, D: Tensor, a_diag: Tensor, g_diag: Tensor, step: Tensor,
+                           carries: Tensor):
+    """Gradients of the fused layer: ``(grad_inputs, grad_B, grad_C, grad_D, grad_a,
+    grad_g, grad_step)`` from the forward's ``carries``.  One kernel for
+    grad_inputs and the scan's parameter gradients; grad_B and grad_C are GEMMs
+    over the grad_bu and conj(x) it returns, grad_D a sum."""
+    batch, length, hidden, ssm = _check_layer_args(inputs, B, C, D, a_diag, g_diag, step)
+    u, go, Bc, Cc, Dc, a, g, s = (t.contiguous() for t in
+                                  (inputs, grad_output, B, C, D, a_diag, g_diag, step))
+    dev = u.device
+    gu = torch.empty_like(u)
+    gbu = torch.empty((batch, length, ssm, 2), dtype=torch.float32, device=dev)
+    xq = torch.empty_like(gbu)
+    ga, gg, gs = (torch.empty(ssm, dtype=torch.float32, device=dev) for _ in range(3))
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().ossm_dlinoss_layer_backward(
+            _VARIANTS[variant.lower()], u.data_ptr(), go.data_ptr(), Bc.data_ptr(), Cc.data_ptr(),
+            Dc.data_ptr(), a.data_ptr(), g.data_ptr(), s.data_ptr(), carries.data_ptr(),
+            gu.data_ptr(), gbu.data_ptr(), xq.data_ptr(), ga.data_ptr(), gg.data_ptr(),
+            gs.data_ptr(), batch, length, hidden, ssm, _lib.stream_of(u)))
+    rows = batch * length
+    uf, gof = u.reshape(rows, hidden), go.reshape(rows, hidden)
+    # grad_B[p, h, c] = sum_r grad_bu[r, p, c] u[r, h];  grad_C[h, p, c] = sum_r go[r, h] xq[r, p, c]
+    gB = _sum_rows_product(gbu.reshape(rows, 2 * ssm), uf)
+    gB = gB.reshape(ssm, 2, hidden).permute(0, 2, 1).contiguous()
+    gC = _sum_rows_product(gof, xq.reshape(rows, 2 * ssm)).reshape(hidden, ssm, 2)
+    gD = (gof * uf).sum(0)
+    return gu, gB, gC, gD, ga, gg, gs
+
+
+def _sum_rows_product(a: Tensor, b: Tensor, split: int = 128) -> Tensor:
+    """a^T b for row-major a [R, M], b [R, N] with R much larger than M, N (the
+    weight gradients sum over every (batch, step) row): R is split into
+    ``split`` slices multiplied as one batched GEMM and the partials added,
+    the shape the library GEMMs run well (one GEMM with K = R ran at ~24
+    TFLOP/s here)."""
+    R = a.size(0)
+    if R < 4 * split or R % split != 0:
+        return a.t() @ b
+    return torch.bmm(a.view(split, R // split, -1).transpose(1, 2), b.view(split, R // split, -1)).sum(0)
 
 
 def unfused_layer_forward(variant: str, inputs: Tensor, B: Tensor, C: Tensor, D: Tensor,
@@ -121,19 +184,30 @@ def unfused_layer_forward(variant: str, inputs: Tensor, B: Tensor, C: Tensor, D:
 
 
 class DlinossLayerFn(torch.autograd.Function):
-    """Fused forward; backward by recomputation through ``unfused_layer_forward``."""
+    """Fused forward and backward (``dlinoss_layer_backward``); shapes whose
+    backward does not fit recompute through ``unfused_layer_forward``."""
 
     @staticmethod
     def forward(ctx, variant: str, inputs: Tensor, B: Tensor, C: Tensor, D: Tensor,
                 a_diag: Tensor, g_diag: Tensor, step: Tensor) -> Tensor:  # type: ignore[override]
         ctx.variant = variant
-        ctx.save_for_backward(inputs, B, C, D, a_diag, g_diag, step)
-        return dlinoss_layer_forward(variant, inputs, B, C, D, a_diag, g_diag, step)
+        batch, length, hidden = inputs.shape
+        ssm = B.size(0)
+        carries = None
+        if any(ctx.needs_input_grad[1:]) and _bwd_fits(hidden, ssm):
+            carries = torch.empty((batch, -(-length // _CHUNK), ssm, 4), dtype=torch.float32,
+                                  device=inputs.device)
+        ctx.fused_bwd = carries is not None
+        ctx.save_for_backward(inputs, B, C, D, a_diag, g_diag, step, carries)
+        return dlinoss_layer_forward(variant, inputs, B, C, D, a_diag, g_diag, step, carries)
 
     @staticmethod
     def backward(ctx, grad_out: Tensor):  # type: ignore[override]
-        saved = ctx.saved_tensors
+        *saved, carries = ctx.saved_tensors
         needs = ctx.needs_input_grad[1:]
+        if ctx.fused_bwd:
+            grads = dlinoss_layer_backward(ctx.variant, *saved[:1], grad_out, *saved[1:], carries)
+            return (None, *[gr if n else None for gr, n in zip(grads, needs)])
         with torch.enable_grad():
             leaves = [t.detach().requires_grad_(bool(n)) for t, n in zip(saved, needs)]
             y = unfused_layer_forward(ctx.variant, *leaves)

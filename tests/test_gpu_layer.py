@@ -228,3 +228,57 @@ def test_layer_repeatable(layers):
     y1 = to_np(layers.dlinoss_layer_forward("im", *args))
     y2 = to_np(layers.dlinoss_layer_forward("im", *args))
     assert np.abs(y1 - y2).max() <= 1e-6 * max(1.0, np.abs(y1).max())
+
+
+@pytest.mark.parametrize("shape", [(2, 70, 13, 9), (3, 33, 40, 4), (1, 1, 8, 8)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_layer_fused_backward_odd_sizes(layers, shape):
+    """The fused backward on sizes that take the unaligned paths (H, P not
+    multiples of 4, one-step rows) against fp64 oracle gradients."""
+    nb, L, H, P = shape
+    announce(f"layer fused bwd odd B={nb} L={L} H={H} P={P}")
+    args = _layer_inputs(nb, L, H, P, 12, "im")
+    gy = np.random.default_rng(13).normal(size=(nb, L, H)).astype(np.float32)
+    leaves = [to_dev(x).requires_grad_(True) for x in args]
+    y = layers.DlinossLayerFn.apply("im", *leaves)
+    y.backward(to_dev(gy))
+    ref = _oracle_grads("im", args, gy.astype(np.float64))
+    for t, r, n in zip(leaves, ref, ["inputs", "B", "C", "D", "a_diag", "g_diag", "step"]):
+        err = rel_fro(to_np(t.grad), r)
+        assert err < 5e-5, f"grad {n}: relative error {err:.2e}"
+    no_device_errors()
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_layer_fused_backward_matches_unfused_at_size(layers, variant):
+    """At H = P = 128 over 1000 steps (32 chunks through the reverse look-back)
+    the fused backward's gradients equal the unfused composition's."""
+    nb, L, H, P = 4, 1000, 128, 128
+    announce(f"layer fused vs unfused bwd {variant} B={nb} L={L}")
+    args = [to_dev(x) for x in _layer_inputs(nb, L, H, P, 21, variant)]
+    gy = torch.randn(nb, L, H, device="cuda")
+    l1 = [t.clone().requires_grad_(True) for t in args]
+    layers.DlinossLayerFn.apply(variant, *l1).backward(gy)
+    l2 = [t.clone().requires_grad_(True) for t in args]
+    layers.unfused_layer_forward(variant, *l2).backward(gy)
+    for a_, b_, n in zip(l1, l2, ["inputs", "B", "C", "D", "a_diag", "g_diag", "step"]):
+        assert np.isfinite(to_np(a_.grad)).all()
+        err = rel_fro(to_np(a_.grad), to_np(b_.grad))
+        assert err < 1e-4, f"{variant} grad {n}: {err:.2e}"
+    no_device_errors()
+
+
+def test_layer_backward_falls_back_when_lds_is_short(layers):
+    """H = P = 256 needs more LDS than one workgroup has for the fused backward:
+    the forward stays fused, the backward recomputes through the composition."""
+    nb, L, H, P = 1, 40, 256, 256
+    announce("layer backward fallback H=P=256")
+    assert not layers._bwd_fits(H, P)
+    args = _layer_inputs(nb, L, H, P, 31, "imex1")
+    gy = np.random.default_rng(32).normal(size=(nb, L, H)).astype(np.float32)
+    leaves = [to_dev(x).requires_grad_(True) for x in args]
+    layers.DlinossLayerFn.apply("imex1", *leaves).backward(to_dev(gy))
+    ref = _oracle_grads("imex1", args, gy.astype(np.float64))
+    for t, r in zip(leaves, ref):
+        assert rel_fro(to_np(t.grad), r) < 5e-5
+    no_device_errors()
