@@ -317,10 +317,22 @@ def _detail_configs(torch, K, dev, reps=10):
     with torch.no_grad():
         tu = _ev_time(torch, lambda: LY.unfused_layer_forward("imex1", *args), reps, 3)
     flops = 8 * B * L * H * P
-    out["dlinoss_layer_fwd_c2_shape"] = {"fused_ms": tf, "unfused_ms": tu,
-                                         "TFLOPs": flops / (tf / 1e3) / 1e12,
-                                         "mfma_frac_fp32": flops / (tf / 1e3) / PEAK_MFMA_FP32}
-    del args
+    leaves = [t.clone().requires_grad_(True) for t in args]
+    gy = torch.randn(B, L, H, device=dev, generator=g)
+
+    def fused_step():
+        LY.DlinossLayerFn.apply("imex1", *leaves).backward(gy)
+
+    def unfused_step():
+        LY.unfused_layer_forward("imex1", *leaves).backward(gy)
+
+    tfb = _ev_time(torch, fused_step, reps, 3)
+    tufb = _ev_time(torch, unfused_step, reps, 3)
+    out["dlinoss_layer_c2_shape"] = {"fused_fwd_ms": tf, "unfused_fwd_ms": tu,
+                                     "fused_fwd_bwd_ms": tfb, "unfused_fwd_bwd_ms": tufb,
+                                     "fwd_TFLOPs": flops / (tf / 1e3) / 1e12,
+                                     "fwd_mfma_frac_fp32": flops / (tf / 1e3) / PEAK_MFMA_FP32}
+    del args, leaves, gy
     # Fused Mamba mixer (projections included) at C3's and C4's shapes, forward
     # and forward + backward
     from ossm_amd.mamba import MambaMixer
