@@ -42,7 +42,7 @@ enum {
 
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
-/* Library ABI version (bumped on any change of the entry points; currently 8). */
+/* Library ABI version (bumped on any change of the entry points; currently 9). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -167,6 +167,25 @@ int ossm_sdlinoss_backward(int variant, const float* A, int64_t a_len, int64_t a
                            const void* grad_output, float* grad_A, float* grad_G,
                            float* grad_step, void* grad_bu, int64_t length, int64_t batch,
                            int64_t ssm, ossm_stream_t stream);
+
+/*
+ * complex128 forms of the two entries above: the reference's device kernels
+ * dispatch complex128 too (sdlinoss_imex1_cuda.cu:232, 271, and siblings).  A, G,
+ * step are fp64 [X_len, X_batch, M]; bu, states, grad_output, grad_bu are c128
+ * with the layouts above; grad_A, grad_G, grad_step fp64.  One lane per channel
+ * walks the sequence (the backward reads every step's previous state from states);
+ * broadcast gradients are summed in a fixed order.
+ */
+int ossm_sdlinoss_forward_f64(int variant, const double* A, int64_t a_len, int64_t a_batch,
+                              const double* G, int64_t g_len, int64_t g_batch, const double* step,
+                              int64_t s_len, int64_t s_batch, const void* bu, void* states,
+                              int64_t length, int64_t batch, int64_t ssm, ossm_stream_t stream);
+int ossm_sdlinoss_backward_f64(int variant, const double* A, int64_t a_len, int64_t a_batch,
+                               const double* G, int64_t g_len, int64_t g_batch,
+                               const double* step, int64_t s_len, int64_t s_batch, const void* bu,
+                               const void* states, const void* grad_output, double* grad_A,
+                               double* grad_G, double* grad_step, void* grad_bu, int64_t length,
+                               int64_t batch, int64_t ssm, ossm_stream_t stream);
 
 /*
  * bf16 storage variants of the two entries above.  No counterpart in the

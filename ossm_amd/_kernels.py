@@ -425,9 +425,26 @@ def _sdl_param(param: torch.Tensor, name: str, length: int, batch: int, ssm: int
         _check(param.size(0) in (length, 1) and param.size(1) in (batch, 1),
                f"{name} must have shape (L,B,M) with optional singleton L/B axes; got {shape}")
         la, ba = param.size(0), param.size(1)
-    _check(param.dtype == torch.float32,
-           f"{name} must be float32 on the device (the MI355X kernels compute complex64 only)")
     return param.contiguous(), la, ba
+
+
+# complex dtype of bu -> (real parameter dtype, forward entry, backward entry)
+_SDL_ENTRIES = {
+    torch.complex64: (torch.float32, "ossm_sdlinoss_forward", "ossm_sdlinoss_backward"),
+    torch.complex128: (torch.float64, "ossm_sdlinoss_forward_f64", "ossm_sdlinoss_backward_f64"),
+}
+
+
+def _sdl_entries(variant: str, direction: str, bu: torch.Tensor, params):
+    """The reference's device kernels dispatch complex64 and complex128
+    (AT_DISPATCH_COMPLEX_TYPES, sdlinoss_imex1_cuda.cu:232, 271); parameters
+    must be the matching real dtype."""
+    _check(bu.dtype in _SDL_ENTRIES,
+           f"sdlinoss_{variant}_{direction}: bu must be complex64 or complex128, got {bu.dtype}")
+    real, fwd, bwd = _SDL_ENTRIES[bu.dtype]
+    for p, name in params:
+        _check(p.dtype == real, f"{name} must be {real} to match bu ({bu.dtype}); got {p.dtype}")
+    return fwd if direction == "forward" else bwd
 
 
 def _sdl_forward(variant: str, A, G, step, bu):
@@ -441,15 +458,15 @@ def _sdl_forward(variant: str, A, G, step, bu):
     out = torch.empty((length, batch, ssm, 2), dtype=bu.dtype, device=bu.device)
     if length == 0:
         return out
-    _check(bu.dtype == torch.complex64,
-           f"sdlinoss_{variant}_forward: the MI355X kernels compute complex64 only")
-    views = [_sdl_param(p, n, length, batch, ssm) for p, n in ((A, "A"), (G, "G"), (step, "step"))]
+    named = ((A, "A"), (G, "G"), (step, "step"))
+    entry = _sdl_entries(variant, "forward", bu, named)
+    views = [_sdl_param(p, n, length, batch, ssm) for p, n in named]
     b = bu.contiguous()
     args = []
     for v, la, ba in views:
         args += [v.data_ptr(), la, ba]
     with torch.cuda.device(bu.device):
-        _lib.check(_lib.load().ossm_sdlinoss_forward(
+        _lib.check(getattr(_lib.load(), entry)(
             _VARIANT_CODE[variant], *args, b.data_ptr(), out.data_ptr(), length, batch, ssm,
             _lib.stream_of(b)))
     return out
@@ -471,17 +488,19 @@ def _sdl_backward(variant: str, A, G, step, bu, states, grad_output):
     grad_bu = torch.empty_like(bu)
     if length == 0 or batch == 0 or ssm == 0:
         return [g.zero_() for g in grads] + [grad_bu]
-    _check(bu.dtype == torch.complex64,
-           f"sdlinoss_{variant}_backward: the MI355X kernels compute complex64 only")
+    named = ((A, "A"), (G, "G"), (step, "step"))
+    entry = _sdl_entries(variant, "backward", bu, named)
+    _check(states.dtype == bu.dtype and grad_output.dtype == bu.dtype,
+           "states and grad_output must have bu's dtype")
     _check(tuple(states.shape) == (length, batch, ssm, 2),
            "states must have shape (length, batch, ssm_size, 2)")
-    views = [_sdl_param(p, n, length, batch, ssm) for p, n in ((A, "A"), (G, "G"), (step, "step"))]
+    views = [_sdl_param(p, n, length, batch, ssm) for p, n in named]
     b = bu.contiguous()
     args = []
     for v, la, ba in views:
         args += [v.data_ptr(), la, ba]
     with torch.cuda.device(bu.device):
-        _lib.check(_lib.load().ossm_sdlinoss_backward(
+        _lib.check(getattr(_lib.load(), entry)(
             _VARIANT_CODE[variant], *args, b.data_ptr(), states.data_ptr(), grad_output.data_ptr(),
             grads[0].data_ptr(), grads[1].data_ptr(), grads[2].data_ptr(), grad_bu.data_ptr(),
             length, batch, ssm, _lib.stream_of(b)))

@@ -1,0 +1,366 @@
+// Selective D-LinOSS in complex128 (float64 parameters) on gfx950.  The
+// reference's device kernels dispatch complex128 as well as complex64
+// (sdlinoss_imex1_cuda.cu:232, 271, and the imex2 / im / ex siblings), so the
+// drop-in has to serve both.  fp64 is the accuracy path, not the hot one:
+// one lane per channel walks the sequence, forward in time for the states and
+// in reverse for the adjoint, and consecutive lanes own consecutive channels,
+// so every load and store of a wave is one contiguous run.
+//
+// Recurrence and chain rule are the complex64 kernels' (sdlinoss_<v>.cpp
+// forward kernels, backward kernels sdlinoss_imex1.cpp:186-220,
+// sdlinoss_imex2.cpp:178-221, sdlinoss_im.cpp:176-225,
+// sdlinoss_ex.cpp:163-189), in double, with the division by S kept as a
+// division:
+//   dt = clamp(step, 1e-6, 1), comb = -a x + bu, tmpw = alpha w + dt^2 comb,
+//   w' = tmpw / S, x' = x + w'.
+// Parameter gradients broadcast over time are summed over time in the lane
+// (sequential, fixed order); those broadcast over batch rows are summed over
+// the rows afterwards by one lane per output element, also in a fixed order.
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+#include <string>
+
+#include "../../include/ossm_scan.h"
+#include "runtime.hpp"
+
+namespace ossm {
+namespace {
+
+constexpr double kDtMin64 = 1e-6;
+constexpr double kDtMax64 = 1.0;
+constexpr double kClampMin64 = 1e-6;
+constexpr int kBlock64 = 256;
+
+// One parameter [La, Ba, M]: element (t, channel ch = b M + m) at
+// p[t * t_stride + (by_channel ? ch : m)].
+struct View64 {
+  const double* p;
+  long long t_stride;
+  int by_channel;
+};
+
+struct Params64 {
+  View64 v[3];  // a, g, step
+  int M;
+};
+
+__device__ __forceinline__ double at64(const View64& v, int t, int ch, int m) {
+  return v.p[static_cast<size_t>(t) * v.t_stride + (v.by_channel ? ch : m)];
+}
+
+template <int V>
+__device__ __forceinline__ double alpha64(double dt, double g) {
+  if constexpr (V == OSSM_DLINOSS_IMEX2 || V == OSSM_DLINOSS_EX) return 1.0 - dt * g;
+  else return 1.0;
+}
+
+template <int V>
+__device__ __forceinline__ double s_raw64(double dt, double g, double a) {
+  if constexpr (V == OSSM_DLINOSS_IMEX1) return 1.0 + dt * g;
+  else if constexpr (V == OSSM_DLINOSS_IMEX2) return 1.0 + dt * dt * a;
+  else if constexpr (V == OSSM_DLINOSS_IM) return 1.0 + dt * g + dt * dt * a;
+  else return 1.0;
+}
+
+__device__ __forceinline__ double dt64(double step_raw) {
+  return fmin(fmax(step_raw, kDtMin64), kDtMax64);
+}
+
+// ---- forward: states[t] = (w_t, x_t) ------------------------------------------
+template <int V>
+__global__ __launch_bounds__(kBlock64) void sdl64_forward_kernel(Params64 prm,
+                                                                 const double2* __restrict__ bu,
+                                                                 double2* __restrict__ states,
+                                                                 int L, int nc) {
+  const int ch = static_cast<int>(blockIdx.x) * kBlock64 + static_cast<int>(threadIdx.x);
+  if (ch >= nc) return;
+  const int m = ch % prm.M;
+  double wr = 0.0, wi = 0.0, xr = 0.0, xi = 0.0;
+  for (int t = 0; t < L; ++t) {
+    const double a = at64(prm.v[0], t, ch, m), g = at64(prm.v[1], t, ch, m);
+    const double dt = dt64(at64(prm.v[2], t, ch, m));
+    const double dt2 = dt * dt, alpha = alpha64<V>(dt, g);
+    const double2 b = bu[static_cast<size_t>(t) * nc + ch];
+    double tr = alpha * wr + dt2 * (-a * xr + b.x);
+    double ti = alpha * wi + dt2 * (-a * xi + b.y);
+    if constexpr (V != OSSM_DLINOSS_EX) {
+      const double S = fmax(s_raw64<V>(dt, g, a), kClampMin64);
+      tr /= S;
+      ti /= S;
+    }
+    wr = tr;
+    wi = ti;
+    xr += wr;
+    xi += wi;
+    double2* out = states + 2 * (static_cast<size_t>(t) * nc + ch);
+    out[0] = make_double2(wr, wi);
+    out[1] = make_double2(xr, xi);
+  }
+}
+
+// ---- backward -------------------------------------------------------------------
+// Where parameter p's gradient goes (mode[p]): 0 = per element at
+// out[t * nc + ch] (full shape); 1 = summed over time, written at out[ch];
+// 2 = per element, to be summed over the batch rows afterwards.
+struct Grads64 {
+  double* out[3];
+  int mode[3];
+};
+
+template <int V>
+__global__ __launch_bounds__(kBlock64) void sdl64_backward_kernel(
+    Params64 prm, const double2* __restrict__ bu, const double2* __restrict__ states,
+    const double2* __restrict__ gout, double2* __restrict__ gin, Grads64 dst, int L, int nc) {
+  const int ch = static_cast<int>(blockIdx.x) * kBlock64 + static_cast<int>(threadIdx.x);
+  if (ch >= nc) return;
+  const int m = ch % prm.M;
+  // adjoint of the state after step t: (lw, lx); the upstream gradient
+  // enters through x
+  double lwr = 0.0, lwi = 0.0, lxr = 0.0, lxi = 0.0;
+  double tsum[3] = {0.0, 0.0, 0.0};
+  for (int t = L - 1; t >= 0; --t) {
+    const size_t e = static_cast<size_t>(t) * nc + ch;
+    const double2 go = gout[e];
+    lxr += go.x;
+    lxi += go.y;
+    double2 wp = make_double2(0.0, 0.0), xp = make_double2(0.0, 0.0);
+    if (t > 0) {
+      wp = states[2 * (e - nc)];
+      xp = states[2 * (e - nc) + 1];
+    }
+    const double2 b = bu[e];
+    const double a = at64(prm.v[0], t, ch, m), g = at64(prm.v[1], t, ch, m);
+    const double step_raw = at64(prm.v[2], t, ch, m);
+    const double dt = dt64(step_raw), dt2 = dt * dt, alpha = alpha64<V>(dt, g);
+    // gradient w.r.t. the new w, through both components (x' = x + w')
+    const double gwr = lwr + lxr, gwi = lwi + lxi;
+    const double combr = -a * xp.x + b.x, combi = -a * xp.y + b.y;
+    double gdt = 0.0, gA = 0.0, gG = 0.0;
+    double gtr = gwr, gti = gwi;  // gradient w.r.t. tmpw
+    if constexpr (V != OSSM_DLINOSS_EX) {
+      const double s_raw = s_raw64<V>(dt, g, a);
+      const double S = fmax(s_raw, kClampMin64);
+      const double tmpr = alpha * wp.x + dt2 * combr, tmpi = alpha * wp.y + dt2 * combi;
+      gtr = gwr / S;
+      gti = gwi / S;
+      const double gS = s_raw > kClampMin64 ? -(gwr * tmpr + gwi * tmpi) / (S * S) : 0.0;
+      if constexpr (V == OSSM_DLINOSS_IMEX1) {
+        gdt = gS * g;
+        gG = gS * dt;
+      } else if constexpr (V == OSSM_DLINOSS_IMEX2) {
+        gdt = gS * (2.0 * dt * a);
+        gA = gS * dt2;
+      } else {
+        gdt = gS * (g + 2.0 * dt * a);
+        gA = gS * dt2;
+        gG = gS * dt;
+      }
+    }
+    // tmpw = alpha w_prev + dt^2 (-a x_prev + bu)
+    if constexpr (V == OSSM_DLINOSS_IMEX2 || V == OSSM_DLINOSS_EX) {
+      gdt += gtr * (-g * wp.x + 2.0 * dt * combr) + gti * (-g * wp.y + 2.0 * dt * combi);
+      gG += gtr * (-dt * wp.x) + gti * (-dt * wp.y);
+    } else {
+      gdt += gtr * (2.0 * dt * combr) + gti * (2.0 * dt * combi);
+    }
+    gA += gtr * (-dt2 * xp.x) + gti * (-dt2 * xp.y);
+    gin[e] = make_double2(gtr * dt2, gti * dt2);
+    const double gp[3] = {gA, gG, (step_raw > kDtMin64 && step_raw < kDtMax64) ? gdt : 0.0};
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      if (dst.mode[p] == 1) tsum[p] += gp[p];
+      else dst.out[p][e] = gp[p];
+    }
+    // carry to the previous state: d/dw_prev = alpha gt, d/dx_prev = lx - dt^2 a gt
+    lwr = alpha * gtr;
+    lwi = alpha * gti;
+    lxr -= dt2 * a * gtr;
+    lxi -= dt2 * a * gti;
+  }
+#pragma unroll
+  for (int p = 0; p < 3; ++p)
+    if (dst.mode[p] == 1) dst.out[p][ch] = tsum[p];
+}
+
+// out[n * C + c] = sum_{r < R} in[(n R + r) C + c], one lane per output, rows in order.
+__global__ __launch_bounds__(kBlock64) void sdl64_rows_sum_kernel(const double* __restrict__ in,
+                                                                  double* __restrict__ out,
+                                                                  long long n_out, int R, int C) {
+  const long long i = static_cast<long long>(blockIdx.x) * kBlock64 + threadIdx.x;
+  if (i >= n_out) return;
+  const long long n = i / C, c = i - n * C;
+  const double* src = in + static_cast<size_t>(n) * R * C + c;
+  double s = 0.0;
+  for (int r = 0; r < R; ++r) s += src[static_cast<size_t>(r) * C];
+  out[i] = s;
+}
+
+__global__ __launch_bounds__(kBlock64) void sdl64_zero_kernel(double* __restrict__ p, long long n) {
+  const long long i = static_cast<long long>(blockIdx.x) * kBlock64 + threadIdx.x;
+  if (i < n) p[i] = 0.0;
+}
+
+unsigned blocks_for(long long n) { return static_cast<unsigned>((n + kBlock64 - 1) / kBlock64); }
+
+struct Shape64 {
+  const double* p;
+  int64_t la, ba;
+};
+
+int check64(int variant, const Shape64 (&s)[3], int64_t L, int64_t B, int64_t M, const char* what) {
+  if (variant < 0 || variant > 3)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "Unknown selective D-LinOSS variant code");
+  if (L < 0 || B < 0 || M < 0)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": negative size");
+  if (L > INT_MAX / 2 || B * M > INT_MAX / 2 || L * B * M > (int64_t(1) << 40))
+    return set_error(OSSM_ERR_UNSUPPORTED, std::string(what) + ": size exceeds 32-bit indexing");
+  const char* names[3] = {"A", "G", "step"};
+  for (int p = 0; p < 3; ++p) {
+    if (s[p].p == nullptr)
+      return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": null " + names[p]);
+    if (!(s[p].la == 1 || s[p].la == L) || !(s[p].ba == 1 || s[p].ba == B))
+      return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(names[p]) +
+                                                      " must have shape (L,B,M) with optional singleton L/B axes");
+  }
+  return OSSM_OK;
+}
+
+Params64 params64(const Shape64 (&s)[3], int64_t L, int64_t B, int64_t M) {
+  Params64 prm{};
+  for (int p = 0; p < 3; ++p) {
+    prm.v[p].p = s[p].p;
+    prm.v[p].t_stride = (s[p].la == 1 && L > 1) ? 0 : s[p].ba * M;
+    prm.v[p].by_channel = s[p].ba == B ? 1 : 0;
+  }
+  prm.M = static_cast<int>(M);
+  return prm;
+}
+
+}  // namespace
+}  // namespace ossm
+
+using namespace ossm;
+
+extern "C" {
+
+int ossm_sdlinoss_forward_f64(int variant, const double* A, int64_t a_len, int64_t a_batch,
+                              const double* G, int64_t g_len, int64_t g_batch, const double* step,
+                              int64_t s_len, int64_t s_batch, const void* bu, void* states,
+                              int64_t length, int64_t batch, int64_t ssm, ossm_stream_t stream_v) {
+  clear_error();
+  const Shape64 shapes[3] = {{A, a_len, a_batch}, {G, g_len, g_batch}, {step, s_len, s_batch}};
+  if (length == 0 || batch == 0 || ssm == 0) {
+    if (variant < 0 || variant > 3)
+      return set_error(OSSM_ERR_INVALID_ARGUMENT, "Unknown selective D-LinOSS variant code");
+    return OSSM_OK;
+  }
+  if (int rc = check64(variant, shapes, length, batch, ssm, "sdlinoss_forward_f64")) return rc;
+  if (!bu || !states) return set_error(OSSM_ERR_INVALID_ARGUMENT, "sdlinoss_forward_f64: null pointer");
+  const Params64 prm = params64(shapes, length, batch, ssm);
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  const int nc = static_cast<int>(batch * ssm), L = static_cast<int>(length);
+  const auto* b = static_cast<const double2*>(bu);
+  auto* st = static_cast<double2*>(states);
+  switch (variant) {
+#define OSSM_SDL64_FWD(V)                                                                         \
+  case V:                                                                                         \
+    hipLaunchKernelGGL(sdl64_forward_kernel<V>, dim3(blocks_for(nc)), dim3(kBlock64), 0, stream, \
+                       prm, b, st, L, nc);                                                        \
+    break;
+    OSSM_SDL64_FWD(OSSM_DLINOSS_IMEX1)
+    OSSM_SDL64_FWD(OSSM_DLINOSS_IMEX2)
+    OSSM_SDL64_FWD(OSSM_DLINOSS_IM)
+    OSSM_SDL64_FWD(OSSM_DLINOSS_EX)
+#undef OSSM_SDL64_FWD
+  }
+  return launch_check("sdl64_forward_kernel");
+}
+
+int ossm_sdlinoss_backward_f64(int variant, const double* A, int64_t a_len, int64_t a_batch,
+                               const double* G, int64_t g_len, int64_t g_batch,
+                               const double* step, int64_t s_len, int64_t s_batch, const void* bu,
+                               const void* states, const void* grad_output, double* grad_A,
+                               double* grad_G, double* grad_step, void* grad_bu, int64_t length,
+                               int64_t batch, int64_t ssm, ossm_stream_t stream_v) {
+  clear_error();
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  const Shape64 shapes[3] = {{A, a_len, a_batch}, {G, g_len, g_batch}, {step, s_len, s_batch}};
+  double* const grads[3] = {grad_A, grad_G, grad_step};
+  if (length == 0 || batch == 0 || ssm == 0) {
+    if (variant < 0 || variant > 3)
+      return set_error(OSSM_ERR_INVALID_ARGUMENT, "Unknown selective D-LinOSS variant code");
+    // nothing to scan: zero parameter gradients (the reference's zeros_like)
+    for (int p = 0; p < 3; ++p) {
+      if (grads[p] == nullptr)
+        return set_error(OSSM_ERR_INVALID_ARGUMENT, "sdlinoss_backward_f64: null pointer");
+      const long long n = shapes[p].la * shapes[p].ba * ssm;
+      if (n <= 0) continue;
+      hipLaunchKernelGGL(sdl64_zero_kernel, dim3(blocks_for(n)), dim3(kBlock64), 0, stream,
+                         grads[p], n);
+      if (int rc = launch_check("sdl64_zero_kernel")) return rc;
+    }
+    return OSSM_OK;
+  }
+  if (int rc = check64(variant, shapes, length, batch, ssm, "sdlinoss_backward_f64")) return rc;
+  if (!bu || !states || !grad_output || !grad_A || !grad_G || !grad_step || !grad_bu)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "sdlinoss_backward_f64: null pointer");
+  const Params64 prm = params64(shapes, length, batch, ssm);
+  const int64_t nc = batch * ssm;
+
+  // gradients summed over batch rows go through a workspace first:
+  // [L, B, M] per element (broadcast over batch only) or [B, M] time sums
+  // (broadcast over both)
+  Grads64 dst{};
+  bool rb[3];
+  size_t offs[3] = {0, 0, 0}, ws_doubles = 0;
+  for (int p = 0; p < 3; ++p) {
+    const bool rt = shapes[p].la == 1 && length > 1;
+    rb[p] = shapes[p].ba == 1 && batch > 1;
+    dst.mode[p] = rt ? 1 : (rb[p] ? 2 : 0);
+    if (rb[p]) {
+      offs[p] = ws_doubles;
+      ws_doubles += static_cast<size_t>(rt ? 1 : length) * nc;
+    }
+  }
+  double* ws = nullptr;
+  if (ws_doubles > 0) {
+    void* raw = nullptr;
+    if (int rc = acquire_workspace(stream, ws_doubles * sizeof(double), &raw)) return rc;
+    ws = static_cast<double*>(raw);
+  }
+  for (int p = 0; p < 3; ++p) dst.out[p] = rb[p] ? ws + offs[p] : grads[p];
+
+  const int n = static_cast<int>(nc), L = static_cast<int>(length);
+  const auto* b = static_cast<const double2*>(bu);
+  const auto* st = static_cast<const double2*>(states);
+  const auto* go = static_cast<const double2*>(grad_output);
+  auto* gi = static_cast<double2*>(grad_bu);
+  switch (variant) {
+#define OSSM_SDL64_BWD(V)                                                                          \
+  case V:                                                                                          \
+    hipLaunchKernelGGL(sdl64_backward_kernel<V>, dim3(blocks_for(n)), dim3(kBlock64), 0, stream, \
+                       prm, b, st, go, gi, dst, L, n);                                             \
+    break;
+    OSSM_SDL64_BWD(OSSM_DLINOSS_IMEX1)
+    OSSM_SDL64_BWD(OSSM_DLINOSS_IMEX2)
+    OSSM_SDL64_BWD(OSSM_DLINOSS_IM)
+    OSSM_SDL64_BWD(OSSM_DLINOSS_EX)
+#undef OSSM_SDL64_BWD
+  }
+  if (int rc = launch_check("sdl64_backward_kernel")) return rc;
+  for (int p = 0; p < 3; ++p) {
+    if (!rb[p]) continue;
+    // [R=B rows] summed: (L or 1) outputs of M columns each
+    const long long rows_out = dst.mode[p] == 1 ? 1 : length;
+    const long long n_out = rows_out * ssm;
+    hipLaunchKernelGGL(sdl64_rows_sum_kernel, dim3(blocks_for(n_out)), dim3(kBlock64), 0, stream,
+                       dst.out[p], grads[p], n_out, static_cast<int>(batch), static_cast<int>(ssm));
+    if (int rc = launch_check("sdl64_rows_sum_kernel")) return rc;
+  }
+  return OSSM_OK;
+}
+
+}  // extern "C"

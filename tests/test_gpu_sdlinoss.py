@@ -148,8 +148,10 @@ def test_sdlinoss_empty_and_errors(K):
         K.sdlinoss_imex1_forward(dA, dG, dS, to_dev(bu)[0])
     with pytest.raises(RuntimeError, match="optional singleton"):
         K.sdlinoss_imex1_forward(dA[:, :1, :].repeat(1, 3, 1), dG, dS, to_dev(bu))
-    with pytest.raises(RuntimeError, match="complex64"):
+    with pytest.raises(RuntimeError, match="to match bu"):
         K.sdlinoss_imex1_forward(dA, dG, dS, to_dev(bu).to(torch.complex128))
+    with pytest.raises(RuntimeError, match="complex64 or complex128"):
+        K.sdlinoss_imex1_forward(dA, dG, dS, to_dev(bu).real.contiguous())
     with pytest.raises(RuntimeError, match="grad_output must match"):
         K.sdlinoss_imex1_backward(dA, dG, dS, to_dev(bu), out, to_dev(go)[:2])
 
@@ -166,3 +168,67 @@ def test_sdlinoss_repeatable(K):
     for a, b, name in zip(g1, g2, NAMES):
         a, b = to_np(a), to_np(b)
         assert_close(a, b, 1e-5, 1e-6 * max(1.0, float(np.abs(b).max())), name)
+
+
+def _to64(args):
+    return [x.astype(np.float64) if x.dtype == np.float32 else x.astype(np.complex128) for x in args]
+
+
+# fp64 bound: both sides compute the same recurrence in double; the oracle's
+# sums over broadcast axes run in another order
+RTOL64, ATOL64 = 1e-10, 1e-12
+
+
+@pytest.mark.parametrize("tag", ["full", "bcast_t", "bcast_b", "m", "lm", "bm"])
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_sdlinoss_complex128_vs_oracle(K, variant, tag):
+    """complex128 inputs (float64 parameters) run on the device, as the
+    reference's kernels dispatch them (sdlinoss_imex1_cuda.cu:232, 271)."""
+    import torch
+
+    L, B, M = 150, 3, 37
+    A, G, S, bu, go = _to64(sdl_inputs(variant, tag, L, B, M, seed=11 + len(tag)))
+    announce(f"sdlinoss c128 {variant} {tag} L={L} B={B} M={M}")
+    dA, dG, dS, dbu = to_dev(A), to_dev(G), to_dev(S), to_dev(bu)
+    states = getattr(K, f"sdlinoss_{variant}_forward")(dA, dG, dS, dbu)
+    assert states.dtype == torch.complex128
+    grads = getattr(K, f"sdlinoss_{variant}_backward")(dA, dG, dS, dbu, states, to_dev(go))
+    ref_st = oracle.sdlinoss_forward(variant, A, G, S, bu)
+    scale = max(1.0, float(np.abs(ref_st).max()))
+    assert_close(to_np(states), ref_st, RTOL64, ATOL64 * scale, "c128 states")
+    ref_g = oracle.sdlinoss_backward(variant, A, G, S, bu, ref_st, go)
+    for got, ref, name in zip(grads, ref_g, NAMES):
+        got = to_np(got)
+        assert got.dtype == ref.dtype and got.shape == ref.shape, name
+        assert_close(got, ref, RTOL64, ATOL64 * max(1.0, float(np.abs(ref).max())), f"c128 {name}")
+
+
+def test_sdlinoss_complex128_golden_and_edges(K):
+    """The reference kernel vectors in fp64 (bound set by their fp32
+    arithmetic), one-step and single-channel shapes, and empty inputs."""
+    import torch
+
+    with np.load(GOLDEN / "sdl_kernel_vectors.npz") as z:
+        v = {k: z[k] for k in z.files}
+    for variant in VARIANTS:
+        k = f"{variant}_full"
+        A, G, S, bu, go = _to64([v[f"{k}_A"], v[f"{k}_G"], v[f"{k}_step"], v["bu"], v["grad"]])
+        announce(f"sdlinoss c128 golden {k}")
+        st = getattr(K, f"sdlinoss_{variant}_forward")(to_dev(A), to_dev(G), to_dev(S), to_dev(bu))
+        scale = float(np.abs(v[f"{k}_states"]).max())
+        assert_close(to_np(st), v[f"{k}_states"], RTOL, ATOL * max(1.0, scale), "c128 golden states")
+    for L, B, M in ((1, 1, 1), (2, 1, 65), (7, 4, 1)):
+        A, G, S, bu, go = _to64(sdl_inputs("im", "full", L, B, M, seed=L + B + M))
+        announce(f"sdlinoss c128 im L={L} B={B} M={M}")
+        st = K.sdlinoss_im_forward(to_dev(A), to_dev(G), to_dev(S), to_dev(bu))
+        grads = K.sdlinoss_im_backward(to_dev(A), to_dev(G), to_dev(S), to_dev(bu), st, to_dev(go))
+        ref_st = oracle.sdlinoss_forward("im", A, G, S, bu)
+        assert_close(to_np(st), ref_st, RTOL64, ATOL64, "c128 edge states")
+        for got, ref, name in zip(grads, oracle.sdlinoss_backward("im", A, G, S, bu, ref_st, go), NAMES):
+            assert_close(to_np(got), ref, RTOL64, ATOL64 * max(1.0, float(np.abs(ref).max())), name)
+    A, G, S, bu, go = _to64(sdl_inputs("imex1", "m", 3, 2, 4, seed=2))
+    dA, dG, dS = to_dev(A), to_dev(G), to_dev(S)
+    out = K.sdlinoss_imex1_forward(dA, dG, dS, to_dev(bu)[:0])
+    assert tuple(out.shape) == (0, 2, 4, 2) and out.dtype == torch.complex128
+    grads = K.sdlinoss_imex1_backward(dA, dG, dS, to_dev(bu)[:0], out, to_dev(go)[:0])
+    assert all(g.dtype == torch.float64 and float(g.abs().sum()) == 0.0 for g in grads[:3])
