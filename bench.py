@@ -60,13 +60,62 @@ def _backlog(torch, ms: float = 25.0) -> None:
     torch.cuda._sleep(int(ms * 1e-3 * 2.4e9))
 
 
+class TimingEvent:
+    """A HIP event for timing only, created with hipEventDisableSystemFence.
+
+    A default event's record performs a system-scope release, i.e. writes back
+    the dirty L2 lines the preceding kernel left (tens of MB of outputs here);
+    that cost ~5 us per record at config 2's shapes and fell inside the interval
+    being measured.  This one only takes the timestamp once the stream reaches
+    it; it is never used to synchronise anything.  Recorded on torch's current
+    stream, which is the stream the library's kernels are launched on."""
+
+    _hip = None
+    _DISABLE_SYSTEM_FENCE = 0x20000000
+
+    def __init__(self, torch):
+        import ctypes
+
+        if TimingEvent._hip is None:
+            lib = Path(torch.__file__).resolve().parent / "lib" / "libamdhip64.so"
+            TimingEvent._hip = ctypes.CDLL(str(lib) if lib.exists() else "libamdhip64.so")
+        self._torch = torch
+        self._ev = ctypes.c_void_p()
+        self._check(TimingEvent._hip.hipEventCreateWithFlags(ctypes.byref(self._ev),
+                                                            ctypes.c_uint(self._DISABLE_SYSTEM_FENCE)),
+                    "hipEventCreateWithFlags")
+
+    @staticmethod
+    def _check(rc: int, what: str) -> None:
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with HIP error {rc}")
+
+    def record(self) -> None:
+        import ctypes
+
+        stream = ctypes.c_void_p(self._torch.cuda.current_stream().cuda_stream)
+        self._check(TimingEvent._hip.hipEventRecord(self._ev, stream), "hipEventRecord")
+
+    def elapsed_time(self, end: "TimingEvent") -> float:
+        """Milliseconds from this event to `end` (both completed)."""
+        import ctypes
+
+        ms = ctypes.c_float()
+        self._check(TimingEvent._hip.hipEventElapsedTime(ctypes.byref(ms), self._ev, end._ev),
+                    "hipEventElapsedTime")
+        return float(ms.value)
+
+    def __del__(self):
+        if TimingEvent._hip is not None and getattr(self, "_ev", None):
+            TimingEvent._hip.hipEventDestroy(self._ev)
+
+
 def _ev_time(torch, fn, reps: int, warm: int) -> float:
     """Median milliseconds of fn() between two events on the current stream."""
     for _ in range(warm):
         fn()
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(reps)]
+    evs = [(TimingEvent(torch), TimingEvent(torch)) for _ in range(reps)]
     _backlog(torch)
     for e0, e1 in evs:
         e0.record()
@@ -407,14 +456,13 @@ def main() -> int:
         bwd(a, gam, dt, bu, st, go)
     torch.cuda.synchronize()
 
-    # Per-launch events on every EVERY-th step of the timed region (an event
-    # record costs ~3 us of GPU time; three on every step added ~9 us to a
-    # 172 us step), the whole region between `start` and `end`.
+    # Per-launch events on every EVERY-th step of the timed region (even a
+    # fence-free record costs ~1.5 us of GPU time: three on every step made a
+    # step 177.5 instead of 173 us), the whole region between `start` and `end`.
     every = max(1, args.events_every)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-           torch.cuda.Event(enable_timing=True)) if i % every == 0 else None
+    ev = [(TimingEvent(torch), TimingEvent(torch), TimingEvent(torch)) if i % every == 0 else None
           for i in range(args.steps)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start, end = TimingEvent(torch), TimingEvent(torch)
     torch.cuda.synchronize()
     _backlog(torch, ms=max(25.0, 0.5 * args.steps))
     start.record()
