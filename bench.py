@@ -106,8 +106,9 @@ class TimingEvent:
         return float(ms.value)
 
     def __del__(self):
-        if TimingEvent._hip is not None and getattr(self, "_ev", None):
-            TimingEvent._hip.hipEventDestroy(self._ev)
+        hip = type(self)._hip  # the class itself, not the module global (None at shutdown)
+        if hip is not None and getattr(self, "_ev", None):
+            hip.hipEventDestroy(self._ev)
 
 
 def _ev_time(torch, fn, reps: int, warm: int) -> float:
