@@ -84,6 +84,24 @@ def _check_layer_args(inputs: Tensor, B: Tensor, C: Tensor, D: Tensor, a: Tensor
     return batch, length, hidden, ssm
 
 
+def _check_on_gpu(tensors, hidden: int, ssm: int) -> None:
+    if any(t.dtype != torch.float32 for t in tensors):
+        raise RuntimeError("the fused D-LinOSS layer computes in float32; got "
+                           + ", ".join(str(t.dtype) for t in tensors))
+    if not all(t.is_cuda for t in tensors) or len({t.device for t in tensors}) != 1:
+        raise RuntimeError("the fused D-LinOSS layer needs every tensor on one GPU")
+    if hidden > _LAYER_MAX or ssm > _LAYER_MAX:
+        raise RuntimeError(f"the fused D-LinOSS layer supports hidden_dim and ssm_size up to "
+                           f"{_LAYER_MAX}, got {hidden} and {ssm}")
+
+
+def _check_carries(carries: Tensor, batch: int, length: int, ssm: int, device) -> None:
+    want = (batch, -(-length // _CHUNK), ssm, 4)
+    if tuple(carries.shape) != want or carries.dtype != torch.float32 or \
+            not carries.is_contiguous() or carries.device != device:
+        raise RuntimeError(f"carries must be a contiguous float32 {want} tensor on {device}")
+
+
 def dlinoss_layer_forward(variant: str, inputs: Tensor, B: Tensor, C: Tensor, D: Tensor,
                           a_diag: Tensor, g_diag: Tensor, step: Tensor,
                           carries: Optional[Tensor] = None) -> Tensor:
@@ -96,23 +114,13 @@ def dlinoss_layer_forward(variant: str, inputs: Tensor, B: Tensor, C: Tensor, D:
         raise ValueError(f"Unknown D-LinOSS variant '{variant}'.")
     batch, length, hidden, ssm = _check_layer_args(inputs, B, C, D, a_diag, g_diag, step)
     tensors = (inputs, B, C, D, a_diag, g_diag, step)
-    if any(t.dtype != torch.float32 for t in tensors):
-        raise RuntimeError("the fused D-LinOSS layer computes in float32; got "
-                           + ", ".join(str(t.dtype) for t in tensors))
-    if not all(t.is_cuda for t in tensors) or len({t.device for t in tensors}) != 1:
-        raise RuntimeError("the fused D-LinOSS layer needs every tensor on one GPU")
-    if hidden > _LAYER_MAX or ssm > _LAYER_MAX:
-        raise RuntimeError(f"the fused D-LinOSS layer supports hidden_dim and ssm_size up to "
-                           f"{_LAYER_MAX}, got {hidden} and {ssm}")
+    _check_on_gpu(tensors, hidden, ssm)
     u, Bc, Cc, Dc, a, g, s = (t.contiguous() for t in tensors)
     out = torch.empty_like(u)
     if out.numel() == 0:
         return out
     if carries is not None:
-        want = (batch, -(-length // _CHUNK), ssm, 4)
-        if tuple(carries.shape) != want or carries.dtype != torch.float32 or \
-                not carries.is_contiguous() or carries.device != u.device:
-            raise RuntimeError(f"carries must be a contiguous float32 {want} tensor on {u.device}")
+        _check_carries(carries, batch, length, ssm, u.device)
     lib = _lib.load()
     with torch.cuda.device(u.device):
         _lib.check(lib.ossm_dlinoss_layer_forward(
@@ -129,17 +137,25 @@ def dlinoss_layer_backward(variant: str, inputs: Tensor, grad_output: Tensor, B:
     grad_g, grad_step)`` from the forward's ``carries``.  One kernel for
     grad_inputs and the scan's parameter gradients; grad_B and grad_C are GEMMs
     over the grad_bu and conj(x) it returns, grad_D a sum."""
+    variant = variant.lower()
+    if variant not in _VARIANTS:
+        raise ValueError(f"Unknown D-LinOSS variant '{variant}'.")
     batch, length, hidden, ssm = _check_layer_args(inputs, B, C, D, a_diag, g_diag, step)
-    u, go, Bc, Cc, Dc, a, g, s = (t.contiguous() for t in
-                                  (inputs, grad_output, B, C, D, a_diag, g_diag, step))
+    if grad_output.shape != inputs.shape:
+        raise RuntimeError(f"grad_output must have the inputs' shape {tuple(inputs.shape)}, "
+                           f"got {tuple(grad_output.shape)}")
+    tensors = (inputs, grad_output, B, C, D, a_diag, g_diag, step)
+    _check_on_gpu(tensors, hidden, ssm)
+    u, go, Bc, Cc, Dc, a, g, s = (t.contiguous() for t in tensors)
     dev = u.device
+    _check_carries(carries, batch, length, ssm, dev)
     gu = torch.empty_like(u)
     gbu = torch.empty((batch, length, ssm, 2), dtype=torch.float32, device=dev)
     xq = torch.empty_like(gbu)
     ga, gg, gs = (torch.empty(ssm, dtype=torch.float32, device=dev) for _ in range(3))
     with torch.cuda.device(dev):
         _lib.check(_lib.load().ossm_dlinoss_layer_backward(
-            _VARIANTS[variant.lower()], u.data_ptr(), go.data_ptr(), Bc.data_ptr(), Cc.data_ptr(),
+            _VARIANTS[variant], u.data_ptr(), go.data_ptr(), Bc.data_ptr(), Cc.data_ptr(),
             Dc.data_ptr(), a.data_ptr(), g.data_ptr(), s.data_ptr(), carries.data_ptr(),
             gu.data_ptr(), gbu.data_ptr(), xq.data_ptr(), ga.data_ptr(), gg.data_ptr(),
             gs.data_ptr(), batch, length, hidden, ssm, _lib.stream_of(u)))

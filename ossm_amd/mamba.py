@@ -47,6 +47,15 @@ def _rows(t: Tensor, name: str) -> Tuple[Tensor, int]:
     return t, int(t.stride(1)) if L > 0 else C
 
 
+def _param(t: Optional[Tensor], name: str) -> Optional[Tensor]:
+    """A parameter the kernels read as contiguous float32 on the device."""
+    if t is None:
+        return None
+    if t.dtype != torch.float32 or not t.is_cuda:
+        raise RuntimeError(f"{name} must be a float32 GPU tensor (got {t.dtype} on {t.device})")
+    return t.contiguous()
+
+
 def _same_device(*ts: Optional[Tensor]) -> None:
     devs = {t.device for t in ts if t is not None}
     if len(devs) > 1:
@@ -57,8 +66,10 @@ def _same_device(*ts: Optional[Tensor]) -> None:
 def _conv_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
     x, ld = _rows(x, "x")
     Bz, L, D = x.shape
-    w = weight.reshape(D, -1).contiguous()
-    b = bias.contiguous() if bias is not None else None
+    w = _param(weight, "conv weight").reshape(D, -1)
+    b = _param(bias, "conv bias")
+    if b is not None and tuple(b.shape) != (D,):
+        raise RuntimeError(f"conv bias must have shape ({D},), got {tuple(b.shape)}")
     _same_device(x, w, b)
     out = torch.empty((Bz, L, D), dtype=torch.float32, device=x.device)
     if out.numel() == 0:
@@ -84,7 +95,7 @@ class ConvSiluFn(torch.autograd.Function):
         x, weight, bias = ctx.saved_tensors
         x, ld = _rows(x, "x")
         Bz, L, D = x.shape
-        w = weight.reshape(D, -1).contiguous()
+        w = _param(weight, "conv weight").reshape(D, -1)
         K = w.size(1)
         go = grad_out.contiguous()
         gx = torch.empty((Bz, L, D), dtype=torch.float32, device=x.device)
@@ -131,8 +142,8 @@ class MambaScanFn(torch.autograd.Function):
             raise RuntimeError("selective_scan_mamba: inconsistent shapes "
                                f"u {tuple(u.shape)} dt {tuple(dt.shape)} A {tuple(A.shape)} "
                                f"B {tuple(Bm.shape)} C {tuple(Cm.shape)}")
-        Ac = A.contiguous()
-        bias = dt_bias.contiguous() if dt_bias is not None else None
+        Ac = _param(A, "A")
+        bias = _param(dt_bias, "dt_bias")
         _same_device(u, dt, Ac, Bm, Cm, z, bias)
         out = torch.empty((Bz, L, D), dtype=torch.float32, device=u.device)
         raw = torch.empty_like(out) if z is not None else None

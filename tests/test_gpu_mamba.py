@@ -228,6 +228,11 @@ def test_mamba_edge_cases_and_errors(M):
     assert out.shape == x.shape and torch.isfinite(out).all()
     with pytest.raises(RuntimeError, match="inconsistent shapes"):
         M.selective_scan_mamba(x, torch.randn(2, 5, 7, device="cuda"), A, Bm, Cm)
+    # parameters of another dtype are rejected, not reinterpreted
+    with pytest.raises(RuntimeError, match="conv weight must be a float32 GPU tensor"):
+        M.mamba_conv_silu(x, torch.randn(8, 1, 4, device="cuda", dtype=torch.float64))
+    with pytest.raises(RuntimeError, match="A must be a float32 GPU tensor"):
+        M.selective_scan_mamba(x, torch.randn(2, 5, 8, device="cuda"), A.double(), Bm, Cm)
     # empty sequence
     e = torch.zeros(2, 0, 8, device="cuda")
     assert M.mamba_conv_silu(e, torch.randn(8, 1, 4, device="cuda")).shape == e.shape

@@ -139,3 +139,25 @@ def test_layer_module_interface():
     bound = 1.0 / math.sqrt(4)
     assert float(layer.B.detach().abs().max()) <= bound
     assert float(layer.C.detach().abs().max()) <= 1.0 / math.sqrt(6)
+
+
+def test_layer_entry_argument_checks():
+    """The public fused-layer entries reject what the kernels cannot read before
+    any device work: an unknown variant, a grad_output of another shape, and
+    tensors that are not float32 on one GPU."""
+    from ossm_amd import layers
+
+    b, L, H, P = 2, 5, 4, 3
+    args = [torch.zeros(b, L, H), torch.zeros(P, H, 2), torch.zeros(H, P, 2), torch.zeros(H),
+            torch.ones(P), torch.ones(P), torch.ones(P)]
+    carries = torch.zeros(b, 1, P, 4)
+    with pytest.raises(ValueError, match="Unknown D-LinOSS variant"):
+        layers.dlinoss_layer_backward("rk4", args[0], args[0], *args[1:], carries)
+    with pytest.raises(RuntimeError, match="grad_output must have the inputs' shape"):
+        layers.dlinoss_layer_backward("imex1", args[0], args[0][:, :2], *args[1:], carries)
+    with pytest.raises(RuntimeError, match="one GPU"):
+        layers.dlinoss_layer_backward("imex1", args[0], args[0], *args[1:], carries)
+    with pytest.raises(RuntimeError, match="one GPU"):
+        layers.dlinoss_layer_forward("imex1", *args)
+    with pytest.raises(RuntimeError, match="float32"):
+        layers.dlinoss_layer_forward("imex1", args[0].double(), *args[1:])

@@ -85,3 +85,13 @@ def test_mixer_module_interface():
     with pytest.raises(RuntimeError, match="GPU only"):
         m(torch.zeros(1, 3, 16))
     assert m(torch.zeros(1, 0, 16)).shape == (1, 0, 16)
+
+
+def test_mixer_entries_reject_what_the_kernels_cannot_read():
+    from ossm_amd.mamba import mamba_conv_silu, selective_scan_mamba
+
+    x = torch.zeros(1, 4, 8)
+    with pytest.raises(RuntimeError, match="float32 GPU tensor"):
+        mamba_conv_silu(x, torch.zeros(8, 1, 4))
+    with pytest.raises(RuntimeError, match="float32 GPU tensor"):
+        selective_scan_mamba(x, x, torch.zeros(8, 2), torch.zeros(1, 4, 2), torch.zeros(1, 4, 2))
