@@ -434,8 +434,9 @@ def main() -> int:
 
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: every box in this run has "
-                          "a single MI355X and the scans need no collectives; DESIGN.md "
-                          "describes how the path would shard", "n_gpus": args.gpus}))
+                          "a single MI355X, and the scans need no collectives (they would shard "
+                          "over batch rows and channels, each GPU scanning its own share)",
+                          "n_gpus": args.gpus}))
         return 2
     if args.calibrate_copy:
         return calibrate_copy()
