@@ -327,14 +327,14 @@ __global__ __launch_bounds__(W * kWave) void diag_forward_kernel(
 #pragma unroll
       for (int i = 0; i < T; ++i) {
         s = cx_step(lam, s, x[i]);
-        group_row(out, t0 + i, nc, g)[lane] = s;
+        stream_store(&group_row(out, t0 + i, nc, g)[lane], s);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < T; ++i) {
         if (t0 + i < L) {
           s = cx_step(lam, s, x[i]);
-          group_row(out, t0 + i, nc, g)[lane] = s;
+          stream_store(&group_row(out, t0 + i, nc, g)[lane], s);
         }
       }
     }
@@ -432,7 +432,7 @@ __global__ __launch_bounds__(W * kWave) void diag_backward_kernel(
 #pragma unroll
       for (int i = T - 1; i >= 0; --i) {
         const V gt = cx_add(go[i], y);
-        group_row(gin, t0 + i, nc, g)[lane] = gt;
+        stream_store(&group_row(gin, t0 + i, nc, g)[lane], gt);
         acc = cx_acc_conj(acc, gt, sp[i]);
         y = cx_mul(lamc, gt);
       }
@@ -441,7 +441,7 @@ __global__ __launch_bounds__(W * kWave) void diag_backward_kernel(
       for (int i = T - 1; i >= 0; --i) {
         if (t0 + i < L) {
           const V gt = cx_add(go[i], y);
-          group_row(gin, t0 + i, nc, g)[lane] = gt;
+          stream_store(&group_row(gin, t0 + i, nc, g)[lane], gt);
           acc = cx_acc_conj(acc, gt, sp[i]);
           y = cx_mul(lamc, gt);
         }

@@ -194,7 +194,7 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_forward_kernel(
 #pragma unroll
       for (int i = 0; i < T; ++i) {
         s = Model::step(k, s, x[i]);
-        group_row(out, t0 + i, nc, g)[lane] = s;
+        stream_store(&group_row(out, t0 + i, nc, g)[lane], s);
       }
     } else {
 #pragma unroll
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_forward_kernel(
         const long long t = t0 + i;
         if (t < L) {
           s = Model::step(k, s, x[i]);
-          group_row(out, t, nc, g)[lane] = s;
+          stream_store(&group_row(out, t, nc, g)[lane], s);
         }
       }
     }
@@ -401,7 +401,7 @@ __device__ __forceinline__ void bwd_back(BwdBuf<Model, T>& b, const BwdTicket& k
         const int i = h * Q + q;
         if (live(i)) {
           const float4 mu = Model::mu(y, b.go[i]);
-          group_row(gin, k.t0 + i, nc, k.g)[lane] = Model::grad_input(cf, mu);
+          stream_store(&group_row(gin, k.t0 + i, nc, k.g)[lane], Model::grad_input(cf, mu));
           if constexpr (Model::kRecompute)
             Model::accumulate(acc, mu, sp_lds[(H > 1 ? q : i) * kWave + lane], b.x[i]);
           else

@@ -333,14 +333,14 @@ __global__ __launch_bounds__(W * kWave) void sdl_forward_kernel(
 #pragma unroll
       for (int i = 0; i < T; ++i) {
         s = sdl_step<V>(k[i], s, x[i]);
-        row_of(out, t0 + i, nc, g)[lane] = s;
+        stream_store(&row_of(out, t0 + i, nc, g)[lane], s);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < T; ++i) {
         if (t0 + i < L) {
           s = sdl_step<V>(k[i], s, x[i]);
-          row_of(out, t0 + i, nc, g)[lane] = s;
+          stream_store(&row_of(out, t0 + i, nc, g)[lane], s);
         }
       }
     }
@@ -530,11 +530,11 @@ __global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
         float gp[3];
         rho = sdl_grad_step<V>(pa[i], pg[i], ps[i], inv[i], s_sp[w][i][lane], x[i], lam, gbu,
                                gp[0], gp[1], gp[2]);
-        row_of(gin, t, nc, g)[lane] = gbu;
+        stream_store(&row_of(gin, t, nc, g)[lane], gbu);
 #pragma unroll
         for (int p = 0; p < 3; ++p) {
           if (go_prm.tsum & (1 << p)) psum[p] += gp[p];
-          else row_of(go_prm.p[p], t, nc, g)[lane] = gp[p];
+          else stream_store(&row_of(go_prm.p[p], t, nc, g)[lane], gp[p]);
         }
       }
     }
