@@ -79,6 +79,8 @@ __global__ __launch_bounds__(kBlock64) void sdl64_forward_kernel(Params64 prm,
   if (ch >= nc) return;
   const int m = ch % prm.M;
   double wr = 0.0, wi = 0.0, xr = 0.0, xi = 0.0;
+  // unrolled so that the loads of several steps are in flight at once
+#pragma unroll 8
   for (int t = 0; t < L; ++t) {
     const double a = at64(prm.v[0], t, ch, m), g = at64(prm.v[1], t, ch, m);
     const double dt = dt64(at64(prm.v[2], t, ch, m));
