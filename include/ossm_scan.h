@@ -42,7 +42,7 @@ enum {
 
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
-/* Library ABI version (bumped on any change of the entry points; currently 9). */
+/* Library ABI version (bumped on any change of the entry points; currently 10). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -176,6 +176,20 @@ int ossm_sdlinoss_backward(int variant, const float* A, int64_t a_len, int64_t a
  * walks the sequence (the backward reads every step's previous state from states);
  * broadcast gradients are summed in a fixed order.
  */
+/*
+ * complex128 forms of ossm_linoss_forward / ossm_linoss_backward: the reference's
+ * device kernel dispatches complex128 too (linoss_scan_cuda.cu:139).  m_ij [P],
+ * b_seq, states, grad_output, grad_b [L,B,P,2], grad_m [P,2,2], all c128.  One lane
+ * per channel walks the sequence; grad_m is summed over batch rows in order.
+ */
+int ossm_linoss_forward_f64(const void* m11, const void* m12, const void* m21, const void* m22,
+                            const void* b_seq, void* states, int64_t length, int64_t batch,
+                            int64_t ssm, ossm_stream_t stream);
+int ossm_linoss_backward_f64(const void* m11, const void* m12, const void* m21, const void* m22,
+                             const void* states, const void* grad_output, void* grad_m,
+                             void* grad_b, int64_t length, int64_t batch, int64_t ssm,
+                             ossm_stream_t stream);
+
 int ossm_sdlinoss_forward_f64(int variant, const double* A, int64_t a_len, int64_t a_batch,
                               const double* G, int64_t g_len, int64_t g_batch, const double* step,
                               int64_t s_len, int64_t s_batch, const void* bu, void* states,

@@ -186,6 +186,12 @@ def dlinoss_ex_backward(a_diag, g_diag, step, bu, states, grad_output):
 
 
 # --------------------------------------------------------------------- LinOSS
+_LINOSS_ENTRIES = {
+    torch.complex64: ("ossm_linoss_forward", "ossm_linoss_backward"),
+    torch.complex128: ("ossm_linoss_forward_f64", "ossm_linoss_backward_f64"),
+}
+
+
 def linoss_scan(m11, m12, m21, m22, b_seq):
     """linoss_scan.cpp:115-146."""
     output = torch.empty_like(b_seq)
@@ -201,12 +207,15 @@ def linoss_scan(m11, m12, m21, m22, b_seq):
     length, batch, ssm, two = b_seq.shape
     _check(two == 2, "b_seq must have shape (length, batch, ssm_size, 2)")
     _on_device(m11, m12, m21, m22, b_seq)
+    # complex64 and complex128, as the reference's device kernel dispatches
+    # (AT_DISPATCH_COMPLEX_TYPES, linoss_scan_cuda.cu:139)
+    _check(b_seq.dtype in _LINOSS_ENTRIES,
+           f"linoss_scan: b_seq must be complex64 or complex128, got {b_seq.dtype}")
     for m in (m11, m12, m21, m22):
         _check(m.dim() == 1 and m.size(0) == ssm, "Coefficient tensors must have shape (ssm_size,)")
-        _check(m.dtype == torch.complex64, "linoss_scan HIP kernel supports complex64 only")
-    _check(b_seq.dtype == torch.complex64, "linoss_scan HIP kernel supports complex64 only")
+        _check(m.dtype == b_seq.dtype, "Coefficient tensors must have b_seq's dtype")
     with torch.cuda.device(b_seq.device):
-        _lib.check(_lib.load().ossm_linoss_forward(
+        _lib.check(getattr(_lib.load(), _LINOSS_ENTRIES[b_seq.dtype][0])(
             m11.data_ptr(), m12.data_ptr(), m21.data_ptr(), m22.data_ptr(), b_seq.data_ptr(),
             output.data_ptr(), length, batch, ssm, _lib.stream_of(b_seq)))
     return output
@@ -225,15 +234,15 @@ def linoss_scan_backward(m11, m12, m21, m22, states, grad_output):
     grad_m = torch.empty((ssm, 2, 2), dtype=states.dtype, device=states.device)
     _check(states.is_cuda, "linoss_scan_backward: HIP path needs device tensors")
     _on_device(m11, m12, m21, m22, states, grad_output)
+    _check(states.dtype in _LINOSS_ENTRIES and grad_output.dtype == states.dtype,
+           "linoss_scan_backward: states and grad_output must be both complex64 or both complex128")
     for m in (m11, m12, m21, m22):
-        _check(m.dim() == 1 and m.size(0) == ssm and m.is_contiguous()
-               and m.dtype == torch.complex64, "Coefficient tensors must be contiguous complex64 (ssm_size,)")
+        _check(m.dim() == 1 and m.size(0) == ssm and m.is_contiguous() and m.dtype == states.dtype,
+               "Coefficient tensors must be contiguous (ssm_size,) of the states' dtype")
     _check(states.is_contiguous() and grad_output.is_contiguous(),
            "states and grad_output must be contiguous")
-    _check(states.dtype == torch.complex64 and grad_output.dtype == torch.complex64,
-           "linoss_scan_backward HIP kernel supports complex64 only")
     with torch.cuda.device(states.device):
-        _lib.check(_lib.load().ossm_linoss_backward(
+        _lib.check(getattr(_lib.load(), _LINOSS_ENTRIES[states.dtype][1])(
             m11.data_ptr(), m12.data_ptr(), m21.data_ptr(), m22.data_ptr(), states.data_ptr(),
             grad_output.data_ptr(), grad_m.data_ptr(), grad_b.data_ptr(), length, batch, ssm,
             _lib.stream_of(states)))

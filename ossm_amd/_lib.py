@@ -50,6 +50,10 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_int, _fp, _c_int64, _c_int64, _fp, _c_int64, _c_int64, _fp, _c_int64, _c_int64,
          _vp, _vp, _vp, _fp, _fp, _fp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_linoss_forward_f64": (
+        ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_linoss_backward_f64": (
+        ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
     "ossm_sdlinoss_forward_f64": (
         ctypes.c_int,
         [ctypes.c_int, _fp, _c_int64, _c_int64, _fp, _c_int64, _c_int64, _fp, _c_int64, _c_int64,

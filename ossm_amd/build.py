@@ -24,7 +24,7 @@ OBJDIR = PKG / "_build"
 LIB = LIBDIR / "libossm_scan.so"
 
 SOURCES = ["runtime.cpp", "oscillator_scan.hip", "selective_scan.hip", "sdlinoss_scan.hip",
-           "diag_scan.hip", "dlinoss_layer.hip", "mamba_conv.hip", "sdlinoss_f64.hip"]
+           "diag_scan.hip", "dlinoss_layer.hip", "mamba_conv.hip", "scan_f64.hip"]
 ARCH = "gfx950"
 
 

@@ -136,7 +136,7 @@ void release_unlaunched(hipStream_t stream, uint64_t n_workgroups) {
 
 extern "C" {
 
-int ossm_abi_version(void) { return 9; }
+int ossm_abi_version(void) { return 10; }
 
 const char* ossm_last_error(void) { return ossm::g_last_error.c_str(); }
 

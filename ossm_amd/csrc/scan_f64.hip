@@ -1,13 +1,13 @@
-// Selective D-LinOSS in complex128 (float64 parameters) on gfx950.  The
-// reference's device kernels dispatch complex128 as well as complex64
-// (sdlinoss_imex1_cuda.cu:232, 271, and the imex2 / im / ex siblings), so the
-// drop-in has to serve both.  fp64 is the accuracy path, not the hot one:
-// one lane per channel walks the sequence, forward in time for the states and
-// in reverse for the adjoint, and consecutive lanes own consecutive channels,
-// so every load and store of a wave is one contiguous run.
+// The complex128 scans on gfx950 that the reference's device kernels dispatch
+// besides complex64: selective D-LinOSS (sdlinoss_imex1_cuda.cu:232, 271, and
+// the imex2 / im / ex siblings) and the LinOSS scan (linoss_scan_cuda.cu:139).
+// fp64 is the accuracy path, not the hot one: one lane per channel walks the
+// sequence, forward in time for the states and in reverse for the adjoint, and
+// consecutive lanes own consecutive channels, so every load and store of a
+// wave is one contiguous run.
 //
-// Recurrence and chain rule are the complex64 kernels' (sdlinoss_<v>.cpp
-// forward kernels, backward kernels sdlinoss_imex1.cpp:186-220,
+// Selective D-LinOSS: recurrence and chain rule of the complex64 kernels
+// (sdlinoss_<v>.cpp forward kernels, backward kernels sdlinoss_imex1.cpp:186-220,
 // sdlinoss_imex2.cpp:178-221, sdlinoss_im.cpp:176-225,
 // sdlinoss_ex.cpp:163-189), in double, with the division by S kept as a
 // division:
@@ -16,6 +16,11 @@
 // Parameter gradients broadcast over time are summed over time in the lane
 // (sequential, fixed order); those broadcast over batch rows are summed over
 // the rows afterwards by one lane per output element, also in a fixed order.
+//
+// LinOSS: s_t = M s_{t-1} + b_t with a complex 2x2 M per oscillator
+// (linoss_scan.cpp:11-96); backward g_t = grad_t + M^H g_{t+1}, grad_b_t = g_t,
+// grad_M_ij = sum over (b, t) of g_i,t conj(s_j,t-1) (linoss.py:83-151), summed
+// over time in the lane and over batch rows afterwards.
 
 #include <hip/hip_runtime.h>
 
@@ -205,6 +210,78 @@ __global__ __launch_bounds__(kBlock64) void sdl64_zero_kernel(double* __restrict
   if (i < n) p[i] = 0.0;
 }
 
+// ---- LinOSS ---------------------------------------------------------------------
+__device__ __forceinline__ double2 cmul(double2 a, double2 b) {
+  return make_double2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+// conj(a) * b
+__device__ __forceinline__ double2 cmulc(double2 a, double2 b) {
+  return make_double2(a.x * b.x + a.y * b.y, a.x * b.y - a.y * b.x);
+}
+__device__ __forceinline__ double2 cadd(double2 a, double2 b) { return make_double2(a.x + b.x, a.y + b.y); }
+
+struct Lin64 {
+  const double2* m[4];  // m11, m12, m21, m22, [P] each
+  int P;
+};
+
+// states [L, nc, 2] and b [L, nc, 2], channel ch = b P + p
+__global__ __launch_bounds__(kBlock64) void lin64_forward_kernel(Lin64 mp,
+                                                                 const double2* __restrict__ b,
+                                                                 double2* __restrict__ states,
+                                                                 int L, int nc) {
+  const int ch = static_cast<int>(blockIdx.x) * kBlock64 + static_cast<int>(threadIdx.x);
+  if (ch >= nc) return;
+  const int p = ch % mp.P;
+  const double2 m11 = mp.m[0][p], m12 = mp.m[1][p], m21 = mp.m[2][p], m22 = mp.m[3][p];
+  double2 s0 = make_double2(0.0, 0.0), s1 = s0;
+#pragma unroll 8
+  for (int t = 0; t < L; ++t) {
+    const size_t e = 2 * (static_cast<size_t>(t) * nc + ch);
+    const double2 n0 = cadd(cadd(cmul(m11, s0), cmul(m12, s1)), b[e]);
+    const double2 n1 = cadd(cadd(cmul(m21, s0), cmul(m22, s1)), b[e + 1]);
+    s0 = n0;
+    s1 = n1;
+    states[e] = s0;
+    states[e + 1] = s1;
+  }
+}
+
+// grad_b [L, nc, 2]; per-channel sums of g_i conj(s_j,t-1) into part[ch][4]
+// (i, j row-major), summed over batch rows afterwards
+__global__ __launch_bounds__(kBlock64) void lin64_backward_kernel(
+    Lin64 mp, const double2* __restrict__ states, const double2* __restrict__ gout,
+    double2* __restrict__ gb, double2* __restrict__ part, int L, int nc) {
+  const int ch = static_cast<int>(blockIdx.x) * kBlock64 + static_cast<int>(threadIdx.x);
+  if (ch >= nc) return;
+  const int p = ch % mp.P;
+  const double2 m11 = mp.m[0][p], m12 = mp.m[1][p], m21 = mp.m[2][p], m22 = mp.m[3][p];
+  double2 g0 = make_double2(0.0, 0.0), g1 = g0;  // adjoint of s_{t+1}, then of s_t
+  double2 acc[4] = {g0, g0, g0, g0};
+  for (int t = L - 1; t >= 0; --t) {
+    const size_t e = 2 * (static_cast<size_t>(t) * nc + ch);
+    // g_t = grad_t + M^H g_{t+1}
+    const double2 h0 = cadd(gout[e], cadd(cmulc(m11, g0), cmulc(m21, g1)));
+    const double2 h1 = cadd(gout[e + 1], cadd(cmulc(m12, g0), cmulc(m22, g1)));
+    g0 = h0;
+    g1 = h1;
+    gb[e] = g0;
+    gb[e + 1] = g1;
+    if (t > 0) {
+      const size_t q = e - 2 * static_cast<size_t>(nc);
+      const double2 sp0 = states[q], sp1 = states[q + 1];
+      // g_i conj(s_j) = conj(conj(g_i) s_j)
+      const double2 a00 = cmulc(g0, sp0), a01 = cmulc(g0, sp1), a10 = cmulc(g1, sp0), a11 = cmulc(g1, sp1);
+      acc[0] = cadd(acc[0], make_double2(a00.x, -a00.y));
+      acc[1] = cadd(acc[1], make_double2(a01.x, -a01.y));
+      acc[2] = cadd(acc[2], make_double2(a10.x, -a10.y));
+      acc[3] = cadd(acc[3], make_double2(a11.x, -a11.y));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) part[4 * static_cast<size_t>(ch) + k] = acc[k];
+}
+
 unsigned blocks_for(long long n) { return static_cast<unsigned>((n + kBlock64 - 1) / kBlock64); }
 
 struct Shape64 {
@@ -363,6 +440,67 @@ int ossm_sdlinoss_backward_f64(int variant, const double* A, int64_t a_len, int6
     if (int rc = launch_check("sdl64_rows_sum_kernel")) return rc;
   }
   return OSSM_OK;
+}
+
+int ossm_linoss_forward_f64(const void* m11, const void* m12, const void* m21, const void* m22,
+                            const void* b_seq, void* states, int64_t length, int64_t batch,
+                            int64_t ssm, ossm_stream_t stream_v) {
+  clear_error();
+  if (length < 0 || batch < 0 || ssm < 0)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "linoss_forward_f64: negative size");
+  if (length == 0 || batch == 0 || ssm == 0) return OSSM_OK;
+  if (length > INT_MAX / 2 || batch * ssm > INT_MAX / 2 || length * batch * ssm > (int64_t(1) << 40))
+    return set_error(OSSM_ERR_UNSUPPORTED, "linoss_forward_f64: size exceeds 32-bit indexing");
+  if (!m11 || !m12 || !m21 || !m22 || !b_seq || !states)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "linoss_forward_f64: null pointer");
+  const Lin64 mp{{static_cast<const double2*>(m11), static_cast<const double2*>(m12),
+                  static_cast<const double2*>(m21), static_cast<const double2*>(m22)},
+                 static_cast<int>(ssm)};
+  const int nc = static_cast<int>(batch * ssm);
+  hipLaunchKernelGGL(lin64_forward_kernel, dim3(blocks_for(nc)), dim3(kBlock64), 0,
+                     static_cast<hipStream_t>(stream_v), mp, static_cast<const double2*>(b_seq),
+                     static_cast<double2*>(states), static_cast<int>(length), nc);
+  return launch_check("lin64_forward_kernel");
+}
+
+int ossm_linoss_backward_f64(const void* m11, const void* m12, const void* m21, const void* m22,
+                             const void* states, const void* grad_output, void* grad_m,
+                             void* grad_b, int64_t length, int64_t batch, int64_t ssm,
+                             ossm_stream_t stream_v) {
+  clear_error();
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  if (length < 0 || batch < 0 || ssm < 0)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "linoss_backward_f64: negative size");
+  if (length > INT_MAX / 2 || batch * ssm > INT_MAX / 2 || length * batch * ssm > (int64_t(1) << 40))
+    return set_error(OSSM_ERR_UNSUPPORTED, "linoss_backward_f64: size exceeds 32-bit indexing");
+  if (!grad_m) return set_error(OSSM_ERR_INVALID_ARGUMENT, "linoss_backward_f64: null pointer");
+  const long long n_m = 8 * ssm;  // [P, 2, 2] complex128 as doubles
+  if (length == 0 || batch == 0 || ssm == 0) {
+    if (n_m > 0) {
+      hipLaunchKernelGGL(sdl64_zero_kernel, dim3(blocks_for(n_m)), dim3(kBlock64), 0, stream,
+                         static_cast<double*>(grad_m), n_m);
+      return launch_check("sdl64_zero_kernel");
+    }
+    return OSSM_OK;
+  }
+  if (!m11 || !m12 || !m21 || !m22 || !states || !grad_output || !grad_b)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "linoss_backward_f64: null pointer");
+  const Lin64 mp{{static_cast<const double2*>(m11), static_cast<const double2*>(m12),
+                  static_cast<const double2*>(m21), static_cast<const double2*>(m22)},
+                 static_cast<int>(ssm)};
+  const int nc = static_cast<int>(batch * ssm);
+  void* raw = nullptr;
+  if (int rc = acquire_workspace(stream, static_cast<size_t>(nc) * 4 * sizeof(double2), &raw)) return rc;
+  hipLaunchKernelGGL(lin64_backward_kernel, dim3(blocks_for(nc)), dim3(kBlock64), 0, stream, mp,
+                     static_cast<const double2*>(states), static_cast<const double2*>(grad_output),
+                     static_cast<double2*>(grad_b), static_cast<double2*>(raw),
+                     static_cast<int>(length), nc);
+  if (int rc = launch_check("lin64_backward_kernel")) return rc;
+  // [B rows][P * 8 doubles] summed over the rows, in order
+  hipLaunchKernelGGL(sdl64_rows_sum_kernel, dim3(blocks_for(n_m)), dim3(kBlock64), 0, stream,
+                     static_cast<const double*>(raw), static_cast<double*>(grad_m), n_m,
+                     static_cast<int>(batch), static_cast<int>(n_m));
+  return launch_check("sdl64_rows_sum_kernel");
 }
 
 }  // extern "C"

@@ -207,3 +207,31 @@ def test_linoss_forward_backward_vs_oracle(K, shape):
     assert_parity(to_np(gb), rgb, tgb, RTOL, ATOL, "grad_b")
     assert_parity(to_np(gm), rgm, tgm, RTOL, _param_atol(tgm), "grad_m")
     no_device_errors()
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (37, 3, 5), (600, 2, 96)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_linoss_complex128_vs_oracle(K, shape):
+    """complex128 LinOSS runs on the device, as the reference's kernel dispatches
+    it (linoss_scan_cuda.cu:139): forward and the native backward against the
+    fp64 oracle at rtol 1e-10."""
+    import torch
+
+    L, B, P = shape
+    ms, b, go = _linoss_inputs(L, B, P, seed=3 * L + P)
+    ms = [m.astype(np.complex128) for m in ms]
+    b, go = b.astype(np.complex128), go.astype(np.complex128)
+    announce(f"linoss c128 L={L} B={B} P={P}")
+    st = K.linoss_scan(*[to_dev(m) for m in ms], to_dev(b))
+    assert st.dtype == torch.complex128
+    ref = oracle.linoss_forward(*ms, b)
+    scale = max(1.0, float(np.abs(ref).max()))
+    assert_close(to_np(st), ref, 1e-10, 1e-12 * scale, "c128 states")
+    gm, gb = K.linoss_scan_backward(*[to_dev(m) for m in ms], st, to_dev(go))
+    rgm, rgb = oracle.linoss_backward(*ms, ref, go)
+    assert_close(to_np(gb), rgb, 1e-10, 1e-12 * max(1.0, float(np.abs(rgb).max())), "c128 grad_b")
+    assert_close(to_np(gm), rgm, 1e-10, 1e-12 * max(1.0, float(np.abs(rgm).max())), "c128 grad_m")
+    # mixed dtypes are rejected, not reinterpreted
+    with pytest.raises(RuntimeError, match="b_seq's dtype"):
+        K.linoss_scan(*[to_dev(m.astype(np.complex64)) for m in ms], to_dev(b))
+    no_device_errors()
