@@ -128,8 +128,9 @@ class SdlinossFn(torch.autograd.Function):
 
 def run_sdlinoss(variant: str, a_diag: Tensor, g_diag: Tensor, step: Tensor, bu: Tensor) -> Tensor:
     """x = states[..., 1] of the selective D-LinOSS recurrence (reference
-    run_sdlinoss, _sdlinoss_scan.py:382-452).  bu is [L, B, M] complex64 on the
-    device; A, G, step are float32 shaped (M,), (L, M), (B, M) or (L|1, B|1, M);
+    run_sdlinoss, _sdlinoss_scan.py:382-452).  bu is [L, B, M] complex64 (float32
+    parameters) or complex128 (float64 parameters) on the device; A, G, step are
+    shaped (M,), (L, M), (B, M) or (L|1, B|1, M);
     their gradients come back in the same shapes (summed over broadcast axes)."""
     variant = variant.lower()
     if variant not in SUPPORTED_VARIANTS:
