@@ -19,8 +19,8 @@ One JSON line is printed.  Besides the contract fields:
                 mean event-timed duration, vs 8 TB/s); ``traffic`` is the
                 measured HBM bytes per launch from rocprofv3 FETCH_SIZE /
                 WRITE_SIZE (profiles/dlinoss_imex1_config2_pmc.json) or null
-  cpu_baseline  the reference's own CPU kernels (oracle/_ref, compiled from the
-                reference sources) on the same workload on this host's cores
+  cpu_baseline  the C restatement of the reference's CPU kernels (oracle/) on
+                the same workload on this host's cores
   detail        per-direction figures, the other BASELINE configs and the fused
                 layers (D-LinOSS layer, Mamba mixer)
 
@@ -197,32 +197,22 @@ def _cpu_model() -> str:
 
 
 def cpu_baseline(L, B, P, budget_s=12.0):
-    """The reference's own CPU kernels (oracle/_ref) on the full config-2
-    workload, else the C restatement (oracle/)."""
+    """The C restatement of the reference's CPU kernels (oracle/, kind "port")
+    on the full config-2 workload, on this host's cores.  Its agreement with
+    the reference's own CPU kernels is pinned by tests/golden/ref_kernel_vectors.npz."""
     import torch
 
     try:
         import oracle
     except Exception as exc:  # pragma: no cover
         return {"error": f"oracle unavailable: {exc}"}
-    ref = oracle.reference_module()
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    torch.set_num_threads(threads)
-    a, gam, dt, bu, go = (x.cpu() for x in dlinoss_inputs(torch, L, B, P, torch.device("cpu")))
-    if ref is None:
-        kind = "port"
+    a, gam, dt, bu, go = (x.cpu().numpy() for x in dlinoss_inputs(torch, L, B, P, torch.device("cpu")))
+    threads = oracle.num_threads()
 
-        def run():
-            st = oracle.dlinoss_forward("imex1", a.numpy(), gam.numpy(), dt.numpy(), bu.numpy())
-            oracle.dlinoss_backward("imex1", a.numpy(), gam.numpy(), dt.numpy(), bu.numpy(), st,
-                                    go.numpy())
-        threads = oracle.num_threads()
-    else:
-        kind = "reference"
+    def run():
+        st = oracle.dlinoss_forward("imex1", a, gam, dt, bu)
+        oracle.dlinoss_backward("imex1", a, gam, dt, bu, st, go)
 
-        def run():
-            st = ref.dlinoss_imex1_forward(a, gam, dt, bu)
-            ref.dlinoss_imex1_backward(a, gam, dt, bu, st, go)
     for _ in range(2):
         run()
     times = []
@@ -232,16 +222,15 @@ def cpu_baseline(L, B, P, budget_s=12.0):
         run()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    src = ("reference CPU kernels compiled from src/ossm/csrc (oracle/_ref)" if kind == "reference"
-           else "C restatement of the reference CPU kernels (oracle/)")
     return {
         "value": L * B * P / med,
         "unit": "state-steps/s",
         "cores": threads,
-        "kind": kind,
+        "kind": "port",
         "sample": (f"the full config-2 workload (D-LinOSS imex1 fwd+bwd, B={B} L={L} P={P}), "
                    f"median of {len(times)} runs after 2 warmups ({sum(times):.1f} s of CPU work), "
-                   f"{src}; the reference parallelises over P only (at most {P} threads)"),
+                   "C restatement of the reference CPU kernels (oracle/, OpenMP over P as the "
+                   f"reference's parallel_for, so at most {P} threads do work)"),
         "seconds_per_step": med,
         "cpu_model": _cpu_model(),
     }
@@ -405,6 +394,46 @@ def _detail_configs(torch, K, dev, reps=10):
     return out
 
 
+CASES = ("c1_linoss_im_fwd", "c3_selective_fp32", "c4_shape_selective_fp32", "c4_selective_bf16",
+         "c5_dlinoss_fwd_long")
+
+
+def run_case(name: str, steps: int, warmup: int) -> int:
+    """One BASELINE config alone (``--case``): `warmup` untimed then `steps`
+    event-timed passes of its launches, for rocprofv3 runs that should hold only
+    that config's kernels.  Prints one JSON line with the median times."""
+    import torch
+
+    from ossm_amd import _kernels as K
+    from ossm_amd import _lib
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    out = {"case": name, "steps": steps, "warmup": warmup}
+    if name == "c1_linoss_im_fwd":
+        m11, m12, m21, m22, b_seq = linoss_im_inputs(torch, 1024, 8, 64, dev)
+        out["fwd_ms"] = _ev_time(torch, lambda: K.linoss_scan(m11, m12, m21, m22, b_seq), steps, warmup)
+    elif name == "c5_dlinoss_fwd_long":
+        a, gam, dt, bu, _ = dlinoss_inputs(torch, 65536, 4, 256, dev, H=64, seed=5)
+        out["fwd_ms"] = _ev_time(torch, lambda: K.dlinoss_imex1_forward(a, gam, dt, bu), steps, warmup)
+    else:
+        shape = (256, 128, 200, 16) if name == "c3_selective_fp32" else (16, 1536, 2048, 16)
+        xs = selective_inputs(torch, *shape, dev)
+        if name == "c4_selective_bf16":
+            xs = tuple(x if x.dim() == 2 else x.bfloat16() for x in xs)
+            fwd, bwd = K.selective_scan_cuda_bf16, K.selective_scan_cuda_bf16_backward
+        else:
+            fwd, bwd = K.selective_scan_cuda, K.selective_scan_cuda_backward
+        u, dts, A, Bm, Cm, z, go = xs
+        res = fwd(u, dts, A, Bm, Cm, z)
+        out["fwd_ms"] = _ev_time(torch, lambda: fwd(u, dts, A, Bm, Cm, z), steps, warmup)
+        out["bwd_ms"] = _ev_time(torch, lambda: bwd(go, u, dts, A, Bm, Cm, z, res[1], res[2], 16),
+                                 steps, warmup)
+    out["device_error_bits"] = _lib.device_error_bits(dev)
+    print(json.dumps(out), flush=True)
+    return 0 if out["device_error_bits"] == 0 else 1
+
+
 def calibrate_copy(nbytes=1 << 30, reps=5):
     """A plain device copy of `nbytes`, for scaling FETCH_SIZE / WRITE_SIZE."""
     import torch
@@ -428,6 +457,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-detail", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--case", choices=CASES,
+                    help="run only this BASELINE config (--steps timed passes), for profiling")
     ap.add_argument("--events-every", type=int, default=4,
                     help="record per-launch events on every N-th timed step")
     args = ap.parse_args()
@@ -440,6 +471,8 @@ def main() -> int:
         return 2
     if args.calibrate_copy:
         return calibrate_copy()
+    if args.case:
+        return run_case(args.case, args.steps, args.warmup)
 
     import torch
 

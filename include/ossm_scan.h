@@ -20,6 +20,13 @@
  * buffer of tagged look-back records (never cleared between calls) and one
  * plain workspace for partial sums; both grow on demand (hipMalloc outside
  * the kernels, after synchronising the stream) and live until process exit.
+ *
+ * Threads and graphs: a call holds its (device, stream) from the launch
+ * bookkeeping (look-back tag, ticket base, workspace) through its last
+ * launch, so calls from several host threads on one stream are safe and
+ * reach the stream whole.  A call whose stream is being captured into a HIP
+ * graph returns OSSM_ERR_UNSUPPORTED before enqueuing anything: the tag and
+ * ticket base are chosen on the host per call, and a replay would reuse them.
  */
 #ifndef OSSM_SCAN_H
 #define OSSM_SCAN_H
@@ -42,7 +49,8 @@ enum {
 
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
-/* Library ABI version (bumped on any change of the entry points; currently 10). */
+/* Library ABI version (bumped on any change of the entry points or their
+   behaviour; currently 11). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */

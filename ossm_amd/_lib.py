@@ -9,6 +9,7 @@ there is no fallback path behind this module.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 from typing import Optional
 
@@ -124,11 +125,25 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+# OSSM_CHECK_DEVICE_ERRORS=1: after every successful call, synchronise the
+# current stream and raise RuntimeError if a kernel raised a protocol error
+# bit (a look-back wait that gave up, an out-of-range ticket).  Off by
+# default: the check costs a stream synchronisation per call.
+CHECK_DEVICE_ERRORS = os.environ.get("OSSM_CHECK_DEVICE_ERRORS", "0") not in ("", "0")
+
+
 def check(rc: int) -> None:
-    """Raise RuntimeError (the reference's TORCH_CHECK surface) on a nonzero status."""
+    """Raise RuntimeError (the reference's TORCH_CHECK surface) on a nonzero status.
+    Called inside the ``torch.cuda.device`` block of the call it checks."""
     if rc != 0:
         msg = load().ossm_last_error().decode(errors="replace")
         raise RuntimeError(msg or f"ossm_scan call failed with status {rc}")
+    if CHECK_DEVICE_ERRORS:
+        bits = device_error_bits()
+        if bits:
+            raise RuntimeError(f"ossm_scan: a kernel raised device error bits {bits:#x} "
+                               "(1 = look-back wait gave up, 2 = out-of-range ticket); "
+                               "its outputs are not valid")
 
 
 def ptr(t: Optional[torch.Tensor]) -> Optional[int]:

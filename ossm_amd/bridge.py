@@ -9,7 +9,10 @@ kernel bridges (the L2 layer above ``ossm._kernels``):
   (_sdlinoss_scan.py:286-452), same save/return semantics.
 * LinOSS: ``try_run_scan`` (_linoss_scan.py:44-63) plus ``LinossScanFn`` whose
   backward is the native ``linoss_scan_backward`` instead of the reference's
-  Python loop (models/linoss.py:83-151).
+  Python loop (models/linoss.py:83-151), and ``LinossMatrixScanFn`` /
+  ``run_associative_scan``, the same with the reference's ``_LinossScanFn``
+  interface (``a_matrix`` [P, 2, 2], ``b_seq``), which ``ossm_amd.linoss.LinOSSLayer``
+  uses and which can replace ``_LinossScanFn`` under the reference's layer.
 * Selective scan: ``try_selective_scan`` and ``SelectiveScanFn``
   (_selective_scan.py:127-297): fp32 only, the no-grad shortcut, the
   ``(out, chunk_states, raw_out)`` forward saved for the backward.
@@ -39,7 +42,8 @@ from . import _kernels
 __all__ = [
     "has_kernels", "extension_error", "run_dlinoss", "run_dlinoss_imex1", "DlinossFn",
     "run_sdlinoss", "SdlinossFn",
-    "try_run_scan", "LinossScanFn", "try_selective_scan", "SelectiveScanFn",
+    "try_run_scan", "LinossScanFn", "LinossMatrixScanFn", "run_associative_scan",
+    "try_selective_scan", "SelectiveScanFn",
     "DiagScanFn", "try_run_lru_scan", "try_run_s5_scan",
 ]
 
@@ -161,6 +165,47 @@ class LinossScanFn(torch.autograd.Function):
         grad_m, grad_b = _kernels.linoss_scan_backward(m11, m12, m21, m22, states,
                                                        grad_states.contiguous())
         return grad_m[:, 0, 0], grad_m[:, 0, 1], grad_m[:, 1, 0], grad_m[:, 1, 1], grad_b
+
+
+_M_ENTRIES = ((0, 0), (0, 1), (1, 0), (1, 1))
+
+
+class LinossMatrixScanFn(torch.autograd.Function):
+    """The reference's ``_LinossScanFn(a_matrix, b_seq)`` interface
+    (models/linoss.py:57-151) on the device, backward included: ``a_matrix`` is
+    [P, 2, 2] (real or complex), ``b_seq`` [L, B, P, 2] complex.  The gradient
+    of ``a_matrix`` is the reference's ``sum_b grad_i conj(s_j,t-1)``, kept
+    complex for a complex ``a_matrix`` and reduced to its real part for a real
+    one (linoss.py:122-132).  Sequences of length 0 or 1 are returned as given,
+    as the reference does (s_0 = b_0)."""
+
+    @staticmethod
+    def forward(ctx, a_matrix: Tensor, b_seq: Tensor) -> Tensor:  # type: ignore[override]
+        if b_seq.size(0) <= 1:
+            ctx.save_for_backward(a_matrix, b_seq)
+            return b_seq
+        b_seq = b_seq.contiguous()
+        ms = [a_matrix[:, i, j].to(dtype=b_seq.dtype).contiguous() for i, j in _M_ENTRIES]
+        states = _kernels.linoss_scan(*ms, b_seq)
+        ctx.save_for_backward(a_matrix, states)
+        return states
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):  # type: ignore[override]
+        a_matrix, states = ctx.saved_tensors
+        if grad_output.size(0) == 0:
+            return torch.zeros_like(a_matrix), grad_output
+        ms = [a_matrix[:, i, j].to(dtype=grad_output.dtype).contiguous() for i, j in _M_ENTRIES]
+        grad_m, grad_b = _kernels.linoss_scan_backward(*ms, states.contiguous(),
+                                                       grad_output.contiguous())
+        if not torch.is_complex(a_matrix):
+            grad_m = grad_m.real
+        return grad_m.to(a_matrix.dtype), grad_b
+
+
+def run_associative_scan(a_matrix: Tensor, b_seq: Tensor) -> Tensor:
+    """reference ``_run_associative_scan`` (models/linoss.py:154-157)."""
+    return LinossMatrixScanFn.apply(a_matrix, b_seq)
 
 
 def try_run_scan(m11: Tensor, m12: Tensor, m21: Tensor, m22: Tensor, b_seq: Tensor) -> Tensor:

@@ -517,6 +517,8 @@ int check_diag_sizes(int64_t L, int64_t B, int64_t P, const char* what) {
 template <class R>
 int diag_forward_impl(const R* lam_re, const R* lam_im, const void* b_seq, void* out, int64_t L,
                       int64_t B, int64_t P, hipStream_t stream) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   static const DiagTile tile = diag_tile(DiagDefaults<R>::kEnvFwd, DiagDefaults<R>::kFwd);
   const int64_t nc = B * P;
   const int64_t CL = int64_t(tile.T) * tile.W;
@@ -527,7 +529,7 @@ int diag_forward_impl(const R* lam_re, const R* lam_im, const void* b_seq, void*
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * CxOf<R>::kWords * nc * sizeof(unsigned long long);
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(stream, rec_bytes, total, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
   bool launched = false;
 #define OSSM_LAUNCH_DIAG_FWD(TT, WW)                                                              \
   if (!launched && tile.T == TT && tile.W == WW) {                                                \
@@ -545,11 +547,11 @@ int diag_forward_impl(const R* lam_re, const R* lam_im, const void* b_seq, void*
   }
 #undef OSSM_LAUNCH_DIAG_FWD
   if (!launched) {
-    release_unlaunched(stream, total);
+    release_unlaunched(call, total);
     return set_error(OSSM_ERR_UNSUPPORTED, std::string(DiagDefaults<R>::kEnvFwd) + " names no built tile");
   }
   if (int rc = launch_check("diag_forward_kernel")) {
-    release_unlaunched(stream, total);
+    release_unlaunched(call, total);
     return rc;
   }
   return OSSM_OK;
@@ -559,6 +561,8 @@ template <class R>
 int diag_backward_impl(const R* lam_re, const R* lam_im, const void* states, const void* gout,
                        R* grad_lambda, void* grad_b, int64_t L, int64_t B, int64_t P,
                        hipStream_t stream) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   static const DiagTile tile = diag_tile(DiagDefaults<R>::kEnvBwd, DiagDefaults<R>::kBwd);
   const int64_t nc = B * P;
   const int64_t CL = int64_t(tile.T) * tile.W;
@@ -570,11 +574,11 @@ int diag_backward_impl(const R* lam_re, const R* lam_im, const void* states, con
   const size_t part_bytes =
       (static_cast<size_t>(n_chunks) * 2 * nc * sizeof(R) + 255) & ~static_cast<size_t>(255);
   void* ws = nullptr;
-  if (int rc = acquire_workspace(stream, part_bytes, &ws)) return rc;
+  if (int rc = acquire_workspace(call, part_bytes, &ws)) return rc;
   R* partials = static_cast<R*>(ws);
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(stream, rec_bytes, total, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
   const ZeroFill zero{{reinterpret_cast<float*>(grad_lambda), nullptr, nullptr},
                       static_cast<int>(2 * P * (sizeof(R) / sizeof(float)))};
   bool launched = false;
@@ -595,11 +599,11 @@ int diag_backward_impl(const R* lam_re, const R* lam_im, const void* states, con
   }
 #undef OSSM_LAUNCH_DIAG_BWD
   if (!launched) {
-    release_unlaunched(stream, total);
+    release_unlaunched(call, total);
     return set_error(OSSM_ERR_UNSUPPORTED, std::string(DiagDefaults<R>::kEnvBwd) + " names no built tile");
   }
   if (int rc = launch_check("diag_backward_kernel")) {
-    release_unlaunched(stream, total);
+    release_unlaunched(call, total);
     return rc;
   }
   return launch_column_sums<2>(partials, P, B, n_chunks, DiagEpilogue<R>{grad_lambda}, stream);

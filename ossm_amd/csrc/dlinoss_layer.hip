@@ -660,6 +660,8 @@ constexpr size_t kMaxLds = 160 * 1024;
 
 template <int V>
 int launch_layer_bwd(LayerBwdArgs args, float* ga, float* gg, float* gs, hipStream_t stream) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   using Model = Dlinoss<V>;
   constexpr int NS = Model::kSums;
   const int64_t n_wg = static_cast<int64_t>(args.Bsz) * args.n_chunks;
@@ -668,23 +670,24 @@ int launch_layer_bwd(LayerBwdArgs args, float* ga, float* gg, float* gs, hipStre
   void* payload = nullptr;
   LaunchSync sync{};
   void* ws = nullptr;
-  if (int rc = acquire_workspace(stream, static_cast<size_t>(args.n_chunks) * NS * nc * sizeof(float), &ws))
+  if (int rc = acquire_workspace(call, static_cast<size_t>(args.n_chunks) * NS * nc * sizeof(float), &ws))
     return rc;
   args.partials = static_cast<float*>(ws);
   args.zero = ZeroFill{{ga, gg, gs}, args.P};
-  if (int rc = acquire_scratch(stream, rec_bytes, n_wg, &payload, &sync)) return rc;
   const bool vec = args.H % 4 == 0 && args.P % 4 == 0 && aligned16(args.u) && aligned16(args.gy) &&
                    aligned16(args.Bw) && aligned16(args.Cw);
   auto kern = vec ? dlinoss_layer_bwd_kernel<V, true> : dlinoss_layer_bwd_kernel<V, false>;
   const size_t lds = layer_bwd_lds_bytes(args.H, args.P);
+  // before the ticket reservation: a failure here leaves nothing reserved
   if (int rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(lds)),
                          "hipFuncSetAttribute"))
     return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, n_wg, &payload, &sync)) return rc;
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(n_wg)), dim3(kLayerThreads), lds, stream, args,
                      static_cast<unsigned long long*>(payload), sync);
-  if (hipPeekAtLastError() != hipSuccess) release_unlaunched(stream, n_wg);
+  if (hipPeekAtLastError() != hipSuccess) release_unlaunched(call, n_wg);
   if (int rc = launch_check("dlinoss_layer_bwd_kernel")) return rc;
   if (args.P == 0) return OSSM_OK;
   const typename Model::Params prm{args.a, args.g, args.dt, args.P};
@@ -700,24 +703,27 @@ size_t layer_lds_bytes(int64_t H, int64_t P) {
 
 template <int V>
 int launch_layer(const LayerArgs& args, hipStream_t stream) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   const int64_t n_wg = static_cast<int64_t>(args.Bsz) * args.n_chunks;
   const int64_t nc = static_cast<int64_t>(args.Bsz) * args.P;
   const size_t rec_bytes = static_cast<size_t>(args.n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(stream, rec_bytes, n_wg, &payload, &sync)) return rc;
   const bool vec = args.H % 4 == 0 && args.P % 4 == 0 && aligned16(args.u) && aligned16(args.Bw) &&
                    aligned16(args.Cw);
   auto kern = vec ? dlinoss_layer_fwd_kernel<V, true> : dlinoss_layer_fwd_kernel<V, false>;
   const size_t lds = layer_lds_bytes(args.H, args.P);
+  // before the ticket reservation: a failure here leaves nothing reserved
   if (int rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(lds)),
                          "hipFuncSetAttribute"))
     return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, n_wg, &payload, &sync)) return rc;
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(n_wg)), dim3(kLayerThreads), lds, stream, args,
                      static_cast<unsigned long long*>(payload), sync);
-  if (hipPeekAtLastError() != hipSuccess) release_unlaunched(stream, n_wg);
+  if (hipPeekAtLastError() != hipSuccess) release_unlaunched(call, n_wg);
   return launch_check("dlinoss_layer_fwd_kernel");
 }
 

@@ -343,6 +343,8 @@ int ossm_mamba_conv_backward(const float* x, int64_t ld_x, const float* weight, 
   clear_error();
   if (int rc = check_conv(batch, length, dim, width, ld_x, "mamba_conv_backward")) return rc;
   hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   if (dim > 0 && (batch == 0 || length == 0)) {
     if (!grad_weight) return set_error(OSSM_ERR_INVALID_ARGUMENT, "mamba_conv_backward: null pointer");
     if (int rc = zero(grad_weight, dim * width, stream)) return rc;
@@ -354,7 +356,7 @@ int ossm_mamba_conv_backward(const float* x, int64_t ld_x, const float* weight, 
   const int n_spans = static_cast<int>((length + kBwdSpan - 1) / kBwdSpan);
   const int64_t R = batch * n_spans;
   void* ws = nullptr;
-  if (int rc = acquire_workspace(stream, static_cast<size_t>(R * (width + 1) * dim) * sizeof(float), &ws))
+  if (int rc = acquire_workspace(call, static_cast<size_t>(R * (width + 1) * dim) * sizeof(float), &ws))
     return rc;
   ConvArgs a{x, weight, bias, grad_out, grad_x, static_cast<float*>(ws), grad_weight, grad_bias,
              static_cast<int>(batch), static_cast<int>(length), static_cast<int>(dim),

@@ -507,6 +507,8 @@ Tile parse_tile(const char* env, Tile dflt) {
 template <class Model>
 int launch_forward(const typename Model::Params& prm, const void* in, void* out, int64_t L,
                    int64_t nc, hipStream_t stream) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   static const Tile tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{16, 8, 1, 1});
   const int64_t CL = int64_t(tile.T) * tile.W;
   const int64_t n_chunks = (L + CL - 1) / CL;
@@ -516,7 +518,7 @@ int launch_forward(const typename Model::Params& prm, const void* in, void* out,
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(stream, rec_bytes, n_chunks * n_groups, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, n_chunks * n_groups, &payload, &sync)) return rc;
   const dim3 grid(static_cast<unsigned>(n_chunks * n_groups));
   bool launched = false;
 #define OSSM_LAUNCH_FWD(TT, WW, OO)                                                           \
@@ -531,11 +533,11 @@ int launch_forward(const typename Model::Params& prm, const void* in, void* out,
   OSSM_FWD_TILES(OSSM_LAUNCH_FWD)
 #undef OSSM_LAUNCH_FWD
   if (!launched) {
-    release_unlaunched(stream, n_chunks * n_groups);
+    release_unlaunched(call, n_chunks * n_groups);
     return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_FWD names no built tile");
   }
   if (int rc = launch_check("osc_forward_kernel")) {
-    release_unlaunched(stream, n_chunks * n_groups);
+    release_unlaunched(call, n_chunks * n_groups);
     return rc;
   }
   return OSSM_OK;
@@ -549,6 +551,8 @@ template <class Model>
 int launch_backward(const typename Model::Params& prm, const void* in, const void* states,
                     const void* gout, void* gin, float* out0, float* out1, float* out2, int64_t L,
                     int64_t B, int64_t P, hipStream_t stream) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   static const Tile tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{16, 8, 1, 1});
   constexpr int NS = Model::kSums;
   const int64_t nc = B * P;
@@ -561,12 +565,12 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   const size_t part_bytes =
       (static_cast<size_t>(n_chunks) * NS * nc * sizeof(float) + 255) & ~static_cast<size_t>(255);
   void* ws = nullptr;
-  if (int rc = acquire_workspace(stream, part_bytes, &ws)) return rc;
+  if (int rc = acquire_workspace(call, part_bytes, &ws)) return rc;
   ParamReduce red{static_cast<float*>(ws)};
   const int64_t total = n_chunks * n_groups;
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(stream, rec_bytes, total, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
   const ZeroFill zero{{out0, out1, out2}, static_cast<int>(Model::kOutsPerColumn * P)};
   bool launched = false;
 #define OSSM_LAUNCH_BWD(TT, WW, OO, HH)                                                          \
@@ -582,7 +586,7 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
                        static_cast<int>(n_chunks), static_cast<unsigned long long*>(payload),    \
                        sync);                                                                    \
     if (int rc = launch_check("osc_backward_kernel")) {                                          \
-      release_unlaunched(stream, total);                                                       \
+      release_unlaunched(call, total);                                                       \
       return rc;                                                                                 \
     }                                                                                            \
     launched = true;                                                                             \
@@ -590,7 +594,7 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   OSSM_BWD_TILES(OSSM_LAUNCH_BWD)
 #undef OSSM_LAUNCH_BWD
   if (!launched) {
-    release_unlaunched(stream, total);
+    release_unlaunched(call, total);
     return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_BWD names no built tile");
   }
   return launch_column_sums<NS>(red.partials, P, B, n_chunks,

@@ -3,6 +3,7 @@
 
 #include <cstdlib>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <utility>
 
@@ -25,9 +26,24 @@ struct Workspace {
   size_t bytes = 0;
 };
 
-std::mutex g_mu;
-std::map<std::pair<int, hipStream_t>, Scratch> g_scratch;
-std::map<std::pair<int, hipStream_t>, Workspace> g_workspace;
+// Everything the library keeps for one (device, stream).  `call` is held by a
+// StreamCall for the whole of one C call; `scratch` and `workspace` are only
+// touched under it.
+struct StreamState {
+  std::recursive_mutex call;
+  Scratch scratch;
+  Workspace workspace;
+};
+
+std::mutex g_mu;  // guards the map itself (never held while waiting on `call`)
+std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamState>> g_streams;
+
+StreamState& state_of(int dev, hipStream_t stream) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  auto& slot = g_streams[{dev, stream}];
+  if (!slot) slot.reset(new StreamState());
+  return *slot;  // never erased: the address stays valid
+}
 
 }  // namespace
 
@@ -58,18 +74,31 @@ bool scan_order_by_ticket() {
   return by_ticket;
 }
 
-int acquire_scratch(hipStream_t stream, size_t payload_bytes, uint64_t n_workgroups,
+StreamCall::StreamCall(hipStream_t stream) : stream_(stream) {
+  if ((status_ = hip_check(hipGetDevice(&device_), "hipGetDevice"))) return;
+  lock_ = std::unique_lock<std::recursive_mutex>(state_of(device_, stream).call);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(stream, &cap);
+  if (e != hipSuccess || cap != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();  // keep a refused call from surfacing as a later launch error
+    status_ = set_error(OSSM_ERR_UNSUPPORTED,
+                        std::string("ossm_scan: the stream is being captured into a HIP graph (") +
+                            (e != hipSuccess ? hipGetErrorString(e) : "capture active") +
+                            "); the scans choose look-back tags and ticket bases on the host per "
+                            "call, so a replayed graph would reuse them: run the scan eagerly");
+  }
+}
+
+int acquire_scratch(StreamCall& call, size_t payload_bytes, uint64_t n_workgroups,
                     void** payload, LaunchSync* sync) {
+  if (call.status()) return call.status();
   const bool by_ticket = scan_order_by_ticket();
   if (!by_ticket) n_workgroups = 0;  // no ticket is drawn
-  int dev = 0;
-  if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
-  std::lock_guard<std::mutex> lock(g_mu);
-  Scratch& s = g_scratch[{dev, stream}];
+  Scratch& s = state_of(call.device(), call.stream()).scratch;
   if (s.base == nullptr || s.payload < payload_bytes) {
     // Grow: earlier launches on this stream may still read the old buffer.
     if (s.base != nullptr) {
-      if (int rc = hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize")) return rc;
+      if (int rc = hip_check(hipStreamSynchronize(call.stream()), "hipStreamSynchronize")) return rc;
       if (int rc = hip_check(hipFree(s.base), "hipFree(scratch)")) return rc;
       s.base = nullptr;
     }
@@ -99,14 +128,12 @@ int acquire_scratch(hipStream_t stream, size_t payload_bytes, uint64_t n_workgro
   return OSSM_OK;
 }
 
-int acquire_workspace(hipStream_t stream, size_t bytes, void** ptr) {
-  int dev = 0;
-  if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
-  std::lock_guard<std::mutex> lock(g_mu);
-  Workspace& w = g_workspace[{dev, stream}];
+int acquire_workspace(StreamCall& call, size_t bytes, void** ptr) {
+  if (call.status()) return call.status();
+  Workspace& w = state_of(call.device(), call.stream()).workspace;
   if (w.base == nullptr || w.bytes < bytes) {
     if (w.base != nullptr) {
-      if (int rc = hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize")) return rc;
+      if (int rc = hip_check(hipStreamSynchronize(call.stream()), "hipStreamSynchronize")) return rc;
       if (int rc = hip_check(hipFree(w.base), "hipFree(workspace)")) return rc;
       w.base = nullptr;
       w.bytes = 0;
@@ -122,21 +149,17 @@ int acquire_workspace(hipStream_t stream, size_t bytes, void** ptr) {
   return OSSM_OK;
 }
 
-void release_unlaunched(hipStream_t stream, uint64_t n_workgroups) {
-  if (!scan_order_by_ticket()) return;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return;
-  std::lock_guard<std::mutex> lock(g_mu);
-  auto it = g_scratch.find({dev, stream});
-  if (it != g_scratch.end() && it->second.next_ticket >= n_workgroups)
-    it->second.next_ticket -= n_workgroups;
+void release_unlaunched(StreamCall& call, uint64_t n_workgroups) {
+  if (!scan_order_by_ticket() || call.status()) return;
+  Scratch& s = state_of(call.device(), call.stream()).scratch;
+  if (s.next_ticket >= n_workgroups) s.next_ticket -= n_workgroups;
 }
 
 }  // namespace ossm
 
 extern "C" {
 
-int ossm_abi_version(void) { return 10; }
+int ossm_abi_version(void) { return 11; }
 
 const char* ossm_last_error(void) { return ossm::g_last_error.c_str(); }
 
@@ -144,18 +167,24 @@ uint32_t ossm_device_error_bits(ossm_stream_t stream_v) {
   hipStream_t stream = static_cast<hipStream_t>(stream_v);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0xffffffffu;
-  void* base = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(ossm::g_mu);
-    auto it = ossm::g_scratch.find({dev, stream});
-    if (it == ossm::g_scratch.end()) return 0;
-    base = it->second.base;
-  }
+  ossm::StreamState& st = ossm::state_of(dev, stream);
+  std::lock_guard<std::recursive_mutex> hold(st.call);
+  ossm::Scratch& s = st.scratch;
+  if (s.base == nullptr) return 0;
   if (hipStreamSynchronize(stream) != hipSuccess) return 0xffffffffu;
   uint32_t bits = 0;
-  char* err = static_cast<char*>(base) + ossm::kHdrErr;
-  if (hipMemcpy(&bits, err, sizeof(bits), hipMemcpyDeviceToHost) != hipSuccess) return 0xffffffffu;
-  if (bits != 0) (void)hipMemset(err, 0, sizeof(bits));
+  char* base = static_cast<char*>(s.base);
+  if (hipMemcpy(&bits, base + ossm::kHdrErr, sizeof(bits), hipMemcpyDeviceToHost) != hipSuccess)
+    return 0xffffffffu;
+  // With the stream drained, the device counter holds every ticket drawn on
+  // this scratch (each workgroup draws exactly one).  A failed protocol, or a
+  // reservation whose launch never happened, can leave the host's count out of
+  // step with it: take the device's value, so later launches start in step.
+  unsigned long long t = 0;
+  if (hipMemcpy(&t, base + ossm::kHdrTicket, sizeof(t), hipMemcpyDeviceToHost) == hipSuccess &&
+      ossm::scan_order_by_ticket())
+    s.next_ticket = t;
+  if (bits != 0) (void)hipMemset(base + ossm::kHdrErr, 0, sizeof(bits));
   return bits;
 }
 

@@ -366,6 +366,8 @@ int ossm_sdlinoss_backward_f64(int variant, const double* A, int64_t a_len, int6
                                int64_t batch, int64_t ssm, ossm_stream_t stream_v) {
   clear_error();
   hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   const Shape64 shapes[3] = {{A, a_len, a_batch}, {G, g_len, g_batch}, {step, s_len, s_batch}};
   double* const grads[3] = {grad_A, grad_G, grad_step};
   if (length == 0 || batch == 0 || ssm == 0) {
@@ -407,7 +409,7 @@ int ossm_sdlinoss_backward_f64(int variant, const double* A, int64_t a_len, int6
   double* ws = nullptr;
   if (ws_doubles > 0) {
     void* raw = nullptr;
-    if (int rc = acquire_workspace(stream, ws_doubles * sizeof(double), &raw)) return rc;
+    if (int rc = acquire_workspace(call, ws_doubles * sizeof(double), &raw)) return rc;
     ws = static_cast<double*>(raw);
   }
   for (int p = 0; p < 3; ++p) dst.out[p] = rb[p] ? ws + offs[p] : grads[p];
@@ -469,6 +471,8 @@ int ossm_linoss_backward_f64(const void* m11, const void* m12, const void* m21, 
                              ossm_stream_t stream_v) {
   clear_error();
   hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   if (length < 0 || batch < 0 || ssm < 0)
     return set_error(OSSM_ERR_INVALID_ARGUMENT, "linoss_backward_f64: negative size");
   if (length > INT_MAX / 2 || batch * ssm > INT_MAX / 2 || length * batch * ssm > (int64_t(1) << 40))
@@ -490,7 +494,7 @@ int ossm_linoss_backward_f64(const void* m11, const void* m12, const void* m21, 
                  static_cast<int>(ssm)};
   const int nc = static_cast<int>(batch * ssm);
   void* raw = nullptr;
-  if (int rc = acquire_workspace(stream, static_cast<size_t>(nc) * 4 * sizeof(double2), &raw)) return rc;
+  if (int rc = acquire_workspace(call, static_cast<size_t>(nc) * 4 * sizeof(double2), &raw)) return rc;
   hipLaunchKernelGGL(lin64_backward_kernel, dim3(blocks_for(nc)), dim3(kBlock64), 0, stream, mp,
                      static_cast<const double2*>(states), static_cast<const double2*>(grad_output),
                      static_cast<double2*>(grad_b), static_cast<double2*>(raw),

@@ -109,8 +109,9 @@ __device__ __forceinline__ void zero_fill_block(const ZeroFill& z) {
       for (int i = threadIdx.x; i < z.n; i += blockDim.x) z.p[k][i] = 0.f;
 }
 
-// Zero-fill used where the reference returns zero gradients (empty scans);
-// a kernel rather than hipMemsetAsync so the call can sit in a captured graph.
+// Zero-fill used where the reference returns zero gradients (empty scans).
+// A kernel rather than hipMemsetAsync: memset nodes are not trusted inside
+// graphs on this platform, and a caller may capture the surrounding work.
 __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0.f;

@@ -691,6 +691,8 @@ TileTW sdl_tile(const char* env, TileTW dflt) {
 template <int V, int T, int W>
 int sdl_forward_tw(const SdlParams& prm, const void* bu, void* states, int64_t L, int64_t nc,
                    hipStream_t stream) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   const int64_t n_chunks = (L + T * W - 1) / (T * W);
   const int64_t n_groups = (nc + kWave - 1) / kWave;
   if (n_chunks * n_groups > INT_MAX)
@@ -699,14 +701,14 @@ int sdl_forward_tw(const SdlParams& prm, const void* bu, void* states, int64_t L
   void* payload = nullptr;
   LaunchSync sync{};
   const int64_t total = n_chunks * n_groups;
-  if (int rc = acquire_scratch(stream, rec_bytes, total, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
   hipLaunchKernelGGL((sdl_forward_kernel<V, T, W>), dim3(static_cast<unsigned>(total)),
                      dim3(W * kWave), 0, stream, prm, static_cast<const float2*>(bu),
                      static_cast<float4*>(states), static_cast<int>(L), static_cast<int>(nc),
                      static_cast<int>(n_groups), static_cast<int>(n_chunks),
                      static_cast<unsigned long long*>(payload), sync);
   if (int rc = launch_check("sdl_forward_kernel")) {
-    release_unlaunched(stream, total);
+    release_unlaunched(call, total);
     return rc;
   }
   return OSSM_OK;
@@ -727,6 +729,8 @@ template <int V, int T, int W>
 int sdl_backward_tw(const SdlParams& prm, const ParamShape (&shapes)[3], const void* bu,
                     const void* states, const void* gout, float* const (&grads)[3], void* gbu,
                     int64_t L, int64_t B, int64_t M, hipStream_t stream) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   const int64_t nc = B * M;
   const int64_t n_chunks = (L + T * W - 1) / (T * W);
   const int64_t n_groups = (nc + kWave - 1) / kWave;
@@ -756,7 +760,7 @@ int sdl_backward_tw(const SdlParams& prm, const ParamShape (&shapes)[3], const v
     const size_t buf_bytes = (ws_floats * sizeof(float) + 255) & ~static_cast<size_t>(255);
     const size_t part_bytes = 3 * static_cast<size_t>(kSumGroups) * max_out * sizeof(double);
     void* ws = nullptr;
-    if (int rc = acquire_workspace(stream, buf_bytes + part_bytes, &ws)) return rc;
+    if (int rc = acquire_workspace(call, buf_bytes + part_bytes, &ws)) return rc;
     bufs = static_cast<float*>(ws);
     part = reinterpret_cast<double*>(static_cast<char*>(ws) + buf_bytes);
   }
@@ -770,7 +774,7 @@ int sdl_backward_tw(const SdlParams& prm, const ParamShape (&shapes)[3], const v
   void* payload = nullptr;
   LaunchSync sync{};
   const int64_t total = n_chunks * n_groups;
-  if (int rc = acquire_scratch(stream, rec_bytes, total, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
   hipLaunchKernelGGL((sdl_backward_kernel<V, T, W>), dim3(static_cast<unsigned>(total)),
                      dim3(W * kWave), 0, stream, prm, static_cast<const float2*>(bu),
                      static_cast<const float4*>(states), static_cast<const float2*>(gout),
@@ -778,7 +782,7 @@ int sdl_backward_tw(const SdlParams& prm, const ParamShape (&shapes)[3], const v
                      static_cast<int>(n_groups), static_cast<int>(n_chunks),
                      static_cast<unsigned long long*>(payload), sync);
   if (int rc = launch_check("sdl_backward_kernel")) {
-    release_unlaunched(stream, total);
+    release_unlaunched(call, total);
     return rc;
   }
   ColSums sums{};

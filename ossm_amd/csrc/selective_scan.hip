@@ -1246,6 +1246,8 @@ int selective_forward_impl(const E* u, const E* dt, const float* A, const E* Bm,
                            const E* gate, E* out, E* raw_out, float* chunk_states, int64_t batch,
                            int64_t dim, int64_t length, int64_t dstate, hipStream_t stream,
                            const char* what, const MambaLayout* ml = nullptr) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   clear_error();
   if (int rc = check_selective(batch, dim, length, dstate, what)) return rc;
   if (batch == 0 || dim == 0 || length == 0) return OSSM_OK;
@@ -1267,7 +1269,7 @@ int selective_forward_impl(const E* u, const E* dt, const float* A, const E* Bm,
       a.acc = raw_out != nullptr ? raw_out : out;  // summed in place, then overwritten
     } else {
       void* ws = nullptr;
-      if (int rc = acquire_workspace(stream, static_cast<size_t>(batch * dim * length) * sizeof(float), &ws))
+      if (int rc = acquire_workspace(call, static_cast<size_t>(batch * dim * length) * sizeof(float), &ws))
         return rc;
       a.acc = static_cast<float*>(ws);
     }
@@ -1320,6 +1322,8 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
                             int64_t batch, int64_t dim, int64_t length, int64_t dstate,
                             hipStream_t stream, const char* what,
                             const MambaLayout* ml = nullptr) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   clear_error();
   if (int rc = check_selective(batch, dim, length, dstate, what)) return rc;
   if (batch == 0 || dim == 0 || length == 0) {
@@ -1344,7 +1348,7 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
   const size_t part_floats =
       static_cast<size_t>(2 * n_dtiles * n_bln + batch * n_dn) + (staged ? 2 * n_rows : 0);
   void* ws = nullptr;
-  if (int rc = acquire_workspace(stream, part_floats * sizeof(float), &ws)) return rc;
+  if (int rc = acquire_workspace(call, part_floats * sizeof(float), &ws)) return rc;
   float* part_dB = static_cast<float*>(ws);
   float* part_dC = part_dB + n_dtiles * n_bln;
   float* part_dA = part_dC + n_dtiles * n_bln;

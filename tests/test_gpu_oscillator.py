@@ -132,11 +132,14 @@ def test_dlinoss_config2_full_size(K, variant):
     st64, (_, _, _, tgb) = _oracle64(variant, a, g, dt, bus, gos)
     assert_parity(to_np(st[:, bs]), ref, st64, RTOL, ATOL, "states slice")
     assert_parity(to_np(gp[3][:, bs]), rgb, tgb, RTOL, ATOL, "grad_bu slice")
-    # whole-problem parameter gradients vs the oracle on all channels
+    # whole-problem parameter gradients vs the oracle on all channels: relative
+    # norm, and elementwise (atol scaled by the sums' size, fp64 fallback)
     full = oracle.dlinoss_forward(variant, a, g, dt, bu)
     rg = oracle.dlinoss_backward(variant, a, g, dt, bu, full, go)
-    for got, r, key in zip(gp[:3], rg[:3], ("grad_a", "grad_g", "grad_step")):
+    _, tg = _oracle64(variant, a, g, dt, bu, go)
+    for got, r, t, key in zip(gp[:3], rg[:3], tg[:3], ("grad_a", "grad_g", "grad_step")):
         assert rel_fro(to_np(got), r) < 1e-4, key
+        assert_parity(to_np(got), r, t, RTOL, _param_atol(t), key)
     # linearity: scan(bu + 2 bu') = scan(bu) + 2 scan(bu')
     bu2 = torch.roll(to_dev(bu), shifts=1, dims=1)
     s2 = _fwd(K, variant, a, g, dt, to_np(bu2))
@@ -160,6 +163,13 @@ def test_dlinoss_config5_long_sequence(K):
     e_cpu = rel_fro(ref32, ref64)
     assert e_gpu <= 4 * e_cpu + 1e-6, (e_gpu, e_cpu)
     assert rel_fro(st, ref32) < 1e-4
+    # elementwise on channel slices: batch row 1 (every oscillator, all 65536
+    # steps, so every one of the 512 chunk carries of 256 channels) and every
+    # 8th oscillator of the other rows
+    assert_parity(st[:, 1], ref32[:, 1], ref64[:, 1], RTOL, ATOL, "states row 1")
+    for b in (0, 2, 3):
+        assert_parity(st[:, b, ::8], ref32[:, b, ::8], ref64[:, b, ::8], RTOL, ATOL,
+                      f"states row {b}, every 8th oscillator")
     no_device_errors()
 
 
@@ -234,4 +244,74 @@ def test_linoss_complex128_vs_oracle(K, shape):
     # mixed dtypes are rejected, not reinterpreted
     with pytest.raises(RuntimeError, match="b_seq's dtype"):
         K.linoss_scan(*[to_dev(m.astype(np.complex64)) for m in ms], to_dev(b))
+    no_device_errors()
+
+
+def _linoss_grad(rng, L, B, P):
+    return (rng.normal(size=(L, B, P, 2)) + 1j * rng.normal(size=(L, B, P, 2))).astype(np.complex64)
+
+
+def test_linoss_imex_unit_modulus(K):
+    """LinOSS-IMEX (linoss.py:253-258): M = [[1, -dt a], [dt, 1 - dt^2 a]] has
+    det M = 1 and, for dt^2 a < 4, both eigenvalues on the unit circle, so
+    neither the chunk powers M^T nor the look-back carries decay.  L = 4096
+    (32 chunks of 128 steps per channel), b = (bu dt, bu dt^2); forward and the
+    native backward against the oracle and fp64 truth."""
+    L, B, P = 4096, 4, 64
+    rng = np.random.default_rng(4096)
+    a = rng.uniform(0.1, 1.0, P)
+    dt = 1 / (1 + np.exp(-rng.normal(size=P)))
+    ms64 = [np.ones(P), -dt * a, dt, 1 - dt * dt * a]
+    lam = np.linalg.eigvals(np.stack([np.stack(ms64[:2], -1), np.stack(ms64[2:], -1)], -2))
+    assert np.allclose(np.abs(lam), 1.0, atol=1e-12)  # the regime under test
+    ms = [m.astype(np.complex64) for m in ms64]
+    bu = (rng.normal(size=(L, B, P)) + 1j * rng.normal(size=(L, B, P))).astype(np.complex64)
+    dtc = dt.astype(np.complex64)
+    b = np.ascontiguousarray(np.stack([bu * dtc, bu * dtc * dtc], -1).astype(np.complex64))
+    go = _linoss_grad(rng, L, B, P)
+    announce(f"linoss IMEX |lambda|=1 L={L} B={B} P={P}")
+    st = K.linoss_scan(*[to_dev(m) for m in ms], to_dev(b))
+    ref = oracle.linoss_forward(*ms, b)
+    ms128 = [m.astype(np.complex128) for m in ms]
+    st64 = oracle.linoss_forward(*ms128, b.astype(np.complex128))
+    assert_parity(to_np(st), ref, st64, RTOL, ATOL, "IMEX states")
+    gm, gb = K.linoss_scan_backward(*[to_dev(m) for m in ms], st, to_dev(go))
+    rgm, rgb = oracle.linoss_backward(*ms, ref, go)
+    tgm, tgb = oracle.linoss_backward(*ms128, st64, go.astype(np.complex128))
+    assert_parity(to_np(gb), rgb, tgb, RTOL, ATOL, "IMEX grad_b")
+    assert_parity(to_np(gm), rgm, tgm, RTOL, _param_atol(tgm), "IMEX grad_m")
+    no_device_errors()
+
+
+def test_linoss_config1_workload(K):
+    """BASELINE config 1 exactly: LinOSS-IM forward, B=8 L=1024 P=64 H=64 with
+    A_diag = relu(N(0,1)) + 0.1, dt = sigmoid(N(0,1)), B complex N(0, 1/H),
+    u ~ N(0,1), bu = u B^T and b_seq = (bu m11 dt, bu m21 dt) (linoss.py:244-251);
+    every state against the oracle (elementwise, fp64 fallback), plus the
+    native backward."""
+    Bsz, L, P, H = 8, 1024, 64, 64
+    rng = np.random.default_rng(1)
+    A = np.maximum(rng.normal(size=P), 0.0) + 0.1
+    dt = 1 / (1 + np.exp(-rng.normal(size=P)))
+    Bw = (rng.normal(size=(P, H)) + 1j * rng.normal(size=(P, H))) / np.sqrt(H)
+    u = rng.normal(size=(Bsz, L, H))
+    bu = np.ascontiguousarray((u @ Bw.T).transpose(1, 0, 2))  # [L, B, P]
+    schur = 1 / (1 + dt * dt * A)
+    ms64 = [1 - dt * dt * A * schur, -dt * A * schur, dt * schur, schur]
+    b64 = np.stack([bu * ms64[0] * dt, bu * ms64[2] * dt], -1)
+    ms = [m.astype(np.complex64) for m in ms64]
+    b = np.ascontiguousarray(b64.astype(np.complex64))
+    announce(f"linoss IM config1 B={Bsz} L={L} P={P} H={H}")
+    st = K.linoss_scan(*[to_dev(m) for m in ms], to_dev(b))
+    ref = oracle.linoss_forward(*ms, b)
+    ms128 = [m.astype(np.complex128) for m in ms]
+    st64 = oracle.linoss_forward(*ms128, b.astype(np.complex128))
+    assert tuple(st.shape) == (L, Bsz, P, 2)
+    assert_parity(to_np(st), ref, st64, RTOL, ATOL, "config1 states")
+    go = _linoss_grad(rng, L, Bsz, P)
+    gm, gb = K.linoss_scan_backward(*[to_dev(m) for m in ms], st, to_dev(go))
+    rgm, rgb = oracle.linoss_backward(*ms, ref, go)
+    tgm, tgb = oracle.linoss_backward(*ms128, st64, go.astype(np.complex128))
+    assert_parity(to_np(gb), rgb, tgb, RTOL, ATOL, "config1 grad_b")
+    assert_parity(to_np(gm), rgm, tgm, RTOL, _param_atol(tgm), "config1 grad_m")
     no_device_errors()
