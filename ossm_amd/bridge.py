@@ -1,8 +1,10 @@
 """Autograd bridges over the MI355X scan library, mirroring the reference's
 kernel bridges (the L2 layer above ``ossm._kernels``):
 
-* D-LinOSS: ``run_dlinoss``, ``has_kernels``, ``extension_error`` and one
-  autograd Function per variant — reference src/ossm/models/_dlinoss_scan.py:416-680.
+* D-LinOSS: ``run_dlinoss``, ``has_kernels``, ``extension_error``, the
+  ``ossm::dlinoss_<v>_{forward,backward}`` torch.library operators with Meta
+  implementations (_dlinoss_scan.py:176-406) and one autograd Function per
+  variant over them — reference src/ossm/models/_dlinoss_scan.py:416-680.
   Forward saves ``(a, g, step, bu, states)`` and returns ``states[..., 1]``;
   backward passes ``grad_output.contiguous()`` (:461-498).
 * Selective D-LinOSS: ``run_sdlinoss`` and ``SdlinossFn``
@@ -40,7 +42,7 @@ from torch import Tensor
 from . import _kernels
 
 __all__ = [
-    "has_kernels", "extension_error", "run_dlinoss", "run_dlinoss_imex1", "DlinossFn",
+    "has_kernels", "extension_error", "run_dlinoss", "run_dlinoss_imex1", "DlinossFn", "CUSTOM_OPS",
     "run_sdlinoss", "SdlinossFn",
     "try_run_scan", "LinossScanFn", "LinossMatrixScanFn", "run_associative_scan",
     "try_selective_scan", "SelectiveScanFn",
@@ -67,14 +69,76 @@ def extension_error() -> Optional[Exception]:
 
 
 # ------------------------------------------------------------------ D-LinOSS
+# torch.library operators ``ossm::dlinoss_<v>_{forward,backward}`` with the
+# reference's schema strings (_dlinoss_scan.py:183-206), so torch.compile can
+# trace the scans with fake tensors and still call the device kernels: the
+# CompositeExplicitAutograd implementation is the drop-in module's entry
+# point, the Meta implementation only produces outputs of the right shape and
+# dtype.  When the operators already exist (the reference's bridge imported
+# in the same process defines them too, over ``ossm._kernels``), the existing
+# definitions and implementations are kept.
+_OP_FWD = "dlinoss_{v}_forward(Tensor a_diag, Tensor g_diag, Tensor step, Tensor bu) -> Tensor"
+_OP_BWD = ("dlinoss_{v}_backward(Tensor a_diag, Tensor g_diag, Tensor step, Tensor bu, "
+           "Tensor states, Tensor grad_output) -> (Tensor, Tensor, Tensor, Tensor)")
+_OPS_LIBRARY = None
+
+
+def _forward_meta(a_diag: Tensor, g_diag: Tensor, step: Tensor, bu: Tensor) -> Tensor:
+    return bu.new_empty((*bu.shape, 2))
+
+
+def _backward_meta(a_diag: Tensor, g_diag: Tensor, step: Tensor, bu: Tensor, states: Tensor,
+                   grad_output: Tensor):
+    return (torch.empty_like(a_diag), torch.empty_like(g_diag), torch.empty_like(step),
+            torch.empty_like(bu))
+
+
+def _register_ops() -> bool:
+    """Define and implement the operators; False when torch.library is missing."""
+    global _OPS_LIBRARY
+    try:
+        from torch.library import Library
+    except ImportError:  # pragma: no cover - very old torch
+        return False
+    try:
+        lib = Library("ossm", "DEF")
+        for v in SUPPORTED_VARIANTS:
+            lib.define(_OP_FWD.format(v=v))
+            lib.define(_OP_BWD.format(v=v))
+    except RuntimeError:
+        lib = Library("ossm", "IMPL")  # defined already: keep the definitions
+    for v in SUPPORTED_VARIANTS:
+        for name, impl, meta in ((f"dlinoss_{v}_forward", getattr(_kernels, f"dlinoss_{v}_forward"),
+                                  _forward_meta),
+                                 (f"dlinoss_{v}_backward", getattr(_kernels, f"dlinoss_{v}_backward"),
+                                  _backward_meta)):
+            for fn, key in ((impl, "CompositeExplicitAutograd"), (meta, "Meta")):
+                try:
+                    lib.impl(name, fn, key)
+                except RuntimeError:
+                    pass  # an implementation is registered already
+    _OPS_LIBRARY = lib
+    return True
+
+
+CUSTOM_OPS = _register_ops()
+
+
+def _dlinoss_op(variant: str, direction: str):
+    if CUSTOM_OPS:
+        return getattr(torch.ops.ossm, f"dlinoss_{variant}_{direction}")
+    return getattr(_kernels, f"dlinoss_{variant}_{direction}")
+
+
 class DlinossFn(torch.autograd.Function):
     """Autograd bridge of one D-LinOSS variant (reference _DlinossImex1Fn and
-    siblings, _dlinoss_scan.py:458-600)."""
+    siblings, _dlinoss_scan.py:458-600), through the ``ossm::dlinoss_*``
+    operators."""
 
     @staticmethod
     def forward(ctx, variant: str, a_diag: Tensor, g_diag: Tensor, step: Tensor,
                 bu: Tensor) -> Tensor:  # type: ignore[override]
-        states = getattr(_kernels, f"dlinoss_{variant}_forward")(a_diag, g_diag, step, bu)
+        states = _dlinoss_op(variant, "forward")(a_diag, g_diag, step, bu)
         ctx.variant = variant
         ctx.save_for_backward(a_diag, g_diag, step, bu, states)
         return states[..., 1]
@@ -82,7 +146,7 @@ class DlinossFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output: Tensor):  # type: ignore[override]
         a_diag, g_diag, step, bu, states = ctx.saved_tensors
-        grad_a, grad_g, grad_step, grad_bu = getattr(_kernels, f"dlinoss_{ctx.variant}_backward")(
+        grad_a, grad_g, grad_step, grad_bu = _dlinoss_op(ctx.variant, "backward")(
             a_diag, g_diag, step, bu, states, grad_output.contiguous())
         return None, grad_a, grad_g, grad_step, grad_bu
 

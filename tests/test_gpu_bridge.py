@@ -239,3 +239,30 @@ def test_sdlinoss_layer_outputs_and_grads(bridge, variant, shape):
     for got, r, name in zip(dev, ref, names):
         np.testing.assert_allclose(got.grad.cpu().numpy(), r.grad.numpy(), rtol=5e-4,
                                    atol=1e-4 * max(1.0, float(r.grad.abs().max())), err_msg=name)
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_dlinoss_torch_library_ops_opcheck(bridge, variant):
+    """``torch.library.opcheck`` on ``ossm::dlinoss_<v>_{forward,backward}``
+    (schema, fake-tensor / Meta consistency with the device kernels, AOT
+    dispatch), and a ``torch.compile`` trace of ``run_dlinoss`` that agrees
+    with the eager call (to the last bits the look-back's association may
+    change between runs)."""
+    assert bridge.CUSTOM_OPS
+    g = torch.Generator().manual_seed(5)
+    L, B, P = 70, 2, 9
+    a = (torch.rand(P, generator=g) * 0.9 + 0.1).cuda()
+    gg = torch.rand(P, generator=g).cuda()
+    dt = torch.sigmoid(torch.randn(P, generator=g)).cuda()
+    bu = torch.complex(torch.randn(L, B, P, generator=g), torch.randn(L, B, P, generator=g)).cuda()
+    go = torch.complex(torch.randn(L, B, P, generator=g), torch.randn(L, B, P, generator=g)).cuda()
+    announce(f"torch.library opcheck dlinoss_{variant}")
+    fwd = getattr(torch.ops.ossm, f"dlinoss_{variant}_forward")
+    bwd = getattr(torch.ops.ossm, f"dlinoss_{variant}_backward")
+    torch.library.opcheck(fwd, (a, gg, dt, bu))
+    states = fwd(a, gg, dt, bu)
+    torch.library.opcheck(bwd, (a, gg, dt, bu, states, go))
+    eager = bridge.run_dlinoss(variant, a, gg, dt, bu)
+    compiled = torch.compile(lambda *xs: bridge.run_dlinoss(variant, *xs), backend="aot_eager",
+                             fullgraph=True)
+    torch.testing.assert_close(compiled(a, gg, dt, bu), eager, rtol=1e-6, atol=1e-6)

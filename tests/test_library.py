@@ -106,3 +106,34 @@ def test_cpu_delegate_routes_to_the_reference_module():
         assert torch.equal(got, ref.dlinoss_im_forward(a, g, dt, bu))
     finally:
         _kernels.set_cpu_delegate(None)
+
+
+# the reference's operator schemas (_dlinoss_scan.py:183-206)
+_REF_FWD_SCHEMA = "ossm::dlinoss_{v}_forward(Tensor a_diag, Tensor g_diag, Tensor step, Tensor bu) -> Tensor"
+_REF_BWD_SCHEMA = ("ossm::dlinoss_{v}_backward(Tensor a_diag, Tensor g_diag, Tensor step, Tensor bu, "
+                   "Tensor states, Tensor grad_output) -> (Tensor, Tensor, Tensor, Tensor)")
+
+
+@pytest.mark.parametrize("variant", ["imex1", "imex2", "im", "ex"])
+def test_torch_library_ops_schema_and_meta(variant):
+    """The ``ossm::dlinoss_*`` operators carry the reference's schemas, and
+    their Meta implementations give outputs of the kernels' shapes and dtypes
+    (states [L, B, P, 2] like bu; gradients like a, g, step and bu)."""
+    import torch
+
+    from ossm_amd import _lib, bridge
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libossm_scan.so not built (python -m ossm_amd.build)")
+    assert bridge.CUSTOM_OPS
+    fwd = getattr(torch.ops.ossm, f"dlinoss_{variant}_forward")
+    bwd = getattr(torch.ops.ossm, f"dlinoss_{variant}_backward")
+    assert str(fwd.default._schema) == _REF_FWD_SCHEMA.format(v=variant)
+    assert str(bwd.default._schema) == _REF_BWD_SCHEMA.format(v=variant)
+    a = torch.empty(5, device="meta")
+    bu = torch.empty(7, 3, 5, dtype=torch.complex64, device="meta")
+    st = fwd(a, a, a, bu)
+    assert st.shape == (7, 3, 5, 2) and st.dtype == torch.complex64 and st.device.type == "meta"
+    grads = bwd(a, a, a, bu, st, bu)
+    assert [tuple(g.shape) for g in grads] == [(5,), (5,), (5,), (7, 3, 5)]
+    assert [g.dtype for g in grads] == [torch.float32] * 3 + [torch.complex64]
