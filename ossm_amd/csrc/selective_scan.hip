@@ -50,6 +50,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <climits>
 #include <initializer_list>
 #include <cstdint>
@@ -376,23 +377,6 @@ __device__ __forceinline__ void store_cols_softplus(float* __restrict__ s, const
   }
 }
 
-// kSeg consecutive steps t .. of channel d of a [B, L, D] tensor (row stride
-// ld): strided scalar accesses; reads past L use a clamped in-range step.
-template <class E>
-__device__ __forceinline__ void load_seg_bld(float (&v)[8], const E* __restrict__ g, size_t base,
-                                             int ld, int d, int t, int L) {
-#pragma unroll
-  for (int k = 0; k < 8; ++k) v[k] = Elem<E>::load1(g + base + static_cast<size_t>(min(t + k, L - 1)) * ld + d);
-}
-
-template <class E>
-__device__ __forceinline__ void store_seg_bld(E* __restrict__ g, size_t base, int ld, int d, int t,
-                                              int L, const float (&v)[8]) {
-#pragma unroll
-  for (int k = 0; k < 8; ++k)
-    if (t + k < L) Elem<E>::store1(g + base + static_cast<size_t>(t + k) * ld + d, v[k]);
-}
-
 // B or C rows t0..t0+TT-1, states n_base..n_base+15 (zero outside the
 // tensor, so padded states contribute nothing); LDS layout s[t * 16 + j].
 template <int TT>
@@ -448,10 +432,17 @@ struct FwdArgs {
   const float* dt_bias;
 };
 
+// vec4: N % 4 == 0 and chunk_states 16-byte aligned, so a lane whose four
+// states all lie below N stores them with one 16-byte store (the four lanes
+// of a channel: 64 contiguous bytes); lanes past N store nothing.
 __device__ __forceinline__ void write_ckpt(float* ckpt, size_t lane_row, int slot, int N,
-                                           int n0, const float (&h)[kNpw]) {
+                                           int n0, const float (&h)[kNpw], bool vec4) {
   const int c = slot >> 1, half = slot & 1;
   float* p = ckpt + lane_row + static_cast<size_t>(c) * 2 * N + half * N;
+  if (vec4 && n0 + kNpw <= N) {
+    *reinterpret_cast<float4*>(p + n0) = make_float4(h[0], h[1], h[2], h[3]);
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < kNpw; ++j)
     if (n0 + j < N) p[n0 + j] = h[j];
@@ -485,56 +476,66 @@ constexpr int kGroups = kPassStates / kNpw;  // state groups per channel (4)
 constexpr int kWaveCh = kWave / kGroups;     // channels per wave (16)
 constexpr int kSeg = kFwdTile / kGroups;     // output steps per lane per tile (8)
 
-// 8 consecutive steps of one row of a [.., L] tensor, from step t (a multiple
-// of 4); reads past the end use clamped in-range addresses (values unused).
+// The lane's 8 output steps of a tile: 4g .. 4g+3 and 16+4g .. 16+4g+3 for
+// state group g, so that the four lanes of a channel cover 16 contiguous steps
+// (64 bytes of fp32) with each 4-step access.
+__device__ __forceinline__ int seg_step(int g, int k) { return (k < 4 ? 0 : 12) + 4 * g + k; }
+
+// The lane's 8 steps of one row of a [.., L] tensor in tile t0; reads past
+// the end use clamped in-range addresses (values unused).
 template <bool VEC, class E>
 __device__ __forceinline__ void load_seg(float (&v)[kSeg], const E* __restrict__ g, size_t row,
-                                         int t, int L) {
-  if constexpr (VEC) {
+                                         int t0, int grp, int L) {
 #pragma unroll
-    for (int q = 0; q < kSeg / 4; ++q) {
-      const float4 x = Elem<E>::load4(g + row + min(t + 4 * q, L - 4));
+  for (int q = 0; q < 2; ++q) {
+    const int t = t0 + 16 * q + 4 * grp;
+    if constexpr (VEC) {
+      const float4 x = Elem<E>::load4(g + row + min(t, L - 4));
       v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
-    }
-  } else {
+    } else {
 #pragma unroll
-    for (int k = 0; k < kSeg; ++k) v[k] = Elem<E>::load1(g + row + min(t + k, L - 1));
+      for (int k = 0; k < 4; ++k) v[4 * q + k] = Elem<E>::load1(g + row + min(t + k, L - 1));
+    }
   }
 }
 
-// Stores the steps of an 8-step segment that lie before L.
+// Stores the lane's 8 steps of tile t0 that lie before L.
 template <bool VEC, class E>
-__device__ __forceinline__ void store_seg(E* __restrict__ g, size_t row, int t, int L,
+__device__ __forceinline__ void store_seg(E* __restrict__ g, size_t row, int t0, int grp, int L,
                                           const float (&v)[kSeg]) {
-  if constexpr (VEC) {  // L % 4 == 0, so a group of 4 is all in or all out
 #pragma unroll
-    for (int q = 0; q < kSeg / 4; ++q)
-      if (t + 4 * q < L)
-        Elem<E>::store4(g + row + t + 4 * q, make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]));
-  } else {
+  for (int q = 0; q < 2; ++q) {
+    const int t = t0 + 16 * q + 4 * grp;
+    if constexpr (VEC) {  // L % 4 == 0, so a group of 4 is all in or all out
+      if (t < L) Elem<E>::store4(g + row + t, make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]));
+    } else {
 #pragma unroll
-    for (int k = 0; k < kSeg; ++k)
-      if (t + k < L) Elem<E>::store1(g + row + t + k, v[k]);
+      for (int k = 0; k < 4; ++k)
+        if (t + k < L) Elem<E>::store1(g + row + t + k, v[4 * q + k]);
+    }
   }
 }
 
 // Sums y over the kGroups state groups of each channel: lane (c, g) enters
 // with its group's partial y for steps 0..31 of the tile and leaves with the
-// full y of steps 8g .. 8g+7.  permlane32 swaps pair groups g and g ^ 2 (the
-// two halves keep steps 0..15 and 16..31), permlane16 swaps pair g and g ^ 1.
+// full y of its steps seg_step(g, 0..7).  permlane32 swaps pair groups g and
+// g ^ 2 (the lower half keeps steps 0..7 and 16..23, the upper half 8..15 and
+// 24..31), permlane16 swaps pair g and g ^ 1.
 __device__ __forceinline__ void reduce_groups(float (&yv)[kFwdTile], float (&out)[kSeg]) {
   float s1[kFwdTile / 2];
 #pragma unroll
-  for (int i = 0; i < kFwdTile / 2; ++i) {
-    float lo = yv[i], hi = yv[i + kFwdTile / 2];
+  for (int k = 0; k < kFwdTile / 2; ++k) {
+    const int i = k < 8 ? k : k + 8;
+    float lo = yv[i], hi = yv[i + 8];
     swap32(lo, hi);
-    s1[i] = lo + hi;  // lanes 0..31: step i, lanes 32..63: step i + 16 (groups g, g ^ 2)
+    s1[k] = lo + hi;
   }
 #pragma unroll
-  for (int i = 0; i < kSeg; ++i) {
-    float lo = s1[i], hi = s1[i + kSeg];
+  for (int j = 0; j < kSeg; ++j) {
+    const int k = j < 4 ? j : j + 4;
+    float lo = s1[k], hi = s1[k + 4];
     swap16(lo, hi);
-    out[i] = lo + hi;  // row r: step 8r + i, all four groups
+    out[j] = lo + hi;
   }
 }
 
@@ -575,22 +576,55 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   const size_t ck_row = (static_cast<size_t>(b) * a.D + (dvalid ? d : 0)) * a.n_chunks * 2 * a.N;
   const int dc = dvalid ? d : a.D - 1;
   const size_t my_row = row0 + static_cast<size_t>(dc) * a.L;  // [.., L] row of d (BDL)
-  const size_t out0 = row0 * a.D;                              // (b, 0, 0) of out/raw/acc (BLD)
   const bool ck = a.ckpt != nullptr && dvalid;
-  auto load_gate = [&](float (&zv)[kSeg], int t) {
-    if constexpr (BLD) load_seg_bld(zv, a.z, row0 * a.ld_z, a.ld_z, dc, t, a.L);
-    else load_seg<VEC>(zv, a.z, my_row, t, a.L);
+  const bool ck4 = a.N % 4 == 0 && (reinterpret_cast<uintptr_t>(a.ckpt) & 15) == 0;
+  // [B, D, L] only: the gate and the outputs of the lane's 8 steps of tile t0
+  auto load_gate = [&](float (&zv)[kSeg], int t0) { load_seg<VEC>(zv, a.z, my_row, t0, g, a.L); };
+  auto put_seg = [&](auto* dst, int t0, const float (&v)[kSeg]) {
+    store_seg<VEC>(dst, my_row, t0, g, a.L, v);
   };
-  auto put_seg = [&](auto* dst, int t, const float (&v)[kSeg]) {
-    if constexpr (BLD) store_seg_bld(dst, out0, a.D, d, t, a.L, v);
-    else store_seg<VEC>(dst, my_row, t, a.L, v);
-  };
+
+  // Time split: with gridDim.z == 2 the sequence is cut at tile m; segment 0
+  // scans tiles [0, m), segment 1 first re-runs h over [0, m) (no outputs, the
+  // same per-step arithmetic, so the state it reaches is bitwise the one
+  // segment 0 computes) and then scans [m, n_tiles) from it.
+  const int n_tiles = (a.L + TT - 1) / TT;
+  const int m_split = (n_tiles + 1) / 2;
+  const int seg = gridDim.z > 1 ? static_cast<int>(blockIdx.z) : 0;
+  const int t_lo = seg == 1 ? m_split * TT : 0;
+  const int t_hi = (gridDim.z > 1 && seg == 0) ? min(a.L, m_split * TT) : a.L;
 
   FwdTile nxt;
   float zn[kSeg];  // the gate of the lane's output segment, one tile ahead
   fwd_prefetch<E, VEC, BLD>(nxt, a, row0, bc0, d0, 0);
-  if constexpr (GATED && !BLD) load_gate(zn, kSeg * g);
-  for (int t0 = 0; t0 < a.L; t0 += TT) {
+  for (int t0 = 0; t0 < t_lo; t0 += TT) {
+    // h only over the earlier segment's tiles
+    __syncthreads();
+    if constexpr (BLD) {
+      store_cols<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
+      store_cols_softplus<TT, RS>(s_dt, nxt.dt, a.dt_bias, d0, a.D, t0, a.L);
+    } else {
+      store_rows<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
+      store_rows<TT, RS>(s_dt, nxt.dt, d0, a.D, t0, a.L);
+    }
+    store_states<TT>(s_B, nxt.B, t0, a.L, a.N, a.n_base);
+    __syncthreads();
+    fwd_prefetch<E, VEC, BLD>(nxt, a, row0, bc0, d0, t0 + TT);
+    const float* urow = s_u + r * RS;
+    const float* dtrow = s_dt + r * RS;
+    const float* Bcol = s_B + g * kNpw;
+#pragma unroll 8
+    for (int i = 0; i < TT; ++i) {
+      const float dtv = dtrow[i];
+      const float dtu = dtv * urow[i];
+      const float4 Bt = *reinterpret_cast<const float4*>(Bcol + i * kPassStates);
+      const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
+#pragma unroll
+      for (int j = 0; j < kNpw; ++j) h[j] = fmaf(fast_exp2(dtv * A2[j]), h[j], dtu * Bv[j]);
+    }
+  }
+  if constexpr (GATED && !BLD) load_gate(zn, t_lo);
+  for (int t0 = t_lo; t0 < t_hi; t0 += TT) {
     __syncthreads();  // the previous tile's LDS readers are done
     if constexpr (BLD) {
       store_cols<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
@@ -605,9 +639,9 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
 #pragma unroll
     for (int k = 0; k < kSeg; ++k) zt[k] = zn[k];
     __syncthreads();
-    if (t0 + TT < a.L) {
+    if (t0 + TT < t_hi) {
       fwd_prefetch<E, VEC, BLD>(nxt, a, row0, bc0, d0, t0 + TT);
-      if constexpr (GATED && !BLD) load_gate(zn, t0 + TT + kSeg * g);
+      if constexpr (GATED && !BLD) load_gate(zn, t0 + TT);
     }
     // BLD: this tile's gate, for the row stores after the step loop
     RowRegs<TT> zq;
@@ -673,7 +707,7 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     }
     if (ck) {
 #pragma unroll
-      for (int q = 0; q < TT / kCkpt; ++q) write_ckpt(a.ckpt, ck_row, t0 / kCkpt + q, a.N, n0, hck[q]);
+      for (int q = 0; q < TT / kCkpt; ++q) write_ckpt(a.ckpt, ck_row, t0 / kCkpt + q, a.N, n0, hck[q], ck4);
     }
 
     // y over the state groups (within the wave), then this lane's 8 outputs
@@ -682,7 +716,7 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     if constexpr (BLD) {
       // through LDS, so that rows of 64 channels leave as 16-byte runs
 #pragma unroll
-      for (int k = 0; k < kSeg; ++k) s_y[(kSeg * g + k) * YS + r] = y[k];
+      for (int k = 0; k < kSeg; ++k) s_y[seg_step(g, k) * YS + r] = y[k];
       __syncthreads();
 #pragma unroll
       for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
@@ -722,23 +756,21 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
         }
       }
     } else if (dvalid) {
-      const int t = t0 + kSeg * g;
       if (!a.first) {
         float prev[kSeg];
-        if constexpr (BLD) load_seg_bld(prev, a.acc, out0, a.D, d, t, a.L);
-        else load_seg<false>(prev, a.acc, my_row, t, a.L);
+        load_seg<VEC>(prev, a.acc, my_row, t0, g, a.L);
 #pragma unroll
         for (int k = 0; k < kSeg; ++k) y[k] += prev[k];
       }
       if (a.last) {
-        if (a.raw != nullptr) put_seg(a.raw, t, y);
+        if (a.raw != nullptr) put_seg(a.raw, t0, y);
         if constexpr (GATED) {
 #pragma unroll
           for (int k = 0; k < kSeg; ++k) y[k] *= zt[k] * sigmoid(zt[k]);
         }
-        put_seg(a.out, t, y);
+        put_seg(a.out, t0, y);
       } else {
-        put_seg(a.acc, t, y);
+        put_seg(a.acc, t0, y);
       }
     }
   }
@@ -763,7 +795,7 @@ struct BwdArgs {
   float* ddt_acc;
   float* part_dB;      // [n_dtiles, B, L, N]
   float* part_dC;
-  float* part_dA;      // [B, D, N]
+  float* part_dA;      // [time segments * B, D, N]
   int Bsz, D, L, N, n_base, n_chunks;
   int first, last, vec;
   int ld_bc;           // row stride of B and C
@@ -811,6 +843,29 @@ __device__ __forceinline__ void bwd_prefetch(BwdTile& f, const BwdArgs<E>& a, si
   }
 }
 
+// What the adjoint-only pass of the time split reads per tile: dt, the
+// upstream gradient and the gate (for gy), and C.
+struct AdjTile {
+  RowRegs<kBwdTile> dt, go, z;
+  StateRegs<kBwdTile> C;
+};
+
+template <class E, bool VEC, bool GATED, bool BLD>
+__device__ __forceinline__ void adj_prefetch(AdjTile& f, const BwdArgs<E>& a, size_t row0, size_t bc0,
+                                             int d0, int tile) {
+  const int t0 = tile * kBwdTile;
+  if constexpr (BLD) {
+    load_cols<kBwdTile, VEC>(f.dt, a.dt, row0 * a.ld_dt, a.ld_dt, d0, a.D, t0, a.L);
+    load_cols<kBwdTile, VEC>(f.go, a.gout, row0 * a.D, a.D, d0, a.D, t0, a.L);
+    if constexpr (GATED) load_cols<kBwdTile, VEC>(f.z, a.z, row0 * a.ld_z, a.ld_z, d0, a.D, t0, a.L);
+  } else {
+    load_rows<kBwdTile, VEC>(f.dt, a.dt, row0, d0, a.D, t0, a.L);
+    load_rows<kBwdTile, VEC>(f.go, a.gout, row0, d0, a.D, t0, a.L);
+    if constexpr (GATED) load_rows<kBwdTile, VEC>(f.z, a.z, row0, d0, a.D, t0, a.L);
+  }
+  load_states<kBwdTile>(f.C, a.Cm, bc0, a.ld_bc, t0, a.L, a.N, a.n_base);
+}
+
 template <class E, bool VEC, bool GATED, bool BLD>
 __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   static_assert(!BLD || std::is_same_v<E, float>, "the [B, L, D] layout is fp32");
@@ -849,10 +904,71 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   const size_t ck_row = (static_cast<size_t>(b) * a.D + (dvalid ? d : 0)) * a.n_chunks * 2 * a.N;
   const size_t part0 = (static_cast<size_t>(blockIdx.x) * a.Bsz + b) * a.L * a.N;
   const int n_tiles = (a.L + TT - 1) / TT;
+  // Time split (gridDim.z == 2): segment 1 runs tiles [m, n_tiles), segment 0
+  // tiles [0, m) after an adjoint-only pass over [m, n_tiles) that carries gs
+  // from the end of the sequence to the cut with the main loop's per-step
+  // arithmetic (so the carry is bitwise the one segment 1 reaches).
+  const int seg = gridDim.z > 1 ? static_cast<int>(blockIdx.z) : 0;
+  const int m_split = (n_tiles + 1) / 2;
+  const int tile_lo = seg == 1 ? m_split : 0;
+  const int tile_hi = (gridDim.z > 1 && seg == 0) ? m_split : n_tiles;
+  if (tile_hi < n_tiles) {
+    AdjTile p;
+    adj_prefetch<E, VEC, GATED, BLD>(p, a, row0, bc0, d0, n_tiles - 1);
+    for (int tile = n_tiles - 1; tile >= tile_hi; --tile) {
+      const int t0 = tile * TT;
+      __syncthreads();
+      if constexpr (BLD) {
+        store_cols_softplus<TT, RS>(s_dt, p.dt, a.dt_bias, d0, a.D, t0, a.L);
+      } else {
+        store_rows<TT, RS>(s_dt, p.dt, d0, a.D, t0, a.L);
+      }
+      store_states<TT>(s_C, p.C, t0, a.L, a.N, a.n_base);
+#pragma unroll
+      for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+        float4 gy;
+        if constexpr (BLD) gy = masked_cols<TT>(p.go, k, d0, a.D, t0, a.L);
+        else gy = masked<TT>(p.go, k, d0, a.D, t0, a.L);
+        if constexpr (GATED) {
+          const float4 zz = p.z.v[k];
+          gy = make_float4(gy.x * zz.x * sigmoid(zz.x), gy.y * zz.y * sigmoid(zz.y),
+                           gy.z * zz.z * sigmoid(zz.z), gy.w * zz.w * sigmoid(zz.w));
+        }
+        if constexpr (BLD) {
+          int step, c4;
+          tile_pos_bld<TT>(k, step, c4);
+          put_col4(s_gy, RS, c4, step, gy);
+        } else {
+          int rr, cc;
+          tile_pos<TT>(k, rr, cc);
+          float* q = s_gy + rr * RS + cc;
+          q[0] = gy.x;
+          q[1] = gy.y;
+          q[2] = gy.z;
+          q[3] = gy.w;
+        }
+      }
+      __syncthreads();
+      if (tile > tile_hi) adj_prefetch<E, VEC, GATED, BLD>(p, a, row0, bc0, d0, tile - 1);
+      if (wave_active) {
+        const float* dtrow = s_dt + lane * RS;
+        const float* gyrow = s_gy + lane * RS;
+        const float* Ccol = s_C + w * kNpw;
+#pragma unroll 4
+        for (int i = TT - 1; i >= 0; --i) {
+          const float gy = gyrow[i], dtv = dtrow[i];
+          const float4 Ct = *reinterpret_cast<const float4*>(Ccol + i * kPassStates);
+          const float Cv[4] = {Ct.x, Ct.y, Ct.z, Ct.w};
+#pragma unroll
+          for (int j = 0; j < kNpw; ++j) gs[j] = fmaf(gy, Cv[j], gs[j]) * fast_exp2(dtv * A2[j]);
+        }
+      }
+    }
+  }
 
   BwdTile nxt;
-  bwd_prefetch<E, VEC, GATED, BLD>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, n_tiles - 1);
-  for (int tile = n_tiles - 1; tile >= 0; --tile) {
+  bwd_prefetch<E, VEC, GATED, BLD>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile_hi - 1);
+  for (int tile = tile_hi - 1; tile >= tile_lo; --tile) {
     const int t0 = tile * TT;
     const int nsteps = min(TT, a.L - t0);
     __syncthreads();  // the previous tile's LDS readers are done
@@ -928,7 +1044,7 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
 #pragma unroll
     for (int j = 0; j < kNpw; ++j) h0[j] = (tile > 0 && dvalid && n0 + j < a.N) ? nxt.h0[j] : 0.f;
     __syncthreads();
-    if (tile > 0) bwd_prefetch<E, VEC, GATED, BLD>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile - 1);
+    if (tile > tile_lo) bwd_prefetch<E, VEC, GATED, BLD>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile - 1);
 
     if (wave_active) {
       const float* dtrow = s_dt + lane * RS;
@@ -1045,8 +1161,12 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
       if (c < nsteps) {
         float* dst = (r < 2 ? a.part_dB : a.part_dC) + part0 + static_cast<size_t>(t0 + c) * a.N;
         const int nn = n0 + 2 * (r & 1);
-        if (nn < a.N) dst[nn] = keep0;
-        if (nn + 1 < a.N) dst[nn + 1] = keep1;
+        if (nn + 1 < a.N && a.N % 2 == 0) {
+          *reinterpret_cast<float2*>(dst + nn) = make_float2(keep0, keep1);
+        } else {
+          if (nn < a.N) dst[nn] = keep0;
+          if (nn + 1 < a.N) dst[nn + 1] = keep1;
+        }
       }
     }
     __syncthreads();
@@ -1135,22 +1255,31 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   }
 
   if (dvalid && wave_active) {
+    // one row of partials per (segment, batch row)
+    const size_t prow = static_cast<size_t>(seg) * a.Bsz + b;
 #pragma unroll
     for (int j = 0; j < kNpw; ++j)
-      if (n0 + j < a.N) a.part_dA[(static_cast<size_t>(b) * a.D + d) * a.N + n0 + j] = gA[j];
+      if (n0 + j < a.N) a.part_dA[(prow * a.D + d) * a.N + n0 + j] = gA[j];
   }
 }
 
-// Adds the per-tile partials in a fixed order: dB, dC over channel tiles,
-// dA over batch rows.
+// Adds the partials in a fixed order.  Blocks [0, n_bc_blocks): dB and dC,
+// one element per thread, summed over the channel tiles.  The remaining
+// blocks: dA, kFinCols columns per block, each column summed over `rows`
+// partial rows (batch rows x time segments) by kFinGroups row groups (eight
+// loads in flight each) and then over the groups in order through LDS.
+constexpr int kFinThreads = 1024;
+constexpr int kFinCols = 64;
+constexpr int kFinGroups = kFinThreads / kFinCols;
+
 template <class E>
-__global__ void selective_finish_kernel(const float* __restrict__ part_dB,
-                                        const float* __restrict__ part_dC,
-                                        const float* __restrict__ part_dA, E* __restrict__ dB,
-                                        E* __restrict__ dC, float* __restrict__ dA,
-                                        int64_t n_bln, int n_dtiles, int64_t n_dn, int Bsz) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n_bln) {
+__global__ __launch_bounds__(kFinThreads) void selective_finish_kernel(
+    const float* __restrict__ part_dB, const float* __restrict__ part_dC,
+    const float* __restrict__ part_dA, E* __restrict__ dB, E* __restrict__ dC,
+    float* __restrict__ dA, int64_t n_bln, int n_dtiles, int64_t n_dn, int rows, int n_bc_blocks) {
+  if (static_cast<int>(blockIdx.x) < n_bc_blocks) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kFinThreads + threadIdx.x;
+    if (i >= n_bln) return;
     // tiles added in ascending order; the loads of 8 tiles are issued before
     // any of them is added (the sum stays the same, bit for bit)
     constexpr int kBatch = 8;
@@ -1175,11 +1304,30 @@ __global__ void selective_finish_kernel(const float* __restrict__ part_dB,
     }
     Elem<E>::store1(dB + i, sb);
     Elem<E>::store1(dC + i, sc);
+    return;
   }
-  if (i < n_dn) {
-    float s = 0.f;
-    for (int bb = 0; bb < Bsz; ++bb) s += part_dA[static_cast<size_t>(bb) * n_dn + i];
-    dA[i] = s;
+  __shared__ float s_part[kFinGroups][kFinCols];
+  const int c = threadIdx.x % kFinCols, grp = threadIdx.x / kFinCols;
+  const int64_t col = static_cast<int64_t>(blockIdx.x - n_bc_blocks) * kFinCols + c;
+  const int64_t cc = col < n_dn ? col : n_dn - 1;
+  float s = 0.f;
+  constexpr int kBatch = 8;
+  int r = grp;
+  for (; r + (kBatch - 1) * kFinGroups < rows; r += kBatch * kFinGroups) {
+    float v[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) v[q] = part_dA[static_cast<size_t>(r + q * kFinGroups) * n_dn + cc];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) s += v[q];
+  }
+  for (; r < rows; r += kFinGroups) s += part_dA[static_cast<size_t>(r) * n_dn + cc];
+  s_part[grp][c] = s;
+  __syncthreads();
+  if (grp == 0 && col < n_dn) {
+    float t = 0.f;
+#pragma unroll
+    for (int q = 0; q < kFinGroups; ++q) t += s_part[q][c];
+    dA[col] = t;
   }
 }
 
@@ -1238,6 +1386,26 @@ bool cols_vectorizable(int64_t D, const MambaLayout& ml, std::initializer_list<c
   return true;
 }
 
+// Time segments per (batch row, channel tile): 2 when the grid would leave
+// the GPU's compute units unevenly or thinly loaded (fewer than two
+// workgroups per CU) and each half still holds at least two tiles, else 1.
+// OSSM_SEL_SPLIT=1|2 overrides.  The split re-runs one half's recurrence
+// (h only forward, the adjoint only backward) in the other half's workgroups.
+int time_segments(int64_t n_wg, int64_t L, int tile) {
+  static const int forced = [] {
+    const char* v = std::getenv("OSSM_SEL_SPLIT");
+    return v == nullptr ? 0 : std::atoi(v);
+  }();
+  if (L < 4 * static_cast<int64_t>(tile)) return 1;
+  if (forced == 1 || forced == 2) return forced;
+  int dev = 0, n_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n_cu <= 0)
+    return 1;
+  return n_wg < 2 * static_cast<int64_t>(n_cu) ? 2 : 1;
+}
+
 // E = float: the fp32 API of the reference.  E = bf16_t: the same scan with
 // bf16 rows, B and C in HBM (A, chunk_states and dA stay fp32).  ml: the
 // [B, L, D] layout (fp32 only); null for the reference's [B, D, L].
@@ -1290,7 +1458,10 @@ int selective_forward_impl(const E* u, const E* dt, const float* A, const E* Bm,
   } else {
     a.vec = rows_vectorizable(length, sizeof(E), {u, dt, gate, out, raw_out}) ? 1 : 0;
   }
-  const dim3 grid(static_cast<unsigned>((dim + kWave - 1) / kWave), static_cast<unsigned>(batch));
+  const int64_t n_dtiles = (dim + kWave - 1) / kWave;
+  const int n_seg = time_segments(n_dtiles * batch, length, kFwdTile);
+  const dim3 grid(static_cast<unsigned>(n_dtiles), static_cast<unsigned>(batch),
+                  static_cast<unsigned>(n_seg));
   for (int p = 0; p < n_pass; ++p) {
     a.n_base = p * kPassStates;
     a.first = p == 0;
@@ -1345,8 +1516,10 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
   const int64_t n_dn = dim * dstate;
   const int64_t n_rows = batch * dim * length;
   const bool staged = !std::is_same_v<E, float> && n_pass > 1;  // fp32 du/ddt between passes
+  const int n_seg = time_segments(n_dtiles * batch, length, kBwdTile);
+  const int64_t dA_rows = n_seg * batch;  // dA partial rows: (segment, batch row)
   const size_t part_floats =
-      static_cast<size_t>(2 * n_dtiles * n_bln + batch * n_dn) + (staged ? 2 * n_rows : 0);
+      static_cast<size_t>(2 * n_dtiles * n_bln + dA_rows * n_dn) + (staged ? 2 * n_rows : 0);
   void* ws = nullptr;
   if (int rc = acquire_workspace(call, part_floats * sizeof(float), &ws)) return rc;
   float* part_dB = static_cast<float*>(ws);
@@ -1370,7 +1543,7 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
     a.du_acc = du;  // summed in place
     a.ddt_acc = ddt;
   } else {
-    a.du_acc = staged ? part_dA + batch * n_dn : nullptr;
+    a.du_acc = staged ? part_dA + dA_rows * n_dn : nullptr;
     a.ddt_acc = staged ? a.du_acc + n_rows : nullptr;
   }
   a.part_dB = part_dB;
@@ -1383,7 +1556,7 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
   a.n_chunks = static_cast<int>(num_chunks(length));
   // the staged fp32 sums sit at a 16-byte multiple only when n_bln and B*D*N are
   // multiples of 4; otherwise the rows go element by element
-  const bool staged_aligned = !staged || (n_bln % 4 == 0 && (batch * n_dn) % 4 == 0);
+  const bool staged_aligned = !staged || (n_bln % 4 == 0 && (dA_rows * n_dn) % 4 == 0);
   a.ld_bc = static_cast<int>(dstate);
   if (ml != nullptr) {
     a.ld_bc = static_cast<int>(ml->ld_bc);
@@ -1398,7 +1571,8 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
                 ? 1
                 : 0;
   }
-  const dim3 grid(static_cast<unsigned>(n_dtiles), static_cast<unsigned>(batch));
+  const dim3 grid(static_cast<unsigned>(n_dtiles), static_cast<unsigned>(batch),
+                  static_cast<unsigned>(n_seg));
   for (int p = 0; p < n_pass; ++p) {
     a.n_base = p * kPassStates;
     a.first = p == 0;
@@ -1420,10 +1594,12 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, a);
     if (int rc = launch_check("selective_bwd_kernel")) return rc;
   }
-  const int64_t n_fin = n_bln > n_dn ? n_bln : n_dn;
-  hipLaunchKernelGGL(selective_finish_kernel<E>, dim3(static_cast<unsigned>((n_fin + 255) / 256)),
-                     dim3(256), 0, stream, part_dB, part_dC, part_dA, dB, dC, dA, n_bln,
-                     static_cast<int>(n_dtiles), n_dn, static_cast<int>(batch));
+  const int64_t n_bc_blocks = (n_bln + kFinThreads - 1) / kFinThreads;
+  const int64_t n_dA_blocks = (n_dn + kFinCols - 1) / kFinCols;
+  hipLaunchKernelGGL(selective_finish_kernel<E>, dim3(static_cast<unsigned>(n_bc_blocks + n_dA_blocks)),
+                     dim3(kFinThreads), 0, stream, part_dB, part_dC, part_dA, dB, dC, dA, n_bln,
+                     static_cast<int>(n_dtiles), n_dn, static_cast<int>(dA_rows),
+                     static_cast<int>(n_bc_blocks));
   if (int rc = launch_check("selective_finish_kernel")) return rc;
   if (gate == nullptr && dgate != nullptr) return zero_fill(dgate, n_rows, stream);
   return OSSM_OK;
