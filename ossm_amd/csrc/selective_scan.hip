@@ -72,6 +72,15 @@ constexpr int kChunk = 2 * kCkpt;            // chunk_states row = two checkpoin
 constexpr int kFwdTile = 32;                 // forward LDS tile (steps)
 constexpr int kBwdTile = kCkpt;              // backward LDS tile (steps)
 constexpr float kLog2e = 1.4426950408889634f;
+// Workgroups per compute unit the time split aims for (forward, backward).
+#ifndef OSSM_SEL_FWD_WG_PER_CU
+#define OSSM_SEL_FWD_WG_PER_CU 1
+#endif
+#ifndef OSSM_SEL_BWD_WG_PER_CU
+#define OSSM_SEL_BWD_WG_PER_CU 2
+#endif
+constexpr int kFwdWgPerCu = OSSM_SEL_FWD_WG_PER_CU;
+constexpr int kBwdWgPerCu = OSSM_SEL_BWD_WG_PER_CU;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -584,15 +593,14 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     store_seg<VEC>(dst, my_row, t0, g, a.L, v);
   };
 
-  // Time split: with gridDim.z == 2 the sequence is cut at tile m; segment 0
-  // scans tiles [0, m), segment 1 first re-runs h over [0, m) (no outputs, the
-  // same per-step arithmetic, so the state it reaches is bitwise the one
-  // segment 0 computes) and then scans [m, n_tiles) from it.
+  // Time split: gridDim.z segments of consecutive tiles; segment s scans
+  // tiles [s n / S, (s + 1) n / S) after re-running h alone over the tiles
+  // before them (no outputs, the same per-step arithmetic, so the state it
+  // reaches is bitwise the one the earlier segments compute).
   const int n_tiles = (a.L + TT - 1) / TT;
-  const int m_split = (n_tiles + 1) / 2;
-  const int seg = gridDim.z > 1 ? static_cast<int>(blockIdx.z) : 0;
-  const int t_lo = seg == 1 ? m_split * TT : 0;
-  const int t_hi = (gridDim.z > 1 && seg == 0) ? min(a.L, m_split * TT) : a.L;
+  const int n_seg = static_cast<int>(gridDim.z), seg = static_cast<int>(blockIdx.z);
+  const int t_lo = (seg * n_tiles / n_seg) * TT;
+  const int t_hi = min(a.L, ((seg + 1) * n_tiles / n_seg) * TT);
 
   FwdTile nxt;
   float zn[kSeg];  // the gate of the lane's output segment, one tile ahead
@@ -877,8 +885,13 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   __shared__ float s_gy[kWave * RS];
   __shared__ __align__(16) float s_B[TT * kPassStates];
   __shared__ __align__(16) float s_C[TT * kPassStates];
-  __shared__ float s_du[kMaxWaves * kWave * RS];
-  __shared__ float s_ddt[kMaxWaves * kWave * RS];
+  // per-wave du / ddt partials, [wave][channel][step], rows of DS floats: a
+  // lane writes 4 steps as one 16-byte store (rows 80 bytes apart, so the 16
+  // lanes of a quarter-wave hit disjoint banks) and the finish reads 4 steps
+  // of a channel with one 16-byte load
+  constexpr int DS = TT + 4;
+  __shared__ __align__(16) float s_du[kMaxWaves * kWave * DS];
+  __shared__ __align__(16) float s_ddt[kMaxWaves * kWave * DS];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
@@ -904,14 +917,14 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   const size_t ck_row = (static_cast<size_t>(b) * a.D + (dvalid ? d : 0)) * a.n_chunks * 2 * a.N;
   const size_t part0 = (static_cast<size_t>(blockIdx.x) * a.Bsz + b) * a.L * a.N;
   const int n_tiles = (a.L + TT - 1) / TT;
-  // Time split (gridDim.z == 2): segment 1 runs tiles [m, n_tiles), segment 0
-  // tiles [0, m) after an adjoint-only pass over [m, n_tiles) that carries gs
-  // from the end of the sequence to the cut with the main loop's per-step
-  // arithmetic (so the carry is bitwise the one segment 1 reaches).
-  const int seg = gridDim.z > 1 ? static_cast<int>(blockIdx.z) : 0;
-  const int m_split = (n_tiles + 1) / 2;
-  const int tile_lo = seg == 1 ? m_split : 0;
-  const int tile_hi = (gridDim.z > 1 && seg == 0) ? m_split : n_tiles;
+  // Time split: gridDim.z segments of consecutive tiles; segment s runs tiles
+  // [s n / S, (s + 1) n / S) after an adjoint-only pass over the tiles after
+  // them that carries gs from the end of the sequence with the main loop's
+  // per-step arithmetic (so the carry is bitwise the one the later segments
+  // reach).
+  const int n_seg = static_cast<int>(gridDim.z), seg = static_cast<int>(blockIdx.z);
+  const int tile_lo = seg * n_tiles / n_seg;
+  const int tile_hi = (seg + 1) * n_tiles / n_seg;
   if (tile_hi < n_tiles) {
     AdjTile p;
     adj_prefetch<E, VEC, GATED, BLD>(p, a, row0, bc0, d0, n_tiles - 1);
@@ -1052,8 +1065,8 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
       const float* gyrow = s_gy + lane * RS;
       const float* Bcol = s_B + w * kNpw;
       const float* Ccol = s_C + w * kNpw;
-      float* durow = s_du + (w * kWave + lane) * RS;
-      float* ddtrow = s_ddt + (w * kWave + lane) * RS;
+      float* durow = s_du + (w * kWave + lane) * DS;
+      float* ddtrow = s_ddt + (w * kWave + lane) * DS;
       float keep0 = 0.f, keep1 = 0.f;
 
       // Steps s0 .. s0 + HT - 1 of the tile, entered with the state before
@@ -1095,6 +1108,7 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
         float ngy = gyrow[s0 + il], ndt = dtrow[s0 + il], nu = urow[s0 + il];
         float4 nB = *reinterpret_cast<const float4*>(Bcol + (s0 + il) * kPassStates);
         float4 nC = *reinterpret_cast<const float4*>(Ccol + (s0 + il) * kPassStates);
+        float du4[4], dd4[4];  // the current group of 4 steps, written together
 #pragma unroll
         for (int i = il; i >= 0; --i) {
           const float gy = ngy, dtv = ndt, uv = nu;
@@ -1123,8 +1137,12 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
             v[4 + j] = gy * hs[i][j];  // dC contribution
             gs[j] = gsn;
           }
-          durow[s0 + i] = dtv * S1;
-          ddtrow[s0 + i] = fmaf(uv, S1, S2);
+          du4[i & 3] = dtv * S1;
+          dd4[i & 3] = fmaf(uv, S1, S2);
+          if ((i & 3) == 0) {
+            *reinterpret_cast<float4*>(durow + s0 + i) = make_float4(du4[0], du4[1], du4[2], du4[3]);
+            *reinterpret_cast<float4*>(ddtrow + s0 + i) = make_float4(dd4[0], dd4[1], dd4[2], dd4[3]);
+          }
           float o0, o1;
           reduce8(v, o0, o1);
           if ((lane & 15) == s0 + i) {
@@ -1185,8 +1203,8 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
         for (int v = 0; v < nw; ++v) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            su[e] += s_du[(v * kWave + c4 + e) * RS + step];
-            sd[e] += s_ddt[(v * kWave + c4 + e) * RS + step];
+            su[e] += s_du[(v * kWave + c4 + e) * DS + step];
+            sd[e] += s_ddt[(v * kWave + c4 + e) * DS + step];
           }
         }
 #pragma unroll
@@ -1224,16 +1242,16 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
       if (dd >= a.D || t >= a.L) continue;
       float4 su = make_float4(0.f, 0.f, 0.f, 0.f), sd = su;
       for (int v = 0; v < nw; ++v) {
-        const float* pu = s_du + (v * kWave + r) * RS + c;
-        const float* pd = s_ddt + (v * kWave + r) * RS + c;
-        su.x += pu[0];
-        su.y += pu[1];
-        su.z += pu[2];
-        su.w += pu[3];
-        sd.x += pd[0];
-        sd.y += pd[1];
-        sd.z += pd[2];
-        sd.w += pd[3];
+        const float4 pu = *reinterpret_cast<const float4*>(s_du + (v * kWave + r) * DS + c);
+        const float4 pd = *reinterpret_cast<const float4*>(s_ddt + (v * kWave + r) * DS + c);
+        su.x += pu.x;
+        su.y += pu.y;
+        su.z += pu.z;
+        su.w += pu.w;
+        sd.x += pd.x;
+        sd.y += pd.y;
+        sd.z += pd.z;
+        sd.w += pd.w;
       }
       const size_t gi = row0 + static_cast<size_t>(dd) * a.L + t;
       if (!a.first) {
@@ -1386,24 +1404,32 @@ bool cols_vectorizable(int64_t D, const MambaLayout& ml, std::initializer_list<c
   return true;
 }
 
-// Time segments per (batch row, channel tile): 2 when the grid would leave
-// the GPU's compute units unevenly or thinly loaded (fewer than two
-// workgroups per CU) and each half still holds at least two tiles, else 1.
-// OSSM_SEL_SPLIT=1|2 overrides.  The split re-runs one half's recurrence
-// (h only forward, the adjoint only backward) in the other half's workgroups.
-int time_segments(int64_t n_wg, int64_t L, int tile) {
+// Time segments per (batch row, channel tile), 1, 2 or 4: the fewest that
+// give at least `want` workgroups per compute unit, with every segment at
+// least two tiles long.  OSSM_SEL_SPLIT=1|2|4 overrides.  Segment s re-runs
+// the recurrence of the other segments it depends on (h only forward, the
+// adjoint only backward) before its own tiles.
+int time_segments(int64_t n_wg, int64_t L, int tile, int want) {
   static const int forced = [] {
     const char* v = std::getenv("OSSM_SEL_SPLIT");
     return v == nullptr ? 0 : std::atoi(v);
   }();
-  if (L < 4 * static_cast<int64_t>(tile)) return 1;
-  if (forced == 1 || forced == 2) return forced;
-  int dev = 0, n_cu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      n_cu <= 0)
-    return 1;
-  return n_wg < 2 * static_cast<int64_t>(n_cu) ? 2 : 1;
+  const int64_t n_tiles = (L + tile - 1) / tile;
+  int n_cu = 0;
+  if (forced == 1 || forced == 2 || forced == 4) {
+    n_cu = 1;
+  } else {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n_cu <= 0)
+      return 1;
+  }
+  int s = 1;
+  while (s < 4 && n_tiles >= 4 * s &&
+         (forced ? s < forced : n_wg * s < static_cast<int64_t>(want) * n_cu))
+    s *= 2;
+  return s;
 }
 
 // E = float: the fp32 API of the reference.  E = bf16_t: the same scan with
@@ -1459,7 +1485,7 @@ int selective_forward_impl(const E* u, const E* dt, const float* A, const E* Bm,
     a.vec = rows_vectorizable(length, sizeof(E), {u, dt, gate, out, raw_out}) ? 1 : 0;
   }
   const int64_t n_dtiles = (dim + kWave - 1) / kWave;
-  const int n_seg = time_segments(n_dtiles * batch, length, kFwdTile);
+  const int n_seg = time_segments(n_dtiles * batch, length, kFwdTile, kFwdWgPerCu);
   const dim3 grid(static_cast<unsigned>(n_dtiles), static_cast<unsigned>(batch),
                   static_cast<unsigned>(n_seg));
   for (int p = 0; p < n_pass; ++p) {
@@ -1516,7 +1542,7 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
   const int64_t n_dn = dim * dstate;
   const int64_t n_rows = batch * dim * length;
   const bool staged = !std::is_same_v<E, float> && n_pass > 1;  // fp32 du/ddt between passes
-  const int n_seg = time_segments(n_dtiles * batch, length, kBwdTile);
+  const int n_seg = time_segments(n_dtiles * batch, length, kBwdTile, kBwdWgPerCu);
   const int64_t dA_rows = n_seg * batch;  // dA partial rows: (segment, batch row)
   const size_t part_floats =
       static_cast<size_t>(2 * n_dtiles * n_bln + dA_rows * n_dn) + (staged ? 2 * n_rows : 0);
