@@ -50,6 +50,31 @@ METRIC = "scan state-steps/s (B·L·state) + % of HBM peak, fwd and fwd+bwd, 1 G
 DL_BYTES_FWD = 24  # read bu (8) + write states (16)
 DL_BYTES_BWD = 24  # read bu (8) + read grad (8) + write grad_bu (8)
 PMC_FILE = ROOT / "profiles" / "dlinoss_imex1_config2_pmc.json"
+SEL_PROFILE = ROOT / "profiles" / "selective_scan_c3_c4_counters.json"
+
+
+def _valu_floors(case: str) -> dict:
+    """VALU issue floors (us) of the selective kernels at `case`, measured with
+    rocprofv3 counters (SEL_PROFILE); {} when the profile is absent."""
+    try:
+        return json.loads(SEL_PROFILE.read_text())["cases"].get(case, {})
+    except (OSError, ValueError, KeyError):
+        return {}
+
+
+def _valu_entry(case: str, fwd_ms: float, bwd_ms: float) -> dict:
+    """VALU-floor fractions of this run's event-timed launches: the fraction of
+    each direction's time that the VALU issue of its kernels (rocprof-counted
+    instructions x 4 cycles, v_exp_f32 x 8, over 1024 SIMDs at 2.4 GHz) needs."""
+    fl = _valu_floors(case)
+    if not fl:
+        return {}
+    f_us = fl.get("fwd", {}).get("valu_floor_us")
+    b_us = sum(fl.get(k, {}).get("valu_floor_us", 0.0) for k in ("bwd", "finish"))
+    return {"valu_floor_us_fwd": f_us, "valu_floor_us_bwd": b_us,
+            "valu_frac_fwd": f_us / (fwd_ms * 1e3) if f_us else None,
+            "valu_frac_bwd": b_us / (bwd_ms * 1e3) if b_us else None,
+            "valu_source": SEL_PROFILE.name}
 
 
 # ----------------------------------------------------------------- timing
@@ -305,7 +330,7 @@ def _detail_configs(torch, K, dev, reps=10):
     del b_seq, go, st
     # C3 / C4-shape: selective scan fwd+bwd, fp32, gated
     for key, (Bz, D, L, N) in (("c3_selective_fp32", (256, 128, 200, 16)),
-                               ("c4_shape_selective_fp32", (16, 1536, 2048, 16))):
+                               ("c4_shape_selective_fp32", (16, 1536, 2048, 16))):  # keys of SEL_PROFILE
         u, dts, A, Bm, Cm, z, go = selective_inputs(torch, Bz, D, L, N, dev)
         res = K.selective_scan_cuda(u, dts, A, Bm, Cm, z)
         tf = _ev_time(torch, lambda: K.selective_scan_cuda(u, dts, A, Bm, Cm, z), reps, 3)
@@ -319,7 +344,7 @@ def _detail_configs(torch, K, dev, reps=10):
                     "hbm_frac_fwd": fb / (tf / 1e3) / PEAK_HBM,
                     "hbm_frac_bwd": bb / (tb / 1e3) / PEAK_HBM,
                     "hbm_frac_fwd_bwd": (fb + bb) / ((tf + tb) / 1e3) / PEAK_HBM,
-                    "note": "bound by VALU (one exp and ~20 FMA-class ops per state-step fwd+bwd), not HBM"}
+                    **_valu_entry(key, tf, tb)}
         del u, dts, Bm, Cm, z, go, res
     # C4 as specified: bf16 storage of u, dt, B, C, z, outputs and input gradients;
     # fp32 state, sums, A and dA (ossm_selective_*_bf16)
@@ -338,7 +363,7 @@ def _detail_configs(torch, K, dev, reps=10):
                                 "hbm_frac_fwd": fb / (tf / 1e3) / PEAK_HBM,
                                 "hbm_frac_bwd": bb / (tb / 1e3) / PEAK_HBM,
                                 "hbm_frac_fwd_bwd": (fb + bb) / ((tf + tb) / 1e3) / PEAK_HBM,
-                                "note": "bound by VALU as the fp32 case; bf16 halves the bytes only"}
+                                **_valu_entry("c4_selective_bf16", tf, tb)}
     del u, dts, Bm, Cm, z, go, res
     # Fused D-LinOSS layer forward at config 2's shape (H = P = 128): one kernel,
     # MFMA-bound (8 H P flops per (b, t)); against the unfused layer's steps

@@ -845,6 +845,14 @@ __device__ __forceinline__ void bwd_prefetch(BwdTile& f, const BwdArgs<E>& a, si
   // state after step t0 - 1 = checkpoint slot tile - 1 (zero before the start)
   const int slot = max(tile - 1, 0);
   const float* p = a.ckpt + ck_row + static_cast<size_t>(slot >> 1) * 2 * a.N + (slot & 1) * a.N;
+  if (a.N % 4 == 0 && n0 + kNpw <= a.N && (reinterpret_cast<uintptr_t>(a.ckpt) & 15) == 0) {
+    const float4 v = *reinterpret_cast<const float4*>(p + n0);
+    f.h0[0] = v.x;
+    f.h0[1] = v.y;
+    f.h0[2] = v.z;
+    f.h0[3] = v.w;
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < kNpw; ++j) {
     f.h0[j] = p[min(n0 + j, a.N - 1)];  // masked where it is consumed
@@ -979,12 +987,103 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
     }
   }
 
+  // du / ddt of the tile at ft0, summed over the waves (states) from their
+  // LDS partials and accumulated over passes
+  auto finish_dudt = [&](const int ft0) {
+    const int t0 = ft0;
+    if constexpr (BLD) {
+      // 4 channels at one step per thread; ddt is taken through the softplus:
+      // d softplus(x) / dx = sigmoid(x), from softplus(x) staged in s_dt
+#pragma unroll
+      for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+        int step, c4;
+        tile_pos_bld<TT>(k, step, c4);
+        const int dd = d0 + c4, t = t0 + step;
+        if (dd >= a.D || t >= a.L) continue;
+        float su[4] = {0.f, 0.f, 0.f, 0.f}, sd[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int v = 0; v < nw; ++v) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            su[e] += s_du[(v * kWave + c4 + e) * DS + step];
+            sd[e] += s_ddt[(v * kWave + c4 + e) * DS + step];
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sd[e] *= sigmoid_of_softplus(s_dt[(c4 + e) * RS + step]);
+        const size_t gi = (row0 + t) * a.D + dd;
+        const int ne = min(4, a.D - dd);
+        if (!a.first) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (e < ne) {
+              su[e] += a.du_acc[gi + e];
+              sd[e] += a.ddt_acc[gi + e];
+            }
+        }
+        E* du = a.last ? a.du : reinterpret_cast<E*>(a.du_acc);
+        E* ddt = a.last ? a.ddt : reinterpret_cast<E*>(a.ddt_acc);
+        if (VEC) {
+          Elem<E>::store4(du + gi, make_float4(su[0], su[1], su[2], su[3]));
+          Elem<E>::store4(ddt + gi, make_float4(sd[0], sd[1], sd[2], sd[3]));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (e < ne) {
+              Elem<E>::store1(du + gi + e, su[e]);
+              Elem<E>::store1(ddt + gi + e, sd[e]);
+            }
+        }
+      }
+    } else {
+#pragma unroll
+    for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+      int r, c;
+      tile_pos<TT>(k, r, c);
+      const int dd = d0 + r, t = t0 + c;
+      if (dd >= a.D || t >= a.L) continue;
+      float4 su = make_float4(0.f, 0.f, 0.f, 0.f), sd = su;
+      for (int v = 0; v < nw; ++v) {
+        const float4 pu = *reinterpret_cast<const float4*>(s_du + (v * kWave + r) * DS + c);
+        const float4 pd = *reinterpret_cast<const float4*>(s_ddt + (v * kWave + r) * DS + c);
+        su.x += pu.x;
+        su.y += pu.y;
+        su.z += pu.z;
+        su.w += pu.w;
+        sd.x += pd.x;
+        sd.y += pd.y;
+        sd.z += pd.z;
+        sd.w += pd.w;
+      }
+      const size_t gi = row0 + static_cast<size_t>(dd) * a.L + t;
+      if (!a.first) {
+        su.x += a.du_acc[gi];
+        sd.x += a.ddt_acc[gi];
+        if (t + 1 < a.L) { su.y += a.du_acc[gi + 1]; sd.y += a.ddt_acc[gi + 1]; }
+        if (t + 2 < a.L) { su.z += a.du_acc[gi + 2]; sd.z += a.ddt_acc[gi + 2]; }
+        if (t + 3 < a.L) { su.w += a.du_acc[gi + 3]; sd.w += a.ddt_acc[gi + 3]; }
+      }
+      if (a.last) {
+        store_row4<VEC>(a.du, gi, t, a.L, su);
+        store_row4<VEC>(a.ddt, gi, t, a.L, sd);
+      } else {
+        store_row4<VEC>(a.du_acc, gi, t, a.L, su);
+        store_row4<VEC>(a.ddt_acc, gi, t, a.L, sd);
+      }
+    }
+    }
+  };
+
   BwdTile nxt;
+  int prev_t0 = -1;  // [B, D, L]: the tile whose du / ddt are still to be finished
   bwd_prefetch<E, VEC, GATED, BLD>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile_hi - 1);
   for (int tile = tile_hi - 1; tile >= tile_lo; --tile) {
     const int t0 = tile * TT;
     const int nsteps = min(TT, a.L - t0);
     __syncthreads();  // the previous tile's LDS readers are done
+    float4 dz_v = make_float4(0.f, 0.f, 0.f, 0.f);
+    size_t dz_off = 0;
+    int dz_t = 0;
+    bool dz_ok = false;
     if constexpr (BLD) {
       store_cols<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
       store_cols_softplus<TT, RS>(s_dt, nxt.dt, a.dt_bias, d0, a.D, t0, a.L);
@@ -1026,6 +1125,7 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
         put_col4(s_gy, RS, c4, step, gy);
       }
     } else {
+    static_assert(RowRegs<TT>::kQ == 1, "one deferred dz store per thread");
 #pragma unroll
     for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
       int r, c;
@@ -1043,7 +1143,10 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
                                          go.y * y.y * (sg.y * (1.f + zz.y * (1.f - sg.y))),
                                          go.z * y.z * (sg.z * (1.f + zz.z * (1.f - sg.z))),
                                          go.w * y.w * (sg.w * (1.f + zz.w * (1.f - sg.w))));
-          store_row4<VEC>(a.dz, row0 + static_cast<size_t>(dd) * a.L + t, t, a.L, dzv);
+          dz_v = dzv;  // stored after the next tile's loads are issued
+          dz_off = row0 + static_cast<size_t>(dd) * a.L + t;
+          dz_t = t;
+          dz_ok = true;
         }
       }
       float* p = s_gy + r * RS + c;
@@ -1056,8 +1159,18 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
     float h0[kNpw];
 #pragma unroll
     for (int j = 0; j < kNpw; ++j) h0[j] = (tile > 0 && dvalid && n0 + j < a.N) ? nxt.h0[j] : 0.f;
-    __syncthreads();
-    if (tile > tile_lo) bwd_prefetch<E, VEC, GATED, BLD>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile - 1);
+    if constexpr (BLD) {
+      __syncthreads();
+      if (tile > tile_lo) bwd_prefetch<E, VEC, GATED, BLD>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile - 1);
+    } else {
+      // the next tile's loads go out before this interval's stores (dz, and
+      // du / ddt of the previous tile, whose LDS partials this barrier
+      // interval still holds)
+      if (tile > tile_lo) bwd_prefetch<E, VEC, GATED, BLD>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile - 1);
+      if (dz_ok) store_row4<VEC>(a.dz, dz_off, dz_t, a.L, dz_v);
+      if (prev_t0 >= 0) finish_dudt(prev_t0);
+      __syncthreads();
+    }
 
     if (wave_active) {
       const float* dtrow = s_dt + lane * RS;
@@ -1187,89 +1300,16 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
         }
       }
     }
-    __syncthreads();
-
-    // finish du / ddt over the waves (states), accumulate over passes
     if constexpr (BLD) {
-      // 4 channels at one step per thread; ddt is taken through the softplus:
-      // d softplus(x) / dx = sigmoid(x), from softplus(x) staged in s_dt
-#pragma unroll
-      for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
-        int step, c4;
-        tile_pos_bld<TT>(k, step, c4);
-        const int dd = d0 + c4, t = t0 + step;
-        if (dd >= a.D || t >= a.L) continue;
-        float su[4] = {0.f, 0.f, 0.f, 0.f}, sd[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int v = 0; v < nw; ++v) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            su[e] += s_du[(v * kWave + c4 + e) * DS + step];
-            sd[e] += s_ddt[(v * kWave + c4 + e) * DS + step];
-          }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sd[e] *= sigmoid_of_softplus(s_dt[(c4 + e) * RS + step]);
-        const size_t gi = (row0 + t) * a.D + dd;
-        const int ne = min(4, a.D - dd);
-        if (!a.first) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (e < ne) {
-              su[e] += a.du_acc[gi + e];
-              sd[e] += a.ddt_acc[gi + e];
-            }
-        }
-        E* du = a.last ? a.du : reinterpret_cast<E*>(a.du_acc);
-        E* ddt = a.last ? a.ddt : reinterpret_cast<E*>(a.ddt_acc);
-        if (VEC) {
-          Elem<E>::store4(du + gi, make_float4(su[0], su[1], su[2], su[3]));
-          Elem<E>::store4(ddt + gi, make_float4(sd[0], sd[1], sd[2], sd[3]));
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (e < ne) {
-              Elem<E>::store1(du + gi + e, su[e]);
-              Elem<E>::store1(ddt + gi + e, sd[e]);
-            }
-        }
-      }
+      __syncthreads();
+      finish_dudt(t0);
     } else {
-#pragma unroll
-    for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
-      int r, c;
-      tile_pos<TT>(k, r, c);
-      const int dd = d0 + r, t = t0 + c;
-      if (dd >= a.D || t >= a.L) continue;
-      float4 su = make_float4(0.f, 0.f, 0.f, 0.f), sd = su;
-      for (int v = 0; v < nw; ++v) {
-        const float4 pu = *reinterpret_cast<const float4*>(s_du + (v * kWave + r) * DS + c);
-        const float4 pd = *reinterpret_cast<const float4*>(s_ddt + (v * kWave + r) * DS + c);
-        su.x += pu.x;
-        su.y += pu.y;
-        su.z += pu.z;
-        su.w += pu.w;
-        sd.x += pd.x;
-        sd.y += pd.y;
-        sd.z += pd.z;
-        sd.w += pd.w;
-      }
-      const size_t gi = row0 + static_cast<size_t>(dd) * a.L + t;
-      if (!a.first) {
-        su.x += a.du_acc[gi];
-        sd.x += a.ddt_acc[gi];
-        if (t + 1 < a.L) { su.y += a.du_acc[gi + 1]; sd.y += a.ddt_acc[gi + 1]; }
-        if (t + 2 < a.L) { su.z += a.du_acc[gi + 2]; sd.z += a.ddt_acc[gi + 2]; }
-        if (t + 3 < a.L) { su.w += a.du_acc[gi + 3]; sd.w += a.ddt_acc[gi + 3]; }
-      }
-      if (a.last) {
-        store_row4<VEC>(a.du, gi, t, a.L, su);
-        store_row4<VEC>(a.ddt, gi, t, a.L, sd);
-      } else {
-        store_row4<VEC>(a.du_acc, gi, t, a.L, su);
-        store_row4<VEC>(a.ddt_acc, gi, t, a.L, sd);
-      }
+      prev_t0 = t0;  // finished while the next tile is staged
     }
-    }
+  }
+  if constexpr (!BLD) {
+    __syncthreads();
+    finish_dudt(prev_t0);
   }
 
   if (dvalid && wave_active) {
