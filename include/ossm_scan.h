@@ -50,7 +50,7 @@ enum {
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
 /* Library ABI version (bumped on any change of the entry points or their
-   behaviour; currently 11). */
+   behaviour; currently 12). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -60,7 +60,9 @@ const char* ossm_last_error(void);
  * Synchronises `stream` and returns (then clears) the device-side error bits
  * of its scratch buffer: bit 0 = a look-back wait gave up (bounded spin
  * exceeded), bit 1 = a workgroup drew an out-of-range ticket.  0 means every
- * launch on this stream since the last check completed its protocol.
+ * launch on this stream since the last check completed its protocol.  Once
+ * ossm_dlinoss_forward_noalloc has run on the current device, the device is
+ * synchronised and the bits of its fixed array are included too.
  */
 uint32_t ossm_device_error_bits(ossm_stream_t stream);
 
@@ -74,6 +76,25 @@ uint32_t ossm_device_error_bits(ossm_stream_t stream);
 int ossm_dlinoss_forward(int variant, const float* a_diag, const float* g_diag,
                          const float* step, const void* bu, void* states, int64_t length,
                          int64_t batch, int64_t ssm, ossm_stream_t stream);
+
+/*
+ * Allocation-free D-LinOSS forward.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments, results and errors as
+ * ossm_dlinoss_forward, but the look-back records live in a fixed 16 MiB
+ * device array (plus a 256-byte header) that the library holds on each GPU it
+ * runs on until the process ends, so the call allocates nothing.  Limit: half
+ * a byte of records per state-step, i.e. at most 33,554,432 state-steps
+ * (L*B*P) per call; larger problems return OSSM_ERR_UNSUPPORTED with a
+ * message.  Every call on a GPU shares that array: calls that overlap on one
+ * GPU (two streams, or two host threads' streams) race and must be ordered by
+ * the caller.  Refuses HIP-graph capture like the other entry points.  Its
+ * device error bits are reported by ossm_device_error_bits.
+ */
+int ossm_dlinoss_forward_noalloc(int variant, const float* a_diag, const float* g_diag,
+                                 const float* step, const void* bu, void* states,
+                                 int64_t length, int64_t batch, int64_t ssm,
+                                 ossm_stream_t stream);
 
 /*
  * D-LinOSS backward, replaces dlinoss_<v>_backward:

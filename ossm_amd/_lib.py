@@ -27,6 +27,8 @@ _SIGNATURES = {
     "ossm_device_error_bits": (ctypes.c_uint32, [_vp]),
     "ossm_dlinoss_forward": (
         ctypes.c_int, [ctypes.c_int, _fp, _fp, _fp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_dlinoss_forward_noalloc": (
+        ctypes.c_int, [ctypes.c_int, _fp, _fp, _fp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
     "ossm_dlinoss_backward": (
         ctypes.c_int,
         [ctypes.c_int, _fp, _fp, _fp, _vp, _vp, _vp, _fp, _fp, _fp, _vp, _c_int64, _c_int64,

@@ -43,6 +43,7 @@
 #include <cstdlib>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -504,40 +505,63 @@ Tile parse_tile(const char* env, Tile dflt) {
   X(16, 8, 1, 1) X(16, 8, 4, 2) X(16, 8, 2, 2) X(16, 4, 1, 1) X(8, 8, 1, 1) X(8, 8, 4, 2)      \
   X(32, 4, 1, 1) X(32, 4, 2, 2) X(8, 16, 1, 1)
 
-template <class Model>
-int launch_forward(const typename Model::Params& prm, const void* in, void* out, int64_t L,
-                   int64_t nc, hipStream_t stream) {
-  StreamCall call(stream);
-  if (call.status()) return call.status();
+// Launch geometry of a forward scan: the tile, the chunk grid and the bytes
+// of look-back records it needs (two 4-word records per chunk and channel).
+struct FwdPlan {
+  Tile tile;
+  int64_t n_chunks, n_groups, total;
+  size_t rec_bytes;
+};
+
+FwdPlan fwd_plan(int64_t L, int64_t nc) {
   static const Tile tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{16, 8, 1, 1});
+  FwdPlan pl;
+  pl.tile = tile;
   const int64_t CL = int64_t(tile.T) * tile.W;
-  const int64_t n_chunks = (L + CL - 1) / CL;
-  const int64_t n_groups = (nc + kWave - 1) / kWave;
-  if (n_chunks * n_groups > INT_MAX)
-    return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
-  const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
-  void* payload = nullptr;
-  LaunchSync sync{};
-  if (int rc = acquire_scratch(call, rec_bytes, n_chunks * n_groups, &payload, &sync)) return rc;
-  const dim3 grid(static_cast<unsigned>(n_chunks * n_groups));
+  pl.n_chunks = (L + CL - 1) / CL;
+  pl.n_groups = (nc + kWave - 1) / kWave;
+  pl.total = pl.n_chunks * pl.n_groups;
+  pl.rec_bytes = static_cast<size_t>(pl.n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
+  return pl;
+}
+
+// Enqueues the forward kernel of plan `pl` with look-back records at
+// `payload` and launch bookkeeping `sync`.  The caller undoes its ticket
+// reservation when this returns an error (nothing was launched).
+template <class Model>
+int enqueue_forward(const FwdPlan& pl, const typename Model::Params& prm, const void* in, void* out,
+                    int64_t L, int64_t nc, hipStream_t stream, void* payload, const LaunchSync& sync) {
+  const Tile& tile = pl.tile;
+  const dim3 grid(static_cast<unsigned>(pl.total));
   bool launched = false;
 #define OSSM_LAUNCH_FWD(TT, WW, OO)                                                           \
   if (!launched && tile.T == TT && tile.W == WW && tile.O == OO) {                            \
     hipLaunchKernelGGL((osc_forward_kernel<Model, TT, WW, OO>), grid, dim3(WW * kWave), 0, stream, \
                        prm, static_cast<const typename Model::In*>(in),                       \
                        static_cast<float4*>(out), static_cast<int>(L), static_cast<int>(nc),  \
-                       static_cast<int>(n_groups), static_cast<int>(n_chunks),                \
+                       static_cast<int>(pl.n_groups), static_cast<int>(pl.n_chunks),          \
                        static_cast<unsigned long long*>(payload), sync);                      \
     launched = true;                                                                          \
   }
   OSSM_FWD_TILES(OSSM_LAUNCH_FWD)
 #undef OSSM_LAUNCH_FWD
-  if (!launched) {
-    release_unlaunched(call, n_chunks * n_groups);
-    return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_FWD names no built tile");
-  }
-  if (int rc = launch_check("osc_forward_kernel")) {
-    release_unlaunched(call, n_chunks * n_groups);
+  if (!launched) return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_FWD names no built tile");
+  return launch_check("osc_forward_kernel");
+}
+
+template <class Model>
+int launch_forward(const typename Model::Params& prm, const void* in, void* out, int64_t L,
+                   int64_t nc, hipStream_t stream) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
+  const FwdPlan pl = fwd_plan(L, nc);
+  if (pl.total > INT_MAX)
+    return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
+  void* payload = nullptr;
+  LaunchSync sync{};
+  if (int rc = acquire_scratch(call, pl.rec_bytes, pl.total, &payload, &sync)) return rc;
+  if (int rc = enqueue_forward<Model>(pl, prm, in, out, L, nc, stream, payload, sync)) {
+    release_unlaunched(call, pl.total);
     return rc;
   }
   return OSSM_OK;
@@ -625,11 +649,144 @@ int dlinoss_backward_v(const float* a, const float* g, const float* dt, const vo
 }
 
 }  // namespace
+
+// ---- allocation-free D-LinOSS forward ------------------------------------------
+// ossm_dlinoss_forward_noalloc keeps its look-back records in this array: a
+// 256-byte header (the launch-ticket counter at kHdrTicket, the error bits at
+// kHdrErr) and kNoAllocRecordBytes of tagged records.  Device memory is
+// zero at load, which is the state the protocol starts from (tag 0 is never a
+// launch's tag, the ticket counter matches the host's count of 0).  Each GPU
+// holds its own copy until the process ends; its address on a device comes
+// from hipGetSymbolAddress, taken once per device on that device's first
+// call.  Every call on a GPU shares its copy: records are tagged per launch,
+// so nothing needs clearing between calls, but calls that overlap on one GPU
+// (several streams, or several processes' launches interleaved) race.
+constexpr size_t kNoAllocRecordBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kHdrBytes + kNoAllocRecordBytes];
+
+constexpr int kNoAllocMaxDevices = 64;
+struct NoAllocDevice {
+  std::mutex mu;                        // held from bookkeeping through the launch
+  char* ptr = nullptr;                  // device address of `scratch` on this device
+  unsigned int epoch = 0;               // tag of the most recent launch
+  unsigned long long next_ticket = 0;   // device ticket counter after all queued launches
+};
+NoAllocDevice g_noalloc[kNoAllocMaxDevices];
+
+// The address of `scratch` on device `dev` (current), looked up once.
+// Called with g_noalloc[dev].mu held.
+int noalloc_address(int dev) {
+  NoAllocDevice& s = g_noalloc[dev];
+  if (s.ptr != nullptr) return OSSM_OK;
+  void* p = nullptr;
+  if (int rc = hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"))
+    return rc;
+  s.ptr = static_cast<char*>(p);
+  return OSSM_OK;
+}
+
+uint32_t noalloc_error_bits(int dev) {
+  if (dev < 0 || dev >= kNoAllocMaxDevices) return 0;
+  NoAllocDevice& s = g_noalloc[dev];
+  std::lock_guard<std::mutex> hold(s.mu);
+  if (s.ptr == nullptr) return 0;  // the allocation-free path never ran here
+  // the array is shared by every stream of the device: drain them all
+  if (hipDeviceSynchronize() != hipSuccess) return 0xffffffffu;
+  uint32_t bits = 0;
+  unsigned long long t = 0;
+  if (hipMemcpy(&bits, s.ptr + kHdrErr, sizeof(bits), hipMemcpyDeviceToHost) != hipSuccess ||
+      hipMemcpy(&t, s.ptr + kHdrTicket, sizeof(t), hipMemcpyDeviceToHost) != hipSuccess)
+    return 0xffffffffu;
+  if (scan_order_by_ticket()) s.next_ticket = t;  // every workgroup drew exactly one ticket
+  if (bits != 0) {
+    const uint32_t zero = 0;
+    (void)hipMemcpy(s.ptr + kHdrErr, &zero, sizeof(zero), hipMemcpyHostToDevice);
+  }
+  return bits;
+}
+
+namespace {
+
+template <int V>
+int dlinoss_forward_noalloc_v(const FwdPlan& pl, const float* a, const float* g, const float* dt,
+                              const void* bu, void* states, int64_t L, int64_t B, int64_t P,
+                              hipStream_t stream, void* payload, const LaunchSync& sync) {
+  typename Dlinoss<V>::Params prm{a, g, dt, static_cast<int>(P)};
+  return enqueue_forward<Dlinoss<V>>(pl, prm, bu, states, L, B * P, stream, payload, sync);
+}
+
+}  // namespace
 }  // namespace ossm
 
 using namespace ossm;
 
 extern "C" {
+
+int ossm_dlinoss_forward_noalloc(int variant, const float* a_diag, const float* g_diag,
+                                 const float* step, const void* bu, void* states, int64_t length,
+                                 int64_t batch, int64_t ssm, ossm_stream_t stream_v) {
+  clear_error();
+  if (int rc = check_sizes(length, batch, ssm, "dlinoss_forward_noalloc")) return rc;
+  if (length == 0 || batch == 0 || ssm == 0) return OSSM_OK;
+  if (!a_diag || !g_diag || !step || !bu || !states)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "dlinoss_forward_noalloc: null pointer");
+  if (variant < OSSM_DLINOSS_IMEX1 || variant > OSSM_DLINOSS_EX)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "Unknown D-LinOSS variant code");
+  const FwdPlan pl = fwd_plan(length, batch * ssm);
+  if (pl.total > INT_MAX)
+    return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
+  if (pl.rec_bytes > kNoAllocRecordBytes)
+    return set_error(OSSM_ERR_UNSUPPORTED,
+                     "dlinoss_forward_noalloc: this problem needs " + std::to_string(pl.rec_bytes) +
+                         " bytes of look-back records, more than the fixed " +
+                         std::to_string(kNoAllocRecordBytes) +
+                         "-byte scratch (half a byte per state-step: at most 33,554,432 "
+                         "state-steps per call); use ossm_dlinoss_forward");
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  int dev = 0;
+  if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev >= kNoAllocMaxDevices)
+    return set_error(OSSM_ERR_UNSUPPORTED, "dlinoss_forward_noalloc: device index above 63");
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  const hipError_t ce = hipStreamIsCapturing(stream, &cap);
+  if (ce != hipSuccess || cap != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return set_error(OSSM_ERR_UNSUPPORTED,
+                     "dlinoss_forward_noalloc: the stream is being captured into a HIP graph; the "
+                     "launch tag and ticket base are chosen on the host per call: run it eagerly");
+  }
+  NoAllocDevice& s = g_noalloc[dev];
+  std::lock_guard<std::mutex> hold(s.mu);
+  if (int rc = noalloc_address(dev)) return rc;
+  const bool by_ticket = scan_order_by_ticket();
+  s.epoch += 1;
+  if (s.epoch == 0) s.epoch = 1;
+  LaunchSync sync{};
+  sync.ticket = reinterpret_cast<unsigned long long*>(s.ptr + kHdrTicket);
+  sync.err = reinterpret_cast<unsigned int*>(s.ptr + kHdrErr);
+  sync.base = s.next_ticket;
+  sync.tag = s.epoch;
+  sync.use_ticket = by_ticket ? 1 : 0;
+  if (by_ticket) s.next_ticket += pl.total;
+  void* payload = s.ptr + kHdrBytes;
+  int rc = OSSM_OK;
+  switch (variant) {
+    case OSSM_DLINOSS_IMEX1:
+      rc = dlinoss_forward_noalloc_v<OSSM_DLINOSS_IMEX1>(pl, a_diag, g_diag, step, bu, states, length, batch, ssm, stream, payload, sync);
+      break;
+    case OSSM_DLINOSS_IMEX2:
+      rc = dlinoss_forward_noalloc_v<OSSM_DLINOSS_IMEX2>(pl, a_diag, g_diag, step, bu, states, length, batch, ssm, stream, payload, sync);
+      break;
+    case OSSM_DLINOSS_IM:
+      rc = dlinoss_forward_noalloc_v<OSSM_DLINOSS_IM>(pl, a_diag, g_diag, step, bu, states, length, batch, ssm, stream, payload, sync);
+      break;
+    default:
+      rc = dlinoss_forward_noalloc_v<OSSM_DLINOSS_EX>(pl, a_diag, g_diag, step, bu, states, length, batch, ssm, stream, payload, sync);
+      break;
+  }
+  if (rc != OSSM_OK && by_ticket) s.next_ticket -= pl.total;  // nothing was launched
+  return rc;
+}
 
 int ossm_dlinoss_forward(int variant, const float* a_diag, const float* g_diag, const float* step,
                          const void* bu, void* states, int64_t length, int64_t batch, int64_t ssm,

@@ -159,7 +159,7 @@ void release_unlaunched(StreamCall& call, uint64_t n_workgroups) {
 
 extern "C" {
 
-int ossm_abi_version(void) { return 11; }
+int ossm_abi_version(void) { return 12; }
 
 const char* ossm_last_error(void) { return ossm::g_last_error.c_str(); }
 
@@ -167,10 +167,12 @@ uint32_t ossm_device_error_bits(ossm_stream_t stream_v) {
   hipStream_t stream = static_cast<hipStream_t>(stream_v);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0xffffffffu;
+  const uint32_t fixed_bits = ossm::noalloc_error_bits(dev);
+  if (fixed_bits == 0xffffffffu) return fixed_bits;
   ossm::StreamState& st = ossm::state_of(dev, stream);
   std::lock_guard<std::recursive_mutex> hold(st.call);
   ossm::Scratch& s = st.scratch;
-  if (s.base == nullptr) return 0;
+  if (s.base == nullptr) return fixed_bits;
   if (hipStreamSynchronize(stream) != hipSuccess) return 0xffffffffu;
   uint32_t bits = 0;
   char* base = static_cast<char*>(s.base);
@@ -185,7 +187,7 @@ uint32_t ossm_device_error_bits(ossm_stream_t stream_v) {
       ossm::scan_order_by_ticket())
     s.next_ticket = t;
   if (bits != 0) (void)hipMemset(base + ossm::kHdrErr, 0, sizeof(bits));
-  return bits;
+  return bits | fixed_bits;
 }
 
 }  // extern "C"

@@ -88,4 +88,9 @@ void release_unlaunched(StreamCall& call, uint64_t n_workgroups);
 // Launch-error check after a kernel launch (reference: C10_CUDA_KERNEL_LAUNCH_CHECK).
 int launch_check(const char* what);
 
+// Error bits of the allocation-free forward's fixed scratch on device `dev`
+// (0 if that path never ran there); synchronises the device, clears the bits
+// and re-reads its ticket counter.  Defined beside that scratch.
+uint32_t noalloc_error_bits(int dev);
+
 }  // namespace ossm

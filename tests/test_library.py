@@ -56,7 +56,7 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     # every declared symbol has a ctypes signature in the binding
     assert set(_declared_functions()) == set(_lib.EXPORTED)
-    assert _lib.load().ossm_abi_version() == 11
+    assert _lib.load().ossm_abi_version() == 12
 
 
 def test_dropin_module_has_every_reference_name():

@@ -1,0 +1,64 @@
+"""GPU test of the allocation-free entry point ossm_dlinoss_forward_noalloc,
+called through the C ABI and checked against ossm_dlinoss_forward (the
+allocating entry point with the same kernels) to the north-star tolerance:
+two calls in a row, the second smaller, then a problem above the fixed
+scratch's limit, which must be refused with a message."""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from tests.gpu_util import announce, assert_close, dlinoss_inputs, need_gpu, no_device_errors, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+RTOL, ATOL = 1e-4, 1e-5
+LIMIT_STATE_STEPS = 1 << 25  # 16 MiB of records at half a byte per state-step
+
+
+@pytest.fixture(scope="module")
+def lib():
+    need_gpu()
+    from ossm_amd import _lib
+
+    return _lib
+
+
+def _call(lib, name, variant, a, g, dt, bu, out):
+    L, B, P = bu.shape
+    stream = torch.cuda.current_stream().cuda_stream
+    return getattr(lib.load(), name)(variant, a.data_ptr(), g.data_ptr(), dt.data_ptr(), bu.data_ptr(),
+                                     out.data_ptr(), L, B, P, stream)
+
+
+@pytest.mark.parametrize("variant", [0, 2], ids=["imex1", "im"])
+def test_noalloc_forward_matches_allocating_entry(lib, variant):
+    names = {0: "imex1", 2: "im"}
+    for L, B, P, seed in ((4096, 32, 128, 11), (777, 3, 70, 12)):  # config 2, then smaller
+        a, g, dt, bu, _ = dlinoss_inputs(L, B, P, seed=seed, variant=names[variant])
+        ad, gd, dtd, bud = (to_dev(x) for x in (a, g, dt, bu))
+        ref = torch.empty((L, B, P, 2), dtype=torch.complex64, device="cuda")
+        got = torch.full((L, B, P, 2), float("nan"), dtype=torch.complex64, device="cuda")
+        announce(f"noalloc dlinoss {names[variant]} L={L} B={B} P={P}")
+        lib.check(_call(lib, "ossm_dlinoss_forward", variant, ad, gd, dtd, bud, ref))
+        lib.check(_call(lib, "ossm_dlinoss_forward_noalloc", variant, ad, gd, dtd, bud, got))
+        torch.cuda.synchronize()
+        assert_close(to_np(got), to_np(ref), RTOL, ATOL, f"noalloc vs allocating L={L} B={B} P={P}")
+        no_device_errors()
+
+
+def test_noalloc_forward_rejects_problems_above_its_scratch(lib):
+    L, B, P = 4096, 64, 160  # 41.9M state-steps: 21 MB of records
+    assert L * B * P > LIMIT_STATE_STEPS
+    small = torch.zeros(1, dtype=torch.float32, device="cuda")
+    announce("noalloc dlinoss above the fixed scratch")
+    rc = lib.load().ossm_dlinoss_forward_noalloc(0, small.data_ptr(), small.data_ptr(), small.data_ptr(),
+                                                 small.data_ptr(), small.data_ptr(), L, B, P,
+                                                 torch.cuda.current_stream().cuda_stream)
+    assert rc == 3  # OSSM_ERR_UNSUPPORTED, before anything is launched
+    msg = lib.load().ossm_last_error().decode()
+    assert "fixed" in msg and "ossm_dlinoss_forward" in msg, msg
+    no_device_errors()
