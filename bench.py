@@ -21,8 +21,9 @@ One JSON line is printed.  Besides the contract fields:
                 WRITE_SIZE (profiles/dlinoss_imex1_config2_pmc.json) or null
   cpu_baseline  the C restatement of the reference's CPU kernels (oracle/) on
                 the same workload on this host's cores
-  detail        per-direction figures, the other BASELINE configs and the fused
-                layers (D-LinOSS layer, Mamba mixer)
+  detail        per-direction figures, torch elementwise kernels moving the
+                same bytes (``hbm_reference``), the other BASELINE configs and
+                the fused layers (D-LinOSS layer, Mamba mixer)
 
 ``--calibrate-copy`` runs only a device-to-device copy of known size, for
 scaling the FETCH_SIZE / WRITE_SIZE counters.
@@ -149,6 +150,28 @@ def _ev_time(torch, fn, reps: int, warm: int) -> float:
         e1.record()
     torch.cuda.synchronize()
     return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+
+
+def _hbm_reference(torch, dev, units: int, fwd_ms: float, bwd_ms: float, reps: int = 20) -> dict:
+    """torch's own elementwise kernels moving the D-LinOSS scans' algorithmic
+    bytes, timed like them (fence-free events around each launch, a device spin
+    ahead): an add of two complex64 [L,B,P] tensors into a third (the
+    backward's 8 + 8 bytes read and 8 written per state-step) and a broadcast
+    multiply of one into [L,B,P,2] (the forward's 8 read, 16 written).  That
+    is what plain HBM-bound library code reaches on this box with the same
+    bytes; ``*_vs_torch`` is the torch time over the scan's."""
+    x = torch.randn(units, dtype=torch.complex64, device=dev)
+    y = torch.randn_like(x)
+    z = torch.empty_like(x)
+    two = torch.ones(2, dtype=torch.complex64, device=dev)
+    s = torch.empty(units, 2, dtype=torch.complex64, device=dev)
+    add_ms = _ev_time(torch, lambda: torch.add(x, y, out=z), reps, 3)
+    mul_ms = _ev_time(torch, lambda: torch.mul(x[:, None], two, out=s), reps, 3)
+    del x, y, z, s
+    return {"add_like_backward_ms": add_ms, "add_GBps": 24 * units / (add_ms / 1e3) / 1e9,
+            "backward_vs_torch": add_ms / bwd_ms,
+            "mul_like_forward_ms": mul_ms, "mul_GBps": 24 * units / (mul_ms / 1e3) / 1e9,
+            "forward_vs_torch": mul_ms / fwd_ms}
 
 
 # ----------------------------------------------------------------- inputs
@@ -606,6 +629,7 @@ def main() -> int:
         "device_error_bits": err_bits,
     }
     del st
+    detail["hbm_reference"] = _hbm_reference(torch, dev, units, fwd_ms, bwd_ms)
     if not args.no_detail:
         del a, gam, dt, bu, go
         torch.cuda.empty_cache()

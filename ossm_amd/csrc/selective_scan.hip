@@ -35,9 +35,17 @@
 //   dB_t  = sum_d gacc dt u,   dC_t = sum_d gy h_t
 // A tile is done in two 8-step halves, the later one first: the forward is
 // re-run from the checkpoint (once more over the first half, to reach the
-// second), each half's h and exp(dt A) are held in registers while the adjoint
-// runs over it in reverse.  Holding all 16 steps costs 64 more VGPRs: one wave
-// per SIMD instead of two.
+// second; that pass keeps the first half's exp(dt A) for later), each half's h
+// and exp(dt A) are held in registers while the adjoint runs over it in
+// reverse.  Holding all 16 steps' states costs 64 more VGPRs: one wave per
+// SIMD instead of two.
+// Time split: with fewer (batch row, 64-channel) rows than twice the CUs the
+// grid's z dimension cuts each row's tiles into 2 or 4 segments; a segment
+// first carries the adjoint from the end of the sequence through the later
+// segments' tiles (adjoint only: no recompute, no sums), with the main loop's
+// per-step arithmetic, so the carry is bitwise the one the later segments
+// reach.  The forward splits the same way when there are fewer rows than CUs,
+// re-running h only over the earlier segments' tiles.
 // dB/dC are sums over channels: each wave reduces its 64 lanes with the
 // gfx950 cross-row swaps (v_permlane32_swap / v_permlane16_swap) and row DPP,
 // and writes one partial per 64-channel tile; dA partials are per batch row.
@@ -1188,8 +1196,14 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
       // and contribute exact zeros.  Each step's LDS operands are read one step
       // ahead; the empty asm with a memory clobber after every step keeps the
       // compiler from hoisting all of them to the top (registers).
-      auto sub_tile = [&](auto s0_tag, const float (&hst)[kNpw]) {
+      // exp(dt A) of the first half, kept from the pass that finds the state
+      // in the middle of the tile (so the first half does not take its
+      // exponentials twice)
+      float dA0[HT][kNpw];
+      auto sub_tile = [&](auto s0_tag, const float (&hst)[kNpw], auto cached_tag) {
         constexpr int s0 = decltype(s0_tag)::value;
+        constexpr bool cached = decltype(cached_tag)::value;
+        static_assert(!cached || s0 == 0, "only the first half has cached exponentials");
         float hs[HT][kNpw], dAs[HT][kNpw];
         {
           float h[kNpw];
@@ -1209,7 +1223,7 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
             const float dtu = dtv * uv;
 #pragma unroll
             for (int j = 0; j < kNpw; ++j) {
-              const float dA = fast_exp2(dtv * A2[j]);
+              const float dA = cached ? dA0[i][j] : fast_exp2(dtv * A2[j]);
               h[j] = fmaf(dA, h[j], dtu * Bv[j]);
               hs[i][j] = h[j];
               dAs[i][j] = dA;
@@ -1267,8 +1281,9 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
       };
 
       // The second half first (from the state after step HT - 1, found by one
-      // more forward pass over the first half), then the first half.  A tile
-      // that ends within its first half skips the second: all padding.
+      // more forward pass over the first half, whose exponentials the first
+      // half then reuses), then the first half.  A tile that ends within its
+      // first half skips the second: all padding.
       if (nsteps > HT) {
         float hmid[kNpw];
 #pragma unroll
@@ -1280,11 +1295,16 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
           const float4 Bt = *reinterpret_cast<const float4*>(Bcol + i * kPassStates);
           const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
 #pragma unroll
-          for (int j = 0; j < kNpw; ++j) hmid[j] = fmaf(fast_exp2(dtv * A2[j]), hmid[j], dtu * Bv[j]);
+          for (int j = 0; j < kNpw; ++j) {
+            dA0[i][j] = fast_exp2(dtv * A2[j]);
+            hmid[j] = fmaf(dA0[i][j], hmid[j], dtu * Bv[j]);
+          }
         }
-        sub_tile(std::integral_constant<int, HT>{}, hmid);
+        sub_tile(std::integral_constant<int, HT>{}, hmid, std::false_type{});
+        sub_tile(std::integral_constant<int, 0>{}, h0, std::true_type{});
+      } else {
+        sub_tile(std::integral_constant<int, 0>{}, h0, std::false_type{});
       }
-      sub_tile(std::integral_constant<int, 0>{}, h0);
 
       // lane (row r, column c) holds the tile-partials of step t0 + c:
       // r = 0: dB[n0], dB[n0+1]; r = 1: dB[n0+2], dB[n0+3]; r = 2, 3: same for dC
