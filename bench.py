@@ -265,7 +265,7 @@ def cpu_baseline(L, B, P, budget_s=12.0):
         run()
     times = []
     t_start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 400):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
@@ -438,6 +438,24 @@ def _detail_configs(torch, K, dev, reps=10):
         tfb = _ev_time(torch, step, reps, 3)
         out[key] = {"fwd_ms": tf, "fwd_bwd_ms": tfb, "d_inner": 2 * dm, "d_state": 16}
         del mixer, u, gy
+    # LinOSS layer (IM and IMEX) at config 1's shape: the device scan forward and
+    # its native backward, with the layer's projections (torch)
+    from ossm_amd.linoss import LinOSSLayer
+    L, B, H, P = 1024, 8, 64, 64
+    for disc in ("IM", "IMEX"):
+        torch.manual_seed(10)
+        layer = LinOSSLayer(P, H, disc).to(dev)
+        u = torch.randn(B, L, H, device=dev, requires_grad=True)
+        gy = torch.randn(B, L, H, device=dev)
+        with torch.no_grad():
+            tf = _ev_time(torch, lambda: layer(u), reps, 3)
+
+        def lstep():
+            layer(u).backward(gy)
+
+        tfb = _ev_time(torch, lstep, reps, 3)
+        out[f"linoss_layer_{disc.lower()}_c1_shape"] = {"fwd_ms": tf, "fwd_bwd_ms": tfb}
+        del layer, u, gy
     torch.cuda.empty_cache()
     return out
 
