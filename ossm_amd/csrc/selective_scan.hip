@@ -5,15 +5,18 @@
 // per (batch b, channel d), tensors u, dt, z, out [B,D,L]; A [D,N]; B, C [B,L,N].
 //
 // Parallel decomposition
-//   A workgroup owns one batch row b and 64 consecutive channels d and walks
-//   the whole sequence; up to 16 states run per launch ("pass"), 4 per lane in
+//   A workgroup owns one batch row b and 64 (forward: 64 or 32) consecutive
+//   channels d and walks the sequence (or one time segment of it); up to 16
+//   states run per launch ("pass"), 4 (forward: 4 or 2) per lane in
 //   registers; larger N runs ceil(N/16) passes that accumulate y (forward) and
 //   du/ddt (backward) in the output tensors.  Time is processed in tiles
 //   staged through LDS: u, dt (and the gated upstream gradient) are loaded with
 //   coalesced row reads and read back per channel.
-//   Forward: lane = (channel c = lane % 16, state group g = lane / 16), so a
-//   wave holds all 16 states of 16 channels and y is summed over the states
-//   inside the wave (cross-row swaps), with no LDS round trip.
+//   Forward: lane = (channel, state group) with 4 states per lane (16
+//   channels per wave, 64 per workgroup) or, when that leaves the SIMDs short
+//   of waves, 2 (8 channels per wave, 32 per workgroup); a wave holds all 16
+//   states of its channels and y is summed over the states inside the wave
+//   (cross-row swaps and DPP), with no LDS round trip.
 //   Backward: lane = channel and wave w carries states 4w .. 4w + 3, so the
 //   sums over channels (dB, dC) finish inside a wave and the sums over states
 //   (du, ddt) across the waves through LDS.
@@ -142,6 +145,17 @@ __device__ __forceinline__ void reduce8(const float (&v)[8], float& o0, float& o
   o1 = row_allreduce(s1 + s3);
 }
 
+__device__ __forceinline__ void unpack(float4 v, float (&o)[4]) {
+  o[0] = v.x;
+  o[1] = v.y;
+  o[2] = v.z;
+  o[3] = v.w;
+}
+__device__ __forceinline__ void unpack(float2 v, float (&o)[2]) {
+  o[0] = v.x;
+  o[1] = v.y;
+}
+
 // ---- element types -----------------------------------------------------------
 // The row tensors (u, dt, z, out, grads) and B/C are fp32 or bf16 in HBM; the
 // recurrence, its state and every sum run in fp32.  bf16 is stored as its
@@ -190,17 +204,19 @@ struct Elem<bf16_t> {
 };
 
 // ---- tile staging -----------------------------------------------------------
-// Every launch runs kThreads threads.  A tile of a [.., L] tensor is 64 rows
-// (channels d0..d0+63) x TT steps; thread i owns the float4 column groups
+// Every launch runs kThreads threads.  A tile of a [.., L] tensor is ROWS rows
+// (channels d0..d0+ROWS-1: 64, or 32 for the forward with 2 states per lane)
+// x TT steps; thread i owns the float4 column groups
 // q = i + k * kThreads of it, so its global loads are 16-byte row segments,
 // consecutive threads covering a row.  Loads go to registers first and are
 // written to LDS one tile later: the next tile's HBM reads overlap this
 // tile's recurrence.
 constexpr int kThreads = kMaxWaves * kWave;
 
-template <int TT>
+template <int TT, int ROWS = kWave>
 struct RowRegs {
-  static constexpr int kQ = kWave * TT / 4 / kThreads;
+  static constexpr int kQ = ROWS * TT / 4 / kThreads;
+  static_assert(kQ >= 1, "a tile has at least one float4 per thread");
   float4 v[kQ];
 };
 
@@ -217,11 +233,11 @@ __device__ __forceinline__ void tile_pos(int k, int& row, int& c) {
 // address, so the loads carry no branches and all stay in flight together;
 // they are zeroed when the tile is written to LDS (store_rows), not here, so
 // that nothing waits on the loads before then.
-template <int TT, bool VEC, class E>
-__device__ __forceinline__ void load_rows(RowRegs<TT>& r, const E* __restrict__ g,
+template <int TT, bool VEC, class E, int ROWS>
+__device__ __forceinline__ void load_rows(RowRegs<TT, ROWS>& r, const E* __restrict__ g,
                                           size_t row0, int d0, int D, int t0, int L) {
 #pragma unroll
-  for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+  for (int k = 0; k < RowRegs<TT, ROWS>::kQ; ++k) {
     int row, c;
     tile_pos<TT>(k, row, c);
     const int t = t0 + c;
@@ -245,8 +261,8 @@ __device__ __forceinline__ bool row_ok(int k, int e, int d0, int D, int t0, int 
   return d0 + row < D && t0 + c + e < L;
 }
 
-template <int TT>
-__device__ __forceinline__ float4 masked(const RowRegs<TT>& r, int k, int d0, int D, int t0,
+template <int TT, int ROWS>
+__device__ __forceinline__ float4 masked(const RowRegs<TT, ROWS>& r, int k, int d0, int D, int t0,
                                          int L) {
   const float4 v = r.v[k];
   return make_float4(row_ok<TT>(k, 0, d0, D, t0, L) ? v.x : 0.f,
@@ -255,11 +271,11 @@ __device__ __forceinline__ float4 masked(const RowRegs<TT>& r, int k, int d0, in
                      row_ok<TT>(k, 3, d0, D, t0, L) ? v.w : 0.f);
 }
 
-template <int TT, int RS>
-__device__ __forceinline__ void store_rows(float* __restrict__ s, const RowRegs<TT>& r, int d0,
+template <int TT, int RS, int ROWS>
+__device__ __forceinline__ void store_rows(float* __restrict__ s, const RowRegs<TT, ROWS>& r, int d0,
                                            int D, int t0, int L) {
 #pragma unroll
-  for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+  for (int k = 0; k < RowRegs<TT, ROWS>::kQ; ++k) {
     int row, c;
     tile_pos<TT>(k, row, c);
     const float4 v = masked<TT>(r, k, d0, D, t0, L);
@@ -449,31 +465,61 @@ struct FwdArgs {
   const float* dt_bias;
 };
 
-// vec4: N % 4 == 0 and chunk_states 16-byte aligned, so a lane whose four
-// states all lie below N stores them with one 16-byte store (the four lanes
-// of a channel: 64 contiguous bytes); lanes past N store nothing.
-__device__ __forceinline__ void write_ckpt(float* ckpt, size_t lane_row, int slot, int N,
-                                           int n0, const float (&h)[kNpw], bool vec4) {
+// The forward's lane layout for NPW states per lane: lane = (channel
+// c = lane % CW, state group g = lane / CW), GR = 16 / NPW groups, so a wave
+// holds all 16 states of CW = 64 / GR channels and a workgroup 4 CW channels.
+// After the y reduction a lane holds SEG = 32 / GR output steps of its channel:
+//   NPW = 4: steps 4g..4g+3 and 16+4g..16+4g+3 (the four lanes of a channel
+//            cover 16 contiguous steps, 64 bytes of fp32, per 4-step access);
+//   NPW = 2: steps 4g..4g+3 (the eight lanes of a channel cover the tile's 32
+//            steps, 128 bytes).
+// NPW = 2 has twice the waves for the same work (at BASELINE config 4, 768
+// workgroups on 256 CUs instead of 384) for a third reduction stage and twice
+// the per-lane dt / u reads per state.
+template <int NPW>
+struct FwdLayout {
+  static_assert(NPW == 4 || NPW == 2, "4 or 2 states per lane");
+  static constexpr int kGroups = kPassStates / NPW;
+  static constexpr int kWaveCh = kWave / kGroups;
+  static constexpr int kRows = kMaxWaves * kWaveCh;
+  static constexpr int kSeg = kFwdTile / kGroups;
+  static __device__ __forceinline__ int step(int g, int k) {
+    if constexpr (NPW == 4) return (k < 4 ? 0 : 12) + 4 * g + k;
+    else return 4 * g + k;
+  }
+};
+
+// vec: N % 4 == 0 and chunk_states 16-byte aligned, so a lane whose NPW
+// states all lie below N stores them with one 16-byte (8-byte) store (the
+// lanes of a channel: 64 contiguous bytes); lanes past N store nothing.
+template <int NPW>
+__device__ __forceinline__ void write_ckpt(float* ckpt, size_t lane_row, int slot, int N, int n0,
+                                           const float (&h)[NPW], bool vec) {
   const int c = slot >> 1, half = slot & 1;
   float* p = ckpt + lane_row + static_cast<size_t>(c) * 2 * N + half * N;
-  if (vec4 && n0 + kNpw <= N) {
-    *reinterpret_cast<float4*>(p + n0) = make_float4(h[0], h[1], h[2], h[3]);
+  if (vec && n0 + NPW <= N) {
+    if constexpr (NPW == 4) {
+      *reinterpret_cast<float4*>(p + n0) = make_float4(h[0], h[1], h[2], h[3]);
+    } else {
+      *reinterpret_cast<float2*>(p + n0) = make_float2(h[0], h[1]);
+    }
     return;
   }
 #pragma unroll
-  for (int j = 0; j < kNpw; ++j)
+  for (int j = 0; j < NPW; ++j)
     if (n0 + j < N) p[n0 + j] = h[j];
 }
 
+template <int ROWS>
 struct FwdTile {
-  RowRegs<kFwdTile> u, dt;
+  RowRegs<kFwdTile, ROWS> u, dt;
   StateRegs<kFwdTile> B, C;
 };
 
 // row0: (b, 0, 0) of the [B, D, L] tensors; with BLD, bl0 = b * L is the
 // first row of batch b and each tensor adds its own row stride.
-template <class E, bool VEC, bool BLD>
-__device__ __forceinline__ void fwd_prefetch(FwdTile& f, const FwdArgs<E>& a, size_t row0,
+template <class E, bool VEC, bool BLD, int ROWS>
+__device__ __forceinline__ void fwd_prefetch(FwdTile<ROWS>& f, const FwdArgs<E>& a, size_t row0,
                                              size_t bc0, int d0, int t0) {
   if constexpr (BLD) {
     load_cols<kFwdTile, VEC>(f.u, a.u, row0 * a.ld_u, a.ld_u, d0, a.D, t0, a.L);
@@ -486,26 +532,14 @@ __device__ __forceinline__ void fwd_prefetch(FwdTile& f, const FwdArgs<E>& a, si
   load_states<kFwdTile>(f.C, a.Cm, bc0, a.ld_bc, t0, a.L, a.N, a.n_base);
 }
 
-// The forward's lane layout: lane = (channel c = lane % 16, state group
-// g = lane / 16), so a wave holds all 16 states of 16 channels and a lane's
-// finished outputs are 8 consecutive steps of its channel.
-constexpr int kGroups = kPassStates / kNpw;  // state groups per channel (4)
-constexpr int kWaveCh = kWave / kGroups;     // channels per wave (16)
-constexpr int kSeg = kFwdTile / kGroups;     // output steps per lane per tile (8)
-
-// The lane's 8 output steps of a tile: 4g .. 4g+3 and 16+4g .. 16+4g+3 for
-// state group g, so that the four lanes of a channel cover 16 contiguous steps
-// (64 bytes of fp32) with each 4-step access.
-__device__ __forceinline__ int seg_step(int g, int k) { return (k < 4 ? 0 : 12) + 4 * g + k; }
-
-// The lane's 8 steps of one row of a [.., L] tensor in tile t0; reads past
-// the end use clamped in-range addresses (values unused).
-template <bool VEC, class E>
-__device__ __forceinline__ void load_seg(float (&v)[kSeg], const E* __restrict__ g, size_t row,
-                                         int t0, int grp, int L) {
+// The lane's SEG steps of one row of a [.., L] tensor in tile t0, as 4-step
+// pieces; reads past the end use clamped in-range addresses (values unused).
+template <int NPW, bool VEC, class E>
+__device__ __forceinline__ void load_seg(float (&v)[FwdLayout<NPW>::kSeg], const E* __restrict__ g,
+                                         size_t row, int t0, int grp, int L) {
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int t = t0 + 16 * q + 4 * grp;
+  for (int q = 0; q < FwdLayout<NPW>::kSeg / 4; ++q) {
+    const int t = t0 + FwdLayout<NPW>::step(grp, 4 * q);
     if constexpr (VEC) {
       const float4 x = Elem<E>::load4(g + row + min(t, L - 4));
       v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
@@ -516,13 +550,13 @@ __device__ __forceinline__ void load_seg(float (&v)[kSeg], const E* __restrict__
   }
 }
 
-// Stores the lane's 8 steps of tile t0 that lie before L.
-template <bool VEC, class E>
+// Stores the lane's SEG steps of tile t0 that lie before L.
+template <int NPW, bool VEC, class E>
 __device__ __forceinline__ void store_seg(E* __restrict__ g, size_t row, int t0, int grp, int L,
-                                          const float (&v)[kSeg]) {
+                                          const float (&v)[FwdLayout<NPW>::kSeg]) {
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int t = t0 + 16 * q + 4 * grp;
+  for (int q = 0; q < FwdLayout<NPW>::kSeg / 4; ++q) {
+    const int t = t0 + FwdLayout<NPW>::step(grp, 4 * q);
     if constexpr (VEC) {  // L % 4 == 0, so a group of 4 is all in or all out
       if (t < L) Elem<E>::store4(g + row + t, make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]));
     } else {
@@ -533,38 +567,72 @@ __device__ __forceinline__ void store_seg(E* __restrict__ g, size_t row, int t0,
   }
 }
 
-// Sums y over the kGroups state groups of each channel: lane (c, g) enters
-// with its group's partial y for steps 0..31 of the tile and leaves with the
-// full y of its steps seg_step(g, 0..7).  permlane32 swaps pair groups g and
-// g ^ 2 (the lower half keeps steps 0..7 and 16..23, the upper half 8..15 and
-// 24..31), permlane16 swaps pair g and g ^ 1.
-__device__ __forceinline__ void reduce_groups(float (&yv)[kFwdTile], float (&out)[kSeg]) {
-  float s1[kFwdTile / 2];
+// Sums y over the state groups of each channel: lane (c, g) enters with its
+// group's partial y for steps 0..31 of the tile and leaves with the full y of
+// its steps FwdLayout<NPW>::step(g, 0..SEG-1).
+//   NPW = 4: permlane32 swaps pair groups g and g ^ 2 (the lower half keeps
+//   steps 0..7 and 16..23, the upper half 8..15 and 24..31), permlane16 swaps
+//   pair g and g ^ 1.
+//   NPW = 2: permlane32 pairs g and g ^ 4 (the lower half keeps steps 0..15),
+//   permlane16 pairs g and g ^ 2 (even 16-lane rows keep the lower 8 of their
+//   16), and a row_ror:8 DPP pairs g and g ^ 1 (lanes l and l ^ 8): each keeps
+//   its 4 steps and sends the partner the other 4.
+template <int NPW>
+__device__ __forceinline__ void reduce_groups(float (&yv)[kFwdTile],
+                                              float (&out)[FwdLayout<NPW>::kSeg], int g) {
+  if constexpr (NPW == 4) {
+    float s1[kFwdTile / 2];
 #pragma unroll
-  for (int k = 0; k < kFwdTile / 2; ++k) {
-    const int i = k < 8 ? k : k + 8;
-    float lo = yv[i], hi = yv[i + 8];
-    swap32(lo, hi);
-    s1[k] = lo + hi;
-  }
+    for (int k = 0; k < kFwdTile / 2; ++k) {
+      const int i = k < 8 ? k : k + 8;
+      float lo = yv[i], hi = yv[i + 8];
+      swap32(lo, hi);
+      s1[k] = lo + hi;
+    }
 #pragma unroll
-  for (int j = 0; j < kSeg; ++j) {
-    const int k = j < 4 ? j : j + 4;
-    float lo = s1[k], hi = s1[k + 4];
-    swap16(lo, hi);
-    out[j] = lo + hi;
+    for (int j = 0; j < 8; ++j) {
+      const int k = j < 4 ? j : j + 4;
+      float lo = s1[k], hi = s1[k + 4];
+      swap16(lo, hi);
+      out[j] = lo + hi;
+    }
+  } else {
+    float s1[16], s2[8];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      float lo = yv[k], hi = yv[k + 16];
+      swap32(lo, hi);
+      s1[k] = lo + hi;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      float lo = s1[k], hi = s1[k + 8];
+      swap16(lo, hi);
+      s2[k] = lo + hi;
+    }
+    const bool odd = (g & 1) != 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float keep = odd ? s2[k + 4] : s2[k];
+      const float send = odd ? s2[k] : s2[k + 4];
+      out[k] = keep + dpp<0x128>(send);  // row_ror:8
+    }
   }
 }
 
 // GATED kernels multiply by silu(z) in the last pass; VEC: L % 4 == 0 and
-// u/dt/z/out rows 16-byte aligned.
-template <class E, bool VEC, bool GATED, bool BLD>
+// u/dt/z/out rows 16-byte aligned.  NPW: states per lane (FwdLayout); the
+// [B, L, D] layout (BLD) runs 4.
+template <class E, bool VEC, bool GATED, bool BLD, int NPW>
 __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
+  using LY = FwdLayout<NPW>;
   constexpr int TT = kFwdTile;
   constexpr int RS = TT + 1;  // odd row stride: lane-per-row accesses hit distinct banks
-  static_assert(kGroups == 4 && TT == 32 && kSeg == 8, "reduce_groups assumes 4 x 32 steps");
-  __shared__ float s_u[kWave * RS];
-  __shared__ float s_dt[kWave * RS];
+  constexpr int ROWS = LY::kRows, CW = LY::kWaveCh, SEG = LY::kSeg;
+  static_assert(TT == 32, "reduce_groups assumes 32-step tiles");
+  static_assert(!BLD || NPW == 4, "the [B, L, D] layout stages 64 channels");
+  __shared__ float s_u[ROWS * RS];
+  __shared__ float s_dt[ROWS * RS];
   __shared__ __align__(16) float s_B[TT * kPassStates];
   __shared__ __align__(16) float s_C[TT * kPassStates];
   // BLD: the tile's y, [step][channel], stored to HBM as rows of channels
@@ -573,17 +641,17 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
-  const int c = lane & (kWaveCh - 1), g = lane / kWaveCh;
+  const int c = lane & (CW - 1), g = lane / CW;
   const int b = blockIdx.y;
-  const int d0 = blockIdx.x * kWave;
-  const int r = w * kWaveCh + c;  // the lane's channel row in the workgroup's tile
+  const int d0 = blockIdx.x * ROWS;
+  const int r = w * CW + c;  // the lane's channel row in the workgroup's tile
   const int d = d0 + r;
   const bool dvalid = d < a.D;
-  const int n0 = a.n_base + g * kNpw;  // first state of this lane
+  const int n0 = a.n_base + g * NPW;  // first state of this lane
 
-  float A2[kNpw], h[kNpw];
+  float A2[NPW], h[NPW];
 #pragma unroll
-  for (int j = 0; j < kNpw; ++j) {
+  for (int j = 0; j < NPW; ++j) {
     A2[j] = (dvalid && n0 + j < a.N) ? a.A[static_cast<size_t>(d) * a.N + n0 + j] * kLog2e : 0.f;
     h[j] = 0.f;
   }
@@ -595,10 +663,15 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   const size_t my_row = row0 + static_cast<size_t>(dc) * a.L;  // [.., L] row of d (BDL)
   const bool ck = a.ckpt != nullptr && dvalid;
   const bool ck4 = a.N % 4 == 0 && (reinterpret_cast<uintptr_t>(a.ckpt) & 15) == 0;
-  // [B, D, L] only: the gate and the outputs of the lane's 8 steps of tile t0
-  auto load_gate = [&](float (&zv)[kSeg], int t0) { load_seg<VEC>(zv, a.z, my_row, t0, g, a.L); };
-  auto put_seg = [&](auto* dst, int t0, const float (&v)[kSeg]) {
-    store_seg<VEC>(dst, my_row, t0, g, a.L, v);
+  // [B, D, L] only: the gate and the outputs of the lane's SEG steps of tile t0
+  auto load_gate = [&](float (&zv)[SEG], int t0) { load_seg<NPW, VEC>(zv, a.z, my_row, t0, g, a.L); };
+  auto put_seg = [&](auto* dst, int t0, const float (&v)[SEG]) {
+    store_seg<NPW, VEC>(dst, my_row, t0, g, a.L, v);
+  };
+  // this lane's NPW states of B or C at step i of a staged tile, as one load
+  using SV = std::conditional_t<NPW == 4, float4, float2>;
+  auto state_vals = [&](const float* col, int i) {
+    return *reinterpret_cast<const SV*>(col + i * kPassStates);
   };
 
   // Time split: gridDim.z segments of consecutive tiles; segment s scans
@@ -610,8 +683,8 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   const int t_lo = (seg * n_tiles / n_seg) * TT;
   const int t_hi = min(a.L, ((seg + 1) * n_tiles / n_seg) * TT);
 
-  FwdTile nxt;
-  float zn[kSeg];  // the gate of the lane's output segment, one tile ahead
+  FwdTile<ROWS> nxt;
+  float zn[SEG];  // the gate of the lane's output segment, one tile ahead
   fwd_prefetch<E, VEC, BLD>(nxt, a, row0, bc0, d0, 0);
   for (int t0 = 0; t0 < t_lo; t0 += TT) {
     // h only over the earlier segment's tiles
@@ -628,15 +701,15 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     fwd_prefetch<E, VEC, BLD>(nxt, a, row0, bc0, d0, t0 + TT);
     const float* urow = s_u + r * RS;
     const float* dtrow = s_dt + r * RS;
-    const float* Bcol = s_B + g * kNpw;
+    const float* Bcol = s_B + g * NPW;
 #pragma unroll 8
     for (int i = 0; i < TT; ++i) {
       const float dtv = dtrow[i];
       const float dtu = dtv * urow[i];
-      const float4 Bt = *reinterpret_cast<const float4*>(Bcol + i * kPassStates);
-      const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
+      float Bv[NPW];
+      unpack(state_vals(Bcol, i), Bv);
 #pragma unroll
-      for (int j = 0; j < kNpw; ++j) h[j] = fmaf(fast_exp2(dtv * A2[j]), h[j], dtu * Bv[j]);
+      for (int j = 0; j < NPW; ++j) h[j] = fmaf(fast_exp2(dtv * A2[j]), h[j], dtu * Bv[j]);
     }
   }
   if constexpr (GATED && !BLD) load_gate(zn, t_lo);
@@ -651,9 +724,9 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     }
     store_states<TT>(s_B, nxt.B, t0, a.L, a.N, a.n_base);
     store_states<TT>(s_C, nxt.C, t0, a.L, a.N, a.n_base);
-    float zt[kSeg];
+    float zt[SEG];
 #pragma unroll
-    for (int k = 0; k < kSeg; ++k) zt[k] = zn[k];
+    for (int k = 0; k < SEG; ++k) zt[k] = zn[k];
     __syncthreads();
     if (t0 + TT < t_hi) {
       fwd_prefetch<E, VEC, BLD>(nxt, a, row0, bc0, d0, t0 + TT);
@@ -666,15 +739,16 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     // Every tile runs all TT steps: past L the staged dt, u, B and C are zero,
     // so h stays at the last step's state and y is zero there; the checkpoint
     // slots of the last tile then hold that final state, as their layout says.
-    float yv[TT];  // this lane's y partial (its 4 states) per step
-    float hck[TT / kCkpt][kNpw];  // h after steps 15 and 31, checkpointed after the loop
-    auto step = [&](int i, float dtv, float uv, float4 Bt, float4 Ct) {
+    float yv[TT];  // this lane's y partial (its NPW states) per step
+    float hck[TT / kCkpt][NPW];  // h after steps 15 and 31, checkpointed after the loop
+    auto step = [&](int i, float dtv, float uv, SV Bt, SV Ct) {
       const float dtu = dtv * uv;
-      const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
-      const float Cv[4] = {Ct.x, Ct.y, Ct.z, Ct.w};
+      float Bv[NPW], Cv[NPW];
+      unpack(Bt, Bv);
+      unpack(Ct, Cv);
       float y = 0.f;
 #pragma unroll
-      for (int j = 0; j < kNpw; ++j) {
+      for (int j = 0; j < NPW; ++j) {
         const float dA = fast_exp2(dtv * A2[j]);
         h[j] = fmaf(dA, h[j], dtu * Bv[j]);
         y = fmaf(Cv[j], h[j], y);
@@ -685,13 +759,13 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
       yv[i] = y;
       if ((i + 1) % kCkpt == 0) {
 #pragma unroll
-        for (int j = 0; j < kNpw; ++j) hck[i / kCkpt][j] = h[j];
+        for (int j = 0; j < NPW; ++j) hck[i / kCkpt][j] = h[j];
       }
     };
     const float* urow = s_u + r * RS;
     const float* dtrow = s_dt + r * RS;
-    const float* Bcol = s_B + g * kNpw;
-    const float* Ccol = s_C + g * kNpw;
+    const float* Bcol = s_B + g * NPW;
+    const float* Ccol = s_C + g * NPW;
     {
       // Software-pipelined: the LDS operands of the next kGroup steps are read
       // before this group is computed, so a read's latency is covered by a
@@ -699,15 +773,15 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
       // hoisting every step's reads to the top (256 VGPRs without it).
       constexpr int kGroup = 4;
       float pdt[2][kGroup], pu[2][kGroup];
-      float4 pB[2][kGroup], pC[2][kGroup];
+      SV pB[2][kGroup], pC[2][kGroup];
       auto fetch = [&](int buf, int gr) {
 #pragma unroll
         for (int q = 0; q < kGroup; ++q) {
           const int i = gr * kGroup + q;
           pdt[buf][q] = dtrow[i];
           pu[buf][q] = urow[i];
-          pB[buf][q] = *reinterpret_cast<const float4*>(Bcol + i * kPassStates);
-          pC[buf][q] = *reinterpret_cast<const float4*>(Ccol + i * kPassStates);
+          pB[buf][q] = state_vals(Bcol, i);
+          pC[buf][q] = state_vals(Ccol, i);
         }
       };
       fetch(0, 0);
@@ -723,16 +797,16 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     }
     if (ck) {
 #pragma unroll
-      for (int q = 0; q < TT / kCkpt; ++q) write_ckpt(a.ckpt, ck_row, t0 / kCkpt + q, a.N, n0, hck[q], ck4);
+      for (int q = 0; q < TT / kCkpt; ++q) write_ckpt<NPW>(a.ckpt, ck_row, t0 / kCkpt + q, a.N, n0, hck[q], ck4);
     }
 
-    // y over the state groups (within the wave), then this lane's 8 outputs
-    float y[kSeg];
-    reduce_groups(yv, y);
+    // y over the state groups (within the wave), then this lane's SEG outputs
+    float y[SEG];
+    reduce_groups<NPW>(yv, y, g);
     if constexpr (BLD) {
       // through LDS, so that rows of 64 channels leave as 16-byte runs
 #pragma unroll
-      for (int k = 0; k < kSeg; ++k) s_y[seg_step(g, k) * YS + r] = y[k];
+      for (int k = 0; k < SEG; ++k) s_y[LY::step(g, k) * YS + r] = y[k];
       __syncthreads();
 #pragma unroll
       for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
@@ -773,16 +847,16 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
       }
     } else if (dvalid) {
       if (!a.first) {
-        float prev[kSeg];
-        load_seg<VEC>(prev, a.acc, my_row, t0, g, a.L);
+        float prev[SEG];
+        load_seg<NPW, VEC>(prev, a.acc, my_row, t0, g, a.L);
 #pragma unroll
-        for (int k = 0; k < kSeg; ++k) y[k] += prev[k];
+        for (int k = 0; k < SEG; ++k) y[k] += prev[k];
       }
       if (a.last) {
         if (a.raw != nullptr) put_seg(a.raw, t0, y);
         if constexpr (GATED) {
 #pragma unroll
-          for (int k = 0; k < kSeg; ++k) y[k] *= zt[k] * sigmoid(zt[k]);
+          for (int k = 0; k < SEG; ++k) y[k] *= zt[k] * sigmoid(zt[k]);
         }
         put_seg(a.out, t0, y);
       } else {
@@ -1492,6 +1566,27 @@ int time_segments(int64_t n_wg, int64_t L, int tile, int want) {
   return s;
 }
 
+// States per lane of the [B, D, L] forward for `rows64` (batch row, 64-channel)
+// rows: 2 while 64-channel workgroups would give fewer than kFwdNpw2Below
+// waves per SIMD (OSSM_SEL_FWD_NPW=2|4 overrides).
+#ifndef OSSM_SEL_FWD_NPW2_BELOW
+#define OSSM_SEL_FWD_NPW2_BELOW 4
+#endif
+int fwd_states_per_lane(int64_t rows64) {
+  static const int forced = [] {
+    const char* v = std::getenv("OSSM_SEL_FWD_NPW");
+    return v == nullptr ? 0 : std::atoi(v);
+  }();
+  if (forced == 2 || forced == 4) return forced;
+  int dev = 0, n_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n_cu <= 0)
+    return 4;
+  // kMaxWaves waves per workgroup over 4 SIMDs per CU
+  return rows64 * kMaxWaves < static_cast<int64_t>(OSSM_SEL_FWD_NPW2_BELOW) * 4 * n_cu ? 2 : 4;
+}
+
 // E = float: the fp32 API of the reference.  E = bf16_t: the same scan with
 // bf16 rows, B and C in HBM (A, chunk_states and dA stay fp32).  ml: the
 // [B, L, D] layout (fp32 only); null for the reference's [B, D, L].
@@ -1544,7 +1639,11 @@ int selective_forward_impl(const E* u, const E* dt, const float* A, const E* Bm,
   } else {
     a.vec = rows_vectorizable(length, sizeof(E), {u, dt, gate, out, raw_out}) ? 1 : 0;
   }
-  const int64_t n_dtiles = (dim + kWave - 1) / kWave;
+  // states per lane: 2 (32-channel workgroups) when 64-channel workgroups
+  // would leave the SIMDs short of waves, else 4; the [B, L, D] layout runs 4
+  const int npw = ml != nullptr ? 4 : fwd_states_per_lane(((dim + kWave - 1) / kWave) * batch);
+  const int rows = npw == 4 ? FwdLayout<4>::kRows : FwdLayout<2>::kRows;
+  const int64_t n_dtiles = (dim + rows - 1) / rows;
   const int n_seg = time_segments(n_dtiles * batch, length, kFwdTile, kFwdWgPerCu);
   const dim3 grid(static_cast<unsigned>(n_dtiles), static_cast<unsigned>(batch),
                   static_cast<unsigned>(n_seg));
@@ -1554,17 +1653,19 @@ int selective_forward_impl(const E* u, const E* dt, const float* A, const E* Bm,
     a.last = p == n_pass - 1;
     using K = void (*)(FwdArgs<E>);
     K kern;
-    if constexpr (std::is_same_v<E, float>) {
-      if (ml != nullptr) {
-        kern = a.vec ? (gate ? selective_fwd_kernel<E, true, true, true> : selective_fwd_kernel<E, true, false, true>)
-                     : (gate ? selective_fwd_kernel<E, false, true, true> : selective_fwd_kernel<E, false, false, true>);
+    if (ml != nullptr) {
+      if constexpr (std::is_same_v<E, float>) {
+        kern = a.vec ? (gate ? selective_fwd_kernel<E, true, true, true, 4> : selective_fwd_kernel<E, true, false, true, 4>)
+                     : (gate ? selective_fwd_kernel<E, false, true, true, 4> : selective_fwd_kernel<E, false, false, true, 4>);
       } else {
-        kern = a.vec ? (gate ? selective_fwd_kernel<E, true, true, false> : selective_fwd_kernel<E, true, false, false>)
-                     : (gate ? selective_fwd_kernel<E, false, true, false> : selective_fwd_kernel<E, false, false, false>);
+        return set_error(OSSM_ERR_UNSUPPORTED, std::string(what) + ": the [B, L, D] layout is fp32");
       }
+    } else if (npw == 4) {
+      kern = a.vec ? (gate ? selective_fwd_kernel<E, true, true, false, 4> : selective_fwd_kernel<E, true, false, false, 4>)
+                   : (gate ? selective_fwd_kernel<E, false, true, false, 4> : selective_fwd_kernel<E, false, false, false, 4>);
     } else {
-      kern = a.vec ? (gate ? selective_fwd_kernel<E, true, true, false> : selective_fwd_kernel<E, true, false, false>)
-                   : (gate ? selective_fwd_kernel<E, false, true, false> : selective_fwd_kernel<E, false, false, false>);
+      kern = a.vec ? (gate ? selective_fwd_kernel<E, true, true, false, 2> : selective_fwd_kernel<E, true, false, false, 2>)
+                   : (gate ? selective_fwd_kernel<E, false, true, false, 2> : selective_fwd_kernel<E, false, false, false, 2>);
     }
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, a);
     if (int rc = launch_check("selective_fwd_kernel")) return rc;

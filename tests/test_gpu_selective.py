@@ -93,8 +93,12 @@ def test_selective_matches_reference_kernel_vectors(K, tag):
 # (B, D, L, N): tiny, ragged (D not a multiple of 64, L not a multiple of 4 or
 # 16, N not a multiple of 4), several passes over the states (N > 16), the
 # shapes of the reference's own tests (test_scan_parity.py:63-183)
+# The forward runs 2 states per lane while 64-channel workgroups would give
+# fewer than 4 waves per SIMD, else 4: on a 256-CU MI355X every shape below
+# runs 2 except (64, 1024, 64, 16) (1,024 rows of 64 channels), which runs 4.
 SHAPES = [(1, 1, 1, 1), (2, 5, 3, 3), (2, 70, 37, 5), (3, 65, 100, 16), (1, 130, 129, 20),
-          (2, 32, 256, 32), (2, 48, 192, 32), (4, 96, 384, 64), (1, 3, 50, 256)]
+          (2, 32, 256, 32), (2, 48, 192, 32), (4, 96, 384, 64), (1, 3, 50, 256),
+          (64, 1024, 64, 16)]
 
 
 @pytest.mark.parametrize("gated", [True, False], ids=["gate", "nogate"])

@@ -106,8 +106,10 @@ def _check_vs_fp32(bf, f32, what):
     assert frac >= 0.99, f"{what}: only {frac:.4f} of elements equal to the rounded fp32 path"
 
 
+# (64, 1024, 64, 16) runs the forward with 4 states per lane on a 256-CU
+# MI355X, the others with 2 (see test_gpu_selective.SHAPES)
 SHAPES = [(1, 1, 1, 1), (2, 70, 37, 5), (3, 65, 100, 16), (1, 130, 129, 20), (2, 48, 192, 32),
-          (4, 96, 384, 64)]
+          (4, 96, 384, 64), (64, 1024, 64, 16)]
 
 
 @pytest.mark.parametrize("gated", [True, False], ids=["gate", "nogate"])
