@@ -285,7 +285,7 @@ def cpu_baseline(L, B, P, budget_s=12.0):
 
 
 # ------------------------------------------------------------ other configs
-def _detail_configs(torch, K, dev, reps=10):
+def _detail_configs(torch, K, dev, reps=20):
     """The other BASELINE configs, each timed with events (median of `reps`)."""
     out = {}
     # C1: LinOSS-IM forward, B=8 L=1024 P=64
