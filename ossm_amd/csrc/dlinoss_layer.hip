@@ -39,6 +39,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdint>
 #include <string>
@@ -57,7 +58,15 @@ constexpr int kLc = 32;            // time steps per chunk = MFMA tile rows
 constexpr int kLayerWaves = 4;
 constexpr int kLayerThreads = kLayerWaves * kWave;
 constexpr int kLayerMax = 256;     // largest hidden / ssm size
-constexpr int kAhead = 8;          // weight groups (of 4 k-steps) loaded ahead
+// oscillator groups of 32 per wave in the backward's bu projection (Pp / 32
+// groups over kLayerWaves waves)
+constexpr int kBwdGroups = kLayerMax / 32 / kLayerWaves;
+// Weight groups (of 4 k-steps) loaded ahead in the projection loops.  It
+// divides every trip count (Hp / 8 and Pp / 4 with Hp, Pp multiples of 32),
+// so the unrolled loop bodies have no tail branches and the prefetches are
+// unconditional (the last groups reload a clamped in-range group, unused):
+// the compiler then keeps them in flight instead of waiting for each.
+constexpr int kAhead = 4;
 
 __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
@@ -85,25 +94,33 @@ __device__ __forceinline__ int acc_row(int r, int lane) {
   return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
 }
 
+// Weight loads are branch-free: an element outside the tensor reads a
+// clamped in-range address and is then zeroed, so the loads of the
+// projection loops stay unconditional and in flight together.
+__device__ __forceinline__ float4 keep4(bool ok, float4 v) {
+  return ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+__device__ __forceinline__ float2 keep2(bool ok, float2 v) { return ok ? v : make_float2(0.f, 0.f); }
+
 // In-projection weights of oscillator p for h = h0 .. h0 + 3, as
 // (re h0, im h0, re h0+1, im h0+1) and (re h0+2, ..): B[p, h, 0..1].  Zero
 // outside the tensor.  VEC: H % 4 == 0 and B 16-byte aligned.
 template <bool VEC>
 __device__ __forceinline__ void load_bw(const LayerArgs& A, int p, int h0, float4 (&w)[2]) {
   if (VEC) {
-    if (p < A.P && h0 < A.H) {
-      const float4* src = reinterpret_cast<const float4*>(A.Bw + (static_cast<size_t>(p) * A.H + h0) * 2);
-      w[0] = src[0];
-      w[1] = src[1];
-    } else {
-      w[0] = w[1] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    const bool ok = p < A.P && h0 < A.H;
+    const float4* src = reinterpret_cast<const float4*>(
+        A.Bw + (static_cast<size_t>(min(p, A.P - 1)) * A.H + min(h0, A.H - 4)) * 2);
+    w[0] = keep4(ok, src[0]);
+    w[1] = keep4(ok, src[1]);
   } else {
     float v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int h = h0 + (j >> 1);
-      v[j] = (p < A.P && h < A.H) ? A.Bw[(static_cast<size_t>(p) * A.H + h) * 2 + (j & 1)] : 0.f;
+      const bool ok = p < A.P && h < A.H;
+      const float x = A.Bw[(static_cast<size_t>(min(p, A.P - 1)) * A.H + min(h, A.H - 1)) * 2 + (j & 1)];
+      v[j] = ok ? x : 0.f;
     }
     w[0] = make_float4(v[0], v[1], v[2], v[3]);
     w[1] = make_float4(v[4], v[5], v[6], v[7]);
@@ -116,17 +133,65 @@ __device__ __forceinline__ void load_bw(const LayerArgs& A, int p, int h0, float
 template <bool VEC>
 __device__ __forceinline__ float4 load_cw(const LayerArgs& A, int h, int p0) {
   if (VEC) {
-    if (h < A.H && p0 < A.P)
-      return *reinterpret_cast<const float4*>(A.Cw + (static_cast<size_t>(h) * A.P + p0) * 2);
-    return make_float4(0.f, 0.f, 0.f, 0.f);
+    const bool ok = h < A.H && p0 < A.P;
+    return keep4(ok, *reinterpret_cast<const float4*>(
+                         A.Cw + (static_cast<size_t>(min(h, A.H - 1)) * A.P + min(p0, A.P - 2)) * 2));
   }
   float v[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int pj = p0 + (j >> 1);
-    v[j] = (h < A.H && pj < A.P) ? A.Cw[(static_cast<size_t>(h) * A.P + pj) * 2 + (j & 1)] : 0.f;
+    const bool ok = h < A.H && pj < A.P;
+    const float x = A.Cw[(static_cast<size_t>(min(h, A.H - 1)) * A.P + min(pj, A.P - 1)) * 2 + (j & 1)];
+    v[j] = ok ? x : 0.f;
   }
   return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Rows t0 .. t0 + nt - 1 of a [B, L, H] tensor to LDS [kLc][HS], zero-padded,
+// in two halves, so that a chunk's rows can be loaded early and written to
+// LDS when their phase begins: the thread's share is the float4
+// groups e = threadIdx.x + k * kLayerThreads, k < Hp / 32 (kLc x Hp / 4
+// groups over the workgroup), all loaded before any is waited on.  Rows past
+// nt and columns past H read a clamped in-range address and are zeroed when
+// written to LDS.
+struct RowStage {
+  float4 v[kLayerMax / 32];
+};
+
+template <bool VEC>
+__device__ __forceinline__ void stage_load(RowStage& r, const float* __restrict__ src, size_t row0,
+                                           int nt, int H, int Hp) {
+  const int q4 = Hp / 4, n = Hp / 32;
+#pragma unroll
+  for (int k = 0; k < kLayerMax / 32; ++k) {
+    if (k >= n) break;  // uniform
+    const int e = threadIdx.x + k * kLayerThreads;
+    const int t = min(e / q4, nt - 1), h = (e - (e / q4) * q4) * 4;
+    const float* p = src + row0 + static_cast<size_t>(t) * H;
+    if (VEC) {
+      r.v[k] = *reinterpret_cast<const float4*>(p + min(h, H - 4));
+    } else {
+      r.v[k] = make_float4(p[min(h, H - 1)], p[min(h + 1, H - 1)], p[min(h + 2, H - 1)],
+                           p[min(h + 3, H - 1)]);
+    }
+  }
+}
+
+__device__ __forceinline__ void stage_store(const RowStage& r, float* __restrict__ dst, int nt, int H,
+                                            int Hp, int HS) {
+  const int q4 = Hp / 4, n = Hp / 32;
+#pragma unroll
+  for (int k = 0; k < kLayerMax / 32; ++k) {
+    if (k >= n) break;  // uniform
+    const int e = threadIdx.x + k * kLayerThreads;
+    const int t = e / q4, h = (e - t * q4) * 4;
+    const float4 v = r.v[k];
+    const bool row = t < nt;
+    *reinterpret_cast<float4*>(dst + t * HS + h) =
+        make_float4(row && h < H ? v.x : 0.f, row && h + 1 < H ? v.y : 0.f,
+                    row && h + 2 < H ? v.z : 0.f, row && h + 3 < H ? v.w : 0.f);
+  }
 }
 
 template <int V, bool VEC>
@@ -154,23 +219,9 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_fwd_kernel(
 
   // 1. u rows t0 .. t0 + nt - 1 (contiguous) -> LDS, zero-padded to 32 x Hp
   {
-    const int q4 = Hp / 4;
-    for (int e = threadIdx.x; e < kLc * q4; e += kLayerThreads) {
-      const int t = e / q4, h = (e - t * q4) * 4;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (t < nt) {
-        const float* src = A.u + row0 + static_cast<size_t>(t) * A.H + h;
-        if (VEC) {
-          if (h < A.H) v = *reinterpret_cast<const float4*>(src);
-        } else {
-          v.x = h < A.H ? src[0] : 0.f;
-          v.y = h + 1 < A.H ? src[1] : 0.f;
-          v.z = h + 2 < A.H ? src[2] : 0.f;
-          v.w = h + 3 < A.H ? src[3] : 0.f;
-        }
-      }
-      *reinterpret_cast<float4*>(sU + t * HS + h) = v;
-    }
+    RowStage st;
+    stage_load<VEC>(st, A.u, row0, nt, A.H, Hp);
+    stage_store(st, sU, nt, A.H, Hp, HS);
   }
   __syncthreads();
 
@@ -193,10 +244,9 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_fwd_kernel(
 #pragma unroll
         for (int j = 0; j < kAhead; ++j) {
           const int q = q0 + j;
-          if (q >= ng) break;  // uniform; ng need not be a multiple of kAhead
           const float4 av = *reinterpret_cast<const float4*>(arow + 4 * q);
           const float4 w0 = wb[j][0], w1 = wb[j][1];
-          if (q + kAhead < ng) load_bw<VEC>(A, p, half * hh + 4 * (q + kAhead), wb[j]);
+          load_bw<VEC>(A, p, half * hh + 4 * min(q + kAhead, ng - 1), wb[j]);
           acc_re = mfma32(av.x, w0.x, acc_re);
           acc_im = mfma32(av.x, w0.y, acc_im);
           acc_re = mfma32(av.y, w0.z, acc_re);
@@ -288,10 +338,9 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_fwd_kernel(
 #pragma unroll
         for (int j = 0; j < kAhead; ++j) {
           const int q = q0 + j;
-          if (q >= ng) break;  // uniform
           const float4 av = *reinterpret_cast<const float4*>(arow + 8 * q);
           const float4 cv = cb[j];
-          if (q + kAhead < ng) cb[j] = load_cw<VEC>(A, h, 4 * (q + kAhead) + 2 * kk);
+          cb[j] = load_cw<VEC>(A, h, 4 * min(q + kAhead, ng - 1) + 2 * kk);
           acc = mfma32(av.x, cv.x, acc);
           acc = mfma32(av.y, cv.y, acc);
           acc = mfma32(av.z, cv.z, acc);
@@ -357,13 +406,15 @@ __device__ __forceinline__ void load_cw_pair(const LayerBwdArgs& A, int h0, int 
   for (int j = 0; j < 4; ++j) {
     const int h = h0 + j;
     const bool ok = p < A.P && h < A.H;
-    if (VEC && ok) {
-      const float2 c = *reinterpret_cast<const float2*>(A.Cw + (static_cast<size_t>(h) * A.P + p) * 2);
+    const size_t i = (static_cast<size_t>(min(h, A.H - 1)) * A.P + min(p, A.P - 1)) * 2;
+    if (VEC) {
+      const float2 c = keep2(ok, *reinterpret_cast<const float2*>(A.Cw + i));
       v[2 * j] = c.x;
       v[2 * j + 1] = c.y;
     } else {
-      v[2 * j] = ok ? A.Cw[(static_cast<size_t>(h) * A.P + p) * 2] : 0.f;
-      v[2 * j + 1] = ok ? A.Cw[(static_cast<size_t>(h) * A.P + p) * 2 + 1] : 0.f;
+      const float re = A.Cw[i], im = A.Cw[i + 1];
+      v[2 * j] = ok ? re : 0.f;
+      v[2 * j + 1] = ok ? im : 0.f;
     }
   }
   w[0] = make_float4(v[0], v[1], v[2], v[3]);
@@ -386,38 +437,12 @@ __device__ __forceinline__ float4 load_bw_pair(const LayerBwdArgs& A, int h, int
   for (int j = 0; j < 2; ++j) {
     const int pj = p0 + j;
     const bool ok = pj < A.P && h < A.H;
-    if (ok) {
-      const float2 b = *reinterpret_cast<const float2*>(A.Bw + (static_cast<size_t>(pj) * A.H + h) * 2);
-      v[2 * j] = b.x;
-      v[2 * j + 1] = b.y;
-    } else {
-      v[2 * j] = v[2 * j + 1] = 0.f;
-    }
+    const float2 b = keep2(ok, *reinterpret_cast<const float2*>(
+                                   A.Bw + (static_cast<size_t>(min(pj, A.P - 1)) * A.H + min(h, A.H - 1)) * 2));
+    v[2 * j] = b.x;
+    v[2 * j + 1] = b.y;
   }
   return make_float4(v[0], v[1], v[2], v[3]);
-}
-
-// Rows t0 .. t0 + nt - 1 of a [B, L, H] tensor -> LDS [kLc][HS], zero-padded.
-template <bool VEC>
-__device__ __forceinline__ void stage_rows(float* __restrict__ dst, const float* __restrict__ src,
-                                           size_t row0, int nt, int H, int Hp, int HS) {
-  const int q4 = Hp / 4;
-  for (int e = threadIdx.x; e < kLc * q4; e += kLayerThreads) {
-    const int t = e / q4, h = (e - t * q4) * 4;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (t < nt) {
-      const float* p = src + row0 + static_cast<size_t>(t) * H + h;
-      if (VEC) {
-        if (h < H) v = *reinterpret_cast<const float4*>(p);
-      } else {
-        v.x = h < H ? p[0] : 0.f;
-        v.y = h + 1 < H ? p[1] : 0.f;
-        v.z = h + 2 < H ? p[2] : 0.f;
-        v.w = h + 3 < H ? p[3] : 0.f;
-      }
-    }
-    *reinterpret_cast<float4*>(dst + t * HS + h) = v;
-  }
 }
 
 template <int V, bool VEC>
@@ -431,8 +456,8 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
   const int Hp = round32(A.H), Pp = round32(A.P);
   const int HS = Hp + 4, XS = 2 * Pp + 4;
   float* sA = smem;                   // [kLc][HS]   gy rows, then u rows
-  float* sX = sA + kLc * HS;          // [kLc][Pp][2] bu
-  float* sG = sX + kLc * XS;          // [kLc][Pp][2] g_x, then grad_bu
+  float* sX = smem;                   // [kLc][Pp][2] bu, over sA once u is read
+  float* sG = smem + kLc * max(HS, XS);  // [kLc][Pp][2] g_x, then grad_bu
   float4* s_agg = reinterpret_cast<float4*>(sG + kLc * XS);  // [P]
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -450,8 +475,18 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
   const int half = lane >> 5, m = lane & 31;
   const int hh = Hp / 2, ng1 = hh / 4;
 
+  // Every HBM read the chunk needs before its last phase goes out now: the
+  // gy and u rows (to LDS at phases 1 and 2) and the carry entering the
+  // chunk (phase 3).
+  RowStage st_gy, st_u;
+  stage_load<VEC>(st_gy, A.gy, row0, nt, A.H, Hp);
+  stage_load<VEC>(st_u, A.u, row0, nt, A.H, Hp);
+  const int p = threadIdx.x;
+  const bool osc = p < A.P;
+  const float4 carry_in = A.carries[(static_cast<size_t>(b) * A.n_chunks + c) * A.P + min(p, A.P - 1)];
+
   // 1. gy -> LDS; g_x = gy (C_re - i C_im) on the matrix cores -> sG
-  stage_rows<VEC>(sA, A.gy, row0, nt, A.H, Hp, HS);
+  stage_store(st_gy, sA, nt, A.H, Hp, HS);
   __syncthreads();
   {
     const float* arow = sA + m * HS + half * hh;
@@ -467,10 +502,9 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
 #pragma unroll
         for (int j = 0; j < kAhead; ++j) {
           const int q = q0 + j;
-          if (q >= ng1) break;
           const float4 av = *reinterpret_cast<const float4*>(arow + 4 * q);
           const float4 w0 = wb[j][0], w1 = wb[j][1];
-          if (q + kAhead < ng1) load_cw_pair<VEC>(A, half * hh + 4 * (q + kAhead), p, wb[j]);
+          load_cw_pair<VEC>(A, half * hh + 4 * min(q + kAhead, ng1 - 1), p, wb[j]);
           acc_re = mfma32(av.x, w0.x, acc_re);
           acc_im = mfma32(av.x, w0.y, acc_im);
           acc_re = mfma32(av.y, w0.z, acc_re);
@@ -490,16 +524,20 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
   }
   __syncthreads();
 
-  // 2. u -> LDS (over gy); bu on the matrix cores -> sX
-  stage_rows<VEC>(sA, A.u, row0, nt, A.H, Hp, HS);
+  // 2. u -> LDS (over gy); bu on the matrix cores, held in the accumulators
+  //    until every wave has read u, then written to sX over it
+  stage_store(st_u, sA, nt, A.H, Hp, HS);
   __syncthreads();
   {
     const float* arow = sA + m * HS + half * hh;
-    for (int pg = w; pg < Pp / 32; pg += kLayerWaves) {
-      const int p = pg * 32 + m;
-      floatx16 acc_re, acc_im;
+    floatx16 acc_re[kBwdGroups], acc_im[kBwdGroups];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc_re[r] = acc_im[r] = 0.f;
+    for (int i = 0; i < kBwdGroups; ++i) {
+      const int pg = w + i * kLayerWaves;
+      if (pg >= Pp / 32) break;  // uniform
+      const int p = pg * 32 + m;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc_re[i][r] = acc_im[i][r] = 0.f;
       float4 wb[kAhead][2];
 #pragma unroll
       for (int j = 0; j < kAhead; ++j) load_bw_b<VEC>(A, p, half * hh + 4 * j, wb[j]);
@@ -507,32 +545,36 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
 #pragma unroll
         for (int j = 0; j < kAhead; ++j) {
           const int q = q0 + j;
-          if (q >= ng1) break;
           const float4 av = *reinterpret_cast<const float4*>(arow + 4 * q);
           const float4 w0 = wb[j][0], w1 = wb[j][1];
-          if (q + kAhead < ng1) load_bw_b<VEC>(A, p, half * hh + 4 * (q + kAhead), wb[j]);
-          acc_re = mfma32(av.x, w0.x, acc_re);
-          acc_im = mfma32(av.x, w0.y, acc_im);
-          acc_re = mfma32(av.y, w0.z, acc_re);
-          acc_im = mfma32(av.y, w0.w, acc_im);
-          acc_re = mfma32(av.z, w1.x, acc_re);
-          acc_im = mfma32(av.z, w1.y, acc_im);
-          acc_re = mfma32(av.w, w1.z, acc_re);
-          acc_im = mfma32(av.w, w1.w, acc_im);
+          load_bw_b<VEC>(A, p, half * hh + 4 * min(q + kAhead, ng1 - 1), wb[j]);
+          acc_re[i] = mfma32(av.x, w0.x, acc_re[i]);
+          acc_im[i] = mfma32(av.x, w0.y, acc_im[i]);
+          acc_re[i] = mfma32(av.y, w0.z, acc_re[i]);
+          acc_im[i] = mfma32(av.y, w0.w, acc_im[i]);
+          acc_re[i] = mfma32(av.z, w1.x, acc_re[i]);
+          acc_im[i] = mfma32(av.z, w1.y, acc_im[i]);
+          acc_re[i] = mfma32(av.w, w1.z, acc_re[i]);
+          acc_im[i] = mfma32(av.w, w1.w, acc_im[i]);
         }
       }
+    }
+    __syncthreads();  // u is read: sX may overwrite it
+#pragma unroll
+    for (int i = 0; i < kBwdGroups; ++i) {
+      const int pg = w + i * kLayerWaves;
+      if (pg >= Pp / 32) break;  // uniform
+      const int p = pg * 32 + m;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int t = acc_row(r, lane);
-        *reinterpret_cast<float2*>(sX + t * XS + 2 * p) = make_float2(acc_re[r], acc_im[r]);
+        *reinterpret_cast<float2*>(sX + t * XS + 2 * p) = make_float2(acc_re[i][r], acc_im[i][r]);
       }
     }
   }
   __syncthreads();
 
   // 3. states, adjoint, grad_bu, parameter sums: one thread per oscillator
-  const int p = threadIdx.x;
-  const bool osc = p < A.P;
   const int nc = A.Bsz * A.P;
   const int ch = b * A.P + p;
   const bool scan = A.n_chunks > 1;
@@ -544,7 +586,7 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
   float4 e = f4zero();
   if (osc) {
     k = Model::coef_of({A.a[p], A.g[p], A.dt[p]});
-    float4 s = A.carries[(static_cast<size_t>(b) * A.n_chunks + c) * A.P + p];
+    float4 s = carry_in;
 #pragma unroll
     for (int t = 0; t < kLc; ++t) {
       sp[t] = s;
@@ -612,6 +654,11 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
       floatx16 acc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+      // gy for the D skip, loaded before the MFMA loop (clamped in range)
+      float gyv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        gyv[r] = A.gy[row0 + static_cast<size_t>(min(acc_row(r, lane), nt - 1)) * A.H + min(h, A.H - 1)];
       float4 cb[kAhead];
 #pragma unroll
       for (int j = 0; j < kAhead; ++j) cb[j] = load_bw_pair(A, h, 4 * j + 2 * kk);
@@ -619,10 +666,9 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
 #pragma unroll
         for (int j = 0; j < kAhead; ++j) {
           const int q = q0 + j;
-          if (q >= ng) break;
           const float4 av = *reinterpret_cast<const float4*>(arow + 8 * q);
           const float4 cv = cb[j];
-          if (q + kAhead < ng) cb[j] = load_bw_pair(A, h, 4 * (q + kAhead) + 2 * kk);
+          cb[j] = load_bw_pair(A, h, 4 * min(q + kAhead, ng - 1) + 2 * kk);
           acc = mfma32(av.x, cv.x, acc);
           acc = mfma32(av.y, cv.y, acc);
           acc = mfma32(av.z, cv.z, acc);
@@ -634,10 +680,7 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int t = acc_row(r, lane);
-          if (t < nt) {
-            const size_t gi = row0 + static_cast<size_t>(t) * A.H + h;
-            A.grad_u[gi] = acc[r] + A.gy[gi] * dh;
-          }
+          if (t < nt) A.grad_u[row0 + static_cast<size_t>(t) * A.H + h] = acc[r] + gyv[r] * dh;
         }
       }
     }
@@ -653,7 +696,8 @@ struct LayerParamEpilogue {
 
 size_t layer_bwd_lds_bytes(int64_t H, int64_t P) {
   const int64_t Hp = (H + 31) / 32 * 32, Pp = (P + 31) / 32 * 32;
-  return static_cast<size_t>(kLc * (Hp + 4) + 2 * kLc * (2 * Pp + 4) + 4 * P) * sizeof(float);
+  return static_cast<size_t>(kLc * std::max(Hp + 4, 2 * Pp + 4) + kLc * (2 * Pp + 4) + 4 * P) *
+         sizeof(float);
 }
 
 constexpr size_t kMaxLds = 160 * 1024;

@@ -44,10 +44,11 @@ _LDS = 160 * 1024
 
 
 def _bwd_fits(hidden: int, ssm: int) -> bool:
-    """The fused backward's LDS (u or gy rows, bu and grad_bu tiles) fits one
-    workgroup (mirrors layer_bwd_lds_bytes in dlinoss_layer.hip)."""
+    """The fused backward's LDS (u or gy rows with bu over them, grad_bu tiles)
+    fits one workgroup (mirrors layer_bwd_lds_bytes in dlinoss_layer.hip; true
+    for every size up to 256)."""
     hp, pp = -(-hidden // 32) * 32, -(-ssm // 32) * 32
-    return (_CHUNK * (hp + 4) + 2 * _CHUNK * (2 * pp + 4) + 4 * ssm) * 4 <= _LDS
+    return (_CHUNK * max(hp + 4, 2 * pp + 4) + _CHUNK * (2 * pp + 4) + 4 * ssm) * 4 <= _LDS
 
 
 def project_parameters(A_diag: Tensor, G_diag: Tensor, steps: Tensor) -> Tuple[Tensor, Tensor, Tensor]:

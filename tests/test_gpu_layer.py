@@ -268,14 +268,32 @@ def test_layer_fused_backward_matches_unfused_at_size(layers, variant):
     no_device_errors()
 
 
-def test_layer_backward_falls_back_when_lds_is_short(layers):
-    """H = P = 256 needs more LDS than one workgroup has for the fused backward:
-    the forward stays fused, the backward recomputes through the composition."""
-    nb, L, H, P = 1, 40, 256, 256
-    announce("layer backward fallback H=P=256")
-    assert not layers._bwd_fits(H, P)
+def test_layer_fused_backward_at_256(layers):
+    """H = P = 256, the largest fused size: two oscillator groups per wave in
+    the bu projection (bu held in the accumulators until u is read) and the
+    fused backward's LDS at its largest, against fp64 oracle gradients."""
+    nb, L, H, P = 2, 70, 256, 256
+    announce("layer fused backward H=P=256")
+    assert layers._bwd_fits(H, P)
     args = _layer_inputs(nb, L, H, P, 31, "imex1")
     gy = np.random.default_rng(32).normal(size=(nb, L, H)).astype(np.float32)
+    leaves = [to_dev(x).requires_grad_(True) for x in args]
+    layers.DlinossLayerFn.apply("imex1", *leaves).backward(to_dev(gy))
+    ref = _oracle_grads("imex1", args, gy.astype(np.float64))
+    for t, r, n in zip(leaves, ref, ["inputs", "B", "C", "D", "a_diag", "g_diag", "step"]):
+        err = rel_fro(to_np(t.grad), r)
+        assert err < 5e-5, f"grad {n}: relative error {err:.2e}"
+    no_device_errors()
+
+
+def test_layer_backward_recompute_path(layers, monkeypatch):
+    """The recomputing backward (through the unfused composition), taken when
+    the fused backward's LDS would not fit, forced here at a small size."""
+    nb, L, H, P = 1, 40, 48, 40
+    announce("layer backward recompute path")
+    monkeypatch.setattr(layers, "_bwd_fits", lambda hidden, ssm: False)
+    args = _layer_inputs(nb, L, H, P, 33, "imex1")
+    gy = np.random.default_rng(34).normal(size=(nb, L, H)).astype(np.float32)
     leaves = [to_dev(x).requires_grad_(True) for x in args]
     layers.DlinossLayerFn.apply("imex1", *leaves).backward(to_dev(gy))
     ref = _oracle_grads("imex1", args, gy.astype(np.float64))
