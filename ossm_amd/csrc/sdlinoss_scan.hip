@@ -238,12 +238,40 @@ __device__ __forceinline__ float param_at(const ParamView& v, long long t, const
   return v.p[static_cast<size_t>(t * v.t_stride) + (v.by_channel ? li.pch : li.pm)];
 }
 
+// The parameters of steps t0 .. t0 + T - 1 (clamped rows); TB: broadcast over
+// time, one read each.
+template <int T, bool TB>
+__device__ __forceinline__ void load_params(const SdlParams& prm, long long t0, int L,
+                                            const LaneIdx& li, float (&pa)[T], float (&pg)[T],
+                                            float (&ps)[T]) {
+  if constexpr (TB) {
+    const float a = param_at(prm.a, 0, li), g = param_at(prm.g, 0, li), s = param_at(prm.s, 0, li);
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      pa[i] = a;
+      pg[i] = g;
+      ps[i] = s;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      const long long t = min(t0 + i, static_cast<long long>(L - 1));
+      pa[i] = param_at(prm.a, t, li);
+      pg[i] = param_at(prm.g, t, li);
+      ps[i] = param_at(prm.s, t, li);
+    }
+  }
+}
+
 // ============================================================================
 // Forward
 // ============================================================================
 // One workgroup = one time chunk of W*T steps for 64 channels; wave w owns
 // steps [t0, t0 + T).  Workgroups take chunks first-first in ticket order.
-template <int V, int T, int W>
+// TB: all three parameters broadcast over time (time stride 0): they are
+// read once and every per-step coefficient is the same value, which the
+// compiler then computes once.
+template <int V, int T, int W, bool TB>
 __global__ __launch_bounds__(W * kWave) void sdl_forward_kernel(
     SdlParams prm, const float2* __restrict__ bu, float4* __restrict__ out, int L, int nc,
     int n_groups, int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
@@ -266,13 +294,7 @@ __global__ __launch_bounds__(W * kWave) void sdl_forward_kernel(
   // loads (clamped rows): parameters, then bu
   float pa[T], pg[T], ps[T];
   float2 x[T];
-#pragma unroll
-  for (int i = 0; i < T; ++i) {
-    const long long t = min(t0 + i, static_cast<long long>(L - 1));
-    pa[i] = param_at(prm.a, t, li);
-    pg[i] = param_at(prm.g, t, li);
-    ps[i] = param_at(prm.s, t, li);
-  }
+  load_params<T, TB>(prm, t0, L, li, pa, pg, ps);
 #pragma unroll
   for (int i = 0; i < T; ++i) x[i] = row_of(bu, min(t0 + i, static_cast<long long>(L - 1)), nc, g)[li.lc];
 
@@ -410,7 +432,7 @@ struct SdlGradOut {
   int tsum;
 };
 
-template <int V, int T, int W>
+template <int V, int T, int W, bool TB>
 __global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
     SdlParams prm, const float2* __restrict__ bu, const float4* states,
     const float2* __restrict__ gout, float2* __restrict__ gin, SdlGradOut go_prm, int L, int nc,
@@ -441,14 +463,9 @@ __global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
   asm volatile("" ::: "memory");
   float pa[T], pg[T], ps[T];
   float2 x[T], go[T];
+  load_params<T, TB>(prm, t0, L, li, pa, pg, ps);
 #pragma unroll
-  for (int i = 0; i < T; ++i) {
-    const long long t = min(t0 + i, static_cast<long long>(L - 1));
-    pa[i] = param_at(prm.a, t, li);
-    pg[i] = param_at(prm.g, t, li);
-    ps[i] = param_at(prm.s, t, li);
-    x[i] = row_of(bu, t, nc, g)[li.lc];
-  }
+  for (int i = 0; i < T; ++i) x[i] = row_of(bu, min(t0 + i, static_cast<long long>(L - 1)), nc, g)[li.lc];
   asm volatile("" ::: "memory");
 #pragma unroll
   for (int i = T - 1; i >= 0; --i) go[i] = row_of(gout, min(t0 + i, static_cast<long long>(L - 1)), nc, g)[li.lc];
@@ -702,7 +719,9 @@ int sdl_forward_tw(const SdlParams& prm, const void* bu, void* states, int64_t L
   LaunchSync sync{};
   const int64_t total = n_chunks * n_groups;
   if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
-  hipLaunchKernelGGL((sdl_forward_kernel<V, T, W>), dim3(static_cast<unsigned>(total)),
+  const bool tb = prm.a.t_stride == 0 && prm.g.t_stride == 0 && prm.s.t_stride == 0;
+  hipLaunchKernelGGL((tb ? sdl_forward_kernel<V, T, W, true> : sdl_forward_kernel<V, T, W, false>),
+                     dim3(static_cast<unsigned>(total)),
                      dim3(W * kWave), 0, stream, prm, static_cast<const float2*>(bu),
                      static_cast<float4*>(states), static_cast<int>(L), static_cast<int>(nc),
                      static_cast<int>(n_groups), static_cast<int>(n_chunks),
@@ -775,7 +794,9 @@ int sdl_backward_tw(const SdlParams& prm, const ParamShape (&shapes)[3], const v
   LaunchSync sync{};
   const int64_t total = n_chunks * n_groups;
   if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
-  hipLaunchKernelGGL((sdl_backward_kernel<V, T, W>), dim3(static_cast<unsigned>(total)),
+  const bool tb = prm.a.t_stride == 0 && prm.g.t_stride == 0 && prm.s.t_stride == 0;
+  hipLaunchKernelGGL((tb ? sdl_backward_kernel<V, T, W, true> : sdl_backward_kernel<V, T, W, false>),
+                     dim3(static_cast<unsigned>(total)),
                      dim3(W * kWave), 0, stream, prm, static_cast<const float2*>(bu),
                      static_cast<const float4*>(states), static_cast<const float2*>(gout),
                      static_cast<float2*>(gbu), dst, static_cast<int>(L), static_cast<int>(nc),
