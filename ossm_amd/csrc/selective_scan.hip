@@ -975,11 +975,14 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   __shared__ float s_gy[kWave * RS];
   __shared__ __align__(16) float s_B[TT * kPassStates];
   __shared__ __align__(16) float s_C[TT * kPassStates];
-  // per-wave du / ddt partials, [wave][channel][step], rows of DS floats: a
-  // lane writes 4 steps as one 16-byte store (rows 80 bytes apart, so the 16
-  // lanes of a quarter-wave hit disjoint banks) and the finish reads 4 steps
-  // of a channel with one 16-byte load
-  constexpr int DS = TT + 4;
+  // per-wave du / ddt partials, [wave][channel][step], rows of DS = 16 floats
+  // with the four 4-step groups of channel c rotated by (c >> 2) & 3
+  // (du_col): a lane writes 4 steps of its channel as one 16-byte store and
+  // the finish reads 4 steps of a channel with one 16-byte load, and both
+  // touch 16 distinct 16-byte bank groups per quarter-wave
+  constexpr int DS = TT;
+  static_assert(TT == 16, "du_col rotates four 4-step groups");
+  auto du_col = [](int c, int step) { return ((((step >> 2) + (c >> 2)) & 3) << 2) | (step & 3); };
   __shared__ __align__(16) float s_du[kMaxWaves * kWave * DS];
   __shared__ __align__(16) float s_ddt[kMaxWaves * kWave * DS];
 
@@ -1086,8 +1089,8 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
         for (int v = 0; v < nw; ++v) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            su[e] += s_du[(v * kWave + c4 + e) * DS + step];
-            sd[e] += s_ddt[(v * kWave + c4 + e) * DS + step];
+            su[e] += s_du[(v * kWave + c4 + e) * DS + du_col(c4 + e, step)];
+            sd[e] += s_ddt[(v * kWave + c4 + e) * DS + du_col(c4 + e, step)];
           }
         }
 #pragma unroll
@@ -1125,8 +1128,8 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
       if (dd >= a.D || t >= a.L) continue;
       float4 su = make_float4(0.f, 0.f, 0.f, 0.f), sd = su;
       for (int v = 0; v < nw; ++v) {
-        const float4 pu = *reinterpret_cast<const float4*>(s_du + (v * kWave + r) * DS + c);
-        const float4 pd = *reinterpret_cast<const float4*>(s_ddt + (v * kWave + r) * DS + c);
+        const float4 pu = *reinterpret_cast<const float4*>(s_du + (v * kWave + r) * DS + du_col(r, c));
+        const float4 pd = *reinterpret_cast<const float4*>(s_ddt + (v * kWave + r) * DS + du_col(r, c));
         su.x += pu.x;
         su.y += pu.y;
         su.z += pu.z;
@@ -1341,8 +1344,8 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
           du4[i & 3] = dtv * S1;
           dd4[i & 3] = fmaf(uv, S1, S2);
           if ((i & 3) == 0) {
-            *reinterpret_cast<float4*>(durow + s0 + i) = make_float4(du4[0], du4[1], du4[2], du4[3]);
-            *reinterpret_cast<float4*>(ddtrow + s0 + i) = make_float4(dd4[0], dd4[1], dd4[2], dd4[3]);
+            *reinterpret_cast<float4*>(durow + du_col(lane, s0 + i)) = make_float4(du4[0], du4[1], du4[2], du4[3]);
+            *reinterpret_cast<float4*>(ddtrow + du_col(lane, s0 + i)) = make_float4(dd4[0], dd4[1], dd4[2], dd4[3]);
           }
           float o0, o1;
           reduce8(v, o0, o1);
