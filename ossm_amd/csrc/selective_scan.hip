@@ -19,7 +19,10 @@
 //   (cross-row swaps and DPP), with no LDS round trip.
 //   Backward: lane = channel and wave w carries states 4w .. 4w + 3, so the
 //   sums over channels (dB, dC) finish inside a wave and the sums over states
-//   (du, ddt) across the waves through LDS.
+//   (du, ddt) across the waves through LDS; or, when 64-channel workgroups
+//   would leave the device short of them, 32 channels per workgroup with 2
+//   states per lane (selective_bwd2_kernel: half the registers, three
+//   workgroups per CU instead of two).
 //
 // Transcendentals: exp(dt A) = exp2(dt * (A log2 e)) with A log2 e formed once
 //   per lane, so each state-step costs one v_exp_f32.
@@ -37,11 +40,10 @@
 //   dA    = sum_{b,t} gacc dt e^{dt A} h_{t-1},   dz = gout * y * silu'(z) (y = raw_out)
 //   dB_t  = sum_d gacc dt u,   dC_t = sum_d gy h_t
 // A tile is done in two 8-step halves, the later one first: the forward is
-// re-run from the checkpoint (once more over the first half, to reach the
-// second; that pass keeps the first half's exp(dt A) for later), each half's h
-// and exp(dt A) are held in registers while the adjoint runs over it in
-// reverse.  Holding all 16 steps' states costs 64 more VGPRs: one wave per
-// SIMD instead of two.
+// re-run from the checkpoint over the whole tile once (the first half's
+// trajectory kept for later, the second half's held while the adjoint runs
+// over it in reverse).  The 2-states-per-lane kernel stages 32-step tiles and
+// starts each 16-step half from its own checkpoint.
 // Time split: with fewer (batch row, 64-channel) rows than twice the CUs the
 // grid's z dimension cuts each row's tiles into 2 or 4 segments; a segment
 // first carries the adjoint from the end of the sequence through the later
@@ -92,6 +94,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 #endif
 constexpr int kFwdWgPerCu = OSSM_SEL_FWD_WG_PER_CU;
 constexpr int kBwdWgPerCu = OSSM_SEL_BWD_WG_PER_CU;
+constexpr int kBwd2WgPerCu = 3;  // the 2-states-per-lane backward
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -119,17 +122,20 @@ __device__ __forceinline__ float dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
                                                                0xf, 0xf, false));
 }
-// Sum over the 16 lanes of each row, result in every lane of the row.
-__device__ __forceinline__ float row_allreduce(float v) {
-  v += dpp<0x128>(v);  // row_ror:8
-  v += dpp<0x124>(v);  // row_ror:4
-  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
-  return v;
+// Masked DPP move: lanes whose 4-lane bank is set in BANKS take v from the
+// lane CTRL selects, the others keep `old`.
+template <int CTRL, int BANKS>
+__device__ __forceinline__ float dpp_masked(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                               __builtin_bit_cast(int, v), CTRL, 0xf,
+                                                               BANKS, false));
 }
-// Sums v[0..7] over all 64 lanes; lanes of row r (= lane / 16) receive the
-// totals of v[2r] and v[2r+1].
-__device__ __forceinline__ void reduce8(const float (&v)[8], float& o0, float& o1) {
+// Sums v[0..7] over all 64 lanes; every lane of half-row k (lanes 8k..8k+7)
+// receives the total of v[k].  Two transposing stages across rows
+// (permlane32 / permlane16 swaps), a third between the two halves of each row
+// (two masked row_ror:8 moves: the low half keeps its first value and takes
+// the high half's, the high half the reverse), then an 8-lane all-reduce.
+__device__ __forceinline__ float reduce8(const float (&v)[8]) {
   float a0 = v[0], a1 = v[1], a2 = v[2], a3 = v[3];
   float b0 = v[4], b1 = v[5], b2 = v[6], b3 = v[7];
   swap32(a0, b0);
@@ -140,9 +146,14 @@ __device__ __forceinline__ void reduce8(const float (&v)[8], float& o0, float& o
   float s0 = a0 + b0, s1 = a1 + b1, s2 = a2 + b2, s3 = a3 + b3;
   swap16(s0, s2);
   swap16(s1, s3);
-  // row 0: (v0, v1), row 1: (v2, v3), row 2: (v4, v5), row 3: (v6, v7), 4-lane sums
-  o0 = row_allreduce(s0 + s2);
-  o1 = row_allreduce(s1 + s3);
+  // row r: p = 4-lane sums of v[2r], q of v[2r + 1]
+  const float p = s0 + s2, q = s1 + s3;
+  // low half: p + p of the lane 8 above; high half: q + q of the lane 8 below
+  float r = dpp_masked<0x128, 0xC>(p, q) + dpp_masked<0x128, 0x3>(q, p);
+  r += dpp<0x141>(r);  // row_half_mirror
+  r += dpp<0x4E>(r);   // quad_perm [2,3,0,1]
+  r += dpp<0xB1>(r);   // quad_perm [1,0,3,2]
+  return r;
 }
 
 __device__ __forceinline__ void unpack(float4 v, float (&o)[4]) {
@@ -1265,49 +1276,50 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
       const float* Ccol = s_C + w * kNpw;
       float* durow = s_du + (w * kWave + lane) * DS;
       float* ddtrow = s_ddt + (w * kWave + lane) * DS;
-      float keep0 = 0.f, keep1 = 0.f;
+      // keep[h]: this lane's share of the dB / dC tile partials of steps
+      // 8h .. 8h + 7 (see reduce8 for which lane holds which total)
+      float keep[2] = {0.f, 0.f};
 
-      // Steps s0 .. s0 + HT - 1 of the tile, entered with the state before
-      // step s0: the forward is re-run into registers, then the adjoint runs in
-      // reverse.  Steps past L were staged as zeros, so they leave h unchanged
-      // and contribute exact zeros.  Each step's LDS operands are read one step
-      // ahead; the empty asm with a memory clobber after every step keeps the
-      // compiler from hoisting all of them to the top (registers).
-      // exp(dt A) of the first half, kept from the pass that finds the state
-      // in the middle of the tile (so the first half does not take its
-      // exponentials twice)
-      float dA0[HT][kNpw];
-      auto sub_tile = [&](auto s0_tag, const float (&hst)[kNpw], auto cached_tag) {
+      // The forward over steps s0 .. s0 + HT - 1 of the tile from the state
+      // before step s0, into registers: the state after each step and its
+      // exp(dt A).  Steps past L were staged as zeros, so they leave h
+      // unchanged and contribute exact zeros below.  Each step's LDS operands
+      // are read one step ahead; the empty asm with a memory clobber after
+      // every step keeps the compiler from hoisting all of them to the top
+      // (registers).
+      auto forward_half = [&](auto s0_tag, const float (&hst)[kNpw], float (&hs)[HT][kNpw],
+                              float (&dAs)[HT][kNpw]) {
         constexpr int s0 = decltype(s0_tag)::value;
-        constexpr bool cached = decltype(cached_tag)::value;
-        static_assert(!cached || s0 == 0, "only the first half has cached exponentials");
-        float hs[HT][kNpw], dAs[HT][kNpw];
-        {
-          float h[kNpw];
+        float h[kNpw];
 #pragma unroll
-          for (int j = 0; j < kNpw; ++j) h[j] = hst[j];
-          float ndt = dtrow[s0], nu = urow[s0];
-          float4 nB = *reinterpret_cast<const float4*>(Bcol + s0 * kPassStates);
+        for (int j = 0; j < kNpw; ++j) h[j] = hst[j];
+        float ndt = dtrow[s0], nu = urow[s0];
+        float4 nB = *reinterpret_cast<const float4*>(Bcol + s0 * kPassStates);
 #pragma unroll
-          for (int i = 0; i < HT; ++i) {
-            const float dtv = ndt, uv = nu;
-            const float Bv[4] = {nB.x, nB.y, nB.z, nB.w};
-            if (i + 1 < HT) {
-              ndt = dtrow[s0 + i + 1];
-              nu = urow[s0 + i + 1];
-              nB = *reinterpret_cast<const float4*>(Bcol + (s0 + i + 1) * kPassStates);
-            }
-            const float dtu = dtv * uv;
-#pragma unroll
-            for (int j = 0; j < kNpw; ++j) {
-              const float dA = cached ? dA0[i][j] : fast_exp2(dtv * A2[j]);
-              h[j] = fmaf(dA, h[j], dtu * Bv[j]);
-              hs[i][j] = h[j];
-              dAs[i][j] = dA;
-            }
-            asm volatile("" ::: "memory");
+        for (int i = 0; i < HT; ++i) {
+          const float dtv = ndt, uv = nu;
+          const float Bv[4] = {nB.x, nB.y, nB.z, nB.w};
+          if (i + 1 < HT) {
+            ndt = dtrow[s0 + i + 1];
+            nu = urow[s0 + i + 1];
+            nB = *reinterpret_cast<const float4*>(Bcol + (s0 + i + 1) * kPassStates);
           }
+          const float dtu = dtv * uv;
+#pragma unroll
+          for (int j = 0; j < kNpw; ++j) {
+            const float dA = fast_exp2(dtv * A2[j]);
+            h[j] = fmaf(dA, h[j], dtu * Bv[j]);
+            hs[i][j] = h[j];
+            dAs[i][j] = dA;
+          }
+          asm volatile("" ::: "memory");
         }
+      };
+      // The adjoint over the same steps in reverse, from the trajectory the
+      // forward above left (hst = the state before step s0).
+      auto adjoint_half = [&](auto s0_tag, const float (&hst)[kNpw], const float (&hs)[HT][kNpw],
+                              const float (&dAs)[HT][kNpw]) {
+        constexpr int s0 = decltype(s0_tag)::value;
         constexpr int il = HT - 1;
         float ngy = gyrow[s0 + il], ndt = dtrow[s0 + il], nu = urow[s0 + il];
         float4 nB = *reinterpret_cast<const float4*>(Bcol + (s0 + il) * kPassStates);
@@ -1347,53 +1359,52 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
             *reinterpret_cast<float4*>(durow + du_col(lane, s0 + i)) = make_float4(du4[0], du4[1], du4[2], du4[3]);
             *reinterpret_cast<float4*>(ddtrow + du_col(lane, s0 + i)) = make_float4(dd4[0], dd4[1], dd4[2], dd4[3]);
           }
-          float o0, o1;
-          reduce8(v, o0, o1);
-          if ((lane & 15) == s0 + i) {
-            keep0 = o0;
-            keep1 = o1;
-          }
+          const float o = reduce8(v);
+          if ((lane & 7) == i) keep[s0 / HT] = o;
           asm volatile("" ::: "memory");
         }
       };
 
-      // The second half first (from the state after step HT - 1, found by one
-      // more forward pass over the first half, whose exponentials the first
-      // half then reuses), then the first half.  A tile that ends within its
-      // first half skips the second: all padding.
+      // The second half first (from the state after step HT - 1), then the
+      // first, whose trajectory the forward over it kept.  A tile that ends
+      // within its first half skips the second: all padding.  The [B, L, D]
+      // kernels (more registers for their column staging) keep only the first
+      // half's exponentials across the second half and re-run its states.
+      float hs0[HT][kNpw], dA0[HT][kNpw];
+      forward_half(std::integral_constant<int, 0>{}, h0, hs0, dA0);
       if (nsteps > HT) {
-        float hmid[kNpw];
+        float hs1[HT][kNpw], dA1[HT][kNpw];
+        forward_half(std::integral_constant<int, HT>{}, hs0[HT - 1], hs1, dA1);
+        adjoint_half(std::integral_constant<int, HT>{}, hs0[HT - 1], hs1, dA1);
+        if constexpr (BLD) {
+          float h[kNpw];
 #pragma unroll
-        for (int j = 0; j < kNpw; ++j) hmid[j] = h0[j];
+          for (int j = 0; j < kNpw; ++j) h[j] = h0[j];
 #pragma unroll
-        for (int i = 0; i < HT; ++i) {
-          const float dtv = dtrow[i];
-          const float dtu = dtv * urow[i];
-          const float4 Bt = *reinterpret_cast<const float4*>(Bcol + i * kPassStates);
-          const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
+          for (int i = 0; i < HT; ++i) {
+            const float dtu = dtrow[i] * urow[i];
+            const float4 Bt = *reinterpret_cast<const float4*>(Bcol + i * kPassStates);
+            const float Bv[4] = {Bt.x, Bt.y, Bt.z, Bt.w};
 #pragma unroll
-          for (int j = 0; j < kNpw; ++j) {
-            dA0[i][j] = fast_exp2(dtv * A2[j]);
-            hmid[j] = fmaf(dA0[i][j], hmid[j], dtu * Bv[j]);
+            for (int j = 0; j < kNpw; ++j) {
+              h[j] = fmaf(dA0[i][j], h[j], dtu * Bv[j]);
+              hs0[i][j] = h[j];
+            }
           }
         }
-        sub_tile(std::integral_constant<int, HT>{}, hmid, std::false_type{});
-        sub_tile(std::integral_constant<int, 0>{}, h0, std::true_type{});
-      } else {
-        sub_tile(std::integral_constant<int, 0>{}, h0, std::false_type{});
       }
+      adjoint_half(std::integral_constant<int, 0>{}, h0, hs0, dA0);
 
-      // lane (row r, column c) holds the tile-partials of step t0 + c:
-      // r = 0: dB[n0], dB[n0+1]; r = 1: dB[n0+2], dB[n0+3]; r = 2, 3: same for dC
-      const int r = lane >> 4, c = lane & 15;
-      if (c < nsteps) {
-        float* dst = (r < 2 ? a.part_dB : a.part_dC) + part0 + static_cast<size_t>(t0 + c) * a.N;
-        const int nn = n0 + 2 * (r & 1);
-        if (nn + 1 < a.N && a.N % 2 == 0) {
-          *reinterpret_cast<float2*>(dst + nn) = make_float2(keep0, keep1);
-        } else {
-          if (nn < a.N) dst[nn] = keep0;
-          if (nn + 1 < a.N) dst[nn + 1] = keep1;
+      // lane l holds the tile partial of step t0 + 8h + (l & 7) in keep[h]:
+      // dB[n0 + k] for k = (l >> 3) & 7 < 4, dC[n0 + k - 4] for the rest
+      const int k = (lane >> 3) & 7, c8 = lane & 7;
+      const int nn = n0 + (k & 3);
+      if (nn < a.N) {
+        float* dst = (k < 4 ? a.part_dB : a.part_dC) + part0 + nn;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int c = 8 * h + c8;
+          if (c < nsteps) dst[static_cast<size_t>(t0 + c) * a.N] = keep[h];
         }
       }
     }
@@ -1415,6 +1426,460 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
 #pragma unroll
     for (int j = 0; j < kNpw; ++j)
       if (n0 + j < a.N) a.part_dA[(prow * a.D + d) * a.N + n0 + j] = gA[j];
+  }
+}
+
+// ---- backward, 2 states per lane ---------------------------------------------
+// lane = (channel c = lane % 32, state pair: wave w holds states 4w..4w+3,
+// lanes 0..31 the first two, lanes 32..63 the other two), so a workgroup holds
+// 32 channels x 16 states with half the registers per lane of the kernel
+// above: three workgroups fit on a compute unit instead of two.  Tiles of 32
+// steps are staged; each 16-step half starts from the checkpoint the forward
+// wrote for it (after step 15 of the tile, or before the tile), is re-run
+// forward into registers and then walked backward, so no step is recomputed.
+// dB / dC are summed over the 32 channels of a pair (reduce4_32); du / ddt
+// over the two pairs of a wave with a permlane32 swap and over the four waves
+// through LDS.
+constexpr int kB2Rows = 32;       // channels per workgroup
+constexpr int kB2Tile = kChunk;   // staged steps (two checkpoint intervals)
+constexpr int kB2Half = kCkpt;    // steps whose trajectory is held in registers
+
+// Sums v[0..3] over the 32 channel lanes of each pair (lanes with the same
+// lane / 32): lanes of row r = lane / 16 receive, in their low half (lane % 16
+// < 8), the total of v[r & 1] and, in their high half, of v[2 + (r & 1)].
+__device__ __forceinline__ float reduce4_32(const float (&v)[4]) {
+  float a0 = v[0], a1 = v[1], b0 = v[2], b1 = v[3];
+  swap16(a0, a1);
+  swap16(b0, b1);
+  // even rows: 2-lane sums (channels c, c + 16) of v[0] / v[2], odd rows of v[1] / v[3]
+  const float p = a0 + a1, q = b0 + b1;
+  float r = dpp_masked<0x128, 0xC>(p, q) + dpp_masked<0x128, 0x3>(q, p);
+  r += dpp<0x141>(r);  // row_half_mirror
+  r += dpp<0x4E>(r);   // quad_perm [2,3,0,1]
+  r += dpp<0xB1>(r);   // quad_perm [1,0,3,2]
+  return r;
+}
+
+struct BwdTile2 {
+  float4 u, dt, go, z, raw;  // this thread's 4 steps of one channel row
+  float B[2], C[2];          // StateRegs of the tile
+  float h0[2];               // this lane's two states before the tile, unmasked
+  float hm[2];               // and after its step kB2Half - 1
+};
+
+// Addressing of the 2-states-per-lane backward: every global access is a
+// workgroup-uniform base (scalar registers) plus a 32-bit lane offset, so the
+// loop-invariant part of an address costs one VGPR instead of two.  The host
+// takes this kernel only when every offset fits (bwd2_offsets_fit).
+template <bool VEC, class E>
+__device__ __forceinline__ float4 b2_load_row(const E* __restrict__ base, uint32_t roff, int t, int L) {
+  if constexpr (VEC) {
+    return Elem<E>::load4(base + (roff + static_cast<uint32_t>(min(t, L - 4))));
+  } else {
+    return make_float4(Elem<E>::load1(base + (roff + static_cast<uint32_t>(min(t, L - 1)))),
+                       Elem<E>::load1(base + (roff + static_cast<uint32_t>(min(t + 1, L - 1)))),
+                       Elem<E>::load1(base + (roff + static_cast<uint32_t>(min(t + 2, L - 1)))),
+                       Elem<E>::load1(base + (roff + static_cast<uint32_t>(min(t + 3, L - 1)))));
+  }
+}
+
+// B or C of steps t0.. (rows of stride ld from `base` = the batch row's first)
+template <class E>
+__device__ __forceinline__ void b2_load_states(float (&v)[2], const E* __restrict__ base, int ld, int t0,
+                                               int L, int N, int n_base) {
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int e = threadIdx.x + k * kThreads;
+    const int t = e / kPassStates, j = e - t * kPassStates;
+    v[k] = Elem<E>::load1(base + static_cast<uint32_t>(min(t0 + t, L - 1) * ld + min(n_base + j, N - 1)));
+  }
+}
+
+__device__ __forceinline__ void b2_load_pair(float (&h)[2], const float* __restrict__ base, uint32_t off,
+                                             int n0, int N, bool vec2) {
+  if (vec2) {
+    const float2 v = *reinterpret_cast<const float2*>(base + (off + static_cast<uint32_t>(n0)));
+    h[0] = v.x;
+    h[1] = v.y;
+  } else {
+    h[0] = base[off + static_cast<uint32_t>(min(n0, N - 1))];  // masked where they are consumed
+    h[1] = base[off + static_cast<uint32_t>(min(n0 + 1, N - 1))];
+  }
+}
+
+// Workgroup-uniform bases of the 2-states-per-lane backward.
+template <class E>
+struct Bwd2Bases {
+  const E *u, *dt, *go, *z, *raw;  // (b, d0, 0) of the [B, D, L] tensors
+  const E *Bm, *Cm;                // (b, 0, 0) of B and C
+  const float* ck;                 // chunk_states of (b, d0)
+};
+
+template <class E, bool VEC, bool GATED>
+__device__ __forceinline__ void bwd2_prefetch(BwdTile2& f, const BwdArgs<E>& a, const Bwd2Bases<E>& g,
+                                              uint32_t roff, int cc, uint32_t ckoff, int n0, bool vec2,
+                                              int tile) {
+  const int t0 = tile * kB2Tile;
+  f.u = b2_load_row<VEC>(g.u, roff, t0 + cc, a.L);
+  f.dt = b2_load_row<VEC>(g.dt, roff, t0 + cc, a.L);
+  f.go = b2_load_row<VEC>(g.go, roff, t0 + cc, a.L);
+  if constexpr (GATED) {
+    f.z = b2_load_row<VEC>(g.z, roff, t0 + cc, a.L);
+    f.raw = b2_load_row<VEC>(g.raw, roff, t0 + cc, a.L);
+  }
+  b2_load_states(f.B, g.Bm, a.ld_bc, t0, a.L, a.N, a.n_base);
+  b2_load_states(f.C, g.Cm, a.ld_bc, t0, a.L, a.N, a.n_base);
+  // chunk_states row k holds h after steps 32k + 15 and 32k + 31
+  b2_load_pair(f.h0, g.ck, ckoff + static_cast<uint32_t>(max(tile - 1, 0) * 2 * a.N + a.N), n0, a.N, vec2);
+  b2_load_pair(f.hm, g.ck, ckoff + static_cast<uint32_t>(tile * 2 * a.N), n0, a.N, vec2);
+}
+
+struct AdjTile2 {
+  float4 dt, go, z;
+  float C[2];
+};
+
+template <class E, bool VEC, bool GATED>
+__device__ __forceinline__ void adj2_prefetch(AdjTile2& f, const BwdArgs<E>& a, const Bwd2Bases<E>& g,
+                                              uint32_t roff, int cc, int tile) {
+  const int t0 = tile * kB2Tile;
+  f.dt = b2_load_row<VEC>(g.dt, roff, t0 + cc, a.L);
+  f.go = b2_load_row<VEC>(g.go, roff, t0 + cc, a.L);
+  if constexpr (GATED) f.z = b2_load_row<VEC>(g.z, roff, t0 + cc, a.L);
+  b2_load_states(f.C, g.Cm, a.ld_bc, t0, a.L, a.N, a.n_base);
+}
+
+// A staged float4 of (row r, steps t..t+3), zero outside the tensor.
+__device__ __forceinline__ float4 b2_mask(float4 v, bool row_ok, int t, int L) {
+  return make_float4(row_ok && t < L ? v.x : 0.f, row_ok && t + 1 < L ? v.y : 0.f,
+                     row_ok && t + 2 < L ? v.z : 0.f, row_ok && t + 3 < L ? v.w : 0.f);
+}
+__device__ __forceinline__ void b2_put(float* p, float4 v) {
+  p[0] = v.x;
+  p[1] = v.y;
+  p[2] = v.z;
+  p[3] = v.w;
+}
+__device__ __forceinline__ void b2_store_states(float* __restrict__ s, const float (&v)[2], int t0, int L,
+                                                int N, int n_base) {
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int e = threadIdx.x + k * kThreads;
+    const int t = e / kPassStates, j = e - t * kPassStates;
+    s[e] = (t0 + t < L && n_base + j < N) ? v[k] : 0.f;
+  }
+}
+
+template <class E, bool VEC, bool GATED>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
+void selective_bwd2_kernel(BwdArgs<E> a) {
+  constexpr int TT = kB2Tile;
+  constexpr int HT = kB2Half;
+  constexpr int RS = TT + 1;
+  constexpr int ROWS = kB2Rows;
+  static_assert(ROWS * TT == 4 * kThreads, "one float4 of each row tensor per thread");
+  __shared__ float s_u[ROWS * RS];
+  __shared__ float s_dt[ROWS * RS];
+  __shared__ float s_gy[ROWS * RS];
+  __shared__ __align__(16) float s_B[TT * kPassStates];
+  __shared__ __align__(16) float s_C[TT * kPassStates];
+  // per-wave du / ddt partials (sums over the wave's four states),
+  // [wave][channel][step], with the eight 4-step groups of channel c rotated
+  // by (c >> 1) & 7 (du_col): 16-byte stores by 32 consecutive channels and
+  // the finish's 16-byte reads both touch 16 distinct 16-byte bank groups
+  // per quarter-wave
+  auto du_col = [](int c, int step) { return ((((step >> 2) + (c >> 1)) & 7) << 2) | (step & 3); };
+  __shared__ __align__(16) float s_du[kMaxWaves * ROWS * TT];
+  __shared__ __align__(16) float s_ddt[kMaxWaves * ROWS * TT];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const int c = lane & (ROWS - 1);
+  const int hi = lane >> 5;
+  const int b = blockIdx.y;
+  const int d0 = blockIdx.x * ROWS;
+  const bool dvalid = d0 + c < a.D;
+  const int n0 = a.n_base + 4 * w + 2 * hi;  // this lane's states n0, n0 + 1
+  const int nw = min(kMaxWaves, (a.N - a.n_base + 3) / 4);
+  const bool wave_active = w < nw;
+  const bool vec2 = a.N % 2 == 0 && n0 + 2 <= a.N && (reinterpret_cast<uintptr_t>(a.ckpt) & 7) == 0;
+  // staging position of this thread: channel row rs, steps cs..cs+3
+  const int rs = static_cast<int>(threadIdx.x) >> 3, cs = (static_cast<int>(threadIdx.x) & 7) * 4;
+  const bool rs_ok = d0 + rs < a.D;
+  const uint32_t roff = static_cast<uint32_t>(min(d0 + rs, a.D - 1) - d0) * static_cast<uint32_t>(a.L);
+
+  float A2[2], Af[2], gs[2], gA[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    Af[j] = (dvalid && n0 + j < a.N) ? a.A[static_cast<size_t>(d0 + c) * a.N + n0 + j] : 0.f;
+    A2[j] = Af[j] * kLog2e;
+    gs[j] = 0.f;
+    gA[j] = 0.f;
+  }
+  const size_t rowbase = (static_cast<size_t>(b) * a.D + d0) * a.L;
+  Bwd2Bases<E> g;
+  g.u = a.u + rowbase;
+  g.dt = a.dt + rowbase;
+  g.go = a.gout + rowbase;
+  g.z = GATED ? a.z + rowbase : nullptr;
+  g.raw = GATED ? a.raw + rowbase : nullptr;
+  g.Bm = a.Bm + static_cast<size_t>(b) * a.L * a.ld_bc;
+  g.Cm = a.Cm + static_cast<size_t>(b) * a.L * a.ld_bc;
+  g.ck = a.ckpt + (static_cast<size_t>(b) * a.D + d0) * a.n_chunks * 2 * a.N;
+  const uint32_t ckoff = static_cast<uint32_t>(dvalid ? c : 0) * static_cast<uint32_t>(a.n_chunks * 2 * a.N);
+  const int n_tiles = (a.L + TT - 1) / TT;
+  // time split as in selective_bwd_kernel: segment s runs tiles
+  // [s n / S, (s + 1) n / S) after an adjoint-only pass over the later tiles
+  const int n_seg = static_cast<int>(gridDim.z), seg = static_cast<int>(blockIdx.z);
+  const int tile_lo = seg * n_tiles / n_seg;
+  const int tile_hi = (seg + 1) * n_tiles / n_seg;
+  if (tile_hi < n_tiles) {
+    AdjTile2 p;
+    adj2_prefetch<E, VEC, GATED>(p, a, g, roff, cs, n_tiles - 1);
+    for (int tile = n_tiles - 1; tile >= tile_hi; --tile) {
+      const int t0 = tile * TT;
+      __syncthreads();
+      b2_put(s_dt + rs * RS + cs, b2_mask(p.dt, rs_ok, t0 + cs, a.L));
+      b2_store_states(s_C, p.C, t0, a.L, a.N, a.n_base);
+      float4 gy = b2_mask(p.go, rs_ok, t0 + cs, a.L);
+      if constexpr (GATED) {
+        const float4 zz = p.z;
+        gy = make_float4(gy.x * zz.x * sigmoid(zz.x), gy.y * zz.y * sigmoid(zz.y),
+                         gy.z * zz.z * sigmoid(zz.z), gy.w * zz.w * sigmoid(zz.w));
+      }
+      b2_put(s_gy + rs * RS + cs, gy);
+      __syncthreads();
+      if (tile > tile_hi) adj2_prefetch<E, VEC, GATED>(p, a, g, roff, cs, tile - 1);
+      if (wave_active) {
+        const float* dtrow = s_dt + c * RS;
+        const float* gyrow = s_gy + c * RS;
+        const float* Ccol = s_C + 4 * w + 2 * hi;
+#pragma unroll 4
+        for (int i = TT - 1; i >= 0; --i) {
+          const float gy = gyrow[i], dtv = dtrow[i];
+          const float2 Ct = *reinterpret_cast<const float2*>(Ccol + i * kPassStates);
+          const float Cv[2] = {Ct.x, Ct.y};
+#pragma unroll
+          for (int j = 0; j < 2; ++j) gs[j] = fmaf(gy, Cv[j], gs[j]) * fast_exp2(dtv * A2[j]);
+        }
+      }
+    }
+  }
+
+  // du / ddt of the tile at t0, summed over the waves from their LDS partials
+  // and accumulated over passes: thread = (channel rs, steps cs..cs+3)
+  auto finish_dudt = [&](const int t0) {
+    const int t = t0 + cs;
+    if (!rs_ok || t >= a.L) return;
+    float4 su = make_float4(0.f, 0.f, 0.f, 0.f), sd = su;
+    for (int v = 0; v < nw; ++v) {
+      const float4 pu = *reinterpret_cast<const float4*>(s_du + (v * ROWS + rs) * TT + du_col(rs, cs));
+      const float4 pd = *reinterpret_cast<const float4*>(s_ddt + (v * ROWS + rs) * TT + du_col(rs, cs));
+      su.x += pu.x;
+      su.y += pu.y;
+      su.z += pu.z;
+      su.w += pu.w;
+      sd.x += pd.x;
+      sd.y += pd.y;
+      sd.z += pd.z;
+      sd.w += pd.w;
+    }
+    const uint32_t off = roff + static_cast<uint32_t>(t);
+    if (!a.first) {
+      const float* pu = a.du_acc + rowbase;
+      const float* pd = a.ddt_acc + rowbase;
+      su.x += pu[off];
+      sd.x += pd[off];
+      if (t + 1 < a.L) { su.y += pu[off + 1]; sd.y += pd[off + 1]; }
+      if (t + 2 < a.L) { su.z += pu[off + 2]; sd.z += pd[off + 2]; }
+      if (t + 3 < a.L) { su.w += pu[off + 3]; sd.w += pd[off + 3]; }
+    }
+    if (a.last) {
+      store_row4<VEC>(a.du + rowbase, off, t, a.L, su);
+      store_row4<VEC>(a.ddt + rowbase, off, t, a.L, sd);
+    } else {
+      store_row4<VEC>(a.du_acc + rowbase, off, t, a.L, su);
+      store_row4<VEC>(a.ddt_acc + rowbase, off, t, a.L, sd);
+    }
+  };
+
+  BwdTile2 nxt;
+  int prev_t0 = -1;  // the tile whose du / ddt are still to be finished
+  bwd2_prefetch<E, VEC, GATED>(nxt, a, g, roff, cs, ckoff, n0, vec2, tile_hi - 1);
+  for (int tile = tile_hi - 1; tile >= tile_lo; --tile) {
+    const int t0 = tile * TT;
+    const int nsteps = min(TT, a.L - t0);
+    __syncthreads();  // the previous tile's LDS readers are done
+    b2_put(s_u + rs * RS + cs, b2_mask(nxt.u, rs_ok, t0 + cs, a.L));
+    b2_put(s_dt + rs * RS + cs, b2_mask(nxt.dt, rs_ok, t0 + cs, a.L));
+    b2_store_states(s_B, nxt.B, t0, a.L, a.N, a.n_base);
+    b2_store_states(s_C, nxt.C, t0, a.L, a.N, a.n_base);
+    // gated upstream gradient into LDS; the first pass also writes dz
+    float4 dz_v = make_float4(0.f, 0.f, 0.f, 0.f);
+    bool dz_ok = false;
+    {
+      float4 gy = b2_mask(nxt.go, rs_ok, t0 + cs, a.L);
+      if constexpr (GATED) {
+        const float4 zz = nxt.z, go = gy;
+        const float4 sg = make_float4(sigmoid(zz.x), sigmoid(zz.y), sigmoid(zz.z), sigmoid(zz.w));
+        gy = make_float4(go.x * zz.x * sg.x, go.y * zz.y * sg.y, go.z * zz.z * sg.z, go.w * zz.w * sg.w);
+        if (a.first && rs_ok && t0 + cs < a.L) {
+          const float4 y = nxt.raw;
+          dz_v = make_float4(go.x * y.x * (sg.x * (1.f + zz.x * (1.f - sg.x))),
+                             go.y * y.y * (sg.y * (1.f + zz.y * (1.f - sg.y))),
+                             go.z * y.z * (sg.z * (1.f + zz.z * (1.f - sg.z))),
+                             go.w * y.w * (sg.w * (1.f + zz.w * (1.f - sg.w))));
+          dz_ok = true;
+        }
+      }
+      b2_put(s_gy + rs * RS + cs, gy);
+    }
+    float h0[2], hm[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const bool ok = dvalid && n0 + j < a.N;
+      h0[j] = (tile > 0 && ok) ? nxt.h0[j] : 0.f;
+      hm[j] = ok ? nxt.hm[j] : 0.f;
+    }
+    // the next tile's loads go out before this interval's stores (dz, and
+    // du / ddt of the previous tile, whose LDS partials this barrier interval
+    // still holds)
+    if (tile > tile_lo) bwd2_prefetch<E, VEC, GATED>(nxt, a, g, roff, cs, ckoff, n0, vec2, tile - 1);
+    if (dz_ok) store_row4<VEC>(a.dz + rowbase, roff + static_cast<uint32_t>(t0 + cs), t0 + cs, a.L, dz_v);
+    if (prev_t0 >= 0) finish_dudt(prev_t0);
+    __syncthreads();
+
+    if (wave_active) {
+      const float* dtrow = s_dt + c * RS;
+      const float* urow = s_u + c * RS;
+      const float* gyrow = s_gy + c * RS;
+      const float* Bcol = s_B + 4 * w + 2 * hi;
+      const float* Ccol = s_C + 4 * w + 2 * hi;
+      float* durow = (hi ? s_ddt : s_du) + (w * ROWS + c) * TT;
+      // keep[m]: this lane's share of the dB / dC tile partials of steps
+      // 8m .. 8m + 7 (see reduce4_32 for which lane holds which total)
+      float keep[4] = {0.f, 0.f, 0.f, 0.f};
+
+      // forward over steps s0 .. s0 + HT - 1 from the state before s0: the
+      // state after each step and its exp(dt A), in registers; operands read
+      // one step ahead, the empty asm keeping the reads from being hoisted
+      auto forward_half = [&](auto s0_tag, const float (&hst)[2], float (&hs)[HT][2], float (&dAs)[HT][2]) {
+        constexpr int s0 = decltype(s0_tag)::value;
+        float h[2] = {hst[0], hst[1]};
+        float ndt = dtrow[s0], nu = urow[s0];
+        float2 nB = *reinterpret_cast<const float2*>(Bcol + s0 * kPassStates);
+#pragma unroll
+        for (int i = 0; i < HT; ++i) {
+          const float dtv = ndt, uv = nu;
+          const float Bv[2] = {nB.x, nB.y};
+          if (i + 1 < HT) {
+            ndt = dtrow[s0 + i + 1];
+            nu = urow[s0 + i + 1];
+            nB = *reinterpret_cast<const float2*>(Bcol + (s0 + i + 1) * kPassStates);
+          }
+          const float dtu = dtv * uv;
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const float dA = fast_exp2(dtv * A2[j]);
+            h[j] = fmaf(dA, h[j], dtu * Bv[j]);
+            hs[i][j] = h[j];
+            dAs[i][j] = dA;
+          }
+          asm volatile("" ::: "memory");
+        }
+      };
+      // the adjoint over the same steps in reverse
+      auto adjoint_half = [&](auto s0_tag, const float (&hst)[2], const float (&hs)[HT][2],
+                              const float (&dAs)[HT][2]) {
+        constexpr int s0 = decltype(s0_tag)::value;
+        constexpr int il = HT - 1;
+        float ngy = gyrow[s0 + il], ndt = dtrow[s0 + il], nu = urow[s0 + il];
+        float2 nB = *reinterpret_cast<const float2*>(Bcol + (s0 + il) * kPassStates);
+        float2 nC = *reinterpret_cast<const float2*>(Ccol + (s0 + il) * kPassStates);
+        float du4[4], dd4[4];
+#pragma unroll
+        for (int i = il; i >= 0; --i) {
+          const float gy = ngy, dtv = ndt, uv = nu;
+          const float Bv[2] = {nB.x, nB.y};
+          const float Cv[2] = {nC.x, nC.y};
+          if (i > 0) {
+            ngy = gyrow[s0 + i - 1];
+            ndt = dtrow[s0 + i - 1];
+            nu = urow[s0 + i - 1];
+            nB = *reinterpret_cast<const float2*>(Bcol + (s0 + i - 1) * kPassStates);
+            nC = *reinterpret_cast<const float2*>(Ccol + (s0 + i - 1) * kPassStates);
+          }
+          const float dtu = dtv * uv;
+          float S1 = 0.f, S2 = 0.f;
+          float v[4];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const float hprev = i > 0 ? hs[i > 0 ? i - 1 : 0][j] : hst[j];
+            const float gacc = fmaf(gy, Cv[j], gs[j]);
+            const float gsn = gacc * dAs[i][j];
+            const float q = gsn * hprev;
+            gA[j] = fmaf(dtv, q, gA[j]);
+            S2 = fmaf(Af[j], q, S2);
+            S1 = fmaf(gacc, Bv[j], S1);
+            v[j] = gacc * dtu;         // dB contribution
+            v[2 + j] = gy * hs[i][j];  // dC contribution
+            gs[j] = gsn;
+          }
+          du4[i & 3] = dtv * S1;
+          dd4[i & 3] = fmaf(uv, S1, S2);
+          if ((i & 3) == 0) {
+            // over the wave's two pairs: lanes 0..31 keep du, 32..63 ddt
+            float x[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              float pu = du4[k], pd = dd4[k];
+              swap32(pu, pd);
+              x[k] = pu + pd;
+            }
+            *reinterpret_cast<float4*>(durow + du_col(c, s0 + i)) = make_float4(x[0], x[1], x[2], x[3]);
+          }
+          const float o = reduce4_32(v);
+          if ((lane & 7) == (i & 7)) keep[s0 / 8 + (i >> 3)] = o;
+          asm volatile("" ::: "memory");
+        }
+      };
+
+      // the second half first (from the checkpoint after step HT - 1), then
+      // the first; a tile that ends within its first half skips the second
+      if (nsteps > HT) {
+        float hs[HT][2], dAs[HT][2];
+        forward_half(std::integral_constant<int, HT>{}, hm, hs, dAs);
+        adjoint_half(std::integral_constant<int, HT>{}, hm, hs, dAs);
+      }
+      {
+        float hs[HT][2], dAs[HT][2];
+        forward_half(std::integral_constant<int, 0>{}, h0, hs, dAs);
+        adjoint_half(std::integral_constant<int, 0>{}, h0, hs, dAs);
+      }
+
+      // lane l holds in keep[m] the tile partial of step t0 + 8m + (l & 7):
+      // dB (low half of its row) or dC (high half) of state n_base + 4w + l / 16
+      const int n = a.n_base + 4 * w + (lane >> 4), c8 = lane & 7;
+      if (n < a.N) {
+        float* dst = (((lane >> 3) & 1) ? a.part_dC : a.part_dB) +
+                     (static_cast<size_t>(blockIdx.x) * a.Bsz + b) * a.L * a.N;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int st = 8 * m + c8;
+          if (st < nsteps) dst[static_cast<uint32_t>((t0 + st) * a.N + n)] = keep[m];
+        }
+      }
+    }
+    prev_t0 = t0;  // finished while the next tile is staged
+  }
+  __syncthreads();
+  finish_dudt(prev_t0);
+
+  if (dvalid && wave_active) {
+    float* dst = a.part_dA + ((static_cast<size_t>(seg) * a.Bsz + b) * a.D + d0) * a.N;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (n0 + j < a.N) dst[static_cast<uint32_t>(c * a.N + n0 + j)] = gA[j];
   }
 }
 
@@ -1569,6 +2034,30 @@ int time_segments(int64_t n_wg, int64_t L, int tile, int want) {
   return s;
 }
 
+// The 2-states-per-lane backward addresses everything as a workgroup base
+// plus a 32-bit (int) offset.
+bool bwd2_offsets_fit(int64_t L, int64_t N, int64_t ld_bc) {
+  const int64_t lim = INT_MAX;
+  return kB2Rows * L < lim && L * std::max(N, ld_bc) < lim &&
+         kB2Rows * num_chunks(L) * 2 * N < lim;
+}
+
+// States per lane of the [B, D, L] backward for `rows64` (batch row,
+// 64-channel) rows: 4 (two 64-channel workgroups per compute unit) while that
+// fills the device without a time split, 2 below (32-channel workgroups,
+// three per compute unit: twice the workgroups at 1.5x the occupancy).
+// OSSM_SEL_BWD_NPW=2|4 overrides.
+int bwd_states_per_lane(int64_t rows64) {
+  const char* env = std::getenv("OSSM_SEL_BWD_NPW");  // read per call: tests switch it
+  const int forced = env == nullptr ? 0 : std::atoi(env);
+  if (forced == 2 || forced == 4) return forced;
+  int dev = 0, n_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+    return 4;
+  return rows64 < static_cast<int64_t>(kBwdWgPerCu) * n_cu ? 2 : 4;
+}
+
 // States per lane of the [B, D, L] forward for `rows64` (batch row, 64-channel)
 // rows: 2 while 64-channel workgroups would give fewer than kFwdNpw2Below
 // waves per SIMD (OSSM_SEL_FWD_NPW=2|4 overrides).
@@ -1701,12 +2190,17 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
     return set_error(OSSM_ERR_INVALID_ARGUMENT,
                      std::string(what) + ": a gated scan needs raw_outputs and dgate");
   const int n_pass = static_cast<int>((dstate + kPassStates - 1) / kPassStates);
-  const int64_t n_dtiles = (dim + kWave - 1) / kWave;
+  // [B, D, L]: 2 states per lane (32-channel workgroups) or 4 (64-channel)
+  const bool npw2 = ml == nullptr && bwd2_offsets_fit(length, dstate, dstate) &&
+                    bwd_states_per_lane(batch * ((dim + kWave - 1) / kWave)) == 2;
+  const int64_t wg_rows = npw2 ? kB2Rows : kWave;
+  const int64_t n_dtiles = (dim + wg_rows - 1) / wg_rows;
   const int64_t n_bln = batch * length * dstate;
   const int64_t n_dn = dim * dstate;
   const int64_t n_rows = batch * dim * length;
   const bool staged = !std::is_same_v<E, float> && n_pass > 1;  // fp32 du/ddt between passes
-  const int n_seg = time_segments(n_dtiles * batch, length, kBwdTile, kBwdWgPerCu);
+  const int n_seg = npw2 ? time_segments(n_dtiles * batch, length, kB2Tile, kBwd2WgPerCu)
+                         : time_segments(n_dtiles * batch, length, kBwdTile, kBwdWgPerCu);
   const int64_t dA_rows = n_seg * batch;  // dA partial rows: (segment, batch row)
   const size_t part_floats =
       static_cast<size_t>(2 * n_dtiles * n_bln + dA_rows * n_dn) + (staged ? 2 * n_rows : 0);
@@ -1769,7 +2263,10 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
     a.last = p == n_pass - 1;
     using K = void (*)(BwdArgs<E>);
     K kern;
-    if constexpr (std::is_same_v<E, float>) {
+    if (npw2) {
+      kern = a.vec ? (gate ? selective_bwd2_kernel<E, true, true> : selective_bwd2_kernel<E, true, false>)
+                   : (gate ? selective_bwd2_kernel<E, false, true> : selective_bwd2_kernel<E, false, false>);
+    } else if constexpr (std::is_same_v<E, float>) {
       if (ml != nullptr) {
         kern = a.vec ? (gate ? selective_bwd_kernel<E, true, true, true> : selective_bwd_kernel<E, true, false, true>)
                      : (gate ? selective_bwd_kernel<E, false, true, true> : selective_bwd_kernel<E, false, false, true>);

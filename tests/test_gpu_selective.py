@@ -96,6 +96,8 @@ def test_selective_matches_reference_kernel_vectors(K, tag):
 # The forward runs 2 states per lane while 64-channel workgroups would give
 # fewer than 4 waves per SIMD, else 4: on a 256-CU MI355X every shape below
 # runs 2 except (64, 1024, 64, 16) (1,024 rows of 64 channels), which runs 4.
+# The backward likewise runs 2 states per lane below 512 such rows: every shape
+# but (64, 1024, 64, 16); test_selective_backward_both_layouts runs both.
 SHAPES = [(1, 1, 1, 1), (2, 5, 3, 3), (2, 70, 37, 5), (3, 65, 100, 16), (1, 130, 129, 20),
           (2, 32, 256, 32), (2, 48, 192, 32), (4, 96, 384, 64), (1, 3, 50, 256),
           (64, 1024, 64, 16)]
@@ -112,6 +114,26 @@ def test_selective_forward_backward_vs_oracle(K, shape, gated):
     _check_all(out, grads, *args, what=f"{shape}")
     if not gated:
         assert float(grads[5].abs().max()) == 0.0
+
+
+# ragged channels and steps (a last tile shorter than half a 32-step tile and
+# one longer), several passes over the states, and long rows that the time
+# split cuts into segments
+LAYOUT_SHAPES = [(2, 70, 37, 5), (3, 65, 100, 16), (1, 130, 129, 20), (4, 96, 384, 64),
+                 (1, 3, 50, 256), (1, 64, 1000, 16), (2, 40, 2070, 16)]
+
+
+@pytest.mark.parametrize("npw", [2, 4])
+@pytest.mark.parametrize("shape", LAYOUT_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_selective_backward_both_layouts(K, shape, npw, monkeypatch):
+    """The backward with 2 and with 4 states per lane (OSSM_SEL_BWD_NPW forces
+    the choice the library otherwise makes from the shape), gated."""
+    monkeypatch.setenv("OSSM_SEL_BWD_NPW", str(npw))
+    Bz, D, L, N = shape
+    args = selective_inputs(Bz, D, L, N, seed=5 * Bz + D + 3 * L + N + npw)
+    announce(f"selective backward npw={npw} B={Bz} D={D} L={L} N={N}")
+    out, _, _, grads = _run(K, *args)
+    _check_all(out, grads, *args, what=f"npw{npw} {shape}")
 
 
 def test_selective_checkpoints_are_states(K):

@@ -115,6 +115,19 @@ SHAPES = [(1, 1, 1, 1), (2, 70, 37, 5), (3, 65, 100, 16), (1, 130, 129, 20), (2,
 @pytest.mark.parametrize("gated", [True, False], ids=["gate", "nogate"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_selective_bf16_vs_oracle_and_fp32_path(K, shape, gated):
+    _bf16_case(K, shape, gated)
+
+
+@pytest.mark.parametrize("npw", [2, 4])
+@pytest.mark.parametrize("shape", [(2, 70, 37, 5), (1, 130, 129, 20), (4, 96, 384, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_selective_bf16_backward_both_layouts(K, shape, npw, monkeypatch):
+    """bf16 storage with the backward forced to 2 and to 4 states per lane."""
+    monkeypatch.setenv("OSSM_SEL_BWD_NPW", str(npw))
+    _bf16_case(K, shape, True)
+
+
+def _bf16_case(K, shape, gated):
     import torch
 
     Bz, D, L, N = shape
