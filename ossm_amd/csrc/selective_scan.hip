@@ -104,6 +104,27 @@ __device__ __forceinline__ float sigmoid(float z) {
   return __builtin_amdgcn_rcpf(1.f + fast_exp2(-z * kLog2e));
 }
 
+// Issue priority from the share of a workgroup's tiles still to run: waves of
+// the workgroups sharing a SIMD are otherwise issued oldest first, so the
+// first workgroup on a CU finishes well before the last and the CU's final
+// stretch runs one or two waves per SIMD.  With the wave that is behind (more
+// tiles left) ahead in the arbitration the workgroups resynchronise each time
+// they cross a level: priority 3 while more than half the tiles are left, 2
+// above a quarter, 1 above an eighth, 0 for the last eighth (finer at the end,
+// where a lead turns into idle SIMD time).  remaining in 1..total.
+__device__ __forceinline__ void balance_priority(int remaining, int total) {
+  const int r8 = 8 * remaining;
+  if (r8 > 4 * total) {
+    __builtin_amdgcn_s_setprio(3);
+  } else if (r8 > 2 * total) {
+    __builtin_amdgcn_s_setprio(2);
+  } else if (r8 > total) {
+    __builtin_amdgcn_s_setprio(1);
+  } else {
+    __builtin_amdgcn_s_setprio(0);
+  }
+}
+
 // ---- cross-lane helpers -------------------------------------------------------
 // permlane32 swap: lanes 32..63 of a trade places with lanes 0..31 of b.
 __device__ __forceinline__ void swap32(float& a, float& b) {
@@ -725,6 +746,7 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   }
   if constexpr (GATED && !BLD) load_gate(zn, t_lo);
   for (int t0 = t_lo; t0 < t_hi; t0 += TT) {
+    balance_priority((t_hi - t0 + TT - 1) / TT, (t_hi - t_lo + TT - 1) / TT);
     __syncthreads();  // the previous tile's LDS readers are done
     if constexpr (BLD) {
       store_cols<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
@@ -1175,6 +1197,7 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   for (int tile = tile_hi - 1; tile >= tile_lo; --tile) {
     const int t0 = tile * TT;
     const int nsteps = min(TT, a.L - t0);
+    balance_priority(tile - tile_lo + 1, tile_hi - tile_lo);
     __syncthreads();  // the previous tile's LDS readers are done
     float4 dz_v = make_float4(0.f, 0.f, 0.f, 0.f);
     size_t dz_off = 0;
@@ -1709,6 +1732,7 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
   for (int tile = tile_hi - 1; tile >= tile_lo; --tile) {
     const int t0 = tile * TT;
     const int nsteps = min(TT, a.L - t0);
+    balance_priority(tile - tile_lo + 1, tile_hi - tile_lo);
     __syncthreads();  // the previous tile's LDS readers are done
     b2_put(s_u + rs * RS + cs, b2_mask(nxt.u, rs_ok, t0 + cs, a.L));
     b2_put(s_dt + rs * RS + cs, b2_mask(nxt.dt, rs_ok, t0 + cs, a.L));
