@@ -143,19 +143,19 @@ __device__ __forceinline__ float dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
                                                                0xf, 0xf, false));
 }
-// Masked DPP move: lanes whose 4-lane bank is set in BANKS take v from the
-// lane CTRL selects, the others keep `old`.
-template <int CTRL, int BANKS>
-__device__ __forceinline__ float dpp_masked(float old, float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
-                                                               __builtin_bit_cast(int, v), CTRL, 0xf,
-                                                               BANKS, false));
+// Transposing stage between the two halves of each 16-lane row: the low half
+// returns p + p of the lane 8 above, the high half q + q of the lane 8 below
+// (each half keeps one value and sends the other: two selects and one
+// row_ror:8 add).
+__device__ __forceinline__ float transpose_ror8(float p, float q) {
+  const bool hi = (threadIdx.x & 8) != 0;
+  const float keep = hi ? q : p, send = hi ? p : q;
+  return keep + dpp<0x128>(send);
 }
 // Sums v[0..7] over all 64 lanes; every lane of half-row k (lanes 8k..8k+7)
 // receives the total of v[k].  Two transposing stages across rows
 // (permlane32 / permlane16 swaps), a third between the two halves of each row
-// (two masked row_ror:8 moves: the low half keeps its first value and takes
-// the high half's, the high half the reverse), then an 8-lane all-reduce.
+// (transpose_ror8), then an 8-lane all-reduce.
 __device__ __forceinline__ float reduce8(const float (&v)[8]) {
   float a0 = v[0], a1 = v[1], a2 = v[2], a3 = v[3];
   float b0 = v[4], b1 = v[5], b2 = v[6], b3 = v[7];
@@ -169,8 +169,7 @@ __device__ __forceinline__ float reduce8(const float (&v)[8]) {
   swap16(s1, s3);
   // row r: p = 4-lane sums of v[2r], q of v[2r + 1]
   const float p = s0 + s2, q = s1 + s3;
-  // low half: p + p of the lane 8 above; high half: q + q of the lane 8 below
-  float r = dpp_masked<0x128, 0xC>(p, q) + dpp_masked<0x128, 0x3>(q, p);
+  float r = transpose_ror8(p, q);
   r += dpp<0x141>(r);  // row_half_mirror
   r += dpp<0x4E>(r);   // quad_perm [2,3,0,1]
   r += dpp<0xB1>(r);   // quad_perm [1,0,3,2]
@@ -1475,8 +1474,7 @@ __device__ __forceinline__ float reduce4_32(const float (&v)[4]) {
   swap16(a0, a1);
   swap16(b0, b1);
   // even rows: 2-lane sums (channels c, c + 16) of v[0] / v[2], odd rows of v[1] / v[3]
-  const float p = a0 + a1, q = b0 + b1;
-  float r = dpp_masked<0x128, 0xC>(p, q) + dpp_masked<0x128, 0x3>(q, p);
+  float r = transpose_ror8(a0 + a1, b0 + b1);
   r += dpp<0x141>(r);  // row_half_mirror
   r += dpp<0x4E>(r);   // quad_perm [2,3,0,1]
   r += dpp<0xB1>(r);   // quad_perm [1,0,3,2]
