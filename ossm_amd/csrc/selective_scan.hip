@@ -1581,13 +1581,25 @@ __device__ __forceinline__ void b2_put(float* p, float4 v) {
   p[2] = v.z;
   p[3] = v.w;
 }
-__device__ __forceinline__ void b2_store_states(float* __restrict__ s, const float (&v)[2], int t0, int L,
-                                                int N, int n_base) {
+// (dt_t, u_t) pairs of steps cs..cs+3 of one channel row.
+__device__ __forceinline__ void b2_put_dtu(float* p, float4 dt, float4 u) {
+  *reinterpret_cast<float2*>(p) = make_float2(dt.x, u.x);
+  *reinterpret_cast<float2*>(p + 2) = make_float2(dt.y, u.y);
+  *reinterpret_cast<float2*>(p + 4) = make_float2(dt.z, u.z);
+  *reinterpret_cast<float2*>(p + 6) = make_float2(dt.w, u.w);
+}
+// B (when given) and C of the tile per state pair: s[(pair * kB2Tile + t) * 4
+// + (state & 1)] = B, + 2 = C; zero outside the tensor.
+__device__ __forceinline__ void b2_store_bc(float* __restrict__ s, const float* B, const float (&C)[2], int t0,
+                                            int L, int N, int n_base) {
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int e = threadIdx.x + k * kThreads;
     const int t = e / kPassStates, j = e - t * kPassStates;
-    s[e] = (t0 + t < L && n_base + j < N) ? v[k] : 0.f;
+    const bool ok = t0 + t < L && n_base + j < N;
+    float* q = s + ((j >> 1) * kB2Tile + t) * 4 + (j & 1);
+    if (B != nullptr) q[0] = ok ? B[k] : 0.f;
+    q[2] = ok ? C[k] : 0.f;
   }
 }
 
@@ -1599,11 +1611,14 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
   constexpr int RS = TT + 1;
   constexpr int ROWS = kB2Rows;
   static_assert(ROWS * TT == 4 * kThreads, "one float4 of each row tensor per thread");
-  __shared__ float s_u[ROWS * RS];
-  __shared__ float s_dt[ROWS * RS];
+  // dt and u interleaved, (dt_t, u_t) at [c * RS2 + 2t]: one 8-byte read per
+  // step; rows of 66 floats put the 32 channels' reads on distinct banks
+  constexpr int RS2 = 2 * TT + 2;
+  __shared__ __align__(16) float s_dtu[ROWS * RS2];
   __shared__ float s_gy[ROWS * RS];
-  __shared__ __align__(16) float s_B[TT * kPassStates];
-  __shared__ __align__(16) float s_C[TT * kPassStates];
+  // B and C of each state pair interleaved, (B_n, B_n+1, C_n, C_n+1) at
+  // [(pair * TT + t) * 4]: one 16-byte read per step
+  __shared__ __align__(16) float s_BC[kPassStates / 2 * TT * 4];
   // per-wave du / ddt partials (sums over the wave's four states),
   // [wave][channel][step], with the eight 4-step groups of channel c rotated
   // by (c >> 1) & 7 (du_col): 16-byte stores by 32 consecutive channels and
@@ -1660,8 +1675,8 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
     for (int tile = n_tiles - 1; tile >= tile_hi; --tile) {
       const int t0 = tile * TT;
       __syncthreads();
-      b2_put(s_dt + rs * RS + cs, b2_mask(p.dt, rs_ok, t0 + cs, a.L));
-      b2_store_states(s_C, p.C, t0, a.L, a.N, a.n_base);
+      b2_put_dtu(s_dtu + rs * RS2 + 2 * cs, b2_mask(p.dt, rs_ok, t0 + cs, a.L), make_float4(0.f, 0.f, 0.f, 0.f));
+      b2_store_bc(s_BC, nullptr, p.C, t0, a.L, a.N, a.n_base);
       float4 gy = b2_mask(p.go, rs_ok, t0 + cs, a.L);
       if constexpr (GATED) {
         const float4 zz = p.z;
@@ -1672,13 +1687,13 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
       __syncthreads();
       if (tile > tile_hi) adj2_prefetch<E, VEC, GATED>(p, a, g, roff, cs, tile - 1);
       if (wave_active) {
-        const float* dtrow = s_dt + c * RS;
+        const float* dturow = s_dtu + c * RS2;
         const float* gyrow = s_gy + c * RS;
-        const float* Ccol = s_C + 4 * w + 2 * hi;
+        const float* BCrow = s_BC + (2 * w + hi) * TT * 4;
 #pragma unroll 4
         for (int i = TT - 1; i >= 0; --i) {
-          const float gy = gyrow[i], dtv = dtrow[i];
-          const float2 Ct = *reinterpret_cast<const float2*>(Ccol + i * kPassStates);
+          const float gy = gyrow[i], dtv = dturow[2 * i];
+          const float2 Ct = *reinterpret_cast<const float2*>(BCrow + 4 * i + 2);
           const float Cv[2] = {Ct.x, Ct.y};
 #pragma unroll
           for (int j = 0; j < 2; ++j) gs[j] = fmaf(gy, Cv[j], gs[j]) * fast_exp2(dtv * A2[j]);
@@ -1732,10 +1747,9 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
     const int nsteps = min(TT, a.L - t0);
     balance_priority(tile - tile_lo + 1, tile_hi - tile_lo);
     __syncthreads();  // the previous tile's LDS readers are done
-    b2_put(s_u + rs * RS + cs, b2_mask(nxt.u, rs_ok, t0 + cs, a.L));
-    b2_put(s_dt + rs * RS + cs, b2_mask(nxt.dt, rs_ok, t0 + cs, a.L));
-    b2_store_states(s_B, nxt.B, t0, a.L, a.N, a.n_base);
-    b2_store_states(s_C, nxt.C, t0, a.L, a.N, a.n_base);
+    b2_put_dtu(s_dtu + rs * RS2 + 2 * cs, b2_mask(nxt.dt, rs_ok, t0 + cs, a.L),
+               b2_mask(nxt.u, rs_ok, t0 + cs, a.L));
+    b2_store_bc(s_BC, nxt.B, nxt.C, t0, a.L, a.N, a.n_base);
     // gated upstream gradient into LDS; the first pass also writes dz
     float4 dz_v = make_float4(0.f, 0.f, 0.f, 0.f);
     bool dz_ok = false;
@@ -1772,11 +1786,9 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
     __syncthreads();
 
     if (wave_active) {
-      const float* dtrow = s_dt + c * RS;
-      const float* urow = s_u + c * RS;
+      const float* dturow = s_dtu + c * RS2;
       const float* gyrow = s_gy + c * RS;
-      const float* Bcol = s_B + 4 * w + 2 * hi;
-      const float* Ccol = s_C + 4 * w + 2 * hi;
+      const float* BCrow = s_BC + (2 * w + hi) * TT * 4;  // this lane's state pair
       float* durow = (hi ? s_ddt : s_du) + (w * ROWS + c) * TT;
       // keep[m]: this lane's share of the dB / dC tile partials of steps
       // 8m .. 8m + 7 (see reduce4_32 for which lane holds which total)
@@ -1788,16 +1800,15 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
       auto forward_half = [&](auto s0_tag, const float (&hst)[2], float (&hs)[HT][2], float (&dAs)[HT][2]) {
         constexpr int s0 = decltype(s0_tag)::value;
         float h[2] = {hst[0], hst[1]};
-        float ndt = dtrow[s0], nu = urow[s0];
-        float2 nB = *reinterpret_cast<const float2*>(Bcol + s0 * kPassStates);
+        float2 ndu = *reinterpret_cast<const float2*>(dturow + 2 * s0);
+        float2 nB = *reinterpret_cast<const float2*>(BCrow + 4 * s0);
 #pragma unroll
         for (int i = 0; i < HT; ++i) {
-          const float dtv = ndt, uv = nu;
+          const float dtv = ndu.x, uv = ndu.y;
           const float Bv[2] = {nB.x, nB.y};
           if (i + 1 < HT) {
-            ndt = dtrow[s0 + i + 1];
-            nu = urow[s0 + i + 1];
-            nB = *reinterpret_cast<const float2*>(Bcol + (s0 + i + 1) * kPassStates);
+            ndu = *reinterpret_cast<const float2*>(dturow + 2 * (s0 + i + 1));
+            nB = *reinterpret_cast<const float2*>(BCrow + 4 * (s0 + i + 1));
           }
           const float dtu = dtv * uv;
 #pragma unroll
@@ -1815,21 +1826,19 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
                               const float (&dAs)[HT][2]) {
         constexpr int s0 = decltype(s0_tag)::value;
         constexpr int il = HT - 1;
-        float ngy = gyrow[s0 + il], ndt = dtrow[s0 + il], nu = urow[s0 + il];
-        float2 nB = *reinterpret_cast<const float2*>(Bcol + (s0 + il) * kPassStates);
-        float2 nC = *reinterpret_cast<const float2*>(Ccol + (s0 + il) * kPassStates);
+        float ngy = gyrow[s0 + il];
+        float2 ndu = *reinterpret_cast<const float2*>(dturow + 2 * (s0 + il));
+        float4 nBC = *reinterpret_cast<const float4*>(BCrow + 4 * (s0 + il));
         float du4[4], dd4[4];
 #pragma unroll
         for (int i = il; i >= 0; --i) {
-          const float gy = ngy, dtv = ndt, uv = nu;
-          const float Bv[2] = {nB.x, nB.y};
-          const float Cv[2] = {nC.x, nC.y};
+          const float gy = ngy, dtv = ndu.x, uv = ndu.y;
+          const float Bv[2] = {nBC.x, nBC.y};
+          const float Cv[2] = {nBC.z, nBC.w};
           if (i > 0) {
             ngy = gyrow[s0 + i - 1];
-            ndt = dtrow[s0 + i - 1];
-            nu = urow[s0 + i - 1];
-            nB = *reinterpret_cast<const float2*>(Bcol + (s0 + i - 1) * kPassStates);
-            nC = *reinterpret_cast<const float2*>(Ccol + (s0 + i - 1) * kPassStates);
+            ndu = *reinterpret_cast<const float2*>(dturow + 2 * (s0 + i - 1));
+            nBC = *reinterpret_cast<const float4*>(BCrow + 4 * (s0 + i - 1));
           }
           const float dtu = dtv * uv;
           float S1 = 0.f, S2 = 0.f;
