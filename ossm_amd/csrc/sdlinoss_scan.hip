@@ -696,7 +696,7 @@ struct TileTW {
   int T, W;
 };
 #define OSSM_SDL_FWD_TILES(X) X(8, 16) X(16, 8) X(8, 8) X(16, 4) X(4, 16)
-#define OSSM_SDL_BWD_TILES(X) X(8, 8) X(8, 4) X(4, 8) X(4, 16) X(16, 4)
+#define OSSM_SDL_BWD_TILES(X) X(8, 8) X(8, 4) X(4, 8) X(4, 16) X(16, 4) X(16, 8)
 
 TileTW sdl_tile(const char* env, TileTW dflt) {
   const char* e = std::getenv(env);
@@ -832,7 +832,12 @@ template <int V>
 int sdl_backward_v(const SdlParams& prm, const ParamShape (&shapes)[3], const void* bu,
                    const void* states, const void* gout, float* const (&grads)[3], void* gbu,
                    int64_t L, int64_t B, int64_t M, hipStream_t stream) {
-  static const TileTW tile = sdl_tile("OSSM_SDL_TILE_BWD", TileTW{16, 4});
+  // Parameters broadcast over time run 8 waves of 16 steps (128-step chunks,
+  // one workgroup per CU: 109 vs 116 us at config 2's shape), per-step
+  // parameters 4 waves (the 8-wave tile is no faster for them).
+  static const TileTW forced = sdl_tile("OSSM_SDL_TILE_BWD", TileTW{0, 0});
+  const bool tb = prm.a.t_stride == 0 && prm.g.t_stride == 0 && prm.s.t_stride == 0;
+  const TileTW tile = forced.T != 0 ? forced : (tb ? TileTW{16, 8} : TileTW{16, 4});
 #define OSSM_SDL_BWD_CASE(TT, WW)                                                            \
   if (tile.T == TT && tile.W == WW)                                                          \
     return sdl_backward_tw<V, TT, WW>(prm, shapes, bu, states, gout, grads, gbu, L, B, M, stream);
