@@ -575,7 +575,8 @@ __global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
 // ============================================================================
 // Sums over broadcast axes: out[n][c] = sum_r in[n][r][c], in fp64, fixed
 // order.  Pass 1: block (64-column tile, row group q) sums rows
-// r = q*4 + wave + k*4G; pass 2 adds the G row groups.
+// r = q*4 + wave + k*4G; pass 2 adds the G row groups.  Short reductions
+// (sdl_colsum_direct) take one launch instead.
 // ============================================================================
 constexpr int kSumGroups = 32;
 
@@ -637,6 +638,28 @@ __global__ __launch_bounds__(256) void sdl_colsum_pass2(ColSums all) {
   out[i] = static_cast<float>(s);
 }
 
+// One launch for short reductions (R <= kDirectRows): a thread per output,
+// its rows in order in fp64, eight loads in flight.
+constexpr int kDirectRows = 256;
+__global__ __launch_bounds__(256) void sdl_colsum_direct(ColSums all) {
+  const ColSum& cs = all.s[blockIdx.z];
+  const int C = cs.C, R = cs.R;
+  const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<long long>(cs.nb) * C) return;
+  const int n = static_cast<int>(i / C), col = static_cast<int>(i - static_cast<long long>(n) * C);
+  const float* src = cs.in + static_cast<size_t>(n) * R * C + col;
+  double s = 0.0;
+  for (int r0 = 0; r0 < R; r0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[static_cast<size_t>(min(r0 + u, R - 1)) * C];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (r0 + u < R) s += static_cast<double>(v[u]);
+  }
+  cs.out[i] = static_cast<float>(s);
+}
+
 __global__ void sdl_zero_kernel(float* __restrict__ p, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0.f;
@@ -666,15 +689,23 @@ ParamView view_of(const ParamShape& s, int64_t L, int64_t B, int64_t M) {
   return v;
 }
 
-// Runs the `n` reductions of `all` in two launches.
+// Runs the `n` reductions of `all`: in one launch when every one sums at
+// most kDirectRows rows, else in two.
 int launch_colsums(const ColSums& all, int n, hipStream_t stream) {
   if (n == 0) return OSSM_OK;
-  int64_t max_blocks = 0, max_out = 0;
+  int64_t max_blocks = 0, max_out = 0, max_rows = 0;
   for (int k = 0; k < n; ++k) {
     max_blocks = std::max<int64_t>(max_blocks, static_cast<int64_t>(all.s[k].nb) * all.s[k].col_tiles);
     max_out = std::max<int64_t>(max_out, static_cast<int64_t>(all.s[k].nb) * all.s[k].C);
+    max_rows = std::max<int64_t>(max_rows, all.s[k].R);
   }
-  if (max_blocks > INT_MAX) return set_error(OSSM_ERR_UNSUPPORTED, "gradient reduction too large");
+  if (max_blocks > INT_MAX || (max_out + 255) / 256 > INT_MAX)
+    return set_error(OSSM_ERR_UNSUPPORTED, "gradient reduction too large");
+  if (max_rows <= kDirectRows) {
+    hipLaunchKernelGGL(sdl_colsum_direct, dim3(static_cast<unsigned>((max_out + 255) / 256), 1, n),
+                       dim3(256), 0, stream, all);
+    return launch_check("sdl_colsum_direct");
+  }
   hipLaunchKernelGGL(sdl_colsum_pass1, dim3(static_cast<unsigned>(max_blocks), kSumGroups, n),
                      dim3(256), 0, stream, all);
   if (int rc = launch_check("sdl_colsum_pass1")) return rc;

@@ -110,7 +110,8 @@ def test_sdlinoss_matches_reference_kernel_vectors(K, variant, tag):
 
 
 # (L, B, M): tiny, ragged channel counts (B*M not a multiple of 64), several
-# forward chunks (128 steps) and backward chunks (64 steps), long look-back
+# forward chunks (128 steps) and backward chunks (64 steps; 128 with parameters
+# broadcast over time), long look-back
 SHAPES = [(1, 1, 1), (5, 2, 3), (70, 3, 5), (300, 3, 70), (1000, 2, 64), (129, 5, 33)]
 
 
@@ -122,6 +123,18 @@ def test_sdlinoss_vs_oracle_layouts(K, variant, tag):
     announce(f"sdlinoss {variant} {tag} L={L} B={B} M={M}")
     states, grads = _run(K, variant, *args)
     _check(variant, *args, states, grads, f"{variant}/{tag}")
+
+
+@pytest.mark.parametrize("tag", ["bcast_t", "m"])
+def test_sdlinoss_long_parameter_reductions(K, tag):
+    """Parameters broadcast over time on long rows: [1,B,M] sums 32 chunk
+    partials per output (the one-launch column sum), [M] sums 32 chunks x 16
+    batch rows (more than 256 rows: the two-pass column sum)."""
+    L, B, M = 4096, 16, 64
+    args = sdl_inputs("imex1", tag, L, B, M, seed=21 + len(tag))
+    announce(f"sdlinoss imex1 {tag} L={L} B={B} M={M}")
+    states, grads = _run(K, "imex1", *args)
+    _check("imex1", *args, states, grads, f"imex1/{tag}/long")
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
