@@ -496,6 +496,65 @@ struct FwdArgs {
   const float* dt_bias;
 };
 
+// (dt_t, u_t) pairs of a [.., L] row tile: s[row * RS2 + 2t].
+template <int TT, int RS2, int ROWS>
+__device__ __forceinline__ void store_rows_dtu(float* __restrict__ s, const RowRegs<TT, ROWS>& dt,
+                                               const RowRegs<TT, ROWS>& u, int d0, int D, int t0, int L) {
+#pragma unroll
+  for (int k = 0; k < RowRegs<TT, ROWS>::kQ; ++k) {
+    int row, c;
+    tile_pos<TT>(k, row, c);
+    const float4 a = masked<TT>(dt, k, d0, D, t0, L);
+    const float4 b = masked<TT>(u, k, d0, D, t0, L);
+    float* p = s + row * RS2 + 2 * c;
+    *reinterpret_cast<float2*>(p) = make_float2(a.x, b.x);
+    *reinterpret_cast<float2*>(p + 2) = make_float2(a.y, b.y);
+    *reinterpret_cast<float2*>(p + 4) = make_float2(a.z, b.z);
+    *reinterpret_cast<float2*>(p + 6) = make_float2(a.w, b.w);
+  }
+}
+
+// The same from a [B, L, D] tile, dt through its softplus (as
+// store_cols_softplus).
+template <int TT, int RS2>
+__device__ __forceinline__ void store_cols_dtu(float* __restrict__ s, const RowRegs<TT>& dt,
+                                               const RowRegs<TT>& u, const float* __restrict__ bias,
+                                               int d0, int D, int t0, int L) {
+#pragma unroll
+  for (int k = 0; k < RowRegs<TT>::kQ; ++k) {
+    int step, c4;
+    tile_pos_bld<TT>(k, step, c4);
+    const float4 v = dt.v[k];
+    const float x[4] = {v.x, v.y, v.z, v.w};
+    const float4 uu = masked_cols<TT>(u, k, d0, D, t0, L);
+    const float uv[4] = {uu.x, uu.y, uu.z, uu.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = min(d0 + c4 + e, D - 1);
+      const float sp = col_ok<TT>(k, e, d0, D, t0, L) ? softplus(x[e] + (bias != nullptr ? bias[d] : 0.f)) : 0.f;
+      *reinterpret_cast<float2*>(s + (c4 + e) * RS2 + 2 * step) = make_float2(sp, uv[e]);
+    }
+  }
+}
+
+// B and C rows of a tile per state group of NPW: s[(t * groups + group) * 2 NPW
+// + (state % NPW)] = B, + NPW = C (the groups of a step contiguous, so the
+// lanes of a wave reading one step touch distinct banks); zero outside the
+// tensor.
+template <int TT, int NPW>
+__device__ __forceinline__ void store_bc(float* __restrict__ s, const StateRegs<TT>& B,
+                                         const StateRegs<TT>& C, int t0, int L, int N, int n_base) {
+#pragma unroll
+  for (int k = 0; k < StateRegs<TT>::kQ; ++k) {
+    const int e = threadIdx.x + k * kThreads;
+    const int t = e / kPassStates, j = e - t * kPassStates;
+    const bool ok = t0 + t < L && n_base + j < N;
+    float* q = s + (t * (kPassStates / NPW) + j / NPW) * 2 * NPW + (j % NPW);
+    q[0] = ok ? B.v[k] : 0.f;
+    q[NPW] = ok ? C.v[k] : 0.f;
+  }
+}
+
 // The forward's lane layout for NPW states per lane: lane = (channel
 // c = lane % CW, state group g = lane / CW), GR = 16 / NPW groups, so a wave
 // holds all 16 states of CW = 64 / GR channels and a workgroup 4 CW channels.
@@ -662,10 +721,13 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   constexpr int ROWS = LY::kRows, CW = LY::kWaveCh, SEG = LY::kSeg;
   static_assert(TT == 32, "reduce_groups assumes 32-step tiles");
   static_assert(!BLD || NPW == 4, "the [B, L, D] layout stages 64 channels");
-  __shared__ float s_u[ROWS * RS];
-  __shared__ float s_dt[ROWS * RS];
-  __shared__ __align__(16) float s_B[TT * kPassStates];
-  __shared__ __align__(16) float s_C[TT * kPassStates];
+  // dt and u interleaved, (dt_t, u_t) at [row * RS2 + 2t]: one 8-byte read per
+  // step (rows of 66 floats: the wave's rows on distinct banks)
+  constexpr int RS2 = 2 * TT + 2;
+  __shared__ __align__(8) float s_dtu[ROWS * RS2];
+  // B and C of each state group interleaved: (B of its NPW states, C of them)
+  // at [(t * groups + group) * 2 NPW], one or two 16-byte reads per step
+  __shared__ __align__(16) float s_BC[kPassStates * TT * 2];
   // BLD: the tile's y, [step][channel], stored to HBM as rows of channels
   constexpr int YS = kWave + 4;  // row stride (floats): 16-byte rows, banks staggered
   __shared__ __align__(16) float s_y[BLD ? TT * YS : 1];
@@ -699,10 +761,19 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   auto put_seg = [&](auto* dst, int t0, const float (&v)[SEG]) {
     store_seg<NPW, VEC>(dst, my_row, t0, g, a.L, v);
   };
-  // this lane's NPW states of B or C at step i of a staged tile, as one load
+  // this lane's NPW states of B and of C at step i of a staged tile
   using SV = std::conditional_t<NPW == 4, float4, float2>;
-  auto state_vals = [&](const float* col, int i) {
-    return *reinterpret_cast<const SV*>(col + i * kPassStates);
+  struct BCv {
+    SV b, c;
+  };
+  auto bc_vals = [&](const float* grp, int i) {
+    const float* p = grp + i * 2 * kPassStates;
+    if constexpr (NPW == 4) {
+      return BCv{*reinterpret_cast<const float4*>(p), *reinterpret_cast<const float4*>(p + 4)};
+    } else {
+      const float4 v = *reinterpret_cast<const float4*>(p);
+      return BCv{make_float2(v.x, v.y), make_float2(v.z, v.w)};
+    }
   };
 
   // Time split: gridDim.z segments of consecutive tiles; segment s scans
@@ -721,24 +792,22 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     // h only over the earlier segment's tiles
     __syncthreads();
     if constexpr (BLD) {
-      store_cols<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
-      store_cols_softplus<TT, RS>(s_dt, nxt.dt, a.dt_bias, d0, a.D, t0, a.L);
+      store_cols_dtu<TT, RS2>(s_dtu, nxt.dt, nxt.u, a.dt_bias, d0, a.D, t0, a.L);
     } else {
-      store_rows<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
-      store_rows<TT, RS>(s_dt, nxt.dt, d0, a.D, t0, a.L);
+      store_rows_dtu<TT, RS2>(s_dtu, nxt.dt, nxt.u, d0, a.D, t0, a.L);
     }
-    store_states<TT>(s_B, nxt.B, t0, a.L, a.N, a.n_base);
+    store_bc<TT, NPW>(s_BC, nxt.B, nxt.C, t0, a.L, a.N, a.n_base);
     __syncthreads();
     fwd_prefetch<E, VEC, BLD>(nxt, a, row0, bc0, d0, t0 + TT);
-    const float* urow = s_u + r * RS;
-    const float* dtrow = s_dt + r * RS;
-    const float* Bcol = s_B + g * NPW;
+    const float* dturow = s_dtu + r * RS2;
+    const float* BCgrp = s_BC + g * 2 * NPW;
 #pragma unroll 8
     for (int i = 0; i < TT; ++i) {
-      const float dtv = dtrow[i];
-      const float dtu = dtv * urow[i];
+      const float2 du = *reinterpret_cast<const float2*>(dturow + 2 * i);
+      const float dtv = du.x;
+      const float dtu = dtv * du.y;
       float Bv[NPW];
-      unpack(state_vals(Bcol, i), Bv);
+      unpack(bc_vals(BCgrp, i).b, Bv);
 #pragma unroll
       for (int j = 0; j < NPW; ++j) h[j] = fmaf(fast_exp2(dtv * A2[j]), h[j], dtu * Bv[j]);
     }
@@ -748,14 +817,11 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
     balance_priority((t_hi - t0 + TT - 1) / TT, (t_hi - t_lo + TT - 1) / TT);
     __syncthreads();  // the previous tile's LDS readers are done
     if constexpr (BLD) {
-      store_cols<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
-      store_cols_softplus<TT, RS>(s_dt, nxt.dt, a.dt_bias, d0, a.D, t0, a.L);
+      store_cols_dtu<TT, RS2>(s_dtu, nxt.dt, nxt.u, a.dt_bias, d0, a.D, t0, a.L);
     } else {
-      store_rows<TT, RS>(s_u, nxt.u, d0, a.D, t0, a.L);
-      store_rows<TT, RS>(s_dt, nxt.dt, d0, a.D, t0, a.L);
+      store_rows_dtu<TT, RS2>(s_dtu, nxt.dt, nxt.u, d0, a.D, t0, a.L);
     }
-    store_states<TT>(s_B, nxt.B, t0, a.L, a.N, a.n_base);
-    store_states<TT>(s_C, nxt.C, t0, a.L, a.N, a.n_base);
+    store_bc<TT, NPW>(s_BC, nxt.B, nxt.C, t0, a.L, a.N, a.n_base);
     float zt[SEG];
 #pragma unroll
     for (int k = 0; k < SEG; ++k) zt[k] = zn[k];
@@ -794,10 +860,8 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
         for (int j = 0; j < NPW; ++j) hck[i / kCkpt][j] = h[j];
       }
     };
-    const float* urow = s_u + r * RS;
-    const float* dtrow = s_dt + r * RS;
-    const float* Bcol = s_B + g * NPW;
-    const float* Ccol = s_C + g * NPW;
+    const float* dturow = s_dtu + r * RS2;
+    const float* BCgrp = s_BC + g * 2 * NPW;
     {
       // Software-pipelined: the LDS operands of the next kGroup steps are read
       // before this group is computed, so a read's latency is covered by a
@@ -810,10 +874,12 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
 #pragma unroll
         for (int q = 0; q < kGroup; ++q) {
           const int i = gr * kGroup + q;
-          pdt[buf][q] = dtrow[i];
-          pu[buf][q] = urow[i];
-          pB[buf][q] = state_vals(Bcol, i);
-          pC[buf][q] = state_vals(Ccol, i);
+          const float2 du = *reinterpret_cast<const float2*>(dturow + 2 * i);
+          pdt[buf][q] = du.x;
+          pu[buf][q] = du.y;
+          const BCv bc = bc_vals(BCgrp, i);
+          pB[buf][q] = bc.b;
+          pC[buf][q] = bc.c;
         }
       };
       fetch(0, 0);
