@@ -1654,8 +1654,9 @@ __device__ __forceinline__ void b2_put_dtu(float* p, float4 dt, float4 u) {
   *reinterpret_cast<float2*>(p + 4) = make_float2(dt.z, u.z);
   *reinterpret_cast<float2*>(p + 6) = make_float2(dt.w, u.w);
 }
-// B (when given) and C of the tile per state pair: s[(pair * kB2Tile + t) * 4
-// + (state & 1)] = B, + 2 = C; zero outside the tensor.
+// B (when given) and C of the tile per state pair: s[(t * 8 + pair) * 4 +
+// (state & 1)] = B, + 2 = C (the pairs of a step contiguous: a wave's two pairs
+// on distinct banks); zero outside the tensor.
 __device__ __forceinline__ void b2_store_bc(float* __restrict__ s, const float* B, const float (&C)[2], int t0,
                                             int L, int N, int n_base) {
 #pragma unroll
@@ -1663,7 +1664,7 @@ __device__ __forceinline__ void b2_store_bc(float* __restrict__ s, const float* 
     const int e = threadIdx.x + k * kThreads;
     const int t = e / kPassStates, j = e - t * kPassStates;
     const bool ok = t0 + t < L && n_base + j < N;
-    float* q = s + ((j >> 1) * kB2Tile + t) * 4 + (j & 1);
+    float* q = s + (t * (kPassStates / 2) + (j >> 1)) * 4 + (j & 1);
     if (B != nullptr) q[0] = ok ? B[k] : 0.f;
     q[2] = ok ? C[k] : 0.f;
   }
@@ -1683,7 +1684,7 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
   __shared__ __align__(16) float s_dtu[ROWS * RS2];
   __shared__ float s_gy[ROWS * RS];
   // B and C of each state pair interleaved, (B_n, B_n+1, C_n, C_n+1) at
-  // [(pair * TT + t) * 4]: one 16-byte read per step
+  // [(t * 8 + pair) * 4]: one 16-byte read per step
   __shared__ __align__(16) float s_BC[kPassStates / 2 * TT * 4];
   // per-wave du / ddt partials (sums over the wave's four states),
   // [wave][channel][step], with the eight 4-step groups of channel c rotated
@@ -1755,11 +1756,11 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
       if (wave_active) {
         const float* dturow = s_dtu + c * RS2;
         const float* gyrow = s_gy + c * RS;
-        const float* BCrow = s_BC + (2 * w + hi) * TT * 4;
+        const float* BCrow = s_BC + (2 * w + hi) * 4;
 #pragma unroll 4
         for (int i = TT - 1; i >= 0; --i) {
           const float gy = gyrow[i], dtv = dturow[2 * i];
-          const float2 Ct = *reinterpret_cast<const float2*>(BCrow + 4 * i + 2);
+          const float2 Ct = *reinterpret_cast<const float2*>(BCrow + 32 * i + 2);
           const float Cv[2] = {Ct.x, Ct.y};
 #pragma unroll
           for (int j = 0; j < 2; ++j) gs[j] = fmaf(gy, Cv[j], gs[j]) * fast_exp2(dtv * A2[j]);
@@ -1854,7 +1855,7 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
     if (wave_active) {
       const float* dturow = s_dtu + c * RS2;
       const float* gyrow = s_gy + c * RS;
-      const float* BCrow = s_BC + (2 * w + hi) * TT * 4;  // this lane's state pair
+      const float* BCrow = s_BC + (2 * w + hi) * 4;  // this lane's state pair
       float* durow = (hi ? s_ddt : s_du) + (w * ROWS + c) * TT;
       // keep[m]: this lane's share of the dB / dC tile partials of steps
       // 8m .. 8m + 7 (see reduce4_32 for which lane holds which total)
@@ -1867,14 +1868,14 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
         constexpr int s0 = decltype(s0_tag)::value;
         float h[2] = {hst[0], hst[1]};
         float2 ndu = *reinterpret_cast<const float2*>(dturow + 2 * s0);
-        float2 nB = *reinterpret_cast<const float2*>(BCrow + 4 * s0);
+        float2 nB = *reinterpret_cast<const float2*>(BCrow + 32 * s0);
 #pragma unroll
         for (int i = 0; i < HT; ++i) {
           const float dtv = ndu.x, uv = ndu.y;
           const float Bv[2] = {nB.x, nB.y};
           if (i + 1 < HT) {
             ndu = *reinterpret_cast<const float2*>(dturow + 2 * (s0 + i + 1));
-            nB = *reinterpret_cast<const float2*>(BCrow + 4 * (s0 + i + 1));
+            nB = *reinterpret_cast<const float2*>(BCrow + 32 * (s0 + i + 1));
           }
           const float dtu = dtv * uv;
 #pragma unroll
@@ -1894,7 +1895,7 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
         constexpr int il = HT - 1;
         float ngy = gyrow[s0 + il];
         float2 ndu = *reinterpret_cast<const float2*>(dturow + 2 * (s0 + il));
-        float4 nBC = *reinterpret_cast<const float4*>(BCrow + 4 * (s0 + il));
+        float4 nBC = *reinterpret_cast<const float4*>(BCrow + 32 * (s0 + il));
         float du4[4], dd4[4];
 #pragma unroll
         for (int i = il; i >= 0; --i) {
@@ -1904,7 +1905,7 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
           if (i > 0) {
             ngy = gyrow[s0 + i - 1];
             ndu = *reinterpret_cast<const float2*>(dturow + 2 * (s0 + i - 1));
-            nBC = *reinterpret_cast<const float4*>(BCrow + 4 * (s0 + i - 1));
+            nBC = *reinterpret_cast<const float4*>(BCrow + 32 * (s0 + i - 1));
           }
           const float dtu = dtv * uv;
           float S1 = 0.f, S2 = 0.f;
