@@ -1982,25 +1982,60 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
 }
 
 // Adds the partials in a fixed order.  Blocks [0, n_bc_blocks): dB and dC,
-// one element per thread, summed over the channel tiles.  The remaining
-// blocks: dA, kFinCols columns per block, each column summed over `rows`
-// partial rows (batch rows x time segments) by kFinGroups row groups (eight
-// loads in flight each) and then over the groups in order through LDS.
-constexpr int kFinThreads = 1024;
-constexpr int kFinCols = 64;
+// summed over the channel tiles, kFinVec consecutive elements per thread when
+// `vec` (16-byte loads; n_bln % 4 == 0 and 16-byte aligned outputs), else one.
+// The remaining blocks: dA, kFinCols columns per block, each column summed over
+// `rows` partial rows (batch rows x time segments) by kFinGroups row groups
+// (eight loads in flight each) and then over the groups in order through LDS.
+constexpr int kFinThreads = 256;
+constexpr int kFinCols = 16;
 constexpr int kFinGroups = kFinThreads / kFinCols;
+constexpr int kFinVec = 4;
 
 template <class E>
 __global__ __launch_bounds__(kFinThreads) void selective_finish_kernel(
     const float* __restrict__ part_dB, const float* __restrict__ part_dC,
     const float* __restrict__ part_dA, E* __restrict__ dB, E* __restrict__ dC,
-    float* __restrict__ dA, int64_t n_bln, int n_dtiles, int64_t n_dn, int rows, int n_bc_blocks) {
+    float* __restrict__ dA, int64_t n_bln, int n_dtiles, int64_t n_dn, int rows, int n_bc_blocks,
+    int vec) {
   if (static_cast<int>(blockIdx.x) < n_bc_blocks) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kFinThreads + threadIdx.x;
-    if (i >= n_bln) return;
     // tiles added in ascending order; the loads of 8 tiles are issued before
     // any of them is added (the sum stays the same, bit for bit)
     constexpr int kBatch = 8;
+    if (vec) {
+      const int64_t i = (static_cast<int64_t>(blockIdx.x) * kFinThreads + threadIdx.x) * kFinVec;
+      if (i >= n_bln) return;
+      float4 sb = make_float4(0.f, 0.f, 0.f, 0.f), sc = sb;
+      auto add = [](float4& s, float4 v) {
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+      };
+      int k = 0;
+      for (; k + kBatch <= n_dtiles; k += kBatch) {
+        float4 vb[kBatch], vc[kBatch];
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q) {
+          vb[q] = *reinterpret_cast<const float4*>(part_dB + static_cast<size_t>(k + q) * n_bln + i);
+          vc[q] = *reinterpret_cast<const float4*>(part_dC + static_cast<size_t>(k + q) * n_bln + i);
+        }
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q) {
+          add(sb, vb[q]);
+          add(sc, vc[q]);
+        }
+      }
+      for (; k < n_dtiles; ++k) {
+        add(sb, *reinterpret_cast<const float4*>(part_dB + static_cast<size_t>(k) * n_bln + i));
+        add(sc, *reinterpret_cast<const float4*>(part_dC + static_cast<size_t>(k) * n_bln + i));
+      }
+      Elem<E>::store4(dB + i, sb);
+      Elem<E>::store4(dC + i, sc);
+      return;
+    }
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kFinThreads + threadIdx.x;
+    if (i >= n_bln) return;
     float sb = 0.f, sc = 0.f;
     int k = 0;
     for (; k + kBatch <= n_dtiles; k += kBatch) {
@@ -2379,12 +2414,15 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, a);
     if (int rc = launch_check("selective_bwd_kernel")) return rc;
   }
-  const int64_t n_bc_blocks = (n_bln + kFinThreads - 1) / kFinThreads;
+  const int fin_vec = n_bln % kFinVec == 0 && aligned_to(dB, kFinVec * sizeof(E)) &&
+                      aligned_to(dC, kFinVec * sizeof(E));
+  const int64_t per_block = static_cast<int64_t>(kFinThreads) * (fin_vec ? kFinVec : 1);
+  const int64_t n_bc_blocks = (n_bln + per_block - 1) / per_block;
   const int64_t n_dA_blocks = (n_dn + kFinCols - 1) / kFinCols;
   hipLaunchKernelGGL(selective_finish_kernel<E>, dim3(static_cast<unsigned>(n_bc_blocks + n_dA_blocks)),
                      dim3(kFinThreads), 0, stream, part_dB, part_dC, part_dA, dB, dC, dA, n_bln,
                      static_cast<int>(n_dtiles), n_dn, static_cast<int>(dA_rows),
-                     static_cast<int>(n_bc_blocks));
+                     static_cast<int>(n_bc_blocks), fin_vec);
   if (int rc = launch_check("selective_finish_kernel")) return rc;
   if (gate == nullptr && dgate != nullptr) return zero_fill(dgate, n_rows, stream);
   return OSSM_OK;
