@@ -284,8 +284,10 @@ __device__ __forceinline__ void bwd_load(BwdBuf<Model, T>& b, const BwdTicket& k
 // final pass reads it (bwd_back): with H = 1 the front stages all of them;
 // with H = 2 it only runs to the middle of the sub-chunk (s_mid) and the
 // back recomputes each half in turn, halving the LDS footprint for one extra
-// half sweep.  All waves call it together.
-template <class Model, int T, int W, int S, int H>
+// half sweep.  SS = 2 (H = 1 only) stages every other state, s_{t-1} of the
+// even steps; the back rebuilds an odd step's from the even one before it with
+// one forward step, for half the LDS.  All waves call it together.
+template <class Model, int T, int W, int S, int H, int SS>
 __device__ __forceinline__ float4 bwd_front(
     BwdBuf<Model, T>& b, const BwdTicket& k, int L, int nc, int n_chunks,
     unsigned long long* __restrict__ rec, const LaunchSync& sync, float4 (*s_agg)[kWave],
@@ -307,7 +309,7 @@ __device__ __forceinline__ float4 bwd_front(
       if constexpr (H == 1) {
 #pragma unroll
         for (int i = 0; i < T; ++i) {
-          s_sp[w][i][lane] = s;
+          if (i % SS == 0) s_sp[w][i / SS][lane] = s;
           if (live(i)) s = Model::step(cf, s, b.x[i]);
         }
       } else {
@@ -369,7 +371,7 @@ __device__ __forceinline__ float4 bwd_front(
 // sums) from carry y, then the chunk's per-channel partial sums.  `sp_lds` is
 // the wave's own S = T/H staging slots (see bwd_front); `s_sums` holds each
 // wave's NS sums, which wave 0 adds after a barrier.
-template <class Model, int T, int W, int H>
+template <class Model, int T, int W, int H, int SS>
 __device__ __forceinline__ void bwd_back(BwdBuf<Model, T>& b, const BwdTicket& k, float4 y,
                                          float4 s_mid, float4* sp_lds,
                                          typename Model::GOut* __restrict__ gin,
@@ -403,7 +405,10 @@ __device__ __forceinline__ void bwd_back(BwdBuf<Model, T>& b, const BwdTicket& k
         if (live(i)) {
           const float4 mu = Model::mu(y, b.go[i]);
           stream_store(&group_row(gin, k.t0 + i, nc, k.g)[lane], Model::grad_input(cf, mu));
-          if constexpr (Model::kRecompute)
+          if constexpr (Model::kRecompute && SS == 2) {
+            const float4 se = sp_lds[(i / 2) * kWave + lane];  // s_{t-1} of the even step
+            Model::accumulate(acc, mu, (i & 1) ? Model::step(cf, se, b.x[i - 1]) : se, b.x[i]);
+          } else if constexpr (Model::kRecompute)
             Model::accumulate(acc, mu, sp_lds[(H > 1 ? q : i) * kWave + lane], b.x[i]);
           else
             Model::accumulate(acc, mu, b.sp[i], b.x[0]);
@@ -436,7 +441,7 @@ __device__ __forceinline__ void bwd_back(BwdBuf<Model, T>& b, const BwdTicket& k
 
 // One workgroup per (chunk, channel group), chunks handed out last-first in
 // launch-ticket order (so every chunk a look-back waits on is resident).
-template <class Model, int T, int W, int OCC, int H>
+template <class Model, int T, int W, int OCC, int H, int SS>
 __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
     typename Model::Params prm, const typename Model::In* __restrict__ in,
     const float4* states, const typename Model::GIn* __restrict__ gout,
@@ -446,7 +451,8 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
   __shared__ float4 s_agg[W][kWave];
   __shared__ float4 s_carry[kWave];
   // per wave: its T / H staged states s_{t-1}, later its NS partial sums
-  constexpr int kStage = Model::kRecompute ? T / H : 0;
+  static_assert(SS == 1 || (SS == 2 && H == 1 && T % 2 == 0), "every other state: one segment");
+  constexpr int kStage = Model::kRecompute ? T / H / SS : 0;
   constexpr int kSlots = kStage > (NS + 3) / 4 ? kStage : (NS + 3) / 4;
   __shared__ float4 s_sp[W][kSlots][kWave];
   __shared__ int s_ticket;
@@ -458,11 +464,11 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
   bwd_load<Model, T, W>(b, k, prm, in, states, gout, L, nc);
   typename Model::Mat KT;
   float4 s_mid = f4zero();
-  const float4 y = bwd_front<Model, T, W, kSlots, H>(b, k, L, nc, n_chunks, rec, sync, s_agg,
-                                                     s_carry, s_sp, KT, s_mid);
+  const float4 y = bwd_front<Model, T, W, kSlots, H, SS>(b, k, L, nc, n_chunks, rec, sync, s_agg,
+                                                         s_carry, s_sp, KT, s_mid);
   // the per-wave sums go into the wave's own s_{t-1} region, which only the
   // wave itself reads before this point
-  bwd_back<Model, T, W, H>(b, k, y, s_mid, &s_sp[wave_id()][0][0], gin, red, L, nc,
+  bwd_back<Model, T, W, H, SS>(b, k, y, s_mid, &s_sp[wave_id()][0][0], gin, red, L, nc,
                            reinterpret_cast<float*>(&s_sp[0][0][0]), kSlots * kWave * 4);
 }
 
@@ -483,27 +489,30 @@ struct OscEpilogue {
 
 // T steps per lane, W waves per workgroup, OCC = minimum waves per SIMD the
 // register allocation must allow (__launch_bounds__' second argument).
-// H (backward only) = staging segments of the recomputed states.
+// H (backward only) = staging segments of the recomputed states, S (backward
+// only) = 1, or 2 to stage every other state.
 struct Tile {
-  int T, W, O, H;
+  int T, W, O, H, S;
 };
 
-// "TxWxO" or "TxWxOxH" (H defaults to 1).
+// "TxWxO", "TxWxOxH" or "TxWxOxHxS" (H and S default to 1).
 Tile parse_tile(const char* env, Tile dflt) {
   const char* s = std::getenv(env);
   if (!s) return dflt;
-  int t = 0, w = 0, o = 0, h = 1;
-  const int n = std::sscanf(s, "%dx%dx%dx%d", &t, &w, &o, &h);
+  int t = 0, w = 0, o = 0, h = 1, st = 1;
+  const int n = std::sscanf(s, "%dx%dx%dx%dx%d", &t, &w, &o, &h, &st);
   if (n < 3) return dflt;
-  return {t, w, o, h};
+  return {t, w, o, h, st};
 }
 
 // Instantiated tiles (T, W, OCC).
 #define OSSM_FWD_TILES(X) X(16, 8, 1) X(16, 8, 4) X(8, 8, 4) X(16, 4, 4) X(8, 16, 4) X(32, 4, 2)
-// Backward tiles (T, W, OCC, H): H = staging segments of the recomputed states.
+// Backward tiles (T, W, OCC, H, S): H = staging segments of the recomputed
+// states, S = 2 stages every other one.
 #define OSSM_BWD_TILES(X)                                                                     \
-  X(16, 8, 1, 1) X(16, 8, 4, 2) X(16, 8, 2, 2) X(16, 4, 1, 1) X(8, 8, 1, 1) X(8, 8, 4, 2)      \
-  X(32, 4, 1, 1) X(32, 4, 2, 2) X(8, 16, 1, 1)
+  X(16, 8, 1, 1, 1) X(16, 8, 4, 2, 1) X(16, 8, 2, 2, 1) X(16, 4, 1, 1, 1) X(8, 8, 1, 1, 1)    \
+  X(8, 8, 4, 2, 1) X(32, 4, 1, 1, 1) X(32, 4, 2, 2, 1) X(8, 16, 1, 1, 1) X(16, 8, 4, 1, 2)   \
+  X(16, 8, 1, 1, 2)
 
 // Launch geometry of a forward scan: the tile, the chunk grid and the bytes
 // of look-back records it needs (two 4-word records per chunk and channel).
@@ -514,7 +523,7 @@ struct FwdPlan {
 };
 
 FwdPlan fwd_plan(int64_t L, int64_t nc) {
-  static const Tile tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{16, 8, 1, 1});
+  static const Tile tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{16, 8, 1, 1, 1});
   FwdPlan pl;
   pl.tile = tile;
   const int64_t CL = int64_t(tile.T) * tile.W;
@@ -577,7 +586,7 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
                     int64_t B, int64_t P, hipStream_t stream) {
   StreamCall call(stream);
   if (call.status()) return call.status();
-  static const Tile tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{16, 8, 1, 1});
+  static const Tile tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{16, 8, 1, 1, 2});
   constexpr int NS = Model::kSums;
   const int64_t nc = B * P;
   const int64_t CL = int64_t(tile.T) * tile.W;
@@ -597,9 +606,10 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
   const ZeroFill zero{{out0, out1, out2}, static_cast<int>(Model::kOutsPerColumn * P)};
   bool launched = false;
-#define OSSM_LAUNCH_BWD(TT, WW, OO, HH)                                                          \
-  if (!launched && tile.T == TT && tile.W == WW && tile.O == OO && tile.H == HH) {               \
-    hipLaunchKernelGGL((osc_backward_kernel<Model, TT, WW, OO, HH>),                             \
+#define OSSM_LAUNCH_BWD(TT, WW, OO, HH, SS)                                                      \
+  if (!launched && tile.T == TT && tile.W == WW && tile.O == OO && tile.H == HH &&               \
+      tile.S == SS) {                                                                            \
+    hipLaunchKernelGGL((osc_backward_kernel<Model, TT, WW, OO, HH, SS>),                         \
                        dim3(static_cast<unsigned>(total)),                                       \
                        dim3(WW * kWave), 0, stream,                                              \
                        prm, static_cast<const typename Model::In*>(in),                          \
