@@ -190,16 +190,22 @@ __device__ __forceinline__ void unpack(float2 v, float (&o)[2]) {
 // ---- element types -----------------------------------------------------------
 // The row tensors (u, dt, z, out, grads) and B/C are fp32 or bf16 in HBM; the
 // recurrence, its state and every sum run in fp32.  bf16 is stored as its
-// 16 bits; conversions are exact widening and round-to-nearest-even narrowing.
+// 16 bits; conversions are exact widening and round-to-nearest-even narrowing
+// (gfx950's v_cvt_pk_bf16_f32, two values per instruction, NaN kept quiet).
 using bf16_t = uint16_t;
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float bf16_to_f32(bf16_t v) {
   return __uint_as_float(static_cast<uint32_t>(v) << 16);
 }
+// lo in bits 0..15, hi in bits 16..31
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+  const f32x2_v f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_v));
+}
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x40u);  // NaN
-  return static_cast<bf16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  return static_cast<bf16_t>(f32x2_to_bf16x2(f, 0.f));
 }
 
 template <class E>
@@ -227,8 +233,8 @@ struct Elem<bf16_t> {
   static __device__ __forceinline__ float load1(const bf16_t* p) { return bf16_to_f32(*p); }
   static __device__ __forceinline__ void store4(bf16_t* p, float4 v) {
     uint2 w;
-    w.x = static_cast<uint32_t>(f32_to_bf16(v.x)) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16);
-    w.y = static_cast<uint32_t>(f32_to_bf16(v.z)) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16);
+    w.x = f32x2_to_bf16x2(v.x, v.y);
+    w.y = f32x2_to_bf16x2(v.z, v.w);
     *reinterpret_cast<uint2*>(p) = w;
   }
   static __device__ __forceinline__ void store1(bf16_t* p, float v) { *p = f32_to_bf16(v); }
