@@ -15,16 +15,19 @@
 //   1. The chunk's u rows (contiguous in HBM) are staged in LDS.
 //   2. In-projection on the matrix cores, v_mfma_f32_32x32x2f32 (fp32 products
 //      and sums, no reduced precision): the 32 x 2P result (re and im planes)
-//      stays in LDS.  Wave w owns oscillator groups w, w+4, ... of 32; its
-//      lanes read the weights straight from HBM/L2 (every workgroup reads
-//      the same B, so it stays in L2).
+//      waits in the accumulators until every wave has read u, then replaces
+//      u in LDS (one buffer: four workgroups share a CU at H, P <= 128).
+//      Wave w owns oscillator groups w, w+4, ... of 32; its lanes read the
+//      weights straight from HBM/L2 (every workgroup reads the same B, so it
+//      stays in L2).
 //   3. One lane per oscillator scans the 32 steps from a zero state; the
 //      chunk aggregate goes through the decoupled look-back of the oscillatory
 //      scans (tagged records, launch tickets, chunk transition M^32 formed in
 //      fp64) for the carry; the lane re-runs the chunk from the carry and
 //      overwrites the projection with x (imaginary part negated).
 //   4. Out-projection on the matrix cores (K = the oscillators, the two
-//      components as the MFMA's two k slots), plus D u, stored as y rows.
+//      components as the MFMA's two k slots), plus D u (u read again, from
+//      L2), stored as y rows.
 //
 // MFMA operand layout (v_mfma_f32_32x32x2f32, 64 lanes): lane l supplies
 // A[m = l % 32][k = l / 32] and B[k = l / 32][n = l % 32]; accumulator register
@@ -34,8 +37,8 @@
 // lane half j the h range [j H'/2, (j+1) H'/2) and reads both operands as
 // 16-byte runs along h.
 //
-// Limits: hidden and ssm sizes up to 256 (LDS of one workgroup: 32 rows of u
-// and 2 x 32 rows of the projection, padded to multiples of 32).
+// Limits: hidden and ssm sizes up to 256 (LDS of one workgroup: 32 rows of u,
+// or of the projection's 2 x 32, padded to multiples of 32).
 
 #include <hip/hip_runtime.h>
 
@@ -94,58 +97,57 @@ __device__ __forceinline__ int acc_row(int r, int lane) {
   return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
 }
 
-// Weight loads are branch-free: an element outside the tensor reads a
-// clamped in-range address and is then zeroed, so the loads of the
-// projection loops stay unconditional and in flight together.
-__device__ __forceinline__ float4 keep4(bool ok, float4 v) {
-  return ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
-}
-__device__ __forceinline__ float2 keep2(bool ok, float2 v) { return ok ? v : make_float2(0.f, 0.f); }
+// Weight loads are branch-free and unmasked: an element outside the tensor
+// reads a clamped in-range address, so the loads of the projection loops stay
+// unconditional and in flight together.  The matching mask_* zeroes those
+// elements where a loop consumes them, a prefetch distance after the load
+// (a select at load time needs the data, so each iteration would wait for its
+// own loads).
+__device__ __forceinline__ float zero_unless(bool ok, float v) { return ok ? v : 0.f; }
 
 // In-projection weights of oscillator p for h = h0 .. h0 + 3, as
-// (re h0, im h0, re h0+1, im h0+1) and (re h0+2, ..): B[p, h, 0..1].  Zero
-// outside the tensor.  VEC: H % 4 == 0 and B 16-byte aligned.
+// (re h0, im h0, re h0+1, im h0+1) and (re h0+2, ..): B[p, h, 0..1].
+// VEC: H % 4 == 0 and B 16-byte aligned.
 template <bool VEC>
-__device__ __forceinline__ void load_bw(const LayerArgs& A, int p, int h0, float4 (&w)[2]) {
+__device__ __forceinline__ void load_bw(const float* __restrict__ Bw, int H, int P, int p, int h0,
+                                        float4 (&w)[2]) {
+  const float* row = Bw + static_cast<size_t>(min(p, P - 1)) * H * 2;
   if (VEC) {
-    const bool ok = p < A.P && h0 < A.H;
-    const float4* src = reinterpret_cast<const float4*>(
-        A.Bw + (static_cast<size_t>(min(p, A.P - 1)) * A.H + min(h0, A.H - 4)) * 2);
-    w[0] = keep4(ok, src[0]);
-    w[1] = keep4(ok, src[1]);
+    const float4* src = reinterpret_cast<const float4*>(row + min(h0, H - 4) * 2);
+    w[0] = src[0];
+    w[1] = src[1];
   } else {
     float v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int h = h0 + (j >> 1);
-      const bool ok = p < A.P && h < A.H;
-      const float x = A.Bw[(static_cast<size_t>(min(p, A.P - 1)) * A.H + min(h, A.H - 1)) * 2 + (j & 1)];
-      v[j] = ok ? x : 0.f;
-    }
+    for (int j = 0; j < 8; ++j) v[j] = row[min(h0 + (j >> 1), H - 1) * 2 + (j & 1)];
     w[0] = make_float4(v[0], v[1], v[2], v[3]);
     w[1] = make_float4(v[4], v[5], v[6], v[7]);
   }
 }
+__device__ __forceinline__ void mask_bw(int H, int P, int p, int h0, float4 (&w)[2]) {
+  const bool k0 = p < P && h0 < H, k1 = p < P && h0 + 1 < H;
+  const bool k2 = p < P && h0 + 2 < H, k3 = p < P && h0 + 3 < H;
+  w[0] = make_float4(zero_unless(k0, w[0].x), zero_unless(k0, w[0].y), zero_unless(k1, w[0].z),
+                     zero_unless(k1, w[0].w));
+  w[1] = make_float4(zero_unless(k2, w[1].x), zero_unless(k2, w[1].y), zero_unless(k3, w[1].z),
+                     zero_unless(k3, w[1].w));
+}
 
 // Out-projection weights of output column h for oscillators p0, p0 + 1:
-// (re p0, im p0, re p0+1, im p0+1) = C[h, p0 .. p0+1, 0..1], zero outside.
+// (re p0, im p0, re p0+1, im p0+1) = C[h, p0 .. p0+1, 0..1].
 // VEC: P % 4 == 0 (p0 even) and C 16-byte aligned.
 template <bool VEC>
-__device__ __forceinline__ float4 load_cw(const LayerArgs& A, int h, int p0) {
-  if (VEC) {
-    const bool ok = h < A.H && p0 < A.P;
-    return keep4(ok, *reinterpret_cast<const float4*>(
-                         A.Cw + (static_cast<size_t>(min(h, A.H - 1)) * A.P + min(p0, A.P - 2)) * 2));
-  }
+__device__ __forceinline__ float4 load_cw(const float* __restrict__ Cw, int H, int P, int h, int p0) {
+  const float* row = Cw + static_cast<size_t>(min(h, H - 1)) * P * 2;
+  if (VEC) return *reinterpret_cast<const float4*>(row + min(p0, P - 2) * 2);
   float v[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int pj = p0 + (j >> 1);
-    const bool ok = h < A.H && pj < A.P;
-    const float x = A.Cw[(static_cast<size_t>(min(h, A.H - 1)) * A.P + min(pj, A.P - 1)) * 2 + (j & 1)];
-    v[j] = ok ? x : 0.f;
-  }
+  for (int j = 0; j < 4; ++j) v[j] = row[min(p0 + (j >> 1), P - 1) * 2 + (j & 1)];
   return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float4 mask_cw(int H, int P, int h, int p0, float4 w) {
+  const bool k0 = h < H && p0 < P, k1 = h < H && p0 + 1 < P;
+  return make_float4(zero_unless(k0, w.x), zero_unless(k0, w.y), zero_unless(k1, w.z), zero_unless(k1, w.w));
 }
 
 // Rows t0 .. t0 + nt - 1 of a [B, L, H] tensor to LDS [kLc][HS], zero-padded,
@@ -155,16 +157,19 @@ __device__ __forceinline__ float4 load_cw(const LayerArgs& A, int h, int p0) {
 // groups over the workgroup), all loaded before any is waited on.  Rows past
 // nt and columns past H read a clamped in-range address and are zeroed when
 // written to LDS.
+// SK: float4 groups per thread held (Hp / 32 at most; kLayerMax / 32 covers
+// every supported size).
+template <int SK = kLayerMax / 32>
 struct RowStage {
-  float4 v[kLayerMax / 32];
+  float4 v[SK];
 };
 
-template <bool VEC>
-__device__ __forceinline__ void stage_load(RowStage& r, const float* __restrict__ src, size_t row0,
+template <bool VEC, int SK>
+__device__ __forceinline__ void stage_load(RowStage<SK>& r, const float* __restrict__ src, size_t row0,
                                            int nt, int H, int Hp) {
   const int q4 = Hp / 4, n = Hp / 32;
 #pragma unroll
-  for (int k = 0; k < kLayerMax / 32; ++k) {
+  for (int k = 0; k < SK; ++k) {
     if (k >= n) break;  // uniform
     const int e = threadIdx.x + k * kLayerThreads;
     const int t = min(e / q4, nt - 1), h = (e - (e / q4) * q4) * 4;
@@ -178,11 +183,12 @@ __device__ __forceinline__ void stage_load(RowStage& r, const float* __restrict_
   }
 }
 
-__device__ __forceinline__ void stage_store(const RowStage& r, float* __restrict__ dst, int nt, int H,
+template <int SK>
+__device__ __forceinline__ void stage_store(const RowStage<SK>& r, float* __restrict__ dst, int nt, int H,
                                             int Hp, int HS) {
   const int q4 = Hp / 4, n = Hp / 32;
 #pragma unroll
-  for (int k = 0; k < kLayerMax / 32; ++k) {
+  for (int k = 0; k < SK; ++k) {
     if (k >= n) break;  // uniform
     const int e = threadIdx.x + k * kLayerThreads;
     const int t = e / q4, h = (e - t * q4) * 4;
@@ -194,18 +200,24 @@ __device__ __forceinline__ void stage_store(const RowStage& r, float* __restrict
   }
 }
 
-template <int V, bool VEC>
-__global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_fwd_kernel(
+// SMALL: Hp, Pp <= 128 (one oscillator group per wave, four row groups per
+// thread): the registers are sized for that, so that four workgroups share a CU.
+template <int V, bool VEC, bool SMALL>
+__global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(SMALL ? 4 : 1)))
+void dlinoss_layer_fwd_kernel(
     LayerArgs A, unsigned long long* __restrict__ rec, LaunchSync sync) {
   using Model = Dlinoss<V>;
+  constexpr int NG = SMALL ? 1 : kBwdGroups;           // oscillator groups per wave
+  constexpr int SK = SMALL ? 128 / 32 : kLayerMax / 32;  // staged float4 per thread
+  constexpr int AH = SMALL ? 2 : kAhead;                  // weight groups loaded ahead
   extern __shared__ __align__(16) float smem[];
   __shared__ int s_ticket;
 
   const int Hp = round32(A.H), Pp = round32(A.P);
   const int HS = Hp + 4, XS = 2 * Pp + 4;  // row strides (floats): 16-byte rows, banks staggered
-  float* sU = smem;                        // [kLc][HS]     u rows of the chunk
-  float* sX = smem + kLc * HS;             // [kLc][Pp][2]  bu (re, im), then (x.re, -x.im)
-  float4* s_agg = reinterpret_cast<float4*>(sX + kLc * XS);  // [P] chunk aggregates
+  float* sU = smem;  // [kLc][HS]     u rows of the chunk, until the in-projection has read them
+  float* sX = smem;  // [kLc][Pp][2]  then bu (re, im), then (x.re, -x.im)
+  float4* s_agg = reinterpret_cast<float4*>(smem + kLc * max(HS, XS));  // [P] chunk aggregates
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = wave_id();
@@ -219,48 +231,68 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_fwd_kernel(
 
   // 1. u rows t0 .. t0 + nt - 1 (contiguous) -> LDS, zero-padded to 32 x Hp
   {
-    RowStage st;
+    RowStage<SK> st;
     stage_load<VEC>(st, A.u, row0, nt, A.H, Hp);
     stage_store(st, sU, nt, A.H, Hp, HS);
   }
   __syncthreads();
 
   // 2. in-projection: for oscillator group pg (32 oscillators) the wave forms
-  //    the re and im 32 x 32 tiles, K = Hp split over the two lane halves.
+  //    the re and im 32 x 32 tiles, K = Hp split over the two lane halves;
+  //    held in the accumulators until every wave has read u, then written
+  //    to sX over it
   {
     const int half = lane >> 5, m = lane & 31;
     const int hh = Hp / 2;        // h per lane half (a multiple of 16)
     const int ng = hh / 4;        // groups of 4 k-steps (a multiple of 4)
     const float* arow = sU + m * HS + half * hh;
-    for (int pg = w; pg < Pp / 32; pg += kLayerWaves) {
+    floatx16 acc_re[NG], acc_im[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int pg = w + i * kLayerWaves;
+      if (pg >= Pp / 32) break;  // uniform
       const int p = pg * 32 + m;
-      floatx16 acc_re, acc_im;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc_re[r] = acc_im[r] = 0.f;
-      float4 wb[kAhead][2];
+      for (int r = 0; r < 16; ++r) acc_re[i][r] = acc_im[i][r] = 0.f;
+      float4 wb[AH][2];
 #pragma unroll
-      for (int j = 0; j < kAhead; ++j) load_bw<VEC>(A, p, half * hh + 4 * j, wb[j]);
-      for (int q0 = 0; q0 < ng; q0 += kAhead) {
+      for (int j = 0; j < AH; ++j) load_bw<VEC>(A.Bw, A.H, A.P, p, half * hh + 4 * j, wb[j]);
+      // A operand one group ahead: its LDS read overlaps this group's MFMAs
+      float4 an = *reinterpret_cast<const float4*>(arow);
+      for (int q0 = 0; q0 < ng; q0 += AH) {
 #pragma unroll
-        for (int j = 0; j < kAhead; ++j) {
+        for (int j = 0; j < AH; ++j) {
           const int q = q0 + j;
-          const float4 av = *reinterpret_cast<const float4*>(arow + 4 * q);
-          const float4 w0 = wb[j][0], w1 = wb[j][1];
-          load_bw<VEC>(A, p, half * hh + 4 * min(q + kAhead, ng - 1), wb[j]);
-          acc_re = mfma32(av.x, w0.x, acc_re);
-          acc_im = mfma32(av.x, w0.y, acc_im);
-          acc_re = mfma32(av.y, w0.z, acc_re);
-          acc_im = mfma32(av.y, w0.w, acc_im);
-          acc_re = mfma32(av.z, w1.x, acc_re);
-          acc_im = mfma32(av.z, w1.y, acc_im);
-          acc_re = mfma32(av.w, w1.z, acc_re);
-          acc_im = mfma32(av.w, w1.w, acc_im);
+          float4 av = an;
+          an = *reinterpret_cast<const float4*>(arow + 4 * min(q + 1, ng - 1));
+          float4 wq[2] = {wb[j][0], wb[j][1]};
+          mask_bw(A.H, A.P, p, half * hh + 4 * q, wq);
+          const float4 w0 = wq[0], w1 = wq[1];
+          load_bw<VEC>(A.Bw, A.H, A.P, p, half * hh + 4 * min(q + AH, ng - 1), wb[j]);
+          asm volatile("" ::: "memory");  // the prefetch stays here, not next to its use
+          // and the MFMAs below it, after the next group's LDS read
+          asm volatile("" : "+v"(av.x), "+v"(av.y), "+v"(av.z), "+v"(av.w));
+          acc_re[i] = mfma32(av.x, w0.x, acc_re[i]);
+          acc_im[i] = mfma32(av.x, w0.y, acc_im[i]);
+          acc_re[i] = mfma32(av.y, w0.z, acc_re[i]);
+          acc_im[i] = mfma32(av.y, w0.w, acc_im[i]);
+          acc_re[i] = mfma32(av.z, w1.x, acc_re[i]);
+          acc_im[i] = mfma32(av.z, w1.y, acc_im[i]);
+          acc_re[i] = mfma32(av.w, w1.z, acc_re[i]);
+          acc_im[i] = mfma32(av.w, w1.w, acc_im[i]);
         }
       }
+    }
+    __syncthreads();  // u is read: sX may overwrite it
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int pg = w + i * kLayerWaves;
+      if (pg >= Pp / 32) break;  // uniform
+      const int p = pg * 32 + m;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int t = acc_row(r, lane);
-        *reinterpret_cast<float2*>(sX + t * XS + 2 * (pg * 32 + m)) = make_float2(acc_re[r], acc_im[r]);
+        *reinterpret_cast<float2*>(sX + t * XS + 2 * p) = make_float2(acc_re[i][r], acc_im[i][r]);
       }
     }
   }
@@ -331,16 +363,28 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_fwd_kernel(
       floatx16 acc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-      float4 cb[kAhead];
+      // u for the D skip (LDS holds x now), loaded before the MFMA loop
+      // (clamped in range; the chunk's rows were just read, so L2 serves them)
+      float uv[16];
 #pragma unroll
-      for (int j = 0; j < kAhead; ++j) cb[j] = load_cw<VEC>(A, h, 4 * j + 2 * kk);
-      for (int q0 = 0; q0 < ng; q0 += kAhead) {
+      for (int r = 0; r < 16; ++r)
+        uv[r] = A.u[row0 + static_cast<size_t>(min(acc_row(r, lane), nt - 1)) * A.H + min(h, A.H - 1)];
+      float4 cb[AH];
 #pragma unroll
-        for (int j = 0; j < kAhead; ++j) {
+      for (int j = 0; j < AH; ++j) cb[j] = load_cw<VEC>(A.Cw, A.H, A.P, h, 4 * j + 2 * kk);
+      // A operand one group ahead: its LDS read overlaps this group's MFMAs
+      float4 an = *reinterpret_cast<const float4*>(arow);
+      for (int q0 = 0; q0 < ng; q0 += AH) {
+#pragma unroll
+        for (int j = 0; j < AH; ++j) {
           const int q = q0 + j;
-          const float4 av = *reinterpret_cast<const float4*>(arow + 8 * q);
-          const float4 cv = cb[j];
-          cb[j] = load_cw<VEC>(A, h, 4 * min(q + kAhead, ng - 1) + 2 * kk);
+          float4 av = an;
+          an = *reinterpret_cast<const float4*>(arow + 8 * min(q + 1, ng - 1));
+          const float4 cv = mask_cw(A.H, A.P, h, 4 * q + 2 * kk, cb[j]);
+          cb[j] = load_cw<VEC>(A.Cw, A.H, A.P, h, 4 * min(q + AH, ng - 1) + 2 * kk);
+          asm volatile("" ::: "memory");  // the prefetch stays here, not next to its use
+          // and the MFMAs below it, after the next group's LDS read
+          asm volatile("" : "+v"(av.x), "+v"(av.y), "+v"(av.z), "+v"(av.w));
           acc = mfma32(av.x, cv.x, acc);
           acc = mfma32(av.y, cv.y, acc);
           acc = mfma32(av.z, cv.z, acc);
@@ -352,7 +396,7 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_fwd_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int t = acc_row(r, lane);
-          if (t < nt) A.y[row0 + static_cast<size_t>(t) * A.H + h] = acc[r] + sU[t * HS + h] * dh;
+          if (t < nt) A.y[row0 + static_cast<size_t>(t) * A.H + h] = acc[r] + uv[r] * dh;
         }
       }
     }
@@ -397,52 +441,47 @@ struct LayerBwdArgs {
   int Bsz, L, H, P, n_chunks;
 };
 
-// Weights of the g_x projection for output h and oscillator p: (C_re, C_im)[h, p].
+// Weights of the g_x projection for oscillator p and h = h0 .. h0 + 3:
+// (re h0, im h0, re h0+1, im h0+1), (.. h0+2, h0+3) of (C_re, C_im)[h, p].
 template <bool VEC>
-__device__ __forceinline__ void load_cw_pair(const LayerBwdArgs& A, int h0, int p, float4 (&w)[2]) {
-  // h = h0 .. h0 + 3 for one oscillator: (re h0, im h0, re h0+1, im h0+1), (.. h0+2, h0+3)
+__device__ __forceinline__ void load_cw_pair(const float* __restrict__ Cw, int H, int P, int h0, int p,
+                                             float4 (&w)[2]) {
   float v[8];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int h = h0 + j;
-    const bool ok = p < A.P && h < A.H;
-    const size_t i = (static_cast<size_t>(min(h, A.H - 1)) * A.P + min(p, A.P - 1)) * 2;
+    const float* q = Cw + (static_cast<size_t>(min(h0 + j, H - 1)) * P + min(p, P - 1)) * 2;
     if (VEC) {
-      const float2 c = keep2(ok, *reinterpret_cast<const float2*>(A.Cw + i));
+      const float2 c = *reinterpret_cast<const float2*>(q);
       v[2 * j] = c.x;
       v[2 * j + 1] = c.y;
     } else {
-      const float re = A.Cw[i], im = A.Cw[i + 1];
-      v[2 * j] = ok ? re : 0.f;
-      v[2 * j + 1] = ok ? im : 0.f;
+      v[2 * j] = q[0];
+      v[2 * j + 1] = q[1];
     }
   }
   w[0] = make_float4(v[0], v[1], v[2], v[3]);
   w[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
-
-template <bool VEC>
-__device__ __forceinline__ void load_bw_b(const LayerBwdArgs& A, int p, int h0, float4 (&w)[2]) {
-  LayerArgs la{};
-  la.Bw = A.Bw;
-  la.H = A.H;
-  la.P = A.P;
-  load_bw<VEC>(la, p, h0, w);
+// zero outside the tensor: the same pattern as mask_bw with the roles of h and p
+__device__ __forceinline__ void mask_cw_pair(int H, int P, int h0, int p, float4 (&w)[2]) {
+  mask_bw(H, P, p, h0, w);
 }
 
-// (B_re, B_im)[p0, h], (B_re, B_im)[p0 + 1, h], zero outside.
-__device__ __forceinline__ float4 load_bw_pair(const LayerBwdArgs& A, int h, int p0) {
+// (B_re, B_im)[p0, h], (B_re, B_im)[p0 + 1, h].
+__device__ __forceinline__ float4 load_bw_pair(const float* __restrict__ Bw, int H, int P, int h, int p0) {
   float v[4];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int pj = p0 + j;
-    const bool ok = pj < A.P && h < A.H;
-    const float2 b = keep2(ok, *reinterpret_cast<const float2*>(
-                                   A.Bw + (static_cast<size_t>(min(pj, A.P - 1)) * A.H + min(h, A.H - 1)) * 2));
+    const float2 b = *reinterpret_cast<const float2*>(
+        Bw + (static_cast<size_t>(min(p0 + j, P - 1)) * H + min(h, H - 1)) * 2);
     v[2 * j] = b.x;
     v[2 * j + 1] = b.y;
   }
   return make_float4(v[0], v[1], v[2], v[3]);
+}
+// zero outside the tensor: mask_cw's pattern (column h, oscillators p0, p0 + 1)
+__device__ __forceinline__ float4 mask_bw_pair(int H, int P, int h, int p0, float4 w) {
+  return mask_cw(H, P, h, p0, w);
 }
 
 template <int V, bool VEC>
@@ -478,7 +517,7 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
   // Every HBM read the chunk needs before its last phase goes out now: the
   // gy and u rows (to LDS at phases 1 and 2) and the carry entering the
   // chunk (phase 3).
-  RowStage st_gy, st_u;
+  RowStage<> st_gy, st_u;
   stage_load<VEC>(st_gy, A.gy, row0, nt, A.H, Hp);
   stage_load<VEC>(st_u, A.u, row0, nt, A.H, Hp);
   const int p = threadIdx.x;
@@ -497,14 +536,22 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
       for (int r = 0; r < 16; ++r) acc_re[r] = acc_im[r] = 0.f;
       float4 wb[kAhead][2];
 #pragma unroll
-      for (int j = 0; j < kAhead; ++j) load_cw_pair<VEC>(A, half * hh + 4 * j, p, wb[j]);
+      for (int j = 0; j < kAhead; ++j) load_cw_pair<VEC>(A.Cw, A.H, A.P, half * hh + 4 * j, p, wb[j]);
+      // A operand one group ahead: its LDS read overlaps this group's MFMAs
+      float4 an = *reinterpret_cast<const float4*>(arow);
       for (int q0 = 0; q0 < ng1; q0 += kAhead) {
 #pragma unroll
         for (int j = 0; j < kAhead; ++j) {
           const int q = q0 + j;
-          const float4 av = *reinterpret_cast<const float4*>(arow + 4 * q);
-          const float4 w0 = wb[j][0], w1 = wb[j][1];
-          load_cw_pair<VEC>(A, half * hh + 4 * min(q + kAhead, ng1 - 1), p, wb[j]);
+          float4 av = an;
+          an = *reinterpret_cast<const float4*>(arow + 4 * min(q + 1, ng1 - 1));
+          float4 wq[2] = {wb[j][0], wb[j][1]};
+          mask_cw_pair(A.H, A.P, half * hh + 4 * q, p, wq);
+          const float4 w0 = wq[0], w1 = wq[1];
+          load_cw_pair<VEC>(A.Cw, A.H, A.P, half * hh + 4 * min(q + kAhead, ng1 - 1), p, wb[j]);
+          asm volatile("" ::: "memory");  // the prefetch stays here, not next to its use
+          // and the MFMAs below it, after the next group's LDS read
+          asm volatile("" : "+v"(av.x), "+v"(av.y), "+v"(av.z), "+v"(av.w));
           acc_re = mfma32(av.x, w0.x, acc_re);
           acc_im = mfma32(av.x, w0.y, acc_im);
           acc_re = mfma32(av.y, w0.z, acc_re);
@@ -540,14 +587,22 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
       for (int r = 0; r < 16; ++r) acc_re[i][r] = acc_im[i][r] = 0.f;
       float4 wb[kAhead][2];
 #pragma unroll
-      for (int j = 0; j < kAhead; ++j) load_bw_b<VEC>(A, p, half * hh + 4 * j, wb[j]);
+      for (int j = 0; j < kAhead; ++j) load_bw<VEC>(A.Bw, A.H, A.P, p, half * hh + 4 * j, wb[j]);
+      // A operand one group ahead: its LDS read overlaps this group's MFMAs
+      float4 an = *reinterpret_cast<const float4*>(arow);
       for (int q0 = 0; q0 < ng1; q0 += kAhead) {
 #pragma unroll
         for (int j = 0; j < kAhead; ++j) {
           const int q = q0 + j;
-          const float4 av = *reinterpret_cast<const float4*>(arow + 4 * q);
-          const float4 w0 = wb[j][0], w1 = wb[j][1];
-          load_bw_b<VEC>(A, p, half * hh + 4 * min(q + kAhead, ng1 - 1), wb[j]);
+          float4 av = an;
+          an = *reinterpret_cast<const float4*>(arow + 4 * min(q + 1, ng1 - 1));
+          float4 wq[2] = {wb[j][0], wb[j][1]};
+          mask_bw(A.H, A.P, p, half * hh + 4 * q, wq);
+          const float4 w0 = wq[0], w1 = wq[1];
+          load_bw<VEC>(A.Bw, A.H, A.P, p, half * hh + 4 * min(q + kAhead, ng1 - 1), wb[j]);
+          asm volatile("" ::: "memory");  // the prefetch stays here, not next to its use
+          // and the MFMAs below it, after the next group's LDS read
+          asm volatile("" : "+v"(av.x), "+v"(av.y), "+v"(av.z), "+v"(av.w));
           acc_re[i] = mfma32(av.x, w0.x, acc_re[i]);
           acc_im[i] = mfma32(av.x, w0.y, acc_im[i]);
           acc_re[i] = mfma32(av.y, w0.z, acc_re[i]);
@@ -661,14 +716,20 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
         gyv[r] = A.gy[row0 + static_cast<size_t>(min(acc_row(r, lane), nt - 1)) * A.H + min(h, A.H - 1)];
       float4 cb[kAhead];
 #pragma unroll
-      for (int j = 0; j < kAhead; ++j) cb[j] = load_bw_pair(A, h, 4 * j + 2 * kk);
+      for (int j = 0; j < kAhead; ++j) cb[j] = load_bw_pair(A.Bw, A.H, A.P, h, 4 * j + 2 * kk);
+      // A operand one group ahead: its LDS read overlaps this group's MFMAs
+      float4 an = *reinterpret_cast<const float4*>(arow);
       for (int q0 = 0; q0 < ng; q0 += kAhead) {
 #pragma unroll
         for (int j = 0; j < kAhead; ++j) {
           const int q = q0 + j;
-          const float4 av = *reinterpret_cast<const float4*>(arow + 8 * q);
-          const float4 cv = cb[j];
-          cb[j] = load_bw_pair(A, h, 4 * min(q + kAhead, ng - 1) + 2 * kk);
+          float4 av = an;
+          an = *reinterpret_cast<const float4*>(arow + 8 * min(q + 1, ng - 1));
+          const float4 cv = mask_bw_pair(A.H, A.P, h, 4 * q + 2 * kk, cb[j]);
+          cb[j] = load_bw_pair(A.Bw, A.H, A.P, h, 4 * min(q + kAhead, ng - 1) + 2 * kk);
+          asm volatile("" ::: "memory");  // the prefetch stays here, not next to its use
+          // and the MFMAs below it, after the next group's LDS read
+          asm volatile("" : "+v"(av.x), "+v"(av.y), "+v"(av.z), "+v"(av.w));
           acc = mfma32(av.x, cv.x, acc);
           acc = mfma32(av.y, cv.y, acc);
           acc = mfma32(av.z, cv.z, acc);
@@ -741,7 +802,7 @@ int launch_layer_bwd(LayerBwdArgs args, float* ga, float* gg, float* gs, hipStre
 
 size_t layer_lds_bytes(int64_t H, int64_t P) {
   const int64_t Hp = (H + 31) / 32 * 32, Pp = (P + 31) / 32 * 32;
-  return static_cast<size_t>(kLc * (Hp + 4) + kLc * (2 * Pp + 4) + 4 * P) * sizeof(float);
+  return static_cast<size_t>(kLc * std::max(Hp + 4, 2 * Pp + 4) + 4 * P) * sizeof(float);
 }
 
 
@@ -756,7 +817,9 @@ int launch_layer(const LayerArgs& args, hipStream_t stream) {
   LaunchSync sync{};
   const bool vec = args.H % 4 == 0 && args.P % 4 == 0 && aligned16(args.u) && aligned16(args.Bw) &&
                    aligned16(args.Cw);
-  auto kern = vec ? dlinoss_layer_fwd_kernel<V, true> : dlinoss_layer_fwd_kernel<V, false>;
+  const bool small = args.H <= 128 && args.P <= 128;
+  auto kern = vec ? (small ? dlinoss_layer_fwd_kernel<V, true, true> : dlinoss_layer_fwd_kernel<V, true, false>)
+                  : (small ? dlinoss_layer_fwd_kernel<V, false, true> : dlinoss_layer_fwd_kernel<V, false, false>);
   const size_t lds = layer_lds_bytes(args.H, args.P);
   // before the ticket reservation: a failure here leaves nothing reserved
   if (int rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
