@@ -61,8 +61,11 @@ def _check(layers, variant, args, what):
     no_device_errors()
 
 
+# H, P <= 128 run the four-workgroups-per-CU instantiation, larger ones the other
+# (two oscillator groups per wave when P > 128); H % 4 or P % 4 != 0 take the scalar loads
 SHAPES = [(1, 1, 1, 1), (2, 6, 3, 4), (2, 33, 8, 12), (3, 100, 16, 32), (2, 257, 64, 96),
-          (1, 1030, 128, 128), (2, 64, 130, 33), (3, 40, 256, 256), (5, 97, 32, 64)]
+          (1, 1030, 128, 128), (2, 64, 130, 33), (3, 40, 256, 256), (5, 97, 32, 64),
+          (2, 50, 128, 124), (2, 70, 64, 160), (3, 45, 100, 129)]
 
 
 @pytest.mark.parametrize("variant", VARIANTS)
