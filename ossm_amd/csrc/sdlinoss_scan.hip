@@ -423,6 +423,54 @@ __device__ __forceinline__ float4 sdl_grad_step(float a, float g, float step_raw
   return make_float4(alpha * gtr, alpha * gti, fmaf(-dt2 * a, gtr, lam.z), fmaf(-dt2 * a, gti, lam.w));
 }
 
+// Parameters broadcast over time.  A step's three parameter gradients (as
+// sdl_grad_step forms them) are linear in three contractions of the gradient of
+// the new w, gw = (lam.x + lam.z, lam.y + lam.w), with the state before the
+// step and the input:
+//   px = gw . w_prev,  pz = gw . x_prev,  pb = gw . bu
+// (gw . (-a x_prev + bu) = pb - a pz; gw . tmpw = alpha px + dt^2 (pb - a pz)),
+// with coefficients that depend only on the parameters.  With the parameters
+// constant over time the sums of px, pz, pb over the steps give the summed
+// gradients; this is that map (sdl_grad_step's formulas with the per-step
+// contractions replaced by their sums).
+template <int V>
+__device__ __forceinline__ void sdl_param_grads_of_sums(float a, float g, float step_raw, float inv,
+                                                        float px, float pz, float pb, float& ga,
+                                                        float& gg, float& gs) {
+  const float dt = sdl_dt(step_raw);
+  const float dt2 = dt * dt;
+  const float alpha = sdl_alpha<V>(dt, g);
+  const float pc = fmaf(-a, pz, pb);
+  float gdt = 0.f, gA = 0.f, gG = 0.f;
+  float kin = 1.f;  // gtr = gw * kin
+  if constexpr (V != OSSM_DLINOSS_EX) {
+    const float s_raw = sdl_s_raw<V>(dt, g, a);
+    kin = inv;
+    const float gS = -fmaf(alpha, px, dt2 * pc) * (inv * inv) * (s_raw > kClampMin ? 1.f : 0.f);
+    if constexpr (V == OSSM_DLINOSS_IMEX1) {
+      gdt = gS * g;
+      gG = gS * dt;
+    } else if constexpr (V == OSSM_DLINOSS_IMEX2) {
+      gdt = gS * (2.f * dt * a);
+      gA = gS * dt2;
+    } else {
+      gdt = gS * (g + 2.f * dt * a);
+      gA = gS * dt2;
+      gG = gS * dt;
+    }
+  }
+  if constexpr (V == OSSM_DLINOSS_IMEX2 || V == OSSM_DLINOSS_EX) {
+    gdt += kin * fmaf(-g, px, 2.f * dt * pc);
+    gG += kin * (-dt * px);
+  } else {
+    gdt += kin * (2.f * dt * pc);
+  }
+  gA += kin * (-dt2 * pz);
+  ga = gA;
+  gg = gG;
+  gs = (step_raw > kDtMin && step_raw < kDtMax) ? gdt : 0.f;
+}
+
 // Destinations of the parameter gradients.  Bit p of `tsum` (p = 0 a, 1 g,
 // 2 step) set: the parameter is broadcast over time, so each workgroup writes
 // its chunk's sum over time (row c of a [n_chunks, B*M] partials array);
@@ -537,7 +585,34 @@ __global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
   // final reverse pass: per-step gradients (per element, or summed over the
   // sub-chunk for parameters broadcast over time)
   float psum[3] = {0.f, 0.f, 0.f};
-  if (active) {
+  bool by_sums = false;
+  if constexpr (TB) {
+    // every parameter constant over time and every gradient summed over it:
+    // the step keeps only the adjoint, grad_bu and the three contractions
+    // (sdl_param_grads_of_sums), about a third of sdl_grad_step's work
+    if (go_prm.tsum == 7) {
+      by_sums = true;
+      if (active) {
+        const SdlCoef<V> k = sdl_coef_inv<V>(pa[0], pg[0], ps[0], inv[0]);
+        float px = 0.f, pz = 0.f, pb = 0.f;
+#pragma unroll
+        for (int i = T - 1; i >= 0; --i) {
+          if (live(i)) {
+            const float lzr = rho.z + go[i].x, lzi = rho.w + go[i].y;
+            const float gwr = rho.x + lzr, gwi = rho.y + lzi;
+            const float4 sp = s_sp[w][i][lane];
+            px = fmaf(gwr, sp.x, fmaf(gwi, sp.y, px));
+            pz = fmaf(gwr, sp.z, fmaf(gwi, sp.w, pz));
+            pb = fmaf(gwr, x[i].x, fmaf(gwi, x[i].y, pb));
+            stream_store(&row_of(gin, t0 + i, nc, g)[lane], make_float2(k.c2 * gwr, k.c2 * gwi));
+            rho = make_float4(k.c0 * gwr, k.c0 * gwi, fmaf(k.c1, gwr, lzr), fmaf(k.c1, gwi, lzi));
+          }
+        }
+        sdl_param_grads_of_sums<V>(pa[0], pg[0], ps[0], inv[0], px, pz, pb, psum[0], psum[1], psum[2]);
+      }
+    }
+  }
+  if (!by_sums && active) {
 #pragma unroll
     for (int i = T - 1; i >= 0; --i) {
       if (live(i)) {
