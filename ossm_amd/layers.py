@@ -170,16 +170,23 @@ def dlinoss_layer_backward(variant: str, inputs: Tensor, grad_output: Tensor, B:
     return gu, gB, gC, gD, ga, gg, gs
 
 
-def _sum_rows_product(a: Tensor, b: Tensor, split: int = 128) -> Tensor:
+def _sum_rows_product(a: Tensor, b: Tensor, split: int = 32) -> Tensor:
     """a^T b for row-major a [R, M], b [R, N] with R much larger than M, N (the
-    weight gradients sum over every (batch, step) row): R is split into
-    ``split`` slices multiplied as one batched GEMM and the partials added,
-    the shape the library GEMMs run well (one GEMM with K = R ran at ~24
-    TFLOP/s here)."""
+    weight gradients sum over every (batch, step) row): the first
+    split * (R // split) rows are split into ``split`` slices multiplied as one
+    batched GEMM and the partials added, the remaining rows (fewer than
+    ``split``) by one small GEMM.  That is the shape the library GEMMs run
+    well: one GEMM with K = R ran at ~24 TFLOP/s here, 16–64 slices at ~110
+    (128 slices 104, 512 slices 80)."""
     R = a.size(0)
-    if R < 4 * split or R % split != 0:
+    n = R // split
+    if n < 4:
         return a.t() @ b
-    return torch.bmm(a.view(split, R // split, -1).transpose(1, 2), b.view(split, R // split, -1)).sum(0)
+    head = split * n
+    out = torch.bmm(a[:head].view(split, n, -1).transpose(1, 2), b[:head].view(split, n, -1)).sum(0)
+    if head < R:
+        out += a[head:].t() @ b[head:]
+    return out
 
 
 def unfused_layer_forward(variant: str, inputs: Tensor, B: Tensor, C: Tensor, D: Tensor,

@@ -161,3 +161,16 @@ def test_layer_entry_argument_checks():
         layers.dlinoss_layer_forward("imex1", *args)
     with pytest.raises(RuntimeError, match="float32"):
         layers.dlinoss_layer_forward("imex1", args[0].double(), *args[1:])
+
+
+@pytest.mark.parametrize("rows", [3, 100, 127, 128, 130, 1000, 4096])
+def test_weight_gradient_row_sum_split(rows):
+    """The fused layer's weight gradients a^T b over every (batch, step) row,
+    split into batched slices plus a remainder, equal the plain product."""
+    from ossm_amd.layers import _sum_rows_product
+    g = torch.Generator().manual_seed(rows)
+    a = torch.randn(rows, 12, generator=g, dtype=torch.float64)
+    b = torch.randn(rows, 7, generator=g, dtype=torch.float64)
+    got = _sum_rows_product(a, b)
+    assert got.shape == (12, 7)
+    assert torch.allclose(got, a.t() @ b, rtol=1e-12, atol=1e-12)
