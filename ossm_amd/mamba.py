@@ -193,6 +193,31 @@ def selective_scan_mamba(inputs: Tensor, dt: Tensor, A: Tensor, B: Tensor, C: Te
     return MambaScanFn.apply(inputs, dt, A, B, C, gate, dt_bias)
 
 
+class _ColumnSplit(torch.autograd.Function):
+    """``xz[..., :d], xz[..., d:]`` as views, whose backward writes the gradient
+    of ``xz`` in one pass (torch.cat of the two); slicing the tensor directly
+    would, in the backward, zero-fill the whole ``[B, L, 2d]`` gradient once per
+    slice, copy each slice's gradient in and add the two."""
+
+    @staticmethod
+    def forward(ctx, xz: Tensor, d: int):  # type: ignore[override]
+        ctx.d = d
+        ctx.shape = xz.shape
+        return xz[..., :d], xz[..., d:]
+
+    @staticmethod
+    def backward(ctx, gx: Optional[Tensor], gz: Optional[Tensor]):  # type: ignore[override]
+        d, shape = ctx.d, ctx.shape
+        if gx is None and gz is None:
+            return None, None
+        ref = gx if gx is not None else gz
+        if gx is None:
+            gx = torch.zeros(*shape[:-1], d, dtype=ref.dtype, device=ref.device)
+        if gz is None:
+            gz = torch.zeros(*shape[:-1], shape[-1] - d, dtype=ref.dtype, device=ref.device)
+        return torch.cat([gx, gz], dim=-1), None
+
+
 # ------------------------------------------------------------------ the mixer
 class MambaMixer(nn.Module):
     """Mamba mixer (reference ``_MambaMixer``, mambarec.py:63-184) whose conv,
@@ -246,7 +271,7 @@ class MambaMixer(nn.Module):
             raise RuntimeError("the fused Mamba mixer runs on the GPU only")
         Di, R, N = self.d_inner, self.dt_rank, self.d_state
         xz = self.in_proj(inputs).float()
-        x, z = xz[..., :Di], xz[..., Di:]                 # views, row stride 2 * d_inner
+        x, z = _ColumnSplit.apply(xz, Di)                 # views, row stride 2 * d_inner
         x_conv = mamba_conv_silu(x, self.conv1d.weight.float(),
                                  None if self.conv1d.bias is None else self.conv1d.bias.float())
         proj = self.x_proj(x_conv.to(self.x_proj.weight.dtype)).float()
