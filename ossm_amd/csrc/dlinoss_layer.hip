@@ -202,7 +202,11 @@ __device__ __forceinline__ void stage_store(const RowStage<SK>& r, float* __rest
 
 // SMALL: Hp, Pp <= 128 (one oscillator group per wave, four row groups per
 // thread): the registers are sized for that, so that four workgroups share a CU.
-template <int V, bool VEC, bool SMALL>
+// PAD: H or P is not a multiple of 32, so the projections' padded rows and
+// columns read clamped weights that mask_* zeroes; without padding every weight
+// is in range and the loops consume the loads as they are (a select on a loaded
+// value is where the compiler puts the wait for it).
+template <int V, bool VEC, bool SMALL, bool PAD>
 __global__ __launch_bounds__(kLayerThreads) __attribute__((amdgpu_waves_per_eu(SMALL ? 4 : 1)))
 void dlinoss_layer_fwd_kernel(
     LayerArgs A, unsigned long long* __restrict__ rec, LaunchSync sync) {
@@ -266,7 +270,7 @@ void dlinoss_layer_fwd_kernel(
           float4 av = an;
           an = *reinterpret_cast<const float4*>(arow + 4 * min(q + 1, ng - 1));
           float4 wq[2] = {wb[j][0], wb[j][1]};
-          mask_bw(A.H, A.P, p, half * hh + 4 * q, wq);
+          if constexpr (PAD) mask_bw(A.H, A.P, p, half * hh + 4 * q, wq);
           const float4 w0 = wq[0], w1 = wq[1];
           load_bw<VEC>(A.Bw, A.H, A.P, p, half * hh + 4 * min(q + AH, ng - 1), wb[j]);
           asm volatile("" ::: "memory");  // the prefetch stays here, not next to its use
@@ -280,6 +284,7 @@ void dlinoss_layer_fwd_kernel(
           acc_im[i] = mfma32(av.z, w1.y, acc_im[i]);
           acc_re[i] = mfma32(av.w, w1.z, acc_re[i]);
           acc_im[i] = mfma32(av.w, w1.w, acc_im[i]);
+          __builtin_amdgcn_sched_barrier(0);  // groups stay in program order (prefetch distance)
         }
       }
     }
@@ -380,7 +385,7 @@ void dlinoss_layer_fwd_kernel(
           const int q = q0 + j;
           float4 av = an;
           an = *reinterpret_cast<const float4*>(arow + 8 * min(q + 1, ng - 1));
-          const float4 cv = mask_cw(A.H, A.P, h, 4 * q + 2 * kk, cb[j]);
+          const float4 cv = PAD ? mask_cw(A.H, A.P, h, 4 * q + 2 * kk, cb[j]) : cb[j];
           cb[j] = load_cw<VEC>(A.Cw, A.H, A.P, h, 4 * min(q + AH, ng - 1) + 2 * kk);
           asm volatile("" ::: "memory");  // the prefetch stays here, not next to its use
           // and the MFMAs below it, after the next group's LDS read
@@ -389,6 +394,7 @@ void dlinoss_layer_fwd_kernel(
           acc = mfma32(av.y, cv.y, acc);
           acc = mfma32(av.z, cv.z, acc);
           acc = mfma32(av.w, cv.w, acc);
+          __builtin_amdgcn_sched_barrier(0);  // groups stay in program order (prefetch distance)
         }
       }
       if (h < A.H) {
@@ -484,7 +490,8 @@ __device__ __forceinline__ float4 mask_bw_pair(int H, int P, int h, int p0, floa
   return mask_cw(H, P, h, p0, w);
 }
 
-template <int V, bool VEC>
+// PAD: as for the forward (H or P not a multiple of 32: weights masked where used).
+template <int V, bool VEC, bool PAD>
 __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
     LayerBwdArgs A, unsigned long long* __restrict__ rec, LaunchSync sync) {
   using Model = Dlinoss<V>;
@@ -546,7 +553,7 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
           float4 av = an;
           an = *reinterpret_cast<const float4*>(arow + 4 * min(q + 1, ng1 - 1));
           float4 wq[2] = {wb[j][0], wb[j][1]};
-          mask_cw_pair(A.H, A.P, half * hh + 4 * q, p, wq);
+          if constexpr (PAD) mask_cw_pair(A.H, A.P, half * hh + 4 * q, p, wq);
           const float4 w0 = wq[0], w1 = wq[1];
           load_cw_pair<VEC>(A.Cw, A.H, A.P, half * hh + 4 * min(q + kAhead, ng1 - 1), p, wb[j]);
           asm volatile("" ::: "memory");  // the prefetch stays here, not next to its use
@@ -560,6 +567,7 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
           acc_im = mfma32(av.z, w1.y, acc_im);
           acc_re = mfma32(av.w, w1.z, acc_re);
           acc_im = mfma32(av.w, w1.w, acc_im);
+          __builtin_amdgcn_sched_barrier(0);  // groups stay in program order (prefetch distance)
         }
       }
 #pragma unroll
@@ -597,7 +605,7 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
           float4 av = an;
           an = *reinterpret_cast<const float4*>(arow + 4 * min(q + 1, ng1 - 1));
           float4 wq[2] = {wb[j][0], wb[j][1]};
-          mask_bw(A.H, A.P, p, half * hh + 4 * q, wq);
+          if constexpr (PAD) mask_bw(A.H, A.P, p, half * hh + 4 * q, wq);
           const float4 w0 = wq[0], w1 = wq[1];
           load_bw<VEC>(A.Bw, A.H, A.P, p, half * hh + 4 * min(q + kAhead, ng1 - 1), wb[j]);
           asm volatile("" ::: "memory");  // the prefetch stays here, not next to its use
@@ -611,6 +619,7 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
           acc_im[i] = mfma32(av.z, w1.y, acc_im[i]);
           acc_re[i] = mfma32(av.w, w1.z, acc_re[i]);
           acc_im[i] = mfma32(av.w, w1.w, acc_im[i]);
+          __builtin_amdgcn_sched_barrier(0);  // groups stay in program order (prefetch distance)
         }
       }
     }
@@ -725,7 +734,7 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
           const int q = q0 + j;
           float4 av = an;
           an = *reinterpret_cast<const float4*>(arow + 8 * min(q + 1, ng - 1));
-          const float4 cv = mask_bw_pair(A.H, A.P, h, 4 * q + 2 * kk, cb[j]);
+          const float4 cv = PAD ? mask_bw_pair(A.H, A.P, h, 4 * q + 2 * kk, cb[j]) : cb[j];
           cb[j] = load_bw_pair(A.Bw, A.H, A.P, h, 4 * min(q + kAhead, ng - 1) + 2 * kk);
           asm volatile("" ::: "memory");  // the prefetch stays here, not next to its use
           // and the MFMAs below it, after the next group's LDS read
@@ -734,6 +743,7 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
           acc = mfma32(av.y, cv.y, acc);
           acc = mfma32(av.z, cv.z, acc);
           acc = mfma32(av.w, cv.w, acc);
+          __builtin_amdgcn_sched_barrier(0);  // groups stay in program order (prefetch distance)
         }
       }
       if (h < A.H) {
@@ -781,7 +791,9 @@ int launch_layer_bwd(LayerBwdArgs args, float* ga, float* gg, float* gs, hipStre
   args.zero = ZeroFill{{ga, gg, gs}, args.P};
   const bool vec = args.H % 4 == 0 && args.P % 4 == 0 && aligned16(args.u) && aligned16(args.gy) &&
                    aligned16(args.Bw) && aligned16(args.Cw);
-  auto kern = vec ? dlinoss_layer_bwd_kernel<V, true> : dlinoss_layer_bwd_kernel<V, false>;
+  const bool pad = args.H % 32 != 0 || args.P % 32 != 0;
+  auto kern = vec ? (pad ? dlinoss_layer_bwd_kernel<V, true, true> : dlinoss_layer_bwd_kernel<V, true, false>)
+                  : (pad ? dlinoss_layer_bwd_kernel<V, false, true> : dlinoss_layer_bwd_kernel<V, false, false>);
   const size_t lds = layer_bwd_lds_bytes(args.H, args.P);
   // before the ticket reservation: a failure here leaves nothing reserved
   if (int rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -818,8 +830,13 @@ int launch_layer(const LayerArgs& args, hipStream_t stream) {
   const bool vec = args.H % 4 == 0 && args.P % 4 == 0 && aligned16(args.u) && aligned16(args.Bw) &&
                    aligned16(args.Cw);
   const bool small = args.H <= 128 && args.P <= 128;
-  auto kern = vec ? (small ? dlinoss_layer_fwd_kernel<V, true, true> : dlinoss_layer_fwd_kernel<V, true, false>)
-                  : (small ? dlinoss_layer_fwd_kernel<V, false, true> : dlinoss_layer_fwd_kernel<V, false, false>);
+  const bool pad = args.H % 32 != 0 || args.P % 32 != 0;
+  using K = void (*)(LayerArgs, unsigned long long*, LaunchSync);
+  const K kern =
+      vec ? (small ? (pad ? dlinoss_layer_fwd_kernel<V, true, true, true> : dlinoss_layer_fwd_kernel<V, true, true, false>)
+                   : (pad ? dlinoss_layer_fwd_kernel<V, true, false, true> : dlinoss_layer_fwd_kernel<V, true, false, false>))
+          : (small ? (pad ? dlinoss_layer_fwd_kernel<V, false, true, true> : dlinoss_layer_fwd_kernel<V, false, true, false>)
+                   : (pad ? dlinoss_layer_fwd_kernel<V, false, false, true> : dlinoss_layer_fwd_kernel<V, false, false, false>));
   const size_t lds = layer_lds_bytes(args.H, args.P);
   // before the ticket reservation: a failure here leaves nothing reserved
   if (int rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
