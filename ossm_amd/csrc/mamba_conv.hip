@@ -11,9 +11,11 @@
 //   dx[t] = sum_k w[k] dpre[t+K-1-k],  dw[d,k] = sum_{b,t} dpre[b,t,d] x[b,t-K+1+k,d],
 //   dbias[d] = sum_{b,t} dpre[b,t,d].
 //
-// Memory-bound elementwise work: a thread owns 4 channels (16-byte runs along
-// d, so a wave moves 1 KiB per step) and a span of steps, loading all of the
-// span's inputs (and the K-1 before it) before the first is used.  Threads are
+// Memory-bound elementwise work: a thread owns 2 channels (8-byte runs along
+// d, so a wave moves 512 bytes per step) and a span of steps, loading all of
+// the span's inputs (and the K-1 before it) before the first is used; the
+// backward walks its span in tiles that share the overlapping inputs and
+// pre-activation gradients through registers.  Threads are
 // numbered channel group fastest, then span, then batch row, so narrow D still
 // fills whole waves.  The weight and bias gradients are per-thread partial
 // sums over its span, written per (batch row, span) and reduced over those
@@ -68,7 +70,7 @@ __device__ __forceinline__ bool conv_pos(const ConvArgs& a, int& b, int& span, i
 
 __device__ __forceinline__ float sigm(float p) { return 1.f / (1.f + __expf(-p)); }
 
-// C channels per thread (4 with 16-byte moves, else 1), as a fixed-size vector.
+// C channels per thread (2 with 8-byte moves, 4 with 16-byte, else 1), as a fixed-size vector.
 template <int C>
 struct Vec {
   float v[C];
@@ -80,6 +82,9 @@ __device__ __forceinline__ Vec<C> load_vec(const float* p) {
   if constexpr (C == 4) {
     const float4 q = *reinterpret_cast<const float4*>(p);
     r.v[0] = q.x; r.v[1] = q.y; r.v[2] = q.z; r.v[3] = q.w;
+  } else if constexpr (C == 2) {
+    const float2 q = *reinterpret_cast<const float2*>(p);
+    r.v[0] = q.x; r.v[1] = q.y;
   } else {
     r.v[0] = *p;
   }
@@ -90,6 +95,8 @@ template <int C>
 __device__ __forceinline__ void store_vec(float* p, const Vec<C>& r) {
   if constexpr (C == 4) {
     *reinterpret_cast<float4*>(p) = make_float4(r.v[0], r.v[1], r.v[2], r.v[3]);
+  } else if constexpr (C == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(r.v[0], r.v[1]);
   } else {
     *p = r.v[0];
   }
@@ -172,15 +179,25 @@ __global__ __launch_bounds__(kConvThreads) void conv_silu_bwd_kernel(ConvArgs a)
 #pragma unroll
     for (int k = 0; k < K; ++k) gw[k][e] = 0.f;
   }
-  constexpr int NX = kBwdTile + 2 * (K - 1);  // inputs for pre over the tile and its K-1 successors
-  constexpr int NP = kBwdTile + K - 1;        // dpre over the tile and its K-1 successors
-  for (int t0 = span * kBwdSpan; t0 < min(a.L, (span + 1) * kBwdSpan); t0 += kBwdTile) {
-    Vec<C> xs[NX], dp[NP];
+  // One sliding window over the span: xs[i] = x at ts - K + 1 + i, dp[i] =
+  // dpre at ts + i.  Each tile loads its new inputs and forms its new dpre;
+  // the K - 1 values of each it shares with the previous tile stay in
+  // registers (the loops are unrolled, so the indices are fixed).
+  const int ts = span * kBwdSpan;
+  constexpr int NX = kBwdSpan + 2 * (K - 1);
+  constexpr int NP = kBwdSpan + K - 1;
+  Vec<C> xs[NX], dp[NP];
 #pragma unroll
-    for (int i = 0; i < NX; ++i) xs[i] = x_at<C>(a, xb, t0 - K + 1 + i, d);
+  for (int tile = 0; tile < kBwdSpan / kBwdTile; ++tile) {
+    const int base = tile * kBwdTile;
+    if (ts + base >= a.L) break;
+    constexpr int kShareX = 2 * (K - 1), kShareP = K - 1;
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const int t = t0 + i;
+    for (int i = (tile == 0 ? 0 : base + kShareX); i < base + kBwdTile + kShareX; ++i)
+      xs[i] = x_at<C>(a, xb, ts - K + 1 + i, d);
+#pragma unroll
+    for (int i = (tile == 0 ? 0 : base + kShareP); i < base + kBwdTile + kShareP; ++i) {
+      const int t = ts + i;
       const Vec<C> go = t < a.L ? load_vec<C>(a.dout + ob + static_cast<size_t>(t) * a.D + d) : zero_vec<C>();
 #pragma unroll
       for (int e = 0; e < C; ++e) {
@@ -192,8 +209,9 @@ __global__ __launch_bounds__(kConvThreads) void conv_silu_bwd_kernel(ConvArgs a)
       }
     }
 #pragma unroll
-    for (int i = 0; i < kBwdTile; ++i) {
-      const int t = t0 + i;
+    for (int j = 0; j < kBwdTile; ++j) {
+      const int i = base + j;
+      const int t = ts + i;
       if (t >= a.L) break;
       Vec<C> gx;
 #pragma unroll
@@ -258,19 +276,24 @@ dim3 flat_grid(const ConvArgs& a, int C) {
 
 template <int K>
 int launch_fwd(const ConvArgs& a, bool vec, hipStream_t stream) {
-  const dim3 grid = flat_grid(a, vec ? 4 : 1);
+  const dim3 grid = flat_grid(a, vec ? 2 : 1);
   if (vec)
-    hipLaunchKernelGGL((conv_silu_fwd_kernel<K, 4>), grid, dim3(kConvThreads), 0, stream, a);
+    hipLaunchKernelGGL((conv_silu_fwd_kernel<K, 2>), grid, dim3(kConvThreads), 0, stream, a);
   else
     hipLaunchKernelGGL((conv_silu_fwd_kernel<K, 1>), grid, dim3(kConvThreads), 0, stream, a);
   return launch_check("conv_silu_fwd_kernel");
 }
 
+// Both directions take 2 channels per thread (8-byte moves; a wave still
+// covers 512 contiguous bytes of a row): the windows of inputs, upstream
+// gradients and weights grow with the channels (the backward at K = 4: 189
+// VGPRs and two waves per SIMD with 4 channels, 100 and four with 2), and
+// these latency-bound kernels need the waves.
 template <int K>
 int launch_bwd(const ConvArgs& a, bool vec, hipStream_t stream) {
-  const dim3 grid = flat_grid(a, vec ? 4 : 1);
+  const dim3 grid = flat_grid(a, vec ? 2 : 1);
   if (vec)
-    hipLaunchKernelGGL((conv_silu_bwd_kernel<K, 4>), grid, dim3(kConvThreads), 0, stream, a);
+    hipLaunchKernelGGL((conv_silu_bwd_kernel<K, 2>), grid, dim3(kConvThreads), 0, stream, a);
   else
     hipLaunchKernelGGL((conv_silu_bwd_kernel<K, 1>), grid, dim3(kConvThreads), 0, stream, a);
   if (int rc = launch_check("conv_silu_bwd_kernel")) return rc;
