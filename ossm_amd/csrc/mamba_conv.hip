@@ -11,8 +11,9 @@
 //   dx[t] = sum_k w[k] dpre[t+K-1-k],  dw[d,k] = sum_{b,t} dpre[b,t,d] x[b,t-K+1+k,d],
 //   dbias[d] = sum_{b,t} dpre[b,t,d].
 //
-// Memory-bound elementwise work: a thread owns 2 channels (8-byte runs along
-// d, so a wave moves 512 bytes per step) and a span of steps, loading all of
+// Memory-bound elementwise work: a thread owns 2 channels in the forward
+// (8-byte runs along d, so a wave moves 512 bytes per step), 1 in the
+// backward, and a span of steps, loading all of
 // the span's inputs (and the K-1 before it) before the first is used; the
 // backward walks its span in tiles that share the overlapping inputs and
 // pre-activation gradients through registers.  Threads are
@@ -70,7 +71,7 @@ __device__ __forceinline__ bool conv_pos(const ConvArgs& a, int& b, int& span, i
 
 __device__ __forceinline__ float sigm(float p) { return 1.f / (1.f + __expf(-p)); }
 
-// C channels per thread (2 with 8-byte moves, 4 with 16-byte, else 1), as a fixed-size vector.
+// C channels per thread (2 with 8-byte moves, else 1), as a fixed-size vector.
 template <int C>
 struct Vec {
   float v[C];
@@ -79,10 +80,7 @@ struct Vec {
 template <int C>
 __device__ __forceinline__ Vec<C> load_vec(const float* p) {
   Vec<C> r;
-  if constexpr (C == 4) {
-    const float4 q = *reinterpret_cast<const float4*>(p);
-    r.v[0] = q.x; r.v[1] = q.y; r.v[2] = q.z; r.v[3] = q.w;
-  } else if constexpr (C == 2) {
+  if constexpr (C == 2) {
     const float2 q = *reinterpret_cast<const float2*>(p);
     r.v[0] = q.x; r.v[1] = q.y;
   } else {
@@ -93,9 +91,7 @@ __device__ __forceinline__ Vec<C> load_vec(const float* p) {
 
 template <int C>
 __device__ __forceinline__ void store_vec(float* p, const Vec<C>& r) {
-  if constexpr (C == 4) {
-    *reinterpret_cast<float4*>(p) = make_float4(r.v[0], r.v[1], r.v[2], r.v[3]);
-  } else if constexpr (C == 2) {
+  if constexpr (C == 2) {
     *reinterpret_cast<float2*>(p) = make_float2(r.v[0], r.v[1]);
   } else {
     *p = r.v[0];
@@ -274,6 +270,13 @@ dim3 flat_grid(const ConvArgs& a, int C) {
   return dim3(static_cast<unsigned>((threads + kConvThreads - 1) / kConvThreads));
 }
 
+// The forward takes 2 channels per thread (8-byte moves; a wave still covers
+// 512 contiguous bytes of a row), the backward one: its windows of inputs,
+// upstream gradients, weights and weight sums grow with the channels (at K = 4:
+// 189 VGPRs and two waves per SIMD with 4 channels, 100 and four with 2, 64
+// and eight with 1), and this latency-bound kernel needs the waves (C4's
+// shape: 182, 154 and 142 us with its column sums); the forward, lighter,
+// measured best with 2 (84, 77 and 86 us).
 template <int K>
 int launch_fwd(const ConvArgs& a, bool vec, hipStream_t stream) {
   const dim3 grid = flat_grid(a, vec ? 2 : 1);
@@ -284,18 +287,9 @@ int launch_fwd(const ConvArgs& a, bool vec, hipStream_t stream) {
   return launch_check("conv_silu_fwd_kernel");
 }
 
-// Both directions take 2 channels per thread (8-byte moves; a wave still
-// covers 512 contiguous bytes of a row): the windows of inputs, upstream
-// gradients and weights grow with the channels (the backward at K = 4: 189
-// VGPRs and two waves per SIMD with 4 channels, 100 and four with 2), and
-// these latency-bound kernels need the waves.
 template <int K>
-int launch_bwd(const ConvArgs& a, bool vec, hipStream_t stream) {
-  const dim3 grid = flat_grid(a, vec ? 2 : 1);
-  if (vec)
-    hipLaunchKernelGGL((conv_silu_bwd_kernel<K, 2>), grid, dim3(kConvThreads), 0, stream, a);
-  else
-    hipLaunchKernelGGL((conv_silu_bwd_kernel<K, 1>), grid, dim3(kConvThreads), 0, stream, a);
+int launch_bwd(const ConvArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((conv_silu_bwd_kernel<K, 1>), flat_grid(a, 1), dim3(kConvThreads), 0, stream, a);
   if (int rc = launch_check("conv_silu_bwd_kernel")) return rc;
   return launch_column_sums<K + 1>(static_cast<const float*>(a.partials), a.D, 1,
                                    static_cast<int64_t>(a.B) * a.n_spans,
@@ -322,7 +316,7 @@ struct FwdLaunch {
 };
 template <int K>
 struct BwdLaunch {
-  static int run(const ConvArgs& a, bool vec, hipStream_t s) { return launch_bwd<K>(a, vec, s); }
+  static int run(const ConvArgs& a, hipStream_t s) { return launch_bwd<K>(a, s); }
 };
 
 __global__ void conv_zero_kernel(float* __restrict__ p, int64_t n) {
@@ -384,9 +378,7 @@ int ossm_mamba_conv_backward(const float* x, int64_t ld_x, const float* weight, 
   ConvArgs a{x, weight, bias, grad_out, grad_x, static_cast<float*>(ws), grad_weight, grad_bias,
              static_cast<int>(batch), static_cast<int>(length), static_cast<int>(dim),
              static_cast<int>(ld_x), n_spans};
-  const bool vec = dim % 4 == 0 && ld_x % 4 == 0 && aligned16(x) && aligned16(grad_out) &&
-                   aligned16(grad_x) && aligned16(ws);
-  return by_width<BwdLaunch>(static_cast<int>(width), a, vec, stream);
+  return by_width<BwdLaunch>(static_cast<int>(width), a, stream);
 }
 
 }  // extern "C"

@@ -118,7 +118,7 @@ __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
 }
 
 // n floats (all-zero bits, so also n / 2 doubles).
-int fill_zero(float* p, int64_t n, hipStream_t stream) {
+[[maybe_unused]] int fill_zero(float* p, int64_t n, hipStream_t stream) {
   if (n <= 0) return OSSM_OK;
   const int64_t blocks = (n + 255) / 256;
   hipLaunchKernelGGL(fill_zero_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, p, n);

@@ -723,7 +723,6 @@ template <class E, bool VEC, bool GATED, bool BLD, int NPW>
 __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   using LY = FwdLayout<NPW>;
   constexpr int TT = kFwdTile;
-  constexpr int RS = TT + 1;  // odd row stride: lane-per-row accesses hit distinct banks
   constexpr int ROWS = LY::kRows, CW = LY::kWaveCh, SEG = LY::kSeg;
   static_assert(TT == 32, "reduce_groups assumes 32-step tiles");
   static_assert(!BLD || NPW == 4, "the [B, L, D] layout stages 64 channels");
