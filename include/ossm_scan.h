@@ -101,7 +101,7 @@ int ossm_dlinoss_forward_noalloc(int variant, const float* a_diag, const float* 
  *   dlinoss_imex1.cpp:354-390, dlinoss_imex2.cpp:366-402,
  *   dlinoss_im.cpp:384-420,    dlinoss_ex.cpp:301-365.
  * grad_output is the gradient w.r.t. component 1 (x) of the states, [L,B,P] c64.
- * Only the states at sub-chunk boundaries are read; the rest is recomputed
+ * Only the state before each 128-step chunk is read; the rest is recomputed
  * from bu.  grad_a/grad_g/grad_step [P] f32 are overwritten (not accumulated).
  */
 int ossm_dlinoss_backward(int variant, const float* a_diag, const float* g_diag,

@@ -18,12 +18,13 @@
 //   3. every wave rebuilds its own carry from the LDS aggregates and re-runs
 //      its T steps from it, storing the states.
 //
-// Backward (reverse time; reads bu + grad once, states only at sub-chunk
-// starts, writes grad_bu once)
+// Backward (reverse time; reads bu + grad once, states only at chunk starts,
+// writes grad_bu once)
 //   The adjoint mu_t = M^T mu_{t+1} + (0, g_t) is the same chunked scan run
 //   backwards with the transposed transition.  States s_{t-1} needed by the
-//   parameter gradients are recomputed in registers from the checkpoint
-//   states[t0 - 1] instead of reading the whole trajectory.  Per-lane sums of
+//   parameter gradients are recomputed in registers from one checkpoint per
+//   chunk, the state before its first step, and the waves' forward summaries
+//   exchanged through LDS, instead of reading the whole trajectory.  Per-lane sums of
 //   <mu_i, s_j,t-1> and <mu_i, bu_t> go to a partials buffer; one small
 //   kernel adds them over time chunks and batch rows per oscillator in 64 row
 //   groups (fixed order, fp64), applies each variant's chain rule (linear in
@@ -226,7 +227,7 @@ struct BwdBuf {
   typename Model::In x[Model::kRecompute ? T : 1];  // bu_t (recomputing models)
   float4 sp[Model::kRecompute ? 1 : T];             // s_{t-1} read from states (LinOSS)
   typename Model::GIn go[T];
-  float4 ck;                                        // states[t0 - 1] (recomputing models)
+  float4 ck;  // states at the chunk's start, then the wave's s_{t0-1} (recomputing models)
   typename Model::Raw raw;                          // the channel's oscillator parameters
 };
 
@@ -261,7 +262,8 @@ __device__ __forceinline__ void bwd_load(BwdBuf<Model, T>& b, const BwdTicket& k
   const unsigned lc = clamped_lane(k.g, nc);
   b.raw = Model::load_raw(prm, k.g * kWave + static_cast<int>(lc));
   if constexpr (Model::kRecompute)
-    b.ck = group_row(states, max(min(k.t0 - 1, static_cast<long long>(L - 1)), 0ll), nc, k.g)[lc];
+    b.ck = group_row(states, max(min(static_cast<long long>(k.c) * (T * W) - 1,
+                                     static_cast<long long>(L - 1)), 0ll), nc, k.g)[lc];
   asm volatile("" ::: "memory");  // keep the issue order: the compiler would sink these
 #pragma unroll
   for (int i = 0; i < T; ++i) {
@@ -279,45 +281,75 @@ __device__ __forceinline__ void bwd_load(BwdBuf<Model, T>& b, const BwdTicket& k
 // First part of one chunk: reverse aggregate, look-back for the carry from
 // later chunks.  Returns the carry into the wave's sub-chunk (the adjoint
 // after its last step) and sets KT = (M^T)^T.  For recomputing models the
-// states s_{t-1} are rebuilt from the checkpoint states[t0 - 1] in H segments
-// of T/H steps, each staged in LDS (S = T/H slots per wave) just before the
-// final pass reads it (bwd_back): with H = 1 the front stages all of them;
-// with H = 2 it only runs to the middle of the sub-chunk (s_mid) and the
+// states s_{t-1} are rebuilt from one checkpoint per chunk, the state before
+// its first step: wave 0 runs its sub-chunk from it, the other waves first run
+// theirs from a zero state, and each wave v passes its result (wave 0: its end
+// state; the others: the sub-chunk's effect on a zero state) to the later
+// waves through slot kLink of its LDS staging region, from which wave w folds
+// its own first state s_{t0-1} = M^T (...(M^T e_0 + f_1)...) + f_{w-1}.  The
+// states are staged in H segments of T/H steps (S slots per wave) just before
+// the final pass reads them (bwd_back): with H = 1 the front stages all of
+// them; with H = 2 it only runs to the middle of the sub-chunk (s_mid) and the
 // back recomputes each half in turn, halving the LDS footprint for one extra
 // half sweep.  SS = 2 (H = 1 only) stages every other state, s_{t-1} of the
 // even steps; the back rebuilds an odd step's from the even one before it with
-// one forward step, for half the LDS.  All waves call it together.
+// one forward step, for half the LDS.  Slot kLink is read by the later waves
+// between the two barriers, so a staged state that belongs there waits in a
+// register until after the second.  All waves call it together.
 template <class Model, int T, int W, int S, int H, int SS>
 __device__ __forceinline__ float4 bwd_front(
     BwdBuf<Model, T>& b, const BwdTicket& k, int L, int nc, int n_chunks,
     unsigned long long* __restrict__ rec, const LaunchSync& sync, float4 (*s_agg)[kWave],
     float4* s_carry, float4 (*s_sp)[S][kWave], typename Model::Mat& KT, float4& s_mid) {
   static_assert(H == 1 || H == 2, "one or two staging segments");
+  constexpr int kLink = S - 1;
+  constexpr bool kLinkStaged = H == 1 && kLink < T / SS;
   const int lane = threadIdx.x & (kWave - 1);
   const int w = wave_id();
   const auto cf = Model::coef_of(b.raw);
+  float4 held = f4zero();
 
-  // Steps at or past L are never used (every use below is guarded), and lanes
-  // past the last channel only feed values that are never stored, so the
-  // loaded buffers need no masking.  FULL: the whole sub-chunk is in range
-  // (uniform), so the step loops run without guards.
+  // The forward recurrence over the sub-chunk from s.  MODE 0 runs it only
+  // for its result; 1 also stages (H = 1: s_{t-1} of every SS-th step; H = 2:
+  // s_mid); 2 stages and stops where staging ends.  Steps at or past L are
+  // never used (every use below is guarded), and lanes past the last channel
+  // only feed values that are never stored, so the loaded buffers need no
+  // masking.  FULL: the whole sub-chunk is in range (uniform), so the step
+  // loops run without guards.
+  auto forward = [&](auto full_tag, auto mode_tag, float4 s) -> float4 {
+    constexpr bool FULL = decltype(full_tag)::value;
+    constexpr int MODE = decltype(mode_tag)::value;
+    constexpr int N = MODE == 2 && H == 2 ? T / 2 : T;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if constexpr (MODE != 0 && H == 1) {
+        if (i % SS == 0) {
+          if (i / SS == kLink)
+            held = s;
+          else
+            s_sp[w][i / SS][lane] = s;
+        }
+      }
+      if constexpr (MODE == 1 && H == 2) {
+        if (i == T / 2) s_mid = s;
+      }
+      if (FULL || k.t0 + i < L) s = Model::step(cf, s, b.x[i]);
+    }
+    if constexpr (MODE == 2 && H == 2) s_mid = s;
+    return s;
+  };
+  using Summary = std::integral_constant<int, 0>;
+  using StageAll = std::integral_constant<int, 1>;
+  using Stage = std::integral_constant<int, 2>;
+  const float4 start0 = k.c > 0 ? b.ck : f4zero();
+
   auto sweep = [&](auto full_tag) -> float4 {
     constexpr bool FULL = decltype(full_tag)::value;
     auto live = [&](int i) { return FULL || k.t0 + i < L; };
     if constexpr (Model::kRecompute) {
-      float4 s = k.t0 >= 1 ? b.ck : f4zero();
-      if constexpr (H == 1) {
-#pragma unroll
-        for (int i = 0; i < T; ++i) {
-          if (i % SS == 0) s_sp[w][i / SS][lane] = s;
-          if (live(i)) s = Model::step(cf, s, b.x[i]);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < T / 2; ++i)
-          if (live(i)) s = Model::step(cf, s, b.x[i]);
-        s_mid = s;
-      }
+      const float4 link =
+          w == 0 ? forward(full_tag, StageAll{}, start0) : forward(full_tag, Summary{}, f4zero());
+      s_sp[w][kLink][lane] = link;
     } else {
       if (k.t0 == 0) b.sp[0] = f4zero();  // s_{-1} = 0
     }
@@ -328,7 +360,8 @@ __device__ __forceinline__ float4 bwd_front(
       if (live(i)) m = Model::rev_carry(cf, Model::mu(m, b.go[i]));
     return m;
   };
-  const float4 m = k.t0 + T <= L ? sweep(std::true_type{}) : sweep(std::false_type{});
+  const bool full = k.t0 + T <= L;
+  const float4 m = full ? sweep(std::true_type{}) : sweep(std::false_type{});
   s_agg[w][lane] = m;
   KT = mat_pow(mat_adjoint(Model::matrix(cf)), T);
   typename Model::Mat KC{};
@@ -359,7 +392,24 @@ __device__ __forceinline__ float4 bwd_front(
       s_carry[lane] = carry;
     }
   }
+
+  // 3. the other waves' first states, and their staging, while wave 0 walks back
+  if constexpr (Model::kRecompute) {
+    if (w > 0) {
+      const typename Model::Mat MT = mat_pow(Model::matrix(cf), T);
+      float4 s = s_sp[0][kLink][lane];
+      for (int v = 1; v < w; ++v) s = f4add(mat_apply(MT, s), s_sp[v][kLink][lane]);
+      b.ck = s;
+      if (full)
+        forward(std::true_type{}, Stage{}, s);
+      else
+        forward(std::false_type{}, Stage{}, s);
+    } else {
+      b.ck = start0;
+    }
+  }
   __syncthreads();
+  if constexpr (Model::kRecompute && kLinkStaged) s_sp[w][kLink][lane] = held;
 
   // the wave's own carry: the chunk carry through the later waves' sub-chunks
   float4 y = s_carry[lane];
@@ -392,7 +442,7 @@ __device__ __forceinline__ void bwd_back(BwdBuf<Model, T>& b, const BwdTicket& k
     for (int h = H - 1; h >= 0; --h) {
       if constexpr (Model::kRecompute && H > 1) {
         // stage segment h: s_{t-1} for its Q steps, from its first state
-        float4 s = h == 0 ? (k.t0 >= 1 ? b.ck : f4zero()) : s_mid;
+        float4 s = h == 0 ? b.ck : s_mid;
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
           sp_lds[q * kWave + lane] = s;
