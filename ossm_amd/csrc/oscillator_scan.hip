@@ -572,13 +572,29 @@ struct FwdPlan {
   size_t rec_bytes;
 };
 
+// Without OSSM_OSC_TILE_FWD the tile follows the grid (both defaults cover 128
+// steps per chunk, so the grid is the same either way): 8 steps x 16 waves,
+// four waves per SIMD, for 256..2048 workgroups, else 16 x 8.  Measured
+// (imex1, events, us, 16x8 vs 8x16) at [L, B, P]: 64 workgroups [1024, 8, 64]
+// 8.7 vs 9.0; 512: [4096, 8, 128] 23.6 vs 22.0, [1024, 32, 128] 21.7 vs 19.6;
+// 1024: [8192, 16, 64] 39.1 vs 38.0, [4096, 16, 128] 38.5 vs 35.9; 2048:
+// [16384, 8, 128] 69.7 vs 68.7, [4096, 32, 128] 65.9 vs 62.6, [2048, 32, 256]
+// 65.8 vs 62.8; 4096: [4096, 64, 128] 139.8 vs 143.7; 8192: [65536, 4, 256]
+// 285 vs 311.
 FwdPlan fwd_plan(int64_t L, int64_t nc) {
-  static const Tile tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{16, 8, 1, 1, 1});
+  static const Tile env_tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{0, 0, 0, 1, 1});
+  constexpr int64_t CL = 128;
   FwdPlan pl;
-  pl.tile = tile;
-  const int64_t CL = int64_t(tile.T) * tile.W;
   pl.n_chunks = (L + CL - 1) / CL;
   pl.n_groups = (nc + kWave - 1) / kWave;
+  if (env_tile.T > 0) {
+    pl.tile = env_tile;
+    const int64_t cl = int64_t(env_tile.T) * env_tile.W;
+    pl.n_chunks = (L + cl - 1) / cl;
+  } else {
+    const int64_t wgs = pl.n_chunks * pl.n_groups;
+    pl.tile = wgs >= 256 && wgs <= 2048 ? Tile{8, 16, 4, 1, 1} : Tile{16, 8, 1, 1, 1};
+  }
   pl.total = pl.n_chunks * pl.n_groups;
   pl.rec_bytes = static_cast<size_t>(pl.n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
   return pl;
