@@ -63,8 +63,10 @@ def test_dlinoss_matches_reference_kernel_vectors(K, variant):
     no_device_errors()
 
 
-# shapes: tiny, ragged (P and B*P not multiples of 64), many chunks / groups
-SHAPES = [(1, 1, 1), (2, 3, 5), (129, 2, 33), (1000, 3, 70), (2100, 4, 64)]
+# shapes: tiny, ragged (P and B*P not multiples of 64), many chunks / groups;
+# (1000, 32, 64) is 256 workgroups, where the forward switches to its 8-step x
+# 16-wave tile, with a partial last chunk
+SHAPES = [(1, 1, 1), (2, 3, 5), (129, 2, 33), (1000, 3, 70), (2100, 4, 64), (1000, 32, 64)]
 
 
 def _oracle64(variant, a, g, dt, bu, go):
