@@ -556,7 +556,8 @@ Tile parse_tile(const char* env, Tile dflt) {
 }
 
 // Instantiated tiles (T, W, OCC).
-#define OSSM_FWD_TILES(X) X(16, 8, 1) X(16, 8, 4) X(8, 8, 4) X(16, 4, 4) X(8, 16, 4) X(32, 4, 2)
+#define OSSM_FWD_TILES(X) \
+  X(16, 8, 1) X(16, 16, 1) X(16, 8, 4) X(8, 8, 4) X(16, 4, 4) X(8, 16, 4) X(32, 4, 2)
 // Backward tiles (T, W, OCC, H, S): H = staging segments of the recomputed
 // states, S = 2 stages every other one.
 #define OSSM_BWD_TILES(X)                                                                     \
@@ -572,32 +573,31 @@ struct FwdPlan {
   size_t rec_bytes;
 };
 
-// Without OSSM_OSC_TILE_FWD the tile follows the grid (both defaults cover 128
-// steps per chunk, so the grid is the same either way): 8 steps x 16 waves,
-// four waves per SIMD, for 256..2048 workgroups, else 16 x 8.  Measured
-// (imex1, events, us, 16x8 vs 8x16) at [L, B, P]: 64 workgroups [1024, 8, 64]
-// 8.7 vs 9.0; 512: [4096, 8, 128] 23.6 vs 22.0, [1024, 32, 128] 21.7 vs 19.6;
-// 1024: [8192, 16, 64] 39.1 vs 38.0, [4096, 16, 128] 38.5 vs 35.9; 2048:
-// [16384, 8, 128] 69.7 vs 68.7, [4096, 32, 128] 65.9 vs 62.6, [2048, 32, 256]
-// 65.8 vs 62.8; 4096: [4096, 64, 128] 139.8 vs 143.7; 8192: [65536, 4, 256]
-// 285 vs 311.
-FwdPlan fwd_plan(int64_t L, int64_t nc) {
-  static const Tile env_tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{0, 0, 0, 1, 1});
-  constexpr int64_t CL = 128;
+// Without OSSM_OSC_TILE_FWD: 16 steps x 16 waves (256-step chunks, half the
+// look-back records and depth of 128-step ones), unless that leaves fewer
+// than 128 workgroups; then 16 x 8.  Measured (imex1, events, us; 16x8,
+// 8x16 at four waves per SIMD, 16x16) at [L, B, P]: [1024, 8, 64] 8.8, 9.0,
+// 9.7 (32 workgroups at 256 steps); [4096, 8, 128] 23.4, 22.0, 19.6;
+// [1024, 32, 128] 21.0, 18.9, 18.2; [8192, 16, 64] 39.1, 37.5, 34.4;
+// [4096, 16, 128] 37.7, 35.5, 33.3; [4096, 32, 128] 66.1, 63.1, 62.8;
+// [2048, 32, 256] 66.0, 62.7, 61.9; [16384, 8, 128] 70.1, 68.8, 64.2;
+// [4096, 64, 128] 139.6, 146.7, 129.0; [65536, 4, 256] 285.5, 309.6, 278.6.
+FwdPlan fwd_plan_with(int64_t L, int64_t nc, Tile tile) {
   FwdPlan pl;
-  pl.n_chunks = (L + CL - 1) / CL;
+  pl.tile = tile;
+  const int64_t CL = int64_t(tile.T) * tile.W;
   pl.n_groups = (nc + kWave - 1) / kWave;
-  if (env_tile.T > 0) {
-    pl.tile = env_tile;
-    const int64_t cl = int64_t(env_tile.T) * env_tile.W;
-    pl.n_chunks = (L + cl - 1) / cl;
-  } else {
-    const int64_t wgs = pl.n_chunks * pl.n_groups;
-    pl.tile = wgs >= 256 && wgs <= 2048 ? Tile{8, 16, 4, 1, 1} : Tile{16, 8, 1, 1, 1};
-  }
+  pl.n_chunks = (L + CL - 1) / CL;
   pl.total = pl.n_chunks * pl.n_groups;
   pl.rec_bytes = static_cast<size_t>(pl.n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
   return pl;
+}
+
+FwdPlan fwd_plan(int64_t L, int64_t nc) {
+  static const Tile env_tile = parse_tile("OSSM_OSC_TILE_FWD", Tile{0, 0, 0, 1, 1});
+  if (env_tile.T > 0) return fwd_plan_with(L, nc, env_tile);
+  const bool wide = (L + 255) / 256 * ((nc + kWave - 1) / kWave) >= 128;
+  return fwd_plan_with(L, nc, wide ? Tile{16, 16, 1, 1, 1} : Tile{16, 8, 1, 1, 1});
 }
 
 // Enqueues the forward kernel of plan `pl` with look-back records at
@@ -738,6 +738,8 @@ int dlinoss_backward_v(const float* a, const float* g, const float* dt, const vo
 // so nothing needs clearing between calls, but calls that overlap on one GPU
 // (several streams, or several processes' launches interleaved) race.
 constexpr size_t kNoAllocRecordBytes = size_t(16) << 20;
+// 64 bytes of records per channel and 128-step chunk: half a byte per state-step.
+constexpr int64_t kNoAllocStateSteps = int64_t(kNoAllocRecordBytes) * 2;
 static __device__ __align__(256) unsigned char scratch[kHdrBytes + kNoAllocRecordBytes];
 
 constexpr int kNoAllocMaxDevices = 64;
@@ -808,16 +810,19 @@ int ossm_dlinoss_forward_noalloc(int variant, const float* a_diag, const float* 
     return set_error(OSSM_ERR_INVALID_ARGUMENT, "dlinoss_forward_noalloc: null pointer");
   if (variant < OSSM_DLINOSS_IMEX1 || variant > OSSM_DLINOSS_EX)
     return set_error(OSSM_ERR_INVALID_ARGUMENT, "Unknown D-LinOSS variant code");
-  const FwdPlan pl = fwd_plan(length, batch * ssm);
+  // Always 128-step chunks (16 x 8), whatever ossm_dlinoss_forward would pick,
+  // so that the records take the half byte per state-step the limit is stated in.
+  const FwdPlan pl = fwd_plan_with(length, batch * ssm, Tile{16, 8, 1, 1, 1});
   if (pl.total > INT_MAX)
     return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
-  if (pl.rec_bytes > kNoAllocRecordBytes)
+  if (length * batch * ssm > kNoAllocStateSteps || pl.rec_bytes > kNoAllocRecordBytes)
     return set_error(OSSM_ERR_UNSUPPORTED,
-                     "dlinoss_forward_noalloc: this problem needs " + std::to_string(pl.rec_bytes) +
-                         " bytes of look-back records, more than the fixed " +
+                     "dlinoss_forward_noalloc: " + std::to_string(length * batch * ssm) +
+                         " state-steps need " + std::to_string(pl.rec_bytes) +
+                         " bytes of look-back records; the fixed " +
                          std::to_string(kNoAllocRecordBytes) +
-                         "-byte scratch (half a byte per state-step: at most 33,554,432 "
-                         "state-steps per call); use ossm_dlinoss_forward");
+                         "-byte scratch serves at most 33,554,432 state-steps per call (half a "
+                         "byte each); use ossm_dlinoss_forward");
   hipStream_t stream = static_cast<hipStream_t>(stream_v);
   int dev = 0;
   if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;

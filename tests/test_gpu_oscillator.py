@@ -64,8 +64,8 @@ def test_dlinoss_matches_reference_kernel_vectors(K, variant):
 
 
 # shapes: tiny, ragged (P and B*P not multiples of 64), many chunks / groups;
-# (1000, 32, 64) is 256 workgroups, where the forward switches to its 8-step x
-# 16-wave tile, with a partial last chunk
+# (1000, 32, 64) is the smallest grid (128 workgroups) on which the forward
+# takes its 256-step tile (16 steps x 16 waves), with a partial last chunk
 SHAPES = [(1, 1, 1), (2, 3, 5), (129, 2, 33), (1000, 3, 70), (2100, 4, 64), (1000, 32, 64)]
 
 
@@ -152,7 +152,7 @@ def test_dlinoss_config2_full_size(K, variant):
 
 def test_dlinoss_config5_long_sequence(K):
     """BASELINE config 5 (B=4, L=65536, P=256, forward only): cross-workgroup
-    carries over 512 chunks; checked per channel against the oracle and
+    carries over 256 chunks of 256 steps; checked per channel against the oracle and
     against fp64 truth."""
     L, B, P = 65536, 4, 256
     a, g, dt, bu, _ = dlinoss_inputs(L, B, P, seed=5)
@@ -253,13 +253,15 @@ def _linoss_grad(rng, L, B, P):
     return (rng.normal(size=(L, B, P, 2)) + 1j * rng.normal(size=(L, B, P, 2))).astype(np.complex64)
 
 
-def test_linoss_imex_unit_modulus(K):
+@pytest.mark.parametrize("B", [4, 32])
+def test_linoss_imex_unit_modulus(K, B):
     """LinOSS-IMEX (linoss.py:253-258): M = [[1, -dt a], [dt, 1 - dt^2 a]] has
     det M = 1 and, for dt^2 a < 4, both eigenvalues on the unit circle, so
-    neither the chunk powers M^T nor the look-back carries decay.  L = 4096
-    (32 chunks of 128 steps per channel), b = (bu dt, bu dt^2); forward and the
-    native backward against the oracle and fp64 truth."""
-    L, B, P = 4096, 4, 64
+    neither the chunk powers M^T nor the look-back carries decay.  L = 4096,
+    b = (bu dt, bu dt^2); forward and the native backward against the oracle
+    and fp64 truth.  B = 4 leaves 64 workgroups, so the forward runs 128-step
+    chunks; B = 32 runs its 256-step tile (16 steps x 16 waves, M^256)."""
+    L, P = 4096, 64
     rng = np.random.default_rng(4096)
     a = rng.uniform(0.1, 1.0, P)
     dt = 1 / (1 + np.exp(-rng.normal(size=P)))

@@ -137,3 +137,30 @@ def test_torch_library_ops_schema_and_meta(variant):
     grads = bwd(a, a, a, bu, st, bu)
     assert [tuple(g.shape) for g in grads] == [(5,), (5,), (5,), (7, 3, 5)]
     assert [g.dtype for g in grads] == [torch.float32] * 3 + [torch.complex64]
+
+
+@pytest.mark.parametrize("shape", [(4096, 64, 160), (65536, 4, 256), (2**25 + 1, 1, 1)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_noalloc_forward_refuses_above_its_limit_on_the_host(shape):
+    """ossm_dlinoss_forward_noalloc serves at most 33,554,432 state-steps
+    (L*B*P) per call, whatever tile the allocating forward picks for that
+    shape; above it the call returns OSSM_ERR_UNSUPPORTED from its host-side
+    checks, before any HIP call, so the pointers (host dummies here, no GPU)
+    are never read."""
+    import torch  # noqa: F401  (binds the HIP runtime first, as the product does)
+
+    from ossm_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libossm_scan.so not built (python -m ossm_amd.build)")
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    f = lib.ossm_dlinoss_forward_noalloc
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 3 + [ctypes.c_void_p]
+    lib.ossm_last_error.restype = ctypes.c_char_p
+    buf = ctypes.create_string_buffer(16)
+    p = ctypes.addressof(buf)
+    L, B, P = shape
+    assert L * B * P > 2**25
+    assert f(0, p, p, p, p, p, L, B, P, None) == 3  # OSSM_ERR_UNSUPPORTED
+    assert b"33,554,432" in lib.ossm_last_error()
