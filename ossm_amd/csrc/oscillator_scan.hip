@@ -563,7 +563,7 @@ Tile parse_tile(const char* env, Tile dflt) {
 #define OSSM_BWD_TILES(X)                                                                     \
   X(16, 8, 1, 1, 1) X(16, 8, 4, 2, 1) X(16, 8, 2, 2, 1) X(16, 4, 1, 1, 1) X(8, 8, 1, 1, 1)    \
   X(8, 8, 4, 2, 1) X(32, 4, 1, 1, 1) X(32, 4, 2, 2, 1) X(8, 16, 1, 1, 1) X(16, 8, 4, 1, 2)   \
-  X(16, 8, 1, 1, 2)
+  X(16, 8, 1, 1, 2) X(16, 16, 1, 1, 2)
 
 // Launch geometry of a forward scan: the tile, the chunk grid and the bytes
 // of look-back records it needs (two 4-word records per chunk and channel).
@@ -652,7 +652,24 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
                     int64_t B, int64_t P, hipStream_t stream) {
   StreamCall call(stream);
   if (call.status()) return call.status();
-  static const Tile tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{16, 8, 1, 1, 2});
+  // Without OSSM_OSC_TILE_BWD: 16 x 16 (256-step chunks, one 16-wave workgroup
+  // per CU, 145 KiB of LDS) for 128..2047 workgroups at that chunk length, else
+  // 16 x 8.  Measured (imex1, events, us, 16x8 vs 16x16) at [L, B, P]:
+  // [1024, 8, 64] 12.9 vs 15.5 (32 workgroups); [4096, 8, 128] 29.6 vs 24.1;
+  // [1024, 32, 128] 26.7 vs 22.8; [8192, 16, 64] 46.8 vs 43.7; [4096, 16, 128]
+  // 46.5 vs 42.9; [16384, 4, 256] 84.5 vs 78.3; [4096, 32, 128] 78.6 vs 76.6;
+  // [2048, 32, 256] 79.5 vs 71.2; [16384, 8, 128] 84.1 vs 78.2; [4096, 64, 128]
+  // 155.1 vs 164.7 (2048 workgroups).  Sixteen waves cap a lane at 128 VGPRs:
+  // imex1 and ex fit (128, no spills); imex2 and im spill 6 and 2 registers and
+  // the LinOSS backward, which holds every s_{t-1} it reads, 75, so those keep
+  // 16 x 8.
+  constexpr bool kWideFits = std::is_same_v<Model, Dlinoss<OSSM_DLINOSS_IMEX1>> ||
+                             std::is_same_v<Model, Dlinoss<OSSM_DLINOSS_EX>>;
+  static const Tile env_tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{0, 0, 0, 1, 1});
+  const int64_t wgs256 = (L + 255) / 256 * ((B * P + kWave - 1) / kWave);
+  const Tile tile = env_tile.T > 0 ? env_tile
+                    : kWideFits && wgs256 >= 128 && wgs256 < 2048 ? Tile{16, 16, 1, 1, 2}
+                                                                  : Tile{16, 8, 1, 1, 2};
   constexpr int NS = Model::kSums;
   const int64_t nc = B * P;
   const int64_t CL = int64_t(tile.T) * tile.W;
