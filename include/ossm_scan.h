@@ -101,8 +101,8 @@ int ossm_dlinoss_forward_noalloc(int variant, const float* a_diag, const float* 
  *   dlinoss_imex1.cpp:354-390, dlinoss_imex2.cpp:366-402,
  *   dlinoss_im.cpp:384-420,    dlinoss_ex.cpp:301-365.
  * grad_output is the gradient w.r.t. component 1 (x) of the states, [L,B,P] c64.
- * Only the state before each 128-step chunk is read; the rest is recomputed
- * from bu.  grad_a/grad_g/grad_step [P] f32 are overwritten (not accumulated).
+ * Only the state before each chunk (128 or 256 steps, by the launch's tile)
+ * is read; the rest is recomputed from bu.  grad_a/grad_g/grad_step [P] f32 are overwritten (not accumulated).
  */
 int ossm_dlinoss_backward(int variant, const float* a_diag, const float* g_diag,
                           const float* step, const void* bu, const void* states,
