@@ -660,11 +660,10 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   // 46.5 vs 42.9; [16384, 4, 256] 84.5 vs 78.3; [4096, 32, 128] 78.6 vs 76.6;
   // [2048, 32, 256] 79.5 vs 71.2; [16384, 8, 128] 84.1 vs 78.2; [4096, 64, 128]
   // 155.1 vs 164.7 (2048 workgroups).  Sixteen waves cap a lane at 128 VGPRs:
-  // imex1 and ex fit (128, no spills); imex2 and im spill 6 and 2 registers and
-  // the LinOSS backward, which holds every s_{t-1} it reads, 75, so those keep
-  // 16 x 8.
-  constexpr bool kWideFits = std::is_same_v<Model, Dlinoss<OSSM_DLINOSS_IMEX1>> ||
-                             std::is_same_v<Model, Dlinoss<OSSM_DLINOSS_EX>>;
+  // imex1 and ex fit (no spills); imex2 and im spill 6 and 2 registers and still
+  // gain (config 2: 90.5 -> 81.8 and 86.9 -> 80.4 us); the LinOSS backward, which
+  // holds every s_{t-1} it reads, spills 75 and keeps 16 x 8.
+  constexpr bool kWideFits = Model::kRecompute;
   static const Tile env_tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{0, 0, 0, 1, 1});
   const int64_t wgs256 = (L + 255) / 256 * ((B * P + kWave - 1) / kWave);
   const Tile tile = env_tile.T > 0 ? env_tile
