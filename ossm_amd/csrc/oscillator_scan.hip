@@ -750,9 +750,11 @@ int dlinoss_backward_v(const float* a, const float* g, const float* dt, const vo
 // launch's tag, the ticket counter matches the host's count of 0).  Each GPU
 // holds its own copy until the process ends; its address on a device comes
 // from hipGetSymbolAddress, taken once per device on that device's first
-// call.  Every call on a GPU shares its copy: records are tagged per launch,
-// so nothing needs clearing between calls, but calls that overlap on one GPU
-// (several streams, or several processes' launches interleaved) race.
+// call.  The array is per process and per GPU: every call of this process on
+// a GPU shares that GPU's copy (another process has a copy of its own).
+// Records are tagged per launch, so nothing needs clearing between calls, but
+// calls of this process that overlap on one GPU (several streams or threads)
+// race.
 constexpr size_t kNoAllocRecordBytes = size_t(16) << 20;
 // 64 bytes of records per channel and 128-step chunk: half a byte per state-step.
 constexpr int64_t kNoAllocStateSteps = int64_t(kNoAllocRecordBytes) * 2;

@@ -2203,10 +2203,8 @@ int bwd_states_per_lane(int64_t rows64) {
 #define OSSM_SEL_FWD_NPW2_BELOW 4
 #endif
 int fwd_states_per_lane(int64_t rows64) {
-  static const int forced = [] {
-    const char* v = std::getenv("OSSM_SEL_FWD_NPW");
-    return v == nullptr ? 0 : std::atoi(v);
-  }();
+  const char* env = std::getenv("OSSM_SEL_FWD_NPW");  // read per call: tests switch it
+  const int forced = env == nullptr ? 0 : std::atoi(env);
   if (forced == 2 || forced == 4) return forced;
   int dev = 0, n_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess ||

@@ -51,6 +51,23 @@ def assert_parity(actual, ref32, ref64, rtol=1e-4, atol=1e-5, what="", factor=2.
         f"fp32 reference and max|gpu-fp64|={e_gpu:.3e} > {factor}*max|ref-fp64|={e_ref:.3e}+atol")
 
 
+def sum_atol(ref64, k=2e-5) -> float:
+    """The magnitude-scaled absolute tolerance of a gradient that is a sum
+    over many terms (over batch, time or channels): k * max(1, max|ref|).
+    The sum's rounding scales with its terms, not with each element."""
+    return k * max(1.0, float(np.abs(np.asarray(ref64)).max()))
+
+
+def assert_grad_parity(actual, ref32, ref64, what="", rtol=1e-4, k=2e-5):
+    """Elementwise gradient parity: assert_parity at rtol and the
+    magnitude-scaled atol of sum_atol(ref64, k), i.e. every element within
+    tolerance of an fp32 computation of the same gradient or, where that
+    computation's own rounding misses, no less accurate than it against fp64
+    truth."""
+    assert_parity(np.asarray(actual), np.asarray(ref32), np.asarray(ref64), rtol, sum_atol(ref64, k),
+                  what)
+
+
 def rel_fro(a, b) -> float:
     a = np.asarray(a, np.complex128 if np.iscomplexobj(a) else np.float64)
     b = np.asarray(b, a.dtype)

@@ -18,8 +18,8 @@ import pytest
 import torch
 
 import oracle
-from tests.gpu_util import (announce, assert_parity, dlinoss_inputs, need_gpu, no_device_errors,
-                            rel_fro, to_dev, to_np)
+from tests.gpu_util import (announce, assert_grad_parity, assert_parity, dlinoss_inputs, need_gpu,
+                            no_device_errors, rel_fro, sum_atol, to_dev, to_np)
 
 pytestmark = pytest.mark.gpu
 VARIANTS = oracle.VARIANTS
@@ -102,19 +102,22 @@ def test_layer_module_matches_reference_fixture(layers, variant):
     np.testing.assert_allclose(to_np(y), np.asarray(c["outputs"]), rtol=2e-5, atol=2e-5)
 
 
-def _oracle_grads(variant, args, gy):
-    """fp64 gradients of sum(y * gy) w.r.t. (u, B, C, D, a, g, dt) from the
-    oracle's forward and adjoint: g_x = gy (C_re - i C_im) (complex gradient as
+def _oracle_grads(variant, args, gy, dtype=np.float64):
+    """Gradients of sum(y * gy) w.r.t. (u, B, C, D, a, g, dt) from the
+    oracle's forward and adjoint, in `dtype` (fp64: truth; fp32: the
+    reference's arithmetic): g_x = gy (C_re - i C_im) (complex gradient as
     d/dre + i d/dim), the scan adjoint gives grad_bu and (a, g, dt), then the
     two projections' transposes."""
-    u, Bw, Cw, Dw, a, g, dt = (np.asarray(x, np.float64) for x in args)
+    u, Bw, Cw, Dw, a, g, dt = (np.asarray(x, dtype) for x in args)
+    gy = np.asarray(gy, dtype)
+    ct = np.complex128 if dtype == np.float64 else np.complex64
     nb, L, H = u.shape
     P = Bw.shape[0]
     y, states = oracle.dlinoss_layer_forward(variant, u, Bw, Cw, Dw, a, g, dt)
-    bu = np.einsum("blh,ph->lbp", u, Bw[..., 0] + 1j * Bw[..., 1])
+    bu = np.einsum("blh,ph->lbp", u, (Bw[..., 0] + 1j * Bw[..., 1]).astype(ct)).astype(ct)
     x = states[..., 1].transpose(1, 0, 2)  # [B, L, P]
-    gx = np.einsum("blh,hp->blp", gy, Cw[..., 0] - 1j * Cw[..., 1])
-    ga, gg, gs, gbu = oracle.dlinoss_backward(variant, a, g, dt, bu, states,
+    gx = np.einsum("blh,hp->blp", gy, (Cw[..., 0] - 1j * Cw[..., 1]).astype(ct)).astype(ct)
+    ga, gg, gs, gbu = oracle.dlinoss_backward(variant, a, g, dt, np.ascontiguousarray(bu), states,
                                               np.ascontiguousarray(gx.transpose(1, 0, 2)))
     gbu = gbu.transpose(1, 0, 2)  # [B, L, P]
     gu = np.einsum("blp,ph->blh", gbu.real, Bw[..., 0]) + np.einsum("blp,ph->blh", gbu.imag, Bw[..., 1]) + gy * Dw
@@ -122,6 +125,17 @@ def _oracle_grads(variant, args, gy):
     gC = np.stack([np.einsum("blh,blp->hp", gy, x.real), -np.einsum("blh,blp->hp", gy, x.imag)], -1)
     gD = (gy * u).sum((0, 1))
     return [gu, gB, gC, gD, ga, gg, gs]
+
+
+LEAVES = ["inputs", "B", "C", "D", "a_diag", "g_diag", "step"]
+
+
+def _check_grads(got, args, gy, variant, what):
+    """Every gradient elementwise against the fp32 oracle, fp64 as arbiter."""
+    r32 = _oracle_grads(variant, args, gy, np.float32)
+    r64 = _oracle_grads(variant, args, gy, np.float64)
+    for t, a, b, n in zip(got, r32, r64, LEAVES):
+        assert_grad_parity(to_np(t), a, b, f"{what} grad {n}")
 
 
 @pytest.mark.parametrize("variant", VARIANTS)
@@ -135,11 +149,7 @@ def test_layer_gradients(layers, variant):
     leaves = [to_dev(x).requires_grad_(True) for x in args]
     y = layers.DlinossLayerFn.apply(variant, *leaves)
     y.backward(to_dev(gy))
-    ref = _oracle_grads(variant, args, gy.astype(np.float64))
-    names = ["inputs", "B", "C", "D", "a_diag", "g_diag", "step"]
-    for t, r, n in zip(leaves, ref, names):
-        err = rel_fro(to_np(t.grad), r)
-        assert err < 5e-5, f"{variant} grad {n}: relative error {err:.2e}"
+    _check_grads([t.grad for t in leaves], args, gy, variant, variant)
     no_device_errors()
 
 
@@ -160,10 +170,11 @@ def test_layer_module_fused_and_unfused_agree(layers):
     y2 = layers.unfused_layer_forward("imex1", u2, layer.B, layer.C, layer.D, a, g, dt)
     (y2 * y2).sum().backward()
     g_unfused = [p.grad.clone() for p in layer.parameters()] + [u2.grad.clone()]
-    assert rel_fro(to_np(y), to_np(y2)) < 1e-5
+    yr = to_np(y2)
+    np.testing.assert_allclose(to_np(y), yr, rtol=1e-4, atol=1e-5 * max(1.0, float(np.abs(yr).max())))
     for a_, b_ in zip(g_fused, g_unfused):
-        assert np.isfinite(to_np(a_)).all()
-        assert rel_fro(to_np(a_), to_np(b_)) < 1e-4
+        ref = to_np(b_)
+        np.testing.assert_allclose(to_np(a_), ref, rtol=1e-4, atol=sum_atol(ref))
     no_device_errors()
 
 
@@ -245,29 +256,27 @@ def test_layer_fused_backward_odd_sizes(layers, shape):
     leaves = [to_dev(x).requires_grad_(True) for x in args]
     y = layers.DlinossLayerFn.apply("im", *leaves)
     y.backward(to_dev(gy))
-    ref = _oracle_grads("im", args, gy.astype(np.float64))
-    for t, r, n in zip(leaves, ref, ["inputs", "B", "C", "D", "a_diag", "g_diag", "step"]):
-        err = rel_fro(to_np(t.grad), r)
-        assert err < 5e-5, f"grad {n}: relative error {err:.2e}"
+    _check_grads([t.grad for t in leaves], args, gy, "im", f"{shape}")
     no_device_errors()
 
 
 @pytest.mark.parametrize("variant", VARIANTS)
 def test_layer_fused_backward_matches_unfused_at_size(layers, variant):
     """At H = P = 128 over 1000 steps (32 chunks through the reverse look-back)
-    the fused backward's gradients equal the unfused composition's."""
+    the fused backward's gradients and the unfused composition's, each
+    elementwise against the fp32 oracle with fp64 truth as arbiter."""
     nb, L, H, P = 4, 1000, 128, 128
     announce(f"layer fused vs unfused bwd {variant} B={nb} L={L}")
-    args = [to_dev(x) for x in _layer_inputs(nb, L, H, P, 21, variant)]
-    gy = torch.randn(nb, L, H, device="cuda")
+    host = _layer_inputs(nb, L, H, P, 21, variant)
+    args = [to_dev(x) for x in host]
+    gy_h = np.random.default_rng(22).normal(size=(nb, L, H)).astype(np.float32)
+    gy = to_dev(gy_h)
     l1 = [t.clone().requires_grad_(True) for t in args]
     layers.DlinossLayerFn.apply(variant, *l1).backward(gy)
     l2 = [t.clone().requires_grad_(True) for t in args]
     layers.unfused_layer_forward(variant, *l2).backward(gy)
-    for a_, b_, n in zip(l1, l2, ["inputs", "B", "C", "D", "a_diag", "g_diag", "step"]):
-        assert np.isfinite(to_np(a_.grad)).all()
-        err = rel_fro(to_np(a_.grad), to_np(b_.grad))
-        assert err < 1e-4, f"{variant} grad {n}: {err:.2e}"
+    _check_grads([t.grad for t in l1], host, gy_h, variant, f"{variant} fused")
+    _check_grads([t.grad for t in l2], host, gy_h, variant, f"{variant} unfused")
     no_device_errors()
 
 
@@ -282,10 +291,7 @@ def test_layer_fused_backward_at_256(layers):
     gy = np.random.default_rng(32).normal(size=(nb, L, H)).astype(np.float32)
     leaves = [to_dev(x).requires_grad_(True) for x in args]
     layers.DlinossLayerFn.apply("imex1", *leaves).backward(to_dev(gy))
-    ref = _oracle_grads("imex1", args, gy.astype(np.float64))
-    for t, r, n in zip(leaves, ref, ["inputs", "B", "C", "D", "a_diag", "g_diag", "step"]):
-        err = rel_fro(to_np(t.grad), r)
-        assert err < 5e-5, f"grad {n}: relative error {err:.2e}"
+    _check_grads([t.grad for t in leaves], args, gy, "imex1", "H=P=256")
     no_device_errors()
 
 
@@ -299,7 +305,5 @@ def test_layer_backward_recompute_path(layers, monkeypatch):
     gy = np.random.default_rng(34).normal(size=(nb, L, H)).astype(np.float32)
     leaves = [to_dev(x).requires_grad_(True) for x in args]
     layers.DlinossLayerFn.apply("imex1", *leaves).backward(to_dev(gy))
-    ref = _oracle_grads("imex1", args, gy.astype(np.float64))
-    for t, r in zip(leaves, ref):
-        assert rel_fro(to_np(t.grad), r) < 5e-5
+    _check_grads([t.grad for t in leaves], args, gy, "imex1", "recompute path")
     no_device_errors()

@@ -127,6 +127,16 @@ def test_selective_bf16_backward_both_layouts(K, shape, npw, monkeypatch):
     _bf16_case(K, shape, True)
 
 
+@pytest.mark.parametrize("npw", [2, 4])
+@pytest.mark.parametrize("shape", [(2, 70, 37, 5), (1, 130, 129, 20), (4, 96, 384, 64),
+                                   (2, 40, 2070, 16)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_selective_bf16_forward_both_layouts(K, shape, npw, monkeypatch):
+    """bf16 storage with the forward forced to 2 and to 4 states per lane."""
+    monkeypatch.setenv("OSSM_SEL_FWD_NPW", str(npw))
+    _bf16_case(K, shape, True)
+
+
 def _bf16_case(K, shape, gated):
     import torch
 
@@ -163,7 +173,8 @@ def _bf16_case(K, shape, gated):
 def test_selective_bf16_config4(K):
     """BASELINE config 4 (B=16, D=1536, L=2048, N=16, bf16 storage): the full
     tensors against the fp32 entry point on the same values (one-ulp rule),
-    and two batch rows against fp64 truth."""
+    and one batch row (every per-row output and gradient: out, du, ddt, dB,
+    dC, dz) against fp64 truth."""
     Bz, D, L, N = 16, 1536, 2048, 16
     args = [_bf16_round(x) if i != 2 else x
             for i, x in enumerate(selective_inputs(Bz, D, L, N, seed=46))]
@@ -184,7 +195,10 @@ def test_selective_bf16_config4(K):
     _truth_bound(_np(out)[bs], t_out, EPS_BF16, "out slice")
     t_g = oracle.selective_backward(sl(g), sl(u), sl(dt), A.astype(np.float64), sl(Bm), sl(Cm),
                                     sl(z))
-    for idx, name, rel in ((0, "du", EPS_BF16), (1, "ddt", EPS_BF16), (5, "dz", 2 * EPS_BF16)):
+    # dB and dC of a batch row are sums over that row's channels only, so the
+    # slice's fp64 backward is their exact truth
+    for idx, name, rel in ((0, "du", EPS_BF16), (1, "ddt", EPS_BF16), (3, "dB", EPS_BF16),
+                           (4, "dC", EPS_BF16), (5, "dz", 2 * EPS_BF16)):
         _truth_bound(_np(grads[idx])[bs], t_g[idx], rel, name + " slice")
 
 

@@ -1,8 +1,12 @@
 """GPU test of the allocation-free entry point ossm_dlinoss_forward_noalloc,
 called through the C ABI and checked against ossm_dlinoss_forward (the
 allocating entry point with the same kernels) to the north-star tolerance:
-two calls in a row, the second smaller, then a problem above the fixed
-scratch's limit, which must be refused with a message."""
+two calls in a row, the second smaller.
+
+The refusal of problems above the fixed scratch's limit is checked on the
+host (tests/test_library.py): a call that slipped past a regressed guard
+would write look-back records beyond the array, so it is never made on a
+GPU."""
 
 from __future__ import annotations
 
@@ -16,7 +20,6 @@ from tests.gpu_util import announce, assert_close, dlinoss_inputs, need_gpu, no_
 
 pytestmark = pytest.mark.gpu
 RTOL, ATOL = 1e-4, 1e-5
-LIMIT_STATE_STEPS = 1 << 25  # 16 MiB of records at half a byte per state-step
 
 
 @pytest.fixture(scope="module")
@@ -49,16 +52,3 @@ def test_noalloc_forward_matches_allocating_entry(lib, variant):
         assert_close(to_np(got), to_np(ref), RTOL, ATOL, f"noalloc vs allocating L={L} B={B} P={P}")
         no_device_errors()
 
-
-def test_noalloc_forward_rejects_problems_above_its_scratch(lib):
-    L, B, P = 4096, 64, 160  # 41.9M state-steps: 21 MB of records
-    assert L * B * P > LIMIT_STATE_STEPS
-    small = torch.zeros(1, dtype=torch.float32, device="cuda")
-    announce("noalloc dlinoss above the fixed scratch")
-    rc = lib.load().ossm_dlinoss_forward_noalloc(0, small.data_ptr(), small.data_ptr(), small.data_ptr(),
-                                                 small.data_ptr(), small.data_ptr(), L, B, P,
-                                                 torch.cuda.current_stream().cuda_stream)
-    assert rc == 3  # OSSM_ERR_UNSUPPORTED, before anything is launched
-    msg = lib.load().ossm_last_error().decode()
-    assert "fixed" in msg and "ossm_dlinoss_forward" in msg, msg
-    no_device_errors()
