@@ -50,7 +50,7 @@ enum {
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
 /* Library ABI version (bumped on any change of the entry points or their
-   behaviour; currently 12). */
+   behaviour; currently 13). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -109,6 +109,26 @@ int ossm_dlinoss_backward(int variant, const float* a_diag, const float* g_diag,
                           const void* grad_output, float* grad_a, float* grad_g,
                           float* grad_step, void* grad_bu, int64_t length, int64_t batch,
                           int64_t ssm, ossm_stream_t stream);
+
+/*
+ * complex128 forms of ossm_dlinoss_forward / ossm_dlinoss_backward: the
+ * reference's device dispatchers take complex64 and complex128
+ * (AT_DISPATCH_COMPLEX_TYPES, dlinoss_imex1_cuda.cu:196, 234; dlinoss_imex2_cuda.cu,
+ * dlinoss_im_cuda.cu, dlinoss_ex_cuda.cu alike), with a_diag, g_diag, step of the
+ * complex type's value type.  a_diag, g_diag, step [P] fp64; bu, grad_output,
+ * grad_bu [L,B,P] c128; states [L,B,P,2] c128; grad_a, grad_g, grad_step [P] fp64
+ * (overwritten).  One lane per channel walks the sequence (as the reference's
+ * kernels do); the backward reads every step's previous state from states, and
+ * the per-oscillator sums run over batch rows in order.
+ */
+int ossm_dlinoss_forward_f64(int variant, const double* a_diag, const double* g_diag,
+                             const double* step, const void* bu, void* states, int64_t length,
+                             int64_t batch, int64_t ssm, ossm_stream_t stream);
+int ossm_dlinoss_backward_f64(int variant, const double* a_diag, const double* g_diag,
+                              const double* step, const void* bu, const void* states,
+                              const void* grad_output, double* grad_a, double* grad_g,
+                              double* grad_step, void* grad_bu, int64_t length, int64_t batch,
+                              int64_t ssm, ossm_stream_t stream);
 
 /*
  * LinOSS scan forward, replaces linoss_scan (linoss_scan.cpp:115-146):
@@ -198,14 +218,6 @@ int ossm_sdlinoss_backward(int variant, const float* A, int64_t a_len, int64_t a
                            int64_t ssm, ossm_stream_t stream);
 
 /*
- * complex128 forms of the two entries above: the reference's device kernels
- * dispatch complex128 too (sdlinoss_imex1_cuda.cu:232, 271, and siblings).  A, G,
- * step are fp64 [X_len, X_batch, M]; bu, states, grad_output, grad_bu are c128
- * with the layouts above; grad_A, grad_G, grad_step fp64.  One lane per channel
- * walks the sequence (the backward reads every step's previous state from states);
- * broadcast gradients are summed in a fixed order.
- */
-/*
  * complex128 forms of ossm_linoss_forward / ossm_linoss_backward: the reference's
  * device kernel dispatches complex128 too (linoss_scan_cuda.cu:139).  m_ij [P],
  * b_seq, states, grad_output, grad_b [L,B,P,2], grad_m [P,2,2], all c128.  One lane
@@ -219,6 +231,14 @@ int ossm_linoss_backward_f64(const void* m11, const void* m12, const void* m21, 
                              void* grad_b, int64_t length, int64_t batch, int64_t ssm,
                              ossm_stream_t stream);
 
+/*
+ * complex128 forms of ossm_sdlinoss_forward / ossm_sdlinoss_backward: the reference's device kernels
+ * dispatch complex128 too (sdlinoss_imex1_cuda.cu:232, 271, and siblings).  A, G,
+ * step are fp64 [X_len, X_batch, M]; bu, states, grad_output, grad_bu are c128
+ * with the layouts above; grad_A, grad_G, grad_step fp64.  One lane per channel
+ * walks the sequence (the backward reads every step's previous state from states);
+ * broadcast gradients are summed in a fixed order.
+ */
 int ossm_sdlinoss_forward_f64(int variant, const double* A, int64_t a_len, int64_t a_batch,
                               const double* G, int64_t g_len, int64_t g_batch, const double* step,
                               int64_t s_len, int64_t s_batch, const void* bu, void* states,

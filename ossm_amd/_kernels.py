@@ -84,6 +84,26 @@ def _on_device(*tensors: Optional[torch.Tensor]) -> None:
 
 
 # ------------------------------------------------------------------- D-LinOSS
+_DLINOSS_ENTRIES = {torch.complex64: (torch.float32, ""), torch.complex128: (torch.float64, "_f64")}
+_TYPE_NAMES = {torch.float32: "Float", torch.float64: "Double", torch.complex64: "ComplexFloat",
+               torch.complex128: "ComplexDouble"}
+
+
+def _dlinoss_entry(variant: str, direction: str, bu, coeffs, same_as_bu) -> str:
+    """The C entry for bu's dtype, with the reference dispatcher's dtype rules
+    (dlinoss_imex1_cuda.cu:196, 234): complex64 or complex128 bu
+    (AT_DISPATCH_COMPLEX_TYPES), coefficient diagonals of its value type and
+    states / grad_output of its own type (data_ptr<T>)."""
+    if bu.dtype not in _DLINOSS_ENTRIES:
+        raise RuntimeError(f'"dlinoss_{variant}_{direction}_cuda" not implemented for '
+                           f"'{_TYPE_NAMES.get(bu.dtype, str(bu.dtype))}'")
+    real, suffix = _DLINOSS_ENTRIES[bu.dtype]
+    for t, want in [(c, real) for c in coeffs] + [(c, bu.dtype) for c in same_as_bu]:
+        _check(t.dtype == want, f"expected scalar type {_TYPE_NAMES[want]} but found "
+                                f"{_TYPE_NAMES.get(t.dtype, str(t.dtype))}")
+    return f"ossm_dlinoss_{direction}{suffix}"
+
+
 def _dlinoss_forward(variant: str, a_diag, g_diag, step, bu):
     # dlinoss_imex1.cpp:317-352 (same checks in the other variants)
     _check(a_diag.dim() == 1 and g_diag.dim() == 1 and step.dim() == 1,
@@ -101,11 +121,9 @@ def _dlinoss_forward(variant: str, a_diag, g_diag, step, bu):
     if not bu.is_cuda:
         return _delegate(f"dlinoss_{variant}_forward", a_diag, g_diag, step, bu)
     _on_device(a_diag, g_diag, step, bu)
-    _check(bu.dtype == torch.complex64 and a_diag.dtype == torch.float32
-           and g_diag.dtype == torch.float32 and step.dtype == torch.float32,
-           f"dlinoss_{variant} HIP kernel supports complex64 bu with float32 coefficients")
+    entry = _dlinoss_entry(variant, "forward", bu, (a_diag, g_diag, step), ())
     with torch.cuda.device(bu.device):
-        _lib.check(_lib.load().ossm_dlinoss_forward(
+        _lib.check(getattr(_lib.load(), entry)(
             _VARIANT_CODE[variant], a_diag.data_ptr(), g_diag.data_ptr(), step.data_ptr(),
             bu.data_ptr(), output.data_ptr(), length, batch, ssm, _lib.stream_of(bu)))
     return output
@@ -140,12 +158,9 @@ def _dlinoss_backward(variant: str, a_diag, g_diag, step, bu, states, grad_outpu
         return _delegate(f"dlinoss_{variant}_backward", a_diag, g_diag, step, bu, states,
                          grad_output)
     _on_device(a_diag, g_diag, step, bu, states, grad_output)
-    _check(bu.dtype == torch.complex64 and states.dtype == torch.complex64
-           and grad_output.dtype == torch.complex64 and a_diag.dtype == torch.float32
-           and g_diag.dtype == torch.float32 and step.dtype == torch.float32,
-           f"dlinoss_{variant} HIP kernel supports complex64 tensors with float32 coefficients")
+    entry = _dlinoss_entry(variant, "backward", bu, (a_diag, g_diag, step), (states, grad_output))
     with torch.cuda.device(bu.device):
-        _lib.check(_lib.load().ossm_dlinoss_backward(
+        _lib.check(getattr(_lib.load(), entry)(
             _VARIANT_CODE[variant], a_diag.data_ptr(), g_diag.data_ptr(), step.data_ptr(),
             bu.data_ptr(), states.data_ptr(), grad_output.data_ptr(), grad_a.data_ptr(),
             grad_g.data_ptr(), grad_step.data_ptr(), grad_bu.data_ptr(), length, batch, ssm,

@@ -20,6 +20,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libossm_scan.so"
 _c_int64 = ctypes.c_int64
 _vp = ctypes.c_void_p
 _fp = ctypes.c_void_p  # float* passed as raw device addresses
+_dp = ctypes.c_void_p  # double* passed as raw device addresses
 
 _SIGNATURES = {
     "ossm_abi_version": (ctypes.c_int, []),
@@ -53,6 +54,12 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_int, _fp, _c_int64, _c_int64, _fp, _c_int64, _c_int64, _fp, _c_int64, _c_int64,
          _vp, _vp, _vp, _fp, _fp, _fp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_dlinoss_forward_f64": (
+        ctypes.c_int, [ctypes.c_int, _dp, _dp, _dp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_dlinoss_backward_f64": (
+        ctypes.c_int,
+        [ctypes.c_int, _dp, _dp, _dp, _vp, _vp, _vp, _dp, _dp, _dp, _vp, _c_int64, _c_int64,
+         _c_int64, _vp]),
     "ossm_linoss_forward_f64": (
         ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
     "ossm_linoss_backward_f64": (

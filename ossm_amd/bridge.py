@@ -154,16 +154,21 @@ class DlinossFn(torch.autograd.Function):
 def run_dlinoss(variant: str, a_diag: Tensor, g_diag: Tensor, step: Tensor, bu: Tensor) -> Tensor:
     """x = states[..., 1] of the D-LinOSS recurrence for ``variant``
     (reference run_dlinoss, _dlinoss_scan.py:630-680).  bu is [L, B, P]
-    complex64 on the device; a, g, step are [P] float32."""
+    complex on the device; a, g, step are [P] real.  The precision follows the
+    reference's rule for higher-precision inputs (_dlinoss_scan.py:35-48,
+    648-654): float64 / complex128 when any coefficient is float64, else
+    float32 / complex64, with every input cast to it; both run on the device
+    kernels (the reference sends the float64 case to its Python loop)."""
     variant = variant.lower()
     if variant not in SUPPORTED_VARIANTS:
         raise ValueError(f"Unknown D-LinOSS variant '{variant}'.")
     if bu.numel() == 0:
         return bu
-    if bu.dtype != torch.complex64 or any(t.dtype != torch.float32 for t in (a_diag, g_diag, step)):
-        raise RuntimeError("the MI355X D-LinOSS kernels compute in float32/complex64; "
-                           f"got bu {bu.dtype}, coefficients {a_diag.dtype}")
-    return DlinossFn.apply(variant, a_diag, g_diag, step, bu)
+    real = torch.float64 if any(t.dtype == torch.float64 for t in (a_diag, g_diag, step)) \
+        else torch.float32
+    cplx = torch.complex128 if real == torch.float64 else torch.complex64
+    a_diag, g_diag, step = (t.to(dtype=real) for t in (a_diag, g_diag, step))
+    return DlinossFn.apply(variant, a_diag, g_diag, step, bu.to(dtype=cplx))
 
 
 def run_dlinoss_imex1(a_diag: Tensor, g_diag: Tensor, step: Tensor, bu: Tensor) -> Tensor:

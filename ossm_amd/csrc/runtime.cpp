@@ -159,7 +159,7 @@ void release_unlaunched(StreamCall& call, uint64_t n_workgroups) {
 
 extern "C" {
 
-int ossm_abi_version(void) { return 12; }
+int ossm_abi_version(void) { return 13; }
 
 const char* ossm_last_error(void) { return ossm::g_last_error.c_str(); }
 

@@ -1,6 +1,7 @@
 // The complex128 scans on gfx950 that the reference's device kernels dispatch
-// besides complex64: selective D-LinOSS (sdlinoss_imex1_cuda.cu:232, 271, and
-// the imex2 / im / ex siblings) and the LinOSS scan (linoss_scan_cuda.cu:139).
+// besides complex64: D-LinOSS (dlinoss_imex1_cuda.cu:196, 234, and the imex2 /
+// im / ex siblings), selective D-LinOSS (sdlinoss_imex1_cuda.cu:232, 271, and
+// siblings) and the LinOSS scan (linoss_scan_cuda.cu:139).
 // fp64 is the accuracy path, not the hot one: one lane per channel walks the
 // sequence, forward in time for the states and in reverse for the adjoint, and
 // consecutive lanes own consecutive channels, so every load and store of a
@@ -282,6 +283,224 @@ __global__ __launch_bounds__(kBlock64) void lin64_backward_kernel(
   for (int k = 0; k < 4; ++k) part[4 * static_cast<size_t>(ch) + k] = acc[k];
 }
 
+// ---- D-LinOSS (time-invariant parameters) ----------------------------------------
+// The four variants' coefficient tables, adjoint and chain rule in double, as
+// the reference's device kernels run them for complex128 (one thread per
+// channel, dlinoss_imex1_cuda.cu:23-172 and siblings):
+//   new0 = c0 s0 + c1 s1 + c2 bu ;  new1 = c3 s0 + c4 s1 + c5 bu
+// except imex1 (new1 = new0 + s1) and ex (new1 = c3 s0 + s1); tables
+// dlinoss_imex1.cpp:32-48, dlinoss_imex2.cpp:35-47, dlinoss_im.cpp:34-50,
+// dlinoss_ex.cpp:33-42.  No clamp on dt (the reference applies none).
+struct Coef64 {
+  double c0, c1, c2, c3, c4, c5;
+};
+
+struct DlParams64 {
+  const double* a;
+  const double* g;
+  const double* dt;
+  int P;
+};
+
+template <int V>
+__device__ __forceinline__ Coef64 dl64_coef(double alpha, double gamma, double sigma) {
+  if constexpr (V == OSSM_DLINOSS_IMEX1) {
+    const double inv = 1.0 / (1.0 + sigma * gamma);
+    const double s2i = sigma * sigma * inv;
+    return {inv, -alpha * s2i, s2i, 0.0, 0.0, 0.0};
+  } else if constexpr (V == OSSM_DLINOSS_IMEX2) {
+    const double s2 = sigma * sigma;
+    return {1.0 - sigma * gamma, -sigma * alpha, sigma, sigma - s2 * gamma, 1.0 - s2 * alpha, s2};
+  } else if constexpr (V == OSSM_DLINOSS_IM) {
+    const double s2 = sigma * sigma;
+    const double inv = 1.0 / (1.0 + sigma * gamma + s2 * alpha);
+    const double si = sigma * inv;
+    return {inv, -alpha * si, si, si, (1.0 + sigma * gamma) * inv, s2 * inv};
+  } else {
+    return {1.0 - sigma * gamma, -sigma * alpha, sigma, sigma, 0.0, 0.0};
+  }
+}
+
+// Sums per channel the chain rule reads (G_ij = sum <mu_i, s_j,t-1>, F_i =
+// sum <mu_i, bu_t>, real inner products of complex numbers), in the
+// combinations each variant needs:
+//   imex1: G00 + G10, G01 + G11, F0 + F1     ex: G00, G01, F0 + G10
+//   im:    G00, G01, G11, F0 + G10, F1       imex2: G00, G01, G10, G11, F0, F1
+template <int V>
+struct DlSums64 {
+  static constexpr int kN =
+      (V == OSSM_DLINOSS_IMEX1 || V == OSSM_DLINOSS_EX) ? 3 : (V == OSSM_DLINOSS_IM ? 5 : 6);
+};
+
+template <int V>
+__global__ __launch_bounds__(kBlock64) void dl64_forward_kernel(DlParams64 prm,
+                                                                const double2* __restrict__ bu,
+                                                                double2* __restrict__ states,
+                                                                int L, int nc) {
+  const int ch = static_cast<int>(blockIdx.x) * kBlock64 + static_cast<int>(threadIdx.x);
+  if (ch >= nc) return;
+  const int p = ch % prm.P;
+  const Coef64 k = dl64_coef<V>(prm.a[p], prm.g[p], prm.dt[p]);
+  double s0r = 0.0, s0i = 0.0, s1r = 0.0, s1i = 0.0;
+#pragma unroll 8
+  for (int t = 0; t < L; ++t) {
+    const size_t e = static_cast<size_t>(t) * nc + ch;
+    const double2 b = bu[e];
+    const double n0r = s0r * k.c0 + s1r * k.c1 + b.x * k.c2;
+    const double n0i = s0i * k.c0 + s1i * k.c1 + b.y * k.c2;
+    double n1r, n1i;
+    if constexpr (V == OSSM_DLINOSS_IMEX1) {
+      n1r = n0r + s1r;
+      n1i = n0i + s1i;
+    } else if constexpr (V == OSSM_DLINOSS_EX) {
+      n1r = s0r * k.c3 + s1r;
+      n1i = s0i * k.c3 + s1i;
+    } else {
+      n1r = s0r * k.c3 + s1r * k.c4 + b.x * k.c5;
+      n1i = s0i * k.c3 + s1i * k.c4 + b.y * k.c5;
+    }
+    s0r = n0r;
+    s0i = n0i;
+    s1r = n1r;
+    s1i = n1i;
+    states[2 * e] = make_double2(s0r, s0i);
+    states[2 * e + 1] = make_double2(s1r, s1i);
+  }
+}
+
+// Reverse adjoint per channel: mu_t = carry + (0, grad_out_t) (the upstream
+// gradient enters through x); grad_bu_t = f^T mu_t; carry to t-1 = M^T mu_t
+// (dlinoss_imex1.cpp:200-208, dlinoss_imex2.cpp:222-230, dlinoss_im.cpp:229-237,
+// dlinoss_ex.cpp:189-197).  Writes the channel's sums to part[ch * kN + i].
+template <int V>
+__global__ __launch_bounds__(kBlock64) void dl64_backward_kernel(
+    DlParams64 prm, const double2* __restrict__ bu, const double2* __restrict__ states,
+    const double2* __restrict__ gout, double2* __restrict__ gin, double* __restrict__ part, int L,
+    int nc) {
+  constexpr int NS = DlSums64<V>::kN;
+  const int ch = static_cast<int>(blockIdx.x) * kBlock64 + static_cast<int>(threadIdx.x);
+  if (ch >= nc) return;
+  const int p = ch % prm.P;
+  const Coef64 k = dl64_coef<V>(prm.a[p], prm.g[p], prm.dt[p]);
+  double c0r = 0.0, c0i = 0.0, c1r = 0.0, c1i = 0.0;  // carry: gradient w.r.t. s_t
+  double acc[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) acc[i] = 0.0;
+  for (int t = L - 1; t >= 0; --t) {
+    const size_t e = static_cast<size_t>(t) * nc + ch;
+    const double2 go = gout[e], b = bu[e];
+    const double m0r = c0r, m0i = c0i, m1r = c1r + go.x, m1i = c1i + go.y;
+    double2 sp0 = make_double2(0.0, 0.0), sp1 = sp0;  // s_{t-1} (zero before the first step)
+    if (t > 0) {
+      sp0 = states[2 * (e - nc)];
+      sp1 = states[2 * (e - nc) + 1];
+    }
+    if constexpr (V == OSSM_DLINOSS_IMEX1) {
+      const double tr = m0r + m1r, ti = m0i + m1i;
+      acc[0] += tr * sp0.x + ti * sp0.y;
+      acc[1] += tr * sp1.x + ti * sp1.y;
+      acc[2] += tr * b.x + ti * b.y;
+      gin[e] = make_double2(tr * k.c2, ti * k.c2);
+      c0r = tr * k.c0;
+      c0i = ti * k.c0;
+      c1r = m1r + tr * k.c1;
+      c1i = m1i + ti * k.c1;
+    } else if constexpr (V == OSSM_DLINOSS_EX) {
+      acc[0] += m0r * sp0.x + m0i * sp0.y;
+      acc[1] += m0r * sp1.x + m0i * sp1.y;
+      acc[2] += m0r * b.x + m0i * b.y + m1r * sp0.x + m1i * sp0.y;
+      gin[e] = make_double2(m0r * k.c2, m0i * k.c2);
+      c0r = m0r * k.c0 + m1r * k.c3;
+      c0i = m0i * k.c0 + m1i * k.c3;
+      c1r = m0r * k.c1 + m1r;
+      c1i = m0i * k.c1 + m1i;
+    } else {
+      if constexpr (V == OSSM_DLINOSS_IM) {
+        acc[0] += m0r * sp0.x + m0i * sp0.y;
+        acc[1] += m0r * sp1.x + m0i * sp1.y;
+        acc[2] += m1r * sp1.x + m1i * sp1.y;
+        acc[3] += m0r * b.x + m0i * b.y + m1r * sp0.x + m1i * sp0.y;
+        acc[4] += m1r * b.x + m1i * b.y;
+      } else {
+        acc[0] += m0r * sp0.x + m0i * sp0.y;
+        acc[1] += m0r * sp1.x + m0i * sp1.y;
+        acc[2] += m1r * sp0.x + m1i * sp0.y;
+        acc[3] += m1r * sp1.x + m1i * sp1.y;
+        acc[4] += m0r * b.x + m0i * b.y;
+        acc[5] += m1r * b.x + m1i * b.y;
+      }
+      gin[e] = make_double2(m0r * k.c2 + m1r * k.c5, m0i * k.c2 + m1i * k.c5);
+      c0r = m0r * k.c0 + m1r * k.c3;
+      c0i = m0i * k.c0 + m1i * k.c3;
+      c1r = m0r * k.c1 + m1r * k.c4;
+      c1i = m0i * k.c1 + m1i * k.c4;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NS; ++i) part[static_cast<size_t>(ch) * NS + i] = acc[i];
+}
+
+// One lane per oscillator p: the channel sums of the B batch rows added in
+// row order, then the chain rule to (a, g, dt) — imex1 dlinoss_imex1.cpp:219-232,
+// im dlinoss_im.cpp:236-263, imex2 / ex by differentiating the coefficient
+// tables (the terms the reference accumulates per step).
+template <int V>
+__global__ __launch_bounds__(kBlock64) void dl64_param_kernel(DlParams64 prm,
+                                                              const double* __restrict__ part,
+                                                              double* __restrict__ grad_a,
+                                                              double* __restrict__ grad_g,
+                                                              double* __restrict__ grad_step,
+                                                              int B) {
+  constexpr int NS = DlSums64<V>::kN;
+  const int p = static_cast<int>(blockIdx.x) * kBlock64 + static_cast<int>(threadIdx.x);
+  if (p >= prm.P) return;
+  double S[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) S[i] = 0.0;
+  for (int b = 0; b < B; ++b) {
+    const double* src = part + (static_cast<size_t>(b) * prm.P + p) * NS;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) S[i] += src[i];
+  }
+  const double a = prm.a[p], g = prm.g[p], dt = prm.dt[p];
+  double ga, gg, gs;
+  if constexpr (V == OSSM_DLINOSS_IMEX1) {
+    const double inv = 1.0 / (1.0 + dt * g);
+    const double s2i = dt * dt * inv;
+    const double gs2i = S[2] - a * S[1];
+    ga = -s2i * S[1];
+    const double inv_total = S[0] + gs2i * dt * dt;
+    gs = gs2i * (2.0 * dt * inv) - inv_total * g * inv * inv;
+    gg = -inv_total * dt * inv * inv;
+  } else if constexpr (V == OSSM_DLINOSS_IMEX2) {
+    ga = -dt * S[1] - dt * dt * S[3];
+    gg = -dt * S[0] - dt * dt * S[2];
+    gs = -g * S[0] - a * S[1] + (1.0 - 2.0 * dt * g) * S[2] - 2.0 * dt * a * S[3] + S[4] +
+         2.0 * dt * S[5];
+  } else if constexpr (V == OSSM_DLINOSS_IM) {
+    const double inv = 1.0 / (1.0 + dt * g + dt * dt * a);
+    const double si = dt * inv;
+    const double gsi = S[3] - a * S[1];
+    double ginv = S[0] + S[2] * (1.0 + dt * g);
+    const double gt = S[2] * inv;
+    ga = -si * S[1];
+    gg = gt * dt;
+    gs = gt * g + gsi * inv + S[4] * (2.0 * dt * inv);
+    ginv += gsi * dt + S[4] * dt * dt;
+    const double gden = -ginv * inv * inv;
+    ga += gden * dt * dt;
+    gg += gden * dt;
+    gs += gden * (g + 2.0 * dt * a);
+  } else {
+    ga = -dt * S[1];
+    gg = -dt * S[0];
+    gs = -g * S[0] - a * S[1] + S[2];
+  }
+  grad_a[p] = ga;
+  grad_g[p] = gg;
+  grad_step[p] = gs;
+}
+
 unsigned blocks_for(long long n) { return static_cast<unsigned>((n + kBlock64 - 1) / kBlock64); }
 
 struct Shape64 {
@@ -505,6 +724,97 @@ int ossm_linoss_backward_f64(const void* m11, const void* m12, const void* m21, 
                      static_cast<const double*>(raw), static_cast<double*>(grad_m), n_m,
                      static_cast<int>(batch), static_cast<int>(n_m));
   return launch_check("sdl64_rows_sum_kernel");
+}
+
+int ossm_dlinoss_forward_f64(int variant, const double* a_diag, const double* g_diag,
+                             const double* step, const void* bu, void* states, int64_t length,
+                             int64_t batch, int64_t ssm, ossm_stream_t stream_v) {
+  clear_error();
+  if (variant < OSSM_DLINOSS_IMEX1 || variant > OSSM_DLINOSS_EX)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "Unknown D-LinOSS variant code");
+  if (length < 0 || batch < 0 || ssm < 0)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "dlinoss_forward_f64: negative size");
+  if (length == 0 || batch == 0 || ssm == 0) return OSSM_OK;
+  if (length > INT_MAX / 2 || batch * ssm > INT_MAX / 2 || length * batch * ssm > (int64_t(1) << 40))
+    return set_error(OSSM_ERR_UNSUPPORTED, "dlinoss_forward_f64: size exceeds 32-bit indexing");
+  if (!a_diag || !g_diag || !step || !bu || !states)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "dlinoss_forward_f64: null pointer");
+  const DlParams64 prm{a_diag, g_diag, step, static_cast<int>(ssm)};
+  const int nc = static_cast<int>(batch * ssm), L = static_cast<int>(length);
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  const auto* b = static_cast<const double2*>(bu);
+  auto* st = static_cast<double2*>(states);
+  switch (variant) {
+#define OSSM_DL64_FWD(V)                                                                         \
+  case V:                                                                                        \
+    hipLaunchKernelGGL(dl64_forward_kernel<V>, dim3(blocks_for(nc)), dim3(kBlock64), 0, stream, \
+                       prm, b, st, L, nc);                                                       \
+    break;
+    OSSM_DL64_FWD(OSSM_DLINOSS_IMEX1)
+    OSSM_DL64_FWD(OSSM_DLINOSS_IMEX2)
+    OSSM_DL64_FWD(OSSM_DLINOSS_IM)
+    OSSM_DL64_FWD(OSSM_DLINOSS_EX)
+#undef OSSM_DL64_FWD
+  }
+  return launch_check("dl64_forward_kernel");
+}
+
+int ossm_dlinoss_backward_f64(int variant, const double* a_diag, const double* g_diag,
+                              const double* step, const void* bu, const void* states,
+                              const void* grad_output, double* grad_a, double* grad_g,
+                              double* grad_step, void* grad_bu, int64_t length, int64_t batch,
+                              int64_t ssm, ossm_stream_t stream_v) {
+  clear_error();
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  StreamCall call(stream);
+  if (call.status()) return call.status();
+  if (variant < OSSM_DLINOSS_IMEX1 || variant > OSSM_DLINOSS_EX)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "Unknown D-LinOSS variant code");
+  if (length < 0 || batch < 0 || ssm < 0)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "dlinoss_backward_f64: negative size");
+  if (ssm == 0) return OSSM_OK;
+  if (!grad_a || !grad_g || !grad_step)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "dlinoss_backward_f64: null pointer");
+  if (length == 0 || batch == 0) {
+    // nothing to scan: zero parameter gradients (the reference's zeros_like)
+    double* const outs[3] = {grad_a, grad_g, grad_step};
+    for (double* o : outs) {
+      hipLaunchKernelGGL(sdl64_zero_kernel, dim3(blocks_for(ssm)), dim3(kBlock64), 0, stream, o,
+                         static_cast<long long>(ssm));
+      if (int rc = launch_check("sdl64_zero_kernel")) return rc;
+    }
+    return OSSM_OK;
+  }
+  if (length > INT_MAX / 2 || batch * ssm > INT_MAX / 2 || length * batch * ssm > (int64_t(1) << 40))
+    return set_error(OSSM_ERR_UNSUPPORTED, "dlinoss_backward_f64: size exceeds 32-bit indexing");
+  if (!a_diag || !g_diag || !step || !bu || !states || !grad_output || !grad_bu)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, "dlinoss_backward_f64: null pointer");
+  const DlParams64 prm{a_diag, g_diag, step, static_cast<int>(ssm)};
+  const int nc = static_cast<int>(batch * ssm), L = static_cast<int>(length);
+  void* raw = nullptr;
+  if (int rc = acquire_workspace(call, static_cast<size_t>(nc) * 6 * sizeof(double), &raw)) return rc;
+  auto* part = static_cast<double*>(raw);
+  const auto* b = static_cast<const double2*>(bu);
+  const auto* st = static_cast<const double2*>(states);
+  const auto* go = static_cast<const double2*>(grad_output);
+  auto* gi = static_cast<double2*>(grad_bu);
+  const int B = static_cast<int>(batch);
+  switch (variant) {
+#define OSSM_DL64_BWD(V)                                                                          \
+  case V:                                                                                         \
+    hipLaunchKernelGGL(dl64_backward_kernel<V>, dim3(blocks_for(nc)), dim3(kBlock64), 0, stream, \
+                       prm, b, st, go, gi, part, L, nc);                                          \
+    if (int rc = launch_check("dl64_backward_kernel")) return rc;                                 \
+    hipLaunchKernelGGL(dl64_param_kernel<V>, dim3(blocks_for(ssm)), dim3(kBlock64), 0, stream,   \
+                       prm, part, grad_a, grad_g, grad_step, B);                                  \
+    break;
+    OSSM_DL64_BWD(OSSM_DLINOSS_IMEX1)
+    OSSM_DL64_BWD(OSSM_DLINOSS_IMEX2)
+    OSSM_DL64_BWD(OSSM_DLINOSS_IM)
+    OSSM_DL64_BWD(OSSM_DLINOSS_EX)
+#undef OSSM_DL64_BWD
+  }
+  return launch_check("dl64_param_kernel");
 }
 
 }  // extern "C"

@@ -90,11 +90,36 @@ def test_dlinoss_layer_outputs_and_grads(bridge, variant, shape):
                                    atol=1e-4 * max(1.0, float(r.grad.abs().max())), err_msg=name)
 
 
-def test_dlinoss_bridge_rejects_fp64_and_bad_variant(bridge):
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_dlinoss_bridge_fp64_runs_complex128_kernels(bridge, variant):
+    """float64 coefficients select the complex128 kernels (the reference's
+    precision rule, _dlinoss_scan.py:35-48): the layer's outputs and every
+    gradient against autograd of the brute fp64 loop, at rtol 1e-9."""
+    Bsz, L, P, H = 2, 60, 6, 5
+    announce(f"bridge dlinoss fp64 {variant}")
+    params = [p.double() for p in _layer_params(P, H, seed=17)]
+    u = torch.randn(Bsz, L, H, generator=torch.Generator().manual_seed(18), dtype=torch.float64)
+    w = torch.randn(Bsz, L, H, generator=torch.Generator().manual_seed(19), dtype=torch.float64)
+    dev = [p.cuda().requires_grad_() for p in params]
+    y = _dlinoss_layer(bridge.run_dlinoss, variant, *dev, u.cuda())
+    assert y.dtype == torch.float64
+    (y * w.cuda()).sum().backward()
+    ref = [p.clone().requires_grad_() for p in params]
+
+    def brute(variant, a, g, dt, bu):
+        return _brute.dlinoss_states(variant, a, g, dt, bu)[..., 1]
+
+    y64 = _dlinoss_layer(brute, variant, *ref, u)
+    (y64 * w).sum().backward()
+    np.testing.assert_allclose(y.detach().cpu().numpy(), y64.detach().numpy(), rtol=1e-9, atol=1e-11)
+    for got, r, name in zip(dev, ref, ("A", "G", "steps", "B", "C", "D")):
+        np.testing.assert_allclose(got.grad.cpu().numpy(), r.grad.numpy(), rtol=1e-9,
+                                   atol=1e-11 * max(1.0, float(r.grad.abs().max())), err_msg=name)
+
+
+def test_dlinoss_bridge_rejects_bad_variant(bridge):
     x = torch.zeros(4, 1, 2, dtype=torch.complex128, device="cuda")
     p = torch.ones(2, dtype=torch.float64, device="cuda")
-    with pytest.raises(RuntimeError, match="float32"):
-        bridge.run_dlinoss("imex1", p, p, p, x)
     with pytest.raises(ValueError, match="Unknown D-LinOSS variant"):
         bridge.run_dlinoss("nope", p, p, p, x)
     assert bridge.has_kernels() and bridge.has_kernels("im")
@@ -262,6 +287,12 @@ def test_dlinoss_torch_library_ops_opcheck(bridge, variant):
     torch.library.opcheck(fwd, (a, gg, dt, bu))
     states = fwd(a, gg, dt, bu)
     torch.library.opcheck(bwd, (a, gg, dt, bu, states, go))
+    # complex128 with float64 coefficients, as the reference's dispatcher takes
+    d64 = [t.double() for t in (a, gg, dt)] + [bu.to(torch.complex128)]
+    torch.library.opcheck(fwd, tuple(d64))
+    st64 = fwd(*d64)
+    assert st64.dtype == torch.complex128
+    torch.library.opcheck(bwd, (*d64, st64, go.to(torch.complex128)))
     eager = bridge.run_dlinoss(variant, a, gg, dt, bu)
     compiled = torch.compile(lambda *xs: bridge.run_dlinoss(variant, *xs), backend="aot_eager",
                              fullgraph=True)

@@ -116,6 +116,58 @@ def test_dlinoss_rejects_bad_inputs(K):
         K.dlinoss_imex1_forward(to_dev(a), to_dev(g), to_dev(dt), to_dev(bu).transpose(0, 1))
 
 
+# complex128: the reference dispatcher's other complex type (AT_DISPATCH_COMPLEX_TYPES,
+# dlinoss_imex1_cuda.cu:196, 234), coefficients float64
+F64_SHAPES = [(1, 1, 1), (2, 3, 5), (129, 2, 33), (1000, 3, 70), (300, 5, 130)]
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("shape", F64_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_dlinoss_complex128_vs_fp64_oracle(K, variant, shape):
+    """complex128 forward and backward against the oracle's fp64 restatement
+    of the reference kernels, elementwise at rtol 1e-10 (parameter gradients
+    with atol 1e-10 x their magnitude: sums over B*L terms)."""
+    L, B, P = shape
+    a, g, dt, bu, go = dlinoss_inputs(L, B, P, seed=3 * L + B + 5 * P, variant=variant)
+    a, g, dt = (x.astype(np.float64) for x in (a, g, dt))
+    rng = np.random.default_rng(L + B + P)
+    bu = bu.astype(np.complex128) + 1e-3 * rng.normal(size=bu.shape)  # beyond fp32's values
+    go = go.astype(np.complex128)
+    announce(f"dlinoss complex128 {variant} L={L} B={B} P={P}")
+    st = _fwd(K, variant, a, g, dt, bu)
+    assert st.dtype == torch.complex128
+    ga, gg, gs, gb = _bwd(K, variant, a, g, dt, bu, st, go)
+    assert ga.dtype == torch.float64 and gb.dtype == torch.complex128
+    ref = oracle.dlinoss_forward(variant, a, g, dt, bu)
+    rga, rgg, rgs, rgb = oracle.dlinoss_backward(variant, a, g, dt, bu, ref, go)
+    np.testing.assert_allclose(to_np(st), ref, rtol=1e-10, atol=1e-12, err_msg="states")
+    np.testing.assert_allclose(to_np(gb), rgb, rtol=1e-10, atol=1e-12, err_msg="grad_bu")
+    for got, r, key in ((ga, rga, "grad_a"), (gg, rgg, "grad_g"), (gs, rgs, "grad_step")):
+        np.testing.assert_allclose(to_np(got), r, rtol=1e-10,
+                                   atol=1e-10 * max(1.0, float(np.abs(r).max())), err_msg=key)
+    no_device_errors()
+
+
+def test_dlinoss_complex128_dtype_rules(K):
+    """The reference's data_ptr<value_t> rules: complex128 bu needs float64
+    coefficients and complex128 states / grad_output; other bu types are not
+    dispatched; L = 0 gives zero float64 gradients."""
+    a, g, dt, bu, go = dlinoss_inputs(6, 2, 3, seed=4)
+    a64, g64, d64 = (to_dev(x.astype(np.float64)) for x in (a, g, dt))
+    bu64 = to_dev(bu.astype(np.complex128))
+    with pytest.raises(RuntimeError, match="expected scalar type Double but found Float"):
+        K.dlinoss_imex1_forward(to_dev(a), g64, d64, bu64)
+    with pytest.raises(RuntimeError, match="expected scalar type Float but found Double"):
+        K.dlinoss_imex1_forward(a64, g64, d64, to_dev(bu))
+    with pytest.raises(RuntimeError, match="not implemented for 'Float'"):
+        K.dlinoss_imex1_forward(a64, g64, d64, to_dev(bu.real.copy()))
+    st = K.dlinoss_imex1_forward(a64, g64, d64, bu64)
+    with pytest.raises(RuntimeError, match="expected scalar type ComplexDouble but found ComplexFloat"):
+        K.dlinoss_imex1_backward(a64, g64, d64, bu64, st, to_dev(go))
+    grads = K.dlinoss_imex1_backward(a64, g64, d64, bu64[:0], st[:0], to_dev(go.astype(np.complex128))[:0])
+    assert all(t.dtype == torch.float64 and float(t.abs().sum()) == 0 for t in grads[:3])
+
+
 @pytest.mark.parametrize("variant", ["imex1", "im"])
 def test_dlinoss_config2_full_size(K, variant):
     """BASELINE config 2 shape (B=32, L=4096, P=128): every channel of a slice

@@ -36,7 +36,8 @@ def test_header_declares_the_entry_points():
               "ossm_device_error_bits", "ossm_selective_forward_bf16",
               "ossm_selective_backward_bf16", "ossm_sdlinoss_forward", "ossm_sdlinoss_backward",
               "ossm_sdlinoss_forward_f64", "ossm_sdlinoss_backward_f64",
-              "ossm_linoss_forward_f64", "ossm_linoss_backward_f64",
+              "ossm_linoss_forward_f64", "ossm_linoss_backward_f64", "ossm_dlinoss_forward_f64",
+              "ossm_dlinoss_backward_f64",
               "ossm_diag_scan_forward", "ossm_diag_scan_backward", "ossm_diag_scan_forward_f64",
               "ossm_diag_scan_backward_f64", "ossm_dlinoss_layer_forward", "ossm_dlinoss_layer_backward",
               "ossm_selective_mamba_forward", "ossm_selective_mamba_backward",
@@ -56,7 +57,7 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     # every declared symbol has a ctypes signature in the binding
     assert set(_declared_functions()) == set(_lib.EXPORTED)
-    assert _lib.load().ossm_abi_version() == 12
+    assert _lib.load().ossm_abi_version() == 13
 
 
 def test_dropin_module_has_every_reference_name():
