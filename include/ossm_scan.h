@@ -22,11 +22,17 @@
  * the kernels, after synchronising the stream) and live until process exit.
  *
  * Threads and graphs: a call holds its (device, stream) from the launch
- * bookkeeping (look-back tag, ticket base, workspace) through its last
- * launch, so calls from several host threads on one stream are safe and
- * reach the stream whole.  A call whose stream is being captured into a HIP
- * graph returns OSSM_ERR_UNSUPPORTED before enqueuing anything: the tag and
- * ticket base are chosen on the host per call, and a replay would reuse them.
+ * bookkeeping (scratch, workspace) through its last launch, so calls from
+ * several host threads on one stream are safe and reach the stream whole.
+ * Each look-back launch draws its chunk order and record tag on the device
+ * from the scratch's ticket counter, so a call may be captured into a HIP
+ * graph and the graph replayed.  Under capture the scratch and workspace are
+ * used as they are: a call that would need them to grow returns
+ * OSSM_ERR_UNSUPPORTED before enqueuing anything (run it once eagerly on the
+ * stream first), as does OSSM_SCAN_ORDER=dispatch (host-chosen tags).
+ * Buffers a graph captured are never freed.  Replays use the capture
+ * stream's scratch: replay the graph on that stream, or ordered with
+ * everything else that uses it.
  */
 #ifndef OSSM_SCAN_H
 #define OSSM_SCAN_H
@@ -60,11 +66,24 @@ const char* ossm_last_error(void);
  * Synchronises `stream` and returns (then clears) the device-side error bits
  * of its scratch buffer: bit 0 = a look-back wait gave up (bounded spin
  * exceeded), bit 1 = a workgroup drew an out-of-range ticket.  0 means every
- * launch on this stream since the last check completed its protocol.  Once
+ * launch on this stream since the last check completed its protocol.  Either
+ * failure also makes the affected outputs NaN (the chunk carries that could
+ * not be read are NaN), so a failed protocol never returns plausible values.  Once
  * ossm_dlinoss_forward_noalloc has run on the current device, the device is
  * synchronised and the bits of its fixed array are included too.
  */
 uint32_t ossm_device_error_bits(ossm_stream_t stream);
+
+/*
+ * Test hook, no counterpart in the reference: synchronises `stream` and adds
+ * `delta` to the ticket counter of its scratch, as a launch that did not run
+ * to its end would leave it.  The next look-back launches on the stream then
+ * draw out-of-range tickets: they raise bit 1 of ossm_device_error_bits and
+ * their carries are NaN, while every kernel still exits normally;
+ * ossm_device_error_bits puts the counter back in step.  For tests of the
+ * failure path only.
+ */
+int ossm_test_skew_tickets(ossm_stream_t stream, uint64_t delta);
 
 /*
  * D-LinOSS forward, replaces dlinoss_<v>_forward:
@@ -88,8 +107,9 @@ int ossm_dlinoss_forward(int variant, const float* a_diag, const float* g_diag,
  * (L*B*P) per call; larger problems return OSSM_ERR_UNSUPPORTED with a
  * message.  Every call on a GPU shares that array: calls that overlap on one
  * GPU (two streams, or two host threads' streams) race and must be ordered by
- * the caller.  Refuses HIP-graph capture like the other entry points.  Its
- * device error bits are reported by ossm_device_error_bits.
+ * the caller.  May be captured into a HIP graph once it has run eagerly on the
+ * device (the first call looks up the array's address).  Its device error
+ * bits are reported by ossm_device_error_bits.
  */
 int ossm_dlinoss_forward_noalloc(int variant, const float* a_diag, const float* g_diag,
                                  const float* step, const void* bu, void* states,

@@ -24,6 +24,7 @@ _dp = ctypes.c_void_p  # double* passed as raw device addresses
 
 _SIGNATURES = {
     "ossm_abi_version": (ctypes.c_int, []),
+    "ossm_test_skew_tickets": (ctypes.c_int, [_vp, ctypes.c_uint64]),
     "ossm_last_error": (ctypes.c_char_p, []),
     "ossm_device_error_bits": (ctypes.c_uint32, [_vp]),
     "ossm_dlinoss_forward": (

@@ -212,10 +212,14 @@ __device__ __forceinline__ bool drec_decode(const unsigned long long (&w)[kRecWo
 // ... and composing their aggregates with lam_c (the chunk transition) until
 // an inclusive prefix is found.  Every predecessor drew an earlier ticket, so
 // it is resident and publishes its aggregate without waiting: the walk ends.
-// The spin is still bounded; giving up raises kErrSpinTimeout.
+// The spin is still bounded; giving up raises kErrSpinTimeout and returns a
+// NaN carry, as does a poisoned launch.
 template <class V>
 __device__ V diag_lookback(unsigned long long* rec, int c, int dir, int n_chunks, int nc, int ch,
                            V lam_c, const LaunchSync& sync) {
+  using R = typename RealOf<V>::R;
+  const V nan_carry = cx(R(__builtin_nan("")), R(__builtin_nan("")));
+  if (sync.poison) return nan_carry;
   V acc = cx_zero<V>();
   V pw = cx_one<V>();
   int j = c - dir;
@@ -234,7 +238,7 @@ __device__ V diag_lookback(unsigned long long* rec, int c, int dir, int n_chunks
     }
     if (++spins > kSpinLimit) {
       __hip_atomic_fetch_or(sync.err, kErrSpinTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return acc;
+      return nan_carry;
     }
     __builtin_amdgcn_s_sleep(2);
   }
@@ -265,7 +269,6 @@ __global__ __launch_bounds__(W * kWave) void diag_forward_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int w = wave_id();
   const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
-  if (ticket < 0) return;
   const int c = ticket / n_groups;
   const int g = ticket - c * n_groups;
   const int ch = g * kWave + lane;
@@ -361,7 +364,6 @@ __global__ __launch_bounds__(W * kWave) void diag_backward_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int w = wave_id();
   const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
-  if (ticket < 0) return;
   if (ticket == 0) zero_fill_block(zero);  // grad_lambda, for column_sum_kernel
   const int cr = ticket / n_groups;
   const int g = ticket - cr * n_groups;
@@ -529,7 +531,7 @@ int diag_forward_impl(const R* lam_re, const R* lam_im, const void* b_seq, void*
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * CxOf<R>::kWords * nc * sizeof(unsigned long long);
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
   bool launched = false;
 #define OSSM_LAUNCH_DIAG_FWD(TT, WW)                                                              \
   if (!launched && tile.T == TT && tile.W == WW) {                                                \
@@ -546,14 +548,8 @@ int diag_forward_impl(const R* lam_re, const R* lam_im, const void* b_seq, void*
     OSSM_DIAG_TILES_F64(OSSM_LAUNCH_DIAG_FWD)
   }
 #undef OSSM_LAUNCH_DIAG_FWD
-  if (!launched) {
-    release_unlaunched(call, total);
-    return set_error(OSSM_ERR_UNSUPPORTED, std::string(DiagDefaults<R>::kEnvFwd) + " names no built tile");
-  }
-  if (int rc = launch_check("diag_forward_kernel")) {
-    release_unlaunched(call, total);
-    return rc;
-  }
+  if (!launched) return set_error(OSSM_ERR_UNSUPPORTED, std::string(DiagDefaults<R>::kEnvFwd) + " names no built tile");
+  if (int rc = launch_check("diag_forward_kernel")) return rc;
   return OSSM_OK;
 }
 
@@ -578,7 +574,7 @@ int diag_backward_impl(const R* lam_re, const R* lam_im, const void* states, con
   R* partials = static_cast<R*>(ws);
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
   const ZeroFill zero{{reinterpret_cast<float*>(grad_lambda), nullptr, nullptr},
                       static_cast<int>(2 * P * (sizeof(R) / sizeof(float)))};
   bool launched = false;
@@ -598,14 +594,8 @@ int diag_backward_impl(const R* lam_re, const R* lam_im, const void* states, con
     OSSM_DIAG_TILES_F64(OSSM_LAUNCH_DIAG_BWD)
   }
 #undef OSSM_LAUNCH_DIAG_BWD
-  if (!launched) {
-    release_unlaunched(call, total);
-    return set_error(OSSM_ERR_UNSUPPORTED, std::string(DiagDefaults<R>::kEnvBwd) + " names no built tile");
-  }
-  if (int rc = launch_check("diag_backward_kernel")) {
-    release_unlaunched(call, total);
-    return rc;
-  }
+  if (!launched) return set_error(OSSM_ERR_UNSUPPORTED, std::string(DiagDefaults<R>::kEnvBwd) + " names no built tile");
+  if (int rc = launch_check("diag_backward_kernel")) return rc;
   return launch_column_sums<2>(partials, P, B, n_chunks, DiagEpilogue<R>{grad_lambda}, stream);
 }
 

@@ -226,7 +226,6 @@ void dlinoss_layer_fwd_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int w = wave_id();
   const int ticket = launch_order(sync, A.Bsz * A.n_chunks, &s_ticket);
-  if (ticket < 0) return;
   const int c = ticket / A.Bsz;  // every chunk-(c-1) workgroup holds an earlier ticket
   const int b = ticket - c * A.Bsz;
   const int t0 = c * kLc;
@@ -509,7 +508,6 @@ __global__ __launch_bounds__(kLayerThreads) void dlinoss_layer_bwd_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int w = wave_id();
   const int ticket = launch_order(sync, A.Bsz * A.n_chunks, &s_ticket);
-  if (ticket < 0) return;
   if (ticket == 0) zero_fill_block(A.zero);
   const int cr = ticket / A.Bsz;     // chunks in reverse time order
   const int c = A.n_chunks - 1 - cr;
@@ -801,10 +799,9 @@ int launch_layer_bwd(LayerBwdArgs args, float* ga, float* gg, float* gs, hipStre
                                              static_cast<int>(lds)),
                          "hipFuncSetAttribute"))
     return rc;
-  if (int rc = acquire_scratch(call, rec_bytes, n_wg, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(n_wg)), dim3(kLayerThreads), lds, stream, args,
                      static_cast<unsigned long long*>(payload), sync);
-  if (hipPeekAtLastError() != hipSuccess) release_unlaunched(call, n_wg);
   if (int rc = launch_check("dlinoss_layer_bwd_kernel")) return rc;
   if (args.P == 0) return OSSM_OK;
   const typename Model::Params prm{args.a, args.g, args.dt, args.P};
@@ -844,10 +841,9 @@ int launch_layer(const LayerArgs& args, hipStream_t stream) {
                                              static_cast<int>(lds)),
                          "hipFuncSetAttribute"))
     return rc;
-  if (int rc = acquire_scratch(call, rec_bytes, n_wg, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(n_wg)), dim3(kLayerThreads), lds, stream, args,
                      static_cast<unsigned long long*>(payload), sync);
-  if (hipPeekAtLastError() != hipSuccess) release_unlaunched(call, n_wg);
   return launch_check("dlinoss_layer_fwd_kernel");
 }
 

@@ -130,7 +130,6 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_forward_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int w = wave_id();
   const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
-  if (ticket < 0) return;
   const int c = ticket / n_groups;
   const int g = ticket - c * n_groups;
   const int ch = g * kWave + lane;
@@ -507,7 +506,6 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
   __shared__ float4 s_sp[W][kSlots][kWave];
   __shared__ int s_ticket;
   const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
-  if (ticket < 0) return;
   if (ticket == 0) zero_fill_block(zero);  // the parameter-gradient outputs, for column_sum_kernel
   const BwdTicket k = bwd_ticket<T, W>(ticket, n_groups, n_chunks, nc);
   BwdBuf<Model, T> b;
@@ -634,11 +632,8 @@ int launch_forward(const typename Model::Params& prm, const void* in, void* out,
     return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(call, pl.rec_bytes, pl.total, &payload, &sync)) return rc;
-  if (int rc = enqueue_forward<Model>(pl, prm, in, out, L, nc, stream, payload, sync)) {
-    release_unlaunched(call, pl.total);
-    return rc;
-  }
+  if (int rc = acquire_scratch(call, pl.rec_bytes, &payload, &sync)) return rc;
+  if (int rc = enqueue_forward<Model>(pl, prm, in, out, L, nc, stream, payload, sync)) return rc;
   return OSSM_OK;
 }
 
@@ -685,7 +680,7 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   const int64_t total = n_chunks * n_groups;
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
   const ZeroFill zero{{out0, out1, out2}, static_cast<int>(Model::kOutsPerColumn * P)};
   bool launched = false;
 #define OSSM_LAUNCH_BWD(TT, WW, OO, HH, SS)                                                      \
@@ -701,18 +696,12 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
                        static_cast<int>(nc), static_cast<int>(n_groups),                         \
                        static_cast<int>(n_chunks), static_cast<unsigned long long*>(payload),    \
                        sync);                                                                    \
-    if (int rc = launch_check("osc_backward_kernel")) {                                          \
-      release_unlaunched(call, total);                                                       \
-      return rc;                                                                                 \
-    }                                                                                            \
+    if (int rc = launch_check("osc_backward_kernel")) return rc;                        \
     launched = true;                                                                             \
   }
   OSSM_BWD_TILES(OSSM_LAUNCH_BWD)
 #undef OSSM_LAUNCH_BWD
-  if (!launched) {
-    release_unlaunched(call, total);
-    return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_BWD names no built tile");
-  }
+  if (!launched) return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_BWD names no built tile");
   return launch_column_sums<NS>(red.partials, P, B, n_chunks,
                                 OscEpilogue<Model>{prm, out0, out1, out2}, stream);
 }
@@ -747,7 +736,9 @@ int dlinoss_backward_v(const float* a, const float* g, const float* dt, const vo
 // 256-byte header (the launch-ticket counter at kHdrTicket, the error bits at
 // kHdrErr) and kNoAllocRecordBytes of tagged records.  Device memory is
 // zero at load, which is the state the protocol starts from (tag 0 is never a
-// launch's tag, the ticket counter matches the host's count of 0).  Each GPU
+// launch's tag, and a launch starts with the ticket counter at a multiple of
+// 2^32).  The launch's order and tag come from that counter on the device,
+// so the call can be captured into a HIP graph and replayed.  Each GPU
 // holds its own copy until the process ends; its address on a device comes
 // from hipGetSymbolAddress, taken once per device on that device's first
 // call.  The array is per process and per GPU: every call of this process on
@@ -764,8 +755,7 @@ constexpr int kNoAllocMaxDevices = 64;
 struct NoAllocDevice {
   std::mutex mu;                        // held from bookkeeping through the launch
   char* ptr = nullptr;                  // device address of `scratch` on this device
-  unsigned int epoch = 0;               // tag of the most recent launch
-  unsigned long long next_ticket = 0;   // device ticket counter after all queued launches
+  unsigned int epoch = 0;               // tag of the most recent dispatch-order launch
 };
 NoAllocDevice g_noalloc[kNoAllocMaxDevices];
 
@@ -793,7 +783,10 @@ uint32_t noalloc_error_bits(int dev) {
   if (hipMemcpy(&bits, s.ptr + kHdrErr, sizeof(bits), hipMemcpyDeviceToHost) != hipSuccess ||
       hipMemcpy(&t, s.ptr + kHdrTicket, sizeof(t), hipMemcpyDeviceToHost) != hipSuccess)
     return 0xffffffffu;
-  if (scan_order_by_ticket()) s.next_ticket = t;  // every workgroup drew exactly one ticket
+  if ((t & (kEpochSpan - 1)) != 0) {  // a launch that did not run to its end: realign
+    t = (t | (kEpochSpan - 1)) + 1;
+    (void)hipMemcpy(s.ptr + kHdrTicket, &t, sizeof(t), hipMemcpyHostToDevice);
+  }
   if (bits != 0) {
     const uint32_t zero = 0;
     (void)hipMemcpy(s.ptr + kHdrErr, &zero, sizeof(zero), hipMemcpyHostToDevice);
@@ -848,25 +841,34 @@ int ossm_dlinoss_forward_noalloc(int variant, const float* a_diag, const float* 
     return set_error(OSSM_ERR_UNSUPPORTED, "dlinoss_forward_noalloc: device index above 63");
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   const hipError_t ce = hipStreamIsCapturing(stream, &cap);
-  if (ce != hipSuccess || cap != hipStreamCaptureStatusNone) {
+  if (ce != hipSuccess) {
     (void)hipGetLastError();
-    return set_error(OSSM_ERR_UNSUPPORTED,
-                     "dlinoss_forward_noalloc: the stream is being captured into a HIP graph; the "
-                     "launch tag and ticket base are chosen on the host per call: run it eagerly");
+    return set_error(OSSM_ERR_HIP, std::string("hipStreamIsCapturing: ") + hipGetErrorString(ce));
   }
+  const bool capturing = cap != hipStreamCaptureStatusNone;
+  if (capturing && (cap != hipStreamCaptureStatusActive || !scan_order_by_ticket()))
+    return set_error(OSSM_ERR_UNSUPPORTED,
+                     "dlinoss_forward_noalloc: HIP-graph capture needs an active capture and ticket "
+                     "order (OSSM_SCAN_ORDER=dispatch chooses tags on the host per call)");
   NoAllocDevice& s = g_noalloc[dev];
   std::lock_guard<std::mutex> hold(s.mu);
+  if (capturing && s.ptr == nullptr)
+    return set_error(OSSM_ERR_UNSUPPORTED,
+                     "dlinoss_forward_noalloc: call it once eagerly on this device before capturing "
+                     "it (the first call looks up the fixed array's address)");
   if (int rc = noalloc_address(dev)) return rc;
   const bool by_ticket = scan_order_by_ticket();
-  s.epoch += 1;
-  if (s.epoch == 0) s.epoch = 1;
   LaunchSync sync{};
   sync.ticket = reinterpret_cast<unsigned long long*>(s.ptr + kHdrTicket);
   sync.err = reinterpret_cast<unsigned int*>(s.ptr + kHdrErr);
-  sync.base = s.next_ticket;
-  sync.tag = s.epoch;
   sync.use_ticket = by_ticket ? 1 : 0;
-  if (by_ticket) s.next_ticket += pl.total;
+  sync.poison = 0;
+  sync.tag = 0;  // ticket order: drawn on the device
+  if (!by_ticket) {
+    s.epoch += 1;
+    if (s.epoch == 0) s.epoch = 1;
+    sync.tag = s.epoch;
+  }
   void* payload = s.ptr + kHdrBytes;
   int rc = OSSM_OK;
   switch (variant) {
@@ -883,7 +885,6 @@ int ossm_dlinoss_forward_noalloc(int variant, const float* a_diag, const float* 
       rc = dlinoss_forward_noalloc_v<OSSM_DLINOSS_EX>(pl, a_diag, g_diag, step, bu, states, length, batch, ssm, stream, payload, sync);
       break;
   }
-  if (rc != OSSM_OK && by_ticket) s.next_ticket -= pl.total;  // nothing was launched
   return rc;
 }
 

@@ -6,6 +6,7 @@
 #include <memory>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "../../include/ossm_scan.h"
 
@@ -14,17 +15,25 @@ namespace {
 
 thread_local std::string g_last_error;
 
+int release_buffer(void* p, bool captured, const char* what);
+
 struct Scratch {
   void* base = nullptr;       // device buffer: header + payload
   size_t payload = 0;         // payload capacity in bytes
-  unsigned int epoch = 0;     // tag of the most recent launch
-  unsigned long long next_ticket = 0;  // value of the device counter after all queued launches
+  unsigned int epoch = 0;     // tag of the most recent dispatch-order launch
+  bool captured = false;      // a HIP graph holds this buffer's address
 };
 
 struct Workspace {
   void* base = nullptr;
   size_t bytes = 0;
+  bool captured = false;
 };
+
+// Buffers a captured graph may still use: never freed (the graph keeps their
+// addresses and may be replayed until the process ends).
+std::mutex g_retired_mu;
+std::vector<void*> g_retired;
 
 // Everything the library keeps for one (device, stream).  `call` is held by a
 // StreamCall for the whole of one C call; `scratch` and `workspace` are only
@@ -79,27 +88,40 @@ StreamCall::StreamCall(hipStream_t stream) : stream_(stream) {
   lock_ = std::unique_lock<std::recursive_mutex>(state_of(device_, stream).call);
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   const hipError_t e = hipStreamIsCapturing(stream, &cap);
-  if (e != hipSuccess || cap != hipStreamCaptureStatusNone) {
+  if (e != hipSuccess) {
     (void)hipGetLastError();  // keep a refused call from surfacing as a later launch error
-    status_ = set_error(OSSM_ERR_UNSUPPORTED,
-                        std::string("ossm_scan: the stream is being captured into a HIP graph (") +
-                            (e != hipSuccess ? hipGetErrorString(e) : "capture active") +
-                            "); the scans choose look-back tags and ticket bases on the host per "
-                            "call, so a replayed graph would reuse them: run the scan eagerly");
+    status_ = set_error(OSSM_ERR_HIP, std::string("hipStreamIsCapturing: ") + hipGetErrorString(e));
+    return;
   }
+  capturing_ = cap == hipStreamCaptureStatusActive;
+  if (cap == hipStreamCaptureStatusInvalidated)
+    status_ = set_error(OSSM_ERR_UNSUPPORTED, "ossm_scan: the stream's graph capture was invalidated");
 }
 
-int acquire_scratch(StreamCall& call, size_t payload_bytes, uint64_t n_workgroups,
-                    void** payload, LaunchSync* sync) {
+namespace {
+
+int refuse_capture(const char* what) {
+  return set_error(OSSM_ERR_UNSUPPORTED,
+                   std::string("ossm_scan: the stream is being captured into a HIP graph and the ") +
+                       what + "; run this call once eagerly on the stream before capturing it");
+}
+
+}  // namespace
+
+int acquire_scratch(StreamCall& call, size_t payload_bytes, void** payload, LaunchSync* sync) {
   if (call.status()) return call.status();
   const bool by_ticket = scan_order_by_ticket();
-  if (!by_ticket) n_workgroups = 0;  // no ticket is drawn
   Scratch& s = state_of(call.device(), call.stream()).scratch;
+  if (call.capturing() && !by_ticket)
+    return set_error(OSSM_ERR_UNSUPPORTED,
+                     "ossm_scan: OSSM_SCAN_ORDER=dispatch chooses look-back tags on the host per "
+                     "call, which a replayed HIP graph would reuse: capture needs ticket order");
   if (s.base == nullptr || s.payload < payload_bytes) {
+    if (call.capturing()) return refuse_capture("look-back scratch would have to grow");
     // Grow: earlier launches on this stream may still read the old buffer.
     if (s.base != nullptr) {
       if (int rc = hip_check(hipStreamSynchronize(call.stream()), "hipStreamSynchronize")) return rc;
-      if (int rc = hip_check(hipFree(s.base), "hipFree(scratch)")) return rc;
+      if (int rc = release_buffer(s.base, s.captured, "hipFree(scratch)")) return rc;
       s.base = nullptr;
     }
     size_t cap = payload_bytes < (size_t(1) << 20) ? (size_t(1) << 20) : payload_bytes;
@@ -113,17 +135,20 @@ int acquire_scratch(StreamCall& call, size_t payload_bytes, uint64_t n_workgroup
     s.base = p;
     s.payload = cap;
     s.epoch = 0;
-    s.next_ticket = 0;
+    s.captured = false;
   }
-  s.epoch += 1;
-  if (s.epoch == 0) s.epoch = 1;  // 0 is the tag of never-written memory
+  if (call.capturing()) s.captured = true;
   char* b = static_cast<char*>(s.base);
   sync->ticket = reinterpret_cast<unsigned long long*>(b + kHdrTicket);
   sync->err = reinterpret_cast<unsigned int*>(b + kHdrErr);
-  sync->base = s.next_ticket;
-  sync->tag = s.epoch;
   sync->use_ticket = by_ticket ? 1 : 0;
-  s.next_ticket += n_workgroups;
+  sync->poison = 0;
+  sync->tag = 0;  // ticket order: drawn on the device
+  if (!by_ticket) {
+    s.epoch += 1;
+    if (s.epoch == 0) s.epoch = 1;  // 0 is the tag of never-written memory
+    sync->tag = s.epoch;
+  }
   *payload = b + kHdrBytes;
   return OSSM_OK;
 }
@@ -132,9 +157,10 @@ int acquire_workspace(StreamCall& call, size_t bytes, void** ptr) {
   if (call.status()) return call.status();
   Workspace& w = state_of(call.device(), call.stream()).workspace;
   if (w.base == nullptr || w.bytes < bytes) {
+    if (call.capturing()) return refuse_capture("workspace would have to grow");
     if (w.base != nullptr) {
       if (int rc = hip_check(hipStreamSynchronize(call.stream()), "hipStreamSynchronize")) return rc;
-      if (int rc = hip_check(hipFree(w.base), "hipFree(workspace)")) return rc;
+      if (int rc = release_buffer(w.base, w.captured, "hipFree(workspace)")) return rc;
       w.base = nullptr;
       w.bytes = 0;
     }
@@ -144,16 +170,25 @@ int acquire_workspace(StreamCall& call, size_t bytes, void** ptr) {
     if (int rc = hip_check(hipMalloc(&p, cap), "hipMalloc(workspace)")) return rc;
     w.base = p;
     w.bytes = cap;
+    w.captured = false;
   }
+  if (call.capturing()) w.captured = true;
   *ptr = w.base;
   return OSSM_OK;
 }
 
-void release_unlaunched(StreamCall& call, uint64_t n_workgroups) {
-  if (!scan_order_by_ticket() || call.status()) return;
-  Scratch& s = state_of(call.device(), call.stream()).scratch;
-  if (s.next_ticket >= n_workgroups) s.next_ticket -= n_workgroups;
+namespace {
+
+int release_buffer(void* p, bool captured, const char* what) {
+  if (captured) {
+    std::lock_guard<std::mutex> lock(g_retired_mu);
+    g_retired.push_back(p);
+    return OSSM_OK;
+  }
+  return hip_check(hipFree(p), what);
 }
+
+}  // namespace
 
 }  // namespace ossm
 
@@ -178,16 +213,40 @@ uint32_t ossm_device_error_bits(ossm_stream_t stream_v) {
   char* base = static_cast<char*>(s.base);
   if (hipMemcpy(&bits, base + ossm::kHdrErr, sizeof(bits), hipMemcpyDeviceToHost) != hipSuccess)
     return 0xffffffffu;
-  // With the stream drained, the device counter holds every ticket drawn on
-  // this scratch (each workgroup draws exactly one).  A failed protocol, or a
-  // reservation whose launch never happened, can leave the host's count out of
-  // step with it: take the device's value, so later launches start in step.
+  // With the stream drained, every launch on this scratch has run to its end
+  // and left the ticket counter at a multiple of 2^32.  A launch that did not
+  // (an aborted kernel) leaves it out of step; move it to the next multiple,
+  // so that later launches start in step.
   unsigned long long t = 0;
   if (hipMemcpy(&t, base + ossm::kHdrTicket, sizeof(t), hipMemcpyDeviceToHost) == hipSuccess &&
-      ossm::scan_order_by_ticket())
-    s.next_ticket = t;
+      (t & (ossm::kEpochSpan - 1)) != 0) {
+    t = (t | (ossm::kEpochSpan - 1)) + 1;
+    (void)hipMemcpy(base + ossm::kHdrTicket, &t, sizeof(t), hipMemcpyHostToDevice);
+  }
   if (bits != 0) (void)hipMemset(base + ossm::kHdrErr, 0, sizeof(bits));
   return bits | fixed_bits;
+}
+
+int ossm_test_skew_tickets(ossm_stream_t stream_v, uint64_t delta) {
+  ossm::clear_error();
+  hipStream_t stream = static_cast<hipStream_t>(stream_v);
+  int dev = 0;
+  if (int rc = ossm::hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  ossm::StreamState& st = ossm::state_of(dev, stream);
+  std::lock_guard<std::recursive_mutex> hold(st.call);
+  ossm::Scratch& s = st.scratch;
+  if (s.base == nullptr)
+    return ossm::set_error(OSSM_ERR_INVALID_ARGUMENT,
+                           "ossm_test_skew_tickets: no scan has run on this stream yet");
+  if (int rc = ossm::hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize")) return rc;
+  char* base = static_cast<char*>(s.base);
+  unsigned long long t = 0;
+  if (int rc = ossm::hip_check(hipMemcpy(&t, base + ossm::kHdrTicket, sizeof(t), hipMemcpyDeviceToHost),
+                               "hipMemcpy"))
+    return rc;
+  t += delta;
+  return ossm::hip_check(hipMemcpy(base + ossm::kHdrTicket, &t, sizeof(t), hipMemcpyHostToDevice),
+                         "hipMemcpy");
 }
 
 }  // extern "C"

@@ -21,13 +21,25 @@ constexpr size_t kHdrErr = 64;      // uint32_t error bits
 constexpr size_t kHdrBytes = 256;   // payload starts here, 256-byte aligned
 
 // Per-launch synchronisation arguments handed to a look-back kernel.
+//
+// Ticket order (the default): every workgroup draws t = ticket++ when it
+// starts.  Each launch starts with the counter at a multiple of 2^32
+// (kEpochSpan): the low 32 bits of t are the workgroup's order in the launch,
+// the high 32 bits the launch's epoch, and the records' tag is the epoch + 1.
+// The workgroup that draws the launch's last order advances the counter to
+// the next multiple of 2^32.  Nothing per launch is chosen on the host, so a
+// launch captured into a HIP graph draws fresh tags and orders on every
+// replay.  Dispatch order (OSSM_SCAN_ORDER=dispatch) draws no ticket: the
+// order is the workgroup index and the host chooses the tag per call.
 struct LaunchSync {
   unsigned long long* ticket;  // device counter, shared by all launches on this scratch
   unsigned int* err;           // device error bits
-  unsigned long long base;     // value of *ticket when this launch starts
-  unsigned int tag;            // epoch tag of this launch's records (never 0)
+  unsigned int tag;            // records' tag: set on the device in ticket order, by the host in dispatch order
   int use_ticket;              // 1: chunks follow the ticket counter, 0: dispatch order
+  int poison;                  // 0 from the host; 1 on the device when the ticket was out of range
 };
+
+constexpr unsigned long long kEpochSpan = 1ull << 32;
 
 // Whether look-back kernels order their chunks by the ticket counter (the
 // default) or by workgroup index (environment OSSM_SCAN_ORDER=dispatch).
@@ -42,15 +54,15 @@ int hip_check(hipError_t e, const char* what);
 
 // One C call's hold on a (device, stream).  An entry point that uses the
 // stream's scratch or workspace creates one first and keeps it until its last
-// launch is enqueued: the ticket base and tag drawn for a launch, and the
-// partial sums one launch leaves for the next, then belong to launches that
-// reach the stream in the order they were drawn, whatever other host threads
-// do on the same stream.  The lock is recursive (an entry point may call
-// another on the same stream).  status() is nonzero when the device could not
-// be read or the stream is being captured into a graph (launch tags and
-// ticket bases are chosen on the host per call, so a replayed graph would
-// reuse them: capture is refused with OSSM_ERR_UNSUPPORTED before anything is
-// enqueued).
+// launch is enqueued: the partial sums one launch leaves for the next then
+// belong to launches that reach the stream in the order they were enqueued,
+// whatever other host threads do on the same stream.  The lock is recursive
+// (an entry point may call another on the same stream).  status() is nonzero
+// when the device could not be read.  capturing() is true while the stream is
+// being captured into a HIP graph: the scratch and workspace are then used as
+// they are (a capture that would need them to grow is refused with
+// OSSM_ERR_UNSUPPORTED) and are never freed afterwards, since the graph keeps
+// their addresses.
 class StreamCall {
  public:
   explicit StreamCall(hipStream_t stream);
@@ -59,31 +71,31 @@ class StreamCall {
   int status() const { return status_; }
   hipStream_t stream() const { return stream_; }
   int device() const { return device_; }
+  bool capturing() const { return capturing_; }
 
  private:
   hipStream_t stream_;
   int device_ = 0;
   int status_ = 0;
+  bool capturing_ = false;
   std::unique_lock<std::recursive_mutex> lock_;
 };
 
 // Returns a scratch payload of at least `payload_bytes` for the call's stream
-// and the launch bookkeeping for a grid of `n_workgroups` look-back
-// workgroups.  The payload is zero-filled when first allocated and is never
-// cleared again: kernels tag what they write with sync.tag.
-int acquire_scratch(StreamCall& call, size_t payload_bytes, uint64_t n_workgroups,
-                    void** payload, LaunchSync* sync);
+// and the launch bookkeeping of a look-back kernel.  The payload is
+// zero-filled when first allocated and is never cleared again: kernels tag
+// what they write with sync.tag.  Under capture, dispatch order is refused
+// (its tag is chosen on the host) and so is a payload larger than the
+// current one.
+int acquire_scratch(StreamCall& call, size_t payload_bytes, void** payload, LaunchSync* sync);
 
 // Returns a plain device workspace of at least `bytes` for the call's stream,
 // separate from the tagged look-back records: partial sums written here can
 // never be mistaken for a record.  Contents are unspecified; kernels write
 // before they read.  Grows on demand (synchronising the stream before freeing
-// the old one).
+// the old one, unless a graph captured it); refused under capture when it
+// would have to grow.
 int acquire_workspace(StreamCall& call, size_t bytes, void** ptr);
-
-// Undo the ticket reservation of the last acquire_scratch of this call when
-// its kernel failed to launch (the device counter never advanced).
-void release_unlaunched(StreamCall& call, uint64_t n_workgroups);
 
 // Launch-error check after a kernel launch (reference: C10_CUDA_KERNEL_LAUNCH_CHECK).
 int launch_check(const char* what);

@@ -19,6 +19,13 @@ __device__ __forceinline__ float4 f4add(float4 a, float4 b) {
   return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 __device__ __forceinline__ float4 f4zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+// The carry of a chunk whose predecessors could not be read (a bounded wait
+// that gave up, an out-of-range ticket): NaN, so that every output computed
+// from it is NaN rather than a plausible wrong value.
+__device__ __forceinline__ float4 f4nan() {
+  const float q = __builtin_nanf("");
+  return make_float4(q, q, q, q);
+}
 
 // ---- real 2x2 transition [[a, b], [c, d]] (D-LinOSS) -----------------------
 struct RMat {
@@ -188,11 +195,14 @@ constexpr int kLookbackWindow = OSSM_LOOKBACK_WINDOW;
 // with `step_mat` (the chunk transition) until an inclusive prefix is found.
 // Every predecessor drew an earlier ticket, so it is resident and publishes
 // its aggregate without waiting on anything: the walk always ends.  The spin
-// is still bounded; giving up raises kErrSpinTimeout instead of hanging.
+// is still bounded; giving up raises kErrSpinTimeout and returns a NaN carry
+// instead of hanging.  A poisoned launch (out-of-range ticket) returns NaN
+// without walking.
 template <class Mat>
 __device__ float4 lookback(unsigned long long* rec, int c, int dir, int n_chunks, int nc, int ch,
                            Mat step_mat, const LaunchSync& sync) {
   constexpr int K = kLookbackWindow;
+  if (sync.poison) return f4nan();
   float4 acc = f4zero();
   Mat pw = mat_identity(step_mat);
   int j = c - dir;  // next predecessor to fold in
@@ -226,7 +236,7 @@ __device__ float4 lookback(unsigned long long* rec, int c, int dir, int n_chunks
     if (!moved) {
       if (++spins > kSpinLimit) {
         __hip_atomic_fetch_or(sync.err, kErrSpinTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return acc;
+        return f4nan();
       }
       __builtin_amdgcn_s_sleep(2);
     }
@@ -241,35 +251,48 @@ __device__ float4 lookback(unsigned long long* rec, int c, int dir, int n_chunks
 // Ticket order (default, sync.use_ticket): a global atomic counter drawn at
 // workgroup start guarantees that under any dispatch order, at the price of
 // one serialised atomic per workgroup (~10 us per 2048 workgroups measured
-// on a streaming kernel of the same shape).
+// on a streaming kernel of the same shape).  The ticket also gives the
+// launch's record tag (see LaunchSync), written into sync.tag.
 //
 // Dispatch order (OSSM_SCAN_ORDER=dispatch): the workgroup index.  This
 // relies on each XCD dispatching its share of the grid in increasing index
 // order; measured faster for long sequences (config 5 forward 324 vs 346 us)
 // and slower for config 2's forward (86 vs 79 us).
-__device__ __forceinline__ int launch_order(const LaunchSync& sync, int total, int* s_slot);
-
-// Draws this workgroup's ticket (launch order), broadcast through LDS.
-// Returns -1 (and raises kErrBadTicket) when the counter is out of step.
-__device__ __forceinline__ int draw_ticket(const LaunchSync& sync, int total, int* s_slot) {
+//
+// A ticket whose order is out of range means the counter was out of step
+// (a launch on this scratch that did not run to its end): the workgroup
+// raises kErrBadTicket, takes order (rel mod total) — the orders a
+// misaligned launch never draws are exactly those the out-of-range tickets
+// map to — and marks the launch poisoned, so its look-backs return NaN and
+// every output that depends on a carry is NaN.
+__device__ __forceinline__ int launch_order(LaunchSync& sync, int total, int* s_slot) {
+  if (!sync.use_ticket) return static_cast<int>(blockIdx.x);
+  __shared__ unsigned int s_tag;
+  __shared__ int s_poison;
   if (threadIdx.x == 0) {
     const unsigned long long t =
         __hip_atomic_fetch_add(sync.ticket, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    long long rel = static_cast<long long>(t - sync.base);
-    if (rel < 0 || rel >= total) {
+    unsigned long long rel = t & (kEpochSpan - 1);
+    const unsigned long long epoch = t >> 32;
+    int poison = 0;
+    if (rel >= static_cast<unsigned long long>(total)) {
       __hip_atomic_fetch_or(sync.err, kErrBadTicket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      rel = -1;
+      rel %= static_cast<unsigned long long>(total);
+      poison = 1;
+    } else if (rel == static_cast<unsigned long long>(total - 1)) {
+      // the launch's last ticket: the next launch starts at the next epoch
+      __hip_atomic_fetch_add(sync.ticket, kEpochSpan - static_cast<unsigned long long>(total),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     *s_slot = static_cast<int>(rel);
+    s_tag = static_cast<unsigned int>(epoch % 0xffffffffull) + 1u;  // 1 .. 2^32 - 1, never 0
+    s_poison = poison;
   }
   __syncthreads();
-  return *s_slot;
-}
-
-__device__ __forceinline__ int launch_order(const LaunchSync& sync, int total, int* s_slot) {
-  if (!sync.use_ticket) return static_cast<int>(blockIdx.x);
-  // uniform across the workgroup: keep it (and what derives from it) scalar
-  return __builtin_amdgcn_readfirstlane(draw_ticket(sync, total, s_slot));
+  // uniform across the workgroup: keep them (and what derives from them) scalar
+  sync.tag = __builtin_amdgcn_readfirstlane(s_tag);
+  sync.poison = __builtin_amdgcn_readfirstlane(s_poison);
+  return __builtin_amdgcn_readfirstlane(*s_slot);
 }
 
 // Index of the calling wave in its workgroup, as a scalar value.

@@ -180,9 +180,11 @@ __device__ __forceinline__ void tv_fetch(const unsigned long long* rec, int chun
 
 // Carry into chunk c for one channel, walking predecessors c - dir, ...:
 // acc + P * (inclusive of j), where each aggregate (E_j, K_j) passed over
-// adds P E_j to acc and turns P into P K_j.  Bounded spin as in lookback().
+// adds P E_j to acc and turns P into P K_j.  Bounded spin and NaN carry as in
+// lookback().
 __device__ float4 lookback_tv(unsigned long long* rec, int c, int dir, int n_chunks, int nc,
                               int ch, const LaunchSync& sync) {
+  if (sync.poison) return f4nan();
   float4 acc = f4zero();
   RMat P = {1.f, 0.f, 0.f, 1.f};
   int j = c - dir;
@@ -204,7 +206,7 @@ __device__ float4 lookback_tv(unsigned long long* rec, int c, int dir, int n_chu
     }
     if (++spins > kSpinLimit) {
       __hip_atomic_fetch_or(sync.err, kErrSpinTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return acc;
+      return f4nan();
     }
     __builtin_amdgcn_s_sleep(2);
   }
@@ -283,7 +285,6 @@ __global__ __launch_bounds__(W * kWave) void sdl_forward_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int w = wave_id();
   const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
-  if (ticket < 0) return;
   const int c = ticket / n_groups;
   const int g = ticket - c * n_groups;
   const int ch = g * kWave + lane;
@@ -495,7 +496,6 @@ __global__ __launch_bounds__(W * kWave) void sdl_backward_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int w = wave_id();
   const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
-  if (ticket < 0) return;
   // chunks are handed out last-first
   const int cr = ticket / n_groups;
   const int g = ticket - cr * n_groups;
@@ -824,7 +824,7 @@ int sdl_forward_tw(const SdlParams& prm, const void* bu, void* states, int64_t L
   void* payload = nullptr;
   LaunchSync sync{};
   const int64_t total = n_chunks * n_groups;
-  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
   const bool tb = prm.a.t_stride == 0 && prm.g.t_stride == 0 && prm.s.t_stride == 0;
   hipLaunchKernelGGL((tb ? sdl_forward_kernel<V, T, W, true> : sdl_forward_kernel<V, T, W, false>),
                      dim3(static_cast<unsigned>(total)),
@@ -832,10 +832,7 @@ int sdl_forward_tw(const SdlParams& prm, const void* bu, void* states, int64_t L
                      static_cast<float4*>(states), static_cast<int>(L), static_cast<int>(nc),
                      static_cast<int>(n_groups), static_cast<int>(n_chunks),
                      static_cast<unsigned long long*>(payload), sync);
-  if (int rc = launch_check("sdl_forward_kernel")) {
-    release_unlaunched(call, total);
-    return rc;
-  }
+  if (int rc = launch_check("sdl_forward_kernel")) return rc;
   return OSSM_OK;
 }
 
@@ -899,7 +896,7 @@ int sdl_backward_tw(const SdlParams& prm, const ParamShape (&shapes)[3], const v
   void* payload = nullptr;
   LaunchSync sync{};
   const int64_t total = n_chunks * n_groups;
-  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
   const bool tb = prm.a.t_stride == 0 && prm.g.t_stride == 0 && prm.s.t_stride == 0;
   hipLaunchKernelGGL((tb ? sdl_backward_kernel<V, T, W, true> : sdl_backward_kernel<V, T, W, false>),
                      dim3(static_cast<unsigned>(total)),
@@ -908,10 +905,7 @@ int sdl_backward_tw(const SdlParams& prm, const ParamShape (&shapes)[3], const v
                      static_cast<float2*>(gbu), dst, static_cast<int>(L), static_cast<int>(nc),
                      static_cast<int>(n_groups), static_cast<int>(n_chunks),
                      static_cast<unsigned long long*>(payload), sync);
-  if (int rc = launch_check("sdl_backward_kernel")) {
-    release_unlaunched(call, total);
-    return rc;
-  }
+  if (int rc = launch_check("sdl_backward_kernel")) return rc;
   ColSums sums{};
   int n_sums = 0;
   for (int p = 0; p < 3; ++p) {

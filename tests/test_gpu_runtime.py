@@ -1,11 +1,13 @@
 """GPU tests of the library's launch bookkeeping (runtime.cpp): calls from
-several host threads on one stream, and refusal of HIP-graph capture.
+several host threads on one stream, HIP-graph capture and replay, and the
+failure path of the look-back protocol.
 
-The look-back scans draw a launch tag and a ticket base on the host, and the
-backward passes leave partial sums in a per-stream workspace for the launch
-that follows.  Each C call holds its (device, stream) from that bookkeeping
-through its last launch, so calls from different host threads on the same
-stream reach the stream whole and in the order their bookkeeping was drawn.
+The look-back scans draw each workgroup's order and the launch's record tag
+from a per-stream ticket counter on the device, and the backward passes leave
+partial sums in a per-stream workspace for the launch that follows.  Each C
+call holds its (device, stream) through its last launch, so calls from
+different host threads on the same stream reach the stream whole, and a
+captured call draws fresh orders and tags on every replay.
 """
 
 from __future__ import annotations
@@ -116,14 +118,83 @@ def test_two_host_threads_share_one_stream(K):
                              f"thread {i} selective {key}")
 
 
-def test_graph_capture_is_refused(K):
-    """A call made while its stream is being captured into a HIP graph raises
-    RuntimeError before anything is enqueued (the look-back tags and ticket
-    bases are drawn on the host per call; a replay would reuse them).  Eager
-    calls afterwards are unaffected."""
+def _dl_call(K, args, go):
+    st = K.dlinoss_imex1_forward(*args)
+    return [st] + list(K.dlinoss_imex1_backward(*args, st, go))
+
+
+def _errors_on(stream) -> int:
+    from ossm_amd import _lib
+
+    with torch.cuda.stream(stream):
+        return _lib.device_error_bits()
+
+
+def test_graph_capture_replays_dlinoss_config2(K):
+    """D-LinOSS imex1 forward + backward at config 2 (B=32, L=4096, P=128)
+    captured into a HIP graph after an eager warm-up on the capture stream,
+    replayed 10 times with eager calls on the same stream and host
+    synchronisations between the replays: every replay's states and gradients
+    equal the eager result (rtol 1e-4; the look-back may associate carries
+    differently per run), and no protocol error is raised."""
+    L, B, P = 4096, 32, 128
+    a, g, dt, bu, go = dlinoss_inputs(L, B, P, seed=21, variant="imex1")
+    args = [to_dev(x) for x in (a, g, dt, bu)]
+    god = to_dev(go)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    announce("runtime: graph capture dlinoss config 2")
+    with torch.cuda.stream(side):
+        eager = [to_np(x) for x in _dl_call(K, args, god)]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        outs = _dl_call(K, args, god)
+    names = ("states", "grad_a", "grad_g", "grad_step", "grad_bu")
+    small = [x[:300].contiguous() for x in (args[3],)]
+    for r in range(10):
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, ref, name in zip(outs, eager, names):
+            atol = ATOL if name in ("states", "grad_bu") else 2e-5 * max(1.0, float(np.abs(ref).max()))
+            assert_close(to_np(got), ref, RTOL, atol, f"replay {r} {name}")
+        with torch.cuda.stream(side):  # eager work on the capture stream between replays
+            K.dlinoss_imex1_forward(*args[:3], small[0])
+        side.synchronize()
+    assert _errors_on(side) == 0
+
+
+def test_graph_capture_replays_selective(K):
+    """The selective scan forward + backward (gated) captured after an eager
+    warm-up and replayed 5 times: every replay equals the eager result
+    bitwise (the selective scan is deterministic)."""
+    u, dt, A, Bm, Cm, z, go = (to_dev(x) for x in _selective_inputs(31, Bz=8, D=128, L=400))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    announce("runtime: graph capture selective")
+
+    def step():
+        out, ck, raw = K.selective_scan_cuda(u, dt, A, Bm, Cm, z)
+        return [out] + list(K.selective_scan_cuda_backward(go, u, dt, A, Bm, Cm, z, ck, raw, 16))
+
+    with torch.cuda.stream(side):
+        eager = [to_np(x) for x in step()]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        outs = step()
+    for r in range(5):
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, ref, name in zip(outs, eager, ("out", "du", "ddt", "dA", "dB", "dC", "dz")):
+            assert np.array_equal(to_np(got), ref), f"replay {r} {name}"
+    assert _errors_on(side) == 0
+
+
+def test_graph_capture_refused_when_scratch_would_grow(K):
+    """On a stream with no look-back scratch yet (no eager call), a captured
+    call would have to allocate: it raises RuntimeError before anything is
+    enqueued, and eager calls afterwards are unaffected."""
     a, g, dt, bu, _ = dlinoss_inputs(300, 2, 40, seed=7)
     ad, gd, dtd, bud = (to_dev(x) for x in (a, g, dt, bu))
-    u, dts, A, Bm, Cm, z, _ = (to_dev(x) for x in _selective_inputs(9, Bz=2, D=64, L=100))
     torch.cuda.synchronize()
     side = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
@@ -131,13 +202,72 @@ def test_graph_capture_is_refused(K):
     with torch.cuda.stream(side):
         graph.capture_begin()
         try:
-            with pytest.raises(RuntimeError, match="captured into a HIP graph"):
+            with pytest.raises(RuntimeError, match="would have to grow"):
                 K.dlinoss_imex1_forward(ad, gd, dtd, bud)
-            with pytest.raises(RuntimeError, match="captured into a HIP graph"):
-                K.selective_scan_cuda(u, dts, A, Bm, Cm, z)
         finally:
             graph.capture_end()
     torch.cuda.synchronize()
     st = K.dlinoss_imex1_forward(ad, gd, dtd, bud)
     assert_close(to_np(st), oracle.dlinoss_forward("imex1", a, g, dt, bu), RTOL, ATOL, "after capture")
+    no_device_errors()
+
+
+def test_protocol_failure_gives_nan_not_garbage(K):
+    """With the stream's ticket counter knocked out of step from the host (as
+    a launch that did not run to its end would leave it), every workgroup of
+    the next look-back launch draws an out-of-range ticket: the launch raises
+    the bad-ticket bit, the chunks that needed a carry come out NaN (the first
+    chunk, which needs none, is still right), and after the error check the
+    next call is correct again.  Forward and backward of D-LinOSS, and the
+    LRU and selective D-LinOSS forwards."""
+    from ossm_amd import _lib
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    L, B, P = 1000, 2, 64
+    a, g, dt, bu, go = dlinoss_inputs(L, B, P, seed=41, variant="imex1")
+    args = [to_dev(x) for x in (a, g, dt, bu)]
+    ref = oracle.dlinoss_forward("imex1", a, g, dt, bu)
+    rgrads = oracle.dlinoss_backward("imex1", a, g, dt, bu, ref, go)
+    announce("runtime: protocol failure -> NaN")
+    K.dlinoss_imex1_forward(*args)  # the stream's scratch exists
+    assert _lib.device_error_bits() == 0
+    skew = 1 << 20  # far above any launch's workgroup count, far below 2^32
+
+    _lib.check(lib.ossm_test_skew_tickets(stream, skew))
+    st = to_np(K.dlinoss_imex1_forward(*args))
+    assert _lib.device_error_bits() == 2  # bad ticket; the check realigns the counter
+    assert np.isfinite(st[:128]).all()  # the first chunk (128 or 256 steps) needs no carry
+    assert_close(st[:128], ref[:128], RTOL, ATOL, "first chunk")
+    assert np.isnan(st[256:]).all()
+
+    st = K.dlinoss_imex1_forward(*args)
+    _lib.check(lib.ossm_test_skew_tickets(stream, skew))
+    grads = [to_np(x) for x in K.dlinoss_imex1_backward(*args, st, to_dev(go))]
+    assert _lib.device_error_bits() == 2
+    assert all(np.isnan(x).all() for x in grads[:3])  # sums over every chunk
+    # reverse scan: the last chunk (128 steps here) needs no carry
+    assert np.isnan(grads[3][:L - 256]).all() and np.isfinite(grads[3][L - 100:]).all()
+
+    # LRU forward (diagonal scan) and selective D-LinOSS forward
+    lam = torch.polar(torch.rand(P, device="cuda") * 0.5 + 0.5, torch.rand(P, device="cuda"))
+    bseq = torch.randn(L, B, P, 2, device="cuda")
+    K.lru_scan(lam.real.contiguous(), lam.imag.contiguous(), bseq)
+    _lib.check(lib.ossm_test_skew_tickets(stream, skew))
+    y = to_np(K.lru_scan(lam.real.contiguous(), lam.imag.contiguous(), bseq))
+    assert _lib.device_error_bits() == 2
+    assert np.isnan(y[L - 100:]).all() and np.isfinite(y[:64]).all()  # last chunk / first
+    A = to_dev(a)[None, None].expand(L, B, P).contiguous()
+    sdl = lambda: K.sdlinoss_imex1_forward(A, A * 0 + to_dev(g), A * 0 + to_dev(dt), args[3])  # noqa: E731
+    sdl()
+    _lib.check(lib.ossm_test_skew_tickets(stream, skew))
+    y = to_np(sdl())
+    assert _lib.device_error_bits() == 2
+    assert np.isnan(y[L - 100:]).all() and np.isfinite(y[:64]).all()  # last chunk / first
+
+    # back in step: correct and error-free
+    st = to_np(K.dlinoss_imex1_forward(*args))
+    assert_close(st, ref, RTOL, ATOL, "after recovery")
+    grads = K.dlinoss_imex1_backward(*args, to_dev(st), to_dev(go))
+    assert_close(to_np(grads[3]), rgrads[3], RTOL, ATOL, "grad_bu after recovery")
     no_device_errors()

@@ -52,3 +52,33 @@ def test_noalloc_forward_matches_allocating_entry(lib, variant):
         assert_close(to_np(got), to_np(ref), RTOL, ATOL, f"noalloc vs allocating L={L} B={B} P={P}")
         no_device_errors()
 
+
+
+def test_noalloc_forward_under_graph_capture(lib):
+    """The allocation-free forward captured into a HIP graph (after one eager
+    call on the device, which looks up the fixed array's address), replayed
+    five times with eager calls of the allocating entry between the replays:
+    every replay matches the allocating entry to the north-star tolerance."""
+    L, B, P = 2000, 8, 128
+    a, g, dt, bu, _ = dlinoss_inputs(L, B, P, seed=13, variant="imex1")
+    ad, gd, dtd, bud = (to_dev(x) for x in (a, g, dt, bu))
+    ref = torch.empty((L, B, P, 2), dtype=torch.complex64, device="cuda")
+    got = torch.full((L, B, P, 2), float("nan"), dtype=torch.complex64, device="cuda")
+    announce(f"noalloc dlinoss imex1 under graph capture L={L} B={B} P={P}")
+    lib.check(_call(lib, "ossm_dlinoss_forward", 0, ad, gd, dtd, bud, ref))
+    lib.check(_call(lib, "ossm_dlinoss_forward_noalloc", 0, ad, gd, dtd, bud, got))
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        lib.check(_call(lib, "ossm_dlinoss_forward_noalloc", 0, ad, gd, dtd, bud, got))
+    expect = to_np(ref)
+    for r in range(5):
+        got.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_close(to_np(got), expect, RTOL, ATOL, f"replay {r}")
+        lib.check(_call(lib, "ossm_dlinoss_forward", 0, ad, gd, dtd, bud, ref))
+        torch.cuda.synchronize()
+    no_device_errors()
