@@ -648,7 +648,7 @@ def main() -> int:
     bwd_bw = units * DL_BYTES_BWD / (bwd_ms / 1e3)
     if bwd_ms >= fwd_ms:
         dom = {"name": f"dlinoss_{args.variant}_backward",
-               "launches": ["osc_backward_kernel<Dlinoss>", "column_sum_kernel"],
+               "launches": ["osc_backward_kernel<Dlinoss>"],
                "bw": bwd_bw, "ms": bwd_ms, "bytes": units * DL_BYTES_BWD, "key": "backward"}
     else:
         dom = {"name": f"dlinoss_{args.variant}_forward", "launches": ["osc_forward_kernel<Dlinoss>"],

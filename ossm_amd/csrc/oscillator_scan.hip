@@ -25,16 +25,15 @@
 //   parameter gradients are recomputed in registers from one checkpoint per
 //   chunk, the state before its first step, and the waves' forward summaries
 //   exchanged through LDS, instead of reading the whole trajectory.  Per-lane sums of
-//   <mu_i, s_j,t-1> and <mu_i, bu_t> go to a partials buffer; one small
-//   kernel adds them over time chunks and batch rows per oscillator in 64 row
-//   groups (fixed order, fp64), applies each variant's chain rule (linear in
-//   the sums) to every group's share and adds the shares into grad a, g, dt
-//   with float atomics (scan_reduce.hpp).  (A last-workgroup-done reduction
+//   <mu_i, s_j,t-1> and <mu_i, bu_t> are added over the workgroup's waves;
+//   each variant's chain rule is linear in them, so wave 0 applies it to its
+//   chunk's per-channel sums and adds the result into grad a, g, dt with
+//   float atomics, after the launch's order-0 workgroup has zeroed those
+//   outputs and published its tag (zero_fill_publish, scan_reduce.hpp).  (A
+//   separate column-sum launch with fixed-order fp64 row-group sums cost
+//   4.4 us plus a launch gap at config 2; a last-workgroup-done reduction
 //   inside the scan kernel was measured 3x slower: each agent-scope release
-//   fence writes back the XCD's L2, dirty with the workgroup's grad_bu rows;
-//   a fixed tree of tagged records over chunks inside the scan, which needs no
-//   fence, cost the scan kernel as much as it saved, the reducing workgroups
-//   holding their CU while they gather.)
+//   fence writes back the XCD's L2, dirty with the workgroup's grad_bu rows.)
 
 #include <hip/hip_runtime.h>
 
@@ -213,11 +212,6 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_forward_kernel(
 // ============================================================================
 // Backward kernel
 // ============================================================================
-// Destination of the backward's per-(chunk, channel) parameter partial sums.
-struct ParamReduce {
-  float* partials;  // [n_chunks][NS][nc]
-};
-
 // One workgroup's inputs for one chunk, loaded ahead of its use.  Loads use
 // clamped in-range addresses and no branches; out-of-range steps are masked
 // where the values are consumed.
@@ -417,14 +411,18 @@ __device__ __forceinline__ float4 bwd_front(
 }
 
 // Second part: the final reverse pass (grad of the inputs and the parameter
-// sums) from carry y, then the chunk's per-channel partial sums.  `sp_lds` is
-// the wave's own S = T/H staging slots (see bwd_front); `s_sums` holds each
-// wave's NS sums, which wave 0 adds after a barrier.
+// sums) from carry y, then the chunk's share of the parameter gradients.
+// `sp_lds` is the wave's own S = T/H staging slots (see bwd_front); `s_sums`
+// holds each wave's NS sums, which wave 0 adds after a barrier.  The
+// variant's chain rule is linear in the sums, so wave 0 applies it to the
+// chunk's per-channel sums and adds the result into the outputs `zero` names
+// (zeroed by the launch's order-0 workgroup, zero_fill_publish).
 template <class Model, int T, int W, int H, int SS>
 __device__ __forceinline__ void bwd_back(BwdBuf<Model, T>& b, const BwdTicket& k, float4 y,
                                          float4 s_mid, float4* sp_lds,
                                          typename Model::GOut* __restrict__ gin,
-                                         const ParamReduce& red, int L, int nc, float* s_sums,
+                                         const typename Model::Params& prm, const ZeroFill& zero,
+                                         const LaunchSync& sync, int L, int nc, float* s_sums,
                                          int sums_stride) {
   constexpr int NS = Model::kSums;
   constexpr int Q = T / H;  // steps per staged segment
@@ -477,14 +475,20 @@ __device__ __forceinline__ void bwd_back(BwdBuf<Model, T>& b, const BwdTicket& k
   for (int j = 0; j < NS; ++j) mine[j * kWave + lane] = acc[j];
   __syncthreads();
 
-  // this chunk's parameter partial sums (one per channel and sum)
-  if (w == 0 && k.active) {
+  // this chunk's share of the parameter gradients (one channel per lane)
+  if (w == 0) {
+    double S[NS];
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       float v = 0.f;
       for (int u = 0; u < W; ++u) v += s_sums[u * sums_stride + j * kWave + lane];
-      group_row(red.partials, static_cast<long long>(k.c) * NS + j, nc, k.g)[lane] = v;
+      S[j] = v;
     }
+    if (!wait_outputs_zeroed(sync)) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j) S[j] = __builtin_nan("");
+    }
+    if (k.active) Model::epilogue(prm, k.ch % prm.P, S, zero.p[0], zero.p[1], zero.p[2]);
   }
 }
 
@@ -494,8 +498,8 @@ template <class Model, int T, int W, int OCC, int H, int SS>
 __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
     typename Model::Params prm, const typename Model::In* __restrict__ in,
     const float4* states, const typename Model::GIn* __restrict__ gout,
-    typename Model::GOut* __restrict__ gin, ParamReduce red, ZeroFill zero, int L, int nc,
-    int n_groups, int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
+    typename Model::GOut* __restrict__ gin, ZeroFill zero, int L, int nc, int n_groups,
+    int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
   constexpr int NS = Model::kSums;
   __shared__ float4 s_agg[W][kWave];
   __shared__ float4 s_carry[kWave];
@@ -506,7 +510,7 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
   __shared__ float4 s_sp[W][kSlots][kWave];
   __shared__ int s_ticket;
   const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
-  if (ticket == 0) zero_fill_block(zero);  // the parameter-gradient outputs, for column_sum_kernel
+  if (ticket == 0) zero_fill_publish(zero, sync);  // the parameter-gradient outputs
   const BwdTicket k = bwd_ticket<T, W>(ticket, n_groups, n_chunks, nc);
   BwdBuf<Model, T> b;
   bwd_load<Model, T, W>(b, k, prm, in, states, gout, L, nc);
@@ -516,24 +520,9 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_backward_kernel(
                                                          s_carry, s_sp, KT, s_mid);
   // the per-wave sums go into the wave's own s_{t-1} region, which only the
   // wave itself reads before this point
-  bwd_back<Model, T, W, H, SS>(b, k, y, s_mid, &s_sp[wave_id()][0][0], gin, red, L, nc,
-                           reinterpret_cast<float*>(&s_sp[0][0][0]), kSlots * kWave * 4);
+  bwd_back<Model, T, W, H, SS>(b, k, y, s_mid, &s_sp[wave_id()][0][0], gin, prm, zero, sync, L,
+                               nc, reinterpret_cast<float*>(&s_sp[0][0][0]), kSlots * kWave * 4);
 }
-
-// ============================================================================
-// Per-oscillator parameter gradients from the column sums
-// ============================================================================
-// column_sum_kernel calls this with each oscillator's NS sums over one row
-// group of (time chunk, batch row): the variant's chain rule, added into the
-// outputs.
-template <class Model>
-struct OscEpilogue {
-  typename Model::Params prm;
-  float* out0;
-  float* out1;
-  float* out2;
-  __device__ void add(int p, const double* S) const { Model::epilogue(prm, p, S, out0, out1, out2); }
-};
 
 // T steps per lane, W waves per workgroup, OCC = minimum waves per SIMD the
 // register allocation must allow (__launch_bounds__' second argument).
@@ -637,10 +626,13 @@ int launch_forward(const typename Model::Params& prm, const void* in, void* out,
   return OSSM_OK;
 }
 
-// Backward launch: the scan kernel computes grad_in and per-(chunk, channel)
-// parameter sums and clears out0..2; column_sum_kernel reduces the sums per
-// oscillator and adds the chain rule's result into out0..2 (see
-// Model::epilogue).  nc = B * P channels.
+// Backward launch: one kernel.  It computes grad_in; its order-0 workgroup
+// zeroes out0..2 and every workgroup adds its chunk's share of the parameter
+// gradients into them (the chain rule of Model::epilogue applied to the
+// chunk's per-channel sums, one float atomic per output and channel).  A
+// column-sum launch after the scan (fixed-order fp64 sums over row groups)
+// cost 4.4 us plus the launch gap at config 2, where the scan takes ~73 us.
+// nc = B * P channels.
 template <class Model>
 int launch_backward(const typename Model::Params& prm, const void* in, const void* states,
                     const void* gout, void* gin, float* out0, float* out1, float* out2, int64_t L,
@@ -664,7 +656,6 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   const Tile tile = env_tile.T > 0 ? env_tile
                     : kWideFits && wgs256 >= 128 && wgs256 < 2048 ? Tile{16, 16, 1, 1, 2}
                                                                   : Tile{16, 8, 1, 1, 2};
-  constexpr int NS = Model::kSums;
   const int64_t nc = B * P;
   const int64_t CL = int64_t(tile.T) * tile.W;
   const int64_t n_chunks = (L + CL - 1) / CL;
@@ -672,11 +663,6 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   if (n_chunks * n_groups > INT_MAX)
     return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
-  const size_t part_bytes =
-      (static_cast<size_t>(n_chunks) * NS * nc * sizeof(float) + 255) & ~static_cast<size_t>(255);
-  void* ws = nullptr;
-  if (int rc = acquire_workspace(call, part_bytes, &ws)) return rc;
-  ParamReduce red{static_cast<float*>(ws)};
   const int64_t total = n_chunks * n_groups;
   void* payload = nullptr;
   LaunchSync sync{};
@@ -692,7 +678,7 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
                        prm, static_cast<const typename Model::In*>(in),                          \
                        static_cast<const float4*>(states),                                       \
                        static_cast<const typename Model::GIn*>(gout),                            \
-                       static_cast<typename Model::GOut*>(gin), red, zero, static_cast<int>(L),  \
+                       static_cast<typename Model::GOut*>(gin), zero, static_cast<int>(L),       \
                        static_cast<int>(nc), static_cast<int>(n_groups),                         \
                        static_cast<int>(n_chunks), static_cast<unsigned long long*>(payload),    \
                        sync);                                                                    \
@@ -702,8 +688,7 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   OSSM_BWD_TILES(OSSM_LAUNCH_BWD)
 #undef OSSM_LAUNCH_BWD
   if (!launched) return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_BWD names no built tile");
-  return launch_column_sums<NS>(red.partials, P, B, n_chunks,
-                                OscEpilogue<Model>{prm, out0, out1, out2}, stream);
+  return OSSM_OK;
 }
 
 int check_sizes(int64_t L, int64_t B, int64_t P, const char* what) {
@@ -861,6 +846,7 @@ int ossm_dlinoss_forward_noalloc(int variant, const float* a_diag, const float* 
   LaunchSync sync{};
   sync.ticket = reinterpret_cast<unsigned long long*>(s.ptr + kHdrTicket);
   sync.err = reinterpret_cast<unsigned int*>(s.ptr + kHdrErr);
+  sync.flag = reinterpret_cast<unsigned long long*>(s.ptr + kHdrFlag);
   sync.use_ticket = by_ticket ? 1 : 0;
   sync.poison = 0;
   sync.tag = 0;  // ticket order: drawn on the device

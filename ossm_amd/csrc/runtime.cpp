@@ -141,6 +141,7 @@ int acquire_scratch(StreamCall& call, size_t payload_bytes, void** payload, Laun
   char* b = static_cast<char*>(s.base);
   sync->ticket = reinterpret_cast<unsigned long long*>(b + kHdrTicket);
   sync->err = reinterpret_cast<unsigned int*>(b + kHdrErr);
+  sync->flag = reinterpret_cast<unsigned long long*>(b + kHdrFlag);
   sync->use_ticket = by_ticket ? 1 : 0;
   sync->poison = 0;
   sync->tag = 0;  // ticket order: drawn on the device

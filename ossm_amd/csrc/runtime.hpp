@@ -18,6 +18,7 @@ constexpr uint32_t kErrBadTicket = 2u;
 // Layout of the scratch header (bytes from the buffer start).
 constexpr size_t kHdrTicket = 0;    // uint64_t monotonically increasing ticket counter
 constexpr size_t kHdrErr = 64;      // uint32_t error bits
+constexpr size_t kHdrFlag = 128;    // uint64_t: tag of the launch whose outputs are zeroed
 constexpr size_t kHdrBytes = 256;   // payload starts here, 256-byte aligned
 
 // Per-launch synchronisation arguments handed to a look-back kernel.
@@ -34,6 +35,7 @@ constexpr size_t kHdrBytes = 256;   // payload starts here, 256-byte aligned
 struct LaunchSync {
   unsigned long long* ticket;  // device counter, shared by all launches on this scratch
   unsigned int* err;           // device error bits
+  unsigned long long* flag;    // tag of the launch whose accumulated outputs are zeroed
   unsigned int tag;            // records' tag: set on the device in ticket order, by the host in dispatch order
   int use_ticket;              // 1: chunks follow the ticket counter, 0: dispatch order
   int poison;                  // 0 from the host; 1 on the device when the ticket was out of range

@@ -109,6 +109,43 @@ __device__ __forceinline__ void zero_fill_block(const ZeroFill& z) {
       for (int i = threadIdx.x; i < z.n; i += blockDim.x) z.p[k][i] = 0.f;
 }
 
+// The same zero-fill for outputs that the launch's own workgroups then add
+// into (one launch, no column-sum kernel): the workgroup of order 0 writes
+// the zeros through to memory with agent-scope stores, waits until they have
+// all completed, and then publishes the launch's tag in sync.flag.  A
+// workgroup adds its share only after it has read that tag
+// (wait_outputs_zeroed), so no add can land before a zero.  The order-0
+// workgroup is the first to start, so the wait is over long before any
+// workgroup reaches its adds.
+__device__ __forceinline__ void zero_fill_publish(const ZeroFill& z, const LaunchSync& sync) {
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+    if (z.p[k] != nullptr)
+      for (int i = threadIdx.x; i < z.n; i += blockDim.x)
+        __hip_atomic_store(reinterpret_cast<unsigned int*>(z.p[k]) + i, 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);  // every zero of this thread is in memory
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_store(sync.flag, static_cast<unsigned long long>(sync.tag), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits (bounded) until this launch's outputs are zeroed; false after a
+// spin that gave up (kErrSpinTimeout raised: the caller adds NaN instead).
+__device__ __forceinline__ bool wait_outputs_zeroed(const LaunchSync& sync) {
+  uint32_t spins = 0;
+  while (__hip_atomic_load(sync.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
+         static_cast<unsigned long long>(sync.tag)) {
+    if (++spins > kSpinLimit) {
+      __hip_atomic_fetch_or(sync.err, kErrSpinTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return true;
+}
+
 // Zero-fill used where the reference returns zero gradients (empty scans).
 // A kernel rather than hipMemsetAsync: memset nodes are not trusted inside
 // graphs on this platform, and a caller may capture the surrounding work.
