@@ -37,6 +37,7 @@ import json
 import os
 import platform
 import statistics
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -64,19 +65,44 @@ def _valu_floors(case: str) -> dict:
         return {}
 
 
-def _valu_entry(case: str, fwd_ms: float, bwd_ms: float) -> dict:
-    """VALU-floor fractions of this run's event-timed launches: the fraction of
-    each direction's time that the VALU issue of its kernels (rocprof-counted
-    instructions x 4 cycles, v_exp_f32 x 8, over 1024 SIMDs at 2.4 GHz) needs."""
+# Algorithmic VALU floor of the selective scan, in issue slots per (b, d, t, n)
+# state-step (v_exp_f32 counted twice: it occupies the SIMD 8 cycles, other
+# wave64 VALU instructions 4).  Forward: dA = exp(dt A) (mul + exp), h = dA h +
+# x B (mul + fma; x = dt u is per channel-step), y += C h (fma): 5 instructions,
+# 6 slots.  Backward: the forward recompute without y (4 instructions, 5 slots)
+# and the adjoint (gacc = gy C + g, g = gacc dA, q = g h_prev, dA_acc += dt q,
+# S2 += A q, S1 += gacc B, gacc x and gy h for dB / dC: 8), plus one add each
+# for the channel sums of dB and dC: 14 instructions, 15 slots.  Per channel-
+# step work (dt u, the gate, D u, du = dt S1, ddt = u S1 + S2) is over N = 16
+# states and left out.
+SEL_ALG_SLOTS_FWD = 6
+SEL_ALG_SLOTS_BWD = 15
+VALU_SLOT_S = 4 / (1024 * 2.4e9)  # 4 cycles per wave64 slot, 1024 SIMDs at 2.4 GHz
+
+
+def _valu_entry(case: str, fwd_ms: float, bwd_ms: float, state_steps: int) -> dict:
+    """VALU-floor fractions of this run's event-timed launches.  `valu_frac_*`:
+    the fraction of each direction's time that the VALU issue of its kernels
+    as compiled needs (rocprof-counted instructions x 4 cycles, v_exp_f32 x 8,
+    over 1024 SIMDs at 2.4 GHz).  `valu_frac_algorithmic_*`: the same for the
+    algorithmic instruction count (SEL_ALG_SLOTS_* per state-step over 64
+    lanes), so the gap between the two is the instructions the kernels spend on
+    cross-lane sums, addressing and control."""
+    alg_f = state_steps * SEL_ALG_SLOTS_FWD / 64 * VALU_SLOT_S * 1e6
+    alg_b = state_steps * SEL_ALG_SLOTS_BWD / 64 * VALU_SLOT_S * 1e6
+    out = {"valu_floor_algorithmic_us_fwd": alg_f, "valu_floor_algorithmic_us_bwd": alg_b,
+           "valu_frac_algorithmic_fwd": alg_f / (fwd_ms * 1e3),
+           "valu_frac_algorithmic_bwd": alg_b / (bwd_ms * 1e3)}
     fl = _valu_floors(case)
     if not fl:
-        return {}
+        return out
     f_us = fl.get("fwd", {}).get("valu_floor_us")
     b_us = sum(fl.get(k, {}).get("valu_floor_us", 0.0) for k in ("bwd", "finish"))
-    return {"valu_floor_us_fwd": f_us, "valu_floor_us_bwd": b_us,
-            "valu_frac_fwd": f_us / (fwd_ms * 1e3) if f_us else None,
-            "valu_frac_bwd": b_us / (bwd_ms * 1e3) if b_us else None,
-            "valu_source": SEL_PROFILE.name}
+    out.update({"valu_floor_us_fwd": f_us, "valu_floor_us_bwd": b_us,
+                "valu_frac_fwd": f_us / (fwd_ms * 1e3) if f_us else None,
+                "valu_frac_bwd": b_us / (bwd_ms * 1e3) if b_us else None,
+                "valu_source": SEL_PROFILE.name})
+    return out
 
 
 # ----------------------------------------------------------------- timing
@@ -236,8 +262,6 @@ def linoss_im_inputs(torch, L, B, P, device, H=64, seed=0):
 # ------------------------------------------------------------ CPU baseline
 def _cpu_model() -> str:
     """lscpu's "Model name", else /proc/cpuinfo's "model name"."""
-    import subprocess
-
     try:
         res = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10)
         for line in res.stdout.splitlines():
@@ -421,7 +445,7 @@ def _detail_configs(torch, K, dev, reps=20):
                     "hbm_frac_fwd": fb / (tf / 1e3) / PEAK_HBM,
                     "hbm_frac_bwd": bb / (tb / 1e3) / PEAK_HBM,
                     "hbm_frac_fwd_bwd": (fb + bb) / ((tf + tb) / 1e3) / PEAK_HBM,
-                    **_valu_entry(key, tf, tb)}
+                    **_valu_entry(key, tf, tb, T * N)}
         del u, dts, Bm, Cm, z, go, res
     # C4 as specified: bf16 storage of u, dt, B, C, z, outputs and input gradients;
     # fp32 state, sums, A and dA (ossm_selective_*_bf16)
@@ -440,7 +464,7 @@ def _detail_configs(torch, K, dev, reps=20):
                                 "hbm_frac_fwd": fb / (tf / 1e3) / PEAK_HBM,
                                 "hbm_frac_bwd": bb / (tb / 1e3) / PEAK_HBM,
                                 "hbm_frac_fwd_bwd": (fb + bb) / ((tf + tb) / 1e3) / PEAK_HBM,
-                                **_valu_entry("c4_selective_bf16", tf, tb)}
+                                **_valu_entry("c4_selective_bf16", tf, tb, T * N)}
     del u, dts, Bm, Cm, z, go, res
     # Fused D-LinOSS layer forward at config 2's shape (H = P = 128): one kernel,
     # MFMA-bound (8 H P flops per (b, t)); against the unfused layer's steps
@@ -577,6 +601,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-detail", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--issue-rate", action="store_true",
+                    help="run the VALU issue-rate microbenchmark (cycles per wave-instruction)")
     ap.add_argument("--case", choices=CASES,
                     help="run only this BASELINE config (--steps timed passes), for profiling")
     ap.add_argument("--events-every", type=int, default=4,
@@ -591,6 +617,12 @@ def main() -> int:
         return 2
     if args.calibrate_copy:
         return calibrate_copy()
+    if args.issue_rate:
+        # a child process of its own, started before this process touches the GPU
+        from ossm_amd import build as hip_build
+        if not hip_build.ISSUE_RATE.exists():
+            raise SystemExit(f"{hip_build.ISSUE_RATE} is not built: run python -m ossm_amd.build")
+        return subprocess.run([str(hip_build.ISSUE_RATE)]).returncode
     if args.case:
         return run_case(args.case, args.steps, args.warmup)
 

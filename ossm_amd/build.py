@@ -25,6 +25,9 @@ LIB = LIBDIR / "libossm_scan.so"
 
 SOURCES = ["runtime.cpp", "oscillator_scan.hip", "selective_scan.hip", "sdlinoss_scan.hip",
            "diag_scan.hip", "dlinoss_layer.hip", "mamba_conv.hip", "scan_f64.hip"]
+# standalone measurement program (not linked into the library)
+ISSUE_RATE_SRC = "valu_issue_rate.hip"
+ISSUE_RATE = LIBDIR / "valu_issue_rate"
 ARCH = "gfx950"
 
 
@@ -72,8 +75,12 @@ def build(verbose: bool = True) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
+    cmd = [hipcc(), *_flags(), "-x", "hip", str(CSRC / ISSUE_RATE_SRC), "-o", str(ISSUE_RATE)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {ISSUE_RATE_SRC}:\n{res.stderr}")
     if verbose:
-        print(f"built {LIB.relative_to(ROOT)}")
+        print(f"built {LIB.relative_to(ROOT)}, {ISSUE_RATE.relative_to(ROOT)}")
     return LIB
 
 
