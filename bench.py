@@ -10,9 +10,12 @@ synthetic inputs already resident in HBM.  Timing uses HIP events recorded on
 the stream the kernels run on (torch's current stream); a device-side spin
 queued just before the timed region keeps the GPU busy while the host enqueues
 the timed launches, so the events measure the kernels, not host launch gaps.
-``value`` is the whole timed region; the per-launch durations (roofline,
-``detail``) come from events recorded inside it on every fourth step
-(``--events-every``), as each record adds ~3 us of GPU time.
+``value`` is the whole timed region, which holds no event between launches
+(every event costs ~3 us of GPU time per launch).  The per-launch durations
+(roofline, ``detail``) come from a second pass of the same steps right after
+it, in which the forward and backward kernels record their own start and end
+events (``ossm_time_next_launch``, hipExtLaunchKernel), so each pair spans one
+kernel and no event packet.
 
 One JSON line is printed.  Besides the contract fields:
   roofline      HBM roofline of the dominant launch (algorithmic bytes / its
@@ -142,6 +145,11 @@ class TimingEvent:
     def _check(rc: int, what: str) -> None:
         if rc != 0:
             raise RuntimeError(f"{what} failed with HIP error {rc}")
+
+    @property
+    def handle(self) -> int:
+        """The hipEvent_t, for ossm_time_next_launch."""
+        return self._ev.value
 
     def record(self) -> None:
         import ctypes
@@ -605,8 +613,8 @@ def main() -> int:
                     help="run the VALU issue-rate microbenchmark (cycles per wave-instruction)")
     ap.add_argument("--case", choices=CASES,
                     help="run only this BASELINE config (--steps timed passes), for profiling")
-    ap.add_argument("--events-every", type=int, default=4,
-                    help="record per-launch events on every N-th timed step")
+    ap.add_argument("--events-every", type=int, default=1,
+                    help="per-launch events on every N-th step of the launch-timing pass")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -643,35 +651,46 @@ def main() -> int:
         bwd(a, gam, dt, bu, st, go)
     torch.cuda.synchronize()
 
-    # Per-launch events on every EVERY-th step of the timed region (even a
-    # fence-free record costs ~1.5 us of GPU time: three on every step made a
-    # step 177.5 instead of 173 us), the whole region between `start` and `end`.
-    every = max(1, args.events_every)
-    ev = [(TimingEvent(torch), TimingEvent(torch), TimingEvent(torch)) if i % every == 0 else None
-          for i in range(args.steps)]
+    # The timed region: `steps` forward + backward steps with no event between
+    # launches (any event queued between kernels, or bound to a kernel, costs
+    # ~3 us of GPU time per launch, ~2 % of a step), between `start` and `end`.
     start, end = TimingEvent(torch), TimingEvent(torch)
     torch.cuda.synchronize()
     _backlog(torch, ms=max(25.0, 0.5 * args.steps))
     start.record()
-    for trio in ev:
-        if trio is None:
+    for _ in range(args.steps):
+        st = fwd(a, gam, dt, bu)
+        bwd(a, gam, dt, bu, st, go)
+    end.record()
+    torch.cuda.synchronize()
+    err_bits = _lib.device_error_bits(dev)
+    total_ms = start.elapsed_time(end)
+
+    # Per-launch durations: the same steps again (at least 20), the forward and
+    # backward kernels of every EVERY-th step recording their own start and end
+    # events (ossm_time_next_launch: hipExtLaunchKernel binds them to the
+    # dispatch, so the pair spans the kernel alone, not the event packets).
+    every = max(1, args.events_every)
+    n_timing = max(20, args.steps)
+    ev = [tuple(TimingEvent(torch) for _ in range(4)) if i % every == 0 else None
+          for i in range(n_timing)]
+    torch.cuda.synchronize()
+    _backlog(torch, ms=max(25.0, 0.5 * n_timing))
+    for quad in ev:
+        if quad is None:
             st = fwd(a, gam, dt, bu)
             bwd(a, gam, dt, bu, st, go)
             continue
-        e0, e1, e2 = trio
-        e0.record()
+        f0, f1, b0, b1 = quad
+        _lib.time_next_launch(f0.handle, f1.handle)
         st = fwd(a, gam, dt, bu)
-        e1.record()
+        _lib.time_next_launch(b0.handle, b1.handle)
         bwd(a, gam, dt, bu, st, go)
-        e2.record()
-    end.record()
     torch.cuda.synchronize()
-    ev = [trio for trio in ev if trio is not None]
-
-    err_bits = _lib.device_error_bits(dev)
-    total_ms = start.elapsed_time(end)
-    fwd_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1, _ in ev)
-    bwd_ms = statistics.mean(e1.elapsed_time(e2) for _, e1, e2 in ev)
+    ev = [quad for quad in ev if quad is not None]
+    err_bits |= _lib.device_error_bits(dev)
+    fwd_ms = statistics.mean(f0.elapsed_time(f1) for f0, f1, _, _ in ev)
+    bwd_ms = statistics.mean(b0.elapsed_time(b1) for _, _, b0, b1 in ev)
     ms_per_step = total_ms / args.steps
     units = L * B * P
     value = units * args.steps / (total_ms / 1e3)
@@ -704,6 +723,7 @@ def main() -> int:
         "algorithmic_bytes_per_launch": dom["bytes"],
         "bytes_per_state_step": DL_BYTES_BWD if dom["key"] == "backward" else DL_BYTES_FWD,
         "mean_launch_ms": dom["ms"],
+        "launch_timing": "kernel-bound HIP events, launch-timing pass after the timed region",
     }
     out = {
         "metric": METRIC,
@@ -729,7 +749,9 @@ def main() -> int:
                      "GBps": bwd_bw / 1e9, "hbm_frac": bwd_bw / PEAK_HBM},
         "fwd_bwd_hbm_frac": units * (DL_BYTES_FWD + DL_BYTES_BWD) / (ms_per_step / 1e3) / PEAK_HBM,
         "fwd_bwd_kernel_hbm_frac": units * (DL_BYTES_FWD + DL_BYTES_BWD) / ((fwd_ms + bwd_ms) / 1e3) / PEAK_HBM,
-        "launch_events": f"every {every}th timed step ({len(ev)} of {args.steps})",
+        "launch_events": (f"kernel-bound start/stop events (hipExtLaunchKernel) in a second pass "
+                          f"of {n_timing} steps after the timed region, on {len(ev)} of them"),
+        "launch_sum_over_step": (fwd_ms + bwd_ms) / ms_per_step,
         "device_error_bits": err_bits,
     }
     del st

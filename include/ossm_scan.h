@@ -56,7 +56,7 @@ enum {
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
 /* Library ABI version (bumped on any change of the entry points or their
-   behaviour; currently 13). */
+   behaviour; currently 14). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -84,6 +84,19 @@ uint32_t ossm_device_error_bits(ossm_stream_t stream);
  * failure path only.
  */
 int ossm_test_skew_tickets(ossm_stream_t stream, uint64_t delta);
+
+/*
+ * Measurement hook, no counterpart in the reference (for benchmarks and
+ * profilers): the next oscillatory-scan kernel that this host thread launches
+ * through ossm_dlinoss_{forward,backward} or ossm_linoss_{forward,backward}
+ * records `start_event` and `stop_event` (hipEvent_t, created by the caller)
+ * as its own start and end, through hipExtLaunchKernel, so no event packet is
+ * queued between kernels.
+ * hipEventElapsedTime of the pair is then that kernel's duration.  The setting
+ * is used once; passing two nulls clears it.  A launch under stream capture
+ * does not take it and fails with OSSM_ERR_UNSUPPORTED while it is set.
+ */
+int ossm_time_next_launch(void* start_event, void* stop_event);
 
 /*
  * D-LinOSS forward, replaces dlinoss_<v>_forward:

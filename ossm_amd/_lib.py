@@ -25,6 +25,7 @@ _dp = ctypes.c_void_p  # double* passed as raw device addresses
 _SIGNATURES = {
     "ossm_abi_version": (ctypes.c_int, []),
     "ossm_test_skew_tickets": (ctypes.c_int, [_vp, ctypes.c_uint64]),
+    "ossm_time_next_launch": (ctypes.c_int, [_vp, _vp]),
     "ossm_last_error": (ctypes.c_char_p, []),
     "ossm_device_error_bits": (ctypes.c_uint32, [_vp]),
     "ossm_dlinoss_forward": (
@@ -169,3 +170,10 @@ def device_error_bits(device: Optional[torch.device] = None) -> int:
     dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
     with torch.cuda.device(dev):
         return int(load().ossm_device_error_bits(torch.cuda.current_stream(dev).cuda_stream))
+
+
+def time_next_launch(start_event: Optional[int], stop_event: Optional[int]) -> None:
+    """The next LinOSS / D-LinOSS scan kernel this thread launches records these
+    two hipEvent_t handles as its own start and end (no event packets between
+    kernels); two Nones clear the setting."""
+    check(load().ossm_time_next_launch(start_event, stop_event))

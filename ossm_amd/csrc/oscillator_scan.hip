@@ -35,6 +35,7 @@
 //   inside the scan kernel was measured 3x slower: each agent-scope release
 //   fence writes back the XCD's L2, dirty with the workgroup's grad_bu rows.)
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -588,25 +589,33 @@ FwdPlan fwd_plan(int64_t L, int64_t nc) {
 }
 
 // Enqueues the forward kernel of plan `pl` with look-back records at
-// `payload` and launch bookkeeping `sync`.  The caller undoes its ticket
+// `payload` and launch bookkeeping `sync`; `tm` (when set) are events the
+// launch records as its own start and end.  The caller undoes its ticket
 // reservation when this returns an error (nothing was launched).
 template <class Model>
 int enqueue_forward(const FwdPlan& pl, const typename Model::Params& prm, const void* in, void* out,
-                    int64_t L, int64_t nc, hipStream_t stream, void* payload, const LaunchSync& sync) {
+                    int64_t L, int64_t nc, hipStream_t stream, void* payload, const LaunchSync& sync,
+                    const LaunchTiming& tm = LaunchTiming{}) {
   const Tile& tile = pl.tile;
   const dim3 grid(static_cast<unsigned>(pl.total));
   bool launched = false;
+#define OSSM_FWD_ARGS                                                                         \
+  prm, static_cast<const typename Model::In*>(in), static_cast<float4*>(out),                 \
+      static_cast<int>(L), static_cast<int>(nc), static_cast<int>(pl.n_groups),               \
+      static_cast<int>(pl.n_chunks), static_cast<unsigned long long*>(payload), sync
 #define OSSM_LAUNCH_FWD(TT, WW, OO)                                                           \
   if (!launched && tile.T == TT && tile.W == WW && tile.O == OO) {                            \
-    hipLaunchKernelGGL((osc_forward_kernel<Model, TT, WW, OO>), grid, dim3(WW * kWave), 0, stream, \
-                       prm, static_cast<const typename Model::In*>(in),                       \
-                       static_cast<float4*>(out), static_cast<int>(L), static_cast<int>(nc),  \
-                       static_cast<int>(pl.n_groups), static_cast<int>(pl.n_chunks),          \
-                       static_cast<unsigned long long*>(payload), sync);                      \
+    if (tm.start != nullptr)                                                                  \
+      hipExtLaunchKernelGGL((osc_forward_kernel<Model, TT, WW, OO>), grid, dim3(WW * kWave), 0, \
+                            stream, tm.start, tm.stop, 0, OSSM_FWD_ARGS);                     \
+    else                                                                                      \
+      hipLaunchKernelGGL((osc_forward_kernel<Model, TT, WW, OO>), grid, dim3(WW * kWave), 0,  \
+                         stream, OSSM_FWD_ARGS);                                              \
     launched = true;                                                                          \
   }
   OSSM_FWD_TILES(OSSM_LAUNCH_FWD)
 #undef OSSM_LAUNCH_FWD
+#undef OSSM_FWD_ARGS
   if (!launched) return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_FWD names no built tile");
   return launch_check("osc_forward_kernel");
 }
@@ -619,10 +628,12 @@ int launch_forward(const typename Model::Params& prm, const void* in, void* out,
   const FwdPlan pl = fwd_plan(L, nc);
   if (pl.total > INT_MAX)
     return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
+  LaunchTiming tm;
+  if (int rc = take_launch_timing(call, &tm)) return rc;
   void* payload = nullptr;
   LaunchSync sync{};
   if (int rc = acquire_scratch(call, pl.rec_bytes, &payload, &sync)) return rc;
-  if (int rc = enqueue_forward<Model>(pl, prm, in, out, L, nc, stream, payload, sync)) return rc;
+  if (int rc = enqueue_forward<Model>(pl, prm, in, out, L, nc, stream, payload, sync, tm)) return rc;
   return OSSM_OK;
 }
 
@@ -664,29 +675,34 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
     return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * 4 * nc * sizeof(unsigned long long);
   const int64_t total = n_chunks * n_groups;
+  LaunchTiming tm;
+  if (int rc = take_launch_timing(call, &tm)) return rc;
   void* payload = nullptr;
   LaunchSync sync{};
   if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
   const ZeroFill zero{{out0, out1, out2}, static_cast<int>(Model::kOutsPerColumn * P)};
+  const dim3 grid(static_cast<unsigned>(total));
   bool launched = false;
+#define OSSM_BWD_ARGS                                                                            \
+  prm, static_cast<const typename Model::In*>(in), static_cast<const float4*>(states),           \
+      static_cast<const typename Model::GIn*>(gout), static_cast<typename Model::GOut*>(gin),    \
+      zero, static_cast<int>(L), static_cast<int>(nc), static_cast<int>(n_groups),               \
+      static_cast<int>(n_chunks), static_cast<unsigned long long*>(payload), sync
 #define OSSM_LAUNCH_BWD(TT, WW, OO, HH, SS)                                                      \
   if (!launched && tile.T == TT && tile.W == WW && tile.O == OO && tile.H == HH &&               \
       tile.S == SS) {                                                                            \
-    hipLaunchKernelGGL((osc_backward_kernel<Model, TT, WW, OO, HH, SS>),                         \
-                       dim3(static_cast<unsigned>(total)),                                       \
-                       dim3(WW * kWave), 0, stream,                                              \
-                       prm, static_cast<const typename Model::In*>(in),                          \
-                       static_cast<const float4*>(states),                                       \
-                       static_cast<const typename Model::GIn*>(gout),                            \
-                       static_cast<typename Model::GOut*>(gin), zero, static_cast<int>(L),       \
-                       static_cast<int>(nc), static_cast<int>(n_groups),                         \
-                       static_cast<int>(n_chunks), static_cast<unsigned long long*>(payload),    \
-                       sync);                                                                    \
-    if (int rc = launch_check("osc_backward_kernel")) return rc;                        \
+    if (tm.start != nullptr)                                                                     \
+      hipExtLaunchKernelGGL((osc_backward_kernel<Model, TT, WW, OO, HH, SS>), grid,              \
+                            dim3(WW * kWave), 0, stream, tm.start, tm.stop, 0, OSSM_BWD_ARGS);   \
+    else                                                                                         \
+      hipLaunchKernelGGL((osc_backward_kernel<Model, TT, WW, OO, HH, SS>), grid,                 \
+                         dim3(WW * kWave), 0, stream, OSSM_BWD_ARGS);                            \
+    if (int rc = launch_check("osc_backward_kernel")) return rc;                                 \
     launched = true;                                                                             \
   }
   OSSM_BWD_TILES(OSSM_LAUNCH_BWD)
 #undef OSSM_LAUNCH_BWD
+#undef OSSM_BWD_ARGS
   if (!launched) return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_BWD names no built tile");
   return OSSM_OK;
 }

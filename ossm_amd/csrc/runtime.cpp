@@ -11,6 +11,9 @@
 #include "../../include/ossm_scan.h"
 
 namespace ossm {
+
+thread_local LaunchTiming t_launch_timing;
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -73,6 +76,17 @@ int hip_check(hipError_t e, const char* what) {
 
 int launch_check(const char* what) {
   return hip_check(hipGetLastError(), what);
+}
+
+int take_launch_timing(const StreamCall& call, LaunchTiming* out) {
+  *out = LaunchTiming{};
+  if (t_launch_timing.start == nullptr) return OSSM_OK;
+  if (call.capturing())
+    return set_error(OSSM_ERR_UNSUPPORTED,
+                     "ossm_time_next_launch: timing events cannot be recorded under stream capture");
+  *out = t_launch_timing;
+  t_launch_timing = LaunchTiming{};
+  return OSSM_OK;
 }
 
 bool scan_order_by_ticket() {
@@ -195,7 +209,7 @@ int release_buffer(void* p, bool captured, const char* what) {
 
 extern "C" {
 
-int ossm_abi_version(void) { return 13; }
+int ossm_abi_version(void) { return 14; }
 
 const char* ossm_last_error(void) { return ossm::g_last_error.c_str(); }
 
@@ -226,6 +240,15 @@ uint32_t ossm_device_error_bits(ossm_stream_t stream_v) {
   }
   if (bits != 0) (void)hipMemset(base + ossm::kHdrErr, 0, sizeof(bits));
   return bits | fixed_bits;
+}
+
+int ossm_time_next_launch(void* start_event, void* stop_event) {
+  ossm::clear_error();
+  if ((start_event == nullptr) != (stop_event == nullptr))
+    return ossm::set_error(OSSM_ERR_INVALID_ARGUMENT,
+                           "ossm_time_next_launch: give both events or neither");
+  ossm::t_launch_timing = {static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
+  return OSSM_OK;
 }
 
 int ossm_test_skew_tickets(ossm_stream_t stream_v, uint64_t delta) {

@@ -47,6 +47,20 @@ constexpr unsigned long long kEpochSpan = 1ull << 32;
 // default) or by workgroup index (environment OSSM_SCAN_ORDER=dispatch).
 bool scan_order_by_ticket();
 
+// Events that the next oscillatory-scan launch on this host thread records as
+// its own start and end (ossm_time_next_launch); both null when unset.
+struct LaunchTiming {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+extern thread_local LaunchTiming t_launch_timing;
+
+// Takes (and clears) this thread's launch timing for a launch on `call`'s
+// stream.  A set timing under stream capture is refused: returns
+// OSSM_ERR_UNSUPPORTED and leaves it set.
+class StreamCall;
+int take_launch_timing(const StreamCall& call, LaunchTiming* out);
+
 // Records the message for ossm_last_error() and returns `status`.
 int set_error(int status, const std::string& msg);
 int clear_error();

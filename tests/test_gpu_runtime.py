@@ -13,6 +13,7 @@ captured call draws fresh orders and tags on every replay.
 from __future__ import annotations
 
 import threading
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -271,3 +272,77 @@ def test_protocol_failure_gives_nan_not_garbage(K):
     grads = K.dlinoss_imex1_backward(*args, to_dev(st), to_dev(go))
     assert_close(to_np(grads[3]), rgrads[3], RTOL, ATOL, "grad_bu after recovery")
     no_device_errors()
+
+
+def test_time_next_launch_records_kernel_events(K):
+    """ossm_time_next_launch: the next D-LinOSS forward and backward kernels
+    record the given events as their own start and end.  Each elapsed time is
+    positive and below the whole call's wall time between host syncs; the
+    outputs equal those of untimed calls to the usual run-to-run tolerance (the
+    look-back may associate carries differently per run); a set timing is
+    refused under stream capture
+    (RuntimeError, nothing enqueued) and stays set for the next eager launch."""
+    import ctypes
+    import time
+
+    from ossm_amd import _lib
+
+    # the HIP runtime torch loaded (a second copy of the runtime must not load)
+    lib = Path(torch.__file__).resolve().parent / "lib" / "libamdhip64.so"
+    hip = ctypes.CDLL(str(lib) if lib.exists() else "libamdhip64.so")
+    evs = []
+    for _ in range(4):
+        e = ctypes.c_void_p()
+        assert hip.hipEventCreate(ctypes.byref(e)) == 0
+        evs.append(e)
+
+    def elapsed(e0, e1):
+        ms = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1) == 0
+        return ms.value
+
+    L, B, P = 4096, 8, 128
+    a, g, dt, bu, go = dlinoss_inputs(L, B, P, seed=51, variant="imex1")
+    args = [to_dev(x) for x in (a, g, dt, bu)]
+    god = to_dev(go)
+    announce("runtime: time_next_launch")
+    st_ref = K.dlinoss_imex1_forward(*args)
+    gr_ref = K.dlinoss_imex1_backward(*args, st_ref, god)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    _lib.time_next_launch(evs[0].value, evs[1].value)
+    st = K.dlinoss_imex1_forward(*args)
+    _lib.time_next_launch(evs[2].value, evs[3].value)
+    gr = K.dlinoss_imex1_backward(*args, st, god)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    f_ms, b_ms = elapsed(evs[0], evs[1]), elapsed(evs[2], evs[3])
+    assert 0.0 < f_ms < wall_ms and 0.0 < b_ms < wall_ms, (f_ms, b_ms, wall_ms)
+    st_np = to_np(st_ref)
+    assert_close(to_np(st), st_np, RTOL, ATOL, "timed forward")
+    for x, r, name in zip(gr, gr_ref, ("grad_a", "grad_g", "grad_step", "grad_bu")):
+        rn = to_np(r)
+        assert_close(to_np(x), rn, RTOL, 2e-5 * max(1.0, float(np.abs(rn).max())), name)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        K.dlinoss_imex1_forward(*args)  # the side stream's scratch exists
+    side.synchronize()
+    _lib.time_next_launch(evs[0].value, evs[1].value)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        graph.capture_begin()
+        try:
+            with pytest.raises(RuntimeError, match="under stream capture"):
+                K.dlinoss_imex1_forward(*args)
+        finally:
+            graph.capture_end()
+    torch.cuda.synchronize()
+    st2 = K.dlinoss_imex1_forward(*args)  # takes the timing left set
+    torch.cuda.synchronize()
+    assert elapsed(evs[0], evs[1]) > 0.0
+    assert_close(to_np(st2), st_np, RTOL, ATOL, "forward after the refused capture")
+    no_device_errors()
+    for e in evs:
+        hip.hipEventDestroy(e)

@@ -41,7 +41,7 @@ def test_header_declares_the_entry_points():
               "ossm_diag_scan_forward", "ossm_diag_scan_backward", "ossm_diag_scan_forward_f64",
               "ossm_diag_scan_backward_f64", "ossm_dlinoss_layer_forward", "ossm_dlinoss_layer_backward",
               "ossm_selective_mamba_forward", "ossm_selective_mamba_backward",
-              "ossm_mamba_conv_forward", "ossm_mamba_conv_backward"):
+              "ossm_mamba_conv_forward", "ossm_mamba_conv_backward", "ossm_time_next_launch"):
         assert n in names, n
 
 
@@ -57,7 +57,22 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     # every declared symbol has a ctypes signature in the binding
     assert set(_declared_functions()) == set(_lib.EXPORTED)
-    assert _lib.load().ossm_abi_version() == 13
+    assert _lib.load().ossm_abi_version() == 14
+
+
+def test_time_next_launch_argument_checks():
+    """The measurement hook takes both events or neither; it makes no HIP call
+    when set, so it runs here."""
+    from ossm_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libossm_scan.so not built (python -m ossm_amd.build)")
+    lib = _lib.load()
+    assert lib.ossm_time_next_launch(None, ctypes.c_void_p(16)) == 1  # OSSM_ERR_INVALID_ARGUMENT
+    assert b"both events or neither" in lib.ossm_last_error()
+    assert lib.ossm_time_next_launch(None, None) == 0
+    with pytest.raises(RuntimeError, match="both events or neither"):
+        _lib.time_next_launch(16, None)
 
 
 def test_dropin_module_has_every_reference_name():
