@@ -247,6 +247,25 @@ def selective_inputs(torch, Bz, D, L, N, device, seed=0, gated=True):
     return u, dt, A.contiguous(), Bm, Cm, z, go
 
 
+def skip_d(torch, D, device, seed=0):
+    """The configs' skip D ~ N(0,1), one float32 per channel."""
+    g = torch.Generator(device=device).manual_seed(seed + 77)
+    return torch.randn(D, device=device, generator=g)
+
+
+def selective_calls(K, case):
+    """(forward, backward) of a selective case: configs 3 and 4 name a D skip and
+    run through the skip entry points (selective_scan_cuda_skip, fp32 or bf16
+    by the inputs' dtype); the C4-shape fp32 case runs the reference's own API."""
+    if case == "c4_shape_selective_fp32":
+        return (lambda u, dt, A, B, C, D, z: K.selective_scan_cuda(u, dt, A, B, C, z),
+                lambda g, u, dt, A, B, C, D, z, ck, raw: K.selective_scan_cuda_backward(
+                    g, u, dt, A, B, C, z, ck, raw, 16))
+    return (K.selective_scan_cuda_skip,
+            lambda g, u, dt, A, B, C, D, z, ck, raw: K.selective_scan_cuda_skip_backward(
+                g, u, dt, A, B, C, D, z, ck, raw))
+
+
 def linoss_im_inputs(torch, L, B, P, device, H=64, seed=0):
     """Config-1: A = relu(N(0,1)) + 0.1, dt = sigmoid(N(0,1)), B complex N(0,1/H),
     u ~ N(0,1); LinOSS-IM transition and b_seq = (bu m11 dt, bu m21 dt)
@@ -437,18 +456,20 @@ def _detail_configs(torch, K, dev, reps=20):
                                    "hbm_frac_bwd": n * 24 / (tb / 1e3) / PEAK_HBM,
                                    "bytes_per_state_step": [16, 24]}
     del b_seq, go, st
-    # C3 / C4-shape: selective scan fwd+bwd, fp32, gated
+    # C3 (fp32, gate and D skip) / C4-shape (fp32, gate, the reference's API):
+    # selective scan fwd+bwd
     for key, (Bz, D, L, N) in (("c3_selective_fp32", (256, 128, 200, 16)),
                                ("c4_shape_selective_fp32", (16, 1536, 2048, 16))):  # keys of SEL_PROFILE
         u, dts, A, Bm, Cm, z, go = selective_inputs(torch, Bz, D, L, N, dev)
-        res = K.selective_scan_cuda(u, dts, A, Bm, Cm, z)
-        tf = _ev_time(torch, lambda: K.selective_scan_cuda(u, dts, A, Bm, Cm, z), reps, 3)
-        tb = _ev_time(torch, lambda: K.selective_scan_cuda_backward(
-            go, u, dts, A, Bm, Cm, z, res[1], res[2], 16), reps, 3)
+        Dk = skip_d(torch, D, dev)
+        fwd, bwd = selective_calls(K, key)
+        res = fwd(u, dts, A, Bm, Cm, Dk, z)
+        tf = _ev_time(torch, lambda: fwd(u, dts, A, Bm, Cm, Dk, z), reps, 3)
+        tb = _ev_time(torch, lambda: bwd(go, u, dts, A, Bm, Cm, Dk, z, res[1], res[2]), reps, 3)
         T = Bz * D * L
         fb = T * 16 + Bz * L * N * 8          # u, dt, z in; out out; B, C in
         bb = T * 28 + Bz * L * N * 16         # u, dt, z, dout in; du, ddt, dz out; B, C in; dB, dC out
-        out[key] = {"fwd_ms": tf, "bwd_ms": tb,
+        out[key] = {"fwd_ms": tf, "bwd_ms": tb, "skip_d": key != "c4_shape_selective_fp32",
                     "state_steps_per_s_fwd_bwd": T * N / ((tf + tb) / 1e3),
                     "hbm_frac_fwd": fb / (tf / 1e3) / PEAK_HBM,
                     "hbm_frac_bwd": bb / (tb / 1e3) / PEAK_HBM,
@@ -456,18 +477,19 @@ def _detail_configs(torch, K, dev, reps=20):
                     **_valu_entry(key, tf, tb, T * N)}
         del u, dts, Bm, Cm, z, go, res
     # C4 as specified: bf16 storage of u, dt, B, C, z, outputs and input gradients;
-    # fp32 state, sums, A and dA (ossm_selective_*_bf16)
+    # fp32 state, sums, A, D, dA and dD; gate and D skip
     Bz, D, L, N = 16, 1536, 2048, 16
     u, dts, A, Bm, Cm, z, go = (x if x.dtype != torch.float32 or x.dim() == 2 else x.bfloat16()
                                 for x in selective_inputs(torch, Bz, D, L, N, dev))
-    res = K.selective_scan_cuda_bf16(u, dts, A, Bm, Cm, z)
-    tf = _ev_time(torch, lambda: K.selective_scan_cuda_bf16(u, dts, A, Bm, Cm, z), reps, 3)
-    tb = _ev_time(torch, lambda: K.selective_scan_cuda_bf16_backward(
-        go, u, dts, A, Bm, Cm, z, res[1], res[2], 16), reps, 3)
+    Dk = skip_d(torch, D, dev)
+    fwd, bwd = selective_calls(K, "c4_selective_bf16")
+    res = fwd(u, dts, A, Bm, Cm, Dk, z)
+    tf = _ev_time(torch, lambda: fwd(u, dts, A, Bm, Cm, Dk, z), reps, 3)
+    tb = _ev_time(torch, lambda: bwd(go, u, dts, A, Bm, Cm, Dk, z, res[1], res[2]), reps, 3)
     T = Bz * D * L
     fb = T * 8 + Bz * L * N * 4               # as above at 2 bytes per element
     bb = T * 14 + Bz * L * N * 8
-    out["c4_selective_bf16"] = {"fwd_ms": tf, "bwd_ms": tb,
+    out["c4_selective_bf16"] = {"fwd_ms": tf, "bwd_ms": tb, "skip_d": True,
                                 "state_steps_per_s_fwd_bwd": T * N / ((tf + tb) / 1e3),
                                 "hbm_frac_fwd": fb / (tf / 1e3) / PEAK_HBM,
                                 "hbm_frac_bwd": bb / (tb / 1e3) / PEAK_HBM,
@@ -573,13 +595,12 @@ def run_case(name: str, steps: int, warmup: int) -> int:
         xs = selective_inputs(torch, *shape, dev)
         if name == "c4_selective_bf16":
             xs = tuple(x if x.dim() == 2 else x.bfloat16() for x in xs)
-            fwd, bwd = K.selective_scan_cuda_bf16, K.selective_scan_cuda_bf16_backward
-        else:
-            fwd, bwd = K.selective_scan_cuda, K.selective_scan_cuda_backward
+        fwd, bwd = selective_calls(K, name)
         u, dts, A, Bm, Cm, z, go = xs
-        res = fwd(u, dts, A, Bm, Cm, z)
-        out["fwd_ms"] = _ev_time(torch, lambda: fwd(u, dts, A, Bm, Cm, z), steps, warmup)
-        out["bwd_ms"] = _ev_time(torch, lambda: bwd(go, u, dts, A, Bm, Cm, z, res[1], res[2], 16),
+        Dk = skip_d(torch, shape[1], dev)
+        res = fwd(u, dts, A, Bm, Cm, Dk, z)
+        out["fwd_ms"] = _ev_time(torch, lambda: fwd(u, dts, A, Bm, Cm, Dk, z), steps, warmup)
+        out["bwd_ms"] = _ev_time(torch, lambda: bwd(go, u, dts, A, Bm, Cm, Dk, z, res[1], res[2]),
                                  steps, warmup)
     out["device_error_bits"] = _lib.device_error_bits(dev)
     print(json.dumps(out), flush=True)

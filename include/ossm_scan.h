@@ -56,7 +56,7 @@ enum {
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
 /* Library ABI version (bumped on any change of the entry points or their
-   behaviour; currently 14). */
+   behaviour; currently 15). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -305,6 +305,36 @@ int ossm_selective_backward_bf16(const void* grad_out, const void* u, const void
                                  void* ddt, float* dA, void* dB, void* dC, void* dgate,
                                  int64_t batch, int64_t dim, int64_t length, int64_t dstate,
                                  ossm_stream_t stream);
+
+/*
+ * Selective scan with a per-channel skip D, an extension with no counterpart in
+ * the reference (whose selective kernels take no D, selective_scan_cuda.cu:
+ * 253-393; BASELINE configs 3 and 4 name a D skip): the forward of
+ * ossm_selective_forward (elem OSSM_ELEM_F32) or ossm_selective_forward_bf16
+ * (OSSM_ELEM_BF16) with y_t = sum_n Cm_tn h_t + D u_t, i.e.
+ *   raw_out = y + D u,  out = raw_out * silu(gate)  (out = raw_out without a gate),
+ * fused into the scan kernel.  d_skip [dim] f32, not null.
+ */
+enum { OSSM_ELEM_F32 = 0, OSSM_ELEM_BF16 = 1 };
+int ossm_selective_forward_skip(int elem, const void* u, const void* dt, const float* A,
+                                const void* Bm, const void* Cm, const float* d_skip,
+                                const void* gate, void* out, void* raw_out, float* chunk_states,
+                                int64_t batch, int64_t dim, int64_t length, int64_t dstate,
+                                ossm_stream_t stream);
+
+/*
+ * Backward of ossm_selective_forward_skip: the gradients of
+ * ossm_selective_backward / _bf16 (raw_out from the skip forward, which holds
+ * y + D u) with du += D gy and dD[d] = sum over batch and time of gy u, where
+ * gy = grad_out * silu(gate) (grad_out without a gate).  dD [dim] f32, summed
+ * in a fixed order (deterministic).  Both run in the scan kernel.
+ */
+int ossm_selective_backward_skip(int elem, const void* grad_out, const void* u, const void* dt,
+                                 const float* A, const void* Bm, const void* Cm,
+                                 const float* d_skip, const void* gate, const float* chunk_states,
+                                 const void* raw_out, void* du, void* ddt, float* dA, void* dB,
+                                 void* dC, float* dD, void* dgate, int64_t batch, int64_t dim,
+                                 int64_t length, int64_t dstate, ossm_stream_t stream);
 
 /*
  * Diagonal complex scan x_t = lambda_p * x_{t-1} + b_t, x_{-1} = 0, per channel

@@ -48,6 +48,7 @@ __all__ = [
 
 _VARIANT_CODE = {"imex1": 0, "imex2": 1, "im": 2, "ex": 3}
 _MAX_DSTATE = 256  # reference MAX_DSTATE (selective_scan_common.h:41)
+_ELEM = {torch.float32: 0, torch.bfloat16: 1}  # OSSM_ELEM_F32, OSSM_ELEM_BF16
 
 _cpu_delegate: Optional[Any] = None
 
@@ -317,8 +318,28 @@ def selective_scan_cuda_bf16(inputs, dt, A, B, C, gate=None, chunk_length=16):
     return _selective_forward(inputs, dt, A, B, C, gate, torch.bfloat16, "selective_scan_cuda_bf16")
 
 
-def _selective_forward(inputs, dt, A, B, C, gate, dtype, name):
+def selective_scan_cuda_skip(inputs, dt, A, B, C, D, gate=None):
+    """:func:`selective_scan_cuda` (float32 inputs) or :func:`selective_scan_cuda_bf16`
+    (bfloat16) with a per-channel skip ``D`` (float32, shape (channels,)) fused
+    into the scan: ``raw = y + D u``, ``out = raw * silu(gate)``.  An extension
+    with no counterpart in the reference's kernels (BASELINE configs 3 and 4
+    name a D skip); returns ``[outputs, chunk_states, raw_outputs]``."""
+    return _selective_forward(inputs, dt, A, B, C, gate, inputs.dtype, "selective_scan_cuda_skip",
+                              skip=D)
+
+
+def _skip_checks(D, inputs, name):
+    _check(D is not None, f"{name} needs the skip D")
+    _check(D.device == inputs.device, "D must be on the same device as inputs")
+    _check(D.dtype == torch.float32, "D must be float32")
+    _check(D.dim() == 1 and D.size(0) == inputs.size(1), "D must have shape (channels,)")
+
+
+def _selective_forward(inputs, dt, A, B, C, gate, dtype, name, skip=None):
     _check(inputs.is_cuda, "inputs must be CUDA tensor")
+    if skip is not None:
+        _check(dtype in (torch.float32, torch.bfloat16), f"{name} requires float32 or bfloat16 inputs")
+        _skip_checks(skip, inputs, name)
     _selective_checks(inputs, dt, A, B, C, gate, name, dtype)
     batch, dim, length = inputs.shape
     dstate = A.size(1)
@@ -332,9 +353,15 @@ def _selective_forward(inputs, dt, A, B, C, gate, dtype, name):
     out = torch.empty_like(u) if z is not None else raw
     chunks = torch.empty((batch, dim, _num_chunks(length), dstate * 2), dtype=torch.float32,
                          device=u.device)
-    fn = _lib.load().ossm_selective_forward if dtype == torch.float32 else \
-        _lib.load().ossm_selective_forward_bf16
     with torch.cuda.device(u.device):
+        if skip is not None:
+            _lib.check(_lib.load().ossm_selective_forward_skip(
+                _ELEM[dtype], u.data_ptr(), d.data_ptr(), a.data_ptr(), b.data_ptr(), c.data_ptr(),
+                skip.contiguous().data_ptr(), _lib.ptr(z), out.data_ptr(), raw.data_ptr(),
+                chunks.data_ptr(), batch, dim, length, dstate, _lib.stream_of(u)))
+            return [out, chunks, raw]
+        fn = _lib.load().ossm_selective_forward if dtype == torch.float32 else \
+            _lib.load().ossm_selective_forward_bf16
         _lib.check(fn(
             u.data_ptr(), d.data_ptr(), a.data_ptr(), b.data_ptr(), c.data_ptr(), _lib.ptr(z),
             out.data_ptr(), raw.data_ptr(), chunks.data_ptr(), batch, dim, length, dstate,
@@ -364,10 +391,24 @@ def selective_scan_cuda_bf16_backward(grad_output, inputs, dt, A, B, C, gate=Non
                                torch.bfloat16, "selective_scan_cuda_bf16")
 
 
+def selective_scan_cuda_skip_backward(grad_output, inputs, dt, A, B, C, D, gate=None,
+                                      chunk_states=None, raw_outputs=None):
+    """Backward of :func:`selective_scan_cuda_skip`: ``[du, ddt, dA, dB, dC, dD, dgate]``
+    (dA and dD float32, the rest in the inputs' dtype); ``du`` includes
+    ``D * gy`` and ``dD`` is the sum over batch and time of ``gy * u``, with
+    ``gy = grad_output * silu(gate)``.  ``chunk_states`` and ``raw_outputs``
+    come from :func:`selective_scan_cuda_skip` on the same inputs."""
+    return _selective_backward(grad_output, inputs, dt, A, B, C, gate, chunk_states, raw_outputs,
+                               inputs.dtype, "selective_scan_cuda_skip", skip=D)
+
+
 def _selective_backward(grad_output, inputs, dt, A, B, C, gate, chunk_states, raw_outputs, dtype,
-                        name):
+                        name, skip=None):
     dn = "float32" if dtype == torch.float32 else "bfloat16"
     _check(inputs.is_cuda, "inputs must be CUDA tensor")
+    if skip is not None:
+        _check(dtype in (torch.float32, torch.bfloat16), f"{name} requires float32 or bfloat16 inputs")
+        _skip_checks(skip, inputs, name)
     _selective_checks(inputs, dt, A, B, C, gate, name, dtype)
     _check(grad_output.device == inputs.device, "grad_output must be on the same device as inputs")
     _check(grad_output.dtype == dtype, f"grad_output must be {dn}")
@@ -390,18 +431,27 @@ def _selective_backward(grad_output, inputs, dt, A, B, C, gate, chunk_states, ra
     dA = torch.empty_like(a)  # float32 in both storage types
     dB, dC = torch.empty_like(b), torch.empty_like(c)
     dz = torch.empty_like(u)
+    dD = torch.zeros_like(skip) if skip is not None else None
     if length == 0:
-        return [du, ddt, dA.zero_(), dB, dC, dz]
+        return [du, ddt, dA.zero_(), dB, dC, dz] if skip is None else [du, ddt, dA.zero_(), dB, dC, dD, dz]
     cs = chunk_states.contiguous()
     _check(tuple(cs.shape) == (batch, dim, _num_chunks(length), 2 * dstate),
            "chunk_states do not match this library's forward for these inputs")
     raw = None
     if z is not None:
         raw = raw_outputs.contiguous() if raw_outputs is not None else \
-            _selective_forward(inputs, dt, A, B, C, gate, dtype, name)[2]
-    fn = _lib.load().ossm_selective_backward if dtype == torch.float32 else \
-        _lib.load().ossm_selective_backward_bf16
+            _selective_forward(inputs, dt, A, B, C, gate, dtype, name, skip=skip)[2]
     with torch.cuda.device(u.device):
+        if skip is not None:
+            _lib.check(_lib.load().ossm_selective_backward_skip(
+                _ELEM[dtype], gout.data_ptr(), u.data_ptr(), d.data_ptr(), a.data_ptr(),
+                b.data_ptr(), c.data_ptr(), skip.contiguous().data_ptr(), _lib.ptr(z),
+                cs.data_ptr(), _lib.ptr(raw), du.data_ptr(), ddt.data_ptr(), dA.data_ptr(),
+                dB.data_ptr(), dC.data_ptr(), dD.data_ptr(), dz.data_ptr(), batch, dim, length,
+                dstate, _lib.stream_of(u)))
+            return [du, ddt, dA, dB, dC, dD, dz]
+        fn = _lib.load().ossm_selective_backward if dtype == torch.float32 else \
+            _lib.load().ossm_selective_backward_bf16
         _lib.check(fn(
             gout.data_ptr(), u.data_ptr(), d.data_ptr(), a.data_ptr(), b.data_ptr(), c.data_ptr(),
             _lib.ptr(z), cs.data_ptr(), _lib.ptr(raw), du.data_ptr(), ddt.data_ptr(),

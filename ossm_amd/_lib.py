@@ -81,6 +81,14 @@ _SIGNATURES = {
         ctypes.c_int,
         [_vp, _vp, _vp, _fp, _vp, _vp, _vp, _fp, _vp, _vp, _vp, _fp, _vp, _vp, _vp, _c_int64,
          _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_selective_forward_skip": (
+        ctypes.c_int,
+        [ctypes.c_int, _vp, _vp, _fp, _vp, _vp, _fp, _vp, _vp, _vp, _fp, _c_int64, _c_int64,
+         _c_int64, _c_int64, _vp]),
+    "ossm_selective_backward_skip": (
+        ctypes.c_int,
+        [ctypes.c_int, _vp, _vp, _vp, _fp, _vp, _vp, _fp, _vp, _fp, _vp, _vp, _vp, _fp, _vp, _vp,
+         _fp, _vp, _c_int64, _c_int64, _c_int64, _c_int64, _vp]),
     "ossm_diag_scan_forward": (
         ctypes.c_int, [_fp, _fp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
     "ossm_diag_scan_backward": (

@@ -500,6 +500,9 @@ struct FwdArgs {
   // dt given before its softplus, with an optional per-channel bias
   int ld_u, ld_dt, ld_z;
   const float* dt_bias;
+  // [B, D, L] only: per-channel skip D (the extended API): the last pass adds
+  // D u to y before raw_out and the gate; null for the reference's scan
+  const float* dskip;
 };
 
 // (dt_t, u_t) pairs of a [.., L] row tile: s[row * RS2 + 2t].
@@ -746,6 +749,7 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
   const int d = d0 + r;
   const bool dvalid = d < a.D;
   const int n0 = a.n_base + g * NPW;  // first state of this lane
+  const float Dskip = (!BLD && a.dskip != nullptr && dvalid) ? a.dskip[d] : 0.f;
 
   float A2[NPW], h[NPW];
 #pragma unroll
@@ -903,7 +907,15 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
       for (int q = 0; q < TT / kCkpt; ++q) write_ckpt<NPW>(a.ckpt, ck_row, t0 / kCkpt + q, a.N, n0, hck[q], ck4);
     }
 
-    // y over the state groups (within the wave), then this lane's SEG outputs
+    // y over the state groups (within the wave), then this lane's SEG outputs;
+    // with a skip D, u of those steps is read first, behind the reduction
+    float uskip[BLD ? 1 : SEG];
+    if constexpr (!BLD) {
+      if (a.last && a.dskip != nullptr) {
+#pragma unroll
+        for (int k = 0; k < SEG; ++k) uskip[k] = dturow[2 * LY::step(g, k) + 1];
+      }
+    }
     float y[SEG];
     reduce_groups<NPW>(yv, y, g);
     if constexpr (BLD) {
@@ -956,6 +968,10 @@ __global__ __launch_bounds__(kThreads) void selective_fwd_kernel(FwdArgs<E> a) {
         for (int k = 0; k < SEG; ++k) y[k] += prev[k];
       }
       if (a.last) {
+        if (a.dskip != nullptr) {  // + D u, u of this tile as staged
+#pragma unroll
+          for (int k = 0; k < SEG; ++k) y[k] = fmaf(Dskip, uskip[k], y[k]);
+        }
         if (a.raw != nullptr) put_seg(a.raw, t0, y);
         if constexpr (GATED) {
 #pragma unroll
@@ -996,6 +1012,11 @@ struct BwdArgs {
   // D); dt is given before its softplus and ddt is returned w.r.t. it
   int ld_u, ld_dt, ld_z;
   const float* dt_bias;
+  // SKIP kernels ([B, D, L] only): the skip D of the forward; the first pass
+  // adds D gy to du and writes the (segment, batch row) partials of
+  // dD = sum_t gy u into part_dD [time segments * B, D]
+  const float* dskip;
+  float* part_dD;
 };
 
 struct BwdTile {
@@ -1067,9 +1088,10 @@ __device__ __forceinline__ void adj_prefetch(AdjTile& f, const BwdArgs<E>& a, si
   load_states<kBwdTile>(f.C, a.Cm, bc0, a.ld_bc, t0, a.L, a.N, a.n_base);
 }
 
-template <class E, bool VEC, bool GATED, bool BLD>
+template <class E, bool VEC, bool GATED, bool BLD, bool SKIP>
 __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   static_assert(!BLD || std::is_same_v<E, float>, "the [B, L, D] layout is fp32");
+  static_assert(!(BLD && SKIP), "the skip D is for the [B, D, L] layout");
   constexpr int TT = kBwdTile;
   constexpr int HT = TT / 2;  // steps whose trajectory is held in registers at once
   constexpr int RS = TT + 1;
@@ -1088,11 +1110,19 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   auto du_col = [](int c, int step) { return ((((step >> 2) + (c >> 2)) & 3) << 2) | (step & 3); };
   __shared__ __align__(16) float s_du[kMaxWaves * kWave * DS];
   __shared__ __align__(16) float s_ddt[kMaxWaves * kWave * DS];
+  // SKIP: the skip D of the workgroup's channels, and each thread's running
+  // sum of gy u over the steps it stages (dD)
+  __shared__ float s_dsk[SKIP ? kWave : 1];
+  __shared__ float s_dsum[SKIP ? kThreads : 1];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int b = blockIdx.y;
   const int d0 = blockIdx.x * kWave;
+  if constexpr (SKIP) {
+    if (threadIdx.x < kWave) s_dsk[threadIdx.x] = d0 + static_cast<int>(threadIdx.x) < a.D ? a.dskip[d0 + threadIdx.x] : 0.f;
+    s_dsum[threadIdx.x] = 0.f;  // read back by this thread only; s_dsk after the loop's first barrier
+  }
   const int d = d0 + lane;
   const bool dvalid = d < a.D;
   const int n0 = a.n_base + w * kNpw;
@@ -1242,6 +1272,16 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
         sd.z += pd.z;
         sd.w += pd.w;
       }
+      if constexpr (SKIP) {
+        if (a.first) {  // + D gy (the tile's gy is still staged)
+          const float* gq = s_gy + r * RS + c;
+          const float Dd = s_dsk[r];
+          su.x = fmaf(Dd, gq[0], su.x);
+          su.y = fmaf(Dd, gq[1], su.y);
+          su.z = fmaf(Dd, gq[2], su.z);
+          su.w = fmaf(Dd, gq[3], su.w);
+        }
+      }
       const size_t gi = row0 + static_cast<size_t>(dd) * a.L + t;
       if (!a.first) {
         su.x += a.du_acc[gi];
@@ -1269,6 +1309,13 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
     const int nsteps = min(TT, a.L - t0);
     balance_priority(tile - tile_lo + 1, tile_hi - tile_lo);
     __syncthreads();  // the previous tile's LDS readers are done
+    if constexpr (SKIP) {
+      // the previous tile is finished while its gy is still staged.
+      // No barrier before the staging below: a thread's finish reads only
+      // the s_gy slots that the same thread stages (tile_pos), and the
+      // LDS partials, which nothing writes before the next barrier.
+      if (prev_t0 >= 0) finish_dudt(prev_t0);
+    }
     float4 dz_v = make_float4(0.f, 0.f, 0.f, 0.f);
     size_t dz_off = 0;
     int dz_t = 0;
@@ -1343,6 +1390,13 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
       p[1] = gy.y;
       p[2] = gy.z;
       p[3] = gy.w;
+      if constexpr (SKIP) {
+        if (a.first) {  // gy u of the staged steps into this thread's dD sum
+          const float4 uu = masked<TT>(nxt.u, k, d0, a.D, t0, a.L);
+          s_dsum[threadIdx.x] =
+              fmaf(gy.x, uu.x, fmaf(gy.y, uu.y, fmaf(gy.z, uu.z, fmaf(gy.w, uu.w, s_dsum[threadIdx.x]))));
+        }
+      }
     }
     }
     float h0[kNpw];
@@ -1357,7 +1411,7 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
       // interval still holds)
       if (tile > tile_lo) bwd_prefetch<E, VEC, GATED, BLD>(nxt, a, row0, bc0, ck_row, d0, dvalid, n0, tile - 1);
       if (dz_ok) store_row4<VEC>(a.dz, dz_off, dz_t, a.L, dz_v);
-      if (prev_t0 >= 0) finish_dudt(prev_t0);
+      if (!SKIP && prev_t0 >= 0) finish_dudt(prev_t0);
       __syncthreads();
     }
 
@@ -1511,6 +1565,18 @@ __global__ __launch_bounds__(kThreads) void selective_bwd_kernel(BwdArgs<E> a) {
   if constexpr (!BLD) {
     __syncthreads();
     finish_dudt(prev_t0);
+  }
+  if constexpr (SKIP) {
+    if (a.first) {
+      // over the 4 threads (one quad) that staged each channel row
+      float dsum = s_dsum[threadIdx.x];
+      dsum += dpp<0xB1>(dsum);  // quad_perm [1,0,3,2]
+      dsum += dpp<0x4E>(dsum);  // quad_perm [2,3,0,1]
+      int r, c;
+      tile_pos<TT>(0, r, c);
+      if (c == 0 && d0 + r < a.D)
+        a.part_dD[(static_cast<size_t>(seg) * a.Bsz + b) * a.D + d0 + r] = dsum;
+    }
   }
 
   if (dvalid && wave_active) {
@@ -1675,7 +1741,7 @@ __device__ __forceinline__ void b2_store_bc(float* __restrict__ s, const float* 
   }
 }
 
-template <class E, bool VEC, bool GATED>
+template <class E, bool VEC, bool GATED, bool SKIP>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
 void selective_bwd2_kernel(BwdArgs<E> a) {
   constexpr int TT = kB2Tile;
@@ -1700,6 +1766,11 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
   __shared__ __align__(16) float s_du[kMaxWaves * ROWS * TT];
   __shared__ __align__(16) float s_ddt[kMaxWaves * ROWS * TT];
 
+  // SKIP: the skip D of the workgroup's channels, and each thread's running
+  // sum of gy u over the steps it stages (dD)
+  __shared__ float s_dsk[SKIP ? ROWS : 1];
+  __shared__ float s_dsum[SKIP ? kThreads : 1];
+
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int c = lane & (ROWS - 1);
@@ -1707,6 +1778,10 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
   const int b = blockIdx.y;
   const int d0 = blockIdx.x * ROWS;
   const bool dvalid = d0 + c < a.D;
+  if constexpr (SKIP) {
+    if (threadIdx.x < ROWS) s_dsk[threadIdx.x] = d0 + static_cast<int>(threadIdx.x) < a.D ? a.dskip[d0 + threadIdx.x] : 0.f;
+    s_dsum[threadIdx.x] = 0.f;  // read back by this thread only; s_dsk after the loop's first barrier
+  }
   const int n0 = a.n_base + 4 * w + 2 * hi;  // this lane's states n0, n0 + 1
   const int nw = min(kMaxWaves, (a.N - a.n_base + 3) / 4);
   const bool wave_active = w < nw;
@@ -1792,6 +1867,17 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
       sd.z += pd.z;
       sd.w += pd.w;
     }
+    if constexpr (SKIP) {
+      if (a.first) {  // + D gy (the tile's gy is still staged)
+        const float* gq = s_gy + rs * RS + cs;
+        const float Dd = s_dsk[rs];
+        su.x = fmaf(Dd, gq[0], su.x);
+        su.y = fmaf(Dd, gq[1], su.y);
+        su.z = fmaf(Dd, gq[2], su.z);
+        su.w = fmaf(Dd, gq[3], su.w);
+
+      }
+    }
     const uint32_t off = roff + static_cast<uint32_t>(t);
     if (!a.first) {
       const float* pu = a.du_acc + rowbase;
@@ -1819,6 +1905,13 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
     const int nsteps = min(TT, a.L - t0);
     balance_priority(tile - tile_lo + 1, tile_hi - tile_lo);
     __syncthreads();  // the previous tile's LDS readers are done
+    if constexpr (SKIP) {
+      // the previous tile is finished while its gy is still staged.
+      // No barrier before the staging below: a thread's finish reads only
+      // the s_gy slots that the same thread (rs, cs) stages, and the
+      // LDS partials, which nothing writes before the next barrier.
+      if (prev_t0 >= 0) finish_dudt(prev_t0);
+    }
     b2_put_dtu(s_dtu + rs * RS2 + 2 * cs, b2_mask(nxt.dt, rs_ok, t0 + cs, a.L),
                b2_mask(nxt.u, rs_ok, t0 + cs, a.L));
     b2_store_bc(s_BC, nxt.B, nxt.C, t0, a.L, a.N, a.n_base);
@@ -1841,6 +1934,13 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
         }
       }
       b2_put(s_gy + rs * RS + cs, gy);
+      if constexpr (SKIP) {
+        if (a.first) {  // gy u of the staged steps into this thread's dD sum
+          const float4 uu = b2_mask(nxt.u, rs_ok, t0 + cs, a.L);
+          s_dsum[threadIdx.x] =
+              fmaf(gy.x, uu.x, fmaf(gy.y, uu.y, fmaf(gy.z, uu.z, fmaf(gy.w, uu.w, s_dsum[threadIdx.x]))));
+        }
+      }
     }
     float h0[2], hm[2];
 #pragma unroll
@@ -1854,7 +1954,7 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
     // still holds)
     if (tile > tile_lo) bwd2_prefetch<E, VEC, GATED>(nxt, a, g, roff, cs, ckoff, n0, vec2, tile - 1);
     if (dz_ok) store_row4<VEC>(a.dz + rowbase, roff + static_cast<uint32_t>(t0 + cs), t0 + cs, a.L, dz_v);
-    if (prev_t0 >= 0) finish_dudt(prev_t0);
+    if (!SKIP && prev_t0 >= 0) finish_dudt(prev_t0);
     __syncthreads();
 
     if (wave_active) {
@@ -1977,6 +2077,16 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
   }
   __syncthreads();
   finish_dudt(prev_t0);
+  if constexpr (SKIP) {
+    if (a.first) {
+      // over the 8 threads (half a row of 16 lanes) that staged each channel row
+      float dsum = s_dsum[threadIdx.x];
+      dsum += dpp<0xB1>(dsum);   // quad_perm [1,0,3,2]
+      dsum += dpp<0x4E>(dsum);   // quad_perm [2,3,0,1]
+      dsum += dpp<0x141>(dsum);  // row_half_mirror
+      if (cs == 0 && rs_ok) a.part_dD[(static_cast<size_t>(seg) * a.Bsz + b) * a.D + d0 + rs] = dsum;
+    }
+  }
 
   if (dvalid && wave_active) {
     float* dst = a.part_dA + ((static_cast<size_t>(seg) * a.Bsz + b) * a.D + d0) * a.N;
@@ -1989,9 +2099,11 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
 // Adds the partials in a fixed order.  Blocks [0, n_bc_blocks): dB and dC,
 // summed over the channel tiles, kFinVec consecutive elements per thread when
 // `vec` (16-byte loads; n_bln % 4 == 0 and 16-byte aligned outputs), else one.
-// The remaining blocks: dA, kFinCols columns per block, each column summed over
-// `rows` partial rows (batch rows x time segments) by kFinGroups row groups
-// (eight loads in flight each) and then over the groups in order through LDS.
+// The next n_dA_blocks blocks: dA, kFinCols columns per block, each column
+// summed over `rows` partial rows (batch rows x time segments) by kFinGroups
+// row groups (eight loads in flight each) and then over the groups in order
+// through LDS.  The remaining blocks: dD (the skip's gradient, n_d columns)
+// from part_dD the same way.
 constexpr int kFinThreads = 256;
 constexpr int kFinCols = 16;
 constexpr int kFinGroups = kFinThreads / kFinCols;
@@ -2002,7 +2114,7 @@ __global__ __launch_bounds__(kFinThreads) void selective_finish_kernel(
     const float* __restrict__ part_dB, const float* __restrict__ part_dC,
     const float* __restrict__ part_dA, E* __restrict__ dB, E* __restrict__ dC,
     float* __restrict__ dA, int64_t n_bln, int n_dtiles, int64_t n_dn, int rows, int n_bc_blocks,
-    int vec) {
+    int vec, int n_dA_blocks, const float* __restrict__ part_dD, float* __restrict__ dD, int n_d) {
   if (static_cast<int>(blockIdx.x) < n_bc_blocks) {
     // tiles added in ascending order; the loads of 8 tiles are issued before
     // any of them is added (the sum stays the same, bit for bit)
@@ -2065,27 +2177,32 @@ __global__ __launch_bounds__(kFinThreads) void selective_finish_kernel(
     return;
   }
   __shared__ float s_part[kFinGroups][kFinCols];
+  const bool skip_cols = static_cast<int>(blockIdx.x) >= n_bc_blocks + n_dA_blocks;
+  const float* __restrict__ part = skip_cols ? part_dD : part_dA;
+  float* __restrict__ out = skip_cols ? dD : dA;
+  const int64_t n_cols = skip_cols ? n_d : n_dn;
   const int c = threadIdx.x % kFinCols, grp = threadIdx.x / kFinCols;
-  const int64_t col = static_cast<int64_t>(blockIdx.x - n_bc_blocks) * kFinCols + c;
-  const int64_t cc = col < n_dn ? col : n_dn - 1;
+  const int first_block = skip_cols ? n_bc_blocks + n_dA_blocks : n_bc_blocks;
+  const int64_t col = static_cast<int64_t>(static_cast<int>(blockIdx.x) - first_block) * kFinCols + c;
+  const int64_t cc = col < n_cols ? col : n_cols - 1;
   float s = 0.f;
   constexpr int kBatch = 8;
   int r = grp;
   for (; r + (kBatch - 1) * kFinGroups < rows; r += kBatch * kFinGroups) {
     float v[kBatch];
 #pragma unroll
-    for (int q = 0; q < kBatch; ++q) v[q] = part_dA[static_cast<size_t>(r + q * kFinGroups) * n_dn + cc];
+    for (int q = 0; q < kBatch; ++q) v[q] = part[static_cast<size_t>(r + q * kFinGroups) * n_cols + cc];
 #pragma unroll
     for (int q = 0; q < kBatch; ++q) s += v[q];
   }
-  for (; r < rows; r += kFinGroups) s += part_dA[static_cast<size_t>(r) * n_dn + cc];
+  for (; r < rows; r += kFinGroups) s += part[static_cast<size_t>(r) * n_cols + cc];
   s_part[grp][c] = s;
   __syncthreads();
-  if (grp == 0 && col < n_dn) {
+  if (grp == 0 && col < n_cols) {
     float t = 0.f;
 #pragma unroll
     for (int q = 0; q < kFinGroups; ++q) t += s_part[q][c];
-    dA[col] = t;
+    out[col] = t;
   }
 }
 
@@ -2217,12 +2334,14 @@ int fwd_states_per_lane(int64_t rows64) {
 
 // E = float: the fp32 API of the reference.  E = bf16_t: the same scan with
 // bf16 rows, B and C in HBM (A, chunk_states and dA stay fp32).  ml: the
-// [B, L, D] layout (fp32 only); null for the reference's [B, D, L].
+// [B, L, D] layout (fp32 only); null for the reference's [B, D, L].  dskip:
+// the extended API's per-channel skip D ([B, D, L] only), null for none.
 template <class E>
 int selective_forward_impl(const E* u, const E* dt, const float* A, const E* Bm, const E* Cm,
                            const E* gate, E* out, E* raw_out, float* chunk_states, int64_t batch,
                            int64_t dim, int64_t length, int64_t dstate, hipStream_t stream,
-                           const char* what, const MambaLayout* ml = nullptr) {
+                           const char* what, const MambaLayout* ml = nullptr,
+                           const float* dskip = nullptr) {
   StreamCall call(stream);
   if (call.status()) return call.status();
   clear_error();
@@ -2230,8 +2349,11 @@ int selective_forward_impl(const E* u, const E* dt, const float* A, const E* Bm,
   if (batch == 0 || dim == 0 || length == 0) return OSSM_OK;
   if (!u || !dt || !A || !Bm || !Cm || !out)
     return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": null pointer");
+  if (dskip != nullptr && ml != nullptr)
+    return set_error(OSSM_ERR_UNSUPPORTED, std::string(what) + ": the skip D is for the [B, D, L] layout");
   const int n_pass = static_cast<int>((dstate + kPassStates - 1) / kPassStates);
   FwdArgs<E> a{};
+  a.dskip = dskip;
   a.u = u;
   a.dt = dt;
   a.A = A;
@@ -2307,13 +2429,19 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
                             const E* raw_out, E* du, E* ddt, float* dA, E* dB, E* dC, E* dgate,
                             int64_t batch, int64_t dim, int64_t length, int64_t dstate,
                             hipStream_t stream, const char* what,
-                            const MambaLayout* ml = nullptr) {
+                            const MambaLayout* ml = nullptr, const float* dskip = nullptr,
+                            float* dD = nullptr) {
   StreamCall call(stream);
   if (call.status()) return call.status();
   clear_error();
   if (int rc = check_selective(batch, dim, length, dstate, what)) return rc;
+  if ((dskip == nullptr) != (dD == nullptr))
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": give the skip D and dD together");
+  if (dskip != nullptr && ml != nullptr)
+    return set_error(OSSM_ERR_UNSUPPORTED, std::string(what) + ": the skip D is for the [B, D, L] layout");
   if (batch == 0 || dim == 0 || length == 0) {
     // nothing to scan: every gradient is zero (dA still has D*N entries)
+    if (int rc = zero_fill(dD, dim, stream)) return rc;
     if (int rc = zero_fill(dA, dim * dstate, stream)) return rc;
     if (int rc = zero_fill(dB, batch * length * dstate, stream)) return rc;
     if (int rc = zero_fill(dC, batch * length * dstate, stream)) return rc;
@@ -2338,13 +2466,15 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
   const int n_seg = npw2 ? time_segments(n_dtiles * batch, length, kB2Tile, kBwd2WgPerCu)
                          : time_segments(n_dtiles * batch, length, kBwdTile, kBwdWgPerCu);
   const int64_t dA_rows = n_seg * batch;  // dA partial rows: (segment, batch row)
-  const size_t part_floats =
-      static_cast<size_t>(2 * n_dtiles * n_bln + dA_rows * n_dn) + (staged ? 2 * n_rows : 0);
+  const size_t part_floats = static_cast<size_t>(2 * n_dtiles * n_bln + dA_rows * n_dn) +
+                            (staged ? 2 * n_rows : 0) + (dskip ? dA_rows * dim : 0);
   void* ws = nullptr;
   if (int rc = acquire_workspace(call, part_floats * sizeof(float), &ws)) return rc;
   float* part_dB = static_cast<float*>(ws);
   float* part_dC = part_dB + n_dtiles * n_bln;
   float* part_dA = part_dC + n_dtiles * n_bln;
+  // after part_dA and the staged fp32 du / ddt
+  float* part_dD = dskip ? part_dA + dA_rows * n_dn + (staged ? 2 * n_rows : 0) : nullptr;
 
   BwdArgs<E> a{};
   a.gout = grad_out;
@@ -2369,6 +2499,8 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
   a.part_dB = part_dB;
   a.part_dC = part_dC;
   a.part_dA = part_dA;
+  a.dskip = dskip;
+  a.part_dD = part_dD;
   a.Bsz = static_cast<int>(batch);
   a.D = static_cast<int>(dim);
   a.L = static_cast<int>(length);
@@ -2399,20 +2531,25 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
     a.last = p == n_pass - 1;
     using K = void (*)(BwdArgs<E>);
     K kern;
-    if (npw2) {
-      kern = a.vec ? (gate ? selective_bwd2_kernel<E, true, true> : selective_bwd2_kernel<E, true, false>)
-                   : (gate ? selective_bwd2_kernel<E, false, true> : selective_bwd2_kernel<E, false, false>);
-    } else if constexpr (std::is_same_v<E, float>) {
-      if (ml != nullptr) {
-        kern = a.vec ? (gate ? selective_bwd_kernel<E, true, true, true> : selective_bwd_kernel<E, true, false, true>)
-                     : (gate ? selective_bwd_kernel<E, false, true, true> : selective_bwd_kernel<E, false, false, true>);
+    if (npw2 && dskip != nullptr) {
+      kern = a.vec ? (gate ? selective_bwd2_kernel<E, true, true, true> : selective_bwd2_kernel<E, true, false, true>)
+                   : (gate ? selective_bwd2_kernel<E, false, true, true> : selective_bwd2_kernel<E, false, false, true>);
+    } else if (npw2) {
+      kern = a.vec ? (gate ? selective_bwd2_kernel<E, true, true, false> : selective_bwd2_kernel<E, true, false, false>)
+                   : (gate ? selective_bwd2_kernel<E, false, true, false> : selective_bwd2_kernel<E, false, false, false>);
+    } else if (ml != nullptr) {
+      if constexpr (std::is_same_v<E, float>) {
+        kern = a.vec ? (gate ? selective_bwd_kernel<E, true, true, true, false> : selective_bwd_kernel<E, true, false, true, false>)
+                     : (gate ? selective_bwd_kernel<E, false, true, true, false> : selective_bwd_kernel<E, false, false, true, false>);
       } else {
-        kern = a.vec ? (gate ? selective_bwd_kernel<E, true, true, false> : selective_bwd_kernel<E, true, false, false>)
-                     : (gate ? selective_bwd_kernel<E, false, true, false> : selective_bwd_kernel<E, false, false, false>);
+        return set_error(OSSM_ERR_UNSUPPORTED, std::string(what) + ": the [B, L, D] layout is fp32");
       }
+    } else if (dskip != nullptr) {
+      kern = a.vec ? (gate ? selective_bwd_kernel<E, true, true, false, true> : selective_bwd_kernel<E, true, false, false, true>)
+                   : (gate ? selective_bwd_kernel<E, false, true, false, true> : selective_bwd_kernel<E, false, false, false, true>);
     } else {
-      kern = a.vec ? (gate ? selective_bwd_kernel<E, true, true, false> : selective_bwd_kernel<E, true, false, false>)
-                   : (gate ? selective_bwd_kernel<E, false, true, false> : selective_bwd_kernel<E, false, false, false>);
+      kern = a.vec ? (gate ? selective_bwd_kernel<E, true, true, false, false> : selective_bwd_kernel<E, true, false, false, false>)
+                   : (gate ? selective_bwd_kernel<E, false, true, false, false> : selective_bwd_kernel<E, false, false, false, false>);
     }
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, a);
     if (int rc = launch_check("selective_bwd_kernel")) return rc;
@@ -2422,10 +2559,13 @@ int selective_backward_impl(const E* grad_out, const E* u, const E* dt, const fl
   const int64_t per_block = static_cast<int64_t>(kFinThreads) * (fin_vec ? kFinVec : 1);
   const int64_t n_bc_blocks = (n_bln + per_block - 1) / per_block;
   const int64_t n_dA_blocks = (n_dn + kFinCols - 1) / kFinCols;
-  hipLaunchKernelGGL(selective_finish_kernel<E>, dim3(static_cast<unsigned>(n_bc_blocks + n_dA_blocks)),
+  const int64_t n_dD_blocks = dskip ? (dim + kFinCols - 1) / kFinCols : 0;
+  hipLaunchKernelGGL(selective_finish_kernel<E>,
+                     dim3(static_cast<unsigned>(n_bc_blocks + n_dA_blocks + n_dD_blocks)),
                      dim3(kFinThreads), 0, stream, part_dB, part_dC, part_dA, dB, dC, dA, n_bln,
                      static_cast<int>(n_dtiles), n_dn, static_cast<int>(dA_rows),
-                     static_cast<int>(n_bc_blocks), fin_vec);
+                     static_cast<int>(n_bc_blocks), fin_vec, static_cast<int>(n_dA_blocks), part_dD,
+                     dD, static_cast<int>(dim));
   if (int rc = launch_check("selective_finish_kernel")) return rc;
   if (gate == nullptr && dgate != nullptr) return zero_fill(dgate, n_rows, stream);
   return OSSM_OK;
@@ -2528,6 +2668,64 @@ int ossm_selective_backward_bf16(const void* grad_out, const void* u, const void
       chunk_states, static_cast<const E*>(raw_out), static_cast<E*>(du), static_cast<E*>(ddt), dA,
       static_cast<E*>(dB), static_cast<E*>(dC), static_cast<E*>(dgate), batch, dim, length, dstate,
       static_cast<hipStream_t>(stream), "selective_backward_bf16");
+}
+
+int ossm_selective_forward_skip(int elem, const void* u, const void* dt, const float* A,
+                                const void* Bm, const void* Cm, const float* d_skip,
+                                const void* gate, void* out, void* raw_out, float* chunk_states,
+                                int64_t batch, int64_t dim, int64_t length, int64_t dstate,
+                                ossm_stream_t stream) {
+  const char* what = "selective_forward_skip";
+  clear_error();
+  if (d_skip == nullptr) return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": null skip D");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (elem == OSSM_ELEM_F32) {
+    using E = float;
+    return selective_forward_impl<E>(
+        static_cast<const E*>(u), static_cast<const E*>(dt), A, static_cast<const E*>(Bm),
+        static_cast<const E*>(Cm), static_cast<const E*>(gate), static_cast<E*>(out),
+        static_cast<E*>(raw_out), chunk_states, batch, dim, length, dstate, st, what, nullptr, d_skip);
+  }
+  if (elem == OSSM_ELEM_BF16) {
+    using E = bf16_t;
+    return selective_forward_impl<E>(
+        static_cast<const E*>(u), static_cast<const E*>(dt), A, static_cast<const E*>(Bm),
+        static_cast<const E*>(Cm), static_cast<const E*>(gate), static_cast<E*>(out),
+        static_cast<E*>(raw_out), chunk_states, batch, dim, length, dstate, st, what, nullptr, d_skip);
+  }
+  return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": unknown element type");
+}
+
+int ossm_selective_backward_skip(int elem, const void* grad_out, const void* u, const void* dt,
+                                 const float* A, const void* Bm, const void* Cm,
+                                 const float* d_skip, const void* gate, const float* chunk_states,
+                                 const void* raw_out, void* du, void* ddt, float* dA, void* dB,
+                                 void* dC, float* dD, void* dgate, int64_t batch, int64_t dim,
+                                 int64_t length, int64_t dstate, ossm_stream_t stream) {
+  const char* what = "selective_backward_skip";
+  clear_error();
+  if (d_skip == nullptr || dD == nullptr)
+    return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": null skip D or dD");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (elem == OSSM_ELEM_F32) {
+    using E = float;
+    return selective_backward_impl<E>(
+        static_cast<const E*>(grad_out), static_cast<const E*>(u), static_cast<const E*>(dt), A,
+        static_cast<const E*>(Bm), static_cast<const E*>(Cm), static_cast<const E*>(gate),
+        chunk_states, static_cast<const E*>(raw_out), static_cast<E*>(du), static_cast<E*>(ddt), dA,
+        static_cast<E*>(dB), static_cast<E*>(dC), static_cast<E*>(dgate), batch, dim, length, dstate,
+        st, what, nullptr, d_skip, dD);
+  }
+  if (elem == OSSM_ELEM_BF16) {
+    using E = bf16_t;
+    return selective_backward_impl<E>(
+        static_cast<const E*>(grad_out), static_cast<const E*>(u), static_cast<const E*>(dt), A,
+        static_cast<const E*>(Bm), static_cast<const E*>(Cm), static_cast<const E*>(gate),
+        chunk_states, static_cast<const E*>(raw_out), static_cast<E*>(du), static_cast<E*>(ddt), dA,
+        static_cast<E*>(dB), static_cast<E*>(dC), static_cast<E*>(dgate), batch, dim, length, dstate,
+        st, what, nullptr, d_skip, dD);
+  }
+  return set_error(OSSM_ERR_INVALID_ARGUMENT, std::string(what) + ": unknown element type");
 }
 
 }  // extern "C"

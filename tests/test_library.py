@@ -41,7 +41,8 @@ def test_header_declares_the_entry_points():
               "ossm_diag_scan_forward", "ossm_diag_scan_backward", "ossm_diag_scan_forward_f64",
               "ossm_diag_scan_backward_f64", "ossm_dlinoss_layer_forward", "ossm_dlinoss_layer_backward",
               "ossm_selective_mamba_forward", "ossm_selective_mamba_backward",
-              "ossm_mamba_conv_forward", "ossm_mamba_conv_backward", "ossm_time_next_launch"):
+              "ossm_mamba_conv_forward", "ossm_mamba_conv_backward", "ossm_time_next_launch",
+              "ossm_selective_forward_skip", "ossm_selective_backward_skip"):
         assert n in names, n
 
 
@@ -57,7 +58,22 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     # every declared symbol has a ctypes signature in the binding
     assert set(_declared_functions()) == set(_lib.EXPORTED)
-    assert _lib.load().ossm_abi_version() == 14
+    assert _lib.load().ossm_abi_version() == 15
+
+
+def test_selective_skip_entry_points_refuse_a_null_d():
+    """The skip entry points check their own arguments before any HIP call."""
+    from ossm_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libossm_scan.so not built (python -m ossm_amd.build)")
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)  # never dereferenced: the calls fail first
+    assert lib.ossm_selective_forward_skip(0, p, p, p, p, p, None, None, p, p, p, 1, 1, 1, 1, None) == 1
+    assert b"null skip D" in lib.ossm_last_error()
+    assert lib.ossm_selective_backward_skip(0, p, p, p, p, p, p, p, None, p, p, p, p, p, p, p, None,
+                                            None, 1, 1, 1, 1, None) == 1
+    assert b"null skip D or dD" in lib.ossm_last_error()
 
 
 def test_time_next_launch_argument_checks():
