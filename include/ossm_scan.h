@@ -228,7 +228,9 @@ int ossm_selective_backward(const float* grad_out, const float* u, const float* 
  *   im (1, max(1 + dt g + dt^2 a, 1e-6)), ex (1 - dt g, 1).
  * A, G, step are fp32 [X_len, X_batch, M] contiguous with X_len in {1, length} and
  * X_batch in {1, batch} (broadcast over time / batch); bu [L,B,M] c64; states
- * [L,B,M,2] c64 (component 0 = w, 1 = x).
+ * [L,B,M,2] c64 (component 0 = w, 1 = x).  With all three broadcast over time
+ * the scan runs on the D-LinOSS kernels (per-channel constant coefficients);
+ * environment OSSM_SDL_TB_OSC=0 keeps the selective kernels.
  */
 int ossm_sdlinoss_forward(int variant, const float* A, int64_t a_len, int64_t a_batch,
                           const float* G, int64_t g_len, int64_t g_batch, const float* step,

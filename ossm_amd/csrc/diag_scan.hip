@@ -576,7 +576,7 @@ int diag_backward_impl(const R* lam_re, const R* lam_im, const void* states, con
   LaunchSync sync{};
   if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
   const ZeroFill zero{{reinterpret_cast<float*>(grad_lambda), nullptr, nullptr},
-                      static_cast<int>(2 * P * (sizeof(R) / sizeof(float)))};
+                      {static_cast<int>(2 * P * (sizeof(R) / sizeof(float))), 0, 0}};
   bool launched = false;
 #define OSSM_LAUNCH_DIAG_BWD(TT, WW)                                                              \
   if (!launched && tile.T == TT && tile.W == WW) {                                                \

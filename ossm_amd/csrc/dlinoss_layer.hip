@@ -760,7 +760,7 @@ template <class Model>
 struct LayerParamEpilogue {
   typename Model::Params prm;
   float *ga, *gg, *gs;
-  __device__ void add(int p, const double* S) const { Model::epilogue(prm, p, S, ga, gg, gs); }
+  __device__ void add(int p, const double* S) const { Model::epilogue(prm, p, 0, S, ga, gg, gs); }
 };
 
 size_t layer_bwd_lds_bytes(int64_t H, int64_t P) {
@@ -786,7 +786,7 @@ int launch_layer_bwd(LayerBwdArgs args, float* ga, float* gg, float* gs, hipStre
   if (int rc = acquire_workspace(call, static_cast<size_t>(args.n_chunks) * NS * nc * sizeof(float), &ws))
     return rc;
   args.partials = static_cast<float*>(ws);
-  args.zero = ZeroFill{{ga, gg, gs}, args.P};
+  args.zero = ZeroFill{{ga, gg, gs}, {args.P, args.P, args.P}};
   const bool vec = args.H % 4 == 0 && args.P % 4 == 0 && aligned16(args.u) && aligned16(args.gy) &&
                    aligned16(args.Bw) && aligned16(args.Cw);
   const bool pad = args.H % 32 != 0 || args.P % 32 != 0;

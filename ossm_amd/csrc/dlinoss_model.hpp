@@ -167,10 +167,12 @@ struct Dlinoss {
   // differentiating the coefficient tables of dlinoss_imex2.cpp:35-47 /
   // dlinoss_ex.cpp:33-42 (the terms the reference accumulates per step).
   // out0/1/2 = grad_a, grad_g, grad_step.  Linear in S: applied to a share of
-  // the sums, it adds that share's contribution to the outputs.
+  // the sums (channel ch's, of one chunk), it adds that share's contribution
+  // to the outputs.
   static constexpr int kOutsPerColumn = 1;
-  static __device__ void epilogue(const Params& prm, int p, const double* S, float* grad_a,
-                                  float* grad_g, float* grad_step) {
+  static __device__ void epilogue(const Params& prm, int ch, int /*chunk*/, const double* S,
+                                  float* grad_a, float* grad_g, float* grad_step) {
+    const int p = ch % prm.P;
     const double a = prm.a[p], g = prm.g[p], dt = prm.dt[p];
     double ga, gg, gs;
     if constexpr (V == OSSM_DLINOSS_IMEX1) {

@@ -53,6 +53,7 @@
 #include "scan_device.hpp"
 #include "scan_reduce.hpp"
 #include "dlinoss_model.hpp"
+#include "sdl_model.hpp"
 
 namespace ossm {
 namespace {
@@ -108,10 +109,80 @@ struct Linoss {
 
   // grad_m [P, 2, 2] complex = the summed products themselves (out0), added.
   static constexpr int kOutsPerColumn = 8;
-  static __device__ void epilogue(const Params&, int p, const double* S, float* grad_m, float*,
-                                  float*) {
+  static __device__ void epilogue(const Params& prm, int ch, int /*chunk*/, const double* S,
+                                  float* grad_m, float*, float*) {
+    const int p = ch % prm.P;
 #pragma unroll
     for (int j = 0; j < 8; ++j) atomic_put(grad_m + 8 * p + j, S[j]);
+  }
+};
+
+// Selective D-LinOSS (sdlinoss_<v>.cpp) with A, G and step constant over time:
+// per channel one set of coefficients, w' = c0 w + c1 x + c2 bu and x' = x + w'
+// (the imex1 D-LinOSS step's shape, with (c0, c1, c2) = (alpha, -a dt^2, dt^2) / S
+// of the variant; sdl_coef).  The parameter-gradient sums are the three
+// contractions of the new w's gradient gw = mu_w + mu_x with w_{t-1}, x_{t-1}
+// and bu_t, mapped to (dA, dG, dstep) by sdl_param_grads_of_sums and stored per
+// chunk (part[p][chunk * nc + ch]) for the caller's fixed-order sums.
+template <int V>
+struct SdlTb {
+  using In = float2;    // bu_t
+  using GIn = float2;   // grad of x_t
+  using GOut = float2;  // grad of bu_t
+  using Mat = RMat;
+  using Coef = SdlCoef<V>;
+  static constexpr int kSums = 3;
+  static constexpr bool kRecompute = true;
+
+  struct Params {
+    SdlParams v;
+    int P;  // M (the oscillators per batch row)
+    int nc;
+  };
+  struct Raw {
+    float a, g, s;
+  };
+  static __device__ __forceinline__ int at(const ParamView& pv, int ch, int M) {
+    return pv.by_channel ? ch : ch % M;
+  }
+  static __device__ __forceinline__ Raw load_raw(const Params& prm, int ch) {
+    return {prm.v.a.p[at(prm.v.a, ch, prm.P)], prm.v.g.p[at(prm.v.g, ch, prm.P)],
+            prm.v.s.p[at(prm.v.s, ch, prm.P)]};
+  }
+  static __device__ __forceinline__ Coef coef_of(const Raw& r) { return sdl_coef<V>(r.a, r.g, r.s); }
+  static __device__ __forceinline__ Coef coef(const Params& prm, int ch) { return coef_of(load_raw(prm, ch)); }
+  static __device__ __forceinline__ float4 step(const Coef& k, float4 s, float2 bu) {
+    return sdl_step<V>(k, s, bu);
+  }
+  static __device__ __forceinline__ Mat matrix(const Coef& k) { return {k.c0, k.c1, k.c0, 1.f + k.c1}; }
+  static __device__ __forceinline__ float4 mu(float4 carry, float2 go) {
+    return make_float4(carry.x, carry.y, carry.z + go.x, carry.w + go.y);
+  }
+  // carry to t-1 = M^T mu: (c0 gw, mu_x + c1 gw), gw = mu_w + mu_x
+  static __device__ __forceinline__ float4 rev_carry(const Coef& k, float4 m) {
+    const float gr = m.x + m.z, gi = m.y + m.w;
+    return make_float4(k.c0 * gr, k.c0 * gi, fmaf(k.c1, gr, m.z), fmaf(k.c1, gi, m.w));
+  }
+  static __device__ __forceinline__ float2 grad_input(const Coef& k, float4 m) {
+    return make_float2(k.c2 * (m.x + m.z), k.c2 * (m.y + m.w));
+  }
+  static __device__ __forceinline__ void accumulate(float* acc, float4 m, float4 sp, float2 bu) {
+    const float gr = m.x + m.z, gi = m.y + m.w;
+    acc[0] = fmaf(gr, sp.x, fmaf(gi, sp.y, acc[0]));  // gw . w_{t-1}
+    acc[1] = fmaf(gr, sp.z, fmaf(gi, sp.w, acc[1]));  // gw . x_{t-1}
+    acc[2] = fmaf(gr, bu.x, fmaf(gi, bu.y, acc[2]));  // gw . bu_t
+  }
+  static constexpr int kOutsPerColumn = 0;
+  static __device__ void epilogue(const Params& prm, int ch, int chunk, const double* S, float* pa,
+                                  float* pg, float* ps) {
+    const Raw r = load_raw(prm, ch);
+    float ga, gg, gs;
+    sdl_param_grads_of_sums<V>(r.a, r.g, r.s, sdl_inv_of<V>(r.a, r.g, r.s), static_cast<float>(S[0]),
+                               static_cast<float>(S[1]), static_cast<float>(S[2]), ga, gg, gs);
+    const size_t i = static_cast<size_t>(chunk) * prm.nc + ch;
+    pa[i] = ga;
+    pg[i] = gg;
+    ps[i] = gs;
   }
 };
 
@@ -489,7 +560,7 @@ __device__ __forceinline__ void bwd_back(BwdBuf<Model, T>& b, const BwdTicket& k
 #pragma unroll
       for (int j = 0; j < NS; ++j) S[j] = __builtin_nan("");
     }
-    if (k.active) Model::epilogue(prm, k.ch % prm.P, S, zero.p[0], zero.p[1], zero.p[2]);
+    if (k.active) Model::epilogue(prm, k.ch, k.c, S, zero.p[0], zero.p[1], zero.p[2]);
   }
 }
 
@@ -637,19 +708,8 @@ int launch_forward(const typename Model::Params& prm, const void* in, void* out,
   return OSSM_OK;
 }
 
-// Backward launch: one kernel.  It computes grad_in; its order-0 workgroup
-// zeroes out0..2 and every workgroup adds its chunk's share of the parameter
-// gradients into them (the chain rule of Model::epilogue applied to the
-// chunk's per-channel sums, one float atomic per output and channel).  A
-// column-sum launch after the scan (fixed-order fp64 sums over row groups)
-// cost 4.4 us plus the launch gap at config 2, where the scan takes ~73 us.
-// nc = B * P channels.
-template <class Model>
-int launch_backward(const typename Model::Params& prm, const void* in, const void* states,
-                    const void* gout, void* gin, float* out0, float* out1, float* out2, int64_t L,
-                    int64_t B, int64_t P, hipStream_t stream) {
-  StreamCall call(stream);
-  if (call.status()) return call.status();
+// The backward's tile for L steps of nc channels (see launch_backward).
+Tile bwd_tile(int64_t L, int64_t nc, bool recompute) {
   // Without OSSM_OSC_TILE_BWD: 16 x 16 (256-step chunks, one 16-wave workgroup
   // per CU, 145 KiB of LDS) for 128..2047 workgroups at that chunk length, else
   // 16 x 8.  Measured (imex1, events, us, 16x8 vs 16x16) at [L, B, P]:
@@ -661,13 +721,27 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   // imex1 and ex fit (no spills); imex2 and im spill 6 and 2 registers and still
   // gain (config 2: 90.5 -> 81.8 and 86.9 -> 80.4 us); the LinOSS backward, which
   // holds every s_{t-1} it reads, spills 75 and keeps 16 x 8.
-  constexpr bool kWideFits = Model::kRecompute;
   static const Tile env_tile = parse_tile("OSSM_OSC_TILE_BWD", Tile{0, 0, 0, 1, 1});
-  const int64_t wgs256 = (L + 255) / 256 * ((B * P + kWave - 1) / kWave);
-  const Tile tile = env_tile.T > 0 ? env_tile
-                    : kWideFits && wgs256 >= 128 && wgs256 < 2048 ? Tile{16, 16, 1, 1, 2}
-                                                                  : Tile{16, 8, 1, 1, 2};
+  const int64_t wgs256 = (L + 255) / 256 * ((nc + kWave - 1) / kWave);
+  return env_tile.T > 0 ? env_tile
+         : recompute && wgs256 >= 128 && wgs256 < 2048 ? Tile{16, 16, 1, 1, 2}
+                                                        : Tile{16, 8, 1, 1, 2};
+}
+
+// Backward launch: one kernel.  It computes grad_in; its order-0 workgroup
+// zeroes the arrays `zero` names and every workgroup hands its chunk's
+// per-channel sums to Model::epilogue (D-LinOSS, LinOSS: the chain rule
+// applied to the chunk's share, one float atomic per output and channel; a
+// column-sum launch after the scan cost 4.4 us plus the launch gap at config
+// 2, where the scan takes ~73 us).  nc = B * P channels.
+template <class Model>
+int launch_backward(const typename Model::Params& prm, const void* in, const void* states,
+                    const void* gout, void* gin, const ZeroFill& zero, int64_t L, int64_t B,
+                    int64_t P, hipStream_t stream) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
   const int64_t nc = B * P;
+  const Tile tile = bwd_tile(L, nc, Model::kRecompute);
   const int64_t CL = int64_t(tile.T) * tile.W;
   const int64_t n_chunks = (L + CL - 1) / CL;
   const int64_t n_groups = (nc + kWave - 1) / kWave;
@@ -680,7 +754,6 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   void* payload = nullptr;
   LaunchSync sync{};
   if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
-  const ZeroFill zero{{out0, out1, out2}, static_cast<int>(Model::kOutsPerColumn * P)};
   const dim3 grid(static_cast<unsigned>(total));
   bool launched = false;
 #define OSSM_BWD_ARGS                                                                            \
@@ -727,10 +800,58 @@ int dlinoss_backward_v(const float* a, const float* g, const float* dt, const vo
                        const void* states, const void* gout, float* ga, float* gg, float* gs,
                        void* gbu, int64_t L, int64_t B, int64_t P, hipStream_t stream) {
   typename Dlinoss<V>::Params prm{a, g, dt, static_cast<int>(P)};
-  return launch_backward<Dlinoss<V>>(prm, bu, states, gout, gbu, ga, gg, gs, L, B, P, stream);
+  const int n = static_cast<int>(Dlinoss<V>::kOutsPerColumn * P);
+  return launch_backward<Dlinoss<V>>(prm, bu, states, gout, gbu, ZeroFill{{ga, gg, gs}, {n, n, n}},
+                                     L, B, P, stream);
+}
+
+template <int V>
+int sdl_tb_forward_v(const SdlParams& v, const void* bu, void* states, int64_t L, int64_t nc,
+                     hipStream_t stream) {
+  const typename SdlTb<V>::Params prm{v, v.M, static_cast<int>(nc)};
+  return launch_forward<SdlTb<V>>(prm, bu, states, L, nc, stream);
+}
+
+template <int V>
+int sdl_tb_backward_v(const SdlParams& v, const void* bu, const void* states, const void* gout,
+                      void* gbu, float* const (&part)[3], int64_t L, int64_t nc, hipStream_t stream) {
+  const typename SdlTb<V>::Params prm{v, v.M, static_cast<int>(nc)};
+  // the partials are written (not added), so nothing is zeroed first
+  return launch_backward<SdlTb<V>>(prm, bu, states, gout, gbu, ZeroFill{{part[0], part[1], part[2]}, {0, 0, 0}},
+                                   L, nc / v.M, v.M, stream);
 }
 
 }  // namespace
+
+int sdl_tb_chunk_steps(int64_t L, int64_t nc) {
+  const Tile t = bwd_tile(L, nc, true);
+  return t.T * t.W;
+}
+
+int sdl_tb_forward(int variant, const SdlParams& prm, const void* bu, void* states, int64_t L,
+                   int64_t nc, hipStream_t stream) {
+  switch (variant) {
+    case OSSM_DLINOSS_IMEX1: return sdl_tb_forward_v<OSSM_DLINOSS_IMEX1>(prm, bu, states, L, nc, stream);
+    case OSSM_DLINOSS_IMEX2: return sdl_tb_forward_v<OSSM_DLINOSS_IMEX2>(prm, bu, states, L, nc, stream);
+    case OSSM_DLINOSS_IM: return sdl_tb_forward_v<OSSM_DLINOSS_IM>(prm, bu, states, L, nc, stream);
+    default: return sdl_tb_forward_v<OSSM_DLINOSS_EX>(prm, bu, states, L, nc, stream);
+  }
+}
+
+int sdl_tb_backward(int variant, const SdlParams& prm, const void* bu, const void* states,
+                    const void* gout, void* gbu, float* const (&part)[3], int64_t L, int64_t nc,
+                    hipStream_t stream) {
+  switch (variant) {
+    case OSSM_DLINOSS_IMEX1:
+      return sdl_tb_backward_v<OSSM_DLINOSS_IMEX1>(prm, bu, states, gout, gbu, part, L, nc, stream);
+    case OSSM_DLINOSS_IMEX2:
+      return sdl_tb_backward_v<OSSM_DLINOSS_IMEX2>(prm, bu, states, gout, gbu, part, L, nc, stream);
+    case OSSM_DLINOSS_IM:
+      return sdl_tb_backward_v<OSSM_DLINOSS_IM>(prm, bu, states, gout, gbu, part, L, nc, stream);
+    default:
+      return sdl_tb_backward_v<OSSM_DLINOSS_EX>(prm, bu, states, gout, gbu, part, L, nc, stream);
+  }
+}
 
 // ---- allocation-free D-LinOSS forward ------------------------------------------
 // ossm_dlinoss_forward_noalloc keeps its look-back records in this array: a
@@ -978,9 +1099,10 @@ int ossm_linoss_backward(const void* m11, const void* m12, const void* m21, cons
   Linoss::Params prm{static_cast<const float2*>(m11), static_cast<const float2*>(m12),
                      static_cast<const float2*>(m21), static_cast<const float2*>(m22),
                      static_cast<int>(ssm)};
+  const int n = static_cast<int>(Linoss::kOutsPerColumn * ssm);
   return launch_backward<Linoss>(prm, nullptr, states, grad_output, grad_b,
-                                 static_cast<float*>(grad_m), nullptr, nullptr, length, batch, ssm,
-                                 stream);
+                                 ZeroFill{{static_cast<float*>(grad_m), nullptr, nullptr}, {n, 0, 0}},
+                                 length, batch, ssm, stream);
 }
 
 }  // extern "C"

@@ -99,14 +99,14 @@ __device__ __forceinline__ void atomic_put(double* dst, double v) { unsafeAtomic
 // column-sum launch runs after the scan kernel has finished).
 struct ZeroFill {
   float* p[3];
-  int n;  // floats per array
+  int n[3];  // floats per array
 };
 
 __device__ __forceinline__ void zero_fill_block(const ZeroFill& z) {
 #pragma unroll
   for (int k = 0; k < 3; ++k)
     if (z.p[k] != nullptr)
-      for (int i = threadIdx.x; i < z.n; i += blockDim.x) z.p[k][i] = 0.f;
+      for (int i = threadIdx.x; i < z.n[k]; i += blockDim.x) z.p[k][i] = 0.f;
 }
 
 // The same zero-fill for outputs that the launch's own workgroups then add
@@ -121,7 +121,7 @@ __device__ __forceinline__ void zero_fill_publish(const ZeroFill& z, const Launc
 #pragma unroll
   for (int k = 0; k < 3; ++k)
     if (z.p[k] != nullptr)
-      for (int i = threadIdx.x; i < z.n; i += blockDim.x)
+      for (int i = threadIdx.x; i < z.n[k]; i += blockDim.x)
         __hip_atomic_store(reinterpret_cast<unsigned int*>(z.p[k]) + i, 0u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_s_waitcnt(0);  // every zero of this thread is in memory

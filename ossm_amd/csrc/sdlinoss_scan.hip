@@ -45,83 +45,10 @@
 #include "../../include/ossm_scan.h"
 #include "runtime.hpp"
 #include "scan_device.hpp"
+#include "sdl_model.hpp"
 
 namespace ossm {
 namespace {
-
-constexpr float kDtMin = 1e-6f;
-constexpr float kDtMax = 1.0f;
-constexpr float kClampMin = 1e-6f;
-
-// One parameter tensor [La, Ba, M]: element (t, ch) lives at
-// p[t * t_stride + (by_channel ? ch : ch % M)].
-struct ParamView {
-  const float* p;
-  long long t_stride;  // Ba * M, or 0 when broadcast over time
-  int by_channel;      // 1: Ba == B (index by channel); 0: broadcast over batch (index by m)
-};
-
-struct SdlParams {
-  ParamView a, g, s;
-  int M;
-};
-
-// ---- per-step coefficients -------------------------------------------------
-template <int V>
-struct SdlCoef {
-  float c0, c1, c2;
-};
-
-template <int V>
-__device__ __forceinline__ float sdl_alpha(float dt, float g) {
-  if constexpr (V == OSSM_DLINOSS_IMEX2 || V == OSSM_DLINOSS_EX) return 1.f - dt * g;
-  else return 1.f;
-}
-
-template <int V>
-__device__ __forceinline__ float sdl_s_raw(float dt, float g, float a) {
-  if constexpr (V == OSSM_DLINOSS_IMEX1) return 1.f + dt * g;
-  else if constexpr (V == OSSM_DLINOSS_IMEX2) return 1.f + dt * dt * a;
-  else if constexpr (V == OSSM_DLINOSS_IM) return 1.f + dt * g + dt * dt * a;
-  else return 1.f;
-}
-
-__device__ __forceinline__ float sdl_dt(float step_raw) {
-  return fminf(fmaxf(step_raw, kDtMin), kDtMax);
-}
-
-// 1 / S (exactly 1 for ex, which has no implicit part)
-template <int V>
-__device__ __forceinline__ float sdl_inv(float dt, float g, float a) {
-  if constexpr (V == OSSM_DLINOSS_EX) return 1.f;
-  else return 1.f / fmaxf(sdl_s_raw<V>(dt, g, a), kClampMin);
-}
-
-// The coefficients given 1/S (computed once per step and reused).
-template <int V>
-__device__ __forceinline__ SdlCoef<V> sdl_coef_inv(float a, float g, float step_raw, float inv) {
-  const float dt = sdl_dt(step_raw);
-  const float dt2 = dt * dt;
-  return {sdl_alpha<V>(dt, g) * inv, -dt2 * a * inv, dt2 * inv};
-}
-
-template <int V>
-__device__ __forceinline__ float sdl_inv_of(float a, float g, float step_raw) {
-  return sdl_inv<V>(sdl_dt(step_raw), g, a);
-}
-
-template <int V>
-__device__ __forceinline__ SdlCoef<V> sdl_coef(float a, float g, float step_raw) {
-  return sdl_coef_inv<V>(a, g, step_raw, sdl_inv_of<V>(a, g, step_raw));
-}
-
-// (w, x) -> (c0 w + c1 x + c2 bu, x + w')
-template <int V>
-__device__ __forceinline__ float4 sdl_step(const SdlCoef<V>& k, float4 s, float2 bu) {
-  const float wr = fmaf(k.c0, s.x, fmaf(k.c1, s.z, k.c2 * bu.x));
-  const float wi = fmaf(k.c0, s.y, fmaf(k.c1, s.w, k.c2 * bu.y));
-  return make_float4(wr, wi, s.z + wr, s.w + wi);
-}
 
 // M_t * P for a 2x2 P (rows of M_t: (c0, c1), (c0, 1 + c1))
 template <int V>
@@ -422,54 +349,6 @@ __device__ __forceinline__ float4 sdl_grad_step(float a, float g, float step_raw
   gs = (step_raw > kDtMin && step_raw < kDtMax) ? gdt : 0.f;
   // carry to the previous step: d/dw_prev = alpha gt, d/dx_prev = lx - dt^2 a gt
   return make_float4(alpha * gtr, alpha * gti, fmaf(-dt2 * a, gtr, lam.z), fmaf(-dt2 * a, gti, lam.w));
-}
-
-// Parameters broadcast over time.  A step's three parameter gradients (as
-// sdl_grad_step forms them) are linear in three contractions of the gradient of
-// the new w, gw = (lam.x + lam.z, lam.y + lam.w), with the state before the
-// step and the input:
-//   px = gw . w_prev,  pz = gw . x_prev,  pb = gw . bu
-// (gw . (-a x_prev + bu) = pb - a pz; gw . tmpw = alpha px + dt^2 (pb - a pz)),
-// with coefficients that depend only on the parameters.  With the parameters
-// constant over time the sums of px, pz, pb over the steps give the summed
-// gradients; this is that map (sdl_grad_step's formulas with the per-step
-// contractions replaced by their sums).
-template <int V>
-__device__ __forceinline__ void sdl_param_grads_of_sums(float a, float g, float step_raw, float inv,
-                                                        float px, float pz, float pb, float& ga,
-                                                        float& gg, float& gs) {
-  const float dt = sdl_dt(step_raw);
-  const float dt2 = dt * dt;
-  const float alpha = sdl_alpha<V>(dt, g);
-  const float pc = fmaf(-a, pz, pb);
-  float gdt = 0.f, gA = 0.f, gG = 0.f;
-  float kin = 1.f;  // gtr = gw * kin
-  if constexpr (V != OSSM_DLINOSS_EX) {
-    const float s_raw = sdl_s_raw<V>(dt, g, a);
-    kin = inv;
-    const float gS = -fmaf(alpha, px, dt2 * pc) * (inv * inv) * (s_raw > kClampMin ? 1.f : 0.f);
-    if constexpr (V == OSSM_DLINOSS_IMEX1) {
-      gdt = gS * g;
-      gG = gS * dt;
-    } else if constexpr (V == OSSM_DLINOSS_IMEX2) {
-      gdt = gS * (2.f * dt * a);
-      gA = gS * dt2;
-    } else {
-      gdt = gS * (g + 2.f * dt * a);
-      gA = gS * dt2;
-      gG = gS * dt;
-    }
-  }
-  if constexpr (V == OSSM_DLINOSS_IMEX2 || V == OSSM_DLINOSS_EX) {
-    gdt += kin * fmaf(-g, px, 2.f * dt * pc);
-    gG += kin * (-dt * px);
-  } else {
-    gdt += kin * (2.f * dt * pc);
-  }
-  gA += kin * (-dt2 * pz);
-  ga = gA;
-  gg = gG;
-  gs = (step_raw > kDtMin && step_raw < kDtMax) ? gdt : 0.f;
 }
 
 // Destinations of the parameter gradients.  Bit p of `tsum` (p = 0 a, 1 g,
@@ -946,6 +825,57 @@ int sdl_backward_v(const SdlParams& prm, const ParamShape (&shapes)[3], const vo
   return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_SDL_TILE_BWD names no built tile");
 }
 
+// Parameters all constant over time run on the oscillatory-scan kernels
+// (sdl_tb_forward / sdl_tb_backward: chunk transitions as matrix powers, the
+// D-LinOSS kernels' tiles) unless OSSM_SDL_TB_OSC=0 (read per call: tests
+// run both).
+bool tb_on_osc(const SdlParams& prm) {
+  const char* e = std::getenv("OSSM_SDL_TB_OSC");
+  const bool off = e != nullptr && std::string(e) == "0";
+  return !off && prm.a.t_stride == 0 && prm.g.t_stride == 0 && prm.s.t_stride == 0;
+}
+
+// The backward with parameters constant over time on the oscillatory-scan
+// kernels: per-chunk gradient sums into [n_chunks, B*M] partials, then the
+// fixed-order column sums over the chunks (and the batch rows of a parameter
+// broadcast over batch).
+int sdl_backward_tb_osc(int variant, const SdlParams& prm, const ParamShape (&shapes)[3],
+                        const void* bu, const void* states, const void* gout,
+                        float* const (&grads)[3], void* gbu, int64_t L, int64_t B, int64_t M,
+                        hipStream_t stream) {
+  StreamCall call(stream);
+  if (call.status()) return call.status();
+  const int64_t nc = B * M;
+  const int64_t n_chunks = (L + sdl_tb_chunk_steps(L, nc) - 1) / sdl_tb_chunk_steps(L, nc);
+  int64_t max_out = 0;
+  for (int p = 0; p < 3; ++p) max_out = std::max<int64_t>(max_out, shapes[p].ba == 1 && B > 1 ? M : nc);
+  const size_t buf_bytes = (3 * static_cast<size_t>(n_chunks) * nc * sizeof(float) + 255) & ~static_cast<size_t>(255);
+  const size_t part_bytes = 3 * static_cast<size_t>(kSumGroups) * max_out * sizeof(double);
+  void* ws = nullptr;
+  if (int rc = acquire_workspace(call, buf_bytes + part_bytes, &ws)) return rc;
+  float* const bufs = static_cast<float*>(ws);
+  double* const part = reinterpret_cast<double*>(static_cast<char*>(ws) + buf_bytes);
+  float* const chunk_sums[3] = {bufs, bufs + n_chunks * nc, bufs + 2 * n_chunks * nc};
+  if (int rc = sdl_tb_backward(variant, prm, bu, states, gout, gbu, chunk_sums, L, nc, stream)) return rc;
+  ColSums sums{};
+  for (int p = 0; p < 3; ++p) {
+    ColSum& cs = sums.s[p];
+    cs.in = chunk_sums[p];
+    cs.out = grads[p];
+    cs.part = part + static_cast<size_t>(p) * kSumGroups * max_out;
+    cs.nb = 1;
+    if (shapes[p].ba == 1 && B > 1) {  // [n_chunks, B, M] -> [M]
+      cs.R = static_cast<int>(n_chunks * B);
+      cs.C = static_cast<int>(M);
+    } else {  // [n_chunks, B*M] -> [B*M]
+      cs.R = static_cast<int>(n_chunks);
+      cs.C = static_cast<int>(nc);
+    }
+    cs.col_tiles = (cs.C + kWave - 1) / kWave;
+  }
+  return launch_colsums(sums, 3, stream);
+}
+
 int check_sdl(int variant, int64_t L, int64_t B, int64_t M, const char* what) {
   if (variant < 0 || variant > 3)
     return set_error(OSSM_ERR_INVALID_ARGUMENT, "Unknown selective D-LinOSS variant code");
@@ -979,6 +909,7 @@ int ossm_sdlinoss_forward(int variant, const float* A, int64_t a_len, int64_t a_
                       view_of(shapes[2], length, batch, ssm), static_cast<int>(ssm)};
   hipStream_t stream = static_cast<hipStream_t>(stream_v);
   const int64_t nc = batch * ssm;
+  if (tb_on_osc(prm)) return sdl_tb_forward(variant, prm, bu, states, length, nc, stream);
   switch (variant) {
     case OSSM_DLINOSS_IMEX1: return sdl_forward_v<OSSM_DLINOSS_IMEX1>(prm, bu, states, length, nc, stream);
     case OSSM_DLINOSS_IMEX2: return sdl_forward_v<OSSM_DLINOSS_IMEX2>(prm, bu, states, length, nc, stream);
@@ -1013,6 +944,9 @@ int ossm_sdlinoss_backward(int variant, const float* A, int64_t a_len, int64_t a
     return set_error(OSSM_ERR_INVALID_ARGUMENT, "sdlinoss_backward: null pointer");
   const SdlParams prm{view_of(shapes[0], length, batch, ssm), view_of(shapes[1], length, batch, ssm),
                       view_of(shapes[2], length, batch, ssm), static_cast<int>(ssm)};
+  if (tb_on_osc(prm))
+    return sdl_backward_tb_osc(variant, prm, shapes, bu, states, grad_output, grads, grad_bu, length,
+                               batch, ssm, stream);
   switch (variant) {
 #define OSSM_SDL_BWD(V)                                                                          \
   case V:                                                                                        \

