@@ -173,18 +173,21 @@ class TimingEvent:
 
 
 def _ev_time(torch, fn, reps: int, warm: int) -> float:
-    """Median milliseconds of fn() between two events on the current stream."""
+    """Mean milliseconds per fn() over `reps` back-to-back calls between two
+    events on the current stream.  No event sits between the calls: each one
+    queued there costs ~2-4 us of GPU time that would land in the measured
+    interval (the headline's timed region avoids them the same way)."""
     for _ in range(warm):
         fn()
     torch.cuda.synchronize()
-    evs = [(TimingEvent(torch), TimingEvent(torch)) for _ in range(reps)]
+    e0, e1 = TimingEvent(torch), TimingEvent(torch)
     _backlog(torch)
-    for e0, e1 in evs:
-        e0.record()
+    e0.record()
+    for _ in range(reps):
         fn()
-        e1.record()
+    e1.record()
     torch.cuda.synchronize()
-    return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+    return e0.elapsed_time(e1) / reps
 
 
 def _hbm_reference(torch, dev, units: int, fwd_ms: float, bwd_ms: float, reps: int = 20) -> dict:
@@ -391,7 +394,7 @@ def cpu_baseline(L, B, P, budget_s=12.0, port_budget_s=3.0):
 
 # ------------------------------------------------------------ other configs
 def _detail_configs(torch, K, dev, reps=20):
-    """The other BASELINE configs, each timed with events (median of `reps`)."""
+    """The other BASELINE configs, each timed with events (mean of `reps` back-to-back calls)."""
     out = {}
     # C1: LinOSS-IM forward, B=8 L=1024 P=64
     L, B, P = 1024, 8, 64
@@ -575,7 +578,7 @@ CASES = ("c1_linoss_im_fwd", "c3_selective_fp32", "c4_shape_selective_fp32", "c4
 def run_case(name: str, steps: int, warmup: int) -> int:
     """One BASELINE config alone (``--case``): `warmup` untimed then `steps`
     event-timed passes of its launches, for rocprofv3 runs that should hold only
-    that config's kernels.  Prints one JSON line with the median times."""
+    that config's kernels.  Prints one JSON line with the mean times."""
     import torch
 
     from ossm_amd import _kernels as K
