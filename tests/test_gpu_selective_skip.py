@@ -185,6 +185,55 @@ def test_selective_skip_config3_full_size(K):
     check_skip(got, args, "config 3")
 
 
+def _ulp_diff(a_bf16, b_bf16):
+    """Distance in bf16 units in the last place (16-bit patterns as ordered integers)."""
+    import torch
+
+    def key(t):
+        v = t.contiguous().view(torch.int16).to(torch.int32)
+        return torch.where(v < 0, -32768 - v, v)
+
+    return (key(a_bf16) - key(b_bf16)).abs()
+
+
+def test_selective_skip_bf16_config4(K):
+    """BASELINE config 4 as specified (B=16, D=1536, L=2048, N=16, bf16
+    storage, gate and D skip): the full tensors against the fp32 skip path on
+    the same values (at most one bf16 ulp apart, 99 % equal, dz two ulps; dA
+    bit-identical, dD within fp32 summation error), and one batch row (out,
+    du, ddt, dB, dC, dz) within one bf16 ulp of the fp64 composition (dz two)."""
+    import torch
+
+    args = list(skip_inputs(16, 1536, 2048, 16, seed=47))
+    for i in (0, 1, 3, 4, 6, 7):  # u, dt, B, C, z, g to bf16 values
+        args[i] = torch.from_numpy(args[i]).to(torch.bfloat16).float().numpy()
+    announce("selective skip bf16 config 4")
+    got = run_skip(K, *args, dtype=torch.bfloat16)
+    ref = run_skip(K, *args)
+    for a, r, name in zip(got, ref, NAMES):
+        if name == "dA":
+            assert torch.equal(a, r), name
+            continue
+        if name == "dD":
+            torch.testing.assert_close(a, r, rtol=1e-5, atol=1e-5 * float(r.abs().max()))
+            continue
+        d = _ulp_diff(a, r.to(torch.bfloat16))
+        assert int(d.max()) <= (2 if name == "dz" else 1), f"{name}: {int(d.max())} ulps"
+        if name != "dz":  # dz reads y + D u back from the bf16 raw_outputs
+            assert float((d == 0).float().mean()) >= 0.99, name
+    del ref
+    bs = [5]
+    sl = [np.ascontiguousarray(x[bs]).astype(np.float64) if x.ndim == 3 else x.astype(np.float64)
+          for x in args]
+    r64 = skip_reference(*sl)
+    for idx, name in ((0, "out"), (1, "du"), (2, "ddt"), (4, "dB"), (5, "dC"), (7, "dz")):
+        rel = 2 * EPS_BF16 if name == "dz" else EPS_BF16
+        a = to_np(got[idx].float())[bs].astype(np.float64)
+        err = np.abs(a - r64[idx])
+        bound = rel * np.abs(r64[idx]) + 2e-5 * max(1.0, float(np.abs(r64[idx]).max()))
+        assert not (err > bound).any(), f"{name} slice: {int((err > bound).sum())} beyond the bound"
+
+
 def test_selective_skip_errors(K):
     """The skip D must be float32 (channels,) on the inputs' device; the [B, D, L]
     entry points only."""
