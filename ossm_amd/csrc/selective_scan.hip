@@ -1758,11 +1758,11 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
   // [(t * 8 + pair) * 4]: one 16-byte read per step
   __shared__ __align__(16) float s_BC[kPassStates / 2 * TT * 4];
   // per-wave du / ddt partials (sums over the wave's four states),
-  // [wave][channel][step], with the eight 4-step groups of channel c rotated
-  // by (c >> 1) & 7 (du_col): 16-byte stores by 32 consecutive channels and
-  // the finish's 16-byte reads both touch 16 distinct 16-byte bank groups
-  // per quarter-wave
-  auto du_col = [](int c, int step) { return ((((step >> 2) + (c >> 1)) & 7) << 2) | (step & 3); };
+  // [wave][channel][step], with the eight 4-step groups of channel c permuted
+  // by XOR with (c >> 1) & 7 (du_col): 16-byte stores by 32 consecutive
+  // channels and the finish's 16-byte reads both touch 16 distinct 16-byte
+  // bank groups per quarter-wave
+  auto du_col = [](int c, int step) { return ((((step >> 2) ^ (c >> 1)) & 7) << 2) | (step & 3); };
   __shared__ __align__(16) float s_du[kMaxWaves * ROWS * TT];
   __shared__ __align__(16) float s_ddt[kMaxWaves * ROWS * TT];
 
@@ -1851,7 +1851,8 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
 
   // du / ddt of the tile at t0, summed over the waves from their LDS partials
   // and accumulated over passes: thread = (channel rs, steps cs..cs+3)
-  auto finish_dudt = [&](const int t0) {
+  // dgy: D gy of those steps (the skip's share of du), zero without a skip
+  auto finish_dudt = [&](const int t0, const float4 dgy) {
     const int t = t0 + cs;
     if (!rs_ok || t >= a.L) return;
     float4 su = make_float4(0.f, 0.f, 0.f, 0.f), sd = su;
@@ -1868,15 +1869,10 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
       sd.w += pd.w;
     }
     if constexpr (SKIP) {
-      if (a.first) {  // + D gy (the tile's gy is still staged)
-        const float* gq = s_gy + rs * RS + cs;
-        const float Dd = s_dsk[rs];
-        su.x = fmaf(Dd, gq[0], su.x);
-        su.y = fmaf(Dd, gq[1], su.y);
-        su.z = fmaf(Dd, gq[2], su.z);
-        su.w = fmaf(Dd, gq[3], su.w);
-
-      }
+      su.x += dgy.x;
+      su.y += dgy.y;
+      su.z += dgy.z;
+      su.w += dgy.w;
     }
     const uint32_t off = roff + static_cast<uint32_t>(t);
     if (!a.first) {
@@ -1897,6 +1893,19 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
     }
   };
 
+  // D gy of this thread's staged steps of tile t0 (staged now), SKIP first pass only
+  auto skip_dgy = [&](const int t0) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (SKIP) {
+      if (a.first && t0 >= 0) {
+        const float* gq = s_gy + rs * RS + cs;
+        const float Dd = s_dsk[rs];
+        v = make_float4(Dd * gq[0], Dd * gq[1], Dd * gq[2], Dd * gq[3]);
+      }
+    }
+    return v;
+  };
+
   BwdTile2 nxt;
   int prev_t0 = -1;  // the tile whose du / ddt are still to be finished
   bwd2_prefetch<E, VEC, GATED>(nxt, a, g, roff, cs, ckoff, n0, vec2, tile_hi - 1);
@@ -1905,13 +1914,9 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
     const int nsteps = min(TT, a.L - t0);
     balance_priority(tile - tile_lo + 1, tile_hi - tile_lo);
     __syncthreads();  // the previous tile's LDS readers are done
-    if constexpr (SKIP) {
-      // the previous tile is finished while its gy is still staged.
-      // No barrier before the staging below: a thread's finish reads only
-      // the s_gy slots that the same thread (rs, cs) stages, and the
-      // LDS partials, which nothing writes before the next barrier.
-      if (prev_t0 >= 0) finish_dudt(prev_t0);
-    }
+    // SKIP: D gy of the previous tile, read before the staging below replaces
+    // its gy (a thread reads only the s_gy slots that it stages itself)
+    const float4 dgy_prev = skip_dgy(prev_t0);
     b2_put_dtu(s_dtu + rs * RS2 + 2 * cs, b2_mask(nxt.dt, rs_ok, t0 + cs, a.L),
                b2_mask(nxt.u, rs_ok, t0 + cs, a.L));
     b2_store_bc(s_BC, nxt.B, nxt.C, t0, a.L, a.N, a.n_base);
@@ -1954,7 +1959,7 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
     // still holds)
     if (tile > tile_lo) bwd2_prefetch<E, VEC, GATED>(nxt, a, g, roff, cs, ckoff, n0, vec2, tile - 1);
     if (dz_ok) store_row4<VEC>(a.dz + rowbase, roff + static_cast<uint32_t>(t0 + cs), t0 + cs, a.L, dz_v);
-    if (!SKIP && prev_t0 >= 0) finish_dudt(prev_t0);
+    if (prev_t0 >= 0) finish_dudt(prev_t0, dgy_prev);
     __syncthreads();
 
     if (wave_active) {
@@ -1962,6 +1967,7 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
       const float* gyrow = s_gy + c * RS;
       const float* BCrow = s_BC + (2 * w + hi) * 4;  // this lane's state pair
       float* durow = (hi ? s_ddt : s_du) + (w * ROWS + c) * TT;
+      const int du_rot = (c >> 1) & 7;  // du_col(c, 4 G) = (G ^ du_rot) << 2
       // keep[m]: this lane's share of the dB / dC tile partials of steps
       // 8m .. 8m + 7 (see reduce4_32 for which lane holds which total)
       float keep[4] = {0.f, 0.f, 0.f, 0.f};
@@ -2039,7 +2045,12 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
               swap32(pu, pd);
               x[k] = pu + pd;
             }
-            *reinterpret_cast<float4*>(durow + du_col(c, s0 + i)) = make_float4(x[0], x[1], x[2], x[3]);
+            // the column formed here, not hoisted: eight loop-invariant
+            // addresses would be held across the tile (and spilled)
+            int rot = du_rot;
+            asm volatile("" : "+v"(rot));
+            *reinterpret_cast<float4*>(durow + ((((s0 + i) >> 2) ^ rot) << 2)) =
+                make_float4(x[0], x[1], x[2], x[3]);
           }
           const float o = reduce4_32(v);
           if ((lane & 7) == (i & 7)) keep[s0 / 8 + (i >> 3)] = o;
@@ -2076,7 +2087,7 @@ void selective_bwd2_kernel(BwdArgs<E> a) {
     prev_t0 = t0;  // finished while the next tile is staged
   }
   __syncthreads();
-  finish_dudt(prev_t0);
+  finish_dudt(prev_t0, skip_dgy(prev_t0));
   if constexpr (SKIP) {
     if (a.first) {
       // over the 8 threads (half a row of 16 lanes) that staged each channel row
