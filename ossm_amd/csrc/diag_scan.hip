@@ -21,9 +21,12 @@
 //   backward: the same scan in reverse time with conj(lambda); the final pass
 //             stores grad_b and accumulates g_t conj(x_{t-1}) per lane from the
 //             saved states.  HBM: read grad + states, write grad_b (24 B per
-//             state-step).  Per-(chunk, channel) sums are reduced to
-//             grad_lambda[P] by one column-sum launch (64 row groups in fp64 in
-//             a fixed order, added into grad_lambda with float atomics).
+//             state-step).  Each workgroup adds its chunk's per-channel sums
+//             into grad_lambda[P] with one hardware float atomic per
+//             component, after the launch's order-0 workgroup has zeroed
+//             grad_lambda and published its tag (zero_fill_publish): one
+//             launch, no partials (a second, column-sum launch cost ~5 us plus
+//             the gap between launches at config 2's shape).
 //
 // Records carry a complex value as 32-bit payload words, each in a 64-bit word
 // with the launch tag in its high half (2 words in fp32, 4 in fp64: a double
@@ -348,11 +351,12 @@ __global__ __launch_bounds__(W * kWave) void diag_forward_kernel(
 // Backward
 // ============================================================================
 // One workgroup per (chunk, channel group), chunks handed out last-first.
-// partials: [n_chunks][2][nc] (re, im of each chunk's sum of g_t conj(x_{t-1})).
+// grad_lambda: [P] complex as (re, im); each (chunk, channel) adds its sum of
+// g_t conj(x_{t-1}) into it.
 template <class R, int T, int W>
 __global__ __launch_bounds__(W * kWave) void diag_backward_kernel(
     const R* __restrict__ lam_re, const R* __restrict__ lam_im, int P, const Cx<R>* states,
-    const Cx<R>* __restrict__ gout, Cx<R>* __restrict__ gin, R* __restrict__ partials,
+    const Cx<R>* __restrict__ gout, Cx<R>* __restrict__ gin, R* __restrict__ grad_lambda,
     ZeroFill zero, int L, int nc, int n_groups, int n_chunks, unsigned long long* __restrict__ rec,
     LaunchSync sync) {
   using V = Cx<R>;
@@ -364,7 +368,7 @@ __global__ __launch_bounds__(W * kWave) void diag_backward_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int w = wave_id();
   const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
-  if (ticket == 0) zero_fill_block(zero);  // grad_lambda, for column_sum_kernel
+  if (ticket == 0) zero_fill_publish(zero, sync);  // grad_lambda
   const int cr = ticket / n_groups;
   const int g = ticket - cr * n_groups;
   const int c = n_chunks - 1 - cr;
@@ -452,24 +456,19 @@ __global__ __launch_bounds__(W * kWave) void diag_backward_kernel(
   }
   s_sum[w][lane] = acc;
   __syncthreads();
+  // the chunk's share of grad_lambda[p], summed over the waves in a fixed
+  // order; NaN if the zeroed outputs were never seen (a bounded wait that gave
+  // up, kErrSpinTimeout raised)
   if (w == 0 && active) {
     V v = s_sum[0][lane];
 #pragma unroll
     for (int u = 1; u < W; ++u) v = cx_add(v, s_sum[u][lane]);
-    group_row(partials, static_cast<long long>(c) * 2, nc, g)[lane] = v.x;
-    group_row(partials, static_cast<long long>(c) * 2 + 1, nc, g)[lane] = v.y;
+    if (!wait_outputs_zeroed(sync)) v = cx(R(__builtin_nan("")), R(__builtin_nan("")));
+    const int p = ch % P;
+    atomic_put(grad_lambda + 2 * p, static_cast<double>(v.x));
+    atomic_put(grad_lambda + 2 * p + 1, static_cast<double>(v.y));
   }
 }
-
-// grad_lambda[p] += one row group's two column sums (column_sum_kernel).
-template <class R>
-struct DiagEpilogue {
-  R* grad_lambda;  // [P] complex as (re, im), zeroed by the scan kernel
-  __device__ void add(int p, const double* S) const {
-    atomic_put(grad_lambda + 2 * p, S[0]);
-    atomic_put(grad_lambda + 2 * p + 1, S[1]);
-  }
-};
 
 // ============================================================================
 // Host side
@@ -496,17 +495,37 @@ struct DiagDefaults;
 template <>
 struct DiagDefaults<float> {
   // forward 32 x 16 measured best at config 2's shape after the non-temporal stores
-  // (40.4 vs 44.0 us for 16 x 16); backward 16 x 8 (32 x 8 within noise)
-  static constexpr DiagTile kFwd{32, 16}, kBwd{16, 8};
+  // (40.4 vs 44.0 us for 16 x 16).  Backward (parameter gradient added in the
+  // kernel, so every chunk is one float-atomic share of each output): 16 x 16
+  // (256-step chunks, half the shares) for 128 to 2048 workgroups of that tile,
+  // else 16 x 8 (bwd_tile).  Measured (events, us; 16 x 8 / 16 x 16) at
+  // [L, B, P]: [1024, 8, 64] 10.4 / 11.8 (32 workgroups); [4096, 8, 128]
+  // 29.6 / 20.9; [1024, 32, 128] 28.1 / 20.6; [4096, 32, 128] 76.2 / 70.7;
+  // [16384, 8, 512] 270 / 275 (4096 workgroups); [65536, 4, 256] 287 / 288.
+  static constexpr DiagTile kFwd{32, 16}, kBwd{16, 8}, kBwdWide{16, 16};
   static constexpr const char* kEnvFwd = "OSSM_DIAG_TILE_FWD";
   static constexpr const char* kEnvBwd = "OSSM_DIAG_TILE_BWD";
 };
 template <>
 struct DiagDefaults<double> {
-  static constexpr DiagTile kFwd{8, 8}, kBwd{8, 8};
+  // backward 16 x 8 at every measured shape ([1024, 8, 64] 11.5 us, [4096, 8, 128] 37.3,
+  // [1024, 32, 128] 34.2, [4096, 32, 128] 140.0; 8 x 8: 12.4, 45.2, 44.3, 147.4)
+  static constexpr DiagTile kFwd{8, 8}, kBwd{16, 8}, kBwdWide{16, 8};
   static constexpr const char* kEnvFwd = "OSSM_DIAG_TILE_FWD_F64";
   static constexpr const char* kEnvBwd = "OSSM_DIAG_TILE_BWD_F64";
 };
+
+// The backward's tile: the environment's, else kBwdWide when that tile gives
+// 128 to 2048 workgroups, else kBwd.
+template <class R>
+DiagTile bwd_tile(int64_t L, int64_t nc) {
+  static const DiagTile env = diag_tile(DiagDefaults<R>::kEnvBwd, DiagTile{0, 0});
+  if (env.T > 0) return env;
+  constexpr DiagTile wide = DiagDefaults<R>::kBwdWide;
+  const int64_t span = int64_t(wide.T) * wide.W;
+  const int64_t n_wg = (L + span - 1) / span * ((nc + kWave - 1) / kWave);
+  return n_wg >= 128 && n_wg <= 2048 ? wide : DiagDefaults<R>::kBwd;
+}
 
 int check_diag_sizes(int64_t L, int64_t B, int64_t P, const char* what) {
   if (L < 0 || B < 0 || P < 0)
@@ -559,19 +578,14 @@ int diag_backward_impl(const R* lam_re, const R* lam_im, const void* states, con
                        hipStream_t stream) {
   StreamCall call(stream);
   if (call.status()) return call.status();
-  static const DiagTile tile = diag_tile(DiagDefaults<R>::kEnvBwd, DiagDefaults<R>::kBwd);
   const int64_t nc = B * P;
+  const DiagTile tile = bwd_tile<R>(L, nc);
   const int64_t CL = int64_t(tile.T) * tile.W;
   const int64_t n_chunks = (L + CL - 1) / CL;
   const int64_t n_groups = (nc + kWave - 1) / kWave;
   const int64_t total = n_chunks * n_groups;
   if (total > INT_MAX) return set_error(OSSM_ERR_UNSUPPORTED, "problem too large for one launch grid");
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * CxOf<R>::kWords * nc * sizeof(unsigned long long);
-  const size_t part_bytes =
-      (static_cast<size_t>(n_chunks) * 2 * nc * sizeof(R) + 255) & ~static_cast<size_t>(255);
-  void* ws = nullptr;
-  if (int rc = acquire_workspace(call, part_bytes, &ws)) return rc;
-  R* partials = static_cast<R*>(ws);
   void* payload = nullptr;
   LaunchSync sync{};
   if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
@@ -583,7 +597,7 @@ int diag_backward_impl(const R* lam_re, const R* lam_im, const void* states, con
     hipLaunchKernelGGL((diag_backward_kernel<R, TT, WW>), dim3(static_cast<unsigned>(total)),     \
                        dim3(WW * kWave), 0, stream, lam_re, lam_im, static_cast<int>(P),          \
                        static_cast<const Cx<R>*>(states), static_cast<const Cx<R>*>(gout),        \
-                       static_cast<Cx<R>*>(grad_b), partials, zero, static_cast<int>(L),          \
+                       static_cast<Cx<R>*>(grad_b), grad_lambda, zero, static_cast<int>(L),       \
                        static_cast<int>(nc), static_cast<int>(n_groups),                          \
                        static_cast<int>(n_chunks), static_cast<unsigned long long*>(payload), sync); \
     launched = true;                                                                              \
@@ -595,8 +609,7 @@ int diag_backward_impl(const R* lam_re, const R* lam_im, const void* states, con
   }
 #undef OSSM_LAUNCH_DIAG_BWD
   if (!launched) return set_error(OSSM_ERR_UNSUPPORTED, std::string(DiagDefaults<R>::kEnvBwd) + " names no built tile");
-  if (int rc = launch_check("diag_backward_kernel")) return rc;
-  return launch_column_sums<2>(partials, P, B, n_chunks, DiagEpilogue<R>{grad_lambda}, stream);
+  return launch_check("diag_backward_kernel");
 }
 
 template <class R>

@@ -116,9 +116,11 @@ def test_diag_matches_reference_complex_literal(K):
 
 
 # (L, B, P): single step, ragged channel counts (B*P not a multiple of 64), one
-# and several forward chunks (128 steps), long look-back, one channel
+# and several forward chunks (128 steps), long look-back, one channel; the last
+# shape takes the backward's 16 x 16 tile (340 workgroups of 256-step chunks)
+# with a ragged last chunk and channel group, the others its 16 x 8 tile
 SHAPES = [(1, 1, 1), (5, 2, 3), (70, 3, 5), (128, 1, 64), (300, 3, 70), (1000, 2, 64),
-          (129, 5, 33), (4100, 1, 1)]
+          (129, 5, 33), (4100, 1, 1), (5000, 8, 130)]
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
@@ -214,7 +216,7 @@ def test_diag_bridge_autograd(K):
 
 def test_diag_repeatable(K):
     """Two runs agree to rounding (look-back association depends on publish
-    timing, and the 64 row-group shares of grad_lambda are added atomically)."""
+    timing, and every chunk's share of grad_lambda is added atomically)."""
     lam, b, go = diag_inputs(3000, 4, 96, seed=9)
     announce("diag repeatability")
     s1, l1, b1 = _run(K, lam, b, go)
