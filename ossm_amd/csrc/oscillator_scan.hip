@@ -122,8 +122,10 @@ struct Linoss {
 // (the imex1 D-LinOSS step's shape, with (c0, c1, c2) = (alpha, -a dt^2, dt^2) / S
 // of the variant; sdl_coef).  The parameter-gradient sums are the three
 // contractions of the new w's gradient gw = mu_w + mu_x with w_{t-1}, x_{t-1}
-// and bu_t, mapped to (dA, dG, dstep) by sdl_param_grads_of_sums and stored per
-// chunk (part[p][chunk * nc + ch]) for the caller's fixed-order sums.
+// and bu_t, mapped to (dA, dG, dstep) by sdl_param_grads_of_sums (linear in the
+// sums) and added per chunk into the parameter's gradient element (its batch
+// row's, or the shared one of a parameter broadcast over the batch) with one
+// float atomic each.
 template <int V>
 struct SdlTb {
   using In = float2;    // bu_t
@@ -173,16 +175,15 @@ struct SdlTb {
     acc[2] = fmaf(gr, bu.x, fmaf(gi, bu.y, acc[2]));  // gw . bu_t
   }
   static constexpr int kOutsPerColumn = 0;
-  static __device__ void epilogue(const Params& prm, int ch, int chunk, const double* S, float* pa,
+  static __device__ void epilogue(const Params& prm, int ch, int /*chunk*/, const double* S, float* pa,
                                   float* pg, float* ps) {
     const Raw r = load_raw(prm, ch);
     float ga, gg, gs;
     sdl_param_grads_of_sums<V>(r.a, r.g, r.s, sdl_inv_of<V>(r.a, r.g, r.s), static_cast<float>(S[0]),
                                static_cast<float>(S[1]), static_cast<float>(S[2]), ga, gg, gs);
-    const size_t i = static_cast<size_t>(chunk) * prm.nc + ch;
-    pa[i] = ga;
-    pg[i] = gg;
-    ps[i] = gs;
+    atomic_put(pa + at(prm.v.a, ch, prm.P), ga);
+    atomic_put(pg + at(prm.v.g, ch, prm.P), gg);
+    atomic_put(ps + at(prm.v.s, ch, prm.P), gs);
   }
 };
 
@@ -814,19 +815,17 @@ int sdl_tb_forward_v(const SdlParams& v, const void* bu, void* states, int64_t L
 
 template <int V>
 int sdl_tb_backward_v(const SdlParams& v, const void* bu, const void* states, const void* gout,
-                      void* gbu, float* const (&part)[3], int64_t L, int64_t nc, hipStream_t stream) {
+                      void* gbu, float* const (&grads)[3], int64_t L, int64_t nc, hipStream_t stream) {
   const typename SdlTb<V>::Params prm{v, v.M, static_cast<int>(nc)};
-  // the partials are written (not added), so nothing is zeroed first
-  return launch_backward<SdlTb<V>>(prm, bu, states, gout, gbu, ZeroFill{{part[0], part[1], part[2]}, {0, 0, 0}},
+  // zeroed by the launch's order-0 workgroup before any chunk adds its share
+  auto n_of = [&](const ParamView& pv) { return static_cast<int>(pv.by_channel ? nc : v.M); };
+  return launch_backward<SdlTb<V>>(prm, bu, states, gout, gbu,
+                                   ZeroFill{{grads[0], grads[1], grads[2]}, {n_of(v.a), n_of(v.g), n_of(v.s)}},
                                    L, nc / v.M, v.M, stream);
 }
 
 }  // namespace
 
-int sdl_tb_chunk_steps(int64_t L, int64_t nc) {
-  const Tile t = bwd_tile(L, nc, true);
-  return t.T * t.W;
-}
 
 int sdl_tb_forward(int variant, const SdlParams& prm, const void* bu, void* states, int64_t L,
                    int64_t nc, hipStream_t stream) {
@@ -839,17 +838,17 @@ int sdl_tb_forward(int variant, const SdlParams& prm, const void* bu, void* stat
 }
 
 int sdl_tb_backward(int variant, const SdlParams& prm, const void* bu, const void* states,
-                    const void* gout, void* gbu, float* const (&part)[3], int64_t L, int64_t nc,
+                    const void* gout, void* gbu, float* const (&grads)[3], int64_t L, int64_t nc,
                     hipStream_t stream) {
   switch (variant) {
     case OSSM_DLINOSS_IMEX1:
-      return sdl_tb_backward_v<OSSM_DLINOSS_IMEX1>(prm, bu, states, gout, gbu, part, L, nc, stream);
+      return sdl_tb_backward_v<OSSM_DLINOSS_IMEX1>(prm, bu, states, gout, gbu, grads, L, nc, stream);
     case OSSM_DLINOSS_IMEX2:
-      return sdl_tb_backward_v<OSSM_DLINOSS_IMEX2>(prm, bu, states, gout, gbu, part, L, nc, stream);
+      return sdl_tb_backward_v<OSSM_DLINOSS_IMEX2>(prm, bu, states, gout, gbu, grads, L, nc, stream);
     case OSSM_DLINOSS_IM:
-      return sdl_tb_backward_v<OSSM_DLINOSS_IM>(prm, bu, states, gout, gbu, part, L, nc, stream);
+      return sdl_tb_backward_v<OSSM_DLINOSS_IM>(prm, bu, states, gout, gbu, grads, L, nc, stream);
     default:
-      return sdl_tb_backward_v<OSSM_DLINOSS_EX>(prm, bu, states, gout, gbu, part, L, nc, stream);
+      return sdl_tb_backward_v<OSSM_DLINOSS_EX>(prm, bu, states, gout, gbu, grads, L, nc, stream);
   }
 }
 

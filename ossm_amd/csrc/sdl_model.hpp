@@ -30,14 +30,14 @@ struct SdlParams {
 // constant over time (every parameter view has t_stride 0): the recurrence
 // then has one set of coefficients per channel and runs on the
 // oscillatory-scan kernels (chunk transitions as matrix powers).  The
-// backward writes each chunk's gradient sums of A, G and step into
-// part[p] ([n_chunks, B*M], n_chunks from sdl_tb_chunk_steps) for the
-// caller's fixed-order reductions.
-int sdl_tb_chunk_steps(int64_t L, int64_t nc);
+// backward adds each chunk's share of the gradients of A, G and step into
+// grads[p] (B*M floats for a parameter per batch row, M for one broadcast
+// over the batch, as the parameter's view says) with float atomics, after
+// the launch itself has zeroed them: one launch.
 int sdl_tb_forward(int variant, const SdlParams& prm, const void* bu, void* states, int64_t L,
                    int64_t nc, hipStream_t stream);
 int sdl_tb_backward(int variant, const SdlParams& prm, const void* bu, const void* states,
-                    const void* gout, void* gbu, float* const (&part)[3], int64_t L, int64_t nc,
+                    const void* gout, void* gbu, float* const (&grads)[3], int64_t L, int64_t nc,
                     hipStream_t stream);
 
 namespace {

@@ -836,44 +836,12 @@ bool tb_on_osc(const SdlParams& prm) {
 }
 
 // The backward with parameters constant over time on the oscillatory-scan
-// kernels: per-chunk gradient sums into [n_chunks, B*M] partials, then the
-// fixed-order column sums over the chunks (and the batch rows of a parameter
-// broadcast over batch).
-int sdl_backward_tb_osc(int variant, const SdlParams& prm, const ParamShape (&shapes)[3],
-                        const void* bu, const void* states, const void* gout,
-                        float* const (&grads)[3], void* gbu, int64_t L, int64_t B, int64_t M,
-                        hipStream_t stream) {
-  StreamCall call(stream);
-  if (call.status()) return call.status();
-  const int64_t nc = B * M;
-  const int64_t n_chunks = (L + sdl_tb_chunk_steps(L, nc) - 1) / sdl_tb_chunk_steps(L, nc);
-  int64_t max_out = 0;
-  for (int p = 0; p < 3; ++p) max_out = std::max<int64_t>(max_out, shapes[p].ba == 1 && B > 1 ? M : nc);
-  const size_t buf_bytes = (3 * static_cast<size_t>(n_chunks) * nc * sizeof(float) + 255) & ~static_cast<size_t>(255);
-  const size_t part_bytes = 3 * static_cast<size_t>(kSumGroups) * max_out * sizeof(double);
-  void* ws = nullptr;
-  if (int rc = acquire_workspace(call, buf_bytes + part_bytes, &ws)) return rc;
-  float* const bufs = static_cast<float*>(ws);
-  double* const part = reinterpret_cast<double*>(static_cast<char*>(ws) + buf_bytes);
-  float* const chunk_sums[3] = {bufs, bufs + n_chunks * nc, bufs + 2 * n_chunks * nc};
-  if (int rc = sdl_tb_backward(variant, prm, bu, states, gout, gbu, chunk_sums, L, nc, stream)) return rc;
-  ColSums sums{};
-  for (int p = 0; p < 3; ++p) {
-    ColSum& cs = sums.s[p];
-    cs.in = chunk_sums[p];
-    cs.out = grads[p];
-    cs.part = part + static_cast<size_t>(p) * kSumGroups * max_out;
-    cs.nb = 1;
-    if (shapes[p].ba == 1 && B > 1) {  // [n_chunks, B, M] -> [M]
-      cs.R = static_cast<int>(n_chunks * B);
-      cs.C = static_cast<int>(M);
-    } else {  // [n_chunks, B*M] -> [B*M]
-      cs.R = static_cast<int>(n_chunks);
-      cs.C = static_cast<int>(nc);
-    }
-    cs.col_tiles = (cs.C + kWave - 1) / kWave;
-  }
-  return launch_colsums(sums, 3, stream);
+// kernels, in one launch: each chunk adds its share of the parameter
+// gradients into grads (zeroed by the launch) with float atomics.
+int sdl_backward_tb_osc(int variant, const SdlParams& prm, const void* bu, const void* states,
+                        const void* gout, float* const (&grads)[3], void* gbu, int64_t L, int64_t B,
+                        int64_t M, hipStream_t stream) {
+  return sdl_tb_backward(variant, prm, bu, states, gout, gbu, grads, L, B * M, stream);
 }
 
 int check_sdl(int variant, int64_t L, int64_t B, int64_t M, const char* what) {
@@ -945,8 +913,8 @@ int ossm_sdlinoss_backward(int variant, const float* A, int64_t a_len, int64_t a
   const SdlParams prm{view_of(shapes[0], length, batch, ssm), view_of(shapes[1], length, batch, ssm),
                       view_of(shapes[2], length, batch, ssm), static_cast<int>(ssm)};
   if (tb_on_osc(prm))
-    return sdl_backward_tb_osc(variant, prm, shapes, bu, states, grad_output, grads, grad_bu, length,
-                               batch, ssm, stream);
+    return sdl_backward_tb_osc(variant, prm, bu, states, grad_output, grads, grad_bu, length, batch,
+                               ssm, stream);
   switch (variant) {
 #define OSSM_SDL_BWD(V)                                                                          \
   case V:                                                                                        \

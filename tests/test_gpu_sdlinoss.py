@@ -144,9 +144,9 @@ def test_sdlinoss_time_invariant_on_both_kernels(K, variant, tag, monkeypatch):
 
 @pytest.mark.parametrize("tag", ["bcast_t", "m"])
 def test_sdlinoss_long_parameter_reductions(K, tag):
-    """Parameters broadcast over time on long rows: [1,B,M] sums 32 chunk
-    partials per output (the one-launch column sum), [M] sums 32 chunks x 16
-    batch rows (more than 256 rows: the two-pass column sum)."""
+    """Parameters broadcast over time on long rows (the oscillatory-scan
+    kernels): each output of [1,B,M] gets one share per chunk, each of [M] one
+    per chunk and batch row, added with float atomics in the scan kernel."""
     L, B, M = 4096, 16, 64
     args = sdl_inputs("imex1", tag, L, B, M, seed=21 + len(tag))
     announce(f"sdlinoss imex1 {tag} L={L} B={B} M={M}")
@@ -187,9 +187,10 @@ def test_sdlinoss_empty_and_errors(K):
 
 
 def test_sdlinoss_repeatable(K):
-    """Two runs agree to rounding: the broadcast sums are fixed-order, but the
-    carries between chunks come from the decoupled look-back, whose association
-    depends on which records are already published, so the last bits may differ."""
+    """Two runs agree to rounding: the carries between chunks come from the
+    decoupled look-back, whose association depends on which records are already
+    published, and each chunk's share of the parameter gradients is added with a
+    float atomic, so the last bits may differ."""
     args = sdl_inputs("im", "bcast_t", 500, 4, 96, seed=9)
     announce("sdlinoss repeatability")
     s1, g1 = _run(K, "im", *args)
