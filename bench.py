@@ -404,6 +404,22 @@ def _detail_configs(torch, K, dev, reps=20):
     out["c1_linoss_im_fwd"] = {"ms": ms, "state_steps_per_s": n / (ms / 1e3),
                                "hbm_frac": n * 32 / (ms / 1e3) / PEAK_HBM}
     del b_seq
+    # LinOSS-IM forward and native backward at config 2's shape (no BASELINE
+    # config of its own): forward reads b, writes the states (32 B/state-step);
+    # backward reads the saved states and grad, writes grad_b (48 B/state-step)
+    L, B, P = 4096, 32, 128
+    m11, m12, m21, m22, b_seq = linoss_im_inputs(torch, L, B, P, dev)
+    st = K.linoss_scan(m11, m12, m21, m22, b_seq)
+    go = torch.randn_like(st)
+    tf = _ev_time(torch, lambda: K.linoss_scan(m11, m12, m21, m22, b_seq), reps, 3)
+    tb = _ev_time(torch, lambda: K.linoss_scan_backward(m11, m12, m21, m22, st, go), reps, 3)
+    n = L * B * P
+    out["linoss_im_c2_shape"] = {"fwd_ms": tf, "bwd_ms": tb,
+                                 "state_steps_per_s_fwd_bwd": n / ((tf + tb) / 1e3),
+                                 "hbm_frac_fwd": n * 32 / (tf / 1e3) / PEAK_HBM,
+                                 "hbm_frac_bwd": n * 48 / (tb / 1e3) / PEAK_HBM,
+                                 "bytes_per_state_step": [32, 48]}
+    del b_seq, st, go
     # C5: D-LinOSS imex1 forward, B=4 L=65536 P=256
     L, B, P = 65536, 4, 256
     a, gam, dt, bu, _ = dlinoss_inputs(torch, L, B, P, dev, H=64, seed=5)

@@ -80,6 +80,7 @@ struct Linoss {
     const float2* m21;
     const float2* m22;
     int P;
+    int nc;  // channels B * P: the row length of the backward's partials
   };
 
   using Raw = CMat;
@@ -107,11 +108,25 @@ struct Linoss {
     acc[6] += g.z * sp.z + g.w * sp.w;  acc[7] += g.w * sp.z - g.z * sp.w;  // m22
   }
 
-  // grad_m [P, 2, 2] complex = the summed products themselves (out0), added.
+  // grad_m [P, 2, 2] complex = the summed products themselves.  Each chunk's
+  // per-channel sums are stored (part[(chunk * 8 + j) * nc + ch]) and added
+  // into grad_m by a column-sum launch (LinossColumns): with eight outputs per
+  // oscillator and one share per (chunk, batch row), float atomics from every
+  // workgroup queued on the same addresses and cost ~80 us of a 234 us
+  // backward at [4096, 32, 128] (9 of 23 us at config 1's shape).
   static constexpr int kOutsPerColumn = 8;
-  static __device__ void epilogue(const Params& prm, int ch, int /*chunk*/, const double* S,
-                                  float* grad_m, float*, float*) {
-    const int p = ch % prm.P;
+  static __device__ void epilogue(const Params& prm, int ch, int chunk, const double* S,
+                                  float* part, float*, float*) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      part[(static_cast<size_t>(chunk) * 8 + j) * prm.nc + ch] = static_cast<float>(S[j]);
+  }
+};
+
+// grad_m[p] += one row group's eight column sums of the LinOSS partials.
+struct LinossColumns {
+  float* grad_m;  // [P, 2, 2] complex, zeroed by the scan kernel
+  __device__ void add(int p, const double* S) const {
 #pragma unroll
     for (int j = 0; j < 8; ++j) atomic_put(grad_m + 8 * p + j, S[j]);
   }
@@ -731,10 +746,12 @@ Tile bwd_tile(int64_t L, int64_t nc, bool recompute) {
 
 // Backward launch: one kernel.  It computes grad_in; its order-0 workgroup
 // zeroes the arrays `zero` names and every workgroup hands its chunk's
-// per-channel sums to Model::epilogue (D-LinOSS, LinOSS: the chain rule
-// applied to the chunk's share, one float atomic per output and channel; a
-// column-sum launch after the scan cost 4.4 us plus the launch gap at config
-// 2, where the scan takes ~73 us).  nc = B * P channels.
+// per-channel sums to Model::epilogue (D-LinOSS, selective D-LinOSS with
+// constant parameters: the chain rule applied to the chunk's share, one float
+// atomic per output and channel, since a column-sum launch after the scan
+// cost 4.4 us plus the launch gap at config 2, where the scan takes ~73 us;
+// LinOSS: the shares stored for a column-sum launch, see Linoss).  nc = B * P
+// channels.
 template <class Model>
 int launch_backward(const typename Model::Params& prm, const void* in, const void* states,
                     const void* gout, void* gin, const ZeroFill& zero, int64_t L, int64_t B,
@@ -1077,7 +1094,7 @@ int ossm_linoss_forward(const void* m11, const void* m12, const void* m21, const
     return set_error(OSSM_ERR_INVALID_ARGUMENT, "linoss_forward: null pointer");
   Linoss::Params prm{static_cast<const float2*>(m11), static_cast<const float2*>(m12),
                      static_cast<const float2*>(m21), static_cast<const float2*>(m22),
-                     static_cast<int>(ssm)};
+                     static_cast<int>(ssm), static_cast<int>(batch * ssm)};
   return launch_forward<Linoss>(prm, b_seq, states, length, batch * ssm,
                                 static_cast<hipStream_t>(stream_v));
 }
@@ -1095,13 +1112,27 @@ int ossm_linoss_backward(const void* m11, const void* m12, const void* m21, cons
   if (length == 0 || batch == 0 || ssm == 0) return OSSM_OK;
   if (!m11 || !m12 || !m21 || !m22 || !states || !grad_output || !grad_m || !grad_b)
     return set_error(OSSM_ERR_INVALID_ARGUMENT, "linoss_backward: null pointer");
+  const int64_t nc = batch * ssm;
   Linoss::Params prm{static_cast<const float2*>(m11), static_cast<const float2*>(m12),
                      static_cast<const float2*>(m21), static_cast<const float2*>(m22),
-                     static_cast<int>(ssm)};
+                     static_cast<int>(ssm), static_cast<int>(nc)};
+  // the chunk partials, [n_chunks][8][nc] floats, for the scan's tile
+  StreamCall call(stream);
+  if (call.status()) return call.status();
+  const Tile tile = bwd_tile(length, nc, Linoss::kRecompute);
+  const int64_t n_chunks = (length + int64_t(tile.T) * tile.W - 1) / (int64_t(tile.T) * tile.W);
+  void* ws = nullptr;
+  if (int rc = acquire_workspace(call, static_cast<size_t>(n_chunks) * 8 * nc * sizeof(float), &ws)) return rc;
+  float* part = static_cast<float*>(ws);
   const int n = static_cast<int>(Linoss::kOutsPerColumn * ssm);
-  return launch_backward<Linoss>(prm, nullptr, states, grad_output, grad_b,
-                                 ZeroFill{{static_cast<float*>(grad_m), nullptr, nullptr}, {n, 0, 0}},
-                                 length, batch, ssm, stream);
+  // grad_m is zeroed by the scan kernel (its order-0 workgroup) and filled by
+  // the column sums, which run after it on the stream
+  if (int rc = launch_backward<Linoss>(prm, nullptr, states, grad_output, grad_b,
+                                       ZeroFill{{part, static_cast<float*>(grad_m), nullptr}, {0, n, 0}},
+                                       length, batch, ssm, stream))
+    return rc;
+  return launch_column_sums<8>(part, ssm, batch, n_chunks, LinossColumns{static_cast<float*>(grad_m)},
+                               stream);
 }
 
 }  // extern "C"
