@@ -170,6 +170,7 @@ struct Dlinoss {
   // the sums (channel ch's, of one chunk), it adds that share's contribution
   // to the outputs.
   static constexpr int kOutsPerColumn = 1;
+  static constexpr bool kWaveEpilogue = false;  // one lane per channel (see Linoss)
   static __device__ void epilogue(const Params& prm, int ch, int /*chunk*/, const double* S,
                                   float* grad_a, float* grad_g, float* grad_step) {
     const int p = ch % prm.P;

@@ -108,27 +108,31 @@ struct Linoss {
     acc[6] += g.z * sp.z + g.w * sp.w;  acc[7] += g.w * sp.z - g.z * sp.w;  // m22
   }
 
-  // grad_m [P, 2, 2] complex = the summed products themselves.  Each chunk's
-  // per-channel sums are stored (part[(chunk * 8 + j) * nc + ch]) and added
-  // into grad_m by a column-sum launch (LinossColumns): with eight outputs per
-  // oscillator and one share per (chunk, batch row), float atomics from every
-  // workgroup queued on the same addresses and cost ~80 us of a 234 us
-  // backward at [4096, 32, 128] (9 of 23 us at config 1's shape).
+  // grad_m [P, 2, 2] complex = the summed products themselves, each chunk's
+  // share added with float atomics by the whole wave (kWaveEpilogue): the
+  // wave's 64 channels x 8 sums go through LDS so that each atomic instruction
+  // covers 64 consecutive floats of grad_m (two cache lines) instead of 64
+  // lanes 32 bytes apart (16).  Issued lane by lane they queued in the memory
+  // system: a copy of the kernel without them ran 154 us against 234 us at
+  // [4096, 32, 128] (1024 shares per output), 13.7 against 22.9 us at config
+  // 1's shape.  `active`: the lane's channel is below nc.
   static constexpr int kOutsPerColumn = 8;
-  static __device__ void epilogue(const Params& prm, int ch, int chunk, const double* S,
-                                  float* part, float*, float*) {
+  static constexpr bool kWaveEpilogue = true;
+  static __device__ void epilogue_wave(const Params& prm, int ch, const double* S, float* grad_m) {
+    __shared__ float s_t[8 * kWave];
+    const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      part[(static_cast<size_t>(chunk) * 8 + j) * prm.nc + ch] = static_cast<float>(S[j]);
-  }
-};
-
-// grad_m[p] += one row group's eight column sums of the LinOSS partials.
-struct LinossColumns {
-  float* grad_m;  // [P, 2, 2] complex, zeroed by the scan kernel
-  __device__ void add(int p, const double* S) const {
+    for (int j = 0; j < 8; ++j) s_t[lane * 8 + j] = static_cast<float>(S[j]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int c0 = ch - lane;  // the wave's first channel
 #pragma unroll
-    for (int j = 0; j < 8; ++j) atomic_put(grad_m + 8 * p + j, S[j]);
+    for (int j = 0; j < 8; ++j) {
+      const int f = j * kWave + lane;  // sum f & 7 of the wave's channel f >> 3
+      const int c = c0 + (f >> 3);
+      if (c < prm.nc) atomic_put(grad_m + 8 * (c % prm.P) + (f & 7), static_cast<double>(s_t[f]));
+    }
   }
 };
 
@@ -190,6 +194,7 @@ struct SdlTb {
     acc[2] = fmaf(gr, bu.x, fmaf(gi, bu.y, acc[2]));  // gw . bu_t
   }
   static constexpr int kOutsPerColumn = 0;
+  static constexpr bool kWaveEpilogue = false;
   static __device__ void epilogue(const Params& prm, int ch, int /*chunk*/, const double* S, float* pa,
                                   float* pg, float* ps) {
     const Raw r = load_raw(prm, ch);
@@ -576,7 +581,10 @@ __device__ __forceinline__ void bwd_back(BwdBuf<Model, T>& b, const BwdTicket& k
 #pragma unroll
       for (int j = 0; j < NS; ++j) S[j] = __builtin_nan("");
     }
-    if (k.active) Model::epilogue(prm, k.ch, k.c, S, zero.p[0], zero.p[1], zero.p[2]);
+    if constexpr (Model::kWaveEpilogue)
+      Model::epilogue_wave(prm, k.ch, S, zero.p[0]);
+    else if (k.active)
+      Model::epilogue(prm, k.ch, k.c, S, zero.p[0], zero.p[1], zero.p[2]);
   }
 }
 
@@ -748,9 +756,9 @@ Tile bwd_tile(int64_t L, int64_t nc, bool recompute) {
 // zeroes the arrays `zero` names and every workgroup hands its chunk's
 // per-channel sums to Model::epilogue (D-LinOSS, selective D-LinOSS with
 // constant parameters: the chain rule applied to the chunk's share, one float
-// atomic per output and channel, since a column-sum launch after the scan
-// cost 4.4 us plus the launch gap at config 2, where the scan takes ~73 us;
-// LinOSS: the shares stored for a column-sum launch, see Linoss).  nc = B * P
+// atomic per output and channel; LinOSS: the whole wave's shares at once,
+// Model::epilogue_wave).  A column-sum launch after the scan cost 4.4 us plus
+// the launch gap at config 2, where the scan takes ~73 us.  nc = B * P
 // channels.
 template <class Model>
 int launch_backward(const typename Model::Params& prm, const void* in, const void* states,
@@ -1112,27 +1120,13 @@ int ossm_linoss_backward(const void* m11, const void* m12, const void* m21, cons
   if (length == 0 || batch == 0 || ssm == 0) return OSSM_OK;
   if (!m11 || !m12 || !m21 || !m22 || !states || !grad_output || !grad_m || !grad_b)
     return set_error(OSSM_ERR_INVALID_ARGUMENT, "linoss_backward: null pointer");
-  const int64_t nc = batch * ssm;
   Linoss::Params prm{static_cast<const float2*>(m11), static_cast<const float2*>(m12),
                      static_cast<const float2*>(m21), static_cast<const float2*>(m22),
-                     static_cast<int>(ssm), static_cast<int>(nc)};
-  // the chunk partials, [n_chunks][8][nc] floats, for the scan's tile
-  StreamCall call(stream);
-  if (call.status()) return call.status();
-  const Tile tile = bwd_tile(length, nc, Linoss::kRecompute);
-  const int64_t n_chunks = (length + int64_t(tile.T) * tile.W - 1) / (int64_t(tile.T) * tile.W);
-  void* ws = nullptr;
-  if (int rc = acquire_workspace(call, static_cast<size_t>(n_chunks) * 8 * nc * sizeof(float), &ws)) return rc;
-  float* part = static_cast<float*>(ws);
+                     static_cast<int>(ssm), static_cast<int>(batch * ssm)};
   const int n = static_cast<int>(Linoss::kOutsPerColumn * ssm);
-  // grad_m is zeroed by the scan kernel (its order-0 workgroup) and filled by
-  // the column sums, which run after it on the stream
-  if (int rc = launch_backward<Linoss>(prm, nullptr, states, grad_output, grad_b,
-                                       ZeroFill{{part, static_cast<float*>(grad_m), nullptr}, {0, n, 0}},
-                                       length, batch, ssm, stream))
-    return rc;
-  return launch_column_sums<8>(part, ssm, batch, n_chunks, LinossColumns{static_cast<float*>(grad_m)},
-                               stream);
+  return launch_backward<Linoss>(prm, nullptr, states, grad_output, grad_b,
+                                 ZeroFill{{static_cast<float*>(grad_m), nullptr, nullptr}, {n, 0, 0}},
+                                 length, batch, ssm, stream);
 }
 
 }  // extern "C"
