@@ -550,7 +550,7 @@ int diag_forward_impl(const R* lam_re, const R* lam_im, const void* b_seq, void*
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * CxOf<R>::kWords * nc * sizeof(unsigned long long);
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
   bool launched = false;
 #define OSSM_LAUNCH_DIAG_FWD(TT, WW)                                                              \
   if (!launched && tile.T == TT && tile.W == WW) {                                                \
@@ -588,7 +588,7 @@ int diag_backward_impl(const R* lam_re, const R* lam_im, const void* states, con
   const size_t rec_bytes = static_cast<size_t>(n_chunks) * 2 * CxOf<R>::kWords * nc * sizeof(unsigned long long);
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
   const ZeroFill zero{{reinterpret_cast<float*>(grad_lambda), nullptr, nullptr},
                       {static_cast<int>(2 * P * (sizeof(R) / sizeof(float))), 0, 0}};
   bool launched = false;

@@ -799,7 +799,7 @@ int launch_layer_bwd(LayerBwdArgs args, float* ga, float* gg, float* gs, hipStre
                                              static_cast<int>(lds)),
                          "hipFuncSetAttribute"))
     return rc;
-  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, n_wg, &payload, &sync)) return rc;
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(n_wg)), dim3(kLayerThreads), lds, stream, args,
                      static_cast<unsigned long long*>(payload), sync);
   if (int rc = launch_check("dlinoss_layer_bwd_kernel")) return rc;
@@ -841,7 +841,7 @@ int launch_layer(const LayerArgs& args, hipStream_t stream) {
                                              static_cast<int>(lds)),
                          "hipFuncSetAttribute"))
     return rc;
-  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, n_wg, &payload, &sync)) return rc;
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(n_wg)), dim3(kLayerThreads), lds, stream, args,
                      static_cast<unsigned long long*>(payload), sync);
   return launch_check("dlinoss_layer_fwd_kernel");

@@ -727,7 +727,7 @@ int launch_forward(const typename Model::Params& prm, const void* in, void* out,
   if (int rc = take_launch_timing(call, &tm)) return rc;
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(call, pl.rec_bytes, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, pl.rec_bytes, pl.total, &payload, &sync)) return rc;
   if (int rc = enqueue_forward<Model>(pl, prm, in, out, L, nc, stream, payload, sync, tm)) return rc;
   return OSSM_OK;
 }
@@ -779,7 +779,7 @@ int launch_backward(const typename Model::Params& prm, const void* in, const voi
   if (int rc = take_launch_timing(call, &tm)) return rc;
   void* payload = nullptr;
   LaunchSync sync{};
-  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
   const dim3 grid(static_cast<unsigned>(total));
   bool launched = false;
 #define OSSM_BWD_ARGS                                                                            \
@@ -901,7 +901,7 @@ constexpr int kNoAllocMaxDevices = 64;
 struct NoAllocDevice {
   std::mutex mu;                        // held from bookkeeping through the launch
   char* ptr = nullptr;                  // device address of `scratch` on this device
-  unsigned int epoch = 0;               // tag of the most recent dispatch-order launch
+  unsigned int epoch = 0;               // counter of the dispatch-order tags (next_dispatch_tag)
 };
 NoAllocDevice g_noalloc[kNoAllocMaxDevices];
 
@@ -992,10 +992,11 @@ int ossm_dlinoss_forward_noalloc(int variant, const float* a_diag, const float* 
     return set_error(OSSM_ERR_HIP, std::string("hipStreamIsCapturing: ") + hipGetErrorString(ce));
   }
   const bool capturing = cap != hipStreamCaptureStatusNone;
-  if (capturing && (cap != hipStreamCaptureStatusActive || !scan_order_by_ticket()))
+  if (capturing && cap != hipStreamCaptureStatusActive)
     return set_error(OSSM_ERR_UNSUPPORTED,
-                     "dlinoss_forward_noalloc: HIP-graph capture needs an active capture and ticket "
-                     "order (OSSM_SCAN_ORDER=dispatch chooses tags on the host per call)");
+                     "dlinoss_forward_noalloc: the stream's graph capture was invalidated");
+  bool by_ticket = true;
+  if (int rc = choose_scan_order(dev, capturing, pl.total, &by_ticket)) return rc;
   NoAllocDevice& s = g_noalloc[dev];
   std::lock_guard<std::mutex> hold(s.mu);
   if (capturing && s.ptr == nullptr)
@@ -1003,19 +1004,13 @@ int ossm_dlinoss_forward_noalloc(int variant, const float* a_diag, const float* 
                      "dlinoss_forward_noalloc: call it once eagerly on this device before capturing "
                      "it (the first call looks up the fixed array's address)");
   if (int rc = noalloc_address(dev)) return rc;
-  const bool by_ticket = scan_order_by_ticket();
   LaunchSync sync{};
   sync.ticket = reinterpret_cast<unsigned long long*>(s.ptr + kHdrTicket);
   sync.err = reinterpret_cast<unsigned int*>(s.ptr + kHdrErr);
   sync.flag = reinterpret_cast<unsigned long long*>(s.ptr + kHdrFlag);
   sync.use_ticket = by_ticket ? 1 : 0;
   sync.poison = 0;
-  sync.tag = 0;  // ticket order: drawn on the device
-  if (!by_ticket) {
-    s.epoch += 1;
-    if (s.epoch == 0) s.epoch = 1;
-    sync.tag = s.epoch;
-  }
+  sync.tag = by_ticket ? 0 : next_dispatch_tag(s.epoch);  // ticket order: drawn on the device
   void* payload = s.ptr + kHdrBytes;
   int rc = OSSM_OK;
   switch (variant) {

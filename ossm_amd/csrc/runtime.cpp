@@ -1,6 +1,7 @@
 // Host runtime of libossm_scan: error strings and scratch management.
 #include "runtime.hpp"
 
+#include <atomic>
 #include <cstdlib>
 #include <map>
 #include <memory>
@@ -23,7 +24,7 @@ int release_buffer(void* p, bool captured, const char* what);
 struct Scratch {
   void* base = nullptr;       // device buffer: header + payload
   size_t payload = 0;         // payload capacity in bytes
-  unsigned int epoch = 0;     // tag of the most recent dispatch-order launch
+  unsigned int epoch = 0;     // counter of the dispatch-order tags (next_dispatch_tag)
   bool captured = false;      // a HIP graph holds this buffer's address
 };
 
@@ -89,12 +90,51 @@ int take_launch_timing(const StreamCall& call, LaunchTiming* out) {
   return OSSM_OK;
 }
 
-bool scan_order_by_ticket() {
-  static const bool by_ticket = [] {
-    const char* v = std::getenv("OSSM_SCAN_ORDER");
-    return v == nullptr || std::string(v) != "dispatch";
-  }();
-  return by_ticket;
+namespace {
+
+// Compute units of device `dev`, looked up once per device (0 when the query
+// fails, which leaves every launch in ticket order).
+int cu_count(int dev) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> counts[kMaxDevices] = {};
+  if (dev < 0 || dev >= kMaxDevices) return 0;
+  int n = counts[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      return 0;
+    }
+    counts[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+}  // namespace
+
+int choose_scan_order(int dev, bool capturing, int64_t n_workgroups, bool* by_ticket) {
+  const char* v = std::getenv("OSSM_SCAN_ORDER");
+  const std::string mode = v == nullptr ? std::string("auto") : std::string(v);
+  if (mode == "ticket") {
+    *by_ticket = true;
+  } else if (mode == "dispatch") {
+    if (capturing)
+      return set_error(OSSM_ERR_UNSUPPORTED,
+                       "ossm_scan: OSSM_SCAN_ORDER=dispatch chooses look-back tags on the host per "
+                       "call, which a replayed HIP graph would reuse: capture needs ticket order");
+    *by_ticket = false;
+  } else if (mode == "auto" || mode.empty()) {
+    *by_ticket = capturing || n_workgroups > cu_count(dev);
+  } else {
+    return set_error(OSSM_ERR_INVALID_ARGUMENT,
+                     "ossm_scan: OSSM_SCAN_ORDER must be auto, ticket or dispatch, not '" + mode + "'");
+  }
+  return OSSM_OK;
+}
+
+unsigned int next_dispatch_tag(unsigned int& epoch) {
+  epoch = (epoch + 1) & (kDispatchTagBase - 1);
+  if (epoch == 0) epoch = 1;
+  return kDispatchTagBase | epoch;
 }
 
 StreamCall::StreamCall(hipStream_t stream) : stream_(stream) {
@@ -122,14 +162,12 @@ int refuse_capture(const char* what) {
 
 }  // namespace
 
-int acquire_scratch(StreamCall& call, size_t payload_bytes, void** payload, LaunchSync* sync) {
+int acquire_scratch(StreamCall& call, size_t payload_bytes, int64_t n_workgroups, void** payload,
+                    LaunchSync* sync) {
   if (call.status()) return call.status();
-  const bool by_ticket = scan_order_by_ticket();
+  bool by_ticket = true;
+  if (int rc = choose_scan_order(call.device(), call.capturing(), n_workgroups, &by_ticket)) return rc;
   Scratch& s = state_of(call.device(), call.stream()).scratch;
-  if (call.capturing() && !by_ticket)
-    return set_error(OSSM_ERR_UNSUPPORTED,
-                     "ossm_scan: OSSM_SCAN_ORDER=dispatch chooses look-back tags on the host per "
-                     "call, which a replayed HIP graph would reuse: capture needs ticket order");
   if (s.base == nullptr || s.payload < payload_bytes) {
     if (call.capturing()) return refuse_capture("look-back scratch would have to grow");
     // Grow: earlier launches on this stream may still read the old buffer.
@@ -158,12 +196,7 @@ int acquire_scratch(StreamCall& call, size_t payload_bytes, void** payload, Laun
   sync->flag = reinterpret_cast<unsigned long long*>(b + kHdrFlag);
   sync->use_ticket = by_ticket ? 1 : 0;
   sync->poison = 0;
-  sync->tag = 0;  // ticket order: drawn on the device
-  if (!by_ticket) {
-    s.epoch += 1;
-    if (s.epoch == 0) s.epoch = 1;  // 0 is the tag of never-written memory
-    sync->tag = s.epoch;
-  }
+  sync->tag = by_ticket ? 0 : next_dispatch_tag(s.epoch);  // ticket order: drawn on the device
   *payload = b + kHdrBytes;
   return OSSM_OK;
 }

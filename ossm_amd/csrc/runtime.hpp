@@ -30,8 +30,10 @@ constexpr size_t kHdrBytes = 256;   // payload starts here, 256-byte aligned
 // The workgroup that draws the launch's last order advances the counter to
 // the next multiple of 2^32.  Nothing per launch is chosen on the host, so a
 // launch captured into a HIP graph draws fresh tags and orders on every
-// replay.  Dispatch order (OSSM_SCAN_ORDER=dispatch) draws no ticket: the
-// order is the workgroup index and the host chooses the tag per call.
+// replay.  Dispatch order draws no ticket: the order is the workgroup index
+// and the host chooses the tag per call.  The two tag ranges are disjoint
+// (ticket order 1 .. 2^31 - 1, dispatch order 2^31 .. 2^32 - 1), so launches
+// of either order can follow each other on one scratch.
 struct LaunchSync {
   unsigned long long* ticket;  // device counter, shared by all launches on this scratch
   unsigned int* err;           // device error bits
@@ -43,9 +45,23 @@ struct LaunchSync {
 
 constexpr unsigned long long kEpochSpan = 1ull << 32;
 
-// Whether look-back kernels order their chunks by the ticket counter (the
-// default) or by workgroup index (environment OSSM_SCAN_ORDER=dispatch).
-bool scan_order_by_ticket();
+// First tag of the host-chosen (dispatch-order) range.
+constexpr unsigned int kDispatchTagBase = 0x80000000u;
+
+// Whether a look-back launch of `n_workgroups` workgroups on device `dev`
+// orders its chunks by the ticket counter (*by_ticket = true) or by workgroup
+// index.  Environment OSSM_SCAN_ORDER, read per call: "ticket" or "dispatch"
+// forces one; unset or "auto" takes dispatch order for a grid of at most one
+// workgroup per CU outside stream capture (every workgroup can be resident at
+// once, and the ticket's atomic round trip is ~1 us of a ~10 us launch) and
+// ticket order otherwise.  Forced dispatch order under capture returns
+// OSSM_ERR_UNSUPPORTED (its tag is chosen on the host, which a replay would
+// reuse).
+int choose_scan_order(int dev, bool capturing, int64_t n_workgroups, bool* by_ticket);
+
+// Next host-chosen tag of a dispatch-order launch from the counter `epoch`:
+// kDispatchTagBase .. 2^32 - 1, never a ticket-order tag.
+unsigned int next_dispatch_tag(unsigned int& epoch);
 
 // Events that the next oscillatory-scan launch on this host thread records as
 // its own start and end (ossm_time_next_launch); both null when unset.
@@ -98,12 +114,13 @@ class StreamCall {
 };
 
 // Returns a scratch payload of at least `payload_bytes` for the call's stream
-// and the launch bookkeeping of a look-back kernel.  The payload is
-// zero-filled when first allocated and is never cleared again: kernels tag
-// what they write with sync.tag.  Under capture, dispatch order is refused
-// (its tag is chosen on the host) and so is a payload larger than the
-// current one.
-int acquire_scratch(StreamCall& call, size_t payload_bytes, void** payload, LaunchSync* sync);
+// and the launch bookkeeping of a look-back kernel of `n_workgroups`
+// workgroups (its order from choose_scan_order).  The payload is zero-filled
+// when first allocated and is never cleared again: kernels tag what they
+// write with sync.tag.  Under capture, forced dispatch order is refused (its
+// tag is chosen on the host) and so is a payload larger than the current one.
+int acquire_scratch(StreamCall& call, size_t payload_bytes, int64_t n_workgroups, void** payload,
+                    LaunchSync* sync);
 
 // Returns a plain device workspace of at least `bytes` for the call's stream,
 // separate from the tagged look-back records: partial sums written here can

@@ -254,10 +254,13 @@ __device__ float4 lookback(unsigned long long* rec, int c, int dir, int n_chunks
 // on a streaming kernel of the same shape).  The ticket also gives the
 // launch's record tag (see LaunchSync), written into sync.tag.
 //
-// Dispatch order (OSSM_SCAN_ORDER=dispatch): the workgroup index.  This
-// relies on each XCD dispatching its share of the grid in increasing index
-// order; measured faster for long sequences (config 5 forward 324 vs 346 us)
-// and slower for config 2's forward (86 vs 79 us).
+// Dispatch order (sync.use_ticket == 0, which the host chooses for grids of at
+// most one workgroup per CU): the workgroup index, no atomic.  On an idle
+// device such a grid is resident at once, so nothing waits on a chunk that is
+// not running.  Otherwise (other work on the device, or a larger grid under
+// OSSM_SCAN_ORDER=dispatch) it relies on each XCD dispatching its share of the
+// grid in increasing index order, and a wait that still outlasts the bounded
+// spin gives NaN carries and an error bit.
 //
 // A ticket whose order is out of range means the counter was out of step
 // (a launch on this scratch that did not run to its end): the workgroup
@@ -285,7 +288,8 @@ __device__ __forceinline__ int launch_order(LaunchSync& sync, int total, int* s_
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     *s_slot = static_cast<int>(rel);
-    s_tag = static_cast<unsigned int>(epoch % 0xffffffffull) + 1u;  // 1 .. 2^32 - 1, never 0
+    // 1 .. 2^31 - 1: never 0 (never-written memory) nor a dispatch-order tag
+    s_tag = static_cast<unsigned int>(epoch % (kDispatchTagBase - 1u)) + 1u;
     s_poison = poison;
   }
   __syncthreads();

@@ -703,7 +703,7 @@ int sdl_forward_tw(const SdlParams& prm, const void* bu, void* states, int64_t L
   void* payload = nullptr;
   LaunchSync sync{};
   const int64_t total = n_chunks * n_groups;
-  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
   const bool tb = prm.a.t_stride == 0 && prm.g.t_stride == 0 && prm.s.t_stride == 0;
   hipLaunchKernelGGL((tb ? sdl_forward_kernel<V, T, W, true> : sdl_forward_kernel<V, T, W, false>),
                      dim3(static_cast<unsigned>(total)),
@@ -775,7 +775,7 @@ int sdl_backward_tw(const SdlParams& prm, const ParamShape (&shapes)[3], const v
   void* payload = nullptr;
   LaunchSync sync{};
   const int64_t total = n_chunks * n_groups;
-  if (int rc = acquire_scratch(call, rec_bytes, &payload, &sync)) return rc;
+  if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
   const bool tb = prm.a.t_stride == 0 && prm.g.t_stride == 0 && prm.s.t_stride == 0;
   hipLaunchKernelGGL((tb ? sdl_backward_kernel<V, T, W, true> : sdl_backward_kernel<V, T, W, false>),
                      dim3(static_cast<unsigned>(total)),

@@ -3,8 +3,10 @@ several host threads on one stream, HIP-graph capture and replay, and the
 failure path of the look-back protocol.
 
 The look-back scans draw each workgroup's order and the launch's record tag
-from a per-stream ticket counter on the device, and the backward passes leave
-partial sums in a per-stream workspace for the launch that follows.  Each C
+from a per-stream ticket counter on the device (grids of at most one
+workgroup per CU outside capture take the workgroup index and a host-chosen
+tag instead), and some backward passes leave partial sums in a per-stream
+workspace for the launch that follows.  Each C
 call holds its (device, stream) through its last launch, so calls from
 different host threads on the same stream reach the stream whole, and a
 captured call draws fresh orders and tags on every replay.
@@ -20,8 +22,8 @@ import pytest
 import torch
 
 import oracle
-from tests.gpu_util import (announce, assert_close, dlinoss_inputs, need_gpu, no_device_errors,
-                            to_dev, to_np)
+from tests.gpu_util import (announce, assert_close, assert_parity, dlinoss_inputs, need_gpu,
+                            no_device_errors, to_dev, to_np)
 
 pytestmark = pytest.mark.gpu
 RTOL, ATOL = 1e-4, 1e-5
@@ -213,15 +215,18 @@ def test_graph_capture_refused_when_scratch_would_grow(K):
     no_device_errors()
 
 
-def test_protocol_failure_gives_nan_not_garbage(K):
+def test_protocol_failure_gives_nan_not_garbage(K, monkeypatch):
     """With the stream's ticket counter knocked out of step from the host (as
     a launch that did not run to its end would leave it), every workgroup of
     the next look-back launch draws an out-of-range ticket: the launch raises
     the bad-ticket bit, the chunks that needed a carry come out NaN (the first
     chunk, which needs none, is still right), and after the error check the
     next call is correct again.  Forward and backward of D-LinOSS, and the
-    LRU and selective D-LinOSS forwards."""
+    LRU and selective D-LinOSS forwards.  These grids are small enough for
+    dispatch order, which draws no ticket, so ticket order is forced."""
     from ossm_amd import _lib
+
+    monkeypatch.setenv("OSSM_SCAN_ORDER", "ticket")
 
     lib = _lib.load()
     stream = torch.cuda.current_stream().cuda_stream
@@ -271,6 +276,93 @@ def test_protocol_failure_gives_nan_not_garbage(K):
     assert_close(st, ref, RTOL, ATOL, "after recovery")
     grads = K.dlinoss_imex1_backward(*args, to_dev(st), to_dev(go))
     assert_close(to_np(grads[3]), rgrads[3], RTOL, ATOL, "grad_bu after recovery")
+    no_device_errors()
+
+
+def _dl_truth(a, g, dt, bu, go):
+    """fp32 oracle states and gradients, and the fp64 ones as arbiter."""
+    st = oracle.dlinoss_forward("imex1", a, g, dt, bu)
+    grads = oracle.dlinoss_backward("imex1", a, g, dt, bu, st, go)
+    a64, g64, d64 = (x.astype(np.float64) for x in (a, g, dt))
+    b64, go64 = bu.astype(np.complex128), go.astype(np.complex128)
+    st64 = oracle.dlinoss_forward("imex1", a64, g64, d64, b64)
+    return st, grads, st64, oracle.dlinoss_backward("imex1", a64, g64, d64, b64, st64, go64)
+
+
+# forward grids of 16, 256 and 512 workgroups: the device has 256 CUs, so the
+# default (auto) takes dispatch order for the first two and ticket order for
+# the third
+@pytest.mark.parametrize("shape", [(1000, 2, 64), (4096, 8, 128), (4096, 16, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_scan_orders_alternate_on_one_stream(K, monkeypatch, shape):
+    """D-LinOSS imex1 forward + backward and the LRU forward, launched in
+    ticket, dispatch and automatic order (OSSM_SCAN_ORDER, read per call) in
+    turn on one stream, each call on the other of two input sets: every result
+    matches the oracle.  A launch that took a look-back record, or the
+    zero-filled flag of the parameter gradients, left by the previous launch
+    (of the other order, on other inputs) would carry that launch's values:
+    the tags the host chooses for dispatch order and those drawn on the device
+    for ticket order are disjoint."""
+    L, B, P = shape
+    sets = []
+    for seed in (51, 52):
+        a, g, dt, bu, go = dlinoss_inputs(L, B, P, seed=seed, variant="imex1")
+        lam = (np.random.default_rng(seed).uniform(0.5, 1.0, P)
+               * np.exp(1j * np.random.default_rng(seed + 9).uniform(0, 3, P))).astype(np.complex64)
+        sets.append(dict(dev=[to_dev(x) for x in (a, g, dt, bu)], go=to_dev(go),
+                         truth=_dl_truth(a, g, dt, bu, go),
+                         lam=(torch.from_numpy(lam.real.copy()).cuda(), torch.from_numpy(lam.imag.copy()).cuda()),
+                         lru=(oracle.diag_forward(lam, bu),
+                              oracle.diag_forward(lam.astype(np.complex128), bu.astype(np.complex128)))))
+    names = ("grad_a", "grad_g", "grad_step", "grad_bu")
+    for i, mode in enumerate(("ticket", "dispatch", "auto", "dispatch", "ticket", "auto", "ticket")):
+        monkeypatch.setenv("OSSM_SCAN_ORDER", mode)
+        d = sets[i % 2]
+        announce(f"runtime: scan order {mode} L={L} B={B} P={P} inputs {i % 2}")
+        st = K.dlinoss_imex1_forward(*d["dev"])
+        grads = K.dlinoss_imex1_backward(*d["dev"], st, d["go"])
+        bseq = torch.view_as_real(d["dev"][3]).contiguous()
+        y = K.lru_scan(d["lam"][0], d["lam"][1], bseq)
+        r_st, r_grads, t_st, t_grads = d["truth"]
+        assert_parity(to_np(st), r_st, t_st, RTOL, ATOL, f"{mode} states")
+        for got, r32, r64, name in zip(grads, r_grads, t_grads, names):
+            atol = ATOL if name == "grad_bu" else 2e-5 * max(1.0, float(np.abs(r64).max()))
+            assert_parity(to_np(got), r32, r64, RTOL, atol, f"{mode} {name}")
+        y = to_np(y)
+        y = y[..., 0] + 1j * y[..., 1]
+        assert_parity(y, d["lru"][0], d["lru"][1], RTOL, ATOL, f"{mode} lru")
+    no_device_errors()
+
+
+def test_scan_order_setting_is_checked(K, monkeypatch):
+    """An OSSM_SCAN_ORDER other than auto, ticket or dispatch is refused with
+    RuntimeError before anything is launched; forced dispatch order under
+    stream capture is refused too (its tags are chosen on the host)."""
+    a, g, dt, bu, _ = dlinoss_inputs(100, 2, 64, seed=53, variant="imex1")
+    args = [to_dev(x) for x in (a, g, dt, bu)]
+    K.dlinoss_imex1_forward(*args)
+    monkeypatch.setenv("OSSM_SCAN_ORDER", "tickets")
+    with pytest.raises(RuntimeError, match="OSSM_SCAN_ORDER"):
+        K.dlinoss_imex1_forward(*args)
+    monkeypatch.setenv("OSSM_SCAN_ORDER", "dispatch")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        K.dlinoss_imex1_forward(*args)  # eager warm-up of the side stream's scratch
+    side.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    announce("runtime: scan order setting checks")
+    with torch.cuda.stream(side):
+        graph.capture_begin()
+        try:
+            with pytest.raises(RuntimeError, match="capture needs ticket order"):
+                K.dlinoss_imex1_forward(*args)
+        finally:
+            graph.capture_end()
+    torch.cuda.synchronize()
+    monkeypatch.delenv("OSSM_SCAN_ORDER")
+    st = K.dlinoss_imex1_forward(*args)
+    assert_close(to_np(st), oracle.dlinoss_forward("imex1", a, g, dt, bu), RTOL, ATOL, "after refusals")
     no_device_errors()
 
 
