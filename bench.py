@@ -588,7 +588,7 @@ def _detail_configs(torch, K, dev, reps=20):
 
 
 CASES = ("c1_linoss_im_fwd", "c3_selective_fp32", "c4_shape_selective_fp32", "c4_selective_bf16",
-         "c5_dlinoss_fwd_long")
+         "c5_dlinoss_fwd_long", "sdlinoss_imex1_c2_full")
 
 
 def run_case(name: str, steps: int, warmup: int) -> int:
@@ -609,6 +609,20 @@ def run_case(name: str, steps: int, warmup: int) -> int:
     elif name == "c5_dlinoss_fwd_long":
         a, gam, dt, bu, _ = dlinoss_inputs(torch, 65536, 4, 256, dev, H=64, seed=5)
         out["fwd_ms"] = _ev_time(torch, lambda: K.dlinoss_imex1_forward(a, gam, dt, bu), steps, warmup)
+    elif name == "sdlinoss_imex1_c2_full":
+        # selective D-LinOSS imex1 with per-step parameters at config 2's shape
+        # (the detail run's inputs)
+        L, B, P = 4096, 32, 128
+        g = torch.Generator(device=dev).manual_seed(6)
+        bu, go = (torch.complex(torch.randn(L, B, P, device=dev, generator=g),
+                                torch.randn(L, B, P, device=dev, generator=g)) for _ in range(2))
+        A = torch.rand((L, B, P), device=dev, generator=g) * 0.9 + 0.1
+        G = torch.rand((L, B, P), device=dev, generator=g)
+        S = torch.sigmoid(torch.randn((L, B, P), device=dev, generator=g))
+        st = K.sdlinoss_imex1_forward(A, G, S, bu)
+        out["fwd_ms"] = _ev_time(torch, lambda: K.sdlinoss_imex1_forward(A, G, S, bu), steps, warmup)
+        out["bwd_ms"] = _ev_time(torch, lambda: K.sdlinoss_imex1_backward(A, G, S, bu, st, go),
+                                 steps, warmup)
     else:
         shape = (256, 128, 200, 16) if name == "c3_selective_fp32" else (16, 1536, 2048, 16)
         xs = selective_inputs(torch, *shape, dev)
