@@ -123,7 +123,7 @@ int choose_scan_order(int dev, bool capturing, int64_t n_workgroups, bool* by_ti
                        "call, which a replayed HIP graph would reuse: capture needs ticket order");
     *by_ticket = false;
   } else if (mode == "auto" || mode.empty()) {
-    *by_ticket = capturing || n_workgroups > cu_count(dev);
+    *by_ticket = capturing || n_workgroups * 4 > cu_count(dev);
   } else {
     return set_error(OSSM_ERR_INVALID_ARGUMENT,
                      "ossm_scan: OSSM_SCAN_ORDER must be auto, ticket or dispatch, not '" + mode + "'");

@@ -51,10 +51,20 @@ constexpr unsigned int kDispatchTagBase = 0x80000000u;
 // Whether a look-back launch of `n_workgroups` workgroups on device `dev`
 // orders its chunks by the ticket counter (*by_ticket = true) or by workgroup
 // index.  Environment OSSM_SCAN_ORDER, read per call: "ticket" or "dispatch"
-// forces one; unset or "auto" takes dispatch order for a grid of at most one
-// workgroup per CU outside stream capture (every workgroup can be resident at
-// once, and the ticket's atomic round trip is ~1 us of a ~10 us launch) and
-// ticket order otherwise.  Forced dispatch order under capture returns
+// forces one; unset or "auto" takes dispatch order for a grid of at most a
+// quarter as many workgroups as the device has CUs, outside stream capture,
+// and ticket order otherwise.  Such a grid is resident at once on an idle
+// device, and the ticket's atomic round trip is ~1 us of a ~10 us launch.
+//
+// The quarter bounds what concurrent launches can do.  A dispatch-order
+// workgroup may wait on one of lower index that another XCD has not yet
+// dispatched; dispatch-order launches on other streams whose waiting
+// workgroups fill the XCDs each other's next workgroup needs would stall
+// until the bounded spin gives up (NaN, error bit).  Ticket-order launches
+// always drain, since they wait only on workgroups already running.  With a
+// launch's share of an XCD at most a quarter of its CUs, filling one XCD
+// takes four other such launches, five at once, each of workgroups that hold
+// a whole CU.  Forced dispatch order under capture returns
 // OSSM_ERR_UNSUPPORTED (its tag is chosen on the host, which a replay would
 // reuse).
 int choose_scan_order(int dev, bool capturing, int64_t n_workgroups, bool* by_ticket);

@@ -255,12 +255,13 @@ __device__ float4 lookback(unsigned long long* rec, int c, int dir, int n_chunks
 // launch's record tag (see LaunchSync), written into sync.tag.
 //
 // Dispatch order (sync.use_ticket == 0, which the host chooses for grids of at
-// most one workgroup per CU): the workgroup index, no atomic.  On an idle
-// device such a grid is resident at once, so nothing waits on a chunk that is
-// not running.  Otherwise (other work on the device, or a larger grid under
-// OSSM_SCAN_ORDER=dispatch) it relies on each XCD dispatching its share of the
-// grid in increasing index order, and a wait that still outlasts the bounded
-// spin gives NaN carries and an error bit.
+// most a quarter as many workgroups as CUs; see choose_scan_order): the
+// workgroup index, no atomic.  On an idle device such a grid is resident at
+// once, so nothing waits on a chunk that is not running.  Otherwise (other
+// work on the device, or a larger grid under OSSM_SCAN_ORDER=dispatch) it
+// relies on each XCD dispatching its share of the grid in increasing index
+// order, and a wait that still outlasts the bounded spin gives NaN carries
+// and an error bit.
 //
 // A ticket whose order is out of range means the counter was out of step
 // (a launch on this scratch that did not run to its end): the workgroup
