@@ -190,12 +190,16 @@ def test_sdlinoss_repeatable(K):
     """Two runs agree to rounding: the carries between chunks come from the
     decoupled look-back, whose association depends on which records are already
     published, and each chunk's share of the parameter gradients is added with a
-    float atomic, so the last bits may differ."""
+    float atomic, so the last bits may differ.  A state is a sum of terms of
+    the states' own scale, so its rounding differences are ulps of that scale
+    (the largest |state|), not of the state itself: a state near zero may
+    differ by ~1e-7 between runs."""
     args = sdl_inputs("im", "bcast_t", 500, 4, 96, seed=9)
     announce("sdlinoss repeatability")
     s1, g1 = _run(K, "im", *args)
     s2, g2 = _run(K, "im", *args)
-    assert_close(to_np(s1), to_np(s2), 1e-6, 1e-7, "states")
+    s1, s2 = to_np(s1), to_np(s2)
+    assert_close(s1, s2, 1e-6, 1e-6 * max(1.0, float(np.abs(s2).max())), "states")
     for a, b, name in zip(g1, g2, NAMES):
         a, b = to_np(a), to_np(b)
         assert_close(a, b, 1e-5, 1e-6 * max(1.0, float(np.abs(b).max())), name)
