@@ -26,10 +26,13 @@
  * several host threads on one stream are safe and reach the stream whole.
  * Each look-back launch draws its chunk order and record tag on the device
  * from the scratch's ticket counter, so a call may be captured into a HIP
- * graph and the graph replayed.  Under capture the scratch and workspace are
- * used as they are: a call that would need them to grow returns
- * OSSM_ERR_UNSUPPORTED before enqueuing anything (run it once eagerly on the
- * stream first), as does OSSM_SCAN_ORDER=dispatch (host-chosen tags).
+ * graph and the graph replayed.  (Outside capture, a launch of at most a
+ * quarter as many workgroups as the device has CUs takes the workgroup index
+ * as its chunk order and a host-chosen tag instead, saving the ticket's
+ * atomic round trip.)  Under capture the scratch and workspace are used as
+ * they are: a call that would need them to grow returns OSSM_ERR_UNSUPPORTED
+ * before enqueuing anything (run it once eagerly on the stream first), as
+ * does OSSM_SCAN_ORDER=dispatch (host-chosen tags for every launch).
  * Buffers a graph captured are never freed.  Replays use the capture
  * stream's scratch: replay the graph on that stream, or ordered with
  * everything else that uses it.
@@ -77,9 +80,10 @@ uint32_t ossm_device_error_bits(ossm_stream_t stream);
 /*
  * Test hook, no counterpart in the reference: synchronises `stream` and adds
  * `delta` to the ticket counter of its scratch, as a launch that did not run
- * to its end would leave it.  The next look-back launches on the stream then
- * draw out-of-range tickets: they raise bit 1 of ossm_device_error_bits and
- * their carries are NaN, while every kernel still exits normally;
+ * to its end would leave it.  The next ticket-order look-back launches on
+ * the stream then draw out-of-range tickets: they raise bit 1 of
+ * ossm_device_error_bits and their carries are NaN, while every kernel still
+ * exits normally;
  * ossm_device_error_bits puts the counter back in step.  For tests of the
  * failure path only.
  */
