@@ -210,7 +210,15 @@ struct SdlTb {
 // ============================================================================
 // Forward kernel
 // ============================================================================
-template <class Model, int T, int W, int OCC>
+// PERSIST (ticket order, a grid of fewer workgroups than chunks): workgroup b
+// takes ceil((total - b) / grid) chunks one after the other, so the launch
+// still draws exactly `total` tickets (the protocol of launch_order,
+// out-of-range tickets included), and draws each next ticket while it
+// stores the current chunk: the atomic's round trip and the start of a new
+// workgroup leave the path from one chunk to the next.  A workgroup holding
+// a drawn ticket is running and takes that chunk next without waiting on
+// anything, so every look-back still ends.
+template <class Model, int T, int W, int OCC, bool PERSIST>
 __global__ __launch_bounds__(W * kWave, OCC) void osc_forward_kernel(
     typename Model::Params prm, const typename Model::In* __restrict__ in,
     float4* __restrict__ out, int L, int nc, int n_groups, int n_chunks,
@@ -218,10 +226,33 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_forward_kernel(
   __shared__ float4 s_agg[W][kWave];
   __shared__ float4 s_carry[kWave];
   __shared__ int s_ticket;
+  __shared__ unsigned int s_tag;
+  __shared__ int s_poison;
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = wave_id();
-  const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
+  const int total = n_groups * n_chunks;
+  int order;
+  int left = 1;  // chunks this workgroup still takes, the current one included
+  if constexpr (PERSIST) {
+    left = (total - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) /
+           static_cast<int>(gridDim.x);
+    if (threadIdx.x == 0) {
+      unsigned int tag = 0;
+      int poison = 0;
+      s_ticket = draw_ticket(sync, total, &tag, &poison);
+      s_tag = tag;
+      s_poison = poison;
+    }
+    __syncthreads();
+    sync.tag = __builtin_amdgcn_readfirstlane(s_tag);
+    sync.poison = __builtin_amdgcn_readfirstlane(s_poison);
+    order = __builtin_amdgcn_readfirstlane(s_ticket);
+  } else {
+    order = launch_order(sync, total, &s_ticket);
+  }
+  for (;;) {
+  const int ticket = order;
   const int c = ticket / n_groups;
   const int g = ticket - c * n_groups;
   const int ch = g * kWave + lane;
@@ -279,7 +310,15 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_forward_kernel(
   }
   __syncthreads();
 
-  // 3. own carry, then re-run the sub-chunk and store
+  // 3. own carry, then re-run the sub-chunk and store (PERSIST: the next
+  // ticket is drawn first, its round trip overlapping the stores)
+  int next = 0, next_poison = 0;
+  if constexpr (PERSIST) {
+    if (threadIdx.x == 0 && left > 1) {
+      unsigned int tag = 0;
+      next = draw_ticket(sync, total, &tag, &next_poison);
+    }
+  }
   float4 s = s_carry[lane];
   for (int v = 0; v < w; ++v) s = f4add(mat_apply(MT, s), s_agg[v][lane]);
   if (active) {
@@ -299,6 +338,18 @@ __global__ __launch_bounds__(W * kWave, OCC) void osc_forward_kernel(
         }
       }
     }
+  }
+  if constexpr (!PERSIST) break;
+  if (--left == 0) break;
+  // every wave is past its reads of s_agg and s_carry before the next chunk
+  // writes them
+  if (threadIdx.x == 0) {
+    s_ticket = next;
+    s_poison = next_poison;
+  }
+  __syncthreads();
+  sync.poison = __builtin_amdgcn_readfirstlane(s_poison);
+  order = __builtin_amdgcn_readfirstlane(s_ticket);
   }
 }
 
@@ -687,29 +738,66 @@ FwdPlan fwd_plan(int64_t L, int64_t nc) {
 // `payload` and launch bookkeeping `sync`; `tm` (when set) are events the
 // launch records as its own start and end.  The caller undoes its ticket
 // reservation when this returns an error (nothing was launched).
+// Workgroups of a persistent forward with tile (TT, WW, OO): as many as the
+// device holds at once (0 when the occupancy query fails: no persistent launch).
+template <class Model, int TT, int WW, int OO>
+int64_t forward_persist_grid() {
+  static const int64_t cap = [] {
+    int dev = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(&osc_forward_kernel<Model, TT, WW, OO, true>),
+            WW * kWave, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      return int64_t(0);
+    }
+    return int64_t(per_cu) * device_cu_count(dev);
+  }();
+  return cap;
+}
+
+// OSSM_OSC_PERSIST=0 (read per call) launches one workgroup per chunk always.
+bool forward_persist_enabled() {
+  const char* e = std::getenv("OSSM_OSC_PERSIST");
+  return e == nullptr || std::string(e) != "0";
+}
+
 template <class Model>
 int enqueue_forward(const FwdPlan& pl, const typename Model::Params& prm, const void* in, void* out,
                     int64_t L, int64_t nc, hipStream_t stream, void* payload, const LaunchSync& sync,
                     const LaunchTiming& tm = LaunchTiming{}) {
   const Tile& tile = pl.tile;
-  const dim3 grid(static_cast<unsigned>(pl.total));
   bool launched = false;
 #define OSSM_FWD_ARGS                                                                         \
   prm, static_cast<const typename Model::In*>(in), static_cast<float4*>(out),                 \
       static_cast<int>(L), static_cast<int>(nc), static_cast<int>(pl.n_groups),               \
       static_cast<int>(pl.n_chunks), static_cast<unsigned long long*>(payload), sync
+#define OSSM_FWD_LAUNCH_ONE(TT, WW, OO, PP, NWG)                                              \
+  {                                                                                           \
+    const dim3 grid(static_cast<unsigned>(NWG));                                              \
+    if (tm.start != nullptr)                                                                  \
+      hipExtLaunchKernelGGL((osc_forward_kernel<Model, TT, WW, OO, PP>), grid,                \
+                            dim3(WW * kWave), 0, stream, tm.start, tm.stop, 0, OSSM_FWD_ARGS); \
+    else                                                                                      \
+      hipLaunchKernelGGL((osc_forward_kernel<Model, TT, WW, OO, PP>), grid, dim3(WW * kWave), \
+                         0, stream, OSSM_FWD_ARGS);                                           \
+  }
+  // the default tiles (16 x 16 and 16 x 8) run persistent in ticket order
+  // when the grid has more chunks than the device holds workgroups at once
 #define OSSM_LAUNCH_FWD(TT, WW, OO)                                                           \
   if (!launched && tile.T == TT && tile.W == WW && tile.O == OO) {                            \
-    if (tm.start != nullptr)                                                                  \
-      hipExtLaunchKernelGGL((osc_forward_kernel<Model, TT, WW, OO>), grid, dim3(WW * kWave), 0, \
-                            stream, tm.start, tm.stop, 0, OSSM_FWD_ARGS);                     \
-    else                                                                                      \
-      hipLaunchKernelGGL((osc_forward_kernel<Model, TT, WW, OO>), grid, dim3(WW * kWave), 0,  \
-                         stream, OSSM_FWD_ARGS);                                              \
+    bool persist = false;                                                                     \
+    if constexpr (TT == 16 && OO == 1 && (WW == 16 || WW == 8)) {                             \
+      const int64_t cap = forward_persist_grid<Model, TT, WW, OO>();                          \
+      persist = sync.use_ticket && cap > 0 && pl.total > cap && forward_persist_enabled();     \
+      if (persist) OSSM_FWD_LAUNCH_ONE(TT, WW, OO, true, cap)                                 \
+    }                                                                                         \
+    if (!persist) OSSM_FWD_LAUNCH_ONE(TT, WW, OO, false, pl.total)                            \
     launched = true;                                                                          \
   }
   OSSM_FWD_TILES(OSSM_LAUNCH_FWD)
 #undef OSSM_LAUNCH_FWD
+#undef OSSM_FWD_LAUNCH_ONE
 #undef OSSM_FWD_ARGS
   if (!launched) return set_error(OSSM_ERR_UNSUPPORTED, "OSSM_OSC_TILE_FWD names no built tile");
   return launch_check("osc_forward_kernel");

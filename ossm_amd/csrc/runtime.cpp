@@ -90,11 +90,7 @@ int take_launch_timing(const StreamCall& call, LaunchTiming* out) {
   return OSSM_OK;
 }
 
-namespace {
-
-// Compute units of device `dev`, looked up once per device (0 when the query
-// fails, which leaves every launch in ticket order).
-int cu_count(int dev) {
+int device_cu_count(int dev) {
   constexpr int kMaxDevices = 64;
   static std::atomic<int> counts[kMaxDevices] = {};
   if (dev < 0 || dev >= kMaxDevices) return 0;
@@ -109,8 +105,6 @@ int cu_count(int dev) {
   return n;
 }
 
-}  // namespace
-
 int choose_scan_order(int dev, bool capturing, int64_t n_workgroups, bool* by_ticket) {
   const char* v = std::getenv("OSSM_SCAN_ORDER");
   const std::string mode = v == nullptr ? std::string("auto") : std::string(v);
@@ -123,7 +117,7 @@ int choose_scan_order(int dev, bool capturing, int64_t n_workgroups, bool* by_ti
                        "call, which a replayed HIP graph would reuse: capture needs ticket order");
     *by_ticket = false;
   } else if (mode == "auto" || mode.empty()) {
-    *by_ticket = capturing || n_workgroups * 4 > cu_count(dev);
+    *by_ticket = capturing || n_workgroups * 4 > device_cu_count(dev);
   } else {
     return set_error(OSSM_ERR_INVALID_ARGUMENT,
                      "ossm_scan: OSSM_SCAN_ORDER must be auto, ticket or dispatch, not '" + mode + "'");

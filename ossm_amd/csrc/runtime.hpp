@@ -69,6 +69,10 @@ constexpr unsigned int kDispatchTagBase = 0x80000000u;
 // reuse).
 int choose_scan_order(int dev, bool capturing, int64_t n_workgroups, bool* by_ticket);
 
+// Compute units of device `dev`, looked up once per device (0 when the query
+// fails).
+int device_cu_count(int dev);
+
 // Next host-chosen tag of a dispatch-order launch from the counter `epoch`:
 // kDispatchTagBase .. 2^32 - 1, never a ticket-order tag.
 unsigned int next_dispatch_tag(unsigned int& epoch);

@@ -269,28 +269,40 @@ __device__ float4 lookback(unsigned long long* rec, int c, int dir, int n_chunks
 // misaligned launch never draws are exactly those the out-of-range tickets
 // map to — and marks the launch poisoned, so its look-backs return NaN and
 // every output that depends on a carry is NaN.
+// One ticket draw by the calling thread: the chunk order it gives, the
+// launch's record tag in *tag and, for an out-of-range ticket (see
+// launch_order), 1 in *poison.  The draw of the launch's last order moves the
+// counter to the next epoch.
+__device__ __forceinline__ int draw_ticket(const LaunchSync& sync, int total, unsigned int* tag,
+                                           int* poison) {
+  const unsigned long long t =
+      __hip_atomic_fetch_add(sync.ticket, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  unsigned long long rel = t & (kEpochSpan - 1);
+  const unsigned long long epoch = t >> 32;
+  *poison = 0;
+  if (rel >= static_cast<unsigned long long>(total)) {
+    __hip_atomic_fetch_or(sync.err, kErrBadTicket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    rel %= static_cast<unsigned long long>(total);
+    *poison = 1;
+  } else if (rel == static_cast<unsigned long long>(total - 1)) {
+    // the launch's last ticket: the next launch starts at the next epoch
+    __hip_atomic_fetch_add(sync.ticket, kEpochSpan - static_cast<unsigned long long>(total),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // 1 .. 2^31 - 1: never 0 (never-written memory) nor a dispatch-order tag
+  *tag = static_cast<unsigned int>(epoch % (kDispatchTagBase - 1u)) + 1u;
+  return static_cast<int>(rel);
+}
+
 __device__ __forceinline__ int launch_order(LaunchSync& sync, int total, int* s_slot) {
   if (!sync.use_ticket) return static_cast<int>(blockIdx.x);
   __shared__ unsigned int s_tag;
   __shared__ int s_poison;
   if (threadIdx.x == 0) {
-    const unsigned long long t =
-        __hip_atomic_fetch_add(sync.ticket, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    unsigned long long rel = t & (kEpochSpan - 1);
-    const unsigned long long epoch = t >> 32;
+    unsigned int tag = 0;
     int poison = 0;
-    if (rel >= static_cast<unsigned long long>(total)) {
-      __hip_atomic_fetch_or(sync.err, kErrBadTicket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      rel %= static_cast<unsigned long long>(total);
-      poison = 1;
-    } else if (rel == static_cast<unsigned long long>(total - 1)) {
-      // the launch's last ticket: the next launch starts at the next epoch
-      __hip_atomic_fetch_add(sync.ticket, kEpochSpan - static_cast<unsigned long long>(total),
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    *s_slot = static_cast<int>(rel);
-    // 1 .. 2^31 - 1: never 0 (never-written memory) nor a dispatch-order tag
-    s_tag = static_cast<unsigned int>(epoch % (kDispatchTagBase - 1u)) + 1u;
+    *s_slot = draw_ticket(sync, total, &tag, &poison);
+    s_tag = tag;
     s_poison = poison;
   }
   __syncthreads();

@@ -279,6 +279,65 @@ def test_protocol_failure_gives_nan_not_garbage(K, monkeypatch):
     no_device_errors()
 
 
+# grids of 528 and 1,056 chunks (16 x 16 tiles): more than the device holds at once,
+# so the forward runs persistent (each workgroup two to five chunks, ragged counts)
+@pytest.mark.parametrize("shape", [(8292, 8, 128), (4200, 32, 128)], ids=lambda s: "x".join(map(str, s)))
+def test_persistent_forward_matches_oracle_and_one_chunk_per_workgroup(K, monkeypatch, shape):
+    """The persistent D-LinOSS forward (ticket order, fewer workgroups than
+    chunks, each drawing its next ticket while it stores) against the oracle
+    and against the one-workgroup-per-chunk launch (OSSM_OSC_PERSIST=0), twice
+    in a row on one stream; the LinOSS forward likewise."""
+    L, B, P = shape
+    a, g, dt, bu, _ = dlinoss_inputs(L, B, P, seed=61, variant="imex1")
+    args = [to_dev(x) for x in (a, g, dt, bu)]
+    ref = oracle.dlinoss_forward("imex1", a, g, dt, bu)
+    st64 = oracle.dlinoss_forward("imex1", *(x.astype(np.float64) for x in (a, g, dt)),
+                                  bu.astype(np.complex128))
+    announce(f"runtime: persistent forward L={L} B={B} P={P}")
+    for mode in ("1", "0", "1"):
+        monkeypatch.setenv("OSSM_OSC_PERSIST", mode)
+        st = to_np(K.dlinoss_imex1_forward(*args))
+        assert_parity(st, ref, st64, RTOL, ATOL, f"persist={mode} states")
+    ms = [np.full(P, v, dtype=np.complex64) for v in (0.9 + 0.05j, -0.05, 0.05, 0.9 - 0.05j)]
+    b = (np.random.default_rng(62).normal(size=(L, B, P, 2)) + 0j).astype(np.complex64)
+    lref = oracle.linoss_forward(*ms, b)
+    l64 = oracle.linoss_forward(*(m.astype(np.complex128) for m in ms), b.astype(np.complex128))
+    for mode in ("1", "0"):
+        monkeypatch.setenv("OSSM_OSC_PERSIST", mode)
+        out = to_np(K.linoss_scan(*[to_dev(m) for m in ms], to_dev(b)))
+        assert_parity(out, lref, l64, RTOL, ATOL, f"linoss persist={mode}")
+    no_device_errors()
+
+
+def test_protocol_failure_persistent_forward(K, monkeypatch):
+    """The failure path of the persistent forward: with the ticket counter out
+    of step every draw is out of range, every chunk is still taken exactly
+    once (orders modulo the chunk count), the chunks that needed a carry are
+    NaN, the first chunk is right, and the next call is correct."""
+    from ossm_amd import _lib
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    L, B, P = 8292, 8, 128  # 528 chunks of 256 steps: persistent
+    a, g, dt, bu, _ = dlinoss_inputs(L, B, P, seed=63, variant="imex1")
+    args = [to_dev(x) for x in (a, g, dt, bu)]
+    ref = oracle.dlinoss_forward("imex1", a, g, dt, bu)
+    announce("runtime: persistent forward protocol failure -> NaN")
+    monkeypatch.setenv("OSSM_SCAN_ORDER", "ticket")
+    K.dlinoss_imex1_forward(*args)
+    assert _lib.device_error_bits() == 0
+    _lib.check(lib.ossm_test_skew_tickets(stream, 1 << 20))
+    st = to_np(K.dlinoss_imex1_forward(*args))
+    assert _lib.device_error_bits() == 2
+    assert_close(st[:256], ref[:256], RTOL, ATOL, "first chunk")
+    assert np.isnan(st[256:]).all()
+    st = to_np(K.dlinoss_imex1_forward(*args))
+    st64 = oracle.dlinoss_forward("imex1", *(x.astype(np.float64) for x in (a, g, dt)),
+                                  bu.astype(np.complex128))
+    assert_parity(st, ref, st64, RTOL, ATOL, "after recovery")  # L = 8292: fp64 arbiter
+    no_device_errors()
+
+
 def _dl_truth(a, g, dt, bu, go):
     """fp32 oracle states and gradients, and the fp64 ones as arbiter."""
     st = oracle.dlinoss_forward("imex1", a, g, dt, bu)
