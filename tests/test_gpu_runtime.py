@@ -279,7 +279,7 @@ def test_protocol_failure_gives_nan_not_garbage(K, monkeypatch):
     no_device_errors()
 
 
-# grids of 528 and 1,056 chunks (16 x 16 tiles): more than the device holds at once,
+# grids of 528 and 1,088 chunks (16 x 16 tiles): more than the device holds at once,
 # so the forward runs persistent (each workgroup two to five chunks, ragged counts)
 @pytest.mark.parametrize("shape", [(8292, 8, 128), (4200, 32, 128)], ids=lambda s: "x".join(map(str, s)))
 def test_persistent_forward_matches_oracle_and_one_chunk_per_workgroup(K, monkeypatch, shape):
