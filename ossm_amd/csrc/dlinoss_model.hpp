@@ -171,6 +171,8 @@ struct Dlinoss {
   // to the outputs.
   static constexpr int kOutsPerColumn = 1;
   static constexpr bool kWaveEpilogue = false;  // one lane per channel (see Linoss)
+  // the forward may run persistent (105-109 VGPRs, no spills)
+  static constexpr bool kPersistForward = true;
   static __device__ void epilogue(const Params& prm, int ch, int /*chunk*/, const double* S,
                                   float* grad_a, float* grad_g, float* grad_step) {
     const int p = ch % prm.P;

@@ -118,6 +118,11 @@ struct Linoss {
   // 1's shape.  `active`: the lane's channel is below nc.
   static constexpr int kOutsPerColumn = 8;
   static constexpr bool kWaveEpilogue = true;
+  // The 16 x 16 forward is at the 128-VGPR cap of a 16-wave workgroup (two
+  // complex inputs per step): 9 registers spill one chunk per workgroup, 29
+  // in the persistent loop (config 2's shape 94 -> 123 us), so it keeps one
+  // workgroup per chunk.
+  static constexpr bool kPersistForward = false;
   static __device__ void epilogue_wave(const Params& prm, int ch, const double* S, float* grad_m) {
     __shared__ float s_t[8 * kWave];
     const int lane = threadIdx.x & (kWave - 1);
@@ -195,6 +200,7 @@ struct SdlTb {
   }
   static constexpr int kOutsPerColumn = 0;
   static constexpr bool kWaveEpilogue = false;
+  static constexpr bool kPersistForward = true;  // no spills either way (105 VGPRs)
   static __device__ void epilogue(const Params& prm, int ch, int /*chunk*/, const double* S, float* pa,
                                   float* pg, float* ps) {
     const Raw r = load_raw(prm, ch);
@@ -784,10 +790,11 @@ int enqueue_forward(const FwdPlan& pl, const typename Model::Params& prm, const 
   }
   // the default tiles (16 x 16 and 16 x 8) run persistent in ticket order
   // when the grid has more chunks than the device holds workgroups at once
+  // (models whose persistent loop spills excepted: Model::kPersistForward)
 #define OSSM_LAUNCH_FWD(TT, WW, OO)                                                           \
   if (!launched && tile.T == TT && tile.W == WW && tile.O == OO) {                            \
     bool persist = false;                                                                     \
-    if constexpr (TT == 16 && OO == 1 && (WW == 16 || WW == 8)) {                             \
+    if constexpr (Model::kPersistForward && TT == 16 && OO == 1 && (WW == 16 || WW == 8)) {   \
       const int64_t cap = forward_persist_grid<Model, TT, WW, OO>();                          \
       persist = sync.use_ticket && cap > 0 && pl.total > cap && forward_persist_enabled();     \
       if (persist) OSSM_FWD_LAUNCH_ONE(TT, WW, OO, true, cap)                                 \

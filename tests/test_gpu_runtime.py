@@ -286,7 +286,8 @@ def test_persistent_forward_matches_oracle_and_one_chunk_per_workgroup(K, monkey
     """The persistent D-LinOSS forward (ticket order, fewer workgroups than
     chunks, each drawing its next ticket while it stores) against the oracle
     and against the one-workgroup-per-chunk launch (OSSM_OSC_PERSIST=0), twice
-    in a row on one stream; the LinOSS forward likewise."""
+    in a row on one stream; the selective D-LinOSS forward with parameters
+    constant over time (the same kernel, another model) likewise."""
     L, B, P = shape
     a, g, dt, bu, _ = dlinoss_inputs(L, B, P, seed=61, variant="imex1")
     args = [to_dev(x) for x in (a, g, dt, bu)]
@@ -298,14 +299,16 @@ def test_persistent_forward_matches_oracle_and_one_chunk_per_workgroup(K, monkey
         monkeypatch.setenv("OSSM_OSC_PERSIST", mode)
         st = to_np(K.dlinoss_imex1_forward(*args))
         assert_parity(st, ref, st64, RTOL, ATOL, f"persist={mode} states")
-    ms = [np.full(P, v, dtype=np.complex64) for v in (0.9 + 0.05j, -0.05, 0.05, 0.9 - 0.05j)]
-    b = (np.random.default_rng(62).normal(size=(L, B, P, 2)) + 0j).astype(np.complex64)
-    lref = oracle.linoss_forward(*ms, b)
-    l64 = oracle.linoss_forward(*(m.astype(np.complex128) for m in ms), b.astype(np.complex128))
+    from tests.test_gpu_sdlinoss import sdl_inputs
+
+    A, G, S, sbu, _ = sdl_inputs("imex1", "m", L, B, P, seed=62)
+    sref = oracle.sdlinoss_forward("imex1", A, G, S, sbu)
+    s64 = oracle.sdlinoss_forward("imex1", *(x.astype(np.float64) for x in (A, G, S)),
+                                  sbu.astype(np.complex128))
     for mode in ("1", "0"):
         monkeypatch.setenv("OSSM_OSC_PERSIST", mode)
-        out = to_np(K.linoss_scan(*[to_dev(m) for m in ms], to_dev(b)))
-        assert_parity(out, lref, l64, RTOL, ATOL, f"linoss persist={mode}")
+        out = to_np(K.sdlinoss_imex1_forward(to_dev(A), to_dev(G), to_dev(S), to_dev(sbu)))
+        assert_parity(out, sref, s64, RTOL, ATOL, f"sdlinoss persist={mode}")
     no_device_errors()
 
 
