@@ -392,6 +392,59 @@ def cpu_baseline(L, B, P, budget_s=12.0, port_budget_s=3.0):
     }
 
 
+# ------------------------------------------------ one GPU's share of 8 GPUs
+def _shard_share(torch, K, dev, reps):
+    """One GPU's part of config 2 split over 8 GPUs (this run has one GPU, so
+    nothing crosses devices).  Batch sharding: forward and backward at B = 32/8.
+    Sequence sharding: the sequence in 8 shards of 512 steps; one shard's
+    forward from a zero state, the carries between all shards
+    (ossm_dlinoss_shard_carries, the scan over shards that would cross GPUs)
+    and one shard's fix-up (ossm_dlinoss_shard_fixup: 16 B read + 16 B written
+    per state-step)."""
+    import ctypes
+
+    from ossm_amd import _lib
+
+    out = {}
+    L, B, P = 4096, 4, 128
+    a, gam, dt, bu, go = dlinoss_inputs(torch, L, B, P, dev, seed=8)
+    st = K.dlinoss_imex1_forward(a, gam, dt, bu)
+    tf = _ev_time(torch, lambda: K.dlinoss_imex1_forward(a, gam, dt, bu), reps, 3)
+    tb = _ev_time(torch, lambda: K.dlinoss_imex1_backward(a, gam, dt, bu, st, go), reps, 3)
+    n = L * B * P
+    out["dlinoss_c2_batch_share_g8"] = {
+        "fwd_ms": tf, "bwd_ms": tb, "shape": [L, B, P],
+        "hbm_frac_fwd": n * DL_BYTES_FWD / (tf / 1e3) / PEAK_HBM,
+        "hbm_frac_bwd": n * DL_BYTES_BWD / (tb / 1e3) / PEAK_HBM}
+    del bu, go, st
+    L, B, P, G = 4096, 32, 128, 8
+    a, gam, dt, bu, _ = dlinoss_inputs(torch, L, B, P, dev, seed=9)
+    ns = L // G
+    lib = _lib.load()
+    states = torch.empty((L, B, P, 2), dtype=torch.complex64, device=dev)
+    carries = torch.empty((G, B, P, 2), dtype=torch.complex64, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    lengths = (ctypes.c_int64 * G)(*([ns] * G))
+    for k in range(G):
+        states[k * ns:(k + 1) * ns] = K.dlinoss_imex1_forward(a, gam, dt, bu[k * ns:(k + 1) * ns])
+    ptrs = [t.data_ptr() for t in (a, gam, dt)]
+    shard0 = bu[:ns]
+    t_scan = _ev_time(torch, lambda: K.dlinoss_imex1_forward(a, gam, dt, shard0), reps, 3)
+    t_carry = _ev_time(torch, lambda: _lib.check(lib.ossm_dlinoss_shard_carries(
+        0, *ptrs, states.data_ptr(), L, lengths, G, carries.data_ptr(), B, P, stream)), reps, 3)
+    t_fix = _ev_time(torch, lambda: _lib.check(lib.ossm_dlinoss_shard_fixup(
+        0, *ptrs, carries[1].data_ptr(), states[ns:2 * ns].data_ptr(), ns, B, P, stream)), reps, 3)
+    n = ns * B * P
+    out["dlinoss_c2_sequence_share_g8"] = {
+        "shard_forward_ms": t_scan, "carries_ms": t_carry, "fixup_ms": t_fix,
+        "shard_shape": [ns, B, P], "n_shards": G,
+        "fixup_bytes_per_state_step": 32,
+        "fixup_hbm_frac": n * 32 / (t_fix / 1e3) / PEAK_HBM,
+        "exchange_bytes_per_shard": B * P * 16}
+    del bu, states, carries
+    return out
+
+
 # ------------------------------------------------------------ other configs
 def _detail_configs(torch, K, dev, reps=20):
     """The other BASELINE configs, each timed with events (mean of `reps` back-to-back calls)."""
@@ -429,6 +482,7 @@ def _detail_configs(torch, K, dev, reps=20):
                                   "GBps": n * DL_BYTES_FWD / (ms / 1e3) / 1e9,
                                   "hbm_frac": n * DL_BYTES_FWD / (ms / 1e3) / PEAK_HBM}
     del bu
+    out.update(_shard_share(torch, K, dev, reps))
     # Selective D-LinOSS imex1 at config 2's shape (no BASELINE config of its own):
     # per-step parameters [L,B,M] (12 B/state-step more each way), and
     # time-invariant per-channel parameters [1,B,M]

@@ -59,7 +59,7 @@ enum {
 enum { OSSM_DLINOSS_IMEX1 = 0, OSSM_DLINOSS_IMEX2 = 1, OSSM_DLINOSS_IM = 2, OSSM_DLINOSS_EX = 3 };
 
 /* Library ABI version (bumped on any change of the entry points or their
-   behaviour; currently 15). */
+   behaviour; currently 16). */
 int ossm_abi_version(void);
 
 /* Message of the last failing call on this host thread ("" if none). */
@@ -132,6 +132,31 @@ int ossm_dlinoss_forward_noalloc(int variant, const float* a_diag, const float* 
                                  const float* step, const void* bu, void* states,
                                  int64_t length, int64_t batch, int64_t ssm,
                                  ossm_stream_t stream);
+
+/*
+ * Sequence sharding of the D-LinOSS forward (context parallelism), the part one
+ * GPU runs; no counterpart in the reference, which scans each sequence in one
+ * piece.  The sequence is split into n_shards consecutive shards (lengths
+ * shard_lengths[0 .. n_shards-1], summing to `length`, at most 64 shards) and
+ * each shard's rows of `states` [length, batch, ssm, 2] complex64 were
+ * computed by ossm_dlinoss_forward from a zero state.  The true state entering
+ * shard k is c_0 = 0, c_{k+1} = M^len_k c_k + z_k, where z_k is shard k's last
+ * zero-start state and M the oscillator's transition: ossm_dlinoss_shard_carries
+ * writes every c_k to `carries` [n_shards, batch, ssm, 2] complex64 (the
+ * exclusive scan over shards that would run across GPUs; powers and sums in
+ * fp64).  ossm_dlinoss_shard_fixup then corrects one shard in place,
+ * states[t] += M^(t+1) carry for t = 0 .. length-1 of that shard (`states` and
+ * `length` the shard's rows, `carry` its c_k [batch, ssm, 2] complex64), after
+ * which the states equal those of one ossm_dlinoss_forward over the whole
+ * sequence, to rounding.  Neither allocates or uses look-back scratch.
+ */
+int ossm_dlinoss_shard_carries(int variant, const float* a_diag, const float* g_diag,
+                               const float* step, const void* states, int64_t length,
+                               const int64_t* shard_lengths, int n_shards, void* carries,
+                               int64_t batch, int64_t ssm, ossm_stream_t stream);
+int ossm_dlinoss_shard_fixup(int variant, const float* a_diag, const float* g_diag,
+                             const float* step, const void* carry, void* states, int64_t length,
+                             int64_t batch, int64_t ssm, ossm_stream_t stream);
 
 /*
  * D-LinOSS backward, replaces dlinoss_<v>_backward:

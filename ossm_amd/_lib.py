@@ -113,6 +113,11 @@ _SIGNATURES = {
         ctypes.c_int,
         [_fp, _fp, _c_int64, _fp, _c_int64, _fp, _fp, _fp, _fp, _c_int64, _fp, _c_int64, _fp, _fp,
          _fp, _fp, _fp, _fp, _fp, _fp, _c_int64, _c_int64, _c_int64, _c_int64, _vp]),
+    "ossm_dlinoss_shard_carries": (
+        ctypes.c_int,
+        [ctypes.c_int, _fp, _fp, _fp, _vp, _c_int64, _vp, ctypes.c_int, _vp, _c_int64, _c_int64, _vp]),
+    "ossm_dlinoss_shard_fixup": (
+        ctypes.c_int, [ctypes.c_int, _fp, _fp, _fp, _vp, _vp, _c_int64, _c_int64, _c_int64, _vp]),
     "ossm_mamba_conv_forward": (
         ctypes.c_int, [_fp, _c_int64, _fp, _fp, _fp, _c_int64, _c_int64, _c_int64, _c_int64, _vp]),
     "ossm_mamba_conv_backward": (

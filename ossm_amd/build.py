@@ -24,7 +24,8 @@ OBJDIR = PKG / "_build"
 LIB = LIBDIR / "libossm_scan.so"
 
 SOURCES = ["runtime.cpp", "oscillator_scan.hip", "selective_scan.hip", "sdlinoss_scan.hip",
-           "diag_scan.hip", "dlinoss_layer.hip", "mamba_conv.hip", "scan_f64.hip"]
+           "diag_scan.hip", "dlinoss_layer.hip", "mamba_conv.hip", "scan_f64.hip",
+           "shard_scan.hip"]
 # standalone measurement program (not linked into the library)
 ISSUE_RATE_SRC = "valu_issue_rate.hip"
 ISSUE_RATE = LIBDIR / "valu_issue_rate"

@@ -236,7 +236,7 @@ int release_buffer(void* p, bool captured, const char* what) {
 
 extern "C" {
 
-int ossm_abi_version(void) { return 15; }
+int ossm_abi_version(void) { return 16; }
 
 const char* ossm_last_error(void) { return ossm::g_last_error.c_str(); }
 

@@ -42,7 +42,8 @@ def test_header_declares_the_entry_points():
               "ossm_diag_scan_backward_f64", "ossm_dlinoss_layer_forward", "ossm_dlinoss_layer_backward",
               "ossm_selective_mamba_forward", "ossm_selective_mamba_backward",
               "ossm_mamba_conv_forward", "ossm_mamba_conv_backward", "ossm_time_next_launch",
-              "ossm_selective_forward_skip", "ossm_selective_backward_skip"):
+              "ossm_selective_forward_skip", "ossm_selective_backward_skip",
+              "ossm_dlinoss_shard_carries", "ossm_dlinoss_shard_fixup"):
         assert n in names, n
 
 
@@ -58,7 +59,7 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     # every declared symbol has a ctypes signature in the binding
     assert set(_declared_functions()) == set(_lib.EXPORTED)
-    assert _lib.load().ossm_abi_version() == 15
+    assert _lib.load().ossm_abi_version() == 16
 
 
 def test_selective_skip_entry_points_refuse_a_null_d():
@@ -74,6 +75,30 @@ def test_selective_skip_entry_points_refuse_a_null_d():
     assert lib.ossm_selective_backward_skip(0, p, p, p, p, p, p, p, None, p, p, p, p, p, p, p, None,
                                             None, 1, 1, 1, 1, None) == 1
     assert b"null skip D or dD" in lib.ossm_last_error()
+
+
+def test_shard_entry_points_check_shard_lengths_before_any_hip_call():
+    """ossm_dlinoss_shard_carries refuses shard counts outside 1..64, empty
+    shards and lengths that do not sum to the states' length, and both shard
+    entry points refuse negative sizes, all before any HIP call."""
+    from ossm_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libossm_scan.so not built (python -m ossm_amd.build)")
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)  # never dereferenced: the calls fail first
+
+    def carries(lengths, n, L):
+        arr = (ctypes.c_int64 * max(1, len(lengths)))(*lengths)
+        return lib.ossm_dlinoss_shard_carries(0, p, p, p, p, L, arr, n, p, 2, 8, None)
+
+    assert carries([], 0, 10) == 1 and b"n_shards" in lib.ossm_last_error()
+    assert carries([1] * 65, 65, 65) == 1 and b"n_shards" in lib.ossm_last_error()
+    assert carries([5, 0, 5], 3, 10) == 1 and b"at least one step" in lib.ossm_last_error()
+    assert carries([5, 4], 2, 10) == 1 and b"sum to 9" in lib.ossm_last_error()
+    assert carries([5, 5], 2, -1) == 1 and b"negative size" in lib.ossm_last_error()
+    assert lib.ossm_dlinoss_shard_fixup(0, p, p, p, p, p, -1, 2, 8, None) == 1
+    assert b"negative size" in lib.ossm_last_error()
 
 
 def test_time_next_launch_argument_checks():
