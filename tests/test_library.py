@@ -221,3 +221,22 @@ def test_noalloc_forward_refuses_above_its_limit_on_the_host(shape):
     assert L * B * P > 2**25
     assert f(0, p, p, p, p, p, L, B, P, None) == 3  # OSSM_ERR_UNSUPPORTED
     assert b"33,554,432" in lib.ossm_last_error()
+
+
+def test_sharded_forward_checks_its_arguments_on_the_host():
+    """ossm_amd.shard refuses an unknown variant and host tensors before it
+    reaches the library (no GPU needed)."""
+    import torch
+
+    from ossm_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libossm_scan.so not built (python -m ossm_amd.build)")
+    from ossm_amd import shard
+
+    p = torch.zeros(4)
+    bu = torch.zeros((8, 2, 4), dtype=torch.complex64)
+    with pytest.raises(ValueError, match="Unknown D-LinOSS variant"):
+        shard.dlinoss_forward_sharded("rk4", p, p, p, bu, [8])
+    with pytest.raises(RuntimeError, match="device tensor"):
+        shard.dlinoss_forward_sharded("imex1", p, p, p, bu, [4, 4])
