@@ -149,10 +149,10 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
-# OSSM_CHECK_DEVICE_ERRORS=1: after every successful call, synchronise the
-# current stream and raise RuntimeError if a kernel raised a protocol error
-# bit (a look-back wait that gave up, an out-of-range ticket).  Off by
-# default: the check costs a stream synchronisation per call.
+# OSSM_CHECK_DEVICE_ERRORS=1: after every successful call made outside stream
+# capture, synchronise the current stream and raise RuntimeError if a kernel
+# raised a protocol error bit (a look-back wait that gave up, an out-of-range
+# ticket).  Off by default: the check costs a stream synchronisation per call.
 CHECK_DEVICE_ERRORS = os.environ.get("OSSM_CHECK_DEVICE_ERRORS", "0") not in ("", "0")
 
 
@@ -162,7 +162,9 @@ def check(rc: int) -> None:
     if rc != 0:
         msg = load().ossm_last_error().decode(errors="replace")
         raise RuntimeError(msg or f"ossm_scan call failed with status {rc}")
-    if CHECK_DEVICE_ERRORS:
+    # not under stream capture: the check synchronises the stream and copies
+    # the bits to the host, which a capture cannot record (it would invalidate it)
+    if CHECK_DEVICE_ERRORS and not torch.cuda.is_current_stream_capturing():
         bits = device_error_bits()
         if bits:
             raise RuntimeError(f"ossm_scan: a kernel raised device error bits {bits:#x} "

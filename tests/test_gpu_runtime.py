@@ -227,6 +227,7 @@ def test_protocol_failure_gives_nan_not_garbage(K, monkeypatch):
     from ossm_amd import _lib
 
     monkeypatch.setenv("OSSM_SCAN_ORDER", "ticket")
+    monkeypatch.setattr(_lib, "CHECK_DEVICE_ERRORS", False)  # the bits are read here
 
     lib = _lib.load()
     stream = torch.cuda.current_stream().cuda_stream
@@ -327,6 +328,7 @@ def test_protocol_failure_persistent_forward(K, monkeypatch):
     ref = oracle.dlinoss_forward("imex1", a, g, dt, bu)
     announce("runtime: persistent forward protocol failure -> NaN")
     monkeypatch.setenv("OSSM_SCAN_ORDER", "ticket")
+    monkeypatch.setattr(_lib, "CHECK_DEVICE_ERRORS", False)  # the bits are read here
     K.dlinoss_imex1_forward(*args)
     assert _lib.device_error_bits() == 0
     _lib.check(lib.ossm_test_skew_tickets(stream, 1 << 20))
@@ -339,6 +341,29 @@ def test_protocol_failure_persistent_forward(K, monkeypatch):
                                   bu.astype(np.complex128))
     assert_parity(st, ref, st64, RTOL, ATOL, "after recovery")  # L = 8292: fp64 arbiter
     no_device_errors()
+
+
+def test_protocol_failure_raises_with_device_error_checks(K, monkeypatch):
+    """With OSSM_CHECK_DEVICE_ERRORS=1 (here set on the module), a call whose
+    kernels raise a protocol error bit raises RuntimeError naming the bits, and
+    the calls after it are correct and raise nothing."""
+    from ossm_amd import _lib
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    L, B, P = 1000, 2, 64
+    a, g, dt, bu, _ = dlinoss_inputs(L, B, P, seed=64, variant="imex1")
+    args = [to_dev(x) for x in (a, g, dt, bu)]
+    announce("runtime: protocol failure raises under device error checks")
+    monkeypatch.setenv("OSSM_SCAN_ORDER", "ticket")
+    monkeypatch.setattr(_lib, "CHECK_DEVICE_ERRORS", True)
+    K.dlinoss_imex1_forward(*args)
+    # not through _lib.check: its device check would put the counter back in step
+    assert lib.ossm_test_skew_tickets(stream, 1 << 20) == 0
+    with pytest.raises(RuntimeError, match="device error bits 0x2"):
+        K.dlinoss_imex1_forward(*args)
+    st = to_np(K.dlinoss_imex1_forward(*args))
+    assert_close(st, oracle.dlinoss_forward("imex1", a, g, dt, bu), RTOL, ATOL, "after the error")
 
 
 def _dl_truth(a, g, dt, bu, go):
