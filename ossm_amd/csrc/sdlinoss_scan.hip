@@ -200,7 +200,10 @@ __device__ __forceinline__ void load_params(const SdlParams& prm, long long t0, 
 // TB: all three parameters broadcast over time (time stride 0): they are
 // read once and every per-step coefficient is the same value, which the
 // compiler then computes once.
-template <int V, int T, int W, bool TB>
+// PERSIST: as the oscillatory forward's persistent launch (ticket order, a
+// grid of fewer workgroups than chunks, workgroup b taking ceil((total - b) /
+// grid) chunks and drawing the next ticket while it stores the current one).
+template <int V, int T, int W, bool TB, bool PERSIST>
 __global__ __launch_bounds__(W * kWave) void sdl_forward_kernel(
     SdlParams prm, const float2* __restrict__ bu, float4* __restrict__ out, int L, int nc,
     int n_groups, int n_chunks, unsigned long long* __restrict__ rec, LaunchSync sync) {
@@ -208,10 +211,33 @@ __global__ __launch_bounds__(W * kWave) void sdl_forward_kernel(
   __shared__ float4 s_m[W][kWave];
   __shared__ float4 s_carry[kWave];
   __shared__ int s_ticket;
+  __shared__ unsigned int s_tag;
+  __shared__ int s_poison;
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = wave_id();
-  const int ticket = launch_order(sync, n_groups * n_chunks, &s_ticket);
+  const int total = n_groups * n_chunks;
+  int order;
+  int left = 1;
+  if constexpr (PERSIST) {
+    left = (total - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) /
+           static_cast<int>(gridDim.x);
+    if (threadIdx.x == 0) {
+      unsigned int tag = 0;
+      int poison = 0;
+      s_ticket = draw_ticket(sync, total, &tag, &poison);
+      s_tag = tag;
+      s_poison = poison;
+    }
+    __syncthreads();
+    sync.tag = __builtin_amdgcn_readfirstlane(s_tag);
+    sync.poison = __builtin_amdgcn_readfirstlane(s_poison);
+    order = __builtin_amdgcn_readfirstlane(s_ticket);
+  } else {
+    order = launch_order(sync, total, &s_ticket);
+  }
+  for (;;) {
+  const int ticket = order;
   const int c = ticket / n_groups;
   const int g = ticket - c * n_groups;
   const int ch = g * kWave + lane;
@@ -276,6 +302,13 @@ __global__ __launch_bounds__(W * kWave) void sdl_forward_kernel(
   __syncthreads();
 
   // 3. own carry through the earlier waves, then re-run and store
+  int next = 0, next_poison = 0;
+  if constexpr (PERSIST) {
+    if (threadIdx.x == 0 && left > 1) {
+      unsigned int tag = 0;
+      next = draw_ticket(sync, total, &tag, &next_poison);
+    }
+  }
   float4 s = s_carry[lane];
   for (int v = 0; v < w; ++v) s = f4add(mat_apply(rmat_unpack(s_m[v][lane]), s), s_e[v][lane]);
   if (active) {
@@ -294,6 +327,18 @@ __global__ __launch_bounds__(W * kWave) void sdl_forward_kernel(
         }
       }
     }
+  }
+  if constexpr (!PERSIST) break;
+  if (--left == 0) break;
+  // every wave is past its reads of s_e, s_m and s_carry before the next
+  // chunk writes them
+  if (threadIdx.x == 0) {
+    s_ticket = next;
+    s_poison = next_poison;
+  }
+  __syncthreads();
+  sync.poison = __builtin_amdgcn_readfirstlane(s_poison);
+  order = __builtin_amdgcn_readfirstlane(s_ticket);
   }
 }
 
@@ -705,8 +750,26 @@ int sdl_forward_tw(const SdlParams& prm, const void* bu, void* states, int64_t L
   const int64_t total = n_chunks * n_groups;
   if (int rc = acquire_scratch(call, rec_bytes, total, &payload, &sync)) return rc;
   const bool tb = prm.a.t_stride == 0 && prm.g.t_stride == 0 && prm.s.t_stride == 0;
-  hipLaunchKernelGGL((tb ? sdl_forward_kernel<V, T, W, true> : sdl_forward_kernel<V, T, W, false>),
-                     dim3(static_cast<unsigned>(total)),
+  // persistent (per-step parameters, ticket order) when the grid has more
+  // chunks than the device holds workgroups at once
+  static const int64_t cap = [] {
+    int dev = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(&sdl_forward_kernel<V, T, W, false, true>),
+            W * kWave, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      return int64_t(0);
+    }
+    return int64_t(per_cu) * device_cu_count(dev);
+  }();
+  const char* pe = std::getenv("OSSM_OSC_PERSIST");
+  const bool persist = !tb && sync.use_ticket && cap > 0 && total > cap &&
+                       !(pe != nullptr && std::string(pe) == "0");
+  const auto kern = persist ? sdl_forward_kernel<V, T, W, false, true>
+                            : (tb ? sdl_forward_kernel<V, T, W, true, false>
+                                  : sdl_forward_kernel<V, T, W, false, false>);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(persist ? cap : total)),
                      dim3(W * kWave), 0, stream, prm, static_cast<const float2*>(bu),
                      static_cast<float4*>(states), static_cast<int>(L), static_cast<int>(nc),
                      static_cast<int>(n_groups), static_cast<int>(n_chunks),

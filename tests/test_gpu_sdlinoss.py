@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.gpu_util import announce, assert_close, assert_parity, need_gpu, to_dev, to_np
+from tests.gpu_util import announce, assert_close, assert_parity, need_gpu, no_device_errors, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -184,6 +184,25 @@ def test_sdlinoss_empty_and_errors(K):
         K.sdlinoss_imex1_forward(dA, dG, dS, to_dev(bu).real.contiguous())
     with pytest.raises(RuntimeError, match="grad_output must match"):
         K.sdlinoss_imex1_backward(dA, dG, dS, to_dev(bu), out, to_dev(go)[:2])
+
+
+def test_sdlinoss_persistent_forward(K, monkeypatch):
+    """Per-step parameters on a grid of 512 chunks (more than the device holds
+    workgroups at once): the persistent forward (each workgroup several chunks
+    in ticket order) and the one-workgroup-per-chunk launch (OSSM_OSC_PERSIST=0)
+    against the oracle, with the fp64 arbiter."""
+    L, B, M = 4096, 8, 128
+    args = sdl_inputs("imex1", "full", L, B, M, seed=21)
+    A, G, S, bu, _ = args
+    ref = oracle.sdlinoss_forward("imex1", A, G, S, bu)
+    t64 = oracle.sdlinoss_forward("imex1", *(x.astype(np.float64) for x in (A, G, S)),
+                                  bu.astype(np.complex128))
+    announce(f"sdlinoss persistent forward L={L} B={B} M={M}")
+    for mode in ("1", "0"):
+        monkeypatch.setenv("OSSM_OSC_PERSIST", mode)
+        st = to_np(K.sdlinoss_imex1_forward(*(to_dev(x) for x in (A, G, S, bu))))
+        assert_parity(st, ref, t64, RTOL, ATOL, f"persist={mode} states")
+    no_device_errors()
 
 
 def test_sdlinoss_repeatable(K):
